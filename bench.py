@@ -1,0 +1,186 @@
+"""GPT-2 124M fwd+bwd+AdamW training step on one MI355X ('hip' device).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+Workload: GPT-2 small, fp32, 12 layers, 12 heads, d=768, vocab 50257,
+context 1024, tied embeddings, random-init weights N(0, 0.02) (biases 0,
+LayerNorm 1/0); batch 8 x 1024 synthetic tokens uniform in [0, 50257);
+next-token cross_entropy; full backward; AdamW(lr 6e-4, wd 0.1).
+
+Prints ONE JSON line.  `value` = tokens/s over exactly K timed steps
+(inputs resident in HBM, device synchronised on both sides of the timed
+region).  `roofline` reports the dominant kernel family (the MFMA GEMMs of
+the Linear layers) from HIP events recorded on the library stream around
+every launch during the timed steps; `hbm_kernels` reports the
+memory-bound backward kernels the same way.  `cpu_baseline` times the
+oracle (numpy) on a bounded sample of the same workload on the host.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "GPT-2 124M fwd+bwd+AdamW tokens/s (1 GPU); bwd-kernel HBM GB/s vs peak"
+HBM_PEAK_GBS = 8000.0
+FP32_MFMA_PEAK_TFLOPS = 157.3
+
+V, CTX, D, H, LAYERS = 50257, 1024, 768, 12, 12
+B, T = 8, 1024
+
+
+def linear_flops_per_step(b, t):
+    """Algorithmic FLOPs of the Linear-layer GEMMs in one fwd+bwd step:
+    2*tokens*in*out per product, three products (y, dx, dW) per layer."""
+    tok = b * t
+    per_layer = D * 3 * D + D * D + D * 4 * D + 4 * D * D
+    fwd = 2 * tok * (LAYERS * per_layer + D * V)
+    return 3 * fwd
+
+
+def hbm_bytes_per_step(b, t, nparams):
+    """Algorithmic HBM bytes (inputs read once + outputs written once) per
+    step for the memory-bound backward kernel families."""
+    tok = b * t
+    f = 4
+    return {
+        # dlogits = softmax - onehot: read logits, write dlogits
+        "cross_entropy_bwd": 2 * tok * V * f,
+        # 25 LayerNorms: read dy, x; write dx (+ mean/rstd, gamma)
+        "layer_norm_bwd": (2 * LAYERS + 1) * (3 * tok * D * f + 2 * tok * f + D * f),
+        # GELU backward per layer: read g, x; write dx over [tok, 4D]
+        "unary_backward": LAYERS * 3 * tok * 4 * D * f,
+        # AdamW: read p, g, m, v; write p, m, v
+        "adam": 7 * nparams * f,
+        # embedding backward: read the dout rows, write the touched table rows
+        "embedding_bwd": 2 * (tok * D * f) + 2 * tok * 4,
+    }
+
+
+def run_gpu(steps, warmup):
+    import __graft_entry__ as ge
+    torch = ge.load_package()
+    from torchjs_amd import workloads as W
+    torch.init(0)
+    torch.manual_seed(1234)
+    model = W.GPT2(V, CTX, D, H, LAYERS)
+    with torch.no_grad():
+        for name, p in model.named_parameters():
+            if name.endswith(("ln_1.weight", "ln_2.weight")) or name == "ln_f.weight":
+                p.fill_(1.0)
+            elif name.endswith("bias"):
+                p.zero_()
+            else:
+                p.copy_(torch.randn(*p.shape) * 0.02)
+    nparams = sum(p.numel() for p in model.parameters())
+    opt = torch.optim.AdamW(model.parameters(), lr=6e-4, weight_decay=0.1)
+    rng = np.random.default_rng(1234)
+    toks = rng.integers(0, V, (B, T + 1)).astype(np.int32)
+    ids = torch.tensor(toks[:, :-1])
+    tgt = torch.tensor(toks[:, 1:])
+
+    def step():
+        opt.zero_grad()
+        loss = model.loss(ids, tgt)
+        loss.backward()
+        opt.step()
+        return loss
+
+    for i in range(warmup):
+        loss = step()
+        print("warmup %d loss %.4f" % (i, loss.item()), file=sys.stderr, flush=True)
+    torch.synchronize()
+    torch.hip.kernel_timing(True)
+    torch.hip.kernel_timing_reset()
+    torch.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        loss = step()
+    torch.synchronize()
+    elapsed = time.perf_counter() - t0
+    final_loss = loss.item()
+    fams = torch.hip.kernel_families()
+    timing = {f: torch.hip.kernel_time(f) for f in fams}
+    torch.hip.kernel_timing(False)
+    mem = torch.hip.memory_stats()
+    return elapsed, final_loss, timing, nparams, mem
+
+
+def cpu_baseline():
+    """The oracle (numpy) on a bounded sample: GPT-2 small at B=1, T=128,
+    full 12 layers and vocabulary, fwd + bwd + AdamW."""
+    from oracle import models as om
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+    except Exception:
+        threads = 1
+    cfg = om.Config()
+    r = np.random.default_rng(0)
+    p = om.init_params(cfg, r)
+    tb, tt = 1, 128
+    ids = r.integers(0, V, (tb, tt + 1))
+    t0 = time.perf_counter()
+    _, g = om.gpt2_loss_and_grads(cfg, p, ids[:, :-1], ids[:, 1:])
+    om.adamw_step(p, g, lr=6e-4, wd=0.1, step=1)
+    dt = time.perf_counter() - t0
+    return {"value": tb * tt / dt, "unit": "tokens/s", "cores": int(threads), "kind": "port",
+            "sample": "oracle (numpy float64) GPT-2 124M fwd+bwd+AdamW at B=1, T=128 (128 tokens, "
+                      "full 12 layers and 50257 vocab), %.1f s" % dt}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one MI355X: this build has no multi-GPU path "
+              "(--gpus %d requested)" % args.gpus, file=sys.stderr)
+        sys.exit(2)
+    elapsed, final_loss, timing, nparams, mem = run_gpu(args.steps, args.warmup)
+    tokens = B * T * args.steps
+    ms_step = 1000.0 * elapsed / args.steps
+    # dominant kernel: the Linear GEMMs (MFMA)
+    n_g, ms_g = timing.get("gemm", (0, 0.0))
+    flops = linear_flops_per_step(B, T) * args.steps
+    achieved = flops / (ms_g / 1000.0) / 1e12 if ms_g else 0.0
+    roofline = {"bound": "mfma", "kernel": "gemm (Linear fwd/dgrad/wgrad, fp32 MFMA)",
+                "achieved": round(achieved, 2), "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": None,
+                "launches": n_g, "avg_launch_ms": round(ms_g / max(n_g, 1), 4),
+                "share_of_step": round(ms_g / (ms_step * args.steps), 3)}
+    hbm = {}
+    for fam, byts in hbm_bytes_per_step(B, T, nparams).items():
+        n, ms = timing.get(fam, (0, 0.0))
+        if ms:
+            gbs = byts * args.steps / (ms / 1000.0) / 1e9
+            hbm[fam] = {"GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 3),
+                        "ms_per_step": round(ms / args.steps, 3), "launches_per_step": n // args.steps}
+    top = sorted(((ms / args.steps, f) for f, (n, ms) in timing.items()), reverse=True)[:12]
+    out = {
+        "metric": METRIC, "value": round(tokens / elapsed, 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic tokens uniform in [0,50257); random-init weights N(0,0.02)",
+        "config": {"workload": "GPT-2 124M train step (fwd+bwd+AdamW)", "batch": B, "seq_len": T,
+                   "vocab": V, "layers": LAYERS, "d_model": D, "heads": H,
+                   "optimizer": "AdamW(lr=6e-4, wd=0.1)", "parallelism": "none (1 GPU)"},
+        "roofline": roofline, "hbm_kernels": hbm,
+        "kernel_ms_per_step": {f: round(ms, 3) for ms, f in top},
+        "final_loss": round(final_loss, 4), "peak_mem_GB": round(mem["peak_bytes"] / 1e9, 2),
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

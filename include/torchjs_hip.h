@@ -1,0 +1,447 @@
+/*
+ * torchjs_hip.h — C ABI of libtorchjs_hip.so, the MI355X (gfx950) compute
+ * backend behind torch.js's `'hip'` device.
+ *
+ * torch.js has no backend interface of its own: every op builds WebGPU
+ * objects inline and submits them (src/backend/index.ts:6 re-exports
+ * src/backend/webgpu/index.ts:6-25).  This header is the boundary that
+ * replaces that runtime (device init, buffer pool, uploads/readbacks,
+ * pipeline dispatch, queue sync) and the WGSL kernels of the autograd hot
+ * path.  Each declaration names the reference interface it replaces.
+ *
+ * Conventions
+ *  - Every function returns an int status (TJH_OK == 0).  On failure a
+ *    thread-local message is available from tjh_last_error().
+ *  - All device work is enqueued on ONE library-owned HIP stream, so the
+ *    order of calls is the order of execution, like WebGPU's single queue
+ *    (src/backend/webgpu/dispatch.ts:115-118).  Kernel entry points are
+ *    asynchronous; tjh_d2h and tjh_synchronize block.
+ *  - Device pointers are plain `void*`/`float*` obtained from tjh_malloc.
+ *    Floating-point data is IEEE fp32; index data is int32 (torch.js
+ *    stores integer tensors as Int32Array, src/dtype.ts:7-15).
+ *  - Shapes and strides are int64 arrays counted in ELEMENTS, ndim <= 8.
+ */
+#ifndef TORCHJS_HIP_H
+#define TORCHJS_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TJH_MAX_DIMS 8
+
+/* status codes */
+#define TJH_OK 0
+#define TJH_ERR_INVALID 1         /* bad argument (shape, pointer, op code) */
+#define TJH_ERR_NOT_INITIALIZED 2 /* tjh_init not called                   */
+#define TJH_ERR_OOM 3             /* device allocation failed              */
+#define TJH_ERR_HIP 4             /* HIP runtime error                     */
+#define TJH_ERR_UNSUPPORTED 5     /* valid request the library cannot do   */
+
+/* ------------------------------------------------------------------ */
+/* Lifecycle — replaces initWebGPU / getDevice / getCapabilities /      */
+/* syncDevice (src/backend/webgpu/device.ts:27-97,                      */
+/* src/backend/webgpu/capabilities.ts:42-101,                           */
+/* src/backend/webgpu/dispatch.ts:115-118).                             */
+/* ------------------------------------------------------------------ */
+
+typedef struct {
+  char name[256];         /* marketing name                                */
+  char arch[64];          /* gcnArchName, e.g. "gfx950:sramecc+:xnack-"    */
+  int32_t compute_units;
+  int32_t warp_size;      /* 64 on CDNA                                    */
+  int64_t total_mem;      /* bytes of HBM                                  */
+  int64_t max_alloc;      /* largest single allocation accepted            */
+  int32_t lds_per_block;  /* bytes                                         */
+  int32_t clock_khz;
+  int32_t l2_bytes;
+  int32_t ordinal;
+} tjh_device_info;
+
+/* Message of the last failing call on this thread ("" when none). */
+const char* tjh_last_error(void);
+/* Library version string. */
+const char* tjh_version(void);
+/* Idempotent device init (like initWebGPU, device.ts:27-86): selects the
+ * device, creates the library stream.  A second call with another ordinal
+ * fails with TJH_ERR_INVALID. */
+int tjh_init(int ordinal);
+/* 1 if tjh_init succeeded, else 0 (the "WebGPU not initialized" check,
+ * device.ts:92-97). */
+int tjh_is_initialized(void);
+/* Number of visible HIP devices (0 when none; never initialises one). */
+int tjh_device_count(int* out);
+/* Capability query (getCapabilities, capabilities.ts:42-101). */
+int tjh_get_device_info(tjh_device_info* out);
+/* Block until every enqueued call has finished (syncDevice). */
+int tjh_synchronize(void);
+
+/* ------------------------------------------------------------------ */
+/* Memory — replaces GPUBufferPool / createStorageBuffer /              */
+/* createBufferWithData / readBuffer / copyBufferToBuffer and           */
+/* torch.webgpu.memory_stats (src/backend/webgpu/buffer.ts:10-206,      */
+/* src/webgpu.ts:11-51).                                                */
+/* ------------------------------------------------------------------ */
+
+typedef struct {
+  uint64_t active_bytes;  /* bytes handed out and not yet freed          */
+  uint64_t pooled_bytes;  /* bytes cached for reuse                       */
+  uint64_t peak_bytes;    /* max active_bytes since the last reset        */
+  uint64_t allocations;   /* tjh_malloc calls served                      */
+  uint64_t device_mallocs;/* hipMalloc calls made (cache misses)          */
+} tjh_mem_stats;
+
+/* Stream-ordered caching allocator on HBM.  Blocks are 256-byte aligned.
+ * A block released by tjh_free may be handed out again at once: every
+ * later use is on the same stream, so it runs after the work that used
+ * the block before (GPUBufferPool.acquire/release, buffer.ts:21-114).
+ * bytes == 0 returns a valid unique pointer. */
+int tjh_malloc(size_t bytes, void** out);
+int tjh_free(void* ptr);
+int tjh_memory_stats(tjh_mem_stats* out);
+/* Synchronises and returns every cached block to HIP (bufferPool.clear). */
+int tjh_empty_cache(void);
+int tjh_reset_peak(void);
+
+/* Copies.  tjh_h2d and tjh_d2d are stream-ordered; tjh_d2h waits for the
+ * stream and returns with `dst` filled (readBuffer, buffer.ts:150-206). */
+int tjh_h2d(void* dst, const void* src, size_t bytes);
+int tjh_d2h(void* dst, const void* src, size_t bytes);
+int tjh_d2d(void* dst, const void* src, size_t bytes);
+
+/* ------------------------------------------------------------------ */
+/* Timing — device-side counterpart of the profiler's record_function   */
+/* (src/profiler/index.ts:145-166) and benchmark Timer                  */
+/* (src/utils/benchmark/timer.ts:45-108).  When enabled, each launch of */
+/* a kernel family is bracketed by HIP events on the library stream.    */
+/* ------------------------------------------------------------------ */
+
+int tjh_kprof_enable(int on);
+int tjh_kprof_reset(void);
+/* Synchronises, then reports launches and summed event time for every
+ * kernel family whose name starts with `family` ("" = all). */
+int tjh_kprof_query(const char* family, int64_t* launches, double* total_ms);
+/* Names of families seen so far, '\n'-separated, into buf (truncated). */
+int tjh_kprof_names(char* buf, size_t buflen);
+/* Wall timer on the stream: returns an id; tjh_timer_stop gives ms. */
+int tjh_timer_start(int* id);
+int tjh_timer_stop(int id, double* ms);
+
+/* ------------------------------------------------------------------ */
+/* Fill / RNG / copies — fill.wgsl, random.wgsl:9-46 (with the LCG seed */
+/* step of src/ops/creation.ts:921 applied by the host), expand.wgsl,   */
+/* transpose(_nd).wgsl, slice(_backward).wgsl, Tensor.cat               */
+/* (Tensor.ts:152-235, 1537-2130).                                      */
+/* ------------------------------------------------------------------ */
+
+int tjh_fill_f32(float* out, int64_t n, float value);
+int tjh_fill_i32(int32_t* out, int64_t n, int32_t value);
+/* normal == 0: U[0,1) = xorshift32(seed ^ (i*1664525+1013904223)) / 2^32;
+ * normal != 0: Box-Muller of two successive xorshift32 states. */
+int tjh_random(float* out, int64_t n, uint32_t seed, int normal);
+/* dst[idx] = src[idx] for every index of `shape`, both sides strided
+ * (permute, contiguous, expand, slice, slice-backward, cat). */
+int tjh_copy_strided(int ndim, const int64_t* shape,
+                     const float* src, const int64_t* src_strides,
+                     float* dst, const int64_t* dst_strides);
+/* int32 variant (index tensors). */
+int tjh_copy_strided_i32(int ndim, const int64_t* shape,
+                         const int32_t* src, const int64_t* src_strides,
+                         int32_t* dst, const int64_t* dst_strides);
+/* float <-> int32 conversions (Tensor.to(dtype)); f2i truncates toward 0 */
+int tjh_cast_f32_i32(const float* src, int32_t* dst, int64_t n);
+int tjh_cast_i32_f32(const int32_t* src, float* dst, int64_t n);
+
+/* ------------------------------------------------------------------ */
+/* Elementwise — elementwise.wgsl:5-31, broadcast.wgsl:28-175,          */
+/* scalar.wgsl:10-67, unary.wgsl:5-252, masked_fill.wgsl, and the       */
+/* backward formulas the reference lacks (Tensor.ts:3409-3656).         */
+/* ------------------------------------------------------------------ */
+
+/* unary op codes */
+enum {
+  TJH_UNARY_NEG = 0, TJH_UNARY_EXP, TJH_UNARY_LOG, TJH_UNARY_SQRT,
+  TJH_UNARY_RSQRT, TJH_UNARY_TANH, TJH_UNARY_SIGMOID, TJH_UNARY_RELU,
+  TJH_UNARY_GELU, TJH_UNARY_SQUARE, TJH_UNARY_RECIPROCAL, TJH_UNARY_ERF,
+  TJH_UNARY_ABS, TJH_UNARY_SIN, TJH_UNARY_COS, TJH_UNARY_SILU,
+  TJH_UNARY_LEAKY_RELU, TJH_UNARY_ELU, TJH_UNARY_SOFTPLUS, TJH_UNARY_SIGN,
+  TJH_UNARY_COUNT
+};
+/* binary op codes (tensor op tensor); pow = a^b */
+enum {
+  TJH_BINARY_ADD = 0, TJH_BINARY_SUB, TJH_BINARY_MUL, TJH_BINARY_DIV,
+  TJH_BINARY_POW, TJH_BINARY_MAXIMUM, TJH_BINARY_MINIMUM,
+  TJH_BINARY_COUNT
+};
+/* scalar op codes: out = x op s (reverse != 0: out = s op x) */
+enum {
+  TJH_SCALAR_ADD = 0, TJH_SCALAR_SUB, TJH_SCALAR_MUL, TJH_SCALAR_DIV,
+  TJH_SCALAR_POW, TJH_SCALAR_MAXIMUM, TJH_SCALAR_MINIMUM,
+  TJH_SCALAR_COUNT
+};
+
+/* out[i] = op(x[i]); alpha is the slope/alpha of leaky_relu/elu. */
+int tjh_unary(int op, const float* x, float* out, int64_t n, float alpha);
+/* out[i] = g[i] * op'(x[i]) using the saved input x and/or output y
+ * (y may be NULL for ops whose derivative needs only x). */
+int tjh_unary_backward(int op, const float* g, const float* x,
+                       const float* y, float* out, int64_t n, float alpha);
+/* out (contiguous, `shape`) = a op b with broadcast strides (0 = broadcast
+ * dim).  Handles any ndim <= 8; contiguous and row-broadcast layouts take
+ * vectorised paths. */
+int tjh_binary(int op, int ndim, const int64_t* shape,
+               const float* a, const int64_t* a_strides,
+               const float* b, const int64_t* b_strides, float* out);
+/* Ternary backward helpers over a contiguous, common shape:
+ *  TJH_TERNARY_DIV_B:  out = -g * a / (b*b)
+ *  TJH_TERNARY_POW_A:  out =  g * b * a^(b-1)
+ *  TJH_TERNARY_POW_B:  out =  g * a^b * ln(a)
+ *  TJH_TERNARY_MUL3 :  out =  g * a * b
+ * Each operand is strided over `shape` like tjh_binary. */
+enum { TJH_TERNARY_DIV_B = 0, TJH_TERNARY_POW_A, TJH_TERNARY_POW_B,
+       TJH_TERNARY_MUL3, TJH_TERNARY_COUNT };
+int tjh_ternary(int op, int ndim, const int64_t* shape,
+                const float* g, const int64_t* g_strides,
+                const float* a, const int64_t* a_strides,
+                const float* b, const int64_t* b_strides, float* out);
+int tjh_scalar(int op, const float* x, float s, int reverse, float* out,
+               int64_t n);
+/* pow_scalar backward: out = g * s * x^(s-1) (scalar.wgsl:53-66 for the
+ * forward's integer-exponent rule). */
+int tjh_pow_scalar_backward(const float* g, const float* x, float s,
+                            float* out, int64_t n);
+/* out = alpha*x + y, contiguous (accumulateGrad, Tensor.ts:3670-3677). */
+int tjh_axpy(float alpha, const float* x, const float* y, float* out,
+             int64_t n);
+/* out = mask[idx] != 0 ? value : x[idx]; mask is uint8, strided (may
+ * broadcast).  Backward is the same call with x = g and value = 0
+ * (masked_fill.wgsl, Tensor.ts:804-832). */
+int tjh_masked_fill(int ndim, const int64_t* shape,
+                    const float* x, const int64_t* x_strides,
+                    const uint8_t* mask, const int64_t* mask_strides,
+                    float value, float* out);
+/* comparisons producing float 0/1 (compare.wgsl): op 0 eq,1 ne,2 lt,3 le,
+ * 4 gt, 5 ge; b strided over shape like tjh_binary. */
+int tjh_compare(int op, int ndim, const int64_t* shape,
+                const float* a, const int64_t* a_strides,
+                const float* b, const int64_t* b_strides, float* out);
+
+/* ------------------------------------------------------------------ */
+/* Reductions — reduce_sum.wgsl (+max/min/prod), reduce_dim.wgsl,       */
+/* reduce_broadcast_grad.wgsl, argmax (Tensor.ts:2359-2577, 3794-3906). */
+/* ------------------------------------------------------------------ */
+
+enum { TJH_REDUCE_SUM = 0, TJH_REDUCE_MEAN, TJH_REDUCE_MAX, TJH_REDUCE_MIN,
+       TJH_REDUCE_PROD, TJH_REDUCE_COUNT };
+/* x viewed as contiguous [outer, r, inner]; out[outer, inner] = reduce
+ * over r.  Deterministic (fixed split and combine order).  outer=inner=1
+ * is the full reduction; outer=1 is the broadcast-grad column sum. */
+int tjh_reduce(int op, const float* x, int64_t outer, int64_t r,
+               int64_t inner, float* out);
+/* first index of the max (min when is_min) along r; ties keep the first
+ * index (Tensor.ts:2568). */
+int tjh_argmax(const float* x, int64_t outer, int64_t r, int64_t inner,
+               int is_min, int32_t* out);
+
+/* ------------------------------------------------------------------ */
+/* Softmax / losses — log_softmax.wgsl, log_softmax_backward.wgsl,      */
+/* nll_loss(_backward).wgsl; F.softmax/F.log_softmax/F.cross_entropy/   */
+/* F.nll_loss (src/nn/functional.ts:79-234, src/nn/losses.ts:18-145).   */
+/* ------------------------------------------------------------------ */
+
+/* y = softmax(x) or log_softmax(x) over the last dim of [rows, cols],
+ * row strides ldx/ldy (>= cols). */
+int tjh_softmax_forward(const float* x, int64_t ldx, float* y, int64_t ldy,
+                        int64_t rows, int64_t cols, int log);
+/* dx from y and dy: softmax: y*(dy - sum(dy*y)); log: dy - exp(y)*sum(dy). */
+int tjh_softmax_backward(const float* dy, const float* y, float* dx,
+                         int64_t rows, int64_t cols, int log);
+/* Fused cross entropy over logits [rows, cols] (row stride ld) with int32
+ * targets: lse[r] = logsumexp(x[r]); loss_rows[r] = lse - x[r, t_r]
+ * (0 for ignore_index).  `out` (1 float) receives the reduction:
+ * 0 none (out unused), 1 mean over non-ignored rows, 2 sum. */
+int tjh_cross_entropy_forward(const float* logits, int64_t ld,
+                              const int32_t* targets, int64_t rows,
+                              int64_t cols, int32_t ignore_index,
+                              float* lse, float* loss_rows, int reduction,
+                              float* out);
+/* dlogits[r,c] = (exp(x - lse) - [c == t_r]) * scale_r, where scale_r =
+ * grad_out[0]/count (mean), grad_out[0] (sum) or grad_out[r] (none); rows
+ * with the ignore target get 0.  dlogits row stride ldd.  accumulate != 0
+ * adds into dlogits. */
+int tjh_cross_entropy_backward(const float* logits, int64_t ld,
+                               const int32_t* targets, const float* lse,
+                               const float* grad_out, int64_t rows,
+                               int64_t cols, int32_t ignore_index,
+                               int reduction, float* dlogits, int64_t ldd,
+                               int accumulate);
+/* nll over log-probs [rows, cols]: loss_rows[r] = -logp[r, t_r]. */
+int tjh_nll_loss_forward(const float* logp, int64_t ld,
+                         const int32_t* targets, int64_t rows, int64_t cols,
+                         int32_t ignore_index, float* loss_rows,
+                         int reduction, float* out);
+/* dlogp = 0 except dlogp[r, t_r] = -scale_r (same scale rule as above). */
+int tjh_nll_loss_backward(const int32_t* targets, const float* grad_out,
+                          int64_t rows, int64_t cols, int32_t ignore_index,
+                          int reduction, float* dlogp);
+
+/* ------------------------------------------------------------------ */
+/* LayerNorm — layernorm.wgsl:14-42, nn.LayerNorm                       */
+/* (src/nn/layernorm.ts:25-119); backward is new (reference has none). */
+/* ------------------------------------------------------------------ */
+
+/* y = (x-mean)*rstd*gamma + beta over the last dim; rstd = 1/sqrt(biased
+ * var + eps).  gamma/beta may be NULL (no affine).  mean/rstd [rows]
+ * are saved for the backward. */
+int tjh_layer_norm_forward(const float* x, const float* gamma,
+                           const float* beta, float* y, float* mean,
+                           float* rstd, int64_t rows, int64_t cols,
+                           float eps);
+/* dx (may be NULL), dgamma, dbeta (may be NULL).  accumulate != 0 adds
+ * dgamma/dbeta into existing values. */
+int tjh_layer_norm_backward(const float* dy, const float* x,
+                            const float* gamma, const float* mean,
+                            const float* rstd, float* dx, float* dgamma,
+                            float* dbeta, int64_t rows, int64_t cols,
+                            int accumulate);
+
+/* ------------------------------------------------------------------ */
+/* Embedding / indexing — embedding.wgsl:13-27, index_select.wgsl,      */
+/* Tensor.gather/argmax/nonzero, F.one_hot (src/nn/embedding.ts:25-101, */
+/* Tensor.ts:1242-1345, 2651-2705, src/nn/functional.ts:764-796).       */
+/* ------------------------------------------------------------------ */
+
+/* out[i,:] = weight[clamp(ids[i], 0, num-1), :] (embedding.wgsl:24). */
+int tjh_embedding_forward(const float* weight, int64_t num, int64_t dim,
+                          const int32_t* ids, int64_t n, float* out);
+/* dweight[v,:] (+)= sum over i with clamp(ids[i]) == v of dout[i,:], summed
+ * in increasing i (deterministic). accumulate == 0 zero-fills dweight. */
+int tjh_embedding_backward(const float* dout, const int32_t* ids,
+                           int64_t n, int64_t dim, float* dweight,
+                           int64_t num, int accumulate);
+/* x viewed [outer, src_len, inner]; out [outer, n_idx, inner] =
+ * x[:, idx[j], :]; negative indices wrap once; out-of-range is an error
+ * reported by the host check (index_select.wgsl:20-55). */
+int tjh_index_select(const float* x, int64_t outer, int64_t src_len,
+                     int64_t inner, const int32_t* idx, int64_t n_idx,
+                     float* out);
+/* backward of index_select: dx[:, idx[j], :] += dout[:, j, :] (dx must be
+ * zeroed by the caller); deterministic (sums in increasing j). */
+int tjh_index_add(float* dx, int64_t outer, int64_t src_len, int64_t inner,
+                  const int32_t* idx, int64_t n_idx, const float* dout);
+/* gather along `dim` of a contiguous [outer, src_len, inner] source by an
+ * index of shape [outer, idx_len, inner] (Tensor.ts:2651-2705); negative
+ * indices wrap (Tensor.ts:2686-2687). */
+int tjh_gather(const float* x, int64_t outer, int64_t src_len,
+               int64_t inner, const int32_t* idx, int64_t idx_len,
+               float* out);
+/* scatter_add: dx[o, idx[o,j,i], i] += src[o,j,i] (deterministic). */
+int tjh_scatter_add(float* dx, int64_t outer, int64_t dst_len,
+                    int64_t inner, const int32_t* idx, int64_t idx_len,
+                    const float* src);
+/* one_hot: out[i, c] = (round(x[i]) == c) for 0 <= round(x[i]) < classes,
+ * else the row stays zero (src/nn/functional.ts:786-791).  x is float
+ * (torch.js passes values as f32). */
+int tjh_one_hot(const float* x, int64_t n, int64_t classes, float* out);
+int tjh_one_hot_i32(const int32_t* x, int64_t n, int64_t classes,
+                    float* out);
+/* nonzero in row-major order (Tensor.ts:1323-1345): *count receives nnz
+ * (blocking), out [nnz, ndim] int32 must hold max_out rows. */
+int tjh_nonzero(const float* x, int ndim, const int64_t* shape,
+                int32_t* out, int64_t max_out, int64_t* count);
+
+/* ------------------------------------------------------------------ */
+/* Dense contractions — matmul.wgsl:17-50 / Tensor.matmul, bmm, Linear  */
+/* (Tensor.ts:2132-2331, src/nn/linear.ts:43-66): fp32 MFMA GEMM.       */
+/* ------------------------------------------------------------------ */
+
+/* C[b] = alpha * op(A[b]) . op(B[b]) + beta * C[b] (+ bias), row-major;
+ * op(X) = X^T when trans != 0.  A is [M,K] (or [K,M] when transA), B is
+ * [K,N] (or [N,K] when transB); lda/ldb/ldc are row strides; strides
+ * between batch items may be 0 (broadcast).  bias_mode: 0 none, 1 bias[N]
+ * added to every row, 2 bias[M] added to every column.  beta == 0 never
+ * reads C. */
+int tjh_gemm(int transA, int transB, int64_t M, int64_t N, int64_t K,
+             float alpha, const float* A, int64_t lda, int64_t strideA,
+             const float* B, int64_t ldb, int64_t strideB, float beta,
+             float* C, int64_t ldc, int64_t strideC, int64_t batch,
+             const float* bias, int bias_mode);
+
+/* ------------------------------------------------------------------ */
+/* Attention — F.scaled_dot_product_attention                           */
+/* (src/nn/functional.ts:866-890), MultiheadAttention                   */
+/* (src/nn/attention.ts:112-271).  Flash-style: O(T) extra memory.      */
+/* ------------------------------------------------------------------ */
+
+/* q [B,H,Tq,D], k/v [B,H,Tk,D] given by strides (elements) for the B, H
+ * and T axes; D is contiguous.  o written with its own strides.  lse
+ * [B,H,Tq] (contiguous) saved for the backward.  causal masks key j >
+ * query i (top-left aligned, as torch's is_causal). */
+int tjh_sdpa_forward(const float* q, const float* k, const float* v,
+                     float* o, float* lse, int64_t B, int64_t H, int64_t Tq,
+                     int64_t Tk, int64_t D, const int64_t* q_strides,
+                     const int64_t* k_strides, const int64_t* v_strides,
+                     const int64_t* o_strides, float scale, int causal);
+/* dq/dk/dv written (not accumulated).  Every tensor has its own strides
+ * for the B, H, T axes (D contiguous): strides[0..4] = q, k, v, o, do_;
+ * strides[5..7] = dq, dk, dv; each entry points at 3 int64. */
+int tjh_sdpa_backward(const float* q, const float* k, const float* v,
+                      const float* o, const float* do_, const float* lse,
+                      float* dq, float* dk, float* dv, int64_t B, int64_t H,
+                      int64_t Tq, int64_t Tk, int64_t D,
+                      const int64_t* const* strides, float scale, int causal);
+
+/* ------------------------------------------------------------------ */
+/* Convolution — conv.wgsl:25-60, conv_backward.wgsl:24-119, F.conv2d   */
+/* (src/nn/functional.ts:438-660): NCHW, implicit GEMM on MFMA.         */
+/* ------------------------------------------------------------------ */
+
+typedef struct {
+  int64_t n, c, h, w;        /* input                                    */
+  int64_t oc, kh, kw;        /* weight [oc, c/groups, kh, kw]            */
+  int64_t stride_h, stride_w, pad_h, pad_w, dil_h, dil_w, groups;
+  int64_t oh, ow;            /* output spatial size (filled by caller)   */
+} tjh_conv2d_desc;
+
+int tjh_conv2d_forward(const tjh_conv2d_desc* d, const float* x,
+                       const float* w, const float* bias, float* y);
+/* dx = conv_transpose(dy, w) (written, not accumulated). */
+int tjh_conv2d_backward_input(const tjh_conv2d_desc* d, const float* dy,
+                              const float* w, float* dx);
+/* dw (+)= correlation of x and dy; accumulate != 0 adds. */
+int tjh_conv2d_backward_weight(const tjh_conv2d_desc* d, const float* dy,
+                               const float* x, float* dw, int accumulate);
+
+/* ------------------------------------------------------------------ */
+/* Optimizers — Adam.step / AdamW.step (src/optim/adam.ts:46-133,       */
+/* src/optim/adamw.ts:46-154) as ONE fused multi-tensor launch.         */
+/* ------------------------------------------------------------------ */
+
+/* For each tensor t (host arrays of n_tensors device pointers):
+ *   Adam  (decoupled == 0): g' = g + f32(wd)*p           (adam.ts:62-63)
+ *   AdamW (decoupled != 0): g' = g
+ *   m = f32(b1)*m + f32(1-b1)*g'                         (adam.ts:82)
+ *   v = f32(b2)*v + f32(1-b2)*(g'*g')                    (adam.ts:85)
+ *   denom = sqrt(v / f32(bc2)) + f32(eps), bc_i = 1 - b_i^step[t]
+ *                                                         (adam.ts:96)
+ *   AdamW: p = p*(1 - lr*wd)                             (adamw.ts:129)
+ *   p = p - (lr/bc1) * m / denom                         (adam.ts:114)
+ * m, v and denom are rounded to fp32 after every operation (the reference
+ * computes them as separate fp32 tensor ops); the parameter update is
+ * evaluated in double and rounded once, as the reference's JS loop does
+ * (adam.ts:104-120, adamw.ts:114-133).  The hyper-parameters are doubles
+ * (JS numbers). */
+int tjh_adam_step(int n_tensors, float* const* params,
+                  const float* const* grads, float* const* exp_avg,
+                  float* const* exp_avg_sq, const int64_t* numels,
+                  const int64_t* steps, double lr, double beta1,
+                  double beta2, double eps, double weight_decay,
+                  int decoupled);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* TORCHJS_HIP_H */

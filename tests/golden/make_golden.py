@@ -1,0 +1,279 @@
+"""Writes tests/golden/*.npz: known-answer vectors for the oracle.
+
+The vectors come from PyTorch 2.x on the CPU in float64 (a library that
+implements the same `@pytorch` contracts torch.js declares; it is not the
+reference, which is TypeScript/WGSL and cannot run here).  Inputs are
+small and seeded; every file holds inputs and expected outputs only.
+
+    python tests/golden/make_golden.py
+"""
+import math
+import os
+
+import numpy as np
+import torch
+
+OUT = os.path.dirname(os.path.abspath(__file__))
+torch.set_default_dtype(torch.float64)
+
+
+def t(a, grad=False):
+    return torch.tensor(np.asarray(a, dtype=np.float64), requires_grad=grad)
+
+
+def save(name, **arrays):
+    np.savez_compressed(os.path.join(OUT, name + ".npz"),
+                        **{k: np.asarray(v.detach().numpy() if torch.is_tensor(v) else v)
+                           for k, v in arrays.items()})
+
+
+def unary_ops(rng):
+    x = rng.uniform(-3, 3, size=64)
+    xp = rng.uniform(0.1, 3, size=64)
+    g = rng.standard_normal(64)
+    d = {"x": x, "xp": xp, "g": g}
+    fns = {
+        "neg": (torch.neg, x), "exp": (torch.exp, x), "log": (torch.log, xp),
+        "sqrt": (torch.sqrt, xp), "rsqrt": (torch.rsqrt, xp), "tanh": (torch.tanh, x),
+        "sigmoid": (torch.sigmoid, x), "relu": (torch.relu, x),
+        "gelu": (lambda v: torch.nn.functional.gelu(v), x), "square": (torch.square, x),
+        "reciprocal": (torch.reciprocal, xp), "erf": (torch.erf, x), "abs": (torch.abs, x),
+        "sin": (torch.sin, x), "cos": (torch.cos, x), "silu": (torch.nn.functional.silu, x),
+    }
+    for name, (fn, inp) in fns.items():
+        a = t(inp, True)
+        y = fn(a)
+        y.backward(t(g))
+        d["fwd_" + name] = y
+        d["bwd_" + name] = a.grad
+    save("unary", **d)
+
+
+def binary_ops(rng):
+    a = rng.uniform(0.5, 2.0, size=(3, 4, 5))
+    b = rng.uniform(0.5, 2.0, size=(4, 1))
+    g = rng.standard_normal((3, 4, 5))
+    d = {"a": a, "b": b, "g": g}
+    for name, fn in {"add": torch.add, "sub": torch.sub, "mul": torch.mul, "div": torch.div,
+                     "pow": torch.pow}.items():
+        ta, tb = t(a, True), t(b, True)
+        y = fn(ta, tb)
+        y.backward(t(g))
+        d["fwd_" + name], d["ga_" + name], d["gb_" + name] = y, ta.grad, tb.grad
+    save("binary", **d)
+
+
+def reductions(rng):
+    x = rng.standard_normal((4, 5, 6))
+    d = {"x": x}
+    d["sum_all"] = t(x).sum()
+    d["sum_1"] = t(x).sum(1)
+    d["mean_02"] = t(x).mean((0, 2))
+    d["max_2"] = t(x).amax(2)
+    d["argmax_1"] = t(x).argmax(1).to(torch.int32)
+    ta = t(x, True)
+    ta.mean((0, 2)).backward(t(rng.standard_normal(5)))
+    d["g_mean_02"] = ta.grad
+    save("reduce", **d)
+
+
+def softmax_losses(rng):
+    x = rng.standard_normal((6, 10)) * 3
+    g = rng.standard_normal((6, 10))
+    tgt = np.array([3, 0, 9, -100, 5, 1])
+    d = {"x": x, "g": g, "t": tgt}
+    for name, fn in {"softmax": lambda v: torch.softmax(v, -1),
+                     "log_softmax": lambda v: torch.log_softmax(v, -1)}.items():
+        a = t(x, True)
+        y = fn(a)
+        y.backward(t(g))
+        d["fwd_" + name], d["bwd_" + name] = y, a.grad
+    for red in ("mean", "sum", "none"):
+        a = t(x, True)
+        loss = torch.nn.functional.cross_entropy(a, torch.tensor(tgt), reduction=red)
+        gl = t(rng.standard_normal(6)) if red == "none" else t(1.7)
+        loss.backward(gl)
+        d["ce_" + red], d["ce_g_" + red], d["ce_dx_" + red] = loss, gl, a.grad
+    a = t(x, True)
+    lp = torch.log_softmax(a, -1)
+    nll = torch.nn.functional.nll_loss(lp, torch.tensor(tgt))
+    nll.backward()
+    d["nll"], d["nll_dx"] = nll, a.grad
+    save("softmax_losses", **d)
+
+
+def layer_norm(rng):
+    x = rng.standard_normal((5, 12)) * 2 + 1
+    w = rng.standard_normal(12)
+    b = rng.standard_normal(12)
+    g = rng.standard_normal((5, 12))
+    tx, tw, tb = t(x, True), t(w, True), t(b, True)
+    y = torch.nn.functional.layer_norm(tx, (12,), tw, tb, 1e-5)
+    y.backward(t(g))
+    save("layer_norm", x=x, w=w, b=b, g=g, y=y, dx=tx.grad, dw=tw.grad, db=tb.grad)
+
+
+def embedding_index(rng):
+    w = rng.standard_normal((7, 4))
+    ids = np.array([[1, 6, 1], [0, 1, 3]])
+    g = rng.standard_normal((2, 3, 4))
+    tw = t(w, True)
+    y = torch.nn.functional.embedding(torch.tensor(ids), tw)
+    y.backward(t(g))
+    x = rng.standard_normal((4, 5))
+    idx = np.array([4, 0, 4, 2])
+    tx = t(x, True)
+    ys = tx.index_select(1, torch.tensor(idx))
+    gs = rng.standard_normal(ys.shape)
+    ys.backward(t(gs))
+    gidx = np.array([[0, 4, 4], [1, 1, 0], [3, 2, 2], [4, 0, 1]])
+    tx2 = t(x, True)
+    yg = torch.gather(tx2, 1, torch.tensor(gidx))
+    gg = rng.standard_normal(yg.shape)
+    yg.backward(t(gg))
+    save("embedding_index", w=w, ids=ids, g=g, y=y, dw=tw.grad, x=x, idx=idx, ys=ys, gs=gs,
+         dxs=tx.grad, gidx=gidx, yg=yg, gg=gg, dxg=tx2.grad)
+
+
+def matmul_linear(rng):
+    a = rng.standard_normal((2, 3, 4, 5))
+    b = rng.standard_normal((3, 5, 6))
+    g = rng.standard_normal((2, 3, 4, 6))
+    ta, tb = t(a, True), t(b, True)
+    y = ta @ tb
+    y.backward(t(g))
+    x = rng.standard_normal((2, 3, 5))
+    w = rng.standard_normal((4, 5))
+    bb = rng.standard_normal(4)
+    gl = rng.standard_normal((2, 3, 4))
+    tx, tw, tbb = t(x, True), t(w, True), t(bb, True)
+    yl = torch.nn.functional.linear(tx, tw, tbb)
+    yl.backward(t(gl))
+    save("matmul_linear", a=a, b=b, g=g, y=y, ga=ta.grad, gb=tb.grad, x=x, w=w, bias=bb, gl=gl,
+         yl=yl, dx=tx.grad, dw=tw.grad, dbias=tbb.grad)
+
+
+def attention(rng):
+    d = {}
+    for causal in (False, True):
+        q = rng.standard_normal((2, 3, 7, 8))
+        k = rng.standard_normal((2, 3, 7, 8))
+        v = rng.standard_normal((2, 3, 7, 8))
+        g = rng.standard_normal((2, 3, 7, 8))
+        tq, tk, tv = t(q, True), t(k, True), t(v, True)
+        y = torch.nn.functional.scaled_dot_product_attention(tq, tk, tv, is_causal=causal)
+        y.backward(t(g))
+        s = "c" if causal else "n"
+        d.update({"q" + s: q, "k" + s: k, "v" + s: v, "g" + s: g, "y" + s: y, "dq" + s: tq.grad,
+                  "dk" + s: tk.grad, "dv" + s: tv.grad})
+    save("attention", **d)
+
+
+def conv(rng):
+    d = {}
+    cases = {"a": dict(stride=1, padding=1, dilation=1, groups=1, cin=3, cout=4),
+             "b": dict(stride=2, padding=1, dilation=1, groups=1, cin=4, cout=6),
+             "c": dict(stride=1, padding=2, dilation=2, groups=2, cin=4, cout=6)}
+    for s, c in cases.items():
+        x = rng.standard_normal((2, c["cin"], 7, 6))
+        w = rng.standard_normal((c["cout"], c["cin"] // c["groups"], 3, 3))
+        b = rng.standard_normal(c["cout"])
+        tx, tw, tb = t(x, True), t(w, True), t(b, True)
+        y = torch.nn.functional.conv2d(tx, tw, tb, c["stride"], c["padding"], c["dilation"],
+                                       c["groups"])
+        g = rng.standard_normal(y.shape)
+        y.backward(t(g))
+        d.update({"x" + s: x, "w" + s: w, "b" + s: b, "g" + s: g, "y" + s: y, "dx" + s: tx.grad,
+                  "dw" + s: tw.grad, "db" + s: tb.grad,
+                  "cfg" + s: np.array([c["stride"], c["padding"], c["dilation"], c["groups"]])})
+    save("conv2d", **d)
+
+
+def optim(rng):
+    d = {}
+    for name, cls, wd in (("adam", torch.optim.Adam, 0.01), ("adamw", torch.optim.AdamW, 0.1)):
+        p0 = rng.standard_normal(50)
+        p = t(p0, True)
+        opt = cls([p], lr=1e-2, betas=(0.9, 0.999), eps=1e-8, weight_decay=wd)
+        gs = rng.standard_normal((3, 50))
+        for i in range(3):
+            p.grad = t(gs[i])
+            opt.step()
+        d.update({name + "_p0": p0, name + "_g": gs, name + "_p3": p})
+    save("optim", **d)
+
+
+def models(rng):
+    """Tiny instances of the workloads through torch autograd."""
+    d = {}
+    # chain
+    x = rng.standard_normal((8, 12))
+    bias = rng.standard_normal(12)
+    y = rng.uniform(-1, 1, (8, 12))
+    tx, tb, ty = t(x, True), t(bias, True), t(y, True)
+    loss = (torch.nn.functional.gelu(tx + tb) * ty).sum(0).mean()
+    loss.backward()
+    d.update(chain_x=x, chain_bias=bias, chain_y=y, chain_loss=loss, chain_dx=tx.grad,
+             chain_dbias=tb.grad, chain_dy=ty.grad)
+    # tiny GPT-2 (2 layers, d=16, 2 heads, vocab 23, ctx 8)
+    V, C, D, H, Lr = 23, 8, 16, 2, 2
+    P = {"wte.weight": rng.standard_normal((V, D)) * 0.1, "wpe.weight": rng.standard_normal((C, D)) * 0.1,
+         "ln_f.weight": 1 + 0.1 * rng.standard_normal(D), "ln_f.bias": 0.1 * rng.standard_normal(D)}
+    for i in range(Lr):
+        pre = "h.%d." % i
+        for nm, shp in (("ln_1.weight", (D,)), ("ln_1.bias", (D,)), ("attn.c_attn.weight", (3 * D, D)),
+                        ("attn.c_attn.bias", (3 * D,)), ("attn.c_proj.weight", (D, D)),
+                        ("attn.c_proj.bias", (D,)), ("ln_2.weight", (D,)), ("ln_2.bias", (D,)),
+                        ("mlp.c_fc.weight", (4 * D, D)), ("mlp.c_fc.bias", (4 * D,)),
+                        ("mlp.c_proj.weight", (D, 4 * D)), ("mlp.c_proj.bias", (D,))):
+            base = 1.0 if nm.endswith("ln_1.weight") or nm.endswith("ln_2.weight") else 0.0
+            P[pre + nm] = base + rng.standard_normal(shp) * 0.2
+    T = {k: t(v, True) for k, v in P.items()}
+    ids = rng.integers(0, V, size=(2, C + 1))
+    F = torch.nn.functional
+    inp, tgt = torch.tensor(ids[:, :-1]), torch.tensor(ids[:, 1:])
+    h = F.embedding(inp, T["wte.weight"]) + T["wpe.weight"][:C][None]
+    for i in range(Lr):
+        pre = "h.%d." % i
+        a = F.layer_norm(h, (D,), T[pre + "ln_1.weight"], T[pre + "ln_1.bias"])
+        qkv = F.linear(a, T[pre + "attn.c_attn.weight"], T[pre + "attn.c_attn.bias"])
+        q, k, v = qkv.split(D, 2)
+        sh = lambda z: z.view(2, C, H, D // H).transpose(1, 2)
+        o = F.scaled_dot_product_attention(sh(q), sh(k), sh(v), is_causal=True)
+        o = o.transpose(1, 2).reshape(2, C, D)
+        h = h + F.linear(o, T[pre + "attn.c_proj.weight"], T[pre + "attn.c_proj.bias"])
+        a = F.layer_norm(h, (D,), T[pre + "ln_2.weight"], T[pre + "ln_2.bias"])
+        m = F.linear(F.gelu(F.linear(a, T[pre + "mlp.c_fc.weight"], T[pre + "mlp.c_fc.bias"])),
+                     T[pre + "mlp.c_proj.weight"], T[pre + "mlp.c_proj.bias"])
+        h = h + m
+    h = F.layer_norm(h, (D,), T["ln_f.weight"], T["ln_f.bias"])
+    logits = F.linear(h, T["wte.weight"])
+    loss = F.cross_entropy(logits.reshape(-1, V), tgt.reshape(-1))
+    loss.backward()
+    d["gpt_ids"] = ids
+    d["gpt_cfg"] = np.array([V, C, D, H, Lr])
+    d["gpt_loss"] = loss
+    for k, v in P.items():
+        d["gpt_p:" + k] = v
+        d["gpt_g:" + k] = T[k].grad
+    save("models", **d)
+
+
+def main():
+    rng = np.random.default_rng(20261201)
+    unary_ops(rng)
+    binary_ops(rng)
+    reductions(rng)
+    softmax_losses(rng)
+    layer_norm(rng)
+    embedding_index(rng)
+    matmul_linear(rng)
+    attention(rng)
+    conv(rng)
+    optim(rng)
+    models(rng)
+    print("wrote", sorted(f for f in os.listdir(OUT) if f.endswith(".npz")))
+
+
+if __name__ == "__main__":
+    main()

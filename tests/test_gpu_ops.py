@@ -1,0 +1,487 @@
+"""Parity of every hot-path kernel with the oracle on identical seeded
+inputs (MI355X).  Tolerances: integer / index work bit-exact; fp32
+elementwise rtol 1e-5; reductions, GEMM, attention, conv rtol 1e-4 /
+atol 1e-5 (reduction order differs from the float64 oracle)."""
+import ctypes
+
+import numpy as np
+import pytest
+
+from oracle import ops, rng
+
+pytestmark = pytest.mark.gpu
+
+EW = dict(rtol=1e-5, atol=1e-6)
+RED = dict(rtol=1e-4, atol=1e-5)
+
+
+def f32(a):
+    return np.asarray(a, dtype=np.float32)
+
+
+def check(got, want, **tol):
+    np.testing.assert_allclose(np.asarray(got, dtype=np.float64), np.asarray(want, dtype=np.float64),
+                               **tol)
+
+
+def grad_of(torch, fn, *arrays):
+    """Runs fn on leaf tensors, backprops a seeded upstream grad, returns
+    (output, upstream, grads)."""
+    ts = [torch.tensor(f32(a), requires_grad=True) for a in arrays]
+    out = fn(*ts)
+    g = np.random.default_rng(99).standard_normal(out.shape).astype(np.float32)
+    out.backward(torch.tensor(g))
+    return out.numpy(), g, [t.grad.numpy() if t.grad is not None else None for t in ts]
+
+
+# ------------------------------------------------------------------ runtime
+
+
+def test_device_is_gfx950(torch):
+    info = torch.hip.device_info()
+    assert info["arch"].startswith("gfx950"), info
+    assert info["warp_size"] == 64
+
+
+def test_roundtrip_and_allocator(torch):
+    a = np.arange(1000, dtype=np.float32) - 500.5
+    t = torch.tensor(a)
+    assert np.array_equal(t.numpy(), a)
+    s0 = torch.hip.memory_stats()
+    for _ in range(5):
+        u = torch.zeros(1 << 20)
+        del u
+    s1 = torch.hip.memory_stats()
+    assert s1["device_mallocs"] - s0["device_mallocs"] <= 1  # cached blocks are reused
+    assert s1["peak_bytes"] >= s1["active_bytes"]
+    ints = torch.tensor(np.array([3, -7, 2 ** 30], dtype=np.int32))
+    assert ints.dtype == "int32" and ints.numpy().tolist() == [3, -7, 2 ** 30]
+    assert torch.tensor([-0.0, 1.5]).toArray() == [0.0, 1.5]
+
+
+def test_rng_matches_oracle_stream(torch):
+    torch.manual_seed(1234)
+    u = torch.rand(10007).numpy()
+    n = torch.randn(4099).numpy()
+    s1 = rng.lcg_next(1234)
+    s2 = rng.lcg_next(s1)
+    assert np.array_equal(u, rng.rand(10007, s1))  # integer stream + exact scaling
+    check(n, rng.randn(4099, s2), rtol=1e-5, atol=2e-6)
+
+
+# ------------------------------------------------------------------ elementwise
+
+
+UNARY = ["neg", "exp", "log", "sqrt", "rsqrt", "tanh", "sigmoid", "relu", "gelu", "square",
+         "reciprocal", "erf", "abs", "sin", "cos", "silu", "softplus"]
+
+
+@pytest.mark.parametrize("n", [1, 7, 4099, 1 << 20])
+@pytest.mark.parametrize("op", UNARY)
+def test_unary_fwd_bwd(torch, op, n):
+    r = np.random.default_rng(n)
+    pos = op in ("log", "sqrt", "rsqrt", "reciprocal")
+    x = f32(r.uniform(0.1, 4, n) if pos else r.uniform(-5, 5, n))
+    out, g, (gx,) = grad_of(torch, lambda t: getattr(t, op)(), x)
+    check(out, ops.unary(op, x), **EW)
+    check(gx, ops.unary_backward(op, g, x), rtol=2e-5, atol=2e-6)
+
+
+def test_unary_on_unaligned_view(torch):
+    x = f32(np.random.default_rng(0).uniform(-3, 3, 1001))
+    t = torch.tensor(x)[1:]  # offset by one float: not 16-byte aligned
+    check(t.gelu().numpy(), ops.gelu(x[1:]), **EW)
+    check(t.exp().numpy(), np.exp(x[1:].astype(np.float64)), **EW)
+
+
+@pytest.mark.parametrize("sa,sb", [((64, 33), (64, 33)), ((4096, 4096), (4096,)),
+                                   ((7, 5), (7, 1)), ((3, 4, 5), (4, 1)), ((6,), ()),
+                                   ((2, 1, 5), (3, 1)), ((1, 8), (8, 1))])
+@pytest.mark.parametrize("op", ["add", "sub", "mul", "div", "pow"])
+def test_binary_broadcast_fwd_bwd(torch, op, sa, sb):
+    if op == "pow" and sa == (4096, 4096):
+        pytest.skip("pow backward over 16M elements adds nothing over the small cases")
+    r = np.random.default_rng(len(sa) * 7 + len(sb))
+    a = f32(r.uniform(0.5, 2.0, sa))
+    b = f32(r.uniform(0.5, 2.0, sb))
+    out, g, (ga, gb) = grad_of(torch, lambda x, y: getattr(x, op)(y), a, b)
+    check(out, ops.binary(op, a, b), **EW)
+    ra, rb = ops.binary_backward(op, g, a, b)
+    tol = RED if (ra.size < g.size or rb.size < g.size) else EW
+    check(ga, ra, **tol)
+    check(gb, rb, **tol)
+
+
+@pytest.mark.parametrize("op,s", [("add", 2.5), ("sub", -1.0), ("mul", 0.3), ("div", 7.0),
+                                  ("pow", 2.0), ("pow", 3.0), ("pow", 0.5)])
+def test_scalar_ops(torch, op, s):
+    x = f32(np.random.default_rng(3).uniform(0.2, 3, 5003))
+    out, g, (gx,) = grad_of(torch, lambda t: getattr(t, op)(s), x)
+    if op == "pow":
+        want = ops.pow_scalar(x, s)
+        if s == 2.0:  # repeated multiply: exactly x*x in float32
+            assert np.array_equal(out, x * x)
+        dwant = g * s * ops.pow_scalar(x, s - 1)
+    else:
+        want = ops.binary(op, x, s)
+        dwant = ops.binary_backward(op, g, x, np.float64(s))[0]
+    check(out, want, **EW)
+    check(gx, dwant, **EW)
+
+
+def test_reverse_scalar_and_masked_fill(torch):
+    x = f32(np.random.default_rng(4).uniform(0.5, 2, (6, 9)))
+    t = torch.tensor(x, requires_grad=True)
+    y = (1.0 - t) + (2.0 / t)
+    y.sum().backward()
+    check(y.numpy(), 1.0 - x.astype(np.float64) + 2.0 / x, **EW)
+    check(t.grad.numpy(), -1.0 - 2.0 / x.astype(np.float64) ** 2, **EW)
+    mask = np.triu(np.ones((6, 9)), 1)
+    m = torch.tensor(mask.astype(np.uint8), dtype="uint8")
+    t2 = torch.tensor(x, requires_grad=True)
+    z = t2.masked_fill(m, -1e9)
+    z.backward(torch.ones(6, 9))
+    assert np.array_equal(z.numpy(), np.where(mask > 0, np.float32(-1e9), x))
+    assert np.array_equal(t2.grad.numpy(), (1 - mask).astype(np.float32))
+
+
+# ------------------------------------------------------------------ reductions
+
+
+@pytest.mark.parametrize("shape,dim", [((16777216,), None), ((4096, 4096), 0), ((4096, 4096), 1),
+                                       ((3, 5, 7), (0, 2)), ((8, 1024, 768), (0, 1)),
+                                       ((1, 50257), 1), ((37, 3), 1)])
+def test_sum_mean(torch, shape, dim):
+    x = f32(np.random.default_rng(5).standard_normal(shape))
+    t = torch.tensor(x, requires_grad=True)
+    s = t.sum(dim)
+    m = t.mean(dim)
+    dims = None if dim is None else (dim if isinstance(dim, tuple) else (dim,))
+    check(s.numpy(), ops.reduce("sum", x, dims), rtol=1e-4, atol=1e-5 * np.sqrt(x.size))
+    check(m.numpy(), ops.reduce("mean", x, dims), **RED)
+    m.backward(torch.ones(*m.shape))
+    cnt = x.size // max(1, m.numel())
+    assert np.array_equal(t.grad.numpy(), np.full(shape, np.float32(1.0 / cnt)))
+
+
+def test_max_min_argmax(torch):
+    x = f32(np.random.default_rng(6).integers(-3, 4, (33, 65)))  # many ties
+    t = torch.tensor(x)
+    check(t.amax(1).numpy(), x.max(1), rtol=0, atol=0)
+    check(t.amin(0).numpy(), x.min(0), rtol=0, atol=0)
+    assert np.array_equal(t.argmax(1).numpy(), ops.argmax(x, 1))
+    assert np.array_equal(t.argmin(0).numpy(), ops.argmax(x, 0, is_min=True))
+    assert t.argmax().item() == int(ops.argmax(x))
+    big = f32(np.random.default_rng(7).standard_normal((64, 50257)))
+    assert np.array_equal(torch.tensor(big).argmax(-1).numpy(), ops.argmax(big, 1))
+
+
+# ------------------------------------------------------------------ softmax / losses
+
+
+@pytest.mark.parametrize("shape", [(64, 10), (96, 1024), (5, 50257), (3, 4, 7)])
+@pytest.mark.parametrize("log", [False, True])
+def test_softmax(torch, shape, log):
+    x = f32(np.random.default_rng(8).standard_normal(shape) * 4)
+    fn = (lambda t: t.log_softmax(-1)) if log else (lambda t: t.softmax(-1))
+    out, g, (gx,) = grad_of(torch, fn, x)
+    y = ops.log_softmax(x) if log else ops.softmax(x)
+    check(out, y, **RED)
+    want = ops.log_softmax_backward(g, y) if log else ops.softmax_backward(g, y)
+    check(gx, want, **RED)
+
+
+def test_softmax_other_dim(torch):
+    x = f32(np.random.default_rng(9).standard_normal((4, 6, 5)))
+    out, g, (gx,) = grad_of(torch, lambda t: torch.F.softmax(t, 1), x)
+    y = np.moveaxis(ops.softmax(np.moveaxis(x, 1, -1)), -1, 1)
+    check(out, y, **RED)
+
+
+@pytest.mark.parametrize("rows,cols", [(64, 10), (37, 50257), (128, 1000), (3, 1)])
+@pytest.mark.parametrize("red", ["mean", "sum", "none"])
+def test_cross_entropy(torch, rows, cols, red):
+    r = np.random.default_rng(rows + cols)
+    x = f32(r.standard_normal((rows, cols)) * 2)
+    t = r.integers(0, cols, rows).astype(np.int32)
+    t[::5] = -100  # ignore_index rows
+    xt = torch.tensor(x, requires_grad=True)
+    loss = torch.F.cross_entropy(xt, torch.tensor(t), reduction=red)
+    gl = f32(r.standard_normal(rows)) if red == "none" else np.float32(1.3)
+    loss.backward(torch.tensor(gl))
+    check(loss.numpy(), ops.cross_entropy(x, t, red), **RED)
+    check(xt.grad.numpy(), ops.cross_entropy_backward(x, t, gl, red), **RED)
+
+
+def test_nll_loss(torch):
+    r = np.random.default_rng(11)
+    lp = ops.log_softmax(r.standard_normal((9, 6))).astype(np.float32)
+    t = r.integers(0, 6, 9).astype(np.int32)
+    xt = torch.tensor(lp, requires_grad=True)
+    loss = torch.F.nll_loss(xt, torch.tensor(t))
+    loss.backward()
+    check(loss.item(), ops.nll_loss(lp, t), **RED)
+    check(xt.grad.numpy(), ops.nll_loss_backward(lp.shape, t), **RED)
+
+
+# ------------------------------------------------------------------ layer norm
+
+
+@pytest.mark.parametrize("rows,cols", [(8192, 768), (5, 33), (300, 3072), (7, 1024)])
+def test_layer_norm(torch, rows, cols):
+    r = np.random.default_rng(rows)
+    x = f32(r.standard_normal((rows, cols)) * 2 + 0.5)
+    w = f32(r.standard_normal(cols))
+    b = f32(r.standard_normal(cols))
+    out, g, (gx, gw, gb) = grad_of(
+        torch, lambda a, ww, bb: torch.F.layer_norm(a, (cols,), ww, bb, 1e-5), x, w, b)
+    y, _, _ = ops.layer_norm(x, w, b)
+    check(out, y, **RED)
+    dx, dw, db = ops.layer_norm_backward(g, x, w)
+    check(gx, dx, rtol=1e-4, atol=1e-4)
+    check(gw, dw, rtol=1e-4, atol=1e-3)
+    check(gb, db, rtol=1e-4, atol=1e-3)
+
+
+# ------------------------------------------------------------------ embedding / indexing
+
+
+@pytest.mark.parametrize("V,D,n", [(50257, 768, 8192), (7, 4, 6), (1000, 9, 20000), (3, 64, 1)])
+def test_embedding(torch, V, D, n):
+    r = np.random.default_rng(V + n)
+    w = f32(r.standard_normal((V, D)))
+    ids = r.integers(0, V, n).astype(np.int32)
+    ids[: n // 3] = ids[0]  # a long run of one id
+    wt = torch.tensor(w, requires_grad=True)
+    out = torch.F.embedding(torch.tensor(ids), wt)
+    assert np.array_equal(out.numpy(), w[ids])  # a gather: bit-exact
+    g = f32(r.standard_normal((n, D)))
+    out.backward(torch.tensor(g))
+    want = ops.embedding_backward(g, ids, V)
+    got = wt.grad.numpy()
+    untouched = np.setdiff1d(np.arange(V), ids)
+    assert np.all(got[untouched] == 0)  # exactly the referenced rows are written
+    check(got, want, rtol=1e-4, atol=1e-4)
+    # deterministic
+    wt.grad = None
+    out2 = torch.F.embedding(torch.tensor(ids), wt)
+    out2.backward(torch.tensor(g))
+    assert np.array_equal(wt.grad.numpy(), got)
+
+
+def test_embedding_clamps_ids(torch):
+    w = f32(np.arange(12).reshape(4, 3))
+    out = torch.F.embedding(torch.tensor(np.array([-5, 0, 3, 99], dtype=np.int32)),
+                            torch.tensor(w))
+    assert np.array_equal(out.numpy(), w[[0, 0, 3, 3]])
+
+
+def test_index_select_gather_nonzero_one_hot(torch):
+    r = np.random.default_rng(12)
+    x = f32(r.standard_normal((4, 5, 3)))
+    idx = np.array([4, 0, 4, -1], dtype=np.int32)
+    out, g, (gx,) = grad_of(torch, lambda t: t.index_select(1, torch.tensor(idx)), x)
+    assert np.array_equal(out, ops.index_select(x, 1, idx).astype(np.float32))
+    check(gx, ops.index_select_backward(g, x.shape, 1, idx), **RED)
+    gidx = r.integers(-5, 5, (4, 6, 3)).astype(np.int32)
+    out, g, (gx,) = grad_of(torch, lambda t: t.gather(1, torch.tensor(gidx)), x)
+    assert np.array_equal(out, ops.gather(x, 1, gidx).astype(np.float32))
+    check(gx, ops.scatter_add(x.shape, 1, gidx, g), **RED)
+    z = f32(r.integers(0, 3, (7, 11)) * (r.random((7, 11)) > 0.6))
+    assert np.array_equal(torch.tensor(z).nonzero().numpy(), ops.nonzero(z))
+    assert torch.tensor(np.zeros((3, 3), np.float32)).nonzero().shape == (0, 2)
+    big = f32(r.random(100000) > 0.999)
+    assert np.array_equal(torch.tensor(big).nonzero().numpy(), ops.nonzero(big))
+    xf = np.array([0.5, 2.4, -1, 7, 1.5], dtype=np.float32)
+    assert np.array_equal(torch.F.one_hot(torch.tensor(xf), 4).numpy(), ops.one_hot(xf, 4))
+    xi = np.array([0, 2, 4], dtype=np.int32)
+    assert np.array_equal(torch.F.one_hot(torch.tensor(xi)).numpy(), ops.one_hot(xi))
+
+
+# ------------------------------------------------------------------ GEMM
+
+
+def _raw_gemm(torch, ta, tb, A, B, M, N, K, alpha=1.0, beta=0.0, C0=None, bias=None, bmode=0):
+    from torchjs_amd import _lib as L
+    a = torch.tensor(A)
+    b = torch.tensor(B)
+    c = torch.tensor(C0 if C0 is not None else np.zeros((M, N), np.float32))
+    bb = torch.tensor(bias) if bias is not None else None
+    lda = A.shape[1]
+    ldb = B.shape[1]
+    L.check(L.lib().tjh_gemm(ta, tb, M, N, K, alpha, a.data_ptr(), lda, 0, b.data_ptr(), ldb, 0,
+                             beta, c.data_ptr(), N, 0, 1, bb.data_ptr() if bb else None, bmode))
+    return c.numpy()
+
+
+@pytest.mark.parametrize("M,N,K", [(67, 45, 23), (128, 128, 16), (256, 384, 768), (1, 1, 1),
+                                   (64, 10, 784), (130, 257, 129), (64, 64, 8192),
+                                   (768, 768, 8192)])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_gemm_layouts(torch, M, N, K, ta, tb):
+    r = np.random.default_rng(M * 7 + N * 3 + K)
+    A = f32(r.standard_normal((K, M) if ta else (M, K)))
+    B = f32(r.standard_normal((N, K) if tb else (K, N)))
+    want = (A.T if ta else A).astype(np.float64) @ (B.T if tb else B).astype(np.float64)
+    got = _raw_gemm(torch, ta, tb, A, B, M, N, K)
+    check(got, want, rtol=1e-4, atol=1e-5 * np.sqrt(K) * 4)
+
+
+def test_gemm_epilogue(torch):
+    r = np.random.default_rng(13)
+    M, N, K = 70, 90, 50
+    A, B = f32(r.standard_normal((M, K))), f32(r.standard_normal((K, N)))
+    C0 = f32(r.standard_normal((M, N)))
+    bn, bm = f32(r.standard_normal(N)), f32(r.standard_normal(M))
+    ref = A.astype(np.float64) @ B
+    check(_raw_gemm(torch, 0, 0, A, B, M, N, K, 0.5, 2.0, C0), 0.5 * ref + 2 * C0, **RED)
+    check(_raw_gemm(torch, 0, 0, A, B, M, N, K, bias=bn, bmode=1), ref + bn, **RED)
+    check(_raw_gemm(torch, 0, 0, A, B, M, N, K, bias=bm, bmode=2), ref + bm[:, None], **RED)
+    # split-K path with beta and bias
+    M, N, K = 64, 96, 6000
+    A, B = f32(r.standard_normal((M, K))), f32(r.standard_normal((K, N)))
+    C0 = f32(r.standard_normal((M, N)))
+    bn = f32(r.standard_normal(N))
+    ref = A.astype(np.float64) @ B
+    check(_raw_gemm(torch, 0, 0, A, B, M, N, K, 1.0, 1.0, C0, bn, 1), ref + C0 + bn, rtol=1e-4,
+          atol=1e-3)
+
+
+def test_matmul_autograd_batched_broadcast(torch):
+    r = np.random.default_rng(14)
+    a = f32(r.standard_normal((2, 3, 4, 5)))
+    b = f32(r.standard_normal((3, 5, 6)))
+    out, g, (ga, gb) = grad_of(torch, lambda x, y: x @ y, a, b)
+    check(out, a.astype(np.float64) @ b, **RED)
+    ra, rb = ops.matmul_backward(g, a, b)
+    check(ga, ra, **RED)
+    check(gb, rb, **RED)
+    # 2-D, vector and transposed-view operands
+    m = f32(r.standard_normal((9, 7)))
+    v = f32(r.standard_normal(7))
+    out, g, (gm, gv) = grad_of(torch, lambda x, y: x @ y, m, v)
+    check(out, m.astype(np.float64) @ v, **RED)
+    check(gm, np.outer(g, v), **RED)
+    check(gv, m.T.astype(np.float64) @ g, **RED)
+    out, g, (gm,) = grad_of(torch, lambda x: x.t() @ x, m)
+    check(out, m.T.astype(np.float64) @ m, **RED)
+    check(gm, m.astype(np.float64) @ (g + g.T), **RED)
+    assert torch.tensor([[1., 2.], [3., 4.]]).matmul(torch.tensor([[5., 6.], [7., 8.]])).tolist() \
+        == [[19., 22.], [43., 50.]]
+
+
+@pytest.mark.parametrize("lead,fin,fout", [((64,), 784, 256), ((8, 128), 768, 2304),
+                                           ((3, 5), 7, 10), ((4,), 768, 50257)])
+def test_linear(torch, lead, fin, fout):
+    r = np.random.default_rng(fin + fout)
+    x = f32(r.standard_normal(lead + (fin,)))
+    w = f32(r.standard_normal((fout, fin)) * 0.05)
+    b = f32(r.standard_normal(fout))
+    out, g, (gx, gw, gb) = grad_of(torch, lambda a, ww, bb: torch.F.linear(a, ww, bb), x, w, b)
+    check(out, ops.linear(x, w, b), rtol=1e-4, atol=1e-4)
+    dx, dw, db = ops.linear_backward(g, x, w)
+    check(gx, dx, rtol=1e-4, atol=1e-4)
+    check(gw, dw, rtol=1e-4, atol=1e-3)
+    check(gb, db, rtol=1e-4, atol=1e-3)
+
+
+# ------------------------------------------------------------------ attention
+
+
+@pytest.mark.parametrize("B,H,T,D,causal", [(2, 3, 7, 8, False), (2, 3, 7, 8, True),
+                                            (1, 12, 130, 64, True), (2, 2, 256, 64, False),
+                                            (1, 1, 1, 64, True)])
+def test_sdpa(torch, B, H, T, D, causal):
+    r = np.random.default_rng(B * T + D)
+    q, k, v = (f32(r.standard_normal((B, H, T, D))) for _ in range(3))
+    out, g, (dq, dk, dv) = grad_of(
+        torch, lambda a, b_, c: torch.F.scaled_dot_product_attention(a, b_, c, is_causal=causal),
+        q, k, v)
+    o, _ = ops.sdpa(q, k, v, causal)
+    check(out, o, rtol=1e-4, atol=1e-5)
+    rq, rk, rv = ops.sdpa_backward(g, q, k, v, causal)
+    check(dq, rq, rtol=1e-4, atol=1e-4)
+    check(dk, rk, rtol=1e-4, atol=1e-4)
+    check(dv, rv, rtol=1e-4, atol=1e-4)
+
+
+def test_sdpa_on_qkv_views(torch):
+    """q/k/v as head-split views of one [B,T,3C] projection (GPT-2 layout)."""
+    r = np.random.default_rng(15)
+    B, T, H, hd = 2, 33, 4, 16
+    C = H * hd
+    qkv = f32(r.standard_normal((B, T, 3 * C)))
+
+    def fn(t):
+        q, k, v = t.split(C, dim=2)
+        sh = lambda z: z.view(B, T, H, hd).transpose(1, 2)
+        y = torch.F.scaled_dot_product_attention(sh(q), sh(k), sh(v), is_causal=True)
+        return y.transpose(1, 2).contiguous().view(B, T, C)
+    out, g, (gqkv,) = grad_of(torch, fn, qkv)
+    qa, ka, va = np.split(qkv.astype(np.float64), 3, axis=-1)
+    sh = lambda z: z.reshape(B, T, H, hd).transpose(0, 2, 1, 3)
+    o, _ = ops.sdpa(sh(qa), sh(ka), sh(va), True)
+    check(out, o.transpose(0, 2, 1, 3).reshape(B, T, C), rtol=1e-4, atol=1e-5)
+    gq, gk, gv = ops.sdpa_backward(sh(g.astype(np.float64)), sh(qa), sh(ka), sh(va), True)
+    un = lambda z: z.transpose(0, 2, 1, 3).reshape(B, T, C)
+    check(gqkv, np.concatenate([un(gq), un(gk), un(gv)], -1), rtol=1e-4, atol=1e-4)
+
+
+def test_sdpa_attn_mask_raises(torch):
+    q = torch.zeros(1, 1, 2, 4)
+    with pytest.raises(NotImplementedError, match="attn_mask not yet implemented"):
+        torch.F.scaled_dot_product_attention(q, q, q, attn_mask=q)
+
+
+# ------------------------------------------------------------------ conv
+
+
+@pytest.mark.parametrize("N,C,H,W,OC,k,s,p,d,grp", [
+    (2, 3, 7, 6, 4, 3, 1, 1, 1, 1), (2, 4, 7, 6, 6, 3, 2, 1, 1, 1), (2, 4, 7, 6, 6, 3, 1, 2, 2, 2),
+    (4, 3, 64, 64, 32, 3, 1, 1, 1, 1), (4, 32, 64, 64, 64, 3, 2, 1, 1, 1), (1, 2, 5, 5, 3, 1, 1, 0, 1, 1)])
+def test_conv2d(torch, N, C, H, W, OC, k, s, p, d, grp):
+    r = np.random.default_rng(N * C + OC)
+    x = f32(r.standard_normal((N, C, H, W)))
+    w = f32(r.standard_normal((OC, C // grp, k, k)) * 0.2)
+    b = f32(r.standard_normal(OC))
+    out, g, (gx, gw, gb) = grad_of(
+        torch, lambda a, ww, bb: torch.F.conv2d(a, ww, bb, s, p, d, grp), x, w, b)
+    check(out, ops.conv2d(x, w, b, s, p, d, grp), rtol=1e-4, atol=1e-4)
+    dx, dw, db = ops.conv2d_backward(g, x, w, s, p, d, grp)
+    check(gx, dx, rtol=1e-4, atol=1e-4)
+    check(gw, dw, rtol=1e-4, atol=2e-3)
+    check(gb, db, rtol=1e-4, atol=2e-3)
+
+
+# ------------------------------------------------------------------ optimizers
+
+
+@pytest.mark.parametrize("cls,decoupled,wd", [("Adam", False, 0.0), ("Adam", False, 0.01),
+                                              ("AdamW", True, 0.1), ("AdamW", True, 0.01)])
+def test_adam_bit_exact(torch, cls, decoupled, wd):
+    """The fused kernel reproduces the reference's rounding exactly: fp32
+    moments, fp64 update rounded once."""
+    r = np.random.default_rng(16)
+    shapes = [(257, 31), (4096,), (3,), (768, 768)]
+    ps = [f32(r.standard_normal(s)) for s in shapes]
+    params = [torch.tensor(p, requires_grad=True) for p in ps]
+    opt = getattr(torch.optim, cls)(params, lr=1e-3, weight_decay=wd)
+    ms = [np.zeros_like(p) for p in ps]
+    vs = [np.zeros_like(p) for p in ps]
+    for step in range(1, 4):
+        gs = [f32(r.standard_normal(s)) for s in shapes]
+        for t, g in zip(params, gs):
+            t.grad = torch.tensor(g)
+        opt.step()
+        for i in range(len(ps)):
+            ps[i], ms[i], vs[i] = ops.adam_step(ps[i], gs[i], ms[i], vs[i], step, lr=1e-3,
+                                                weight_decay=wd, decoupled=decoupled)
+    for t, p, m, v in zip(params, ps, ms, vs):
+        st = opt.state[id(t)]
+        # fp32 moments: bit-exact
+        assert np.array_equal(st["exp_avg"].numpy(), m)
+        assert np.array_equal(st["exp_avg_sq"].numpy(), v)
+        # fp64 update rounded once: equal but for double-rounding ties
+        got = t.numpy()
+        assert (got == p).mean() > 0.999
+        assert np.max(np.abs(got.astype(np.float64) - p)) <= np.abs(p).max() * 2 ** -23

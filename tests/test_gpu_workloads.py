@@ -1,0 +1,162 @@
+"""The benchmark workloads end to end on the 'hip' device against the
+oracle: loss, every parameter gradient and the optimizer step, on seeded
+inputs at the full size where the oracle finishes in seconds, reduced
+otherwise; full-size runs are checked through size-independent properties."""
+import numpy as np
+import pytest
+
+from oracle import models as om
+from oracle import ops
+from oracle.rng import Generator
+
+pytestmark = pytest.mark.gpu
+
+
+def check(got, want, rtol=1e-4, atol=1e-5):
+    np.testing.assert_allclose(np.asarray(got, dtype=np.float64), np.asarray(want, dtype=np.float64),
+                               rtol=rtol, atol=atol)
+
+
+def _params(model):
+    return {k: p.numpy() for k, p in model.named_parameters()}
+
+
+def test_mlp_train_step_full_config(torch):
+    """MLP 784->256->ReLU->10, batch 64, CE, backward + one Adam step (lr 1e-3)."""
+    from torchjs_amd import workloads as W
+    g = Generator(1234)
+    x = g.randn((64, 784))
+    t = g.integers((64,), 10)
+    p = {"0.weight": g.uniform((256, 784), -1 / 28, 1 / 28), "0.bias": g.uniform((256,), -1 / 28, 1 / 28),
+         "2.weight": g.uniform((10, 256), -1 / 16, 1 / 16), "2.bias": g.uniform((10,), -1 / 16, 1 / 16)}
+    model = W.mlp()
+    W.load_params(model, p)
+    opt = torch.optim.Adam(model.parameters(), lr=1e-3)
+    loss = torch.F.cross_entropy(model(torch.tensor(x)), torch.tensor(t))
+    loss.backward()
+    ref_loss, ref_g = om.mlp_loss_and_grads(p, x, t)
+    check(loss.item(), ref_loss)
+    for k, prm in model.named_parameters():
+        check(prm.grad.numpy(), ref_g[k], atol=1e-5)
+    opt.step()
+    for k, prm in model.named_parameters():
+        want, _, _ = ops.adam_step(p[k], prm.grad.numpy(), np.zeros_like(p[k]),
+                                   np.zeros_like(p[k]), 1, lr=1e-3)
+        check(prm.numpy(), want, rtol=0, atol=1e-6)
+
+
+@pytest.mark.parametrize("n", [256, 4096])
+def test_chain_full_config(torch, n):
+    """(x + bias) -> GELU -> * y -> sum(0) -> mean; grads for x, bias, y,
+    at 256^2 and the full 4096^2, against the oracle."""
+    from torchjs_amd import workloads as W
+    g = Generator(99 + n)
+    x = g.randn((n, n))
+    b = g.randn((n,))
+    y = g.uniform((n, n), -1, 1)
+    tx, tb, ty = (torch.tensor(a, requires_grad=True) for a in (x, b, y))
+    loss = W.chain_loss(tx, tb, ty)
+    loss.backward()
+    ref, rg = om.chain_loss_and_grads(x, b, y)
+    check(loss.item(), ref, rtol=1e-4, atol=1e-6)
+    # elementwise grads: rtol 1e-5 with an fp32-epsilon floor for values
+    # near the zero of GELU' (Phi(x) + x phi(x) cancels there)
+    eps32 = 2.0 ** -23
+    check(tx.grad.numpy(), rg["x"], rtol=1e-5, atol=4 * eps32 * np.abs(rg["x"]).max())
+    check(tb.grad.numpy(), rg["bias"], rtol=1e-4, atol=1e-7)
+    check(ty.grad.numpy(), rg["y"], rtol=1e-5, atol=4 * eps32 * np.abs(rg["y"]).max())
+    # the bias gradient is the column sum of the x gradient
+    check(tb.grad.numpy(), tx.grad.numpy().astype(np.float64).sum(0), rtol=1e-4, atol=1e-7)
+
+
+def test_cnn_reduced_batch(torch):
+    """The small CNN at batch 4 (full spatial size 64x64) against the oracle."""
+    from torchjs_amd import workloads as W
+    g = Generator(7)
+    x = g.randn((4, 3, 64, 64))
+    t = g.integers((4,), 10)
+    p = {"conv1.weight": g.uniform((32, 3, 3, 3), -0.19, 0.19), "conv1.bias": g.uniform((32,), -0.19, 0.19),
+         "conv2.weight": g.uniform((64, 32, 3, 3), -0.059, 0.059), "conv2.bias": g.uniform((64,), -0.059, 0.059),
+         "fc.weight": g.uniform((10, 64), -0.125, 0.125), "fc.bias": g.uniform((10,), -0.125, 0.125)}
+    model = W.CNN()
+    W.load_params(model, p)
+    loss = torch.F.cross_entropy(model(torch.tensor(x)), torch.tensor(t))
+    loss.backward()
+    ref, rg = om.cnn_loss_and_grads(p, x, t)
+    check(loss.item(), ref)
+    for k, prm in model.named_parameters():
+        check(prm.grad.numpy(), rg[k], rtol=1e-4, atol=1e-5)
+
+
+def test_transformer_block_reduced(torch):
+    """Pre-LN block (d=768, 12 heads, causal) at B=2, T=128; loss = mean(out)."""
+    from torchjs_amd import workloads as W
+    r = np.random.default_rng(21)
+    p = om.block_params(768, r, std=0.02)
+    x = r.standard_normal((2, 128, 768)).astype(np.float32)
+    blk = W.Block(768, 12)
+    W.load_params(blk, p)
+    tx = torch.tensor(x, requires_grad=True)
+    loss = blk(tx).mean()
+    loss.backward()
+    ref, rg = om.block_loss_and_grads(p, x, 12)
+    check(loss.item(), ref, rtol=1e-4, atol=1e-6)
+    check(tx.grad.numpy(), rg["x"], rtol=1e-4, atol=1e-8)
+    for k, prm in blk.named_parameters():
+        scale = np.abs(rg[k]).max()
+        check(prm.grad.numpy(), rg[k], rtol=1e-3, atol=1e-4 * scale + 1e-9)
+
+
+def test_gpt2_tiny_train_step(torch):
+    """GPT-2 (tied embeddings) at vocab 211 / ctx 64 / d 128 / 4 heads / 2
+    layers: loss, every gradient and the AdamW step."""
+    from torchjs_amd import workloads as W
+    cfg = om.Config(vocab=211, ctx=64, d=128, heads=4, layers=2)
+    r = np.random.default_rng(5)
+    p = om.init_params(cfg, r)
+    ids = r.integers(0, cfg.vocab, (3, cfg.ctx + 1)).astype(np.int32)
+    model = W.GPT2(cfg.vocab, cfg.ctx, cfg.d, cfg.heads, cfg.layers)
+    W.load_params(model, p)
+    opt = torch.optim.AdamW(model.parameters(), lr=6e-4, weight_decay=0.1)
+    loss = model.loss(torch.tensor(ids[:, :-1]), torch.tensor(ids[:, 1:]))
+    loss.backward()
+    ref, rg = om.gpt2_loss_and_grads(cfg, p, ids[:, :-1], ids[:, 1:])
+    check(loss.item(), ref, rtol=1e-5, atol=1e-6)
+    for k, prm in model.named_parameters():
+        scale = np.abs(rg[k]).max()
+        check(prm.grad.numpy(), rg[k], rtol=1e-3, atol=1e-4 * scale + 1e-9)
+    opt.step()
+    new = om.adamw_step(p, {k: prm.grad.numpy() for k, prm in model.named_parameters()},
+                        lr=6e-4, wd=0.1, step=1)
+    for k, prm in model.named_parameters():
+        check(prm.numpy(), new[k], rtol=0, atol=2e-7)
+
+
+def test_gpt2_full_shape_step_properties(torch):
+    """GPT-2 small at B=2, T=1024 (the full per-sequence shape): finite loss
+    near ln(50257) at init, tied-embedding grad = head grad + embedding
+    scatter, AdamW moves every parameter by <= lr * (1 + small)."""
+    from torchjs_amd import workloads as W
+    torch.manual_seed(3)
+    model = W.GPT2()
+    with torch.no_grad():
+        for k, prm in model.named_parameters():
+            if k.endswith("ln_1.weight") or k.endswith("ln_2.weight") or k == "ln_f.weight":
+                continue
+            if k.endswith("bias"):
+                prm.zero_()
+            else:
+                prm.copy_(torch.randn(*prm.shape) * 0.02)
+    r = np.random.default_rng(8)
+    ids = r.integers(0, 50257, (2, 1025)).astype(np.int32)
+    loss = model.loss(torch.tensor(ids[:, :-1]), torch.tensor(ids[:, 1:]))
+    loss.backward()
+    lv = loss.item()
+    assert np.isfinite(lv) and abs(lv - np.log(50257)) < 0.5, lv
+    for k, prm in model.named_parameters():
+        assert prm.grad is not None and np.all(np.isfinite(prm.grad.numpy())), k
+    before = {k: prm.numpy() for k, prm in model.named_parameters()}
+    torch.optim.AdamW(model.parameters(), lr=6e-4, weight_decay=0.1).step()
+    for k, prm in model.named_parameters():
+        d = np.abs(prm.numpy().astype(np.float64) - before[k])
+        assert d.max() <= 6e-4 * 1.01 + 6e-4 * 0.1 * np.abs(before[k]).max(), k

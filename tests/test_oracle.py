@@ -1,0 +1,354 @@
+"""Pins the CPU oracle: golden vectors (PyTorch float64), the literal
+known-answer tests of torch.js's own suite, closed forms, published error
+bounds and finite differences.  CPU only."""
+import math
+
+import numpy as np
+import pytest
+
+from conftest import golden
+from oracle import models as om
+from oracle import ops, rng
+
+RT, AT = 1e-9, 1e-12  # golden vectors vs float64 oracle
+
+
+def close(a, b, rtol=RT, atol=AT):
+    np.testing.assert_allclose(np.asarray(a, dtype=np.float64), np.asarray(b, dtype=np.float64),
+                               rtol=rtol, atol=atol)
+
+
+# ------------------------------------------------------------------ golden
+
+
+def test_unary_golden():
+    z = golden("unary")
+    for op in ["neg", "exp", "log", "sqrt", "rsqrt", "tanh", "sigmoid", "relu", "square",
+               "reciprocal", "abs", "sin", "cos", "silu"]:
+        x = z["xp"] if op in ("log", "sqrt", "rsqrt", "reciprocal") else z["x"]
+        close(ops.unary(op, x), z["fwd_" + op])
+        close(ops.unary_backward(op, z["g"], x), z["bwd_" + op])
+    # erf / GELU follow the reference's A&S 7.1.26 erf: |error| <= 1.5e-7
+    close(ops.unary("erf", z["x"]), z["fwd_erf"], rtol=0, atol=1.5e-7)
+    close(ops.gelu(z["x"]), z["fwd_gelu"], rtol=0, atol=3 * 1.5e-7 * 1.5)
+    close(ops.unary_backward("gelu", z["g"], z["x"]), z["bwd_gelu"], rtol=0,
+          atol=1e-6 * np.abs(z["g"]).max())
+
+
+def test_binary_golden():
+    z = golden("binary")
+    for op in ["add", "sub", "mul", "div", "pow"]:
+        close(ops.binary(op, z["a"], z["b"]), z["fwd_" + op])
+        ga, gb = ops.binary_backward(op, z["g"], z["a"], z["b"])
+        close(ga, z["ga_" + op])
+        close(gb, z["gb_" + op])
+
+
+def test_reduce_golden():
+    z = golden("reduce")
+    close(ops.reduce("sum", z["x"]), z["sum_all"])
+    close(ops.reduce("sum", z["x"], [1]), z["sum_1"])
+    close(ops.reduce("mean", z["x"], [0, 2]), z["mean_02"])
+    close(ops.reduce("max", z["x"], [2]), z["max_2"])
+    assert np.array_equal(ops.argmax(z["x"], 1), z["argmax_1"])
+
+
+def test_softmax_losses_golden():
+    z = golden("softmax_losses")
+    y = ops.softmax(z["x"])
+    close(y, z["fwd_softmax"])
+    close(ops.softmax_backward(z["g"], y), z["bwd_softmax"])
+    ly = ops.log_softmax(z["x"])
+    close(ly, z["fwd_log_softmax"])
+    close(ops.log_softmax_backward(z["g"], ly), z["bwd_log_softmax"])
+    for red in ("mean", "sum", "none"):
+        close(ops.cross_entropy(z["x"], z["t"], red), z["ce_" + red])
+        close(ops.cross_entropy_backward(z["x"], z["t"], z["ce_g_" + red], red), z["ce_dx_" + red])
+    close(ops.nll_loss(ly, z["t"]), z["nll"])
+    d = ops.nll_loss_backward(ly.shape, z["t"])
+    close(ops.log_softmax_backward(d, ly), z["nll_dx"])
+
+
+def test_layer_norm_golden():
+    z = golden("layer_norm")
+    y, _, _ = ops.layer_norm(z["x"], z["w"], z["b"])
+    close(y, z["y"])
+    dx, dw, db = ops.layer_norm_backward(z["g"], z["x"], z["w"])
+    close(dx, z["dx"])
+    close(dw, z["dw"])
+    close(db, z["db"])
+
+
+def test_embedding_index_golden():
+    z = golden("embedding_index")
+    close(ops.embedding(z["w"], z["ids"]), z["y"])
+    close(ops.embedding_backward(z["g"], z["ids"], z["w"].shape[0]), z["dw"])
+    close(ops.index_select(z["x"], 1, z["idx"]), z["ys"])
+    close(ops.index_select_backward(z["gs"], z["x"].shape, 1, z["idx"]), z["dxs"])
+    close(ops.gather(z["x"], 1, z["gidx"]), z["yg"])
+    close(ops.scatter_add(z["x"].shape, 1, z["gidx"], z["gg"]), z["dxg"])
+
+
+def test_matmul_linear_golden():
+    z = golden("matmul_linear")
+    close(z["a"] @ z["b"], z["y"])
+    ga, gb = ops.matmul_backward(z["g"], z["a"], z["b"])
+    close(ga, z["ga"])
+    close(gb, z["gb"])
+    close(ops.linear(z["x"], z["w"], z["bias"]), z["yl"])
+    dx, dw, db = ops.linear_backward(z["gl"], z["x"], z["w"])
+    close(dx, z["dx"])
+    close(dw, z["dw"])
+    close(db, z["dbias"])
+
+
+@pytest.mark.parametrize("s,causal", [("n", False), ("c", True)])
+def test_attention_golden(s, causal):
+    z = golden("attention")
+    o, _ = ops.sdpa(z["q" + s], z["k" + s], z["v" + s], causal=causal)
+    close(o, z["y" + s])
+    dq, dk, dv = ops.sdpa_backward(z["g" + s], z["q" + s], z["k" + s], z["v" + s], causal=causal)
+    close(dq, z["dq" + s])
+    close(dk, z["dk" + s])
+    close(dv, z["dv" + s])
+
+
+@pytest.mark.parametrize("s", ["a", "b", "c"])
+def test_conv2d_golden(s):
+    z = golden("conv2d")
+    st, pad, dil, grp = (int(v) for v in z["cfg" + s])
+    close(ops.conv2d(z["x" + s], z["w" + s], z["b" + s], st, pad, dil, grp), z["y" + s])
+    dx, dw, db = ops.conv2d_backward(z["g" + s], z["x" + s], z["w" + s], st, pad, dil, grp)
+    close(dx, z["dx" + s])
+    close(dw, z["dw" + s])
+    close(db, z["db" + s])
+
+
+@pytest.mark.parametrize("name,decoupled,wd", [("adam", False, 0.01), ("adamw", True, 0.1)])
+def test_optim_golden(name, decoupled, wd):
+    """The float32-rounded oracle step tracks torch's float64 Adam/AdamW to
+    float32 precision over 3 steps."""
+    z = golden("optim")
+    p = z[name + "_p0"].astype(np.float32)
+    m = np.zeros_like(p)
+    v = np.zeros_like(p)
+    for i in range(3):
+        p, m, v = ops.adam_step(p, z[name + "_g"][i], m, v, i + 1, lr=1e-2, weight_decay=wd,
+                                decoupled=decoupled)
+    close(p, z[name + "_p3"], rtol=1e-5, atol=1e-6)
+
+
+def test_chain_golden():
+    z = golden("models")
+    loss, g = om.chain_loss_and_grads(z["chain_x"], z["chain_bias"], z["chain_y"])
+    # GELU's A&S erf differs from exact erf by <= 1.5e-7
+    close(loss, z["chain_loss"], rtol=0, atol=1e-6)
+    close(g["x"], z["chain_dx"], rtol=0, atol=1e-7)
+    close(g["bias"], z["chain_dbias"], rtol=0, atol=1e-6)
+    close(g["y"], z["chain_dy"], rtol=0, atol=1e-7)
+
+
+def test_gpt2_golden():
+    z = golden("models")
+    V, C, D, H, Lr = (int(v) for v in z["gpt_cfg"])
+    cfg = om.Config(vocab=V, ctx=C, d=D, heads=H, layers=Lr)
+    P = {k[6:]: z[k] for k in z if k.startswith("gpt_p:")}
+    ids = z["gpt_ids"]
+    loss, grads = om.gpt2_loss_and_grads(cfg, P, ids[:, :-1], ids[:, 1:])
+    close(loss, z["gpt_loss"], rtol=0, atol=1e-6)
+    for k in P:
+        close(grads[k], z["gpt_g:" + k], rtol=1e-5, atol=1e-6)
+
+
+# ------------------------------------------------------------------ torch.js literal tests
+
+
+def test_literal_matmul():
+    """tests/browser.test.ts:19-26: [[1,2],[3,4]] @ [[5,6],[7,8]] = [[19,22],[43,50]]."""
+    a = np.array([[1., 2.], [3., 4.]])
+    b = np.array([[5., 6.], [7., 8.]])
+    assert (a @ b).tolist() == [[19., 22.], [43., 50.]]
+    ga, gb = ops.matmul_backward(np.ones((2, 2)), a, b)
+    assert ga.tolist() == [[11., 15.], [11., 15.]]
+    assert gb.tolist() == [[4., 4.], [6., 6.]]
+
+
+def test_literal_grad_of_mul_and_sum():
+    """tests/compatibility/tensor/tensor_backward.test.ts:11-19: d(2x)/dx = 2."""
+    ga, _ = ops.binary_backward("mul", np.ones(3), np.array([1., 2., 3.]), np.array(2.))
+    assert ga.tolist() == [2., 2., 2.]
+
+
+def test_literal_exp_grad():
+    """tensor_backward.test.ts:396-403: d exp(x)/dx at 1 = e."""
+    assert abs(ops.unary_backward("exp", 1.0, 1.0) - math.e) < 1e-12
+
+
+def test_literal_nll():
+    """tests/compatibility/nn/functional.test.ts:144: nll_loss([[-0.1,-2,-3]], [0]) = 0.1;
+    and :142 cross_entropy([[2,1,0.1]], [0]) > 0."""
+    assert abs(ops.nll_loss(np.array([[-0.1, -2.0, -3.0]]), [0]) - 0.1) < 1e-12
+    ce = ops.cross_entropy(np.array([[2.0, 1.0, 0.1]]), [0])
+    assert ce > 0 and abs(ce - (math.log(math.exp(2) + math.exp(1) + math.exp(0.1)) - 2)) < 1e-12
+
+
+def test_literal_one_hot():
+    """tests/compatibility/nn/functional.test.ts:130-135: 3 classes and
+    auto num_classes = max + 1."""
+    assert ops.one_hot(np.array([0, 1, 2]), 3).reshape(-1).tolist() == [1, 0, 0, 0, 1, 0, 0, 0, 1]
+    assert ops.one_hot(np.array([0, 2, 4])).shape == (3, 5)
+    # Math.round ties go up; out-of-range rows stay zero (functional.ts:786-791)
+    assert ops.one_hot(np.array([0.5, 2.4, -1, 7]), 4).tolist() == \
+        [[0, 1, 0, 0], [0, 0, 1, 0], [0, 0, 0, 0], [0, 0, 0, 0]]
+
+
+def test_literal_nonzero():
+    """tests/compatibility/tensor/tensor_index.test.ts:305-328."""
+    x = np.array([[0, 1, 0], [2, 0, 3]])
+    assert ops.nonzero(x).tolist() == [[0, 1], [1, 0], [1, 2]]
+
+
+def test_literal_argmax_first_on_ties():
+    """Tensor.ts:2568 keeps the first maximum (`val > maxVal`)."""
+    assert int(ops.argmax(np.array([1., 5., 5., 2.]))) == 1
+    assert ops.argmax(np.array([[3., 3.], [1., 4.]]), 1).tolist() == [0, 1]
+
+
+def test_literal_gather_negative_wrap():
+    """Tensor.ts:2686-2687 wraps negative gather indices."""
+    x = np.array([[1., 2., 3.]])
+    assert ops.gather(x, 1, np.array([[-1, 0]])).tolist() == [[3., 1.]]
+
+
+def test_literal_mse():
+    """tests/compatibility/nn/losses.test.ts:70-73: MSE([1,2,3],[2,4,6]) = 14/3."""
+    a = np.array([1., 2., 3.])
+    b = np.array([2., 4., 6.])
+    assert abs(((a - b) ** 2).mean() - 14 / 3) < 1e-12
+
+
+def test_pow_scalar_integer_rule():
+    """scalar.wgsl:53-66: integer exponents 0..10 by repeated multiply."""
+    assert ops.pow_scalar(np.array([3.0]), 2)[0] == 9.0
+    assert ops.pow_scalar(np.array([2.0]), 0)[0] == 1.0
+    assert abs(ops.pow_scalar(np.array([2.0]), 0.5)[0] - math.sqrt(2)) < 1e-15
+
+
+# ------------------------------------------------------------------ closed forms / bounds
+
+
+def test_erf_as_published_bound_and_symmetry():
+    x = np.linspace(-6, 6, 20001)
+    err = np.abs(ops.erf_as(x) - np.array([math.erf(v) for v in x]))
+    assert err.max() <= 1.5e-7  # A&S 7.1.26
+    assert np.allclose(ops.erf_as(-x), -ops.erf_as(x), rtol=0, atol=0)
+
+
+def test_gelu_closed_forms():
+    assert ops.gelu(0.0) == 0.0
+    assert abs(ops.gelu_grad(0.0) - 0.5) < 1e-7
+    assert abs(ops.gelu(10.0) - 10.0) < 1e-12
+    assert abs(ops.gelu(-10.0)) < 1e-20
+    # gelu' = d/dx gelu by central differences (away from the A&S ripple)
+    x = np.linspace(-4, 4, 41)
+    h = 1e-5
+    fd = (ops.gelu(x + h) - ops.gelu(x - h)) / (2 * h)
+    assert np.allclose(ops.gelu_grad(x), fd, atol=2e-6)
+
+
+def test_softmax_ce_closed_forms():
+    c = 7
+    x = np.full((3, c), 2.5)
+    assert np.allclose(ops.softmax(x), 1.0 / c)
+    assert abs(ops.cross_entropy(x, [0, 3, 6]) - math.log(c)) < 1e-12
+    x = np.random.default_rng(1).standard_normal((5, c))
+    g = ops.cross_entropy_backward(x, [0, 1, 2, 3, 4])
+    assert np.allclose(g.sum(axis=1), 0.0, atol=1e-15)
+    assert np.allclose(ops.softmax(x).sum(axis=1), 1.0)
+
+
+def test_layer_norm_invariants():
+    x = np.random.default_rng(2).standard_normal((4, 33)) * 5 + 3
+    y, _, _ = ops.layer_norm(x)
+    assert np.allclose(y.mean(axis=1), 0, atol=1e-12)
+    assert np.allclose((y ** 2).mean(axis=1), 1, atol=1e-5)
+
+
+def test_adam_first_step_sign():
+    """Adam's first step moves each parameter by ~lr*sign(g) (m_hat/sqrt(v_hat) = +-1)."""
+    p = np.zeros(5, np.float32)
+    g = np.array([3., -2., 1e-3, -7., 0.5], np.float32)
+    p1, _, _ = ops.adam_step(p, g, np.zeros(5, np.float32), np.zeros(5, np.float32), 1, lr=0.1)
+    assert np.allclose(p1, -0.1 * np.sign(g), rtol=1e-5)
+
+
+def test_conv_delta_kernel_is_shift():
+    x = np.random.default_rng(3).standard_normal((1, 1, 5, 5))
+    w = np.zeros((1, 1, 3, 3))
+    w[0, 0, 0, 0] = 1.0  # picks x[i-1, j-1] with padding 1
+    y = ops.conv2d(x, w, None, 1, 1)
+    assert np.allclose(y[0, 0, 1:, 1:], x[0, 0, :-1, :-1])
+    assert np.allclose(y[0, 0, 0, :], 0)
+
+
+def _fd_check(f, x, g_analytic, eps=1e-6, n=12, seed=0):
+    r = np.random.default_rng(seed)
+    flat = x.reshape(-1)
+    for i in r.choice(flat.size, size=min(n, flat.size), replace=False):
+        old = flat[i]
+        flat[i] = old + eps
+        fp = f()
+        flat[i] = old - eps
+        fm = f()
+        flat[i] = old
+        fd = (fp - fm) / (2 * eps)
+        assert abs(fd - g_analytic.reshape(-1)[i]) <= 1e-5 * max(1.0, abs(fd)), (i, fd)
+
+
+def test_finite_differences_block():
+    """The transformer-block backward against central differences."""
+    r = np.random.default_rng(4)
+    d, heads = 8, 2
+    p = om.block_params(d, r, std=0.3)
+    p = {k: v.astype(np.float64) for k, v in p.items()}
+    x = r.standard_normal((2, 5, d))
+    loss, g = om.block_loss_and_grads(p, x, heads)
+    _fd_check(lambda: om.block_loss_and_grads(p, x, heads)[0], x, g["x"])
+    w = p["attn.c_attn.weight"]
+    _fd_check(lambda: om.block_loss_and_grads(p, x, heads)[0], w, g["attn.c_attn.weight"])
+
+
+def test_finite_differences_cnn_mlp():
+    r = np.random.default_rng(5)
+    p = {"conv1.weight": r.standard_normal((4, 3, 3, 3)) * 0.3, "conv1.bias": r.standard_normal(4) * 0.1,
+         "conv2.weight": r.standard_normal((5, 4, 3, 3)) * 0.3, "conv2.bias": r.standard_normal(5) * 0.1,
+         "fc.weight": r.standard_normal((3, 5)) * 0.3, "fc.bias": r.standard_normal(3) * 0.1}
+    x = r.standard_normal((2, 3, 6, 6))
+    t = np.array([0, 2])
+    loss, g = om.cnn_loss_and_grads(p, x, t)
+    for k in ("conv1.weight", "conv2.weight", "fc.bias"):
+        _fd_check(lambda: om.cnn_loss_and_grads(p, x, t)[0], p[k], g[k])
+    pm = {"0.weight": r.standard_normal((6, 7)), "0.bias": r.standard_normal(6),
+          "2.weight": r.standard_normal((4, 6)), "2.bias": r.standard_normal(4)}
+    xm = r.standard_normal((3, 7))
+    tm = np.array([1, 3, 0])
+    loss, g = om.mlp_loss_and_grads(pm, xm, tm)
+    _fd_check(lambda: om.mlp_loss_and_grads(pm, xm, tm)[0], pm["0.weight"], g["0.weight"])
+
+
+# ------------------------------------------------------------------ rng
+
+
+def test_rng_integer_streams():
+    """random.wgsl:9-15 xorshift32 and creation.ts:921 LCG, by hand."""
+    assert rng.lcg_next(0) == 12345
+    assert rng.lcg_next(1) == (1103515245 + 12345) & 0x7FFFFFFF
+    x = 1
+    x ^= (x << 13) & 0xFFFFFFFF
+    x ^= x >> 17
+    x ^= (x << 5) & 0xFFFFFFFF
+    assert int(rng.xorshift32(1)) == x
+    u = rng.rand(1000, 42)
+    assert u.min() >= 0 and u.max() < 1 and abs(u.mean() - 0.5) < 0.05
+    n = rng.randn(20000, 7)
+    assert abs(n.mean()) < 0.05 and abs(n.std() - 1) < 0.05

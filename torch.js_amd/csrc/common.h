@@ -1,0 +1,82 @@
+// Shared internals of libtorchjs_hip.so: error reporting, the library
+// stream, launch checking, per-family launch timing and scratch memory.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+#include "../../include/torchjs_hip.h"
+
+namespace tjh {
+
+// Sets the thread-local error message and returns `code`.
+int set_error(int code, const char* fmt, ...);
+void clear_error();
+
+// The library stream (valid after tjh_init).
+hipStream_t stream();
+bool initialized();
+int device_ordinal();
+int num_cus();
+
+// Returns TJH_ERR_NOT_INITIALIZED (with message) unless tjh_init succeeded.
+int require_init();
+
+// Maps a HIP error to TJH_ERR_HIP with the call site in the message.
+int hip_fail(hipError_t e, const char* what);
+
+// Per-family launch timing.  `KernelScope` records a start event before
+// the launch and an end event after it when timing is enabled.
+struct KernelScope {
+  int slot;
+  void* start;  // hipEvent_t of the opening record
+  explicit KernelScope(const char* family);
+  ~KernelScope();
+};
+
+// Checks hipGetLastError after a launch; returns TJH_OK or TJH_ERR_HIP.
+int check_launch(const char* kernel);
+
+// Stream-ordered scratch from the caching allocator.  Released with
+// scratch_free once the kernels using it have been enqueued.
+void* scratch_alloc(size_t bytes);
+void scratch_free(void* p);
+
+// RAII holder for scratch memory.
+struct Scratch {
+  void* p = nullptr;
+  explicit Scratch(size_t bytes) { if (bytes) p = scratch_alloc(bytes); }
+  ~Scratch() { if (p) scratch_free(p); }
+  template <typename T> T* as() const { return static_cast<T*>(p); }
+  bool ok() const { return p != nullptr; }
+};
+
+// The MFMA GEMM behind tjh_gemm, timed under `family` (so products issued
+// inside attention or convolution are reported apart from tjh_gemm's).
+int gemm(const char* family, int transA, int transB, int64_t M, int64_t N, int64_t K,
+         float alpha, const float* A, int64_t lda, int64_t strideA, const float* B, int64_t ldb,
+         int64_t strideB, float beta, float* C, int64_t ldc, int64_t strideC, int64_t batch,
+         const float* bias, int bias_mode);
+
+// Grid size helper: ceil(n / d).
+__host__ __device__ inline int64_t cdiv(int64_t n, int64_t d) { return (n + d - 1) / d; }
+
+}  // namespace tjh
+
+#define TJH_REQUIRE_INIT()                   \
+  do {                                       \
+    int _rc = ::tjh::require_init();         \
+    if (_rc != TJH_OK) return _rc;           \
+  } while (0)
+
+#define TJH_HIP(call)                                  \
+  do {                                                 \
+    hipError_t _e = (call);                            \
+    if (_e != hipSuccess) return ::tjh::hip_fail(_e, #call); \
+  } while (0)
+
+#define TJH_ARG(cond, ...)                                          \
+  do {                                                              \
+    if (!(cond)) return ::tjh::set_error(TJH_ERR_INVALID, __VA_ARGS__); \
+  } while (0)

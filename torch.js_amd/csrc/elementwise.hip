@@ -1,0 +1,821 @@
+// Elementwise kernels: fill, RNG, strided copies, unary / binary / ternary /
+// scalar ops and their backward helpers, masked_fill and comparisons.
+//
+// Layout strategy.  Every call is first reduced on the host to the fewest
+// dimensions (size-1 dims dropped, adjacent dims merged when every operand
+// is contiguous across them).  Then:
+//   * 1-D or 2-D [R, C] layouts where each input is contiguous, a row
+//     vector (stride [0,1]), a column vector ([1,0]) or a scalar take a
+//     128-bit vectorised grid-stride kernel (one float4 per lane per step);
+//   * anything else takes a generic strided kernel (<= 8 dims).
+// The reference's counterparts are elementwise.wgsl:5-31,
+// broadcast.wgsl:28-175, scalar.wgsl:10-67, unary.wgsl:5-252,
+// expand.wgsl, transpose(_nd).wgsl, slice(_backward).wgsl,
+// masked_fill.wgsl, fill.wgsl and random.wgsl.
+
+#include "common.h"
+#include "ops_math.h"
+
+#include <string.h>
+
+namespace tjh {
+namespace {
+
+constexpr int kBlock = 256;
+
+// ------------------------------------------------------------ layouts
+
+constexpr int kMaxOps = 4;  // out + up to 3 inputs
+
+struct Layout {
+  int ndim;
+  int64_t shape[TJH_MAX_DIMS];
+  int64_t st[kMaxOps][TJH_MAX_DIMS];
+};
+
+// Builds a coalesced layout for `nops` operands.  Returns numel.
+int64_t make_layout(Layout& L, int ndim, const int64_t* shape, int nops,
+                    const int64_t* const* strides) {
+  int64_t n = 1;
+  int k = 0;
+  for (int d = 0; d < ndim; ++d) {
+    n *= shape[d];
+    if (shape[d] == 1) continue;
+    L.shape[k] = shape[d];
+    for (int o = 0; o < nops; ++o) L.st[o][k] = strides[o][d];
+    ++k;
+  }
+  if (k == 0) {
+    L.shape[0] = 1;
+    for (int o = 0; o < nops; ++o) L.st[o][0] = 1;
+    k = 1;
+  }
+  // merge dim d into d+1 when contiguous across them for every operand
+  int m = 0;
+  for (int d = 1; d < k; ++d) {
+    bool ok = true;
+    for (int o = 0; o < nops; ++o)
+      if (L.st[o][m] != L.st[o][d] * L.shape[d]) { ok = false; break; }
+    if (ok) {
+      L.shape[m] *= L.shape[d];
+      for (int o = 0; o < nops; ++o) L.st[o][m] = L.st[o][d];
+    } else {
+      ++m;
+      L.shape[m] = L.shape[d];
+      for (int o = 0; o < nops; ++o) L.st[o][m] = L.st[o][d];
+    }
+  }
+  L.ndim = m + 1;
+  return n;
+}
+
+// Operand kinds for the vectorised 2-D path.
+enum Kind { K_CONTIG = 0, K_ROW = 1, K_COL = 2, K_SCALAR = 3, K_NONE = 4 };
+
+// Classifies operand `o` of a layout with <= 2 dims whose output (operand
+// 0) is contiguous.  Returns K_NONE when not one of the simple kinds.
+int classify(const Layout& L, int o) {
+  if (L.ndim == 1) {
+    if (L.st[o][0] == 1) return K_CONTIG;
+    if (L.st[o][0] == 0) return K_SCALAR;
+    return K_NONE;
+  }
+  if (L.ndim != 2) return K_NONE;
+  int64_t C = L.shape[1];
+  int64_t s0 = L.st[o][0], s1 = L.st[o][1];
+  if (s0 == C && s1 == 1) return K_CONTIG;
+  if (s0 == 0 && s1 == 1) return K_ROW;
+  if (s0 == 1 && s1 == 0) return K_COL;
+  if (s0 == 0 && s1 == 0) return K_SCALAR;
+  return K_NONE;
+}
+
+bool out_contiguous(const Layout& L) {
+  int64_t s = 1;
+  for (int d = L.ndim - 1; d >= 0; --d) {
+    if (L.st[0][d] != s) return false;
+    s *= L.shape[d];
+  }
+  return true;
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+int grid_for(int64_t work_items) {
+  int64_t g = cdiv(work_items, kBlock);
+  int64_t cap = (int64_t)num_cus() * 16;
+  if (cap < 1) cap = 1024;
+  if (g > cap) g = cap;
+  if (g < 1) g = 1;
+  return (int)g;
+}
+
+// ------------------------------------------------------------ op tables
+
+__device__ __forceinline__ float unary_f(int op, float x, float alpha) {
+  switch (op) {
+    case TJH_UNARY_NEG: return -x;
+    case TJH_UNARY_EXP: return expf(x);
+    case TJH_UNARY_LOG: return logf(x);
+    case TJH_UNARY_SQRT: return sqrtf(x);
+    case TJH_UNARY_RSQRT: return 1.0f / sqrtf(x);
+    case TJH_UNARY_TANH: return tanhf(x);
+    case TJH_UNARY_SIGMOID: return sigmoid_f(x);
+    case TJH_UNARY_RELU: return fmaxf(x, 0.0f);
+    case TJH_UNARY_GELU: return gelu_f(x);
+    case TJH_UNARY_SQUARE: return x * x;
+    case TJH_UNARY_RECIPROCAL: return 1.0f / x;
+    case TJH_UNARY_ERF: return erf_as(x);
+    case TJH_UNARY_ABS: return fabsf(x);
+    case TJH_UNARY_SIN: return sinf(x);
+    case TJH_UNARY_COS: return cosf(x);
+    case TJH_UNARY_SILU: return x * sigmoid_f(x);
+    case TJH_UNARY_LEAKY_RELU: return x > 0.f ? x : alpha * x;
+    case TJH_UNARY_ELU: return x > 0.f ? x : alpha * (expf(x) - 1.0f);
+    case TJH_UNARY_SOFTPLUS: return x > 20.f ? x : log1pf(expf(x));
+    case TJH_UNARY_SIGN: return (float)((x > 0.f) - (x < 0.f));
+    default: return 0.f;
+  }
+}
+
+// g * d op(x)/dx, using the saved output y where that is cheaper.
+__device__ __forceinline__ float unary_bwd_f(int op, float g, float x, float y,
+                                             float alpha) {
+  switch (op) {
+    case TJH_UNARY_NEG: return -g;
+    case TJH_UNARY_EXP: return g * y;
+    case TJH_UNARY_LOG: return g / x;
+    case TJH_UNARY_SQRT: return g * 0.5f / y;
+    case TJH_UNARY_RSQRT: return g * -0.5f * y * y * y;
+    case TJH_UNARY_TANH: return g * (1.0f - y * y);
+    case TJH_UNARY_SIGMOID: return g * y * (1.0f - y);
+    case TJH_UNARY_RELU: return x > 0.f ? g : 0.0f;
+    case TJH_UNARY_GELU: return g * gelu_grad(x);
+    case TJH_UNARY_SQUARE: return g * 2.0f * x;
+    case TJH_UNARY_RECIPROCAL: return -g * y * y;
+    case TJH_UNARY_ERF: return g * 1.1283791670955126f * expf(-x * x);
+    case TJH_UNARY_ABS: return g * (float)((x > 0.f) - (x < 0.f));
+    case TJH_UNARY_SIN: return g * cosf(x);
+    case TJH_UNARY_COS: return -g * sinf(x);
+    case TJH_UNARY_SILU: {
+      float s = sigmoid_f(x);
+      return g * s * (1.0f + x * (1.0f - s));
+    }
+    case TJH_UNARY_LEAKY_RELU: return x > 0.f ? g : alpha * g;
+    case TJH_UNARY_ELU: return x > 0.f ? g : g * alpha * expf(x);
+    case TJH_UNARY_SOFTPLUS: return x > 20.f ? g : g * sigmoid_f(x);
+    case TJH_UNARY_SIGN: return 0.0f;
+    default: return 0.f;
+  }
+}
+
+// Ops whose backward reads the saved output y.
+bool unary_bwd_needs_y(int op) {
+  return op == TJH_UNARY_EXP || op == TJH_UNARY_SQRT || op == TJH_UNARY_RSQRT ||
+         op == TJH_UNARY_TANH || op == TJH_UNARY_SIGMOID ||
+         op == TJH_UNARY_RECIPROCAL;
+}
+bool unary_bwd_needs_x(int op) {
+  return !(op == TJH_UNARY_NEG || unary_bwd_needs_y(op));
+}
+
+__device__ __forceinline__ float binary_f(int op, float a, float b) {
+  switch (op) {
+    case TJH_BINARY_ADD: return a + b;
+    case TJH_BINARY_SUB: return a - b;
+    case TJH_BINARY_MUL: return a * b;
+    case TJH_BINARY_DIV: return a / b;
+    case TJH_BINARY_POW: return powf(a, b);
+    case TJH_BINARY_MAXIMUM: return (a != a || b != b) ? __builtin_nanf("") : fmaxf(a, b);
+    case TJH_BINARY_MINIMUM: return (a != a || b != b) ? __builtin_nanf("") : fminf(a, b);
+    default: return 0.f;
+  }
+}
+
+// comparison ops: 0 eq 1 ne 2 lt 3 le 4 gt 5 ge
+constexpr int kCmpBase = 100;
+__device__ __forceinline__ float cmp_f(int op, float a, float b) {
+  switch (op) {
+    case 0: return a == b ? 1.f : 0.f;
+    case 1: return a != b ? 1.f : 0.f;
+    case 2: return a < b ? 1.f : 0.f;
+    case 3: return a <= b ? 1.f : 0.f;
+    case 4: return a > b ? 1.f : 0.f;
+    case 5: return a >= b ? 1.f : 0.f;
+    default: return 0.f;
+  }
+}
+
+__device__ __forceinline__ float ternary_f(int op, float g, float a, float b) {
+  switch (op) {
+    case TJH_TERNARY_DIV_B: return -g * a / (b * b);
+    case TJH_TERNARY_POW_A: return g * b * powf(a, b - 1.0f);
+    case TJH_TERNARY_POW_B: return g * powf(a, b) * logf(a);
+    case TJH_TERNARY_MUL3: return g * a * b;
+    default: return 0.f;
+  }
+}
+
+__device__ __forceinline__ float scalar_f(int op, float x, float s) {
+  switch (op) {
+    case TJH_SCALAR_ADD: return x + s;
+    case TJH_SCALAR_SUB: return x - s;
+    case TJH_SCALAR_MUL: return x * s;
+    case TJH_SCALAR_DIV: return x / s;
+    case TJH_SCALAR_POW: return pow_js(x, s);
+    case TJH_SCALAR_MAXIMUM: return fmaxf(x, s);
+    case TJH_SCALAR_MINIMUM: return fminf(x, s);
+    default: return 0.f;
+  }
+}
+__device__ __forceinline__ float scalar_rev_f(int op, float x, float s) {
+  switch (op) {
+    case TJH_SCALAR_ADD: return s + x;
+    case TJH_SCALAR_SUB: return s - x;
+    case TJH_SCALAR_MUL: return s * x;
+    case TJH_SCALAR_DIV: return s / x;
+    case TJH_SCALAR_POW: return powf(s, x);
+    case TJH_SCALAR_MAXIMUM: return fmaxf(s, x);
+    case TJH_SCALAR_MINIMUM: return fminf(s, x);
+    default: return 0.f;
+  }
+}
+
+// ------------------------------------------------------------ loaders
+
+template <int K>
+__device__ __forceinline__ float4 ld4(const float* __restrict__ p, uint32_t i,
+                                      uint32_t C) {
+  if constexpr (K == K_CONTIG) {
+    return *reinterpret_cast<const float4*>(p + i);
+  } else if constexpr (K == K_ROW) {
+    return *reinterpret_cast<const float4*>(p + (i % C));
+  } else if constexpr (K == K_COL) {
+    float v = p[i / C];
+    return make_float4(v, v, v, v);
+  } else {
+    float v = p[0];
+    return make_float4(v, v, v, v);
+  }
+}
+
+template <int K>
+__device__ __forceinline__ float ld1(const float* __restrict__ p, uint32_t i,
+                                     uint32_t C) {
+  if constexpr (K == K_CONTIG) return p[i];
+  else if constexpr (K == K_ROW) return p[i % C];
+  else if constexpr (K == K_COL) return p[i / C];
+  else return p[0];
+}
+
+// ------------------------------------------------------------ kernels
+
+// Functor-style element op over up to three inputs.
+struct UnaryOp {
+  int op; float alpha;
+  __device__ float operator()(float x, float, float) const { return unary_f(op, x, alpha); }
+};
+template <int OP>
+struct UnaryOpT {
+  float alpha;
+  __device__ float operator()(float x, float, float) const { return unary_f(OP, x, alpha); }
+};
+template <int OP>
+struct UnaryBwdT {  // inputs: g, x, y
+  float alpha;
+  __device__ float operator()(float g, float x, float y) const {
+    return unary_bwd_f(OP, g, x, y, alpha);
+  }
+};
+template <int OP>
+struct BinaryT {
+  __device__ float operator()(float a, float b, float) const { return binary_f(OP, a, b); }
+};
+template <int OP>
+struct CmpT {
+  __device__ float operator()(float a, float b, float) const { return cmp_f(OP, a, b); }
+};
+template <int OP>
+struct TernaryT {
+  __device__ float operator()(float g, float a, float b) const { return ternary_f(OP, g, a, b); }
+};
+template <int OP, bool REV>
+struct ScalarT {
+  float s;
+  __device__ float operator()(float x, float, float) const {
+    return REV ? scalar_rev_f(OP, x, s) : scalar_f(OP, x, s);
+  }
+};
+struct PowScalarBwd {
+  float s;
+  __device__ float operator()(float g, float x, float) const {
+    return g * s * pow_js(x, s - 1.0f);
+  }
+};
+struct Axpy {
+  float alpha;
+  __device__ float operator()(float x, float y, float) const { return alpha * x + y; }
+};
+struct CopyOp {
+  __device__ float operator()(float x, float, float) const { return x; }
+};
+
+// Vectorised kernel over a 1-D/2-D layout with contiguous output.
+// NIN inputs of kinds KA, KB, KC; n elements, C = row length (2-D kinds).
+template <int NIN, int KA, int KB, int KC, class F>
+__global__ __launch_bounds__(kBlock) void k_vec(
+    const float* __restrict__ a, const float* __restrict__ b,
+    const float* __restrict__ c, float* __restrict__ out, uint32_t n,
+    uint32_t C, F f) {
+  uint32_t n4 = n >> 2;
+  uint32_t gid = blockIdx.x * blockDim.x + threadIdx.x;
+  uint32_t stride = gridDim.x * blockDim.x;
+  for (uint32_t v = gid; v < n4; v += stride) {
+    uint32_t i = v << 2;
+    float4 xa = ld4<KA>(a, i, C);
+    float4 xb = NIN > 1 ? ld4<KB>(b, i, C) : xa;
+    float4 xc = NIN > 2 ? ld4<KC>(c, i, C) : xa;
+    float4 r;
+    r.x = f(xa.x, xb.x, xc.x);
+    r.y = f(xa.y, xb.y, xc.y);
+    r.z = f(xa.z, xb.z, xc.z);
+    r.w = f(xa.w, xb.w, xc.w);
+    *reinterpret_cast<float4*>(out + i) = r;
+  }
+  uint32_t tail = n - (n4 << 2);
+  if (gid < tail) {
+    uint32_t i = (n4 << 2) + gid;
+    float xa = ld1<KA>(a, i, C);
+    float xb = NIN > 1 ? ld1<KB>(b, i, C) : xa;
+    float xc = NIN > 2 ? ld1<KC>(c, i, C) : xa;
+    out[i] = f(xa, xb, xc);
+  }
+}
+
+// Scalar (non-vector) version of the same, for unaligned pointers or 2-D
+// layouts whose row length is not a multiple of 4.
+template <int NIN, int KA, int KB, int KC, class F>
+__global__ __launch_bounds__(kBlock) void k_scalar1(
+    const float* __restrict__ a, const float* __restrict__ b,
+    const float* __restrict__ c, float* __restrict__ out, uint32_t n,
+    uint32_t C, F f) {
+  uint32_t stride = gridDim.x * blockDim.x;
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    float xa = ld1<KA>(a, i, C);
+    float xb = NIN > 1 ? ld1<KB>(b, i, C) : xa;
+    float xc = NIN > 2 ? ld1<KC>(c, i, C) : xa;
+    out[i] = f(xa, xb, xc);
+  }
+}
+
+// Generic strided kernel: operand 0 is the output.
+template <int NIN, typename I, class F>
+__global__ __launch_bounds__(kBlock) void k_strided(
+    const float* __restrict__ a, const float* __restrict__ b,
+    const float* __restrict__ c, float* __restrict__ out, Layout L, I n, F f) {
+  I stride = (I)gridDim.x * blockDim.x;
+  for (I i = (I)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    I rem = i;
+    I off[kMaxOps] = {0, 0, 0, 0};
+    for (int d = L.ndim - 1; d >= 0; --d) {
+      I s = (I)L.shape[d];
+      I coord = rem % s;
+      rem /= s;
+#pragma unroll
+      for (int o = 0; o <= NIN; ++o) off[o] += coord * (I)L.st[o][d];
+    }
+    float xa = a[off[1]];
+    float xb = NIN > 1 ? b[off[2]] : xa;
+    float xc = NIN > 2 ? c[off[3]] : xa;
+    out[off[0]] = f(xa, xb, xc);
+  }
+}
+
+// Maximum |offset| reachable by operand o.
+int64_t max_offset(const Layout& L, int o) {
+  int64_t m = 0;
+  for (int d = 0; d < L.ndim; ++d) m += (L.shape[d] - 1) * (L.st[o][d] < 0 ? -L.st[o][d] : L.st[o][d]);
+  return m;
+}
+
+template <int NIN, int KA, int KB, int KC, class F>
+void launch_vec_kinds(const float* a, const float* b, const float* c, float* out,
+                      int64_t n, int64_t C, bool vec, F f) {
+  if (vec) {
+    int g = grid_for(cdiv(n, 4));
+    hipLaunchKernelGGL((k_vec<NIN, KA, KB, KC, F>), dim3(g), dim3(kBlock), 0,
+                       stream(), a, b, c, out, (uint32_t)n, (uint32_t)C, f);
+  } else {
+    int g = grid_for(n);
+    hipLaunchKernelGGL((k_scalar1<NIN, KA, KB, KC, F>), dim3(g), dim3(kBlock), 0,
+                       stream(), a, b, c, out, (uint32_t)n, (uint32_t)C, f);
+  }
+}
+
+// Dispatch on operand kinds (each input one of 4 kinds).
+template <int NIN, class F>
+bool launch_fast(const Layout& L, const float* a, const float* b, const float* c,
+                 float* out, int64_t n, F f) {
+  if (n >= (int64_t(1) << 31)) return false;
+  if (!out_contiguous(L)) return false;
+  int ka = classify(L, 1);
+  int kb = NIN > 1 ? classify(L, 2) : K_CONTIG;
+  int kc = NIN > 2 ? classify(L, 3) : K_CONTIG;
+  if (ka == K_NONE || kb == K_NONE || kc == K_NONE) return false;
+  int64_t C = L.ndim == 2 ? L.shape[1] : n;
+  bool rowish = (ka == K_ROW || ka == K_COL || kb == K_ROW || kb == K_COL ||
+                 kc == K_ROW || kc == K_COL);
+  bool vec = aligned16(out) && aligned16(a) && (NIN < 2 || aligned16(b)) &&
+             (NIN < 3 || aligned16(c)) && (!rowish || (C % 4) == 0);
+  // scalar-kind operands need no alignment
+  if (ka == K_SCALAR || kb == K_SCALAR || kc == K_SCALAR) {
+    vec = aligned16(out) && (ka == K_SCALAR || aligned16(a)) &&
+          (NIN < 2 || kb == K_SCALAR || aligned16(b)) &&
+          (NIN < 3 || kc == K_SCALAR || aligned16(c)) && (!rowish || (C % 4) == 0);
+  }
+#define TJH_KB(KA_, KB_, KC_)                                                        \
+  if (ka == KA_ && kb == KB_ && kc == KC_) {                                         \
+    launch_vec_kinds<NIN, KA_, KB_, KC_>(a, b, c, out, n, C, vec, f);                \
+    return true;                                                                     \
+  }
+  if constexpr (NIN == 1) {
+    TJH_KB(K_CONTIG, K_CONTIG, K_CONTIG)
+    TJH_KB(K_ROW, K_CONTIG, K_CONTIG)
+    TJH_KB(K_COL, K_CONTIG, K_CONTIG)
+    TJH_KB(K_SCALAR, K_CONTIG, K_CONTIG)
+  } else if constexpr (NIN == 2) {
+    TJH_KB(K_CONTIG, K_CONTIG, K_CONTIG)
+    TJH_KB(K_CONTIG, K_ROW, K_CONTIG)
+    TJH_KB(K_ROW, K_CONTIG, K_CONTIG)
+    TJH_KB(K_CONTIG, K_COL, K_CONTIG)
+    TJH_KB(K_COL, K_CONTIG, K_CONTIG)
+    TJH_KB(K_CONTIG, K_SCALAR, K_CONTIG)
+    TJH_KB(K_SCALAR, K_CONTIG, K_CONTIG)
+    TJH_KB(K_ROW, K_COL, K_CONTIG)
+    TJH_KB(K_COL, K_ROW, K_CONTIG)
+  } else {
+    TJH_KB(K_CONTIG, K_CONTIG, K_CONTIG)
+    TJH_KB(K_ROW, K_CONTIG, K_CONTIG)
+    TJH_KB(K_CONTIG, K_ROW, K_CONTIG)
+    TJH_KB(K_CONTIG, K_CONTIG, K_ROW)
+    TJH_KB(K_COL, K_CONTIG, K_CONTIG)
+    TJH_KB(K_CONTIG, K_COL, K_CONTIG)
+    TJH_KB(K_CONTIG, K_CONTIG, K_COL)
+  }
+#undef TJH_KB
+  return false;
+}
+
+template <int NIN, class F>
+void launch_strided(const Layout& L, const float* a, const float* b,
+                    const float* c, float* out, int64_t n, F f) {
+  bool small = n < (int64_t(1) << 31);
+  for (int o = 0; o <= NIN && small; ++o) small = max_offset(L, o) < (int64_t(1) << 31);
+  int g = grid_for(n);
+  if (small) {
+    hipLaunchKernelGGL((k_strided<NIN, uint32_t, F>), dim3(g), dim3(kBlock), 0,
+                       stream(), a, b, c, out, L, (uint32_t)n, f);
+  } else {
+    hipLaunchKernelGGL((k_strided<NIN, int64_t, F>), dim3(g), dim3(kBlock), 0,
+                       stream(), a, b, c, out, L, n, f);
+  }
+}
+
+// Full elementwise launch: layout build, fast path or strided path.
+template <int NIN, class F>
+int run_elementwise(const char* name, int ndim, const int64_t* shape,
+                    const int64_t* out_strides, const float* a,
+                    const int64_t* a_st, const float* b, const int64_t* b_st,
+                    const float* c, const int64_t* c_st, float* out, F f) {
+  TJH_ARG(ndim >= 0 && ndim <= TJH_MAX_DIMS, "%s: ndim %d out of range", name, ndim);
+  int64_t zero_shape[1] = {1};
+  int64_t unit[1] = {1};
+  const int64_t* strides[kMaxOps] = {out_strides, a_st, b_st, c_st};
+  if (ndim == 0) {
+    shape = zero_shape;
+    for (int o = 0; o <= NIN; ++o) strides[o] = unit;
+    ndim = 1;
+  }
+  for (int d = 0; d < ndim; ++d)
+    TJH_ARG(shape[d] >= 0, "%s: negative dimension", name);
+  Layout L;
+  int64_t n = make_layout(L, ndim, shape, NIN + 1, strides);
+  if (n == 0) return TJH_OK;
+  KernelScope ks(name);
+  if (!launch_fast<NIN>(L, a, b, c, out, n, f)) launch_strided<NIN>(L, a, b, c, out, n, f);
+  return check_launch(name);
+}
+
+void contiguous_strides(int ndim, const int64_t* shape, int64_t* st) {
+  int64_t s = 1;
+  for (int d = ndim - 1; d >= 0; --d) {
+    st[d] = s;
+    s *= shape[d];
+  }
+}
+
+// 1-D contiguous helper.
+template <int NIN, class F>
+int run_contig(const char* name, const float* a, const float* b, const float* c,
+               float* out, int64_t n, F f) {
+  TJH_ARG(n >= 0, "%s: negative length", name);
+  if (n == 0) return TJH_OK;
+  int64_t st[1] = {1};
+  return run_elementwise<NIN>(name, 1, &n, st, a, st, b, st, c, st, out, f);
+}
+
+// ------------------------------------------------------------ fill / rng
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void k_fill(T* __restrict__ out, int64_t n, T v) {
+  int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) out[i] = v;
+}
+
+__global__ __launch_bounds__(kBlock) void k_fill4(float4* __restrict__ out, int64_t n4, float v) {
+  int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  float4 q = make_float4(v, v, v, v);
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride) out[i] = q;
+}
+
+__device__ __forceinline__ uint32_t xorshift32(uint32_t x) {
+  x ^= x << 13;
+  x ^= x >> 17;
+  x ^= x << 5;
+  return x;
+}
+
+// random.wgsl:9-46: state = seed ^ (idx*1664525 + 1013904223) (mod 2^32),
+// one xorshift step; uniform = u / 2^32; normal = Box-Muller (cos branch)
+// of two successive states with u1 clamped to >= 1e-7.
+__global__ __launch_bounds__(kBlock) void k_random(float* __restrict__ out, int64_t n,
+                                                   uint32_t seed, int normal) {
+  int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    uint32_t idx = (uint32_t)i;
+    uint32_t s1 = xorshift32(seed ^ (idx * 1664525u + 1013904223u));
+    float u1 = (float)s1 / 4294967296.0f;
+    if (!normal) {
+      out[i] = u1;
+    } else {
+      uint32_t s2 = xorshift32(s1);
+      float u2 = (float)s2 / 4294967296.0f;
+      float r = sqrtf(-2.0f * logf(fmaxf(u1, 1e-7f)));
+      out[i] = r * cosf(6.283185307179586f * u2);
+    }
+  }
+}
+
+// ------------------------------------------------------------ int32 copies
+
+__global__ __launch_bounds__(kBlock) void k_copy_i32(const int32_t* __restrict__ src,
+                                                     int32_t* __restrict__ dst, Layout L,
+                                                     int64_t n) {
+  int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    int64_t rem = i, so = 0, dof = 0;
+    for (int d = L.ndim - 1; d >= 0; --d) {
+      int64_t coord = rem % L.shape[d];
+      rem /= L.shape[d];
+      dof += coord * L.st[0][d];
+      so += coord * L.st[1][d];
+    }
+    dst[dof] = src[so];
+  }
+}
+
+__global__ __launch_bounds__(kBlock) void k_f2i(const float* __restrict__ s, int32_t* __restrict__ d,
+                                                int64_t n) {
+  int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+    d[i] = (int32_t)s[i];
+}
+__global__ __launch_bounds__(kBlock) void k_i2f(const int32_t* __restrict__ s, float* __restrict__ d,
+                                                int64_t n) {
+  int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+    d[i] = (float)s[i];
+}
+
+// ------------------------------------------------------------ masked fill
+
+__global__ __launch_bounds__(kBlock) void k_masked_fill(const float* __restrict__ x,
+                                                        const uint8_t* __restrict__ m,
+                                                        float* __restrict__ out, Layout L,
+                                                        int64_t n, float value) {
+  int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    int64_t rem = i, oo = 0, xo = 0, mo = 0;
+    for (int d = L.ndim - 1; d >= 0; --d) {
+      int64_t coord = rem % L.shape[d];
+      rem /= L.shape[d];
+      oo += coord * L.st[0][d];
+      xo += coord * L.st[1][d];
+      mo += coord * L.st[2][d];
+    }
+    out[oo] = m[mo] ? value : x[xo];
+  }
+}
+
+}  // namespace
+}  // namespace tjh
+
+using namespace tjh;
+
+// ====================================================================== C ABI
+
+#define TJH_UNARY_CASES(X)                                                      \
+  X(TJH_UNARY_NEG) X(TJH_UNARY_EXP) X(TJH_UNARY_LOG) X(TJH_UNARY_SQRT)          \
+  X(TJH_UNARY_RSQRT) X(TJH_UNARY_TANH) X(TJH_UNARY_SIGMOID) X(TJH_UNARY_RELU)   \
+  X(TJH_UNARY_GELU) X(TJH_UNARY_SQUARE) X(TJH_UNARY_RECIPROCAL) X(TJH_UNARY_ERF)\
+  X(TJH_UNARY_ABS) X(TJH_UNARY_SIN) X(TJH_UNARY_COS) X(TJH_UNARY_SILU)          \
+  X(TJH_UNARY_LEAKY_RELU) X(TJH_UNARY_ELU) X(TJH_UNARY_SOFTPLUS) X(TJH_UNARY_SIGN)
+
+extern "C" {
+
+int tjh_fill_f32(float* out, int64_t n, float value) {
+  TJH_REQUIRE_INIT();
+  TJH_ARG(n >= 0 && (out || n == 0), "tjh_fill_f32: bad arguments");
+  if (n == 0) return TJH_OK;
+  KernelScope ks("fill");
+  if (aligned16(out) && n % 4 == 0) {
+    hipLaunchKernelGGL(k_fill4, dim3(grid_for(n / 4)), dim3(kBlock), 0, stream(),
+                       reinterpret_cast<float4*>(out), n / 4, value);
+  } else {
+    hipLaunchKernelGGL(k_fill<float>, dim3(grid_for(n)), dim3(kBlock), 0, stream(), out, n, value);
+  }
+  return check_launch("fill");
+}
+
+int tjh_fill_i32(int32_t* out, int64_t n, int32_t value) {
+  TJH_REQUIRE_INIT();
+  TJH_ARG(n >= 0 && (out || n == 0), "tjh_fill_i32: bad arguments");
+  if (n == 0) return TJH_OK;
+  KernelScope ks("fill");
+  hipLaunchKernelGGL(k_fill<int32_t>, dim3(grid_for(n)), dim3(kBlock), 0, stream(), out, n, value);
+  return check_launch("fill_i32");
+}
+
+int tjh_random(float* out, int64_t n, uint32_t seed, int normal) {
+  TJH_REQUIRE_INIT();
+  TJH_ARG(n >= 0 && (out || n == 0), "tjh_random: bad arguments");
+  if (n == 0) return TJH_OK;
+  KernelScope ks("random");
+  hipLaunchKernelGGL(k_random, dim3(grid_for(n)), dim3(kBlock), 0, stream(), out, n, seed, normal);
+  return check_launch("random");
+}
+
+int tjh_copy_strided(int ndim, const int64_t* shape, const float* src,
+                     const int64_t* src_strides, float* dst, const int64_t* dst_strides) {
+  TJH_REQUIRE_INIT();
+  TJH_ARG(ndim == 0 || (shape && src_strides && dst_strides), "tjh_copy_strided: NULL shape/strides");
+  return run_elementwise<1>("copy_strided", ndim, shape, dst_strides, src, src_strides,
+                            nullptr, nullptr, nullptr, nullptr, dst, CopyOp{});
+}
+
+int tjh_copy_strided_i32(int ndim, const int64_t* shape, const int32_t* src,
+                         const int64_t* src_strides, int32_t* dst, const int64_t* dst_strides) {
+  TJH_REQUIRE_INIT();
+  TJH_ARG(ndim >= 0 && ndim <= TJH_MAX_DIMS, "tjh_copy_strided_i32: ndim out of range");
+  int64_t one = 1, unit = 1;
+  if (ndim == 0) { shape = &one; src_strides = &unit; dst_strides = &unit; ndim = 1; }
+  const int64_t* st[2] = {dst_strides, src_strides};
+  Layout L;
+  int64_t n = make_layout(L, ndim, shape, 2, st);
+  if (n == 0) return TJH_OK;
+  KernelScope ks("copy_strided_i32");
+  hipLaunchKernelGGL(k_copy_i32, dim3(grid_for(n)), dim3(kBlock), 0, stream(), src, dst, L, n);
+  return check_launch("copy_strided_i32");
+}
+
+int tjh_cast_f32_i32(const float* src, int32_t* dst, int64_t n) {
+  TJH_REQUIRE_INIT();
+  if (n <= 0) return TJH_OK;
+  KernelScope ks("cast");
+  hipLaunchKernelGGL(k_f2i, dim3(grid_for(n)), dim3(kBlock), 0, stream(), src, dst, n);
+  return check_launch("cast_f32_i32");
+}
+
+int tjh_cast_i32_f32(const int32_t* src, float* dst, int64_t n) {
+  TJH_REQUIRE_INIT();
+  if (n <= 0) return TJH_OK;
+  KernelScope ks("cast");
+  hipLaunchKernelGGL(k_i2f, dim3(grid_for(n)), dim3(kBlock), 0, stream(), src, dst, n);
+  return check_launch("cast_i32_f32");
+}
+
+int tjh_unary(int op, const float* x, float* out, int64_t n, float alpha) {
+  TJH_REQUIRE_INIT();
+  TJH_ARG(op >= 0 && op < TJH_UNARY_COUNT, "tjh_unary: unknown op %d", op);
+  switch (op) {
+#define X(OPC) case OPC: return run_contig<1>("unary", x, nullptr, nullptr, out, n, UnaryOpT<OPC>{alpha});
+    TJH_UNARY_CASES(X)
+#undef X
+  }
+  return set_error(TJH_ERR_INVALID, "tjh_unary: unknown op %d", op);
+}
+
+int tjh_unary_backward(int op, const float* g, const float* x, const float* y, float* out,
+                       int64_t n, float alpha) {
+  TJH_REQUIRE_INIT();
+  TJH_ARG(op >= 0 && op < TJH_UNARY_COUNT, "tjh_unary_backward: unknown op %d", op);
+  TJH_ARG(!unary_bwd_needs_y(op) || y, "tjh_unary_backward: op %d needs the saved output", op);
+  TJH_ARG(!unary_bwd_needs_x(op) || x, "tjh_unary_backward: op %d needs the saved input", op);
+  // unused operands alias g so the loaders read valid memory
+  const float* xx = x ? x : g;
+  const float* yy = y ? y : g;
+  switch (op) {
+#define X(OPC) case OPC: return run_contig<3>("unary_backward", g, xx, yy, out, n, UnaryBwdT<OPC>{alpha});
+    TJH_UNARY_CASES(X)
+#undef X
+  }
+  return set_error(TJH_ERR_INVALID, "tjh_unary_backward: unknown op %d", op);
+}
+
+int tjh_binary(int op, int ndim, const int64_t* shape, const float* a, const int64_t* a_strides,
+               const float* b, const int64_t* b_strides, float* out) {
+  TJH_REQUIRE_INIT();
+  TJH_ARG(ndim >= 0 && ndim <= TJH_MAX_DIMS, "tjh_binary: ndim %d out of range", ndim);
+  int64_t ost[TJH_MAX_DIMS];
+  contiguous_strides(ndim, shape, ost);
+  switch (op) {
+#define B(OPC) case OPC: return run_elementwise<2>("binary", ndim, shape, ost, a, a_strides, b, b_strides, nullptr, nullptr, out, BinaryT<OPC>{});
+    B(TJH_BINARY_ADD) B(TJH_BINARY_SUB) B(TJH_BINARY_MUL) B(TJH_BINARY_DIV)
+    B(TJH_BINARY_POW) B(TJH_BINARY_MAXIMUM) B(TJH_BINARY_MINIMUM)
+#undef B
+  }
+  return set_error(TJH_ERR_INVALID, "tjh_binary: unknown op %d", op);
+}
+
+int tjh_compare(int op, int ndim, const int64_t* shape, const float* a, const int64_t* a_strides,
+                const float* b, const int64_t* b_strides, float* out) {
+  TJH_REQUIRE_INIT();
+  TJH_ARG(ndim >= 0 && ndim <= TJH_MAX_DIMS, "tjh_compare: ndim %d out of range", ndim);
+  int64_t ost[TJH_MAX_DIMS];
+  contiguous_strides(ndim, shape, ost);
+  switch (op) {
+#define C(OPC) case OPC: return run_elementwise<2>("compare", ndim, shape, ost, a, a_strides, b, b_strides, nullptr, nullptr, out, CmpT<OPC>{});
+    C(0) C(1) C(2) C(3) C(4) C(5)
+#undef C
+  }
+  return set_error(TJH_ERR_INVALID, "tjh_compare: unknown op %d", op);
+}
+
+int tjh_ternary(int op, int ndim, const int64_t* shape, const float* g, const int64_t* g_strides,
+                const float* a, const int64_t* a_strides, const float* b,
+                const int64_t* b_strides, float* out) {
+  TJH_REQUIRE_INIT();
+  TJH_ARG(ndim >= 0 && ndim <= TJH_MAX_DIMS, "tjh_ternary: ndim %d out of range", ndim);
+  int64_t ost[TJH_MAX_DIMS];
+  contiguous_strides(ndim, shape, ost);
+  switch (op) {
+#define T(OPC) case OPC: return run_elementwise<3>("ternary", ndim, shape, ost, g, g_strides, a, a_strides, b, b_strides, out, TernaryT<OPC>{});
+    T(TJH_TERNARY_DIV_B) T(TJH_TERNARY_POW_A) T(TJH_TERNARY_POW_B) T(TJH_TERNARY_MUL3)
+#undef T
+  }
+  return set_error(TJH_ERR_INVALID, "tjh_ternary: unknown op %d", op);
+}
+
+int tjh_scalar(int op, const float* x, float s, int reverse, float* out, int64_t n) {
+  TJH_REQUIRE_INIT();
+  switch (op) {
+#define S(OPC)                                                                                  \
+  case OPC:                                                                                     \
+    return reverse ? run_contig<1>("scalar", x, nullptr, nullptr, out, n, ScalarT<OPC, true>{s}) \
+                   : run_contig<1>("scalar", x, nullptr, nullptr, out, n, ScalarT<OPC, false>{s});
+    S(TJH_SCALAR_ADD) S(TJH_SCALAR_SUB) S(TJH_SCALAR_MUL) S(TJH_SCALAR_DIV)
+    S(TJH_SCALAR_POW) S(TJH_SCALAR_MAXIMUM) S(TJH_SCALAR_MINIMUM)
+#undef S
+  }
+  return set_error(TJH_ERR_INVALID, "tjh_scalar: unknown op %d", op);
+}
+
+int tjh_pow_scalar_backward(const float* g, const float* x, float s, float* out, int64_t n) {
+  TJH_REQUIRE_INIT();
+  return run_contig<2>("pow_scalar_backward", g, x, nullptr, out, n, PowScalarBwd{s});
+}
+
+int tjh_axpy(float alpha, const float* x, const float* y, float* out, int64_t n) {
+  TJH_REQUIRE_INIT();
+  return run_contig<2>("axpy", x, y, nullptr, out, n, Axpy{alpha});
+}
+
+int tjh_masked_fill(int ndim, const int64_t* shape, const float* x, const int64_t* x_strides,
+                    const uint8_t* mask, const int64_t* mask_strides, float value, float* out) {
+  TJH_REQUIRE_INIT();
+  TJH_ARG(ndim >= 0 && ndim <= TJH_MAX_DIMS, "tjh_masked_fill: ndim out of range");
+  int64_t one = 1, unit = 1;
+  int64_t ost[TJH_MAX_DIMS];
+  if (ndim == 0) { shape = &one; x_strides = &unit; mask_strides = &unit; ndim = 1; }
+  contiguous_strides(ndim, shape, ost);
+  const int64_t* st[3] = {ost, x_strides, mask_strides};
+  Layout L;
+  int64_t n = make_layout(L, ndim, shape, 3, st);
+  if (n == 0) return TJH_OK;
+  KernelScope ks("masked_fill");
+  hipLaunchKernelGGL(k_masked_fill, dim3(grid_for(n)), dim3(kBlock), 0, stream(), x, mask, out, L,
+                     n, value);
+  return check_launch("masked_fill");
+}
+
+}  // extern "C"

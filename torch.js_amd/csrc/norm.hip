@@ -1,0 +1,785 @@
+// Row-wise kernels over the last dimension: softmax / log_softmax forward
+// and backward, fused cross-entropy forward and backward, nll_loss, and
+// LayerNorm forward and backward.
+//
+// Reference semantics: log_softmax.wgsl:8-36 (max-subtracted),
+// log_softmax_backward.wgsl:17-34, nll_loss(_backward).wgsl,
+// src/nn/losses.ts:18-145 (cross_entropy = nll_loss(log_softmax)),
+// layernorm.wgsl:14-42 (biased variance, eps inside the sqrt) and
+// src/nn/layernorm.ts:25-119.  The reference evaluates a row with ONE
+// thread; here a row is owned by a wave (short rows) or a workgroup (long
+// rows such as the 50257-wide vocabulary) and combined with wave shuffles.
+//
+// Row access is 128-bit wherever the row start is 16-byte aligned; rows
+// whose stride is odd (ld = 50257) peel a scalar prefix up to the next
+// 16-byte boundary, stream float4s, and finish with a scalar tail.
+
+#include "common.h"
+
+#include <float.h>
+
+namespace tjh {
+namespace {
+
+constexpr int kBlock = 256;
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+// Online (max, sum-of-exp) pair.
+struct MS {
+  float m, s;
+};
+__device__ __forceinline__ MS ms_comb(MS a, MS b) {
+  float m = fmaxf(a.m, b.m);
+  if (m == -INFINITY) return MS{m, 0.f};
+  return MS{m, a.s * __expf(a.m - m) + b.s * __expf(b.m - m)};
+}
+__device__ __forceinline__ MS ms_add(MS a, float x) {
+  if (x > a.m) return MS{x, a.s * __expf(a.m - x) + 1.0f};
+  return MS{a.m, a.s + __expf(x - a.m)};
+}
+__device__ __forceinline__ MS wave_ms(MS v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    MS o{__shfl_xor(v.m, off, 64), __shfl_xor(v.s, off, 64)};
+    v = ms_comb(v, o);
+  }
+  return v;
+}
+
+// Calls f(index, value) for every element of row[0..n) with 128-bit loads
+// in the aligned middle.  `lane`/`nl` describe the participating lanes.
+template <class F>
+__device__ __forceinline__ void row_scan(const float* __restrict__ row, int64_t n, int lane,
+                                         int nl, F&& f) {
+  int64_t pre = (int64_t)((16 - ((uintptr_t)row & 15)) & 15) / 4;
+  if (((uintptr_t)row & 3) != 0) pre = n;  // not even float aligned: scalar
+  if (pre > n) pre = n;
+  for (int64_t i = lane; i < pre; i += nl) f(i, row[i]);
+  int64_t n4 = (n - pre) / 4;
+  const float4* p4 = reinterpret_cast<const float4*>(row + pre);
+  for (int64_t i = lane; i < n4; i += nl) {
+    float4 v = p4[i];
+    int64_t b = pre + 4 * i;
+    f(b, v.x);
+    f(b + 1, v.y);
+    f(b + 2, v.z);
+    f(b + 3, v.w);
+  }
+  for (int64_t i = pre + 4 * n4 + lane; i < n; i += nl) f(i, row[i]);
+}
+
+// Block-wide MS reduce (every lane gets the result).
+__device__ __forceinline__ MS block_ms(MS v, float* sm) {
+  v = wave_ms(v);
+  int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  if (lane == 0) { sm[2 * wid] = v.m; sm[2 * wid + 1] = v.s; }
+  __syncthreads();
+  MS r{sm[0], sm[1]};
+  for (int w = 1; w < kBlock / 64; ++w) r = ms_comb(r, MS{sm[2 * w], sm[2 * w + 1]});
+  __syncthreads();
+  return r;
+}
+__device__ __forceinline__ float block_sum(float v, float* sm) {
+  v = wave_sum(v);
+  int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  if (lane == 0) sm[wid] = v;
+  __syncthreads();
+  float r = 0.f;
+  for (int w = 0; w < kBlock / 64; ++w) r += sm[w];
+  __syncthreads();
+  return r;
+}
+
+// ------------------------------------------------------------- softmax
+
+// One row per wave (WAVE) or per block.  y = softmax or log_softmax.
+template <bool WAVE>
+__global__ __launch_bounds__(kBlock) void k_softmax_fwd(const float* __restrict__ x, int64_t ldx,
+                                                        float* __restrict__ y, int64_t ldy,
+                                                        int64_t rows, int64_t cols, int log) {
+  __shared__ float sm[2 * kBlock / 64];
+  int64_t r = WAVE ? (int64_t)blockIdx.x * (kBlock / 64) + (threadIdx.x >> 6) : blockIdx.x;
+  int lane = WAVE ? (threadIdx.x & 63) : threadIdx.x;
+  int nl = WAVE ? 64 : kBlock;
+  if (r >= rows) return;
+  const float* xr = x + r * ldx;
+  float* yr = y + r * ldy;
+  MS ms{-INFINITY, 0.f};
+  row_scan(xr, cols, lane, nl, [&](int64_t, float v) { ms = ms_add(ms, v); });
+  ms = WAVE ? wave_ms(ms) : block_ms(ms, sm);
+  float lse = ms.m + logf(ms.s);
+  float inv = 1.0f / ms.s;
+  for (int64_t i = lane; i < cols; i += nl) {
+    float v = xr[i];
+    yr[i] = log ? v - lse : __expf(v - ms.m) * inv;
+  }
+}
+
+template <bool WAVE>
+__global__ __launch_bounds__(kBlock) void k_softmax_bwd(const float* __restrict__ dy,
+                                                        const float* __restrict__ y,
+                                                        float* __restrict__ dx, int64_t rows,
+                                                        int64_t cols, int log) {
+  __shared__ float sm[kBlock / 64];
+  int64_t r = WAVE ? (int64_t)blockIdx.x * (kBlock / 64) + (threadIdx.x >> 6) : blockIdx.x;
+  int lane = WAVE ? (threadIdx.x & 63) : threadIdx.x;
+  int nl = WAVE ? 64 : kBlock;
+  if (r >= rows) return;
+  const float* g = dy + r * cols;
+  const float* yr = y + r * cols;
+  float* o = dx + r * cols;
+  float s = 0.f;
+  for (int64_t i = lane; i < cols; i += nl) s += log ? g[i] : g[i] * yr[i];
+  s = WAVE ? wave_sum(s) : block_sum(s, sm);
+  for (int64_t i = lane; i < cols; i += nl) {
+    o[i] = log ? g[i] - __expf(yr[i]) * s : yr[i] * (g[i] - s);
+  }
+}
+
+// ------------------------------------------------------------- cross entropy
+
+// One row per block (vocabulary-wide rows) or per wave (short rows).
+template <bool WAVE>
+__global__ __launch_bounds__(kBlock) void k_ce_fwd(const float* __restrict__ x, int64_t ld,
+                                                   const int32_t* __restrict__ t, int64_t rows,
+                                                   int64_t cols, int32_t ignore,
+                                                   float* __restrict__ lse_out,
+                                                   float* __restrict__ loss_rows) {
+  __shared__ float sm[2 * kBlock / 64];
+  int64_t r = WAVE ? (int64_t)blockIdx.x * (kBlock / 64) + (threadIdx.x >> 6) : blockIdx.x;
+  int lane = WAVE ? (threadIdx.x & 63) : threadIdx.x;
+  int nl = WAVE ? 64 : kBlock;
+  if (r >= rows) return;
+  const float* xr = x + r * ld;
+  MS ms{-INFINITY, 0.f};
+  row_scan(xr, cols, lane, nl, [&](int64_t, float v) { ms = ms_add(ms, v); });
+  ms = WAVE ? wave_ms(ms) : block_ms(ms, sm);
+  if (lane == 0) {
+    float lse = ms.m + logf(ms.s);
+    int32_t tr = t[r];
+    lse_out[r] = lse;
+    loss_rows[r] = (tr == ignore || tr < 0 || tr >= cols) ? 0.f : lse - xr[tr];
+  }
+}
+
+// Final reduction of per-row losses: mean over valid rows or sum.  One block.
+__global__ __launch_bounds__(kBlock) void k_loss_reduce(const float* __restrict__ loss_rows,
+                                                        const int32_t* __restrict__ t,
+                                                        int64_t rows, int64_t cols,
+                                                        int32_t ignore, int reduction,
+                                                        float* __restrict__ out) {
+  __shared__ float sm[kBlock / 64];
+  float s = 0.f, c = 0.f;
+  for (int64_t i = threadIdx.x; i < rows; i += kBlock) {
+    s += loss_rows[i];
+    int32_t tr = t[i];
+    c += (tr == ignore || tr < 0 || tr >= cols) ? 0.f : 1.f;
+  }
+  s = block_sum(s, sm);
+  c = block_sum(c, sm);
+  if (threadIdx.x == 0) out[0] = reduction == 1 ? s / c : s;
+}
+
+__device__ __forceinline__ float ce_scale(const float* __restrict__ gout, int reduction,
+                                          int64_t r, float inv_count) {
+  if (reduction == 0) return gout[r];
+  if (reduction == 1) return gout[0] * inv_count;
+  return gout[0];
+}
+
+// dlogits = (softmax - onehot) * scale.  One row per block/wave.
+template <bool WAVE>
+__global__ __launch_bounds__(kBlock) void k_ce_bwd(const float* __restrict__ x, int64_t ld,
+                                                   const int32_t* __restrict__ t,
+                                                   const float* __restrict__ lse,
+                                                   const float* __restrict__ gout,
+                                                   const float* __restrict__ count,
+                                                   int64_t rows, int64_t cols, int32_t ignore,
+                                                   int reduction, float* __restrict__ d,
+                                                   int64_t ldd, int accumulate) {
+  int64_t r = WAVE ? (int64_t)blockIdx.x * (kBlock / 64) + (threadIdx.x >> 6) : blockIdx.x;
+  int lane = WAVE ? (threadIdx.x & 63) : threadIdx.x;
+  int nl = WAVE ? 64 : kBlock;
+  if (r >= rows) return;
+  const float* xr = x + r * ld;
+  float* dr = d + r * ldd;
+  int32_t tr = t[r];
+  bool valid = !(tr == ignore || tr < 0 || tr >= cols);
+  float sc = valid ? ce_scale(gout, reduction, r, count ? 1.0f / count[0] : 1.0f) : 0.f;
+  float l = lse[r];
+  // write-aligned streaming: the output row decides the vector alignment
+  int64_t pre = (int64_t)((16 - ((uintptr_t)dr & 15)) & 15) / 4;
+  if (((uintptr_t)dr & 3) != 0) pre = cols;
+  if (pre > cols) pre = cols;
+  auto val = [&](int64_t i, float xv) {
+    float p = __expf(xv - l);
+    return (p - (i == tr ? 1.f : 0.f)) * sc;
+  };
+  for (int64_t i = lane; i < pre; i += nl) {
+    float v = val(i, xr[i]);
+    dr[i] = accumulate ? dr[i] + v : v;
+  }
+  int64_t n4 = (cols - pre) / 4;
+  float4* d4 = reinterpret_cast<float4*>(dr + pre);
+  bool xal = (((uintptr_t)(xr + pre)) & 15) == 0;
+  for (int64_t i = lane; i < n4; i += nl) {
+    int64_t b = pre + 4 * i;
+    float4 xv;
+    if (xal) xv = *reinterpret_cast<const float4*>(xr + b);
+    else xv = make_float4(xr[b], xr[b + 1], xr[b + 2], xr[b + 3]);
+    float4 o = make_float4(val(b, xv.x), val(b + 1, xv.y), val(b + 2, xv.z), val(b + 3, xv.w));
+    if (accumulate) {
+      float4 q = d4[i];
+      o.x += q.x; o.y += q.y; o.z += q.z; o.w += q.w;
+    }
+    d4[i] = o;
+  }
+  for (int64_t i = pre + 4 * n4 + lane; i < cols; i += nl) {
+    float v = val(i, xr[i]);
+    dr[i] = accumulate ? dr[i] + v : v;
+  }
+}
+
+// count of valid targets (for mean) into one float.
+__global__ __launch_bounds__(kBlock) void k_count_valid(const int32_t* __restrict__ t, int64_t rows,
+                                                        int64_t cols, int32_t ignore,
+                                                        float* __restrict__ out) {
+  __shared__ float sm[kBlock / 64];
+  float c = 0.f;
+  for (int64_t i = threadIdx.x; i < rows; i += kBlock) {
+    int32_t tr = t[i];
+    c += (tr == ignore || tr < 0 || tr >= cols) ? 0.f : 1.f;
+  }
+  c = block_sum(c, sm);
+  if (threadIdx.x == 0) out[0] = c;
+}
+
+__global__ __launch_bounds__(kBlock) void k_nll_fwd(const float* __restrict__ lp, int64_t ld,
+                                                    const int32_t* __restrict__ t, int64_t rows,
+                                                    int64_t cols, int32_t ignore,
+                                                    float* __restrict__ loss_rows) {
+  int64_t r = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (r >= rows) return;
+  int32_t tr = t[r];
+  loss_rows[r] = (tr == ignore || tr < 0 || tr >= cols) ? 0.f : -lp[r * ld + tr];
+}
+
+__global__ __launch_bounds__(kBlock) void k_nll_bwd(const int32_t* __restrict__ t,
+                                                    const float* __restrict__ gout,
+                                                    const float* __restrict__ count,
+                                                    int64_t rows, int64_t cols, int32_t ignore,
+                                                    int reduction, float* __restrict__ d) {
+  int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (i >= rows * cols) return;
+  int64_t r = i / cols, c = i % cols;
+  int32_t tr = t[r];
+  bool valid = !(tr == ignore || tr < 0 || tr >= cols);
+  float v = 0.f;
+  if (valid && c == tr) v = -ce_scale(gout, reduction, r, count ? 1.0f / count[0] : 1.0f);
+  d[i] = v;
+}
+
+// ------------------------------------------------------------- layer norm
+
+// Wave per row, the row kept in registers: cols % 4 == 0, cols <= 64*4*V4.
+template <int V4>
+__global__ __launch_bounds__(kBlock) void k_ln_fwd_wave(const float* __restrict__ x,
+                                                        const float* __restrict__ gamma,
+                                                        const float* __restrict__ beta,
+                                                        float* __restrict__ y,
+                                                        float* __restrict__ mean_out,
+                                                        float* __restrict__ rstd_out, int64_t rows,
+                                                        int64_t cols, float eps) {
+  int64_t r = (int64_t)blockIdx.x * (kBlock / 64) + (threadIdx.x >> 6);
+  int lane = threadIdx.x & 63;
+  if (r >= rows) return;
+  const int c4 = (int)(cols >> 2);
+  const float4* xr = reinterpret_cast<const float4*>(x + r * cols);
+  float4 v[V4];
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < V4; ++j) {
+    int i = lane + 64 * j;
+    if (i < c4) {
+      v[j] = xr[i];
+      s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
+    } else {
+      v[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  }
+  float mean = wave_sum(s) / (float)cols;
+  float q = 0.f;
+#pragma unroll
+  for (int j = 0; j < V4; ++j) {
+    int i = lane + 64 * j;
+    if (i < c4) {
+      float a = v[j].x - mean, b = v[j].y - mean, c = v[j].z - mean, d = v[j].w - mean;
+      q += (a * a + b * b) + (c * c + d * d);
+    }
+  }
+  float var = wave_sum(q) / (float)cols;
+  float rstd = 1.0f / sqrtf(var + eps);
+  float4* yr = reinterpret_cast<float4*>(y + r * cols);
+  const float4* g4 = reinterpret_cast<const float4*>(gamma);
+  const float4* b4 = reinterpret_cast<const float4*>(beta);
+#pragma unroll
+  for (int j = 0; j < V4; ++j) {
+    int i = lane + 64 * j;
+    if (i < c4) {
+      float4 o;
+      o.x = (v[j].x - mean) * rstd;
+      o.y = (v[j].y - mean) * rstd;
+      o.z = (v[j].z - mean) * rstd;
+      o.w = (v[j].w - mean) * rstd;
+      if (gamma) {
+        float4 gg = g4[i];
+        o.x *= gg.x; o.y *= gg.y; o.z *= gg.z; o.w *= gg.w;
+      }
+      if (beta) {
+        float4 bb = b4[i];
+        o.x += bb.x; o.y += bb.y; o.z += bb.z; o.w += bb.w;
+      }
+      yr[i] = o;
+    }
+  }
+  if (lane == 0) {
+    mean_out[r] = mean;
+    rstd_out[r] = rstd;
+  }
+}
+
+// General LayerNorm forward: one block per row, scalar, re-reads the row.
+__global__ __launch_bounds__(kBlock) void k_ln_fwd_block(const float* __restrict__ x,
+                                                         const float* __restrict__ gamma,
+                                                         const float* __restrict__ beta,
+                                                         float* __restrict__ y,
+                                                         float* __restrict__ mean_out,
+                                                         float* __restrict__ rstd_out,
+                                                         int64_t cols, float eps) {
+  __shared__ float sm[kBlock / 64];
+  int64_t r = blockIdx.x;
+  const float* xr = x + r * cols;
+  float s = 0.f;
+  for (int64_t i = threadIdx.x; i < cols; i += kBlock) s += xr[i];
+  float mean = block_sum(s, sm) / (float)cols;
+  float q = 0.f;
+  for (int64_t i = threadIdx.x; i < cols; i += kBlock) {
+    float a = xr[i] - mean;
+    q += a * a;
+  }
+  float var = block_sum(q, sm) / (float)cols;
+  float rstd = 1.0f / sqrtf(var + eps);
+  float* yr = y + r * cols;
+  for (int64_t i = threadIdx.x; i < cols; i += kBlock) {
+    float o = (xr[i] - mean) * rstd;
+    if (gamma) o *= gamma[i];
+    if (beta) o += beta[i];
+    yr[i] = o;
+  }
+  if (threadIdx.x == 0) {
+    mean_out[r] = mean;
+    rstd_out[r] = rstd;
+  }
+}
+
+// LayerNorm backward, dx part + per-block partial dgamma/dbeta.
+// Block b owns rows [b*rpb, (b+1)*rpb); wave w takes rows b*rpb + w + 4k.
+// Lane owns columns 4*(lane + 64*j) .. +3 (cols % 4 == 0, cols <= 256*V4).
+// Partials: pg/pb [nblocks, cols].
+template <int V4>
+__global__ __launch_bounds__(kBlock) void k_ln_bwd_wave(const float* __restrict__ dy,
+                                                        const float* __restrict__ x,
+                                                        const float* __restrict__ gamma,
+                                                        const float* __restrict__ mean,
+                                                        const float* __restrict__ rstd,
+                                                        float* __restrict__ dx,
+                                                        float* __restrict__ pg,
+                                                        float* __restrict__ pb, int64_t rows,
+                                                        int64_t cols, int64_t rpb) {
+  __shared__ float4 red[2][kBlock / 64][64 * 3];  // partial combine across waves
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int c4 = (int)(cols >> 2);
+  float4 ag[V4], ab[V4];
+  float4 gm[V4];
+#pragma unroll
+  for (int j = 0; j < V4; ++j) {
+    ag[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    ab[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    int i = lane + 64 * j;
+    gm[j] = (gamma && i < c4) ? reinterpret_cast<const float4*>(gamma)[i]
+                              : make_float4(1.f, 1.f, 1.f, 1.f);
+  }
+  const float inv_n = 1.0f / (float)cols;
+  int64_t r_beg = (int64_t)blockIdx.x * rpb;
+  int64_t r_end = r_beg + rpb < rows ? r_beg + rpb : rows;
+  for (int64_t r = r_beg + w; r < r_end; r += kBlock / 64) {
+    const float4* g4 = reinterpret_cast<const float4*>(dy + r * cols);
+    const float4* x4 = reinterpret_cast<const float4*>(x + r * cols);
+    const float mu = mean[r], rs = rstd[r];
+    float4 gv[V4], xh[V4];
+    float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+    for (int j = 0; j < V4; ++j) {
+      int i = lane + 64 * j;
+      if (i < c4) {
+        float4 g = g4[i], xv = x4[i];
+        xh[j] = make_float4((xv.x - mu) * rs, (xv.y - mu) * rs, (xv.z - mu) * rs, (xv.w - mu) * rs);
+        gv[j] = g;
+        float4 gg = make_float4(g.x * gm[j].x, g.y * gm[j].y, g.z * gm[j].z, g.w * gm[j].w);
+        s1 += (gg.x + gg.y) + (gg.z + gg.w);
+        s2 += (gg.x * xh[j].x + gg.y * xh[j].y) + (gg.z * xh[j].z + gg.w * xh[j].w);
+        ag[j].x += g.x * xh[j].x; ag[j].y += g.y * xh[j].y;
+        ag[j].z += g.z * xh[j].z; ag[j].w += g.w * xh[j].w;
+        ab[j].x += g.x; ab[j].y += g.y; ab[j].z += g.z; ab[j].w += g.w;
+      }
+    }
+    s1 = wave_sum(s1) * inv_n;
+    s2 = wave_sum(s2) * inv_n;
+    if (dx) {
+      float4* d4 = reinterpret_cast<float4*>(dx + r * cols);
+#pragma unroll
+      for (int j = 0; j < V4; ++j) {
+        int i = lane + 64 * j;
+        if (i < c4) {
+          float4 o;
+          o.x = rs * (gv[j].x * gm[j].x - s1 - xh[j].x * s2);
+          o.y = rs * (gv[j].y * gm[j].y - s1 - xh[j].y * s2);
+          o.z = rs * (gv[j].z * gm[j].z - s1 - xh[j].z * s2);
+          o.w = rs * (gv[j].w * gm[j].w - s1 - xh[j].w * s2);
+          d4[i] = o;
+        }
+      }
+    }
+  }
+  // combine the 4 waves' column partials (fixed order) and write
+  if (pg) {
+    for (int j0 = 0; j0 < V4; j0 += 3) {
+#pragma unroll
+      for (int jj = 0; jj < 3; ++jj) {
+        int j = j0 + jj;
+        if (j < V4) {
+          red[0][w][lane + 64 * jj] = ag[j];
+          red[1][w][lane + 64 * jj] = ab[j];
+        }
+      }
+      __syncthreads();
+      // wave 0 sums for gamma, wave 1 for beta
+      if (w < 2) {
+#pragma unroll
+        for (int jj = 0; jj < 3; ++jj) {
+          int j = j0 + jj;
+          int i = lane + 64 * j;
+          if (j < V4 && i < c4) {
+            float4 s = red[w][0][lane + 64 * jj];
+            for (int q = 1; q < kBlock / 64; ++q) {
+              float4 t = red[w][q][lane + 64 * jj];
+              s.x += t.x; s.y += t.y; s.z += t.z; s.w += t.w;
+            }
+            float* dst = (w == 0 ? pg : pb) + (int64_t)blockIdx.x * cols;
+            reinterpret_cast<float4*>(dst)[i] = s;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+// General LayerNorm backward: one block per row (dx) + partials per row.
+__global__ __launch_bounds__(kBlock) void k_ln_bwd_block(const float* __restrict__ dy,
+                                                         const float* __restrict__ x,
+                                                         const float* __restrict__ gamma,
+                                                         const float* __restrict__ mean,
+                                                         const float* __restrict__ rstd,
+                                                         float* __restrict__ dx,
+                                                         float* __restrict__ pg,
+                                                         float* __restrict__ pb, int64_t cols) {
+  __shared__ float sm[kBlock / 64];
+  int64_t r = blockIdx.x;
+  const float* g = dy + r * cols;
+  const float* xr = x + r * cols;
+  float mu = mean[r], rs = rstd[r];
+  float s1 = 0.f, s2 = 0.f;
+  for (int64_t i = threadIdx.x; i < cols; i += kBlock) {
+    float gg = g[i] * (gamma ? gamma[i] : 1.f);
+    float xh = (xr[i] - mu) * rs;
+    s1 += gg;
+    s2 += gg * xh;
+    if (pg) pg[r * cols + i] = g[i] * xh;
+    if (pb) pb[r * cols + i] = g[i];
+  }
+  s1 = block_sum(s1, sm) / (float)cols;
+  s2 = block_sum(s2, sm) / (float)cols;
+  if (dx) {
+    for (int64_t i = threadIdx.x; i < cols; i += kBlock) {
+      float gg = g[i] * (gamma ? gamma[i] : 1.f);
+      float xh = (xr[i] - mu) * rs;
+      dx[r * cols + i] = rs * (gg - s1 - xh * s2);
+    }
+  }
+}
+
+// Column sum of partials [nb, cols] -> out[cols] (+= when accumulate).
+__global__ __launch_bounds__(kBlock) void k_colsum(const float* __restrict__ p, int64_t nb,
+                                                   int64_t cols, float* __restrict__ out,
+                                                   int accumulate) {
+  int64_t c = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (c >= cols) return;
+  float s = 0.f;
+  for (int64_t b = 0; b < nb; ++b) s += p[b * cols + c];
+  out[c] = accumulate ? out[c] + s : s;
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+}  // namespace
+}  // namespace tjh
+
+using namespace tjh;
+
+extern "C" {
+
+int tjh_softmax_forward(const float* x, int64_t ldx, float* y, int64_t ldy, int64_t rows,
+                        int64_t cols, int log) {
+  TJH_REQUIRE_INIT();
+  TJH_ARG(rows >= 0 && cols >= 0 && ldx >= cols && ldy >= cols, "tjh_softmax_forward: bad sizes");
+  if (rows == 0 || cols == 0) return TJH_OK;
+  KernelScope ks(log ? "log_softmax_fwd" : "softmax_fwd");
+  if (cols <= 2048) {
+    hipLaunchKernelGGL(k_softmax_fwd<true>, dim3((unsigned)cdiv(rows, 4)), dim3(kBlock), 0,
+                       stream(), x, ldx, y, ldy, rows, cols, log);
+  } else {
+    hipLaunchKernelGGL(k_softmax_fwd<false>, dim3((unsigned)rows), dim3(kBlock), 0, stream(), x,
+                       ldx, y, ldy, rows, cols, log);
+  }
+  return check_launch("softmax_forward");
+}
+
+int tjh_softmax_backward(const float* dy, const float* y, float* dx, int64_t rows, int64_t cols,
+                         int log) {
+  TJH_REQUIRE_INIT();
+  TJH_ARG(rows >= 0 && cols >= 0, "tjh_softmax_backward: bad sizes");
+  if (rows == 0 || cols == 0) return TJH_OK;
+  KernelScope ks(log ? "log_softmax_bwd" : "softmax_bwd");
+  if (cols <= 2048) {
+    hipLaunchKernelGGL(k_softmax_bwd<true>, dim3((unsigned)cdiv(rows, 4)), dim3(kBlock), 0,
+                       stream(), dy, y, dx, rows, cols, log);
+  } else {
+    hipLaunchKernelGGL(k_softmax_bwd<false>, dim3((unsigned)rows), dim3(kBlock), 0, stream(), dy,
+                       y, dx, rows, cols, log);
+  }
+  return check_launch("softmax_backward");
+}
+
+int tjh_cross_entropy_forward(const float* logits, int64_t ld, const int32_t* targets,
+                              int64_t rows, int64_t cols, int32_t ignore_index, float* lse,
+                              float* loss_rows, int reduction, float* out) {
+  TJH_REQUIRE_INIT();
+  TJH_ARG(rows >= 0 && cols > 0 && ld >= cols, "tjh_cross_entropy_forward: bad sizes");
+  TJH_ARG(reduction >= 0 && reduction <= 2, "tjh_cross_entropy_forward: bad reduction");
+  TJH_ARG(reduction == 0 || out, "tjh_cross_entropy_forward: reduction needs `out`");
+  if (rows == 0) {
+    if (reduction) return tjh_fill_f32(out, 1, reduction == 1 ? __builtin_nanf("") : 0.f);
+    return TJH_OK;
+  }
+  {
+    KernelScope ks("cross_entropy_fwd");
+    if (cols <= 2048)
+      hipLaunchKernelGGL(k_ce_fwd<true>, dim3((unsigned)cdiv(rows, 4)), dim3(kBlock), 0, stream(),
+                         logits, ld, targets, rows, cols, ignore_index, lse, loss_rows);
+    else
+      hipLaunchKernelGGL(k_ce_fwd<false>, dim3((unsigned)rows), dim3(kBlock), 0, stream(), logits,
+                         ld, targets, rows, cols, ignore_index, lse, loss_rows);
+    int rc = check_launch("cross_entropy_forward");
+    if (rc != TJH_OK) return rc;
+  }
+  if (reduction) {
+    KernelScope ks("loss_reduce");
+    hipLaunchKernelGGL(k_loss_reduce, dim3(1), dim3(kBlock), 0, stream(), loss_rows, targets, rows,
+                       cols, ignore_index, reduction, out);
+    return check_launch("loss_reduce");
+  }
+  return TJH_OK;
+}
+
+int tjh_cross_entropy_backward(const float* logits, int64_t ld, const int32_t* targets,
+                               const float* lse, const float* grad_out, int64_t rows,
+                               int64_t cols, int32_t ignore_index, int reduction, float* dlogits,
+                               int64_t ldd, int accumulate) {
+  TJH_REQUIRE_INIT();
+  TJH_ARG(rows >= 0 && cols > 0 && ld >= cols && ldd >= cols,
+          "tjh_cross_entropy_backward: bad sizes");
+  TJH_ARG(reduction >= 0 && reduction <= 2, "tjh_cross_entropy_backward: bad reduction");
+  if (rows == 0) return TJH_OK;
+  Scratch cnt(reduction == 1 ? sizeof(float) : 0);
+  if (reduction == 1) {
+    if (!cnt.ok()) return set_error(TJH_ERR_OOM, "cross_entropy_backward: no scratch");
+    KernelScope ks("loss_reduce");
+    hipLaunchKernelGGL(k_count_valid, dim3(1), dim3(kBlock), 0, stream(), targets, rows, cols,
+                       ignore_index, cnt.as<float>());
+    int rc = check_launch("count_valid");
+    if (rc != TJH_OK) return rc;
+  }
+  KernelScope ks("cross_entropy_bwd");
+  if (cols <= 2048)
+    hipLaunchKernelGGL(k_ce_bwd<true>, dim3((unsigned)cdiv(rows, 4)), dim3(kBlock), 0, stream(),
+                       logits, ld, targets, lse, grad_out, cnt.as<float>(), rows, cols,
+                       ignore_index, reduction, dlogits, ldd, accumulate);
+  else
+    hipLaunchKernelGGL(k_ce_bwd<false>, dim3((unsigned)rows), dim3(kBlock), 0, stream(), logits,
+                       ld, targets, lse, grad_out, cnt.as<float>(), rows, cols, ignore_index,
+                       reduction, dlogits, ldd, accumulate);
+  return check_launch("cross_entropy_backward");
+}
+
+int tjh_nll_loss_forward(const float* logp, int64_t ld, const int32_t* targets, int64_t rows,
+                         int64_t cols, int32_t ignore_index, float* loss_rows, int reduction,
+                         float* out) {
+  TJH_REQUIRE_INIT();
+  TJH_ARG(rows >= 0 && cols > 0 && ld >= cols, "tjh_nll_loss_forward: bad sizes");
+  TJH_ARG(reduction >= 0 && reduction <= 2, "tjh_nll_loss_forward: bad reduction");
+  if (rows == 0) {
+    if (reduction) return tjh_fill_f32(out, 1, reduction == 1 ? __builtin_nanf("") : 0.f);
+    return TJH_OK;
+  }
+  KernelScope ks("nll_loss_fwd");
+  hipLaunchKernelGGL(k_nll_fwd, dim3((unsigned)cdiv(rows, kBlock)), dim3(kBlock), 0, stream(),
+                     logp, ld, targets, rows, cols, ignore_index, loss_rows);
+  int rc = check_launch("nll_loss_forward");
+  if (rc != TJH_OK || !reduction) return rc;
+  hipLaunchKernelGGL(k_loss_reduce, dim3(1), dim3(kBlock), 0, stream(), loss_rows, targets, rows,
+                     cols, ignore_index, reduction, out);
+  return check_launch("loss_reduce");
+}
+
+int tjh_nll_loss_backward(const int32_t* targets, const float* grad_out, int64_t rows,
+                          int64_t cols, int32_t ignore_index, int reduction, float* dlogp) {
+  TJH_REQUIRE_INIT();
+  TJH_ARG(rows >= 0 && cols > 0, "tjh_nll_loss_backward: bad sizes");
+  if (rows == 0) return TJH_OK;
+  Scratch cnt(reduction == 1 ? sizeof(float) : 0);
+  if (reduction == 1) {
+    if (!cnt.ok()) return set_error(TJH_ERR_OOM, "nll_loss_backward: no scratch");
+    hipLaunchKernelGGL(k_count_valid, dim3(1), dim3(kBlock), 0, stream(), targets, rows, cols,
+                       ignore_index, cnt.as<float>());
+  }
+  KernelScope ks("nll_loss_bwd");
+  hipLaunchKernelGGL(k_nll_bwd, dim3((unsigned)cdiv(rows * cols, kBlock)), dim3(kBlock), 0,
+                     stream(), targets, grad_out, cnt.as<float>(), rows, cols, ignore_index,
+                     reduction, dlogp);
+  return check_launch("nll_loss_backward");
+}
+
+int tjh_layer_norm_forward(const float* x, const float* gamma, const float* beta, float* y,
+                           float* mean, float* rstd, int64_t rows, int64_t cols, float eps) {
+  TJH_REQUIRE_INIT();
+  TJH_ARG(rows >= 0 && cols > 0, "tjh_layer_norm_forward: bad sizes");
+  TJH_ARG(mean && rstd, "tjh_layer_norm_forward: mean/rstd outputs required");
+  if (rows == 0) return TJH_OK;
+  KernelScope ks("layer_norm_fwd");
+  bool vec = cols % 4 == 0 && aligned16(x) && aligned16(y) && (!gamma || aligned16(gamma)) &&
+             (!beta || aligned16(beta));
+  unsigned g = (unsigned)cdiv(rows, 4);
+  if (vec && cols <= 64 * 4 * 4) {
+    hipLaunchKernelGGL(k_ln_fwd_wave<4>, dim3(g), dim3(kBlock), 0, stream(), x, gamma, beta, y,
+                       mean, rstd, rows, cols, eps);
+  } else if (vec && cols <= 64 * 4 * 16) {
+    hipLaunchKernelGGL(k_ln_fwd_wave<16>, dim3(g), dim3(kBlock), 0, stream(), x, gamma, beta, y,
+                       mean, rstd, rows, cols, eps);
+  } else {
+    hipLaunchKernelGGL(k_ln_fwd_block, dim3((unsigned)rows), dim3(kBlock), 0, stream(), x, gamma,
+                       beta, y, mean, rstd, cols, eps);
+  }
+  return check_launch("layer_norm_forward");
+}
+
+int tjh_layer_norm_backward(const float* dy, const float* x, const float* gamma,
+                            const float* mean, const float* rstd, float* dx, float* dgamma,
+                            float* dbeta, int64_t rows, int64_t cols, int accumulate) {
+  TJH_REQUIRE_INIT();
+  TJH_ARG(rows >= 0 && cols > 0, "tjh_layer_norm_backward: bad sizes");
+  if (rows == 0) {
+    if (!accumulate) {
+      if (dgamma) { int rc = tjh_fill_f32(dgamma, cols, 0.f); if (rc) return rc; }
+      if (dbeta) { int rc = tjh_fill_f32(dbeta, cols, 0.f); if (rc) return rc; }
+    }
+    return TJH_OK;
+  }
+  bool want_p = dgamma || dbeta;
+  bool vec = cols % 4 == 0 && aligned16(x) && aligned16(dy) && (!dx || aligned16(dx)) &&
+             (!gamma || aligned16(gamma));
+  int v4 = cols <= 64 * 4 * 3 ? 3 : (cols <= 64 * 4 * 6 ? 6 : (cols <= 64 * 4 * 12 ? 12 : 0));
+  if (vec && v4) {
+    // rows per block: aim for ~4 blocks per CU
+    int cus = num_cus() > 0 ? num_cus() : 256;
+    int64_t rpb = cdiv(rows, 4LL * cus);
+    if (rpb < 4) rpb = 4;
+    int64_t nb = cdiv(rows, rpb);
+    Scratch part(want_p ? (size_t)(2 * nb * cols) * sizeof(float) : 0);
+    if (want_p && !part.ok()) return set_error(TJH_ERR_OOM, "layer_norm_backward: no scratch");
+    float* pg = want_p ? part.as<float>() : nullptr;
+    float* pb = want_p ? part.as<float>() + nb * cols : nullptr;
+    {
+      KernelScope ks("layer_norm_bwd");
+      if (v4 == 3)
+        hipLaunchKernelGGL(k_ln_bwd_wave<3>, dim3((unsigned)nb), dim3(kBlock), 0, stream(), dy, x,
+                           gamma, mean, rstd, dx, pg, pb, rows, cols, rpb);
+      else if (v4 == 6)
+        hipLaunchKernelGGL(k_ln_bwd_wave<6>, dim3((unsigned)nb), dim3(kBlock), 0, stream(), dy, x,
+                           gamma, mean, rstd, dx, pg, pb, rows, cols, rpb);
+      else
+        hipLaunchKernelGGL(k_ln_bwd_wave<12>, dim3((unsigned)nb), dim3(kBlock), 0, stream(), dy, x,
+                           gamma, mean, rstd, dx, pg, pb, rows, cols, rpb);
+      int rc = check_launch("layer_norm_backward");
+      if (rc != TJH_OK) return rc;
+    }
+    if (want_p) {
+      KernelScope ks("layer_norm_bwd_colsum");
+      unsigned g = (unsigned)cdiv(cols, kBlock);
+      if (dgamma)
+        hipLaunchKernelGGL(k_colsum, dim3(g), dim3(kBlock), 0, stream(), pg, nb, cols, dgamma,
+                           accumulate);
+      if (dbeta)
+        hipLaunchKernelGGL(k_colsum, dim3(g), dim3(kBlock), 0, stream(), pb, nb, cols, dbeta,
+                           accumulate);
+      return check_launch("layer_norm_backward_colsum");
+    }
+    return TJH_OK;
+  }
+  // general path: partials per row, then column sums
+  Scratch part(want_p ? (size_t)(2 * rows * cols) * sizeof(float) : 0);
+  if (want_p && !part.ok()) return set_error(TJH_ERR_OOM, "layer_norm_backward: no scratch");
+  float* pg = want_p ? part.as<float>() : nullptr;
+  float* pb = want_p ? part.as<float>() + rows * cols : nullptr;
+  {
+    KernelScope ks("layer_norm_bwd");
+    hipLaunchKernelGGL(k_ln_bwd_block, dim3((unsigned)rows), dim3(kBlock), 0, stream(), dy, x,
+                       gamma, mean, rstd, dx, pg, pb, cols);
+    int rc = check_launch("layer_norm_backward");
+    if (rc != TJH_OK) return rc;
+  }
+  if (want_p) {
+    KernelScope ks("layer_norm_bwd_colsum");
+    unsigned g = (unsigned)cdiv(cols, kBlock);
+    if (dgamma)
+      hipLaunchKernelGGL(k_colsum, dim3(g), dim3(kBlock), 0, stream(), pg, rows, cols, dgamma,
+                         accumulate);
+    if (dbeta)
+      hipLaunchKernelGGL(k_colsum, dim3(g), dim3(kBlock), 0, stream(), pb, rows, cols, dbeta,
+                         accumulate);
+    return check_launch("layer_norm_backward_colsum");
+  }
+  return TJH_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,150 @@
+// Fused multi-tensor Adam / AdamW step.
+//
+// Replaces, per parameter, the ~9 tensor dispatches, 3-4 blocking
+// device->host readbacks, JS update loop and writeBuffer of torch.js's
+// Adam.step / AdamW.step (src/optim/adam.ts:46-133,
+// src/optim/adamw.ts:46-154) with ONE streaming pass per batch of up to
+// kMaxTensors parameters: read p, g, m, v; write p, m, v (28 bytes per
+// parameter, HBM-bound).
+//
+// Rounding follows the reference exactly: the moment updates and the
+// denominator are separate fp32 tensor ops there (each rounded), so they
+// are rounded after every operation here too (contraction disabled); the
+// final parameter update is the reference's JS double-precision loop,
+// rounded once to fp32.
+
+#include "common.h"
+
+namespace tjh {
+namespace {
+
+constexpr int kBlock = 256;
+constexpr int kMaxTensors = 32;
+constexpr int64_t kChunk = kBlock * 4 * 4;  // elements per workgroup
+
+struct AdamTensor {
+  float* p;
+  const float* g;
+  float* m;
+  float* v;
+  int64_t n;
+  int64_t first_block;  // prefix sum of blocks
+  double step_size;     // lr / bc1
+  float bc2;            // f32(1 - beta2^step)
+  int vec;
+};
+
+struct AdamBatch {
+  AdamTensor t[kMaxTensors];
+  int count;
+  float b1, omb1, b2, omb2, eps, wd;  // fp32 scalars as torch.js's tensor ops see them
+  double decay;                        // 1 - lr*wd (AdamW)
+  int decoupled;
+};
+
+// Every fp32 operation is rounded on its own (contraction off; IEEE
+// division and the correctly rounded llvm.sqrt), as the reference's
+// separate tensor ops round them.
+__device__ __forceinline__ void adam_elem(float& p, float g, float& m, float& v,
+                                          const AdamBatch& B, const AdamTensor& T) {
+#pragma clang fp contract(off)
+  if (!B.decoupled && B.wd != 0.f) g = g + p * B.wd;
+  m = m * B.b1 + g * B.omb1;
+  v = v * B.b2 + (g * g) * B.omb2;
+  float denom = __builtin_sqrtf(v / T.bc2) + B.eps;
+  double pd = (double)p;
+  if (B.decoupled) pd = pd * B.decay;
+  pd = pd - T.step_size * ((double)m / (double)denom);
+  p = (float)pd;
+}
+
+__global__ __launch_bounds__(kBlock) void k_adam(AdamBatch B) {
+  int b = blockIdx.x;
+  int ti = 0;
+  while (ti + 1 < B.count && B.t[ti + 1].first_block <= b) ++ti;
+  const AdamTensor& T = B.t[ti];
+  int64_t beg = (int64_t)(b - T.first_block) * kChunk;
+  int64_t end = beg + kChunk < T.n ? beg + kChunk : T.n;
+  if (T.vec) {
+    for (int64_t i = beg + 4 * threadIdx.x; i < end; i += 4 * kBlock) {
+      float4 p = *reinterpret_cast<float4*>(T.p + i);
+      float4 g = *reinterpret_cast<const float4*>(T.g + i);
+      float4 m = *reinterpret_cast<float4*>(T.m + i);
+      float4 v = *reinterpret_cast<float4*>(T.v + i);
+      adam_elem(p.x, g.x, m.x, v.x, B, T);
+      adam_elem(p.y, g.y, m.y, v.y, B, T);
+      adam_elem(p.z, g.z, m.z, v.z, B, T);
+      adam_elem(p.w, g.w, m.w, v.w, B, T);
+      *reinterpret_cast<float4*>(T.p + i) = p;
+      *reinterpret_cast<float4*>(T.m + i) = m;
+      *reinterpret_cast<float4*>(T.v + i) = v;
+    }
+  } else {
+    for (int64_t i = beg + threadIdx.x; i < end; i += kBlock) {
+      float p = T.p[i], m = T.m[i], v = T.v[i];
+      adam_elem(p, T.g[i], m, v, B, T);
+      T.p[i] = p;
+      T.m[i] = m;
+      T.v[i] = v;
+    }
+  }
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+}  // namespace
+}  // namespace tjh
+
+using namespace tjh;
+
+extern "C" int tjh_adam_step(int n_tensors, float* const* params, const float* const* grads,
+                             float* const* exp_avg, float* const* exp_avg_sq,
+                             const int64_t* numels, const int64_t* steps, double lr, double beta1,
+                             double beta2, double eps, double weight_decay, int decoupled) {
+  TJH_REQUIRE_INIT();
+  TJH_ARG(n_tensors >= 0, "tjh_adam_step: negative tensor count");
+  if (n_tensors == 0) return TJH_OK;
+  TJH_ARG(params && grads && exp_avg && exp_avg_sq && numels && steps,
+          "tjh_adam_step: NULL array");
+  AdamBatch B;
+  B.b1 = (float)beta1;
+  B.omb1 = (float)(1.0 - beta1);
+  B.b2 = (float)beta2;
+  B.omb2 = (float)(1.0 - beta2);
+  B.eps = (float)eps;
+  B.wd = (float)weight_decay;
+  B.decay = 1.0 - lr * weight_decay;
+  B.decoupled = decoupled ? 1 : 0;
+  KernelScope ks("adam");
+  int i = 0;
+  while (i < n_tensors) {
+    B.count = 0;
+    int64_t blocks = 0;
+    while (i < n_tensors && B.count < kMaxTensors) {
+      TJH_ARG(numels[i] >= 0 && steps[i] >= 1, "tjh_adam_step: bad numel/step for tensor %d", i);
+      if (numels[i] == 0) { ++i; continue; }
+      AdamTensor& T = B.t[B.count];
+      T.p = params[i];
+      T.g = grads[i];
+      T.m = exp_avg[i];
+      T.v = exp_avg_sq[i];
+      T.n = numels[i];
+      T.first_block = blocks;
+      double bc1 = 1.0 - pow(beta1, (double)steps[i]);
+      double bc2 = 1.0 - pow(beta2, (double)steps[i]);
+      T.step_size = lr / bc1;
+      T.bc2 = (float)bc2;
+      T.vec = (T.n % 4 == 0) && aligned16(T.p) && aligned16(T.g) && aligned16(T.m) &&
+              aligned16(T.v);
+      blocks += cdiv(T.n, kChunk);
+      ++B.count;
+      ++i;
+    }
+    if (B.count == 0) break;
+    TJH_ARG(blocks < (int64_t(1) << 31), "tjh_adam_step: tensors too large");
+    hipLaunchKernelGGL(k_adam, dim3((unsigned)blocks), dim3(kBlock), 0, stream(), B);
+    int rc = check_launch("adam_step");
+    if (rc != TJH_OK) return rc;
+  }
+  return TJH_OK;
+}

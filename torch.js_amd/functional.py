@@ -1,0 +1,460 @@
+"""torch.nn.functional for the 'hip' device (src/nn/functional.ts,
+src/nn/losses.ts): the hot-path ops as fused kernels with their
+backward passes.
+"""
+import ctypes
+import math
+
+import numpy as np
+
+from . import _lib as L
+from .tensor import (Tensor, _DT, _alias, _contig_strides, _empty_padded, _gemm, _k_binary,
+                     _k_contiguous, _k_reduce, _k_scalar, _numel, _record, _view_raw, _wrap_dim,
+                     contiguous, empty, full, mul, permute, reduce_mean, reshape, reshape_raw,
+                     sub, unary, zeros)
+
+
+def relu(x, inplace=False):
+    return unary("relu", x)
+
+
+def gelu(x, approximate="none"):
+    """Exact GELU with the A&S 7.1.26 erf of unary.wgsl:230-252."""
+    if approximate != "none":
+        raise NotImplementedError("only the exact (erf) GELU is implemented")
+    return unary("gelu", x)
+
+
+def sigmoid(x):
+    return unary("sigmoid", x)
+
+
+def tanh(x):
+    return unary("tanh", x)
+
+
+def silu(x):
+    return unary("silu", x)
+
+
+def softplus(x):
+    return unary("softplus", x)
+
+
+def leaky_relu(x, negative_slope=0.01):
+    return unary("leaky_relu", x, negative_slope)
+
+
+def elu(x, alpha=1.0):
+    return unary("elu", x, alpha)
+
+
+# ------------------------------------------------------------ softmax
+
+
+def _rows_view(x):
+    """(ptr, ld) when x is a 2-D row-major view with unit column stride."""
+    if x.ndim == 2 and (x._strides[1] == 1 or x.shape[1] <= 1) and x._strides[0] >= x.shape[1]:
+        return x.data_ptr(), max(x._strides[0], 1)
+    return None
+
+
+def _softmax_impl(x, dim, log):
+    if x.dtype != "float32":
+        x = x.float()
+    nd = x.ndim
+    d = _wrap_dim(dim, nd) if nd else 0
+    if nd == 0:
+        x1 = reshape(x, (1,))
+        out = _softmax_impl(x1, 0, log)
+        return reshape(out, ())
+    if d != nd - 1:
+        perm = list(range(nd))
+        perm[d], perm[-1] = perm[-1], perm[d]
+        y = _softmax_impl(permute(x, perm), -1, log)
+        return permute(y, perm)
+    xc = contiguous(x.detach())
+    cols = x.shape[-1]
+    rows = _numel(x.shape[:-1])
+    out = empty(x.shape)
+    L.check(L.lib().tjh_softmax_forward(xc.data_ptr(), cols, out.data_ptr(), cols, rows, cols,
+                                        1 if log else 0), "softmax")
+    y = out.detach()
+
+    def bwd(g):
+        g = g.contiguous()
+        dx = empty(g.shape)
+        L.check(L.lib().tjh_softmax_backward(g.data_ptr(), y.data_ptr(), dx.data_ptr(), rows, cols,
+                                             1 if log else 0), "softmax_backward")
+        return [dx]
+    return _record(out, "LogSoftmax" if log else "Softmax", [x], bwd)
+
+
+def softmax(x, dim=-1):
+    """F.softmax (src/nn/functional.ts:79-135): max-subtracted; backward
+    y*(g - sum(g*y)) (torch.js records none, D6)."""
+    return _softmax_impl(x, dim, False)
+
+
+def log_softmax(x, dim=-1):
+    """F.log_softmax (src/nn/functional.ts:137-234, log_softmax.wgsl:8-36);
+    backward g - softmax*sum(g) (log_softmax_backward.wgsl:17-34)."""
+    return _softmax_impl(x, dim, True)
+
+
+# ------------------------------------------------------------ losses
+
+_RED = {"none": 0, "mean": 1, "sum": 2}
+
+
+def _class_last_2d(x, target):
+    """[N, C] or [N, C, d1, ...] -> ([rows, C] view, flat int32 targets)."""
+    if x.ndim == 1:
+        x = reshape(x, (1, x.shape[0]))
+    if x.ndim > 2:
+        perm = [0] + list(range(2, x.ndim)) + [1]
+        x = reshape(permute(x, perm), (-1, x.shape[1]))
+    t = target
+    if not isinstance(t, Tensor):
+        from .tensor import tensor as _tensor
+        t = _tensor(np.asarray(t, dtype=np.int32), dtype="int32")
+    if t.dtype != "int32":
+        t = t.to("int32")
+    t = contiguous(reshape(t, (-1,)))
+    if t.numel() != x.shape[0]:
+        raise ValueError("cross_entropy: %d targets for %d rows" % (t.numel(), x.shape[0]))
+    return x, t
+
+
+def cross_entropy(input, target, weight=None, reduction="mean", ignore_index=-100,
+                  label_smoothing=0.0):
+    """F.cross_entropy (src/nn/losses.ts:130-145) = nll_loss(log_softmax),
+    fused: one pass computes logsumexp and the per-row loss, the backward
+    writes (softmax - onehot) * scale in one pass (torch.js's nll_loss
+    reinterprets int targets as floats, D9)."""
+    if weight is not None or label_smoothing:
+        raise NotImplementedError("cross_entropy: class weights / label smoothing are not on the hip path")
+    red = _RED[reduction]
+    x, t = _class_last_2d(input, target)
+    if x.dtype != "float32":
+        x = x.float()
+    rv = _rows_view(x)
+    xd = x.detach()
+    if rv is None:
+        xd = _k_contiguous(xd)
+        rv = _rows_view(xd)
+    rows, cols = x.shape
+    lse = empty((rows,))
+    loss_rows = empty((rows,))
+    out = empty(()) if red else loss_rows
+    L.check(L.lib().tjh_cross_entropy_forward(rv[0], rv[1], t.data_ptr(), rows, cols,
+                                              int(ignore_index), lse.data_ptr(),
+                                              loss_rows.data_ptr(), red,
+                                              out.data_ptr() if red else None),
+            "cross_entropy")
+    def bwd(g):
+        g = g.contiguous()
+        d = _empty_padded(rows, cols) if cols % 4 else empty((rows, cols))
+        xp, ld = _rows_view(xd)
+        L.check(L.lib().tjh_cross_entropy_backward(xp, ld, t.data_ptr(), lse.data_ptr(),
+                                                   g.data_ptr(), rows, cols, int(ignore_index),
+                                                   red, d.data_ptr(), d._strides[0], 0),
+                "cross_entropy_backward")
+        return [d]
+    res = _record(out, "CrossEntropy", [x], bwd)
+    if x is not input and input.ndim == 1 and red == 0:
+        res = reshape(res, ())
+    return res
+
+
+def nll_loss(input, target, weight=None, reduction="mean", ignore_index=-100):
+    """F.nll_loss (src/nn/losses.ts:63-94, nll_loss(_backward).wgsl)."""
+    if weight is not None:
+        raise NotImplementedError("nll_loss: class weights are not on the hip path")
+    red = _RED[reduction]
+    x, t = _class_last_2d(input, target)
+    if x.dtype != "float32":
+        x = x.float()
+    xd = x.detach()
+    rv = _rows_view(xd)
+    if rv is None:
+        xd = _k_contiguous(xd)
+        rv = _rows_view(xd)
+    rows, cols = x.shape
+    loss_rows = empty((rows,))
+    out = empty(()) if red else loss_rows
+    L.check(L.lib().tjh_nll_loss_forward(rv[0], rv[1], t.data_ptr(), rows, cols, int(ignore_index),
+                                         loss_rows.data_ptr(), red,
+                                         out.data_ptr() if red else None), "nll_loss")
+
+    def bwd(g):
+        g = g.contiguous()
+        d = empty((rows, cols))
+        L.check(L.lib().tjh_nll_loss_backward(t.data_ptr(), g.data_ptr(), rows, cols,
+                                              int(ignore_index), red, d.data_ptr()),
+                "nll_loss_backward")
+        return [d]
+    return _record(out, "NLLLoss", [x], bwd)
+
+
+def mse_loss(input, target, reduction="mean"):
+    """F.mse_loss (src/nn/losses.ts): mean((input - target)^2)."""
+    d = sub(input, target)
+    sq = d.pow(2)
+    if reduction == "mean":
+        return reduce_mean(sq)
+    if reduction == "sum":
+        return sq.sum()
+    return sq
+
+
+# ------------------------------------------------------------ normalisation
+
+
+def layer_norm(x, normalized_shape, weight=None, bias=None, eps=1e-5):
+    """nn.LayerNorm forward (layernorm.wgsl:14-42: biased variance, eps
+    inside the sqrt) and backward dx, dgamma, dbeta (torch.js has none, D10)."""
+    if isinstance(normalized_shape, int):
+        normalized_shape = (normalized_shape,)
+    normalized_shape = tuple(normalized_shape)
+    k = len(normalized_shape)
+    if x.shape[x.ndim - k:] != normalized_shape:
+        raise RuntimeError("layer_norm: input shape %s does not end with %s"
+                           % (list(x.shape), list(normalized_shape)))
+    cols = _numel(normalized_shape)
+    rows = x.numel() // max(cols, 1)
+    xc = contiguous(x.detach()) if x.dtype == "float32" else x.float().detach().contiguous()
+    w = weight.detach().contiguous() if weight is not None else None
+    b = bias.detach().contiguous() if bias is not None else None
+    y = empty(x.shape)
+    mean = empty((rows,))
+    rstd = empty((rows,))
+    L.check(L.lib().tjh_layer_norm_forward(xc.data_ptr(), w.data_ptr() if w is not None else None,
+                                           b.data_ptr() if b is not None else None, y.data_ptr(),
+                                           mean.data_ptr(), rstd.data_ptr(), rows, cols,
+                                           float(eps)), "layer_norm")
+    rx = x.requires_grad
+    rw = weight is not None and weight.requires_grad
+    rb = bias is not None and bias.requires_grad
+
+    def bwd(g):
+        g = g.contiguous()
+        dx = empty(x.shape) if rx else None
+        dw = empty(normalized_shape) if rw else None
+        db = empty(normalized_shape) if rb else None
+        L.check(L.lib().tjh_layer_norm_backward(
+            g.data_ptr(), xc.data_ptr(), w.data_ptr() if w is not None else None,
+            mean.data_ptr(), rstd.data_ptr(), dx.data_ptr() if dx is not None else None,
+            dw.data_ptr() if dw is not None else None, db.data_ptr() if db is not None else None,
+            rows, cols, 0), "layer_norm_backward")
+        return [dx, dw, db]
+    return _record(y, "LayerNorm", [x, weight, bias], bwd)
+
+
+# ------------------------------------------------------------ embedding / linear
+
+
+def embedding(input, weight):
+    """nn.Embedding lookup (embedding.wgsl:13-27, ids clamped); backward is a
+    deterministic scatter-add into the table (torch.js: TODO, D11)."""
+    ids = input
+    if not isinstance(ids, Tensor):
+        from .tensor import tensor as _tensor
+        ids = _tensor(np.asarray(ids, dtype=np.int32), dtype="int32")
+    if ids.dtype != "int32":
+        ids = ids.to("int32")
+    ids = ids.contiguous()
+    V, D = weight.shape
+    w = weight.detach().contiguous()
+    out = empty(ids.shape + (D,))
+    n = ids.numel()
+    L.check(L.lib().tjh_embedding_forward(w.data_ptr(), V, D, ids.data_ptr(), n, out.data_ptr()),
+            "embedding")
+
+    def bwd(g):
+        g = g.contiguous()
+        dw = empty((V, D))
+        L.check(L.lib().tjh_embedding_backward(g.data_ptr(), ids.data_ptr(), n, D, dw.data_ptr(),
+                                               V, 0), "embedding_backward")
+        return [dw]
+    return _record(out, "Embedding", [weight], bwd)
+
+
+def linear(x, weight, bias=None):
+    """y = x W^T + b (src/nn/linear.ts:43-66) as ONE GEMM with the bias in
+    the epilogue and W^T read in place; backward dx = g W, dW = g^T x
+    (split-K over tokens), db = column sum of g."""
+    if x.dtype != "float32":
+        x = x.float()
+    out_f, in_f = weight.shape
+    if x.shape[-1] != in_f:
+        raise RuntimeError("linear: input features %d != weight in_features %d"
+                           % (x.shape[-1], in_f))
+    lead = x.shape[:-1]
+    M = _numel(lead)
+    x2 = reshape(x.detach(), (M, in_f))
+    wd = weight.detach()
+    bd = bias.detach().contiguous() if bias is not None else None
+    out2 = _gemm(x2, wd.T, bias=bd, bias_mode=1 if bd is not None else 0)
+    out = reshape_raw(out2, lead + (out_f,))
+    rx, rw = x.requires_grad, weight.requires_grad
+    rb = bias is not None and bias.requires_grad
+
+    def bwd(g):
+        g2 = reshape_raw(g, (M, out_f))
+        dx = reshape_raw(_gemm(g2, wd), lead + (in_f,)) if rx else None
+        dw = _gemm(g2.T, x2) if rw else None
+        db = None
+        if rb:
+            gc = g2 if g2.is_contiguous() else _k_contiguous(g2)
+            db = _view_raw(_k_reduce("sum", gc, [0]), (out_f,))
+        return [dx, dw, db]
+    return _record(out, "Linear", [x, weight, bias], bwd)
+
+
+# ------------------------------------------------------------ convolution
+
+
+def _pair(v):
+    return (v, v) if isinstance(v, int) else tuple(v)
+
+
+def conv2d(input, weight, bias=None, stride=1, padding=0, dilation=1, groups=1):
+    """F.conv2d (src/nn/functional.ts:438-660): NCHW cross-correlation with
+    stride / padding / dilation / groups; dgrad, wgrad and bias grad
+    (torch.js never runs its conv backward, D8)."""
+    x = input
+    if x.dtype != "float32":
+        x = x.float()
+    if x.ndim != 4 or weight.ndim != 4:
+        raise RuntimeError("conv2d expects 4-D input and weight")
+    sh, sw = _pair(stride)
+    ph, pw = _pair(padding)
+    dh, dw_ = _pair(dilation)
+    n, c, h, w = x.shape
+    oc, cg, kh, kw = weight.shape
+    if cg * groups != c:
+        raise RuntimeError("conv2d: weight expects %d input channels, got %d" % (cg * groups, c))
+    oh = (h + 2 * ph - dh * (kh - 1) - 1) // sh + 1
+    ow = (w + 2 * pw - dw_ * (kw - 1) - 1) // sw + 1
+    desc = L.Conv2dDesc(n, c, h, w, oc, kh, kw, sh, sw, ph, pw, dh, dw_, groups, oh, ow)
+    xc = contiguous(x.detach())
+    wc = weight.detach().contiguous()
+    bc = bias.detach().contiguous() if bias is not None else None
+    y = empty((n, oc, oh, ow))
+    L.check(L.lib().tjh_conv2d_forward(ctypes.byref(desc), xc.data_ptr(), wc.data_ptr(),
+                                       bc.data_ptr() if bc is not None else None, y.data_ptr()),
+            "conv2d")
+    rx, rw = x.requires_grad, weight.requires_grad
+    rb = bias is not None and bias.requires_grad
+
+    def bwd(g):
+        g = g.contiguous()
+        dx = dwt = db = None
+        if rx:
+            dx = empty(x.shape)
+            L.check(L.lib().tjh_conv2d_backward_input(ctypes.byref(desc), g.data_ptr(),
+                                                      wc.data_ptr(), dx.data_ptr()),
+                    "conv2d_backward_input")
+        if rw:
+            dwt = empty(weight.shape)
+            L.check(L.lib().tjh_conv2d_backward_weight(ctypes.byref(desc), g.data_ptr(),
+                                                       xc.data_ptr(), dwt.data_ptr(), 0),
+                    "conv2d_backward_weight")
+        if rb:
+            db = _view_raw(_k_reduce("sum", g, [0, 2, 3]), (oc,))
+        return [dx, dwt, db]
+    return _record(y, "Conv2d", [x, weight, bias], bwd)
+
+
+# ------------------------------------------------------------ attention
+
+
+def _bhtd(t):
+    """[B,H,T,D] or [B,T,D] view -> (4-D view, strides of B,H,T)."""
+    if t.ndim == 3:
+        t = _alias(t, (t.shape[0], 1) + t.shape[1:], (t._strides[0], 0) + t._strides[1:],
+                   t._offset)
+    if t.ndim != 4:
+        raise RuntimeError("scaled_dot_product_attention expects 3-D or 4-D tensors")
+    if t._strides[3] != 1 and t.shape[3] > 1:
+        t = _k_contiguous(t)
+    return t
+
+
+def scaled_dot_product_attention(query, key, value, attn_mask=None, dropout_p=0.0,
+                                 is_causal=False, scale=None):
+    """softmax(Q K^T * scale [causal]) V (src/nn/functional.ts:866-890).
+    torch.js ignores is_causal and throws on attn_mask; the causal mask is
+    implemented here, attn_mask still raises.  The output is laid out
+    [B, T, H, D] in memory and returned as a [B, H, T, D] view, so the usual
+    transpose(1, 2) that follows is free."""
+    if attn_mask is not None:
+        raise NotImplementedError("scaled_dot_product_attention: attn_mask not yet implemented")
+    if dropout_p:
+        raise NotImplementedError("scaled_dot_product_attention: dropout is not on the hip path")
+    three = query.ndim == 3
+    q = _bhtd(query.detach())
+    k = _bhtd(key.detach())
+    v = _bhtd(value.detach())
+    B, H, Tq, D = q.shape
+    Tk = k.shape[2]
+    sc = float(scale) if scale is not None else 1.0 / math.sqrt(D)
+    ob = empty((B, Tq, H, D))
+    o = _alias(ob, (B, H, Tq, D), (Tq * H * D, D, H * D, 1), 0)
+    lse = empty((B, H, Tq))
+    L.check(L.lib().tjh_sdpa_forward(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                                     lse.data_ptr(), B, H, Tq, Tk, D, L.i64arr(q._strides[:3]),
+                                     L.i64arr(k._strides[:3]), L.i64arr(v._strides[:3]),
+                                     L.i64arr(o._strides[:3]), sc, 1 if is_causal else 0), "sdpa")
+
+    def grad_like(t):
+        Bx, Hx, Tx, Dx = t.shape
+        buf = empty((Bx, Tx, Hx, Dx))
+        return _alias(buf, t.shape, (Tx * Hx * Dx, Dx, Hx * Dx, 1), 0)
+
+    def bwd(g):
+        if three:
+            g = _alias(g, (g.shape[0], 1) + g.shape[1:], (g._strides[0], 0) + g._strides[1:],
+                       g._offset)
+        if g._strides[3] != 1:
+            g = _k_contiguous(g)
+        dq, dk, dv = grad_like(q), grad_like(k), grad_like(v)
+        arrs = [L.i64arr(t._strides[:3]) for t in (q, k, v, o, g, dq, dk, dv)]
+        ptrs = (L.P_i64 * 8)(*[ctypes.cast(a, L.P_i64) for a in arrs])
+        L.check(L.lib().tjh_sdpa_backward(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                                          g.data_ptr(), lse.data_ptr(), dq.data_ptr(),
+                                          dk.data_ptr(), dv.data_ptr(), B, H, Tq, Tk, D, ptrs, sc,
+                                          1 if is_causal else 0), "sdpa_backward")
+        if three:
+            dq, dk, dv = [_alias(t, (t.shape[0],) + t.shape[2:], (t._strides[0],) + t._strides[2:],
+                                 t._offset) for t in (dq, dk, dv)]
+        return [dq, dk, dv]
+    out = o
+    if three:
+        out = _alias(ob, (B, Tq, D), (Tq * D, D, 1), 0)
+    return _record(out, "SDPA", [query, key, value], bwd)
+
+
+# ------------------------------------------------------------ one_hot
+
+
+def one_hot(input, num_classes=-1):
+    """F.one_hot (src/nn/functional.ts:764-796): values are rounded
+    (Math.round), rows whose class is outside [0, C) stay zero, and C
+    defaults to floor(max) + 1 (read back from the device, as torch.js
+    does).  Float32 output of shape input.shape + (C,)."""
+    x = input.contiguous()
+    n = x.numel()
+    C = int(num_classes)
+    if C <= 0:
+        mx = float(x.numpy().max()) if n else 0.0
+        C = max(1, int(math.floor(mx)) + 1)
+    out = empty(x.shape + (C,))
+    if n:
+        if x.dtype == "int32":
+            L.check(L.lib().tjh_one_hot_i32(x.data_ptr(), n, C, out.data_ptr()), "one_hot")
+        else:
+            xf = x if x.dtype == "float32" else x.float()
+            L.check(L.lib().tjh_one_hot(xf.data_ptr(), n, C, out.data_ptr()), "one_hot")
+    return out

@@ -1,0 +1,342 @@
+"""torch.nn modules for the 'hip' device (src/nn/*.ts): the ones the
+autograd hot path uses.  Module bookkeeping mirrors src/nn/module.ts:17-270;
+the layer maths is in functional.py.
+"""
+import math
+from collections import OrderedDict
+
+import numpy as np
+
+from . import functional as F
+from .tensor import Tensor, from_numpy, ones, randn, zeros
+
+
+class Parameter(Tensor):
+    """A leaf tensor that requires grad (Parameter.create,
+    src/nn/parameter.ts:17-33): wraps the data without copying."""
+
+    __slots__ = ()
+
+    def __new__(cls, data, requires_grad=True):
+        return data.detach().requires_grad_(requires_grad)
+
+    @staticmethod
+    def create(data, requires_grad=True):
+        if isinstance(data, Tensor):
+            return data.detach().requires_grad_(requires_grad)
+        return from_numpy(np.asarray(data, dtype=np.float32), requires_grad=requires_grad)
+
+
+class Module:
+    """nn.Module (src/nn/module.ts:17-270)."""
+
+    def __init__(self):
+        object.__setattr__(self, "_parameters", OrderedDict())
+        object.__setattr__(self, "_modules", OrderedDict())
+        object.__setattr__(self, "training", True)
+
+    def __setattr__(self, name, value):
+        params = self.__dict__.get("_parameters")
+        mods = self.__dict__.get("_modules")
+        if isinstance(value, Module) and mods is not None:
+            mods[name] = value
+        elif isinstance(value, Tensor) and params is not None and value.requires_grad and \
+                value.is_leaf:
+            params[name] = value
+        object.__setattr__(self, name, value)
+
+    def register_parameter(self, name, param):
+        if param is None:
+            object.__setattr__(self, name, None)
+            return
+        self._parameters[name] = param
+        object.__setattr__(self, name, param)
+
+    def register_module(self, name, module):
+        self._modules[name] = module
+        object.__setattr__(self, name, module)
+
+    add_module = register_module
+
+    def forward(self, *args, **kwargs):
+        raise NotImplementedError
+
+    def __call__(self, *args, **kwargs):
+        return self.forward(*args, **kwargs)
+
+    def named_parameters(self, prefix=""):
+        seen = set()
+        for name, p in self._parameters.items():
+            if p is not None and id(p) not in seen:
+                seen.add(id(p))
+                yield (prefix + name, p)
+        for mname, m in self._modules.items():
+            for name, p in m.named_parameters(prefix + mname + "."):
+                if id(p) not in seen:
+                    seen.add(id(p))
+                    yield (name, p)
+
+    def parameters(self):
+        return [p for _, p in self.named_parameters()]
+
+    def children(self):
+        return list(self._modules.values())
+
+    def modules(self):
+        out = [self]
+        for m in self._modules.values():
+            out.extend(m.modules())
+        return out
+
+    def zero_grad(self, set_to_none=True):
+        for p in self.parameters():
+            p.grad = None
+
+    def train(self, mode=True):
+        for m in self.modules():
+            object.__setattr__(m, "training", mode)
+        return self
+
+    def eval(self):
+        return self.train(False)
+
+    def state_dict(self):
+        return OrderedDict((n, p.detach()) for n, p in self.named_parameters())
+
+    def load_state_dict(self, state):
+        params = dict(self.named_parameters())
+        for name, value in state.items():
+            if name not in params:
+                raise KeyError("unexpected key %s in state_dict" % name)
+            tgt = params[name]
+            src = value if isinstance(value, Tensor) else from_numpy(np.asarray(value))
+            if tuple(src.shape) != tgt.shape:
+                raise ValueError("size mismatch for %s: %s vs %s" % (name, list(src.shape),
+                                                                   list(tgt.shape)))
+            from .tensor import _copy_into
+            _copy_into(tgt, src)
+        return self
+
+
+class Linear(Module):
+    """nn.Linear (src/nn/linear.ts:15-67); default init randn*sqrt(1/in)
+    and zero bias, as torch.js initialises it (linear.ts:27-39)."""
+
+    def __init__(self, in_features, out_features, bias=True):
+        super().__init__()
+        self.in_features = in_features
+        self.out_features = out_features
+        k = math.sqrt(1.0 / in_features)
+        self.register_parameter("weight", Parameter.create(randn(out_features, in_features).mul(k)))
+        self.register_parameter("bias", Parameter.create(zeros(out_features)) if bias else None)
+
+    def forward(self, x):
+        if x.ndim == 1:
+            x = x.unsqueeze(0)
+        return F.linear(x, self.weight, self.bias)
+
+
+class LayerNorm(Module):
+    """nn.LayerNorm (src/nn/layernorm.ts:25-119)."""
+
+    def __init__(self, normalized_shape, eps=1e-5, elementwise_affine=True):
+        super().__init__()
+        if isinstance(normalized_shape, int):
+            normalized_shape = (normalized_shape,)
+        self.normalized_shape = tuple(normalized_shape)
+        self.eps = eps
+        self.elementwise_affine = elementwise_affine
+        if elementwise_affine:
+            self.register_parameter("weight", Parameter.create(ones(*self.normalized_shape)))
+            self.register_parameter("bias", Parameter.create(zeros(*self.normalized_shape)))
+        else:
+            self.weight = None
+            self.bias = None
+
+    def forward(self, x):
+        return F.layer_norm(x, self.normalized_shape, self.weight, self.bias, self.eps)
+
+
+class Embedding(Module):
+    """nn.Embedding (src/nn/embedding.ts:25-101); N(0,1) init."""
+
+    def __init__(self, num_embeddings, embedding_dim):
+        super().__init__()
+        self.num_embeddings = num_embeddings
+        self.embedding_dim = embedding_dim
+        self.register_parameter("weight", Parameter.create(randn(num_embeddings, embedding_dim)))
+
+    def forward(self, ids):
+        return F.embedding(ids, self.weight)
+
+
+class Conv2d(Module):
+    """nn.Conv2d (src/nn/conv.ts:470-530); default init randn*sqrt(1/fan_in)
+    (conv.ts:504-506)."""
+
+    def __init__(self, in_channels, out_channels, kernel_size, stride=1, padding=0, dilation=1,
+                 groups=1, bias=True):
+        super().__init__()
+        kh, kw = (kernel_size, kernel_size) if isinstance(kernel_size, int) else kernel_size
+        self.in_channels, self.out_channels = in_channels, out_channels
+        self.kernel_size = (kh, kw)
+        self.stride, self.padding, self.dilation, self.groups = stride, padding, dilation, groups
+        fan_in = in_channels // groups * kh * kw
+        k = math.sqrt(1.0 / fan_in)
+        self.register_parameter(
+            "weight", Parameter.create(randn(out_channels, in_channels // groups, kh, kw).mul(k)))
+        self.register_parameter("bias", Parameter.create(zeros(out_channels)) if bias else None)
+
+    def forward(self, x):
+        return F.conv2d(x, self.weight, self.bias, self.stride, self.padding, self.dilation,
+                        self.groups)
+
+
+class ReLU(Module):
+    def forward(self, x):
+        return F.relu(x)
+
+
+class GELU(Module):
+    def forward(self, x):
+        return F.gelu(x)
+
+
+class Sigmoid(Module):
+    def forward(self, x):
+        return F.sigmoid(x)
+
+
+class Tanh(Module):
+    def forward(self, x):
+        return F.tanh(x)
+
+
+class Identity(Module):
+    def forward(self, x):
+        return x
+
+
+class Dropout(Module):
+    """Identity in eval mode or with p == 0 (the configs use no dropout)."""
+
+    def __init__(self, p=0.5):
+        super().__init__()
+        self.p = p
+
+    def forward(self, x):
+        if not self.training or self.p == 0:
+            return x
+        raise NotImplementedError("Dropout with p > 0 in training mode is not on the hip path")
+
+
+class Flatten(Module):
+    def __init__(self, start_dim=1, end_dim=-1):
+        super().__init__()
+        self.start_dim, self.end_dim = start_dim, end_dim
+
+    def forward(self, x):
+        return x.flatten(self.start_dim, self.end_dim)
+
+
+class Sequential(Module):
+    """nn.Sequential (src/nn/sequential.ts:24-30)."""
+
+    def __init__(self, *mods):
+        super().__init__()
+        for i, m in enumerate(mods):
+            self.register_module(str(i), m)
+
+    def forward(self, x):
+        for m in self._modules.values():
+            x = m(x)
+        return x
+
+    def __getitem__(self, i):
+        return list(self._modules.values())[i]
+
+    def __len__(self):
+        return len(self._modules)
+
+
+class ModuleList(Module):
+    def __init__(self, mods=()):
+        super().__init__()
+        for i, m in enumerate(mods):
+            self.register_module(str(i), m)
+
+    def __iter__(self):
+        return iter(self._modules.values())
+
+    def __getitem__(self, i):
+        return list(self._modules.values())[i]
+
+    def __len__(self):
+        return len(self._modules)
+
+    def append(self, m):
+        self.register_module(str(len(self._modules)), m)
+        return self
+
+
+class CrossEntropyLoss(Module):
+    """nn.CrossEntropyLoss (src/nn/losses.ts:100-124)."""
+
+    def __init__(self, weight=None, reduction="mean", ignore_index=-100, label_smoothing=0.0):
+        super().__init__()
+        self.weight, self.reduction = weight, reduction
+        self.ignore_index, self.label_smoothing = ignore_index, label_smoothing
+
+    def forward(self, input, target):
+        return F.cross_entropy(input, target, self.weight, self.reduction, self.ignore_index,
+                               self.label_smoothing)
+
+
+class NLLLoss(Module):
+    def __init__(self, weight=None, reduction="mean", ignore_index=-100):
+        super().__init__()
+        self.weight, self.reduction, self.ignore_index = weight, reduction, ignore_index
+
+    def forward(self, input, target):
+        return F.nll_loss(input, target, self.weight, self.reduction, self.ignore_index)
+
+
+class MSELoss(Module):
+    def __init__(self, reduction="mean"):
+        super().__init__()
+        self.reduction = reduction
+
+    def forward(self, input, target):
+        return F.mse_loss(input, target, self.reduction)
+
+
+class init:
+    """nn.init (src/nn/init.ts:58-126) over the device RNG."""
+
+    @staticmethod
+    def zeros_(t):
+        from .tensor import no_grad
+        with no_grad():
+            t.zero_()
+        return t
+
+    @staticmethod
+    def ones_(t):
+        from .tensor import no_grad
+        with no_grad():
+            t.fill_(1.0)
+        return t
+
+    @staticmethod
+    def constant_(t, v):
+        from .tensor import no_grad
+        with no_grad():
+            t.fill_(v)
+        return t
+
+    @staticmethod
+    def normal_(t, mean=0.0, std=1.0):
+        from .tensor import _copy_into, no_grad
+        with no_grad():
+            _copy_into(t, randn(*t.shape).mul(std).add(mean))
+        return t

@@ -1,0 +1,1890 @@
+"""Tensor, device storage and the autograd engine of the 'hip' device.
+
+Mirrors torch.js's Tensor (src/tensor/Tensor.ts) for the autograd hot
+path: a Tensor owns (a view of) one device allocation made by the
+library's caching allocator, ops launch the library's HIP kernels on its
+single stream, and `backward()` walks the recorded graph in reverse
+topological order (Tensor.backward, Tensor.ts:3686-3740) with the
+PyTorch semantics torch.js declares:
+
+  * gradients ACCUMULATE into leaf `.grad` across backward calls until
+    zero_grad() (torch.js clears them on every call, Tensor.ts:3714-3719);
+  * every op that torch.js records has a correct vector-Jacobian product
+    (torch.js's matmul, t(), broadcast, GELU, softmax, LayerNorm,
+    Embedding, conv, expand and masked_fill gradients are missing or wrong,
+    Tensor.ts:2212-2221, 3395-3404, 3560-3564, 3627-3632, ...);
+  * views (reshape, transpose, permute, expand, narrow, indexing) share
+    storage and carry strides, so transposed GEMM operands and broadcast
+    gradients never materialise a copy; storage is reference counted, so
+    destroying one alias never frees another's memory (torch.js frees the
+    buffer of every alias, Tensor.ts:241-251).
+"""
+import ctypes
+import math
+import numbers
+
+import numpy as np
+
+from . import _lib as L
+
+# ----------------------------------------------------------------- dtypes
+
+# torch.js stores integer tensors as Int32Array (src/dtype.ts:7-15); int64
+# requests map to int32 the same way.
+_DT = {
+    "float32": (4, np.float32),
+    "int32": (4, np.int32),
+    "uint8": (1, np.uint8),
+    "bool": (1, np.uint8),
+}
+_ALIAS = {"float": "float32", "float16": "float32", "int64": "int32", "long": "int32",
+          "int": "int32", "uint32": "int32", "int8": "int32"}
+
+
+def _norm_dtype(dt):
+    if dt is None:
+        return "float32"
+    if not isinstance(dt, str):
+        dt = np.dtype(dt).name
+    dt = _ALIAS.get(dt, dt)
+    if dt not in _DT:
+        raise TypeError("unsupported dtype %r" % (dt,))
+    return dt
+
+
+# ----------------------------------------------------------------- device state
+
+_state = {"init": False, "ordinal": 0, "seed": None}
+
+
+def init(ordinal=0):
+    """Initialises the 'hip' device (torch.init / initWebGPU,
+    src/backend/webgpu/device.ts:27-86).  Idempotent."""
+    lib = L.lib()
+    L.check(lib.tjh_init(int(ordinal)), "torch.init")
+    _state["init"] = True
+    _state["ordinal"] = int(ordinal)
+    return None
+
+
+def is_initialized():
+    return _state["init"]
+
+
+def _require_init():
+    if not _state["init"]:
+        raise RuntimeError("hip backend not initialized. Call torch.init() first.")
+
+
+def synchronize():
+    """Waits for all queued device work (syncDevice, dispatch.ts:115-118)."""
+    _require_init()
+    L.check(L.lib().tjh_synchronize(), "synchronize")
+
+
+# ----------------------------------------------------------------- grad mode
+
+_grad = {"enabled": True}
+
+
+def is_grad_enabled():
+    return _grad["enabled"]
+
+
+class set_grad_enabled:
+    """Context manager / function (src/grad_mode.ts)."""
+
+    def __init__(self, mode):
+        self.prev = _grad["enabled"]
+        _grad["enabled"] = bool(mode)
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        _grad["enabled"] = self.prev
+        return False
+
+
+class no_grad:
+    """Disables graph recording (torch.no_grad).  torch.js's constructor
+    never disables it (src/grad_mode.ts:27-29); this one does."""
+
+    def __enter__(self):
+        self.prev = _grad["enabled"]
+        _grad["enabled"] = False
+        return self
+
+    def __exit__(self, *exc):
+        _grad["enabled"] = self.prev
+        return False
+
+    def __call__(self, fn):
+        def wrapper(*a, **k):
+            with no_grad():
+                return fn(*a, **k)
+        wrapper.__name__ = getattr(fn, "__name__", "wrapped")
+        return wrapper
+
+
+class enable_grad(no_grad):
+    def __enter__(self):
+        self.prev = _grad["enabled"]
+        _grad["enabled"] = True
+        return self
+
+
+inference_mode = no_grad
+
+# ----------------------------------------------------------------- storage
+
+
+class Storage:
+    """One device allocation from the library's stream-ordered cache."""
+
+    __slots__ = ("ptr", "nbytes", "__weakref__")
+
+    def __init__(self, nbytes):
+        self.ptr = 0
+        _require_init()
+        p = ctypes.c_void_p()
+        L.check(L.lib().tjh_malloc(int(nbytes), ctypes.byref(p)), "malloc")
+        self.ptr = p.value or 0
+        self.nbytes = int(nbytes)
+
+    def __del__(self):
+        lib = L._lib
+        if lib is not None and self.ptr:
+            try:
+                lib.tjh_free(self.ptr)
+            except Exception:
+                pass
+            self.ptr = 0
+
+
+def _contig_strides(shape):
+    st = [1] * len(shape)
+    s = 1
+    for d in range(len(shape) - 1, -1, -1):
+        st[d] = s
+        s *= shape[d]
+    return tuple(st)
+
+
+def _numel(shape):
+    n = 1
+    for s in shape:
+        n *= s
+    return n
+
+
+def _broadcast_shapes(a, b):
+    """broadcastShapes (src/utils/broadcast.ts:11-37)."""
+    n = max(len(a), len(b))
+    out = []
+    for i in range(n):
+        da = a[len(a) - n + i] if len(a) - n + i >= 0 else 1
+        db = b[len(b) - n + i] if len(b) - n + i >= 0 else 1
+        if da != db and da != 1 and db != 1:
+            raise ValueError("shapes %s and %s are not broadcastable" % (list(a), list(b)))
+        out.append(max(da, db) if da != 0 and db != 0 else 0)
+    return tuple(out)
+
+
+def _wrap_dim(d, ndim):
+    if ndim == 0 and d in (0, -1):
+        return 0
+    if d < -ndim or d >= ndim:
+        raise IndexError("dimension %d out of range for %d-d tensor" % (d, ndim))
+    return d + ndim if d < 0 else d
+
+
+# ----------------------------------------------------------------- autograd node
+
+
+class Node:
+    """grad_fn: the vector-Jacobian product of one recorded op
+    (GradFn, src/tensor/types.ts:13-17).  `inputs` are the op's tensor
+    arguments; `fn(grad)` returns one gradient (or None) per input."""
+
+    __slots__ = ("name", "inputs", "fn", "__weakref__")
+
+    def __init__(self, name, inputs, fn):
+        self.name = name
+        self.inputs = inputs
+        self.fn = fn
+
+    def __repr__(self):
+        return "<%sBackward>" % self.name
+
+    # torch.js exposes grad_fn._next_tensors (Tensor.ts:3702-3708)
+    @property
+    def next_tensors(self):
+        return [t for t in self.inputs if t is not None]
+
+
+def _record(out, name, inputs, fn):
+    if _grad["enabled"] and any(t is not None and t.requires_grad for t in inputs):
+        out.requires_grad = True
+        out.grad_fn = Node(name, [t if (t is not None and t.requires_grad) else None
+                                  for t in inputs], fn)
+    return out
+
+
+# ----------------------------------------------------------------- tensor
+
+
+class Tensor:
+    """A strided view of device memory on the 'hip' device."""
+
+    __slots__ = ("_storage", "_offset", "_shape", "_strides", "_dtype", "requires_grad",
+                 "_grad", "grad_fn", "_retains_grad", "__weakref__")
+
+    def __init__(self, storage, shape, strides=None, offset=0, dtype="float32",
+                 requires_grad=False):
+        self._storage = storage
+        self._shape = tuple(int(s) for s in shape)
+        self._strides = tuple(strides) if strides is not None else _contig_strides(self._shape)
+        self._offset = int(offset)
+        self._dtype = dtype
+        self.requires_grad = bool(requires_grad)
+        self._grad = None
+        self.grad_fn = None
+        self._retains_grad = False
+
+    # ------------------------------------------------------------ metadata
+    @property
+    def shape(self):
+        return self._shape
+
+    @property
+    def dtype(self):
+        return self._dtype
+
+    @property
+    def device(self):
+        return "hip"
+
+    @property
+    def ndim(self):
+        return len(self._shape)
+
+    def dim(self):
+        return len(self._shape)
+
+    def numel(self):
+        return _numel(self._shape)
+
+    def size(self, dim=None):
+        if dim is None:
+            return self._shape
+        return self._shape[_wrap_dim(dim, self.ndim)]
+
+    def stride(self, dim=None):
+        if dim is None:
+            return self._strides
+        return self._strides[_wrap_dim(dim, self.ndim)]
+
+    @property
+    def itemsize(self):
+        return _DT[self._dtype][0]
+
+    @property
+    def is_leaf(self):
+        return self.grad_fn is None
+
+    @property
+    def grad(self):
+        return self._grad
+
+    @grad.setter
+    def grad(self, g):
+        self._grad = g
+
+    def data_ptr(self):
+        return self._storage.ptr + self._offset * self.itemsize
+
+    def is_contiguous(self):
+        return self._strides == _contig_strides(self._shape) or self.numel() <= 1 or \
+            all(st == cs for st, cs, sz in zip(self._strides, _contig_strides(self._shape),
+                                               self._shape) if sz != 1)
+
+    def retain_grad(self):
+        self._retains_grad = True
+        return self
+
+    def requires_grad_(self, value=True):
+        self.requires_grad = bool(value)
+        return self
+
+    def __repr__(self):
+        try:
+            arr = self.numpy()
+            body = np.array2string(arr, precision=4, threshold=20)
+        except Exception as e:  # pragma: no cover
+            body = "<unreadable: %s>" % e
+        gf = ", grad_fn=%r" % self.grad_fn if self.grad_fn is not None else ""
+        return "tensor(%s, device='hip', dtype=%s%s)" % (body, self._dtype, gf)
+
+    def __len__(self):
+        if not self._shape:
+            raise TypeError("len() of a 0-d tensor")
+        return self._shape[0]
+
+    # ------------------------------------------------------------ host copies
+    def numpy(self):
+        """Blocking device->host copy (readBuffer, buffer.ts:150-206)."""
+        t = self if self.is_contiguous() else _k_contiguous(self)
+        npdt = _DT[t._dtype][1]
+        out = np.empty(t._shape, dtype=npdt)
+        if out.size:
+            L.check(L.lib().tjh_d2h(out.ctypes.data, t.data_ptr(), out.nbytes), "d2h")
+        return out
+
+    def toArray(self):
+        """Flat list like torch.js's toArray(), -0 normalised to 0
+        (Tensor.ts:253-257)."""
+        a = self.numpy().reshape(-1)
+        if a.dtype == np.float32:
+            a = a + np.float32(0.0)  # -0 -> +0
+        return a.tolist()
+
+    def tolist(self):
+        return self.numpy().tolist()
+
+    def item(self):
+        if self.numel() != 1:
+            raise ValueError("item() needs a one-element tensor, got shape %s" % (list(self._shape),))
+        return self.numpy().reshape(-1)[0].item()
+
+    def __float__(self):
+        return float(self.item())
+
+    # ------------------------------------------------------------ autograd
+    def backward(self, gradient=None, retain_graph=False, create_graph=False):
+        """Tensor.backward (Tensor.ts:3686-3740)."""
+        if create_graph:
+            raise NotImplementedError("create_graph=True is not supported on the hip device")
+        if not self.requires_grad:
+            raise RuntimeError("element 0 of tensors does not require grad and does not have a grad_fn")
+        if gradient is None:
+            if self.numel() != 1:
+                raise RuntimeError("grad can be implicitly created only for scalar outputs")
+            gradient = full(self._shape, 1.0)
+        run_backward([(self, gradient)], retain_graph=retain_graph)
+
+    def detach(self):
+        return Tensor(self._storage, self._shape, self._strides, self._offset, self._dtype)
+
+    def detach_(self):
+        self.grad_fn = None
+        self.requires_grad = False
+        return self
+
+    def zero_(self):
+        _require_writable(self)
+        _fill_view(self, 0.0)
+        return self
+
+    def fill_(self, value):
+        _require_writable(self)
+        _fill_view(self, float(value))
+        return self
+
+    def copy_(self, src):
+        """In-place copy (Tensor.copy_, Tensor.ts:437-446); broadcasts src."""
+        _require_writable(self)
+        src = _as_tensor(src, like=self)
+        if src._dtype != self._dtype:
+            src = src.to(self._dtype)
+        s = src.expand(self._shape) if src._shape != self._shape else src
+        _copy_into(self, s)
+        return self
+
+    def to(self, arg=None, dtype=None):
+        """Tensor.to(dtype | device) (Tensor.ts:904-936)."""
+        target = dtype if dtype is not None else arg
+        if target in (None, "hip", "cuda", "webgpu"):
+            return self
+        if target == "cpu":
+            raise RuntimeError("the hip device has no CPU tensors; use .numpy() to read values")
+        dt = _norm_dtype(target)
+        if dt == self._dtype:
+            return self
+        return _k_cast(self, dt)
+
+    def float(self):
+        return self.to("float32")
+
+    def int(self):
+        return self.to("int32")
+
+    def long(self):
+        return self.to("int32")
+
+    # ------------------------------------------------------------ operators
+    def __add__(self, o):
+        return add(self, o)
+
+    def __radd__(self, o):
+        return add(self, o)
+
+    def __sub__(self, o):
+        return sub(self, o)
+
+    def __rsub__(self, o):
+        return rsub(self, o)
+
+    def __mul__(self, o):
+        return mul(self, o)
+
+    def __rmul__(self, o):
+        return mul(self, o)
+
+    def __truediv__(self, o):
+        return div(self, o)
+
+    def __rtruediv__(self, o):
+        return rdiv(self, o)
+
+    def __pow__(self, o):
+        return pow(self, o)
+
+    def __neg__(self):
+        return neg(self)
+
+    def __matmul__(self, o):
+        return matmul(self, o)
+
+    def __getitem__(self, idx):
+        return _getitem(self, idx)
+
+    def __lt__(self, o):
+        return compare(self, o, "lt")
+
+    def __le__(self, o):
+        return compare(self, o, "le")
+
+    def __gt__(self, o):
+        return compare(self, o, "gt")
+
+    def __ge__(self, o):
+        return compare(self, o, "ge")
+
+    # torch.js method names (Tensor.ts:476-2600)
+    def add(self, o, alpha=1.0):
+        if alpha != 1.0:
+            o = mul(o, alpha) if isinstance(o, Tensor) else o * alpha
+        return add(self, o)
+
+    def sub(self, o):
+        return sub(self, o)
+
+    def mul(self, o):
+        return mul(self, o)
+
+    def div(self, o):
+        return div(self, o)
+
+    def pow(self, o):
+        return pow(self, o)
+
+    def neg(self):
+        return neg(self)
+
+    def matmul(self, o):
+        return matmul(self, o)
+
+    def mm(self, o):
+        if self.ndim != 2 or o.ndim != 2:
+            raise RuntimeError("mm expects 2-D tensors")
+        return matmul(self, o)
+
+    def bmm(self, o):
+        if self.ndim != 3 or o.ndim != 3:
+            raise RuntimeError("bmm expects 3-D tensors")
+        return matmul(self, o)
+
+    def maximum(self, o):
+        return _binary_op("maximum", self, o)
+
+    def minimum(self, o):
+        return _binary_op("minimum", self, o)
+
+    def eq(self, o):
+        return compare(self, o, "eq")
+
+    def ne(self, o):
+        return compare(self, o, "ne")
+
+    def lt(self, o):
+        return compare(self, o, "lt")
+
+    def le(self, o):
+        return compare(self, o, "le")
+
+    def gt(self, o):
+        return compare(self, o, "gt")
+
+    def ge(self, o):
+        return compare(self, o, "ge")
+
+    def sum(self, dim=None, keepdim=False):
+        return reduce_sum(self, dim, keepdim)
+
+    def mean(self, dim=None, keepdim=False):
+        return reduce_mean(self, dim, keepdim)
+
+    def amax(self, dim=None, keepdim=False):
+        return reduce_minmax(self, dim, keepdim, "max")
+
+    def amin(self, dim=None, keepdim=False):
+        return reduce_minmax(self, dim, keepdim, "min")
+
+    def max(self, dim=None, keepdim=False):
+        return reduce_minmax(self, dim, keepdim, "max")
+
+    def min(self, dim=None, keepdim=False):
+        return reduce_minmax(self, dim, keepdim, "min")
+
+    def argmax(self, dim=None, keepdim=False):
+        return argmax(self, dim, keepdim)
+
+    def argmin(self, dim=None, keepdim=False):
+        return argmax(self, dim, keepdim, is_min=True)
+
+    def softmax(self, dim=-1):
+        from .functional import softmax as _softmax
+        return _softmax(self, dim)
+
+    def log_softmax(self, dim=-1):
+        from .functional import log_softmax as _log_softmax
+        return _log_softmax(self, dim)
+
+    def masked_fill(self, mask, value):
+        return masked_fill(self, mask, value)
+
+    def index_select(self, dim, index):
+        return index_select(self, dim, index)
+
+    def gather(self, dim, index):
+        return gather(self, dim, index)
+
+    def nonzero(self):
+        return nonzero(self)
+
+    def clone(self):
+        return clone(self)
+
+    def contiguous(self):
+        return contiguous(self)
+
+    def reshape(self, *shape):
+        return reshape(self, _shape_arg(shape))
+
+    def view(self, *shape):
+        return view(self, _shape_arg(shape))
+
+    def flatten(self, start_dim=0, end_dim=-1):
+        return flatten(self, start_dim, end_dim)
+
+    def squeeze(self, dim=None):
+        return squeeze(self, dim)
+
+    def unsqueeze(self, dim):
+        return unsqueeze(self, dim)
+
+    def transpose(self, d0, d1):
+        return transpose(self, d0, d1)
+
+    def swapaxes(self, d0, d1):
+        return transpose(self, d0, d1)
+
+    def permute(self, *dims):
+        return permute(self, _shape_arg(dims))
+
+    def t(self):
+        if self.ndim > 2:
+            raise RuntimeError("t() expects a tensor with <= 2 dimensions")
+        return transpose(self, 0, 1) if self.ndim == 2 else self
+
+    @property
+    def T(self):
+        return permute(self, tuple(range(self.ndim - 1, -1, -1)))
+
+    def expand(self, *shape):
+        return expand(self, _shape_arg(shape))
+
+    def broadcast_to(self, shape):
+        return expand(self, tuple(shape))
+
+    def expand_as(self, other):
+        return expand(self, other.shape)
+
+    def narrow(self, dim, start, length):
+        return narrow(self, dim, start, length)
+
+    def split(self, split_size, dim=0):
+        return split(self, split_size, dim)
+
+    def chunk(self, chunks, dim=0):
+        return chunk(self, chunks, dim)
+
+    def unbind(self, dim=0):
+        return [select(self, dim, i) for i in range(self.shape[_wrap_dim(dim, self.ndim)])]
+
+    def select(self, dim, index):
+        return select(self, dim, index)
+
+
+def _shape_arg(shape):
+    if len(shape) == 1 and isinstance(shape[0], (list, tuple)):
+        return tuple(shape[0])
+    return tuple(shape)
+
+
+def _add_unary_methods():
+    names = ["exp", "log", "sqrt", "rsqrt", "tanh", "sigmoid", "relu", "gelu", "square",
+             "reciprocal", "erf", "abs", "sin", "cos", "silu", "softplus", "sign"]
+    for n in names:
+        def m(self, _n=n):
+            return unary(_n, self)
+        m.__name__ = n
+        setattr(Tensor, n, m)
+
+    def leaky_relu(self, negative_slope=0.01):
+        return unary("leaky_relu", self, negative_slope)
+
+    def elu(self, alpha=1.0):
+        return unary("elu", self, alpha)
+
+    Tensor.leaky_relu = leaky_relu
+    Tensor.elu = elu
+
+
+# ----------------------------------------------------------------- allocation
+
+
+def empty(shape, dtype="float32", requires_grad=False):
+    shape = tuple(int(s) for s in shape)
+    dtype = _norm_dtype(dtype)
+    st = Storage(max(1, _numel(shape)) * _DT[dtype][0])
+    return Tensor(st, shape, None, 0, dtype, requires_grad)
+
+
+def _empty_padded(rows, cols):
+    """[rows, cols] fp32 whose row stride is rounded up to 4 floats, so every
+    row starts 16-byte aligned (GEMM outputs whose N is not a multiple of
+    4, e.g. a 50257-wide vocabulary)."""
+    ld = (cols + 3) // 4 * 4
+    st = Storage(max(1, rows * ld) * 4)
+    return Tensor(st, (rows, cols), (ld, 1), 0, "float32")
+
+
+def _fill_view(t, value):
+    lib = L.lib()
+    if t.numel() == 0:
+        return
+    if t.is_contiguous():
+        if t._dtype == "float32":
+            L.check(lib.tjh_fill_f32(t.data_ptr(), t.numel(), float(value)), "fill")
+        elif t._dtype == "int32":
+            L.check(lib.tjh_fill_i32(t.data_ptr(), t.numel(), int(value)), "fill")
+        else:
+            tmp = np.full(t._shape, value, dtype=np.uint8)
+            L.check(lib.tjh_h2d(t.data_ptr(), tmp.ctypes.data, tmp.nbytes), "h2d")
+        return
+    src = full((1,), value, dtype=t._dtype).expand(t._shape)
+    _copy_into(t, src)
+
+
+def _require_writable(t):
+    if _grad["enabled"] and t.requires_grad and t.is_leaf:
+        raise RuntimeError("a leaf Variable that requires grad is being used in an in-place operation.")
+
+
+def full(shape, value, dtype="float32", requires_grad=False):
+    t = empty(shape, dtype)
+    _fill_view(t, value)
+    t.requires_grad = requires_grad
+    return t
+
+
+def zeros(*shape, dtype="float32", requires_grad=False):
+    return full(_shape_arg(shape), 0.0, dtype, requires_grad)
+
+
+def ones(*shape, dtype="float32", requires_grad=False):
+    return full(_shape_arg(shape), 1.0, dtype, requires_grad)
+
+
+def zeros_like(t, dtype=None, requires_grad=False):
+    return full(t.shape, 0.0, dtype or t.dtype, requires_grad)
+
+
+def ones_like(t, dtype=None, requires_grad=False):
+    return full(t.shape, 1.0, dtype or t.dtype, requires_grad)
+
+
+def full_like(t, value, dtype=None, requires_grad=False):
+    return full(t.shape, value, dtype or t.dtype, requires_grad)
+
+
+def from_numpy(a, requires_grad=False, dtype=None):
+    a = np.asarray(a)
+    if dtype is None:
+        if a.dtype.kind == "f":
+            dtype = "float32"
+        elif a.dtype.kind == "b":
+            dtype = "bool"
+        elif a.dtype.kind in "iu":
+            dtype = "int32"
+        else:
+            raise TypeError("unsupported numpy dtype %s" % a.dtype)
+    dtype = _norm_dtype(dtype)
+    a = np.asarray(a, dtype=_DT[dtype][1])  # keeps 0-d arrays 0-d
+    if not a.flags.c_contiguous:
+        a = a.copy(order="C")
+    t = empty(a.shape, dtype)
+    if a.size:
+        L.check(L.lib().tjh_h2d(t.data_ptr(), a.ctypes.data, a.nbytes), "h2d")
+    t.requires_grad = requires_grad
+    return t
+
+
+def tensor(data, dtype=None, device="hip", requires_grad=False):
+    """torch.tensor (src/ops/creation.ts:60-84).  Python numbers are JS
+    numbers there, so lists default to float32; numpy arrays keep their
+    kind (integer arrays become int32)."""
+    if isinstance(data, Tensor):
+        t = clone(data.detach())
+        if dtype is not None:
+            t = t.to(dtype)
+        t.requires_grad = requires_grad
+        return t
+    if isinstance(data, np.ndarray):
+        return from_numpy(data, requires_grad=requires_grad, dtype=dtype)
+    a = np.asarray(data, dtype=np.float64)
+    return from_numpy(a, requires_grad=requires_grad, dtype=dtype or "float32")
+
+
+def manual_seed(seed):
+    """Sets the global seed of rand/randn (src/ops/creation.ts:906-908)."""
+    _state["seed"] = int(seed)
+
+
+def _next_seed():
+    # torch.js seeds each rand/randn call with an LCG step of a global seed
+    # (src/ops/creation.ts:921); an unset seed starts from a random value.
+    if _state["seed"] is None:
+        _state["seed"] = int(np.random.randint(0, 2147483647))
+    _state["seed"] = (_state["seed"] * 1103515245 + 12345) & 0x7FFFFFFF
+    return _state["seed"]
+
+
+def _random(shape, normal, requires_grad):
+    t = empty(_shape_arg(shape))
+    if t.numel():
+        L.check(L.lib().tjh_random(t.data_ptr(), t.numel(), _next_seed(), 1 if normal else 0),
+                "random")
+    t.requires_grad = requires_grad
+    return t
+
+
+def rand(*shape, requires_grad=False, dtype=None):
+    """U[0,1) from random.wgsl:17-29's xorshift generator."""
+    return _random(shape, False, requires_grad)
+
+
+def randn(*shape, requires_grad=False, dtype=None):
+    """N(0,1) by Box-Muller from random.wgsl:31-46's generator."""
+    return _random(shape, True, requires_grad)
+
+
+def arange(start, end=None, step=1, dtype=None, requires_grad=False):
+    if end is None:
+        start, end = 0, start
+    isint = all(float(v).is_integer() for v in (start, end, step))
+    dtype = _norm_dtype(dtype or ("int32" if isint else "float32"))
+    a = np.arange(start, end, step).astype(_DT[dtype][1])
+    return from_numpy(a, requires_grad=requires_grad, dtype=dtype)
+
+
+def _as_tensor(x, like=None):
+    if isinstance(x, Tensor):
+        return x
+    dt = like.dtype if like is not None and like.dtype == "float32" else "float32"
+    return full((), float(x), dtype=dt)
+
+
+# ----------------------------------------------------------------- raw kernels
+# Non-differentiable helpers: allocate the output and launch.
+
+
+def _k_contiguous(x):
+    out = empty(x._shape, x._dtype)
+    _copy_into(out, x)
+    return out
+
+
+def _copy_into(dst, src):
+    """dst[...] = src[...] for equal shapes, any strides."""
+    if dst.numel() == 0:
+        return
+    lib = L.lib()
+    shp = L.i64arr(dst._shape)
+    nd = len(dst._shape)
+    if dst._dtype == "float32":
+        L.check(lib.tjh_copy_strided(nd, shp, src.data_ptr(), L.i64arr(src._strides),
+                                     dst.data_ptr(), L.i64arr(dst._strides)), "copy")
+    elif dst._dtype == "int32":
+        L.check(lib.tjh_copy_strided_i32(nd, shp, src.data_ptr(), L.i64arr(src._strides),
+                                         dst.data_ptr(), L.i64arr(dst._strides)), "copy")
+    else:
+        a = src.numpy()
+        if not dst.is_contiguous():
+            raise RuntimeError("strided uint8 copies are not supported")
+        L.check(lib.tjh_h2d(dst.data_ptr(), np.ascontiguousarray(a).ctypes.data, a.nbytes), "h2d")
+
+
+def _k_cast(x, dtype):
+    x = x.contiguous()
+    out = empty(x._shape, dtype)
+    n = x.numel()
+    lib = L.lib()
+    if x._dtype == "float32" and dtype == "int32":
+        L.check(lib.tjh_cast_f32_i32(x.data_ptr(), out.data_ptr(), n), "cast")
+    elif x._dtype == "int32" and dtype == "float32":
+        L.check(lib.tjh_cast_i32_f32(x.data_ptr(), out.data_ptr(), n), "cast")
+    else:
+        a = x.numpy().astype(_DT[dtype][1])
+        return from_numpy(a, dtype=dtype)
+    return out
+
+
+def _k_unary(op, x, alpha=0.0):
+    x = x.contiguous()
+    out = empty(x._shape)
+    L.check(L.lib().tjh_unary(L.UNARY[op], x.data_ptr(), out.data_ptr(), x.numel(), float(alpha)),
+            op)
+    return out
+
+
+def _k_unary_bwd(op, g, x, y, alpha=0.0):
+    g = g.contiguous()
+    out = empty(g._shape)
+    L.check(L.lib().tjh_unary_backward(
+        L.UNARY[op], g.data_ptr(), x.contiguous().data_ptr() if x is not None else None,
+        y.contiguous().data_ptr() if y is not None else None, out.data_ptr(), g.numel(),
+        float(alpha)), op + "_backward")
+    return out
+
+
+def _bstrides(t, shape):
+    """Strides of t broadcast to `shape` (0 on broadcast dims)."""
+    nd = len(shape)
+    off = nd - t.ndim
+    st = []
+    for d in range(nd):
+        if d < off:
+            st.append(0)
+        else:
+            sz = t._shape[d - off]
+            st.append(0 if (sz == 1 and shape[d] != 1) else t._strides[d - off])
+    return st
+
+
+def _k_binary(op, a, b):
+    shape = _broadcast_shapes(a._shape, b._shape)
+    out = empty(shape)
+    if out.numel():
+        L.check(L.lib().tjh_binary(L.BINARY[op], len(shape), L.i64arr(shape), a.data_ptr(),
+                                   L.i64arr(_bstrides(a, shape)), b.data_ptr(),
+                                   L.i64arr(_bstrides(b, shape)), out.data_ptr()), op)
+    return out
+
+
+def _k_ternary(op, g, a, b, shape):
+    out = empty(shape)
+    if out.numel():
+        L.check(L.lib().tjh_ternary(L.TERNARY[op], len(shape), L.i64arr(shape), g.data_ptr(),
+                                    L.i64arr(_bstrides(g, shape)), a.data_ptr(),
+                                    L.i64arr(_bstrides(a, shape)), b.data_ptr(),
+                                    L.i64arr(_bstrides(b, shape)), out.data_ptr()), op)
+    return out
+
+
+def _k_scalar(op, x, s, reverse=False):
+    x = x.contiguous()
+    out = empty(x._shape)
+    L.check(L.lib().tjh_scalar(L.SCALAR[op], x.data_ptr(), float(s), 1 if reverse else 0,
+                               out.data_ptr(), x.numel()), op)
+    return out
+
+
+def _k_axpy(alpha, x, y):
+    """alpha*x + y (same shape)."""
+    x = x.contiguous()
+    y = y.contiguous()
+    out = empty(x._shape)
+    L.check(L.lib().tjh_axpy(float(alpha), x.data_ptr(), y.data_ptr(), out.data_ptr(), x.numel()),
+            "axpy")
+    return out
+
+
+def _reduce_runs(shape, dims):
+    """Groups sorted reduced dims into maximal runs of adjacent dims."""
+    runs = []
+    for d in sorted(dims):
+        if runs and runs[-1][1] == d:
+            runs[-1][1] = d + 1
+        else:
+            runs.append([d, d + 1])
+    return runs
+
+
+def _k_reduce(op, x, dims):
+    """Reduces the given dims of x (keepdim=True layout), fp32."""
+    x = x.contiguous()
+    shape = list(x._shape)
+    dims = sorted(set(dims))
+    total_r = 1
+    for d in dims:
+        total_r *= shape[d]
+    cur = x
+    # reduce runs from the last to the first so earlier indices stay valid
+    for beg, end in reversed(_reduce_runs(shape, dims)):
+        cshape = list(cur._shape)
+        outer = _numel(cshape[:beg])
+        r = _numel(cshape[beg:end])
+        inner = _numel(cshape[end:])
+        oshape = cshape[:beg] + [1] * (end - beg) + cshape[end:]
+        out = empty(oshape)
+        kop = op
+        if op == "mean":
+            kop = "sum"
+        L.check(L.lib().tjh_reduce(L.REDUCE[kop], cur.data_ptr(), outer, r, inner,
+                                   out.data_ptr()), "reduce")
+        cur = out
+    if op == "mean":
+        cur = _k_scalar("mul", cur, 1.0 / total_r if total_r else float("nan"))
+    return cur
+
+
+def _sum_to(g, shape):
+    """Sums a broadcast gradient back to `shape` (torch.js only handles 1-D
+    against 2-D, Tensor.ts:3560-3591)."""
+    shape = tuple(shape)
+    if g._shape == shape:
+        return g
+    nd = g.ndim
+    off = nd - len(shape)
+    dims = [d for d in range(nd) if d < off or (shape[d - off] == 1 and g._shape[d] != 1)]
+    r = _k_reduce("sum", g, dims) if dims else g
+    return _view_raw(r.contiguous(), shape)
+
+
+def _view_raw(t, shape):
+    """View of a contiguous tensor with a new shape (no autograd)."""
+    if _numel(shape) != t.numel():
+        raise RuntimeError("shape %s is invalid for input of size %d" % (list(shape), t.numel()))
+    return Tensor(t._storage, shape, None, t._offset, t._dtype)
+
+
+# ----------------------------------------------------------------- differentiable ops
+
+
+def unary(op, x, alpha=0.0):
+    """_unaryOp (Tensor.ts:3593-3656) with the backward from unary.wgsl's
+    derivatives; GELU uses the exact Phi(x) + x*phi(x) (torch.js uses a tanh
+    form with a wrong pdf term, Tensor.ts:3627-3632)."""
+    if x.dtype != "float32":
+        x = x.float()
+    out = _k_unary(op, x, alpha)
+    needs_y = op in ("exp", "sqrt", "rsqrt", "tanh", "sigmoid", "reciprocal")
+    needs_x = op not in ("neg",) and not needs_y
+    saved_x = x if needs_x else None
+    saved_y = out.detach() if needs_y else None
+
+    def bwd(g):
+        return [_k_unary_bwd(op, g, saved_x, saved_y, alpha)]
+    return _record(out, op, [x], bwd)
+
+
+def neg(x):
+    return unary("neg", x)
+
+
+def _binary_op(op, a, b):
+    if not isinstance(b, Tensor):
+        return _scalar_op(op, a, b)
+    if not isinstance(a, Tensor):
+        return _scalar_op(op, b, a, reverse=True)
+    if a.dtype != "float32":
+        a = a.float()
+    if b.dtype != "float32":
+        b = b.float()
+    out = _k_binary(op, a, b)
+    ash, bsh = a.shape, b.shape
+    ra, rb = a.requires_grad, b.requires_grad
+    if op == "add":
+        def bwd(g):
+            return [_sum_to(g, ash) if ra else None, _sum_to(g, bsh) if rb else None]
+    elif op == "sub":
+        def bwd(g):
+            return [_sum_to(g, ash) if ra else None,
+                    _sum_to(_k_unary("neg", g), bsh) if rb else None]
+    else:
+        sa, sb = a.detach(), b.detach()
+        if op == "mul":
+            def bwd(g):
+                return [_sum_to(_k_binary("mul", g, sb), ash) if ra else None,
+                        _sum_to(_k_binary("mul", g, sa), bsh) if rb else None]
+        elif op == "div":
+            def bwd(g):
+                return [_sum_to(_k_binary("div", g, sb), ash) if ra else None,
+                        _sum_to(_k_ternary("div_b", g, sa, sb, g.shape), bsh) if rb else None]
+        elif op == "pow":
+            def bwd(g):
+                return [_sum_to(_k_ternary("pow_a", g, sa, sb, g.shape), ash) if ra else None,
+                        _sum_to(_k_ternary("pow_b", g, sa, sb, g.shape), bsh) if rb else None]
+        else:  # maximum / minimum: ties split the gradient evenly
+            def bwd(g):
+                sel = compare_raw(sa, sb, "gt" if op == "maximum" else "lt")
+                eq = compare_raw(sa, sb, "eq")
+                wa = _k_binary("add", sel, _k_scalar("mul", eq, 0.5))
+                wb = _k_scalar("add", _k_scalar("mul", wa, -1.0), 1.0)
+                return [_sum_to(_k_binary("mul", g, wa), ash) if ra else None,
+                        _sum_to(_k_binary("mul", g, wb), bsh) if rb else None]
+    return _record(out, op, [a, b], bwd)
+
+
+def _scalar_op(op, x, s, reverse=False):
+    if isinstance(s, Tensor):
+        raise TypeError("scalar op with tensor")
+    if x.dtype != "float32":
+        x = x.float()
+    s = float(s)
+    out = _k_scalar(op, x, s, reverse)
+
+    def bwd(g):
+        if op == "add":
+            return [g]
+        if op == "sub":
+            return [_k_unary("neg", g) if reverse else g]
+        if op == "mul":
+            return [_k_scalar("mul", g, s)]
+        if op == "div":
+            if not reverse:
+                return [_k_scalar("div", g, s)]
+            # d(s/x) = -s/x^2
+            return [_k_ternary("div_b", _k_scalar("mul", g, s), full((), 1.0), x, g.shape)]
+        if op == "pow":
+            if not reverse:
+                gg = g.contiguous()
+                o = empty(gg.shape)
+                L.check(L.lib().tjh_pow_scalar_backward(gg.data_ptr(), x.contiguous().data_ptr(),
+                                                        s, o.data_ptr(), gg.numel()), "pow_bwd")
+                return [o]
+            # d(s^x) = s^x ln s
+            return [_k_scalar("mul", _k_binary("mul", g, out.detach()), math.log(s))]
+        if op in ("maximum", "minimum"):
+            m = compare_raw(x, full((), s), "gt" if op == "maximum" else "lt")
+            return [_k_binary("mul", g, m)]
+        raise NotImplementedError(op)
+    return _record(out, op + "_scalar", [x], bwd)
+
+
+def add(a, b):
+    return _binary_op("add", a, b)
+
+
+def sub(a, b):
+    return _binary_op("sub", a, b)
+
+
+def rsub(a, b):
+    """b - a for a scalar b."""
+    return _scalar_op("sub", a, b, reverse=True)
+
+
+def mul(a, b):
+    return _binary_op("mul", a, b)
+
+
+def div(a, b):
+    return _binary_op("div", a, b)
+
+
+def rdiv(a, b):
+    return _scalar_op("div", a, b, reverse=True)
+
+
+def pow(a, b):
+    """pow with torch.js's integer-exponent rule for scalars (scalar.wgsl:53-66)."""
+    if isinstance(a, Tensor) and not isinstance(b, Tensor):
+        return _scalar_op("pow", a, b)
+    if not isinstance(a, Tensor):
+        return _scalar_op("pow", b, a, reverse=True)
+    return _binary_op("pow", a, b)
+
+
+def compare_raw(a, b, op):
+    if not isinstance(b, Tensor):
+        b = full((), float(b))
+    if not isinstance(a, Tensor):
+        a = full((), float(a))
+    a = a.float() if a.dtype != "float32" else a
+    b = b.float() if b.dtype != "float32" else b
+    shape = _broadcast_shapes(a.shape, b.shape)
+    out = empty(shape)
+    if out.numel():
+        L.check(L.lib().tjh_compare(L.COMPARE[op], len(shape), L.i64arr(shape), a.data_ptr(),
+                                    L.i64arr(_bstrides(a, shape)), b.data_ptr(),
+                                    L.i64arr(_bstrides(b, shape)), out.data_ptr()), op)
+    return out
+
+
+def compare(a, b, op):
+    """eq/ne/lt/le/gt/ge producing float 0/1 (compare.wgsl); no gradient."""
+    return compare_raw(a, b, op)
+
+
+# ------------------------------------------------------------ reductions
+
+
+def _norm_dims(x, dim):
+    if dim is None:
+        return list(range(x.ndim))
+    if isinstance(dim, (list, tuple)):
+        return sorted(set(_wrap_dim(d, x.ndim) for d in dim))
+    return [_wrap_dim(dim, x.ndim)]
+
+
+def _squeeze_shape(shape, dims):
+    return tuple(s for i, s in enumerate(shape) if i not in dims)
+
+
+def reduce_sum(x, dim=None, keepdim=False):
+    """sum (Tensor.ts:2427-2431); backward broadcasts g over the reduced dims
+    after restoring them (torch.js expands without unsqueezing, D13)."""
+    if x.dtype != "float32":
+        x = x.float()
+    dims = _norm_dims(x, dim)
+    r = _k_reduce("sum", x, dims) if dims else x.contiguous()
+    kshape = tuple(1 if i in dims else s for i, s in enumerate(x.shape))
+    out = r if keepdim else _view_raw(r, _squeeze_shape(x.shape, dims))
+    if not keepdim and dim is None:
+        out = _view_raw(r, ())
+    xs = x.shape
+
+    def bwd(g):
+        return [_view_raw(g.contiguous(), kshape).expand(xs)]
+    return _record(out, "Sum", [x], bwd)
+
+
+def reduce_mean(x, dim=None, keepdim=False):
+    """mean (Tensor.ts:2432-2446)."""
+    if x.dtype != "float32":
+        x = x.float()
+    dims = _norm_dims(x, dim)
+    cnt = 1
+    for d in dims:
+        cnt *= x.shape[d]
+    r = _k_reduce("mean", x, dims) if dims else x.contiguous()
+    kshape = tuple(1 if i in dims else s for i, s in enumerate(x.shape))
+    out = r if keepdim else _view_raw(r, _squeeze_shape(x.shape, dims))
+    xs = x.shape
+
+    def bwd(g):
+        gs = _k_scalar("mul", g, 1.0 / cnt) if cnt else g
+        return [_view_raw(gs.contiguous(), kshape).expand(xs)]
+    return _record(out, "Mean", [x], bwd)
+
+
+def reduce_minmax(x, dim, keepdim, which):
+    """amax / amin; ties share the gradient evenly."""
+    if x.dtype != "float32":
+        x = x.float()
+    dims = _norm_dims(x, dim)
+    r = _k_reduce(which, x, dims)
+    kshape = r.shape
+    out = r if keepdim else _view_raw(r, _squeeze_shape(x.shape, dims))
+    xs = x.shape
+
+    def bwd(g):
+        mask = compare_raw(x, r, "eq")
+        cnt = _k_reduce("sum", mask, dims)
+        w = _k_binary("div", mask, cnt)
+        return [_k_binary("mul", w, _view_raw(g.contiguous(), kshape))]
+    return _record(out, which.capitalize(), [x], bwd)
+
+
+def argmax(x, dim=None, keepdim=False, is_min=False):
+    """argmax / argmin (Tensor.ts:2504-2577): first index of the extreme."""
+    if x.dtype != "float32":
+        x = x.float()
+    x = x.contiguous()
+    if dim is None:
+        outer, r, inner = 1, x.numel(), 1
+        oshape = ()
+    else:
+        d = _wrap_dim(dim, x.ndim)
+        outer, r, inner = _numel(x.shape[:d]), x.shape[d], _numel(x.shape[d + 1:])
+        oshape = x.shape[:d] + ((1,) if keepdim else ()) + x.shape[d + 1:]
+    out = empty(oshape, "int32")
+    L.check(L.lib().tjh_argmax(x.data_ptr(), outer, r, inner, 1 if is_min else 0,
+                               out.data_ptr()), "argmax")
+    return out
+
+
+# ------------------------------------------------------------ views
+
+
+def _view_strides(shape, strides, new_shape):
+    """Strides for viewing (shape, strides) as new_shape without a copy, or
+    None when impossible.  Walks the old dims from the innermost, splitting
+    them into chunks that are contiguous among themselves; every chunk must
+    be covered by whole new dims."""
+    new_shape = tuple(new_shape)
+    if _numel(shape) == 0 or len(shape) == 0:
+        return _contig_strides(new_shape)
+    new_strides = [0] * len(new_shape)
+    view_d = len(new_shape) - 1
+    chunk_base = strides[-1]
+    tensor_numel = 1
+    view_numel = 1
+    for td in range(len(shape) - 1, -1, -1):
+        tensor_numel *= shape[td]
+        if td == 0 or (shape[td - 1] != 1 and strides[td - 1] != tensor_numel * chunk_base):
+            while view_d >= 0 and (view_numel < tensor_numel or new_shape[view_d] == 1):
+                new_strides[view_d] = view_numel * chunk_base
+                view_numel *= new_shape[view_d]
+                view_d -= 1
+            if view_numel != tensor_numel:
+                return None
+            if td > 0:
+                chunk_base = strides[td - 1]
+                tensor_numel = 1
+                view_numel = 1
+    if view_d != -1:
+        return None
+    return tuple(new_strides)
+
+
+def _infer_shape(shape, n):
+    """inferShape (src/utils/shape.ts:64-90): one -1 allowed."""
+    shape = list(int(s) for s in shape)
+    if shape.count(-1) > 1:
+        raise RuntimeError("only one dimension can be inferred")
+    if -1 in shape:
+        known = 1
+        for s in shape:
+            if s != -1:
+                known *= s
+        if known == 0 or n % known:
+            raise RuntimeError("shape %s is invalid for input of size %d" % (shape, n))
+        shape[shape.index(-1)] = n // known
+    if _numel(shape) != n:
+        raise RuntimeError("shape %s is invalid for input of size %d" % (shape, n))
+    return tuple(shape)
+
+
+def _alias(x, shape, strides, offset):
+    return Tensor(x._storage, shape, strides, offset, x._dtype)
+
+
+def view(x, shape):
+    shape = _infer_shape(shape, x.numel())
+    st = _view_strides(x.shape, x._strides, shape)
+    if st is None:
+        raise RuntimeError("view size is not compatible with input tensor's size and stride; use reshape")
+    out = _alias(x, shape, st, x._offset)
+    xs = x.shape
+    return _record(out, "View", [x], lambda g: [reshape_raw(g, xs)])
+
+
+def reshape_raw(g, shape):
+    st = _view_strides(g.shape, g._strides, tuple(shape))
+    if st is None:
+        g = g.contiguous()
+        st = _contig_strides(tuple(shape))
+    return Tensor(g._storage, tuple(shape), st, g._offset, g._dtype)
+
+
+def reshape(x, shape):
+    """reshape (Tensor.ts:1603-1628): a view when strides allow, else a copy."""
+    shape = _infer_shape(shape, x.numel())
+    st = _view_strides(x.shape, x._strides, shape)
+    if st is None:
+        return view(contiguous(x), shape)
+    return view(x, shape)
+
+
+def flatten(x, start_dim=0, end_dim=-1):
+    if x.ndim == 0:
+        return reshape(x, (1,))
+    s = _wrap_dim(start_dim, x.ndim)
+    e = _wrap_dim(end_dim, x.ndim)
+    shape = x.shape[:s] + (_numel(x.shape[s:e + 1]),) + x.shape[e + 1:]
+    return reshape(x, shape)
+
+
+def squeeze(x, dim=None):
+    if dim is None:
+        shape = tuple(s for s in x.shape if s != 1)
+    else:
+        d = _wrap_dim(dim, x.ndim)
+        shape = x.shape[:d] + x.shape[d + 1:] if x.shape[d] == 1 else x.shape
+    return reshape(x, shape)
+
+
+def unsqueeze(x, dim):
+    d = _wrap_dim(dim, x.ndim + 1)
+    shape = x.shape[:d] + (1,) + x.shape[d:]
+    st = list(x._strides)
+    st.insert(d, (x._strides[d] * x.shape[d]) if d < x.ndim else 1)
+    out = _alias(x, shape, tuple(st), x._offset)
+    xs = x.shape
+    return _record(out, "Unsqueeze", [x], lambda g: [reshape_raw(g, xs)])
+
+
+def permute(x, dims):
+    dims = tuple(_wrap_dim(d, x.ndim) for d in dims)
+    if sorted(dims) != list(range(x.ndim)):
+        raise RuntimeError("permute: dims %s are not a permutation" % (dims,))
+    shape = tuple(x.shape[d] for d in dims)
+    st = tuple(x._strides[d] for d in dims)
+    out = _alias(x, shape, st, x._offset)
+    inv = [0] * len(dims)
+    for i, d in enumerate(dims):
+        inv[d] = i
+
+    def bwd(g):
+        return [_alias(g, tuple(g.shape[i] for i in inv), tuple(g._strides[i] for i in inv),
+                       g._offset)]
+    return _record(out, "Permute", [x], bwd)
+
+
+def transpose(x, d0, d1):
+    d0 = _wrap_dim(d0, x.ndim)
+    d1 = _wrap_dim(d1, x.ndim)
+    dims = list(range(x.ndim))
+    dims[d0], dims[d1] = dims[d1], dims[d0]
+    return permute(x, dims)
+
+
+def expand(x, shape):
+    """expand / broadcast_to (Tensor.ts:1537-1601) as a 0-stride view;
+    backward sums over the expanded dims (torch.js has none, D12)."""
+    shape = tuple(int(s) for s in shape)
+    nd = len(shape)
+    off = nd - x.ndim
+    if off < 0:
+        raise RuntimeError("expand: target has fewer dims than the tensor")
+    new_shape = []
+    st = []
+    for d in range(nd):
+        want = shape[d]
+        if d < off:
+            if want == -1:
+                raise RuntimeError("expand: -1 not allowed for new leading dims")
+            new_shape.append(want)
+            st.append(0)
+        else:
+            have = x.shape[d - off]
+            if want == -1:
+                want = have
+            if have == want:
+                new_shape.append(want)
+                st.append(x._strides[d - off])
+            elif have == 1:
+                new_shape.append(want)
+                st.append(0)
+            else:
+                raise RuntimeError("expand: size %d cannot expand to %d" % (have, want))
+    out = _alias(x, tuple(new_shape), tuple(st), x._offset)
+    xs = x.shape
+    return _record(out, "Expand", [x], lambda g: [_sum_to(g, xs)])
+
+
+def contiguous(x):
+    if x.is_contiguous():
+        return x
+    out = _k_contiguous(x)
+    return _record(out, "Contiguous", [x], lambda g: [g])
+
+
+def clone(x):
+    out = _k_contiguous(x)
+    return _record(out, "Clone", [x], lambda g: [g])
+
+
+def narrow(x, dim, start, length):
+    d = _wrap_dim(dim, x.ndim)
+    n = x.shape[d]
+    if start < 0:
+        start += n
+    if start < 0 or length < 0 or start + length > n:
+        raise IndexError("narrow: range [%d, %d) out of bounds for size %d" % (start, start + length, n))
+    shape = x.shape[:d] + (length,) + x.shape[d + 1:]
+    out = _alias(x, shape, x._strides, x._offset + start * x._strides[d])
+    xs = x.shape
+
+    def bwd(g):
+        z = zeros(xs)
+        dst = _alias(z, g.shape, z._strides, start * z._strides[d])
+        _copy_into(dst, g)
+        return [z]
+    return _record(out, "Narrow", [x], bwd)
+
+
+def select(x, dim, index):
+    d = _wrap_dim(dim, x.ndim)
+    if index < 0:
+        index += x.shape[d]
+    return squeeze(narrow(x, d, index, 1), d)
+
+
+def split(x, split_size, dim=0):
+    d = _wrap_dim(dim, x.ndim)
+    n = x.shape[d]
+    if isinstance(split_size, (list, tuple)):
+        sizes = list(split_size)
+        if sum(sizes) != n:
+            raise RuntimeError("split sizes %s do not sum to %d" % (sizes, n))
+    else:
+        sizes = [min(split_size, n - i) for i in range(0, n, split_size)]
+    outs = []
+    pos = 0
+    for s in sizes:
+        outs.append(narrow(x, d, pos, s))
+        pos += s
+    return outs
+
+
+def chunk(x, chunks, dim=0):
+    d = _wrap_dim(dim, x.ndim)
+    n = x.shape[d]
+    size = -(-n // chunks)
+    return split(x, size, d)
+
+
+def _getitem(x, idx):
+    if not isinstance(idx, tuple):
+        idx = (idx,)
+    out = x
+    d = 0
+    for it in idx:
+        if it is Ellipsis:
+            d = out.ndim - (len(idx) - 1 - idx.index(Ellipsis)) + 0
+            continue
+        if it is None:
+            out = unsqueeze(out, d)
+            d += 1
+            continue
+        if isinstance(it, numbers.Integral):
+            out = select(out, d, int(it))
+            continue
+        if isinstance(it, slice):
+            start, stop, step = it.indices(out.shape[d])
+            if step != 1:
+                raise NotImplementedError("strided slicing")
+            out = narrow(out, d, start, max(0, stop - start))
+            d += 1
+            continue
+        if isinstance(it, Tensor):
+            out = index_select(out, d, it.reshape(-1))
+            d += 1
+            continue
+        raise TypeError("unsupported index %r" % (it,))
+    return out
+
+
+def cat(tensors, dim=0):
+    """cat (Tensor.ts:152-235): one strided copy per input."""
+    tensors = list(tensors)
+    if not tensors:
+        raise RuntimeError("cat of an empty list")
+    d = _wrap_dim(dim, tensors[0].ndim)
+    dt = tensors[0].dtype
+    shape = list(tensors[0].shape)
+    shape[d] = sum(t.shape[d] for t in tensors)
+    out = empty(shape, dt)
+    pos = 0
+    sizes = []
+    for t in tensors:
+        dst = _alias(out, t.shape, out._strides, pos * out._strides[d])
+        _copy_into(dst, t)
+        sizes.append(t.shape[d])
+        pos += t.shape[d]
+
+    def bwd(g):
+        res = []
+        p = 0
+        for s in sizes:
+            res.append(_alias(g, g.shape[:d] + (s,) + g.shape[d + 1:], g._strides,
+                              g._offset + p * g._strides[d]))
+            p += s
+        return res
+    return _record(out, "Cat", tensors, bwd)
+
+
+def stack(tensors, dim=0):
+    tensors = list(tensors)
+    d = _wrap_dim(dim, tensors[0].ndim + 1)
+    return cat([unsqueeze(t, d) for t in tensors], d)
+
+
+def masked_fill(x, mask, value):
+    """masked_fill (Tensor.ts:804-832) with a broadcastable mask; backward
+    zeroes the masked positions (torch.js has none, D12)."""
+    if x.dtype != "float32":
+        x = x.float()
+    m = mask
+    if m.dtype != "uint8" and m.dtype != "bool":
+        m = _to_mask(m)
+    shape = x.shape
+    mst = _bstrides(m, shape)
+    out = empty(shape)
+    if out.numel():
+        L.check(L.lib().tjh_masked_fill(len(shape), L.i64arr(shape), x.data_ptr(),
+                                        L.i64arr(x._strides), m.data_ptr(), L.i64arr(mst),
+                                        float(value), out.data_ptr()), "masked_fill")
+
+    def bwd(g):
+        g = g.contiguous()
+        o = empty(shape)
+        L.check(L.lib().tjh_masked_fill(len(shape), L.i64arr(shape), g.data_ptr(),
+                                        L.i64arr(g._strides), m.data_ptr(), L.i64arr(mst), 0.0,
+                                        o.data_ptr()), "masked_fill_backward")
+        return [o]
+    return _record(out, "MaskedFill", [x], bwd)
+
+
+def _to_mask(t):
+    a = (t.numpy() != 0).astype(np.uint8)
+    return from_numpy(a, dtype="uint8")
+
+
+# ------------------------------------------------------------ indexing
+
+
+def _idx32(index):
+    if not isinstance(index, Tensor):
+        index = tensor(np.asarray(index, dtype=np.int32), dtype="int32")
+    if index.dtype != "int32":
+        index = index.to("int32")
+    return index.contiguous()
+
+
+def index_select(x, dim, index):
+    """index_select (Tensor.ts:1242-1287) for any rank; backward is an
+    ordered index_add (torch.js has none)."""
+    d = _wrap_dim(dim, x.ndim)
+    index = _idx32(index)
+    if index.ndim != 1:
+        raise RuntimeError("index_select: index must be 1-D")
+    xc = x.contiguous() if x.dtype == "float32" else x.float().contiguous()
+    outer, src, inner = _numel(xc.shape[:d]), xc.shape[d], _numel(xc.shape[d + 1:])
+    n = index.numel()
+    host = index.numpy()
+    if n and (host.max() >= src or host.min() < -src):
+        raise IndexError("index_select: index out of range for dimension of size %d" % src)
+    oshape = xc.shape[:d] + (n,) + xc.shape[d + 1:]
+    out = empty(oshape)
+    L.check(L.lib().tjh_index_select(xc.data_ptr(), outer, src, inner, index.data_ptr(), n,
+                                     out.data_ptr()), "index_select")
+    xs = xc.shape
+
+    def bwd(g):
+        g = g.contiguous()
+        z = zeros(xs)
+        L.check(L.lib().tjh_index_add(z.data_ptr(), outer, src, inner, index.data_ptr(), n,
+                                      g.data_ptr()), "index_add")
+        return [z]
+    return _record(out, "IndexSelect", [x], bwd)
+
+
+def gather(x, dim, index):
+    """gather (Tensor.ts:2651-2705): negative indices wrap; backward is an
+    ordered scatter_add."""
+    d = _wrap_dim(dim, x.ndim)
+    index = _idx32(index)
+    if index.ndim != x.ndim:
+        raise RuntimeError("gather: index must have the same rank as input")
+    for i in range(x.ndim):
+        if i != d and index.shape[i] != x.shape[i]:
+            raise RuntimeError("gather: index shape %s incompatible with input %s"
+                               % (list(index.shape), list(x.shape)))
+    xc = x.contiguous() if x.dtype == "float32" else x.float().contiguous()
+    outer, src, inner = _numel(xc.shape[:d]), xc.shape[d], _numel(xc.shape[d + 1:])
+    ilen = index.shape[d]
+    out = empty(index.shape)
+    L.check(L.lib().tjh_gather(xc.data_ptr(), outer, src, inner, index.data_ptr(), ilen,
+                               out.data_ptr()), "gather")
+    xs = xc.shape
+
+    def bwd(g):
+        g = g.contiguous()
+        z = zeros(xs)
+        L.check(L.lib().tjh_scatter_add(z.data_ptr(), outer, src, inner, index.data_ptr(), ilen,
+                                        g.data_ptr()), "scatter_add")
+        return [z]
+    return _record(out, "Gather", [x], bwd)
+
+
+def nonzero(x):
+    """nonzero (Tensor.ts:1323-1345): [nnz, ndim] int32, row-major order."""
+    xc = x.contiguous() if x.dtype == "float32" else x.float().contiguous()
+    nd = max(1, xc.ndim)
+    shape = xc.shape if xc.ndim else (1,)
+    cnt = ctypes.c_int64(0)
+    L.check(L.lib().tjh_nonzero(xc.data_ptr(), nd, L.i64arr(shape), None, 0, ctypes.byref(cnt)),
+            "nonzero")
+    out = empty((cnt.value, nd), "int32")
+    if cnt.value:
+        L.check(L.lib().tjh_nonzero(xc.data_ptr(), nd, L.i64arr(shape), out.data_ptr(),
+                                    cnt.value, ctypes.byref(cnt)), "nonzero")
+    return out
+
+
+# ------------------------------------------------------------ matmul
+
+
+def _mat_operand(t):
+    """(ptr, ld, trans, batch_stride) of the last two dims of t, or None
+    when they are neither row- nor column-major."""
+    r, c = t.shape[-2], t.shape[-1]
+    s0, s1 = t._strides[-2], t._strides[-1]
+    if (s1 == 1 or c == 1) and s0 >= max(1, c):
+        return t.data_ptr(), max(s0, 1), False
+    if (s0 == 1 or r == 1) and s1 >= max(1, r):
+        return t.data_ptr(), max(s1, 1), True
+    return None
+
+
+def _gemm(a, b, out=None, alpha=1.0, beta=0.0, bias=None, bias_mode=0):
+    """out[M,N] = alpha*a[M,K] @ b[K,N] (+beta*out) (+bias) for 2-D views."""
+    M, K = a.shape
+    K2, N = b.shape
+    assert K == K2
+    oa = _mat_operand(a)
+    if oa is None:
+        a = _k_contiguous(a)
+        oa = _mat_operand(a)
+    ob = _mat_operand(b)
+    if ob is None:
+        b = _k_contiguous(b)
+        ob = _mat_operand(b)
+    if out is None:
+        out = _empty_padded(M, N) if N % 4 else empty((M, N))
+    ldc = out._strides[0] if out._strides[0] >= N else N
+    L.check(L.lib().tjh_gemm(1 if oa[2] else 0, 1 if ob[2] else 0, M, N, K, float(alpha), oa[0],
+                             oa[1], 0, ob[0], ob[1], 0, float(beta), out.data_ptr(), ldc, 0, 1,
+                             bias.data_ptr() if bias is not None else None, bias_mode), "gemm")
+    return out
+
+
+def _bgemm(a, b):
+    """Batched a[B,M,K] @ b[B,N,K...] with uniform batch strides (3-D views)."""
+    Bn, M, K = a.shape
+    _, _, N = b.shape
+    oa = _mat_operand(a)
+    if oa is None:
+        a = _k_contiguous(a)
+        oa = _mat_operand(a)
+    ob = _mat_operand(b)
+    if ob is None:
+        b = _k_contiguous(b)
+        ob = _mat_operand(b)
+    out = empty((Bn, M, N))
+    L.check(L.lib().tjh_gemm(1 if oa[2] else 0, 1 if ob[2] else 0, M, N, K, 1.0, oa[0], oa[1],
+                             a._strides[0] if Bn > 1 else 0, ob[0], ob[1],
+                             b._strides[0] if Bn > 1 else 0, 0.0, out.data_ptr(), N, M * N, Bn,
+                             None, 0), "bgemm")
+    return out
+
+
+def _flatten_batch(t, bshape):
+    """t expanded to bshape + t.shape[-2:], viewed as [B, r, c] with one
+    batch stride; copies when the batch dims cannot share one stride."""
+    full_shape = tuple(bshape) + t.shape[-2:]
+    e = expand(t, full_shape) if t.shape != full_shape else t
+    nb = len(bshape)
+    bst = e._strides[:nb]
+    # one stride for the flattened batch: all-zero, or mergeable dims
+    B = _numel(bshape)
+    if B <= 1:
+        return Tensor(e._storage, (max(B, 1),) + e.shape[-2:], (0,) + e._strides[-2:], e._offset,
+                      e._dtype) if B == 1 else e
+    if all(s == 0 for s in bst):
+        return Tensor(e._storage, (B,) + e.shape[-2:], (0,) + e._strides[-2:], e._offset, e._dtype)
+    ok = all(bst[i] == bst[i + 1] * bshape[i + 1] for i in range(nb - 1))
+    if ok:
+        return Tensor(e._storage, (B,) + e.shape[-2:], (bst[-1],) + e._strides[-2:], e._offset,
+                      e._dtype)
+    c = _k_contiguous(e)
+    return Tensor(c._storage, (B,) + c.shape[-2:], None, c._offset, c._dtype)
+
+
+def matmul(a, b):
+    """matmul with NumPy batch broadcasting (Tensor.ts:2136-2290); backward
+    gives both operands their products (torch.js: the left one only, D1)."""
+    if a.dtype != "float32":
+        a = a.float()
+    if b.dtype != "float32":
+        b = b.float()
+    if a.ndim == 0 or b.ndim == 0:
+        raise RuntimeError("matmul: both arguments need at least 1 dimension")
+    if a.ndim == 1 and b.ndim == 1:
+        return reduce_sum(mul(a, b))
+    if a.ndim == 1:
+        return squeeze(matmul(unsqueeze(a, 0), b), -2)
+    if b.ndim == 1:
+        return squeeze(matmul(a, unsqueeze(b, 1)), -1)
+    if a.shape[-1] != b.shape[-2]:
+        raise RuntimeError("matmul: shapes %s and %s cannot be multiplied"
+                           % (list(a.shape), list(b.shape)))
+    if b.ndim == 2 and a.ndim >= 2:
+        # [..., M, K] @ [K, N]: flatten leading dims into M
+        lead = a.shape[:-1]
+        a2 = reshape(a, (_numel(lead), a.shape[-1])) if a.ndim > 2 else a
+        out2 = _mm(a2, b)
+        return reshape(out2, lead + (b.shape[-1],)) if a.ndim > 2 else out2
+    bshape = _broadcast_shapes(a.shape[:-2], b.shape[:-2])
+    M, K, N = a.shape[-2], a.shape[-1], b.shape[-1]
+    a3 = _flatten_batch(a.detach(), bshape)
+    b3 = _flatten_batch(b.detach(), bshape)
+    out3 = _bgemm(a3, b3)
+    out = _view_raw(out3, tuple(bshape) + (M, N))
+    ash, bsh = a.shape, b.shape
+
+    def bwd(g):
+        g3 = _view_raw(g.contiguous(), (_numel(bshape), M, N))
+        ga = gb = None
+        if a.requires_grad:
+            bt = Tensor(b3._storage, (b3.shape[0], N, K), (b3._strides[0], b3._strides[2],
+                                                           b3._strides[1]), b3._offset)
+            ga = _sum_to(_view_raw(_bgemm(g3, bt), tuple(bshape) + (M, K)), ash)
+        if b.requires_grad:
+            at = Tensor(a3._storage, (a3.shape[0], K, M), (a3._strides[0], a3._strides[2],
+                                                           a3._strides[1]), a3._offset)
+            gb = _sum_to(_view_raw(_bgemm(at, g3), tuple(bshape) + (K, N)), bsh)
+        return [ga, gb]
+    return _record(out, "BMM", [a, b], bwd)
+
+
+def _mm(a, b):
+    out = _gemm(a, b)
+
+    def bwd(g):
+        ga = _gemm(g, b.detach().T) if a.requires_grad else None
+        gb = _gemm(a.detach().T, g) if b.requires_grad else None
+        return [ga, gb]
+    return _record(out, "MM", [a, b], bwd)
+
+
+_add_unary_methods()
+
+
+# ----------------------------------------------------------------- engine
+
+
+def _accumulate(store, key, g):
+    prev = store.get(key)
+    store[key] = g if prev is None else _k_binary("add", prev, g)
+
+
+def _toposort(roots):
+    order = []
+    seen = set()
+    stack = [(n, False) for n in roots if n is not None]
+    while stack:
+        node, done = stack.pop()
+        if done:
+            order.append(node)
+            continue
+        if id(node) in seen:
+            continue
+        seen.add(id(node))
+        stack.append((node, True))
+        for t in node.inputs:
+            if t is not None and t.grad_fn is not None and id(t.grad_fn) not in seen:
+                stack.append((t.grad_fn, False))
+    return order  # post-order: inputs before users
+
+
+def run_backward(pairs, retain_graph=False, inputs=None):
+    """Reverse-topological VJP sweep (Tensor.backward, Tensor.ts:3686-3740;
+    accumulateGrad, Tensor.ts:3670-3677).  With `inputs`, returns their
+    gradients instead of accumulating into leaves (autograd.grad)."""
+    prev = _grad["enabled"]
+    _grad["enabled"] = False
+    try:
+        grads = {}
+        roots = []
+        wanted = {id(t): t for t in inputs} if inputs is not None else None
+        results = {}
+        owned = set()  # storages already handed to a leaf in this pass
+        for t, g in pairs:
+            if g.shape != t.shape:
+                if g.numel() == t.numel():
+                    g = reshape_raw(g, t.shape)
+                else:
+                    g = g.expand(t.shape)
+            if t.grad_fn is None:
+                if wanted is not None:
+                    if id(t) in wanted:
+                        _accumulate(results, id(t), g)
+                elif t.requires_grad:
+                    _leaf_accumulate(t, g, owned, force_copy=True)
+                continue
+            _accumulate(grads, id(t.grad_fn), g)
+            roots.append(t.grad_fn)
+        order = _toposort(roots)
+        for node in reversed(order):
+            g = grads.pop(id(node), None)
+            if g is None:
+                continue
+            if node.fn is None:
+                raise RuntimeError("Trying to backward through the graph a second time; "
+                                   "pass retain_graph=True the first time")
+            in_grads = node.fn(g)
+            del g
+            for t, gi in zip(node.inputs, in_grads):
+                if t is None or gi is None:
+                    continue
+                if tuple(gi.shape) != t.shape:
+                    gi = _sum_to(gi, t.shape) if gi.ndim >= t.ndim else reshape_raw(gi, t.shape)
+                if wanted is not None and id(t) in wanted:
+                    _accumulate(results, id(t), gi)
+                if t.grad_fn is not None:
+                    _accumulate(grads, id(t.grad_fn), gi)
+                    if t._retains_grad and wanted is None:
+                        _leaf_accumulate(t, gi, owned)
+                elif wanted is None and t.requires_grad:
+                    _leaf_accumulate(t, gi, owned)
+            if not retain_graph:
+                # drop the saved tensors and input references: the graph
+                # cannot be replayed (torch.js nulls grad_fn, Tensor.ts:3735-3739)
+                node.fn = None
+                node.inputs = [None] * len(node.inputs)
+        if wanted is not None:
+            return [results.get(id(t)) for t in inputs]
+        return None
+    finally:
+        _grad["enabled"] = prev
+
+
+def _leaf_accumulate(t, g, owned, force_copy=False):
+    """Accumulates into t.grad.  A gradient tensor handed to a leaf is never
+    shared with another leaf (the same incoming grad can flow to several
+    inputs of an add), so later in-place edits of one .grad stay local."""
+    if force_copy or not g.is_contiguous() or id(g._storage) in owned:
+        g = _k_contiguous(g)
+    if t._grad is None:
+        owned.add(id(g._storage))
+        t._grad = Tensor(g._storage, g._shape, g._strides, g._offset, g._dtype)
+    else:
+        t._grad = _k_binary("add", t._grad, g)
