@@ -112,7 +112,7 @@ def run_gpu(steps, warmup):
 
 
 def cpu_baseline():
-    """The oracle (numpy) on a bounded sample: GPT-2 small at B=1, T=128,
+    """The oracle (numpy) on a bounded sample: GPT-2 small at B=1, T=1024,
     full 12 layers and vocabulary, fwd + bwd + AdamW."""
     from oracle import models as om
     try:
@@ -123,15 +123,15 @@ def cpu_baseline():
     cfg = om.Config()
     r = np.random.default_rng(0)
     p = om.init_params(cfg, r)
-    tb, tt = 1, 128
+    tb, tt = 1, 1024
     ids = r.integers(0, V, (tb, tt + 1))
     t0 = time.perf_counter()
     _, g = om.gpt2_loss_and_grads(cfg, p, ids[:, :-1], ids[:, 1:])
     om.adamw_step(p, g, lr=6e-4, wd=0.1, step=1)
     dt = time.perf_counter() - t0
     return {"value": tb * tt / dt, "unit": "tokens/s", "cores": int(threads), "kind": "port",
-            "sample": "oracle (numpy float64) GPT-2 124M fwd+bwd+AdamW at B=1, T=128 (128 tokens, "
-                      "full 12 layers and 50257 vocab), %.1f s" % dt}
+            "sample": "oracle (numpy float64) GPT-2 124M fwd+bwd+AdamW at B=1, T=1024 (1024 "
+                      "tokens, full 12 layers and 50257 vocab), %.1f s" % dt}
 
 
 def main():

@@ -427,6 +427,30 @@ def test_sdpa_on_qkv_views(torch):
     check(gqkv, np.concatenate([un(gq), un(gk), un(gv)], -1), rtol=1e-4, atol=1e-4)
 
 
+@pytest.mark.parametrize("T,causal", [(77, True), (77, False), (1024, True), (33, True)])
+def test_sdpa_flash_gpt2_layout(torch, T, causal):
+    """Head dim 64 (the flash kernels) on [B,T,3C] projection views, with
+    sequence lengths that are not multiples of the 32-row tiles."""
+    r = np.random.default_rng(T)
+    B, H, hd = (1, 2, 64) if T >= 1024 else (2, 3, 64)
+    C = H * hd
+    qkv = f32(r.standard_normal((B, T, 3 * C)))
+
+    def fn(t):
+        q, k, v = t.split(C, dim=2)
+        sh = lambda z: z.view(B, T, H, hd).transpose(1, 2)
+        y = torch.F.scaled_dot_product_attention(sh(q), sh(k), sh(v), is_causal=causal)
+        return y.transpose(1, 2).contiguous().view(B, T, C)
+    out, g, (gqkv,) = grad_of(torch, fn, qkv)
+    qa, ka, va = np.split(qkv.astype(np.float64), 3, axis=-1)
+    sh = lambda z: z.reshape(B, T, H, hd).transpose(0, 2, 1, 3)
+    o, _ = ops.sdpa(sh(qa), sh(ka), sh(va), causal)
+    check(out, o.transpose(0, 2, 1, 3).reshape(B, T, C), rtol=1e-4, atol=1e-5)
+    gq, gk, gv = ops.sdpa_backward(sh(g.astype(np.float64)), sh(qa), sh(ka), sh(va), causal)
+    un = lambda z: z.transpose(0, 2, 1, 3).reshape(B, T, C)
+    check(gqkv, np.concatenate([un(gq), un(gk), un(gv)], -1), rtol=1e-4, atol=1e-4)
+
+
 def test_sdpa_attn_mask_raises(torch):
     q = torch.zeros(1, 1, 2, 4)
     with pytest.raises(NotImplementedError, match="attn_mask not yet implemented"):

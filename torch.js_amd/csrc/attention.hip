@@ -6,7 +6,9 @@
 // implemented is torch's: optional causal mask (key j > query i masked,
 // top-left aligned), lse saved for the backward.
 //
-// This version is GEMM-composed per batch item: S = scale * Q K^T on the
+// Head dim 64 with D-contiguous, 16-byte aligned rows runs the flash
+// kernels of flash.hip.  Any other shape takes the GEMM-composed path
+// below, per batch item: S = scale * Q K^T on the
 // MFMA GEMM (all heads of one batch item in one batched launch), a fused
 // masked softmax that also writes lse, then O = P V.  The backward
 // recomputes P from lse and issues dV = P^T dO, dP = dO V^T,
@@ -118,10 +120,16 @@ int tjh_sdpa_forward(const float* q, const float* k, const float* v, float* o, f
   TJH_ARG(qs && ks && vs && os, "tjh_sdpa_forward: NULL strides");
   if (B == 0 || H == 0 || Tq == 0) return TJH_OK;
   TJH_ARG(Tk > 0, "tjh_sdpa_forward: empty key sequence");
+  {
+    const void* ptrs[4] = {q, k, v, o};
+    const int64_t* sts[4] = {qs, ks, vs, os};
+    if (flash_supported(D, ptrs, sts, 4))
+      return flash_forward(q, k, v, o, lse, B, H, Tq, Tk, qs, ks, vs, os, scale, causal);
+  }
   Scratch S((size_t)(H * Tq * Tk) * sizeof(float));
   if (!S.ok()) return set_error(TJH_ERR_OOM, "sdpa_forward: no scratch for scores");
   float* s = S.as<float>();
-  KernelScope kscope("sdpa_fwd");
+  KernelScope kscope("sdpa_fwd_composite");
   for (int64_t b = 0; b < B; ++b) {
     int rc = gemm("sdpa.gemm", 0, 1, Tq, Tk, D, scale, q + b * qs[0], qs[2], qs[1], k + b * ks[0], ks[2],
                       ks[1], 0.f, s, Tk, Tq * Tk, H, nullptr, 0);
@@ -149,6 +157,12 @@ int tjh_sdpa_backward(const float* q, const float* k, const float* v, const floa
                 *gs = strides[4], *dqs = strides[5], *dks = strides[6], *dvs = strides[7];
   if (B == 0 || H == 0) return TJH_OK;
   if (Tq == 0 || Tk == 0) return TJH_OK;
+  {
+    const void* ptrs[8] = {q, k, v, o, do_, dq, dk, dv};
+    if (flash_supported(D, ptrs, strides, 8))
+      return flash_backward(q, k, v, o, do_, lse, dq, dk, dv, B, H, Tq, Tk, strides, scale,
+                            causal);
+  }
   Scratch Ps((size_t)(H * Tq * Tk) * sizeof(float));
   Scratch dPs((size_t)(H * Tq * Tk) * sizeof(float));
   Scratch Ds((size_t)(H * Tq) * sizeof(float));
@@ -156,7 +170,7 @@ int tjh_sdpa_backward(const float* q, const float* k, const float* v, const floa
   float* P = Ps.as<float>();
   float* dP = dPs.as<float>();
   float* Dr = Ds.as<float>();
-  KernelScope kscope("sdpa_bwd");
+  KernelScope kscope("sdpa_bwd_composite");
   unsigned grows = (unsigned)cdiv(H * Tq, 4);
   for (int64_t b = 0; b < B; ++b) {
     const float* qb = q + b * qs[0];

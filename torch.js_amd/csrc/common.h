@@ -59,6 +59,17 @@ int gemm(const char* family, int transA, int transB, int64_t M, int64_t N, int64
          int64_t strideB, float beta, float* C, int64_t ldc, int64_t strideC, int64_t batch,
          const float* bias, int bias_mode);
 
+// Flash attention for head dim 64 (flash.hip).  `flash_supported` checks
+// the head dim and that every tensor has 16-byte aligned, D-contiguous rows.
+bool flash_supported(int64_t D, const void* const* ptrs, const int64_t* const* strides, int n);
+int flash_forward(const float* q, const float* k, const float* v, float* o, float* lse, int64_t B,
+                  int64_t H, int64_t Tq, int64_t Tk, const int64_t* qs, const int64_t* ks,
+                  const int64_t* vs, const int64_t* os, float scale, int causal);
+int flash_backward(const float* q, const float* k, const float* v, const float* o,
+                   const float* dout, const float* lse, float* dq, float* dk, float* dv,
+                   int64_t B, int64_t H, int64_t Tq, int64_t Tk, const int64_t* const* strides,
+                   float scale, int causal);
+
 // Grid size helper: ceil(n / d).
 __host__ __device__ inline int64_t cdiv(int64_t n, int64_t d) { return (n + d - 1) / d; }
 

@@ -529,15 +529,27 @@ __global__ __launch_bounds__(kBlock) void k_ln_bwd_block(const float* __restrict
   }
 }
 
-// Column sum of partials [nb, cols] -> out[cols] (+= when accumulate).
-__global__ __launch_bounds__(kBlock) void k_colsum(const float* __restrict__ p, int64_t nb,
-                                                   int64_t cols, float* __restrict__ out,
-                                                   int accumulate) {
-  int64_t c = (int64_t)blockIdx.x * kBlock + threadIdx.x;
-  if (c >= cols) return;
-  float s = 0.f;
-  for (int64_t b = 0; b < nb; ++b) s += p[b * cols + c];
-  out[c] = accumulate ? out[c] + s : s;
+// dgamma / dbeta from per-block partials [nb, cols]: the split column
+// reduction of tjh_reduce (deterministic), added into the outputs when
+// accumulating.
+int sum_partials(const float* pg, const float* pb, int64_t nb, int64_t cols, float* dgamma,
+                 float* dbeta, int accumulate) {
+  const float* parts[2] = {pg, pb};
+  float* outs[2] = {dgamma, dbeta};
+  for (int i = 0; i < 2; ++i) {
+    if (!outs[i]) continue;
+    if (!accumulate) {
+      int rc = tjh_reduce(TJH_REDUCE_SUM, parts[i], 1, nb, cols, outs[i]);
+      if (rc != TJH_OK) return rc;
+    } else {
+      Scratch tmp((size_t)cols * sizeof(float));
+      if (!tmp.ok()) return set_error(TJH_ERR_OOM, "layer_norm_backward: no scratch");
+      int rc = tjh_reduce(TJH_REDUCE_SUM, parts[i], 1, nb, cols, tmp.as<float>());
+      if (rc == TJH_OK) rc = tjh_axpy(1.0f, tmp.as<float>(), outs[i], outs[i], cols);
+      if (rc != TJH_OK) return rc;
+    }
+  }
+  return TJH_OK;
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
@@ -720,10 +732,10 @@ int tjh_layer_norm_backward(const float* dy, const float* x, const float* gamma,
              (!gamma || aligned16(gamma));
   int v4 = cols <= 64 * 4 * 3 ? 3 : (cols <= 64 * 4 * 6 ? 6 : (cols <= 64 * 4 * 12 ? 12 : 0));
   if (vec && v4) {
-    // rows per block: aim for ~4 blocks per CU
+    // rows per block: ~2 blocks per CU, >= 16 rows each (fewer partials)
     int cus = num_cus() > 0 ? num_cus() : 256;
-    int64_t rpb = cdiv(rows, 4LL * cus);
-    if (rpb < 4) rpb = 4;
+    int64_t rpb = cdiv(rows, 2LL * cus);
+    if (rpb < 16) rpb = 16;
     int64_t nb = cdiv(rows, rpb);
     Scratch part(want_p ? (size_t)(2 * nb * cols) * sizeof(float) : 0);
     if (want_p && !part.ok()) return set_error(TJH_ERR_OOM, "layer_norm_backward: no scratch");
@@ -743,17 +755,7 @@ int tjh_layer_norm_backward(const float* dy, const float* x, const float* gamma,
       int rc = check_launch("layer_norm_backward");
       if (rc != TJH_OK) return rc;
     }
-    if (want_p) {
-      KernelScope ks("layer_norm_bwd_colsum");
-      unsigned g = (unsigned)cdiv(cols, kBlock);
-      if (dgamma)
-        hipLaunchKernelGGL(k_colsum, dim3(g), dim3(kBlock), 0, stream(), pg, nb, cols, dgamma,
-                           accumulate);
-      if (dbeta)
-        hipLaunchKernelGGL(k_colsum, dim3(g), dim3(kBlock), 0, stream(), pb, nb, cols, dbeta,
-                           accumulate);
-      return check_launch("layer_norm_backward_colsum");
-    }
+    if (want_p) return sum_partials(pg, pb, nb, cols, dgamma, dbeta, accumulate);
     return TJH_OK;
   }
   // general path: partials per row, then column sums
@@ -768,17 +770,7 @@ int tjh_layer_norm_backward(const float* dy, const float* x, const float* gamma,
     int rc = check_launch("layer_norm_backward");
     if (rc != TJH_OK) return rc;
   }
-  if (want_p) {
-    KernelScope ks("layer_norm_bwd_colsum");
-    unsigned g = (unsigned)cdiv(cols, kBlock);
-    if (dgamma)
-      hipLaunchKernelGGL(k_colsum, dim3(g), dim3(kBlock), 0, stream(), pg, rows, cols, dgamma,
-                         accumulate);
-    if (dbeta)
-      hipLaunchKernelGGL(k_colsum, dim3(g), dim3(kBlock), 0, stream(), pb, rows, cols, dbeta,
-                         accumulate);
-    return check_launch("layer_norm_backward_colsum");
-  }
+  if (want_p) return sum_partials(pg, pb, rows, cols, dgamma, dbeta, accumulate);
   return TJH_OK;
 }
 
