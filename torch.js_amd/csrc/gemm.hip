@@ -7,12 +7,17 @@
 //
 // C[b] = alpha * op(A[b]) op(B[b]) + beta * C[b] (+ bias), row-major.
 //
-// Tiling (one workgroup = 256 lanes = 4 wave64):
-//   block tile 128 x 128, K step 16, waves arranged 2 x 2, each wave owns a
-//   64 x 64 sub-tile = 2 x 2 MFMA 32x32 blocks (64 accumulator registers).
-//   A and B tiles are staged in LDS k-major (As[k][m], Bs[k][n]) with a
-//   4-float pad, double-buffered: the next K tile is fetched from HBM into
+// Tiling (one workgroup = 256 lanes = 4 wave64 arranged 2 x 2):
+//   block tile BM x BN in {256x128, 128x128, 128x64, 64x64}, K step 16;
+//   each wave owns a (BM/2) x (BN/2) sub-tile of 32x32 MFMA blocks.  A and
+//   B tiles are staged in LDS k-major (As[k][m], Bs[k][n]) with a 4-float
+//   pad, double-buffered: the next K tile is fetched from HBM into
 //   registers while the MFMAs consume the current LDS tile.
+// The tile is chosen per call from M, N and the CU count so that the
+// number of workgroups divides evenly over the 256 CUs (an 8192 x 768
+// product has 384 tiles of 128x128 — 1.5 per CU — but 768 of 128x64).
+// Small M x N with long K (weight gradients: K = tokens) is split over K;
+// partials are summed by a second pass in a fixed order (deterministic).
 // MFMA operand layout (32x32x2 f32): lane l feeds A[m = l%32][k = l/32] and
 //   B[k = l/32][n = l%32]; accumulator register r of lane l holds
 //   C[8*(r/4) + 4*(l/32) + r%4][l%32].
@@ -23,14 +28,15 @@
 
 #include "common.h"
 
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
 namespace tjh {
 namespace {
 
-constexpr int BM = 128, BN = 128, BK = 16;
+constexpr int BK = 16;
 constexpr int kThreads = 256;
-constexpr int PAD = 4;
-constexpr int LDA_S = BM + PAD;  // LDS row length of As[k][*]
-constexpr int LDB_S = BN + PAD;
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
@@ -50,72 +56,81 @@ struct GemmArgs {
   float* ws;       // split-K partials [batch][split][M][N] (nullptr: none)
 };
 
-// Loads the A tile (BM x BK, rows m0.., cols k0..) for lane t into regs.
-// Non-transposed A ([M][K], k contiguous): 2 float4 along k per lane.
-// Transposed A ([K][M], m contiguous): 2 float4 along m per lane.
-template <bool TRANS>
-__device__ __forceinline__ void load_tile(const float* __restrict__ P, int64_t ld,
-                                          int64_t rows, int64_t cols, int64_t r0,
-                                          int64_t c0, bool vec, float4 (&reg)[2]) {
-  // Logical tile: R = 128 "outer" indices (m or n), BK k indices.
-  // For !TRANS the storage is [outer][k]: element (o, k) at P[o*ld + k].
-  // For TRANS the storage is [k][outer]: element (o, k) at P[k*ld + o].
+// Loads a logical OUTER x BK tile (outer = m for A, n for B) for this lane:
+// V float4 per lane.  !TRANS: storage [outer][k] (k contiguous, 4 float4
+// per outer row); TRANS: storage [k][outer] (outer contiguous).
+// EDGE == false: the caller guarantees the tile is in bounds and 16-byte
+// aligned, so every load is an unconditional 128-bit load.  EDGE == true:
+// every element is guarded (tiles on the problem's edge, unaligned data).
+template <bool TRANS, int OUTER, int V, bool EDGE>
+__device__ __forceinline__ void load_tile(const float* __restrict__ P, int64_t ld, int64_t rows,
+                                          int64_t cols, int64_t r0, int64_t c0,
+                                          float4 (&reg)[V]) {
   const int t = threadIdx.x;
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
+  for (int i = 0; i < V; ++i) {
     int f = t + kThreads * i;
-    if (!TRANS) {
-      int o = f >> 2, kq = f & 3;
-      int64_t go = r0 + o, gk = c0 + kq * 4;
-      if (vec && go < rows && gk + 3 < cols) {
-        reg[i] = *reinterpret_cast<const float4*>(P + go * ld + gk);
+    if (!EDGE) {
+      if (!TRANS) {
+        int o = f >> 2, kq = f & 3;
+        reg[i] = *reinterpret_cast<const float4*>(P + (r0 + o) * ld + c0 + kq * 4);
       } else {
-        float v[4];
+        constexpr int Q = OUTER / 4;
+        int k = f / Q, oq = f % Q;
+        reg[i] = *reinterpret_cast<const float4*>(P + (c0 + k) * ld + r0 + oq * 4);
+      }
+    } else {
+      float v[4];
+      if (!TRANS) {
+        int o = f >> 2, kq = f & 3;
+        int64_t go = r0 + o, gk = c0 + kq * 4;
 #pragma unroll
         for (int j = 0; j < 4; ++j)
           v[j] = (go < rows && gk + j < cols) ? P[go * ld + gk + j] : 0.f;
-        reg[i] = make_float4(v[0], v[1], v[2], v[3]);
-      }
-    } else {
-      int k = f >> 5, oq = f & 31;
-      int64_t gk = c0 + k, go = r0 + oq * 4;
-      if (vec && gk < cols && go + 3 < rows) {
-        reg[i] = *reinterpret_cast<const float4*>(P + gk * ld + go);
       } else {
-        float v[4];
+        constexpr int Q = OUTER / 4;
+        int k = f / Q, oq = f % Q;
+        int64_t gk = c0 + k, go = r0 + oq * 4;
 #pragma unroll
         for (int j = 0; j < 4; ++j)
           v[j] = (gk < cols && go + j < rows) ? P[gk * ld + go + j] : 0.f;
-        reg[i] = make_float4(v[0], v[1], v[2], v[3]);
       }
+      reg[i] = make_float4(v[0], v[1], v[2], v[3]);
     }
   }
 }
 
-// Stores a loaded tile into LDS laid out S[k][outer] (row length LDS_W).
-template <bool TRANS, int LDS_W>
-__device__ __forceinline__ void store_tile(float* __restrict__ S, const float4 (&reg)[2]) {
+// Stores a loaded tile into LDS laid out S[k][outer] (row length W).
+template <bool TRANS, int OUTER, int V, int W>
+__device__ __forceinline__ void store_tile(float* __restrict__ S, const float4 (&reg)[V]) {
   const int t = threadIdx.x;
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
+  for (int i = 0; i < V; ++i) {
     int f = t + kThreads * i;
     if (!TRANS) {
       int o = f >> 2, kq = f & 3;
-      S[(kq * 4 + 0) * LDS_W + o] = reg[i].x;
-      S[(kq * 4 + 1) * LDS_W + o] = reg[i].y;
-      S[(kq * 4 + 2) * LDS_W + o] = reg[i].z;
-      S[(kq * 4 + 3) * LDS_W + o] = reg[i].w;
+      S[(kq * 4 + 0) * W + o] = reg[i].x;
+      S[(kq * 4 + 1) * W + o] = reg[i].y;
+      S[(kq * 4 + 2) * W + o] = reg[i].z;
+      S[(kq * 4 + 3) * W + o] = reg[i].w;
     } else {
-      int k = f >> 5, oq = f & 31;
-      *reinterpret_cast<float4*>(S + k * LDS_W + oq * 4) = reg[i];
+      constexpr int Q = OUTER / 4;
+      int k = f / Q, oq = f % Q;
+      *reinterpret_cast<float4*>(S + k * W + oq * 4) = reg[i];
     }
   }
 }
 
-template <bool TA, bool TB>
+template <int BM, int BN, bool TA, bool TB, bool EDGE>
 __global__ __launch_bounds__(kThreads, 2) void k_gemm(GemmArgs g) {
-  __shared__ __attribute__((aligned(16))) float As[2][BK * LDA_S];
-  __shared__ __attribute__((aligned(16))) float Bs[2][BK * LDB_S];
+  constexpr int LA = BM + 4, LB = BN + 4;       // LDS row lengths
+  constexpr int WM = BM / 2, WN = BN / 2;       // wave tile
+  constexpr int FM = WM / 32, FN = WN / 32;     // MFMA blocks per wave
+  constexpr int VA = BM * BK / (kThreads * 4);  // float4 loads per lane
+  constexpr int VB = BN * BK / (kThreads * 4);
+  static_assert(FM >= 1 && FN >= 1 && VA >= 1 && VB >= 1, "tile too small");
+  __shared__ __attribute__((aligned(16))) float As[2][BK * LA];
+  __shared__ __attribute__((aligned(16))) float Bs[2][BK * LB];
 
   // ---- tile coordinates (grouped ordering for L2 reuse)
   const int tiles_m = g.tiles_m, tiles_n = g.tiles_n;
@@ -143,11 +158,11 @@ __global__ __launch_bounds__(kThreads, 2) void k_gemm(GemmArgs g) {
   const int wm = wid >> 1, wn = wid & 1;
   const int l32 = lane & 31, h = lane >> 5;
 
-  floatx16 acc[2][2];
+  floatx16 acc[FM][FN];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < FN; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
@@ -155,36 +170,47 @@ __global__ __launch_bounds__(kThreads, 2) void k_gemm(GemmArgs g) {
   // B: logical [K][N]; as an "outer = n" tile it is stored [N][K] when TB
   //    (k contiguous, like !TA) and [K][N] when !TB (n contiguous, like TA).
   const int64_t ktiles = kend > kbeg ? cdiv(kend - kbeg, BK) : 0;
-  float4 ra[2], rb[2];
-  load_tile<TA>(A, g.lda, g.M, kend, m0, kbeg, g.vecA, ra);
-  load_tile<!TB>(B, g.ldb, g.N, kend, n0, kbeg, g.vecB, rb);
-  store_tile<TA, LDA_S>(As[0], ra);
-  store_tile<!TB, LDB_S>(Bs[0], rb);
+  float4 ra[VA], rb[VB];
+  load_tile<TA, BM, VA, EDGE>(A, g.lda, g.M, kend, m0, kbeg, ra);
+  load_tile<!TB, BN, VB, EDGE>(B, g.ldb, g.N, kend, n0, kbeg, rb);
+  store_tile<TA, BM, VA, LA>(As[0], ra);
+  store_tile<!TB, BN, VB, LB>(Bs[0], rb);
   __syncthreads();
 
   for (int64_t kt = 0; kt < ktiles; ++kt) {
     const int cur = kt & 1;
     const bool more = kt + 1 < ktiles;
     if (more) {
-      load_tile<TA>(A, g.lda, g.M, kend, m0, kbeg + (kt + 1) * BK, g.vecA, ra);
-      load_tile<!TB>(B, g.ldb, g.N, kend, n0, kbeg + (kt + 1) * BK, g.vecB, rb);
+      const int64_t k0 = kbeg + (kt + 1) * BK;
+      load_tile<TA, BM, VA, EDGE>(A, g.lda, g.M, kend, m0, k0, ra);
+      load_tile<!TB, BN, VB, EDGE>(B, g.ldb, g.N, kend, n0, k0, rb);
     }
-    const float* __restrict__ as = As[cur];
-    const float* __restrict__ bs = Bs[cur];
+    const float* __restrict__ as = As[cur] + wm * WM + l32;
+    const float* __restrict__ bs = Bs[cur] + wn * WN + l32;
+    // fragments of step kk+2 are read from LDS before the MFMAs of step kk
+    float a[2][FM], bv[2][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i) a[0][i] = as[h * LA + i * 32];
+#pragma unroll
+    for (int j = 0; j < FN; ++j) bv[0][j] = bs[h * LB + j * 32];
 #pragma unroll
     for (int kk = 0; kk < BK; kk += 2) {
-      float a0 = as[(kk + h) * LDA_S + wm * 64 + l32];
-      float a1 = as[(kk + h) * LDA_S + wm * 64 + 32 + l32];
-      float b0 = bs[(kk + h) * LDB_S + wn * 64 + l32];
-      float b1 = bs[(kk + h) * LDB_S + wn * 64 + 32 + l32];
-      acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b0, acc[0][0], 0, 0, 0);
-      acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b1, acc[0][1], 0, 0, 0);
-      acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b0, acc[1][0], 0, 0, 0);
-      acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b1, acc[1][1], 0, 0, 0);
+      const int c = (kk >> 1) & 1;
+      if (kk + 2 < BK) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i) a[c ^ 1][i] = as[(kk + 2 + h) * LA + i * 32];
+#pragma unroll
+        for (int j = 0; j < FN; ++j) bv[c ^ 1][j] = bs[(kk + 2 + h) * LB + j * 32];
+      }
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[c][i], bv[c][j], acc[i][j], 0, 0, 0);
     }
     if (more) {
-      store_tile<TA, LDA_S>(As[cur ^ 1], ra);
-      store_tile<!TB, LDB_S>(Bs[cur ^ 1], rb);
+      store_tile<TA, BM, VA, LA>(As[cur ^ 1], ra);
+      store_tile<!TB, BN, VB, LB>(Bs[cur ^ 1], rb);
     }
     __syncthreads();
   }
@@ -194,29 +220,29 @@ __global__ __launch_bounds__(kThreads, 2) void k_gemm(GemmArgs g) {
     // raw partial sums; the reduce kernel applies alpha / beta / bias
     float* __restrict__ W = g.ws + ((int64_t)b * gridDim.y + blockIdx.y) * g.M * g.N;
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < FM; ++i)
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int64_t col = n0 + wn * 64 + j * 32 + l32;
+      for (int j = 0; j < FN; ++j) {
+        const int64_t col = n0 + wn * WN + j * 32 + l32;
         if (col >= g.N) continue;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const int64_t row = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+          const int64_t row = m0 + wm * WM + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
           if (row < g.M) W[row * g.N + col] = acc[i][j][r];
         }
       }
     return;
   }
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
+  for (int i = 0; i < FM; ++i) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int64_t col = n0 + wn * 64 + j * 32 + l32;
+    for (int j = 0; j < FN; ++j) {
+      const int64_t col = n0 + wn * WN + j * 32 + l32;
       if (col >= g.N) continue;
       float bn = (g.bias_mode == 1) ? g.bias[col] : 0.f;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int64_t row = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+        const int64_t row = m0 + wm * WM + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
         if (row < g.M) {
           float v = g.alpha * acc[i][j][r];
           float* cp = C + row * g.ldc + col;
@@ -251,6 +277,166 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(GemmArgs g, int splits) {
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
+// ------------------------------------------------------------ tile choice
+
+struct TileCfg {
+  int bm, bn;
+};
+constexpr TileCfg kTiles[] = {{256, 128}, {128, 128}, {128, 64}, {64, 64}};
+constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
+
+// Measured relative per-FLOP throughput of each tile with the CUs full, by
+// operand layout (GPT-2 products on MI355X): with B read k-contiguous
+// (NT, the forward) 128x128 is fastest; with B read n-contiguous (NN dgrad,
+// TN wgrad) the 128x64 tile's higher occupancy wins.
+float tile_speed(int ti, int ta, int tb) {
+  static const float nt[kNumTiles] = {0.85f, 1.00f, 0.95f, 0.85f};
+  static const float nn[kNumTiles] = {0.80f, 0.91f, 1.00f, 0.85f};
+  static const float tn[kNumTiles] = {0.80f, 0.93f, 1.00f, 0.85f};
+  if (!ta && tb) return nt[ti];
+  if (!ta && !tb) return nn[ti];
+  if (ta && !tb) return tn[ti];
+  return nt[ti];
+}
+
+struct Plan {
+  int tile;
+  int64_t splits;
+};
+
+// Work per CU is balanced when the workgroup count is a multiple of the
+// CU count: fill = (wgs / cus) / ceil(wgs / cus).
+double fill_of(int64_t wgs, int cus) {
+  double r = (double)wgs / cus;
+  return r / (double)cdiv(wgs, cus);
+}
+
+// Split-K factor for `tiles` output tiles: K slices of >= 256, at most 64,
+// chosen for the best fill once the tiles alone cannot fill the CUs twice.
+int64_t choose_splits(int64_t tiles, int64_t K, int cus) {
+  if (tiles >= 2LL * cus || K < 4 * 256) return 1;
+  int64_t smax = K / 256;
+  if (smax > 64) smax = 64;
+  int64_t best = 1;
+  double best_f = -1.0;
+  for (int64_t s = 1; s <= smax; ++s) {
+    if (tiles * s < cus && s < smax) continue;
+    // partial traffic grows with s: prefer fewer splits on near ties
+    double f = fill_of(tiles * s, cus) * (1.0 - 0.004 * (double)s);
+    if (tiles * s < cus) f *= (double)(tiles * s) / cus;
+    if (f > best_f + 1e-9) {
+      best_f = f;
+      best = s;
+    }
+  }
+  return best;
+}
+
+// Picks tile and split maximising (useful fraction of padded work) x
+// (CU fill) x tile speed.  TJH_GEMM_TILE=BMxBN forces a tile.
+Plan choose_plan(int64_t M, int64_t N, int64_t K, int64_t batch, int cus, int ta, int tb) {
+  static int forced = -2;
+  if (forced == -2) {
+    forced = -1;
+    const char* e = getenv("TJH_GEMM_TILE");
+    if (e) {
+      for (int i = 0; i < kNumTiles; ++i) {
+        char buf[32];
+        snprintf(buf, sizeof(buf), "%dx%d", kTiles[i].bm, kTiles[i].bn);
+        if (strcmp(buf, e) == 0) forced = i;
+      }
+    }
+  }
+  Plan best{1, 1};
+  double best_score = -1.0;
+  for (int i = 0; i < kNumTiles; ++i) {
+    if (forced >= 0 && i != forced) continue;
+    const TileCfg& t = kTiles[i];
+    int64_t tm = cdiv(M, t.bm), tn = cdiv(N, t.bn);
+    double useful = (double)(M * N) / (double)(tm * t.bm * tn * t.bn);
+    int64_t tiles = tm * tn * batch;
+    int64_t s = choose_splits(tiles, K, cus);
+    double score = useful * fill_of(tiles * s, cus) * tile_speed(i, ta, tb);
+    if (tiles * s < cus) score *= (double)(tiles * s) / cus;
+    if (score > best_score + 1e-9) {
+      best_score = score;
+      best = Plan{i, s};
+    }
+  }
+  return best;
+}
+
+template <int BM, int BN, bool EDGE>
+void launch_e(const GemmArgs& g, dim3 grid, int ta, int tb) {
+  if (!ta && !tb)
+    hipLaunchKernelGGL((k_gemm<BM, BN, false, false, EDGE>), grid, dim3(kThreads), 0, stream(), g);
+  else if (!ta && tb)
+    hipLaunchKernelGGL((k_gemm<BM, BN, false, true, EDGE>), grid, dim3(kThreads), 0, stream(), g);
+  else if (ta && !tb)
+    hipLaunchKernelGGL((k_gemm<BM, BN, true, false, EDGE>), grid, dim3(kThreads), 0, stream(), g);
+  else
+    hipLaunchKernelGGL((k_gemm<BM, BN, true, true, EDGE>), grid, dim3(kThreads), 0, stream(), g);
+}
+
+template <int BM, int BN>
+void launch(const GemmArgs& g, dim3 grid, int ta, int tb, bool edge) {
+  if (edge) launch_e<BM, BN, true>(g, grid, ta, tb);
+  else launch_e<BM, BN, false>(g, grid, ta, tb);
+}
+
+void launch_tile(int ti, const GemmArgs& g, dim3 grid, int ta, int tb, bool edge) {
+  switch (ti) {
+    case 0: launch<256, 128>(g, grid, ta, tb, edge); break;
+    case 1: launch<128, 128>(g, grid, ta, tb, edge); break;
+    case 2: launch<128, 64>(g, grid, ta, tb, edge); break;
+    default: launch<64, 64>(g, grid, ta, tb, edge); break;
+  }
+}
+
+// One launch of tile `ti` over the whole of g (plus the split-K pass).
+int run_block(int ti, GemmArgs g, int ta, int tb, int64_t splits, int64_t batch, bool edge,
+              int cus) {
+  const TileCfg& tc = kTiles[ti];
+  g.tiles_m = (int)cdiv(g.M, tc.bm);
+  g.tiles_n = (int)cdiv(g.N, tc.bn);
+  TJH_ARG((int64_t)g.tiles_m * g.tiles_n < (int64_t(1) << 31), "tjh_gemm: too many tiles");
+  g.kchunk = cdiv(cdiv(g.K, splits), BK) * BK;
+  if (g.kchunk < BK) g.kchunk = BK;
+  splits = cdiv(g.K, g.kchunk) > 0 ? cdiv(g.K, g.kchunk) : 1;
+  g.ws = nullptr;
+  Scratch ws(splits > 1 ? (size_t)(batch * splits * g.M * g.N) * sizeof(float) : 0);
+  if (splits > 1) {
+    if (!ws.ok()) {
+      splits = 1;
+      g.kchunk = g.K > 0 ? cdiv(g.K, BK) * BK : BK;
+    } else {
+      g.ws = ws.as<float>();
+    }
+  }
+  dim3 grid((unsigned)(g.tiles_m * g.tiles_n), (unsigned)splits, (unsigned)batch);
+  launch_tile(ti, g, grid, ta, tb, edge);
+  int rc = check_launch("gemm");
+  if (rc != TJH_OK || splits == 1) return rc;
+  int64_t blocks = cdiv(g.M * g.N, 256);
+  if (blocks > 4LL * cus) blocks = 4LL * cus;
+  hipLaunchKernelGGL(k_splitk_reduce, dim3((unsigned)blocks, (unsigned)batch), dim3(256), 0,
+                     stream(), g, (int)splits);
+  return check_launch("gemm_splitk_reduce");
+}
+
+// Sub-problem of g: rows [m0, m0+M), cols [n0, n0+N), k [k0, k0+K).
+GemmArgs sub(const GemmArgs& g, int ta, int tb, int64_t m0, int64_t M, int64_t n0, int64_t N,
+             int64_t k0, int64_t K) {
+  GemmArgs s = g;
+  s.M = M; s.N = N; s.K = K;
+  s.A = g.A + (ta ? k0 * g.lda + m0 : m0 * g.lda + k0);
+  s.B = g.B + (tb ? n0 * g.ldb + k0 : k0 * g.ldb + n0);
+  s.C = g.C + m0 * g.ldc + n0;
+  if (g.bias_mode == 1) s.bias = g.bias + n0;
+  else if (g.bias_mode == 2) s.bias = g.bias + m0;
+  return s;
+}
+
 }  // namespace
 }  // namespace tjh
 
@@ -270,6 +456,7 @@ int tjh::gemm(const char* family, int transA, int transB, int64_t M, int64_t N, 
   TJH_ARG(lda >= (transA ? M : K) || (transA ? M : K) <= 1, "tjh_gemm: lda too small");
   TJH_ARG(ldb >= (transB ? K : N) || (transB ? K : N) <= 1, "tjh_gemm: ldb too small");
   TJH_ARG(ldc >= N, "tjh_gemm: ldc too small");
+  const int cus = num_cus() > 0 ? num_cus() : 256;
   GemmArgs g;
   g.A = A; g.B = B; g.C = C; g.bias = bias;
   g.M = M; g.N = N; g.K = K;
@@ -278,52 +465,45 @@ int tjh::gemm(const char* family, int transA, int transB, int64_t M, int64_t N, 
   g.alpha = alpha; g.beta = beta; g.bias_mode = bias_mode;
   g.vecA = aligned16(A) && (lda % 4 == 0) && (strideA % 4 == 0);
   g.vecB = aligned16(B) && (ldb % 4 == 0) && (strideB % 4 == 0);
-  g.tiles_m = (int)cdiv(M, BM);
-  g.tiles_n = (int)cdiv(N, BN);
-  TJH_ARG((int64_t)g.tiles_m * g.tiles_n < (int64_t(1) << 31), "tjh_gemm: too many tiles");
-  // Split K when the output tiles alone cannot fill the machine (weight
-  // gradients: small M x N, K = tokens).  Partials go to scratch and a
-  // second pass sums them in a fixed order.
-  int cus = num_cus() > 0 ? num_cus() : 256;
-  int64_t tiles = (int64_t)g.tiles_m * g.tiles_n * batch;
-  int64_t splits = 1;
-  if (tiles < 2LL * cus && K >= 4 * 256) {
-    splits = cdiv(2LL * cus, tiles);
-    int64_t by_k = K / 256;  // >= 256 of K per split
-    if (splits > by_k) splits = by_k;
-    if (splits > 64) splits = 64;
-    if (splits < 1) splits = 1;
-  }
-  g.kchunk = cdiv(cdiv(K, splits), BK) * BK;
-  if (g.kchunk < BK) g.kchunk = BK;
-  splits = cdiv(K, g.kchunk) > 0 ? cdiv(K, g.kchunk) : 1;
+  g.tiles_m = g.tiles_n = 0;
+  g.kchunk = BK;
   g.ws = nullptr;
-  Scratch ws(splits > 1 ? (size_t)(batch * splits * M * N) * sizeof(float) : 0);
-  if (splits > 1) {
-    if (!ws.ok()) {
-      splits = 1;
-      g.kchunk = K > 0 ? cdiv(K, BK) * BK : BK;
-    } else {
-      g.ws = ws.as<float>();
-    }
-  }
-  dim3 grid((unsigned)(g.tiles_m * g.tiles_n), (unsigned)splits, (unsigned)batch);
   KernelScope ks(family);
-  if (!transA && !transB)
-    hipLaunchKernelGGL((k_gemm<false, false>), grid, dim3(kThreads), 0, stream(), g);
-  else if (!transA && transB)
-    hipLaunchKernelGGL((k_gemm<false, true>), grid, dim3(kThreads), 0, stream(), g);
-  else if (transA && !transB)
-    hipLaunchKernelGGL((k_gemm<true, false>), grid, dim3(kThreads), 0, stream(), g);
-  else
-    hipLaunchKernelGGL((k_gemm<true, true>), grid, dim3(kThreads), 0, stream(), g);
-  int rc = check_launch("gemm");
-  if (rc != TJH_OK || splits == 1) return rc;
-  int64_t blocks = cdiv(M * N, 256);
-  if (blocks > 4LL * cus) blocks = 4LL * cus;
-  hipLaunchKernelGGL(k_splitk_reduce, dim3((unsigned)blocks, (unsigned)batch), dim3(256), 0,
-                     stream(), g, (int)splits);
-  return check_launch("gemm_splitk_reduce");
+  const Plan plan = choose_plan(M, N, K, batch, cus, transA, transB);
+  const TileCfg& tc = kTiles[plan.tile];
+  if (!(g.vecA && g.vecB)) {
+    // unaligned operands: guarded loads everywhere
+    return run_block(plan.tile, g, transA, transB, plan.splits, batch, true, cus);
+  }
+  // Interior block [0,Mm) x [0,Nm) x [0,Km) runs the unguarded kernel; the
+  // row / column strips beyond it run the guarded one; a K remainder is
+  // added by one more guarded pass with beta = 1.
+  const int64_t Mm = M / tc.bm * tc.bm, Nm = N / tc.bn * tc.bn, Km = K / BK * BK;
+  const int64_t Kr = K - Km;
+  GemmArgs gk = g;
+  gk.K = Km;
+  int rc = TJH_OK;
+  if (Km == 0) {
+    // K < 16: one guarded pass does it all
+    return run_block(plan.tile, g, transA, transB, 1, batch, true, cus);
+  }
+  if (Mm > 0 && Nm > 0)
+    rc = run_block(plan.tile, sub(gk, transA, transB, 0, Mm, 0, Nm, 0, Km), transA, transB,
+                   plan.splits, batch, false, cus);
+  if (rc == TJH_OK && Nm < N)  // right strip (all rows)
+    rc = run_block(plan.tile, sub(gk, transA, transB, 0, M, Nm, N - Nm, 0, Km), transA, transB,
+                   1, batch, true, cus);
+  if (rc == TJH_OK && Mm < M && Nm > 0)  // bottom strip (interior columns)
+    rc = run_block(plan.tile, sub(gk, transA, transB, Mm, M - Mm, 0, Nm, 0, Km), transA, transB,
+                   1, batch, true, cus);
+  if (rc == TJH_OK && Kr > 0) {
+    GemmArgs gr = sub(g, transA, transB, 0, M, 0, N, Km, Kr);
+    gr.beta = 1.0f;
+    gr.bias_mode = 0;
+    gr.bias = nullptr;
+    rc = run_block(plan.tile, gr, transA, transB, 1, batch, true, cus);
+  }
+  return rc;
 }
 
 extern "C" int tjh_gemm(int transA, int transB, int64_t M, int64_t N, int64_t K, float alpha,
