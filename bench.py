@@ -134,17 +134,38 @@ def cpu_baseline():
                       "tokens, full 12 layers and 50257 vocab), %.1f s" % dt}
 
 
+def copy_calibration(mib):
+    """A plain contiguous device copy of `mib` MiB through the library's
+    vectorised copy kernel (3 launches): the known-size reference that HBM
+    byte counters are scaled by."""
+    import __graft_entry__ as ge
+    torch = ge.load_package()
+    torch.init(0)
+    n = mib * (1 << 20) // 4
+    x = torch.zeros(n)
+    for _ in range(3):
+        y = x.clone()
+    torch.synchronize()
+    del y
+    print(json.dumps({"copy_calibration_bytes": n * 4, "launches": 3}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="only run the copy-kernel calibration of this many MiB")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one MI355X: this build has no multi-GPU path "
               "(--gpus %d requested)" % args.gpus, file=sys.stderr)
         sys.exit(2)
+    if args.copy_mib:
+        copy_calibration(args.copy_mib)
+        return
     elapsed, final_loss, timing, nparams, mem = run_gpu(args.steps, args.warmup)
     tokens = B * T * args.steps
     ms_step = 1000.0 * elapsed / args.steps

@@ -1,0 +1,54 @@
+"""The Node-API binding (torch.js_amd/node/torchjs_hip_napi.c): the entry
+points torch.js's TypeScript host would call for device 'hip'."""
+import json
+import os
+import shutil
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+ADDON = os.path.join(ROOT, "torch.js_amd", "node", "torchjs_hip.node")
+CHECK = os.path.join(ROOT, "torch.js_amd", "node", "addon_check.js")
+NODE = shutil.which("node")
+
+EXPORTS = ["init", "deviceInfo", "malloc", "h2d", "d2h", "d2hAsync", "synchronize",
+           "memoryStats", "emptyCache", "fill", "random", "copyStrided", "unary",
+           "unaryBackward", "binary", "scalar", "reduce", "softmaxForward", "softmaxBackward",
+           "crossEntropyForward", "crossEntropyBackward", "layerNormForward",
+           "layerNormBackward", "embeddingForward", "embeddingBackward", "gemm", "sdpaForward",
+           "sdpaBackward", "adamStep", "version"]
+
+needs_addon = pytest.mark.skipif(NODE is None or not os.path.exists(ADDON),
+                                 reason="node or the built addon is absent")
+
+
+def _node(script, timeout=60):
+    return subprocess.run([NODE, "-e", script], capture_output=True, text=True, timeout=timeout,
+                          cwd=ROOT)
+
+
+@needs_addon
+def test_addon_exports():
+    r = _node("const a=require(%r); console.log(JSON.stringify(Object.keys(a)))" % ADDON)
+    assert r.returncode == 0, r.stderr
+    keys = json.loads(r.stdout)
+    assert sorted(keys) == sorted(EXPORTS)
+
+
+@needs_addon
+def test_addon_error_before_init():
+    # no device call happens: the library refuses before touching HIP
+    r = _node("const a=require(%r); try { a.synchronize(); console.log('no-throw') } "
+              "catch (e) { console.log(e.message) }" % ADDON)
+    assert r.returncode == 0, r.stderr
+    assert "not initialized" in r.stdout
+
+
+@pytest.mark.gpu
+@needs_addon
+def test_addon_end_to_end():
+    r = subprocess.run([NODE, CHECK], capture_output=True, text=True, timeout=120, cwd=ROOT)
+    assert r.returncode == 0, r.stdout + r.stderr
+    out = json.loads(r.stdout.strip().splitlines()[-1])
+    assert out["ok"] and out["device"].startswith("gfx950")

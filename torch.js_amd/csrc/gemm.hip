@@ -24,7 +24,8 @@
 // Global loads are 128-bit when the operand's contiguous dimension and row
 // stride allow it; edge tiles fall back to guarded scalar loads.
 // Workgroup order: tiles are grouped 8 M-tiles at a time so neighbouring
-// workgroups share B columns in L2.
+// tiles share B columns, and each XCD receives a contiguous run of that
+// order so the sharing happens inside one L2.
 
 #include "common.h"
 
@@ -39,6 +40,10 @@ constexpr int BK = 16;
 constexpr int kThreads = 256;
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+// Staging registers are native 4-wide vectors: a struct float4 copied out
+// of a reinterpret_cast load is not always split into registers by the
+// compiler and then lives in scratch memory.
+typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 struct GemmArgs {
   const float* A;
@@ -65,7 +70,7 @@ struct GemmArgs {
 template <bool TRANS, int OUTER, int V, bool EDGE>
 __device__ __forceinline__ void load_tile(const float* __restrict__ P, int64_t ld, int64_t rows,
                                           int64_t cols, int64_t r0, int64_t c0,
-                                          float4 (&reg)[V]) {
+                                          floatx4 (&reg)[V]) {
   const int t = threadIdx.x;
 #pragma unroll
   for (int i = 0; i < V; ++i) {
@@ -73,11 +78,11 @@ __device__ __forceinline__ void load_tile(const float* __restrict__ P, int64_t l
     if (!EDGE) {
       if (!TRANS) {
         int o = f >> 2, kq = f & 3;
-        reg[i] = *reinterpret_cast<const float4*>(P + (r0 + o) * ld + c0 + kq * 4);
+        reg[i] = *reinterpret_cast<const floatx4*>(P + (r0 + o) * ld + c0 + kq * 4);
       } else {
         constexpr int Q = OUTER / 4;
         int k = f / Q, oq = f % Q;
-        reg[i] = *reinterpret_cast<const float4*>(P + (c0 + k) * ld + r0 + oq * 4);
+        reg[i] = *reinterpret_cast<const floatx4*>(P + (c0 + k) * ld + r0 + oq * 4);
       }
     } else {
       float v[4];
@@ -95,14 +100,14 @@ __device__ __forceinline__ void load_tile(const float* __restrict__ P, int64_t l
         for (int j = 0; j < 4; ++j)
           v[j] = (gk < cols && go + j < rows) ? P[gk * ld + go + j] : 0.f;
       }
-      reg[i] = make_float4(v[0], v[1], v[2], v[3]);
+      reg[i] = floatx4{v[0], v[1], v[2], v[3]};
     }
   }
 }
 
 // Stores a loaded tile into LDS laid out S[k][outer] (row length W).
 template <bool TRANS, int OUTER, int V, int W>
-__device__ __forceinline__ void store_tile(float* __restrict__ S, const float4 (&reg)[V]) {
+__device__ __forceinline__ void store_tile(float* __restrict__ S, const floatx4 (&reg)[V]) {
   const int t = threadIdx.x;
 #pragma unroll
   for (int i = 0; i < V; ++i) {
@@ -116,9 +121,21 @@ __device__ __forceinline__ void store_tile(float* __restrict__ S, const float4 (
     } else {
       constexpr int Q = OUTER / 4;
       int k = f / Q, oq = f % Q;
-      *reinterpret_cast<float4*>(S + k * W + oq * 4) = reg[i];
+      *reinterpret_cast<floatx4*>(S + k * W + oq * 4) = reg[i];
     }
   }
+}
+
+// Workgroups are dispatched to the 8 XCDs round-robin (workgroup w runs on
+// XCD w % 8), and each XCD has its own L2.  Renumbering so that XCD x
+// receives the contiguous run [x*n/8, (x+1)*n/8) of the grouped tile order
+// keeps the tiles that share A rows and B columns on one L2.  A bijection on
+// [0, n): ids past the last multiple of 8 keep their number.
+constexpr int kXcds = 8;
+__device__ __forceinline__ int xcd_tile(int bid, int n) {
+  const int full = n - n % kXcds;
+  if (bid >= full) return bid;
+  return (bid % kXcds) * (full / kXcds) + bid / kXcds;
 }
 
 template <int BM, int BN, bool TA, bool TB, bool EDGE>
@@ -134,7 +151,7 @@ __global__ __launch_bounds__(kThreads, 2) void k_gemm(GemmArgs g) {
 
   // ---- tile coordinates (grouped ordering for L2 reuse)
   const int tiles_m = g.tiles_m, tiles_n = g.tiles_n;
-  int bid = blockIdx.x;
+  int bid = xcd_tile(blockIdx.x, gridDim.x);
   constexpr int GROUP = 8;
   int group_size = GROUP * tiles_n;
   int group = bid / group_size;
@@ -170,7 +187,7 @@ __global__ __launch_bounds__(kThreads, 2) void k_gemm(GemmArgs g) {
   // B: logical [K][N]; as an "outer = n" tile it is stored [N][K] when TB
   //    (k contiguous, like !TA) and [K][N] when !TB (n contiguous, like TA).
   const int64_t ktiles = kend > kbeg ? cdiv(kend - kbeg, BK) : 0;
-  float4 ra[VA], rb[VB];
+  floatx4 ra[VA], rb[VB];
   load_tile<TA, BM, VA, EDGE>(A, g.lda, g.M, kend, m0, kbeg, ra);
   load_tile<!TB, BN, VB, EDGE>(B, g.ldb, g.N, kend, n0, kbeg, rb);
   store_tile<TA, BM, VA, LA>(As[0], ra);

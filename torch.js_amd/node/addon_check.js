@@ -1,0 +1,116 @@
+// End-to-end check of the Node-API binding on a GPU: allocate through the
+// addon, upload, run a GEMM, a cross-entropy forward/backward and one Adam
+// step, read back with d2hAsync, and compare with float64 JavaScript
+// restatements of the same arithmetic.  Prints one JSON line; exits 1 on a
+// mismatch.
+'use strict';
+const path = require('path');
+const hip = require(path.join(__dirname, 'torchjs_hip.node'));
+
+function lcg(seed) {
+  let s = seed >>> 0;
+  return () => {
+    s = (Math.imul(s, 1664525) + 1013904223) >>> 0;
+    return s / 4294967296 - 0.5;
+  };
+}
+
+function upload(arr) {
+  const buf = hip.malloc(arr.byteLength);
+  hip.h2d(buf.ptr, arr);
+  return buf;
+}
+
+async function main() {
+  hip.init(0);
+  const info = hip.deviceInfo();
+  const rnd = lcg(7);
+  const out = { device: info.arch, version: hip.version };
+  let ok = true;
+
+  // GEMM C[M,N] = A[M,K] B[K,N] + bias[N]
+  const M = 67, N = 45, K = 33;
+  const A = Float32Array.from({ length: M * K }, rnd);
+  const Bm = Float32Array.from({ length: K * N }, rnd);
+  const bias = Float32Array.from({ length: N }, rnd);
+  const dA = upload(A), dB = upload(Bm), dBias = upload(bias);
+  const dC = hip.malloc(M * N * 4);
+  hip.gemm(0, 0, M, N, K, 1.0, dA.ptr, K, 0, dB.ptr, N, 0, 0.0, dC.ptr, N, 0, 1, dBias.ptr, 1);
+  const C = await hip.d2hAsync(dC.ptr, new Float32Array(M * N));
+  let gemmErr = 0;
+  for (let i = 0; i < M; ++i) {
+    for (let j = 0; j < N; ++j) {
+      let s = bias[j];
+      for (let k = 0; k < K; ++k) s += A[i * K + k] * Bm[k * N + j];
+      gemmErr = Math.max(gemmErr, Math.abs(C[i * N + j] - s));
+    }
+  }
+  out.gemm_max_abs_err = gemmErr;
+  ok = ok && gemmErr < 1e-5;
+
+  // cross_entropy (mean) forward + backward
+  const R = 9, V = 101;
+  const logits = Float32Array.from({ length: R * V }, () => 4 * rnd());
+  const tg = Int32Array.from({ length: R }, (_, i) => (i * 37) % V);
+  tg[3] = -100;  // ignore_index
+  const dL = upload(logits), dT = upload(tg);
+  const dLse = hip.malloc(R * 4), dRows = hip.malloc(R * 4), dLoss = hip.malloc(4);
+  hip.crossEntropyForward(dL.ptr, V, dT.ptr, R, V, -100, dLse.ptr, dRows.ptr, 1, dLoss.ptr);
+  const one = upload(Float32Array.of(1));
+  const dG = hip.malloc(R * V * 4);
+  hip.crossEntropyBackward(dL.ptr, V, dT.ptr, dLse.ptr, one.ptr, R, V, -100, 1, dG.ptr, V, 0);
+  const loss = (await hip.d2hAsync(dLoss.ptr, new Float32Array(1)))[0];
+  const grad = await hip.d2hAsync(dG.ptr, new Float32Array(R * V));
+  let ref = 0, valid = 0, gErr = 0;
+  const lse = [];
+  for (let r = 0; r < R; ++r) {
+    let mx = -Infinity;
+    for (let c = 0; c < V; ++c) mx = Math.max(mx, logits[r * V + c]);
+    let s = 0;
+    for (let c = 0; c < V; ++c) s += Math.exp(logits[r * V + c] - mx);
+    lse.push(mx + Math.log(s));
+    if (tg[r] !== -100) { ref += lse[r] - logits[r * V + tg[r]]; valid += 1; }
+  }
+  ref /= valid;
+  for (let r = 0; r < R; ++r) {
+    for (let c = 0; c < V; ++c) {
+      let g = 0;
+      if (tg[r] !== -100) g = (Math.exp(logits[r * V + c] - lse[r]) - (c === tg[r] ? 1 : 0)) / valid;
+      gErr = Math.max(gErr, Math.abs(grad[r * V + c] - g));
+    }
+  }
+  out.ce_loss = loss;
+  out.ce_loss_err = Math.abs(loss - ref);
+  out.ce_grad_max_abs_err = gErr;
+  ok = ok && out.ce_loss_err < 1e-5 * Math.max(1, Math.abs(ref)) && gErr < 1e-6;
+
+  // one Adam step (coupled weight decay), step 1
+  const P = 1000;
+  const p = Float32Array.from({ length: P }, rnd);
+  const g = Float32Array.from({ length: P }, rnd);
+  const dp = upload(p), dg = upload(g);
+  const dm = upload(new Float32Array(P)), dv = upload(new Float32Array(P));
+  const lr = 1e-3, b1 = 0.9, b2 = 0.999, eps = 1e-8, wd = 0.01;
+  hip.adamStep([dp.ptr], [dg.ptr], [dm.ptr], [dv.ptr], [P], [1], lr, b1, b2, eps, wd, 0);
+  const p1 = await hip.d2hAsync(dp.ptr, new Float32Array(P));
+  let aErr = 0;
+  for (let i = 0; i < P; ++i) {
+    const gg = g[i] + p[i] * wd;
+    const m = (1 - b1) * gg, v = (1 - b2) * gg * gg;
+    const upd = lr / (1 - b1) * m / (Math.sqrt(v / (1 - b2)) + eps);
+    aErr = Math.max(aErr, Math.abs(p1[i] - (p[i] - upd)));
+  }
+  out.adam_max_abs_err = aErr;
+  ok = ok && aErr < 1e-6;
+
+  hip.synchronize();
+  out.mem = hip.memoryStats();
+  out.ok = ok;
+  console.log(JSON.stringify(out));
+  process.exit(ok ? 0 : 1);
+}
+
+main().catch((e) => {
+  console.error(e && e.stack ? e.stack : e);
+  process.exit(1);
+});

@@ -1,0 +1,554 @@
+/*
+ * Node-API addon: the binding torch.js's TypeScript host uses to reach
+ * libtorchjs_hip.so (include/torchjs_hip.h).
+ *
+ * Device pointers cross into JavaScript as BigInt (so views can add byte
+ * offsets); an allocation is owned by an External whose finalizer returns
+ * it to the library's stream-ordered cache, which is safe whenever the GC
+ * runs because every later use is ordered on the library stream.
+ * Every failing call throws an Error carrying tjh_last_error().
+ * Host data moves through TypedArrays; d2hAsync resolves a Promise from a
+ * libuv worker (napi_async_work) so readbacks do not block the event loop,
+ * the analogue of torch.js's mapAsync readback (buffer.ts:150-206).
+ *
+ * Bound entry points: the runtime (init, device info, malloc / free,
+ * copies, sync, memory stats, timers) and the autograd hot path (fill,
+ * random, unary fwd/bwd, binary, scalar, reduce, softmax fwd/bwd,
+ * cross_entropy fwd/bwd, layer_norm fwd/bwd, embedding fwd/bwd, gemm,
+ * sdpa fwd/bwd, adam_step, copy_strided).
+ */
+#ifndef NAPI_VERSION
+#define NAPI_VERSION 8
+#endif
+#include <node_api.h>
+
+#include <stdint.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "torchjs_hip.h"
+
+#define MAXA 24
+
+static napi_value throw_last(napi_env env, int rc) {
+  char msg[1200];
+  snprintf(msg, sizeof(msg), "torchjs_hip error %d: %s", rc, tjh_last_error());
+  napi_throw_error(env, NULL, msg);
+  return NULL;
+}
+
+#define CHECK_RC(call)                      \
+  do {                                      \
+    int _rc = (call);                       \
+    if (_rc != 0) return throw_last(env, _rc); \
+  } while (0)
+
+static int get_args(napi_env env, napi_callback_info info, size_t want, napi_value* argv) {
+  size_t argc = MAXA;
+  napi_value tmp[MAXA];
+  if (napi_get_cb_info(env, info, &argc, tmp, NULL, NULL) != napi_ok) return 0;
+  if (argc < want) {
+    napi_throw_type_error(env, NULL, "too few arguments");
+    return 0;
+  }
+  for (size_t i = 0; i < want; ++i) argv[i] = tmp[i];
+  return 1;
+}
+
+static int64_t i64(napi_env env, napi_value v) {
+  napi_valuetype t;
+  napi_typeof(env, v, &t);
+  if (t == napi_bigint) {
+    int64_t r = 0;
+    bool lossless;
+    napi_get_value_bigint_int64(env, v, &r, &lossless);
+    return r;
+  }
+  double d = 0;
+  napi_get_value_double(env, v, &d);
+  return (int64_t)d;
+}
+
+static double f64(napi_env env, napi_value v) {
+  double d = 0;
+  napi_get_value_double(env, v, &d);
+  return d;
+}
+
+/* device pointer: BigInt (or 0 / null / undefined -> NULL) */
+static void* ptr(napi_env env, napi_value v) {
+  napi_valuetype t;
+  napi_typeof(env, v, &t);
+  if (t == napi_bigint) {
+    uint64_t r = 0;
+    bool lossless;
+    napi_get_value_bigint_uint64(env, v, &r, &lossless);
+    return (void*)(uintptr_t)r;
+  }
+  return NULL;
+}
+
+/* JS array of numbers -> int64 array (<= 8) */
+static int i64arr(napi_env env, napi_value v, int64_t* out, int maxn) {
+  uint32_t n = 0;
+  napi_get_array_length(env, v, &n);
+  if ((int)n > maxn) n = (uint32_t)maxn;
+  for (uint32_t i = 0; i < n; ++i) {
+    napi_value e;
+    napi_get_element(env, v, i, &e);
+    out[i] = i64(env, e);
+  }
+  return (int)n;
+}
+
+static napi_value undef(napi_env env) {
+  napi_value u;
+  napi_get_undefined(env, &u);
+  return u;
+}
+
+static napi_value bigint(napi_env env, void* p) {
+  napi_value r;
+  napi_create_bigint_uint64(env, (uint64_t)(uintptr_t)p, &r);
+  return r;
+}
+
+static napi_value num(napi_env env, double d) {
+  napi_value r;
+  napi_create_double(env, d, &r);
+  return r;
+}
+
+/* ---------------------------------------------------------------- runtime */
+
+static napi_value js_init(napi_env env, napi_callback_info info) {
+  napi_value a[1];
+  if (!get_args(env, info, 1, a)) return NULL;
+  CHECK_RC(tjh_init((int)i64(env, a[0])));
+  return undef(env);
+}
+
+static napi_value js_device_info(napi_env env, napi_callback_info info) {
+  (void)info;
+  tjh_device_info d;
+  CHECK_RC(tjh_get_device_info(&d));
+  napi_value o, s;
+  napi_create_object(env, &o);
+  napi_create_string_utf8(env, d.name, NAPI_AUTO_LENGTH, &s);
+  napi_set_named_property(env, o, "name", s);
+  napi_create_string_utf8(env, d.arch, NAPI_AUTO_LENGTH, &s);
+  napi_set_named_property(env, o, "arch", s);
+  napi_set_named_property(env, o, "computeUnits", num(env, d.compute_units));
+  napi_set_named_property(env, o, "totalMem", num(env, (double)d.total_mem));
+  napi_set_named_property(env, o, "warpSize", num(env, d.warp_size));
+  return o;
+}
+
+static void free_ext(napi_env env, void* data, void* hint) {
+  (void)env;
+  (void)hint;
+  tjh_free(data);
+}
+
+/* malloc(bytes) -> { ptr: BigInt, handle: External (frees on GC) } */
+static napi_value js_malloc(napi_env env, napi_callback_info info) {
+  napi_value a[1];
+  if (!get_args(env, info, 1, a)) return NULL;
+  void* p = NULL;
+  CHECK_RC(tjh_malloc((size_t)i64(env, a[0]), &p));
+  napi_value o, ext;
+  napi_create_object(env, &o);
+  napi_create_external(env, p, free_ext, NULL, &ext);
+  napi_set_named_property(env, o, "ptr", bigint(env, p));
+  napi_set_named_property(env, o, "handle", ext);
+  return o;
+}
+
+static int typed(napi_env env, napi_value v, void** data, size_t* bytes) {
+  napi_typedarray_type t;
+  size_t len, off;
+  napi_value buf;
+  if (napi_get_typedarray_info(env, v, &t, &len, data, &buf, &off) != napi_ok) return 0;
+  size_t es = 1;
+  switch (t) {
+    case napi_int8_array: case napi_uint8_array: case napi_uint8_clamped_array: es = 1; break;
+    case napi_int16_array: case napi_uint16_array: es = 2; break;
+    case napi_float64_array: case napi_bigint64_array: case napi_biguint64_array: es = 8; break;
+    default: es = 4;
+  }
+  *bytes = len * es;
+  return 1;
+}
+
+static napi_value js_h2d(napi_env env, napi_callback_info info) {
+  napi_value a[2];
+  if (!get_args(env, info, 2, a)) return NULL;
+  void* src;
+  size_t bytes;
+  if (!typed(env, a[1], &src, &bytes)) {
+    napi_throw_type_error(env, NULL, "h2d: expected a TypedArray");
+    return NULL;
+  }
+  CHECK_RC(tjh_h2d(ptr(env, a[0]), src, bytes));
+  return undef(env);
+}
+
+static napi_value js_d2h(napi_env env, napi_callback_info info) {
+  napi_value a[2];
+  if (!get_args(env, info, 2, a)) return NULL;
+  void* dst;
+  size_t bytes;
+  if (!typed(env, a[1], &dst, &bytes)) {
+    napi_throw_type_error(env, NULL, "d2h: expected a TypedArray");
+    return NULL;
+  }
+  CHECK_RC(tjh_d2h(dst, ptr(env, a[0]), bytes));
+  return undef(env);
+}
+
+typedef struct {
+  napi_async_work work;
+  napi_deferred deferred;
+  napi_ref keep;  /* the destination TypedArray */
+  void* dst;
+  const void* src;
+  size_t bytes;
+  int rc;
+  char msg[1024];
+} D2HJob;
+
+static void d2h_exec(napi_env env, void* data) {
+  (void)env;
+  D2HJob* j = (D2HJob*)data;
+  j->rc = tjh_d2h(j->dst, j->src, j->bytes);
+  if (j->rc) snprintf(j->msg, sizeof(j->msg), "%s", tjh_last_error());
+}
+
+static void d2h_done(napi_env env, napi_status status, void* data) {
+  (void)status;
+  D2HJob* j = (D2HJob*)data;
+  napi_value arr;
+  napi_get_reference_value(env, j->keep, &arr);
+  if (j->rc == 0) {
+    napi_resolve_deferred(env, j->deferred, arr);
+  } else {
+    napi_value m, e;
+    napi_create_string_utf8(env, j->msg, NAPI_AUTO_LENGTH, &m);
+    napi_create_error(env, NULL, m, &e);
+    napi_reject_deferred(env, j->deferred, e);
+  }
+  napi_delete_reference(env, j->keep);
+  napi_delete_async_work(env, j->work);
+  free(j);
+}
+
+/* d2hAsync(ptr, typedArray) -> Promise<typedArray> */
+static napi_value js_d2h_async(napi_env env, napi_callback_info info) {
+  napi_value a[2];
+  if (!get_args(env, info, 2, a)) return NULL;
+  D2HJob* j = (D2HJob*)calloc(1, sizeof(D2HJob));
+  if (!typed(env, a[1], &j->dst, &j->bytes)) {
+    free(j);
+    napi_throw_type_error(env, NULL, "d2hAsync: expected a TypedArray");
+    return NULL;
+  }
+  j->src = ptr(env, a[0]);
+  napi_value promise, name;
+  napi_create_promise(env, &j->deferred, &promise);
+  napi_create_reference(env, a[1], 1, &j->keep);
+  napi_create_string_utf8(env, "tjh_d2h", NAPI_AUTO_LENGTH, &name);
+  napi_create_async_work(env, NULL, name, d2h_exec, d2h_done, j, &j->work);
+  napi_queue_async_work(env, j->work);
+  return promise;
+}
+
+static napi_value js_sync(napi_env env, napi_callback_info info) {
+  (void)info;
+  CHECK_RC(tjh_synchronize());
+  return undef(env);
+}
+
+static napi_value js_memory_stats(napi_env env, napi_callback_info info) {
+  (void)info;
+  tjh_mem_stats s;
+  CHECK_RC(tjh_memory_stats(&s));
+  napi_value o;
+  napi_create_object(env, &o);
+  napi_set_named_property(env, o, "activeBytes", num(env, (double)s.active_bytes));
+  napi_set_named_property(env, o, "pooledBytes", num(env, (double)s.pooled_bytes));
+  napi_set_named_property(env, o, "peakBytes", num(env, (double)s.peak_bytes));
+  napi_set_named_property(env, o, "allocations", num(env, (double)s.allocations));
+  return o;
+}
+
+static napi_value js_empty_cache(napi_env env, napi_callback_info info) {
+  (void)info;
+  CHECK_RC(tjh_empty_cache());
+  return undef(env);
+}
+
+/* ---------------------------------------------------------------- kernels */
+
+static napi_value js_fill(napi_env env, napi_callback_info info) {
+  napi_value a[3];
+  if (!get_args(env, info, 3, a)) return NULL;
+  CHECK_RC(tjh_fill_f32((float*)ptr(env, a[0]), i64(env, a[1]), (float)f64(env, a[2])));
+  return undef(env);
+}
+
+static napi_value js_random(napi_env env, napi_callback_info info) {
+  napi_value a[4];
+  if (!get_args(env, info, 4, a)) return NULL;
+  CHECK_RC(tjh_random((float*)ptr(env, a[0]), i64(env, a[1]), (uint32_t)i64(env, a[2]),
+                      (int)i64(env, a[3])));
+  return undef(env);
+}
+
+static napi_value js_copy_strided(napi_env env, napi_callback_info info) {
+  napi_value a[5];
+  if (!get_args(env, info, 5, a)) return NULL;
+  int64_t shape[TJH_MAX_DIMS], ss[TJH_MAX_DIMS], ds[TJH_MAX_DIMS];
+  int nd = i64arr(env, a[0], shape, TJH_MAX_DIMS);
+  i64arr(env, a[2], ss, TJH_MAX_DIMS);
+  i64arr(env, a[4], ds, TJH_MAX_DIMS);
+  CHECK_RC(tjh_copy_strided(nd, shape, (const float*)ptr(env, a[1]), ss, (float*)ptr(env, a[3]), ds));
+  return undef(env);
+}
+
+static napi_value js_unary(napi_env env, napi_callback_info info) {
+  napi_value a[5];
+  if (!get_args(env, info, 5, a)) return NULL;
+  CHECK_RC(tjh_unary((int)i64(env, a[0]), (const float*)ptr(env, a[1]), (float*)ptr(env, a[2]),
+                     i64(env, a[3]), (float)f64(env, a[4])));
+  return undef(env);
+}
+
+static napi_value js_unary_backward(napi_env env, napi_callback_info info) {
+  napi_value a[7];
+  if (!get_args(env, info, 7, a)) return NULL;
+  CHECK_RC(tjh_unary_backward((int)i64(env, a[0]), (const float*)ptr(env, a[1]),
+                              (const float*)ptr(env, a[2]), (const float*)ptr(env, a[3]),
+                              (float*)ptr(env, a[4]), i64(env, a[5]), (float)f64(env, a[6])));
+  return undef(env);
+}
+
+/* binary(op, shape[], a, aStrides[], b, bStrides[], out) */
+static napi_value js_binary(napi_env env, napi_callback_info info) {
+  napi_value a[7];
+  if (!get_args(env, info, 7, a)) return NULL;
+  int64_t shape[TJH_MAX_DIMS], as[TJH_MAX_DIMS], bs[TJH_MAX_DIMS];
+  int nd = i64arr(env, a[1], shape, TJH_MAX_DIMS);
+  i64arr(env, a[3], as, TJH_MAX_DIMS);
+  i64arr(env, a[5], bs, TJH_MAX_DIMS);
+  CHECK_RC(tjh_binary((int)i64(env, a[0]), nd, shape, (const float*)ptr(env, a[2]), as,
+                      (const float*)ptr(env, a[4]), bs, (float*)ptr(env, a[6])));
+  return undef(env);
+}
+
+static napi_value js_scalar(napi_env env, napi_callback_info info) {
+  napi_value a[6];
+  if (!get_args(env, info, 6, a)) return NULL;
+  CHECK_RC(tjh_scalar((int)i64(env, a[0]), (const float*)ptr(env, a[1]), (float)f64(env, a[2]),
+                      (int)i64(env, a[3]), (float*)ptr(env, a[4]), i64(env, a[5])));
+  return undef(env);
+}
+
+static napi_value js_reduce(napi_env env, napi_callback_info info) {
+  napi_value a[6];
+  if (!get_args(env, info, 6, a)) return NULL;
+  CHECK_RC(tjh_reduce((int)i64(env, a[0]), (const float*)ptr(env, a[1]), i64(env, a[2]),
+                      i64(env, a[3]), i64(env, a[4]), (float*)ptr(env, a[5])));
+  return undef(env);
+}
+
+static napi_value js_softmax_forward(napi_env env, napi_callback_info info) {
+  napi_value a[7];
+  if (!get_args(env, info, 7, a)) return NULL;
+  CHECK_RC(tjh_softmax_forward((const float*)ptr(env, a[0]), i64(env, a[1]), (float*)ptr(env, a[2]),
+                               i64(env, a[3]), i64(env, a[4]), i64(env, a[5]), (int)i64(env, a[6])));
+  return undef(env);
+}
+
+static napi_value js_softmax_backward(napi_env env, napi_callback_info info) {
+  napi_value a[6];
+  if (!get_args(env, info, 6, a)) return NULL;
+  CHECK_RC(tjh_softmax_backward((const float*)ptr(env, a[0]), (const float*)ptr(env, a[1]),
+                                (float*)ptr(env, a[2]), i64(env, a[3]), i64(env, a[4]),
+                                (int)i64(env, a[5])));
+  return undef(env);
+}
+
+/* crossEntropyForward(logits, ld, targets, rows, cols, ignore, lse, lossRows, reduction, out) */
+static napi_value js_ce_forward(napi_env env, napi_callback_info info) {
+  napi_value a[10];
+  if (!get_args(env, info, 10, a)) return NULL;
+  CHECK_RC(tjh_cross_entropy_forward((const float*)ptr(env, a[0]), i64(env, a[1]),
+                                     (const int32_t*)ptr(env, a[2]), i64(env, a[3]), i64(env, a[4]),
+                                     (int32_t)i64(env, a[5]), (float*)ptr(env, a[6]),
+                                     (float*)ptr(env, a[7]), (int)i64(env, a[8]),
+                                     (float*)ptr(env, a[9])));
+  return undef(env);
+}
+
+/* crossEntropyBackward(logits, ld, targets, lse, gradOut, rows, cols, ignore, reduction, d, ldd, acc) */
+static napi_value js_ce_backward(napi_env env, napi_callback_info info) {
+  napi_value a[12];
+  if (!get_args(env, info, 12, a)) return NULL;
+  CHECK_RC(tjh_cross_entropy_backward(
+      (const float*)ptr(env, a[0]), i64(env, a[1]), (const int32_t*)ptr(env, a[2]),
+      (const float*)ptr(env, a[3]), (const float*)ptr(env, a[4]), i64(env, a[5]), i64(env, a[6]),
+      (int32_t)i64(env, a[7]), (int)i64(env, a[8]), (float*)ptr(env, a[9]), i64(env, a[10]),
+      (int)i64(env, a[11])));
+  return undef(env);
+}
+
+static napi_value js_ln_forward(napi_env env, napi_callback_info info) {
+  napi_value a[9];
+  if (!get_args(env, info, 9, a)) return NULL;
+  CHECK_RC(tjh_layer_norm_forward((const float*)ptr(env, a[0]), (const float*)ptr(env, a[1]),
+                                  (const float*)ptr(env, a[2]), (float*)ptr(env, a[3]),
+                                  (float*)ptr(env, a[4]), (float*)ptr(env, a[5]), i64(env, a[6]),
+                                  i64(env, a[7]), (float)f64(env, a[8])));
+  return undef(env);
+}
+
+static napi_value js_ln_backward(napi_env env, napi_callback_info info) {
+  napi_value a[11];
+  if (!get_args(env, info, 11, a)) return NULL;
+  CHECK_RC(tjh_layer_norm_backward(
+      (const float*)ptr(env, a[0]), (const float*)ptr(env, a[1]), (const float*)ptr(env, a[2]),
+      (const float*)ptr(env, a[3]), (const float*)ptr(env, a[4]), (float*)ptr(env, a[5]),
+      (float*)ptr(env, a[6]), (float*)ptr(env, a[7]), i64(env, a[8]), i64(env, a[9]),
+      (int)i64(env, a[10])));
+  return undef(env);
+}
+
+static napi_value js_emb_forward(napi_env env, napi_callback_info info) {
+  napi_value a[6];
+  if (!get_args(env, info, 6, a)) return NULL;
+  CHECK_RC(tjh_embedding_forward((const float*)ptr(env, a[0]), i64(env, a[1]), i64(env, a[2]),
+                                 (const int32_t*)ptr(env, a[3]), i64(env, a[4]),
+                                 (float*)ptr(env, a[5])));
+  return undef(env);
+}
+
+static napi_value js_emb_backward(napi_env env, napi_callback_info info) {
+  napi_value a[7];
+  if (!get_args(env, info, 7, a)) return NULL;
+  CHECK_RC(tjh_embedding_backward((const float*)ptr(env, a[0]), (const int32_t*)ptr(env, a[1]),
+                                  i64(env, a[2]), i64(env, a[3]), (float*)ptr(env, a[4]),
+                                  i64(env, a[5]), (int)i64(env, a[6])));
+  return undef(env);
+}
+
+/* gemm(transA, transB, M, N, K, alpha, A, lda, sA, B, ldb, sB, beta, C, ldc, sC, batch, bias, biasMode) */
+static napi_value js_gemm(napi_env env, napi_callback_info info) {
+  napi_value a[19];
+  if (!get_args(env, info, 19, a)) return NULL;
+  CHECK_RC(tjh_gemm((int)i64(env, a[0]), (int)i64(env, a[1]), i64(env, a[2]), i64(env, a[3]),
+                    i64(env, a[4]), (float)f64(env, a[5]), (const float*)ptr(env, a[6]),
+                    i64(env, a[7]), i64(env, a[8]), (const float*)ptr(env, a[9]), i64(env, a[10]),
+                    i64(env, a[11]), (float)f64(env, a[12]), (float*)ptr(env, a[13]),
+                    i64(env, a[14]), i64(env, a[15]), i64(env, a[16]),
+                    (const float*)ptr(env, a[17]), (int)i64(env, a[18])));
+  return undef(env);
+}
+
+/* sdpaForward(q, k, v, o, lse, B, H, Tq, Tk, D, qs[3], ks[3], vs[3], os[3], scale, causal) */
+static napi_value js_sdpa_forward(napi_env env, napi_callback_info info) {
+  napi_value a[16];
+  if (!get_args(env, info, 16, a)) return NULL;
+  int64_t qs[3], ks[3], vs[3], os[3];
+  i64arr(env, a[10], qs, 3);
+  i64arr(env, a[11], ks, 3);
+  i64arr(env, a[12], vs, 3);
+  i64arr(env, a[13], os, 3);
+  CHECK_RC(tjh_sdpa_forward((const float*)ptr(env, a[0]), (const float*)ptr(env, a[1]),
+                            (const float*)ptr(env, a[2]), (float*)ptr(env, a[3]),
+                            (float*)ptr(env, a[4]), i64(env, a[5]), i64(env, a[6]), i64(env, a[7]),
+                            i64(env, a[8]), i64(env, a[9]), qs, ks, vs, os, (float)f64(env, a[14]),
+                            (int)i64(env, a[15])));
+  return undef(env);
+}
+
+/* sdpaBackward(q,k,v,o,dO,lse,dq,dk,dv, B,H,Tq,Tk,D, strides[8][3], scale, causal) */
+static napi_value js_sdpa_backward(napi_env env, napi_callback_info info) {
+  napi_value a[17];
+  if (!get_args(env, info, 17, a)) return NULL;
+  int64_t st[8][3];
+  const int64_t* sp[8];
+  for (uint32_t i = 0; i < 8; ++i) {
+    napi_value e;
+    napi_get_element(env, a[14], i, &e);
+    i64arr(env, e, st[i], 3);
+    sp[i] = st[i];
+  }
+  CHECK_RC(tjh_sdpa_backward(
+      (const float*)ptr(env, a[0]), (const float*)ptr(env, a[1]), (const float*)ptr(env, a[2]),
+      (const float*)ptr(env, a[3]), (const float*)ptr(env, a[4]), (const float*)ptr(env, a[5]),
+      (float*)ptr(env, a[6]), (float*)ptr(env, a[7]), (float*)ptr(env, a[8]), i64(env, a[9]),
+      i64(env, a[10]), i64(env, a[11]), i64(env, a[12]), i64(env, a[13]), sp,
+      (float)f64(env, a[15]), (int)i64(env, a[16])));
+  return undef(env);
+}
+
+/* adamStep(params[], grads[], m[], v[], numels[], steps[], lr, b1, b2, eps, wd, decoupled) */
+static napi_value js_adam_step(napi_env env, napi_callback_info info) {
+  napi_value a[12];
+  if (!get_args(env, info, 12, a)) return NULL;
+  uint32_t n = 0;
+  napi_get_array_length(env, a[0], &n);
+  float** p = (float**)calloc(n ? n : 1, sizeof(float*));
+  const float** g = (const float**)calloc(n ? n : 1, sizeof(float*));
+  float** m = (float**)calloc(n ? n : 1, sizeof(float*));
+  float** v = (float**)calloc(n ? n : 1, sizeof(float*));
+  int64_t* ne = (int64_t*)calloc(n ? n : 1, sizeof(int64_t));
+  int64_t* st = (int64_t*)calloc(n ? n : 1, sizeof(int64_t));
+  for (uint32_t i = 0; i < n; ++i) {
+    napi_value e;
+    napi_get_element(env, a[0], i, &e); p[i] = (float*)ptr(env, e);
+    napi_get_element(env, a[1], i, &e); g[i] = (const float*)ptr(env, e);
+    napi_get_element(env, a[2], i, &e); m[i] = (float*)ptr(env, e);
+    napi_get_element(env, a[3], i, &e); v[i] = (float*)ptr(env, e);
+    napi_get_element(env, a[4], i, &e); ne[i] = i64(env, e);
+    napi_get_element(env, a[5], i, &e); st[i] = i64(env, e);
+  }
+  int rc = tjh_adam_step((int)n, p, g, m, v, ne, st, f64(env, a[6]), f64(env, a[7]),
+                         f64(env, a[8]), f64(env, a[9]), f64(env, a[10]), (int)i64(env, a[11]));
+  free(p); free(g); free(m); free(v); free(ne); free(st);
+  if (rc) return throw_last(env, rc);
+  return undef(env);
+}
+
+/* ---------------------------------------------------------------- module */
+
+#define FN(name, fn)                                                              \
+  {name, NULL, fn, NULL, NULL, NULL,                                               \
+   (napi_property_attributes)(napi_writable | napi_enumerable | napi_configurable), \
+   NULL}
+
+static napi_value init_module(napi_env env, napi_value exports) {
+  napi_property_descriptor desc[] = {
+      FN("init", js_init), FN("deviceInfo", js_device_info), FN("malloc", js_malloc),
+      FN("h2d", js_h2d), FN("d2h", js_d2h), FN("d2hAsync", js_d2h_async),
+      FN("synchronize", js_sync), FN("memoryStats", js_memory_stats),
+      FN("emptyCache", js_empty_cache), FN("fill", js_fill), FN("random", js_random),
+      FN("copyStrided", js_copy_strided), FN("unary", js_unary),
+      FN("unaryBackward", js_unary_backward), FN("binary", js_binary), FN("scalar", js_scalar),
+      FN("reduce", js_reduce), FN("softmaxForward", js_softmax_forward),
+      FN("softmaxBackward", js_softmax_backward), FN("crossEntropyForward", js_ce_forward),
+      FN("crossEntropyBackward", js_ce_backward), FN("layerNormForward", js_ln_forward),
+      FN("layerNormBackward", js_ln_backward), FN("embeddingForward", js_emb_forward),
+      FN("embeddingBackward", js_emb_backward), FN("gemm", js_gemm),
+      FN("sdpaForward", js_sdpa_forward), FN("sdpaBackward", js_sdpa_backward),
+      FN("adamStep", js_adam_step),
+  };
+  napi_define_properties(env, exports, sizeof(desc) / sizeof(desc[0]), desc);
+  napi_value v;
+  napi_create_string_utf8(env, tjh_version(), NAPI_AUTO_LENGTH, &v);
+  napi_set_named_property(env, exports, "version", v);
+  return exports;
+}
+
+NAPI_MODULE(NODE_GYP_MODULE_NAME, init_module)
