@@ -11,9 +11,16 @@ Prints ONE JSON line.  `value` = tokens/s over exactly K timed steps
 (inputs resident in HBM, device synchronised on both sides of the timed
 region).  `roofline` reports the dominant kernel family (the MFMA GEMMs of
 the Linear layers) from HIP events recorded on the library stream around
-every launch during the timed steps; `hbm_kernels` reports the
-memory-bound backward kernels the same way.  `cpu_baseline` times the
-oracle (numpy) on a bounded sample of the same workload on the host.
+each of its launches during the timed steps (no other launch is bracketed
+there); `roofline.traffic` is the HBM bytes per launch measured by
+rocprofv3 counters (profiles/gemm_hbm_traffic_gpt2.json).  `hbm_kernels`
+and `kernel_ms_per_step` come from an instrumented pass after the timed
+region that brackets every launch.  `cpu_baseline` times the oracle
+(numpy) on a bounded sample of the same workload on the host.
+
+    python bench.py --copy-mib 1024      # known-size copy for counter scaling
+    python bench.py --summarize-pmc FETCH WRITE COPY_FETCH COPY_WRITE
+        # rocprofv3 --pmc output dirs -> profiles/gemm_hbm_traffic_gpt2.json
 """
 import argparse
 import json
@@ -28,6 +35,8 @@ sys.path.insert(0, ROOT)
 
 METRIC = "GPT-2 124M fwd+bwd+AdamW tokens/s (1 GPU); bwd-kernel HBM GB/s vs peak"
 HBM_PEAK_GBS = 8000.0
+DOMINANT = "gemm"  # kernel family of the Linear-layer GEMMs (k_gemm + split-K reduce)
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemm_hbm_traffic_gpt2.json")
 FP32_MFMA_PEAK_TFLOPS = 157.3
 
 V, CTX, D, H, LAYERS = 50257, 1024, 768, 12, 12
@@ -95,7 +104,8 @@ def run_gpu(steps, warmup):
         loss = step()
         print("warmup %d loss %.4f" % (i, loss.item()), file=sys.stderr, flush=True)
     torch.synchronize()
-    torch.hip.kernel_timing(True)
+    # timed region: only the dominant kernel family is bracketed by events
+    torch.hip.kernel_timing(True, only=DOMINANT)
     torch.hip.kernel_timing_reset()
     torch.synchronize()
     t0 = time.perf_counter()
@@ -104,11 +114,19 @@ def run_gpu(steps, warmup):
     torch.synchronize()
     elapsed = time.perf_counter() - t0
     final_loss = loss.item()
+    dominant = torch.hip.kernel_time(DOMINANT)
+    # instrumented pass after the timed region: every family, for the
+    # per-kernel breakdown (events between all launches cost ~4% of a step)
+    prof_steps = max(1, min(steps, 5))
+    torch.hip.kernel_timing(True)
+    torch.hip.kernel_timing_reset()
+    for _ in range(prof_steps):
+        step()
     fams = torch.hip.kernel_families()
     timing = {f: torch.hip.kernel_time(f) for f in fams}
     torch.hip.kernel_timing(False)
     mem = torch.hip.memory_stats()
-    return elapsed, final_loss, timing, nparams, mem
+    return elapsed, final_loss, dominant, timing, prof_steps, nparams, mem
 
 
 def cpu_baseline():
@@ -134,6 +152,18 @@ def cpu_baseline():
                       "tokens, full 12 layers and 50257 vocab), %.1f s" % dt}
 
 
+def traffic_per_launch():
+    """HBM bytes per launch of the dominant family, from the rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary kept under profiles/ (each counter
+    scaled by what it reads for a plain copy of known size), or None."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)
+        return int(t["hbm_bytes_per_launch"])
+    except (OSError, ValueError, KeyError):
+        return None
+
+
 def copy_calibration(mib):
     """A plain contiguous device copy of `mib` MiB through the library's
     vectorised copy kernel (3 launches): the known-size reference that HBM
@@ -150,6 +180,53 @@ def copy_calibration(mib):
     print(json.dumps({"copy_calibration_bytes": n * 4, "launches": 3}), flush=True)
 
 
+def _pmc_rows(d):
+    import csv
+    import glob
+    rows = []
+    for f in glob.glob(os.path.join(d, "*counter_collection.csv")):
+        with open(f) as fh:
+            rows += list(csv.DictReader(fh))
+    if not rows:
+        raise SystemExit("no counter_collection.csv under %s" % d)
+    return rows
+
+
+def summarize_pmc(fetch_dir, write_dir, copy_fetch_dir, copy_write_dir):
+    """Scales FETCH_SIZE / WRITE_SIZE (KiB per dispatch) of the k_gemm family
+    by what each counter reads for the library's copy kernel moving a known
+    number of bytes, and writes the per-launch HBM bytes.  A launch is one
+    GEMM call, as the library's timing counts it: its interior k_gemm
+    dispatch (template flag EDGE = false) plus any guarded edge-strip
+    dispatches and the split-K reduce.  Every GPT-2 product has one
+    interior dispatch."""
+    def is_gemm(name):
+        return "k_gemm<" in name or "k_splitk_reduce" in name
+
+    def is_copy(name):
+        return "CopyOp" in name and "k_vec<1" in name
+
+    out = {"kernel_family": "k_gemm (+ k_splitk_reduce)"}
+    for cname, d, cd in (("FETCH_SIZE", fetch_dir, copy_fetch_dir),
+                         ("WRITE_SIZE", write_dir, copy_write_dir)):
+        copies = [float(r["Counter_Value"]) for r in _pmc_rows(cd) if is_copy(r["Kernel_Name"])]
+        copy_kib = 1024.0 * 1024.0  # each calibration copy moves 1 GiB each way
+        scale = copy_kib / (sum(copies) / len(copies))
+        rows = [r for r in _pmc_rows(d) if is_gemm(r["Kernel_Name"])]
+        launches = sum(1 for r in rows if "k_gemm<" in r["Kernel_Name"] and
+                       r["Kernel_Name"].split(">")[0].endswith("false"))
+        kib = sum(float(r["Counter_Value"]) for r in rows)
+        out[cname] = {"raw_kib_per_launch": round(kib / launches, 1), "copy_scale": round(scale, 4),
+                      "bytes_per_launch": round(kib / launches * scale * 1024.0),
+                      "launches": launches}
+    out["hbm_bytes_per_launch"] = out["FETCH_SIZE"]["bytes_per_launch"] + \
+        out["WRITE_SIZE"]["bytes_per_launch"]
+    os.makedirs(os.path.dirname(TRAFFIC_FILE), exist_ok=True)
+    with open(TRAFFIC_FILE, "w") as f:
+        json.dump(out, f, indent=1)
+    print(json.dumps(out))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -158,7 +235,12 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="only run the copy-kernel calibration of this many MiB")
+    ap.add_argument("--summarize-pmc", nargs=4, metavar="DIR", default=None,
+                    help="FETCH WRITE COPY_FETCH COPY_WRITE rocprofv3 --pmc output dirs")
     args = ap.parse_args()
+    if args.summarize_pmc:
+        summarize_pmc(*args.summarize_pmc)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one MI355X: this build has no multi-GPU path "
               "(--gpus %d requested)" % args.gpus, file=sys.stderr)
@@ -166,26 +248,30 @@ def main():
     if args.copy_mib:
         copy_calibration(args.copy_mib)
         return
-    elapsed, final_loss, timing, nparams, mem = run_gpu(args.steps, args.warmup)
+    elapsed, final_loss, dominant, timing, prof_steps, nparams, mem = run_gpu(args.steps,
+                                                                              args.warmup)
     tokens = B * T * args.steps
     ms_step = 1000.0 * elapsed / args.steps
-    # dominant kernel: the Linear GEMMs (MFMA)
-    n_g, ms_g = timing.get("gemm", (0, 0.0))
+    # dominant kernel: the Linear GEMMs (MFMA), timed inside the timed region
+    n_g, ms_g = dominant
     flops = linear_flops_per_step(B, T) * args.steps
     achieved = flops / (ms_g / 1000.0) / 1e12 if ms_g else 0.0
-    roofline = {"bound": "mfma", "kernel": "gemm (Linear fwd/dgrad/wgrad, fp32 MFMA)",
+    roofline = {"bound": "mfma", "kernel": "k_gemm family (Linear fwd/dgrad/wgrad + LM head, "
+                "fp32 MFMA, incl. split-K reduce)",
                 "achieved": round(achieved, 2), "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": None,
+                "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": traffic_per_launch(),
                 "launches": n_g, "avg_launch_ms": round(ms_g / max(n_g, 1), 4),
+                "flop_per_launch": round(flops / max(n_g, 1)),
                 "share_of_step": round(ms_g / (ms_step * args.steps), 3)}
     hbm = {}
     for fam, byts in hbm_bytes_per_step(B, T, nparams).items():
         n, ms = timing.get(fam, (0, 0.0))
         if ms:
-            gbs = byts * args.steps / (ms / 1000.0) / 1e9
+            gbs = byts * prof_steps / (ms / 1000.0) / 1e9
             hbm[fam] = {"GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 3),
-                        "ms_per_step": round(ms / args.steps, 3), "launches_per_step": n // args.steps}
-    top = sorted(((ms / args.steps, f) for f, (n, ms) in timing.items()), reverse=True)[:12]
+                        "ms_per_step": round(ms / prof_steps, 3),
+                        "launches_per_step": n // prof_steps}
+    top = sorted(((ms / prof_steps, f) for f, (n, ms) in timing.items()), reverse=True)[:14]
     out = {
         "metric": METRIC, "value": round(tokens / elapsed, 1), "unit": "tokens/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 3),

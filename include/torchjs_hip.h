@@ -120,6 +120,10 @@ int tjh_d2d(void* dst, const void* src, size_t bytes);
 /* ------------------------------------------------------------------ */
 
 int tjh_kprof_enable(int on);
+/* Restricts timing to the family named exactly `family` (NULL or "" =
+ * every family), so a timed region brackets only the launches it reports
+ * and the others run without events between them. */
+int tjh_kprof_filter(const char* family);
 int tjh_kprof_reset(void);
 /* Synchronises, then reports launches and summed event time for every
  * kernel family whose name starts with `family` ("" = all). */

@@ -11,11 +11,16 @@ Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
 import this package, and only as the checker / the timed CPU baseline.
 The 'hip' product path never calls into it.
 
+Parity unpinned: rng's float streams past the integer stage (see
+oracle/rng.py) and the WGSL built-ins' ULP behaviour; every other function
+is pinned by tests/test_oracle.py (golden vectors, the reference's literal
+tests, closed forms, finite differences).
+
 Precision: floating-point work runs in float64 unless a function says it
 emulates the reference's float32 rounding (the Adam/AdamW moments).
 
 Modules
   ops    per-op forward / backward (each cites the reference file:line)
   rng    torch.js's seeded LCG + xorshift32 generator
-  gpt2   GPT-2 / transformer-block / MLP / CNN forward + explicit backward
+  models GPT-2 / transformer-block / MLP / CNN forward + explicit backward
 """

@@ -67,7 +67,10 @@ class hip:
                 "clock_khz": d.clock_khz, "l2_bytes": d.l2_bytes}
 
     @staticmethod
-    def kernel_timing(enable=True):
+    def kernel_timing(enable=True, only=None):
+        """Brackets launches with HIP events on the library stream; `only`
+        restricts the events to one kernel family."""
+        _lib.check(_lib.lib().tjh_kprof_filter((only or "").encode()), "kprof_filter")
         _lib.check(_lib.lib().tjh_kprof_enable(1 if enable else 0), "kprof_enable")
 
     @staticmethod

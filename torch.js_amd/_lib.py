@@ -71,6 +71,7 @@ SIGNATURES = {
     "tjh_d2h": [c_vp, c_vp, c_sz],
     "tjh_d2d": [c_vp, c_vp, c_sz],
     "tjh_kprof_enable": [c_int],
+    "tjh_kprof_filter": [ctypes.c_char_p],
     "tjh_kprof_reset": [],
     "tjh_kprof_query": [ctypes.c_char_p, P_i64, ctypes.POINTER(c_f64)],
     "tjh_kprof_names": [ctypes.c_char_p, c_sz],

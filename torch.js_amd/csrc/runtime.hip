@@ -186,6 +186,7 @@ struct Family {
 struct Prof {
   std::mutex mu;
   bool on = false;
+  std::string only;  // time only this family ("" = every family)
   std::vector<Family> fams;
   std::unordered_map<std::string, int> index;
   std::vector<hipEvent_t> spare;
@@ -227,6 +228,7 @@ KernelScope::KernelScope(const char* family) : slot(-1), start(nullptr) {
   Prof& P = prof();
   if (!P.on) return;
   std::lock_guard<std::mutex> lk(P.mu);
+  if (!P.only.empty() && P.only != family) return;
   auto it = P.index.find(family);
   if (it == P.index.end()) {
     P.fams.push_back(Family{family, {}, 0, 0.0});
@@ -409,6 +411,13 @@ int tjh_kprof_enable(int on) {
   Prof& P = prof();
   std::lock_guard<std::mutex> lk(P.mu);
   P.on = on != 0;
+  return TJH_OK;
+}
+
+int tjh_kprof_filter(const char* family) {
+  Prof& P = prof();
+  std::lock_guard<std::mutex> lk(P.mu);
+  P.only = family ? family : "";
   return TJH_OK;
 }
 
