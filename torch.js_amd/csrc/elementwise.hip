@@ -103,7 +103,7 @@ bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 int grid_for(int64_t work_items) {
   int64_t g = cdiv(work_items, kBlock);
-  int64_t cap = (int64_t)num_cus() * 16;
+  int64_t cap = (int64_t)num_cus() * 32;
   if (cap < 1) cap = 1024;
   if (g > cap) g = cap;
   if (g < 1) g = 1;
@@ -322,27 +322,44 @@ struct CopyOp {
 
 // Vectorised kernel over a 1-D/2-D layout with contiguous output.
 // NIN inputs of kinds KA, KB, KC; n elements, C = row length (2-D kinds).
+// Each lane handles kUnroll float4 per step, all loads issued before any
+// store, so a workgroup keeps kUnroll x 4 KiB per input in flight.
+constexpr int kUnroll = 4;
+
 template <int NIN, int KA, int KB, int KC, class F>
 __global__ __launch_bounds__(kBlock) void k_vec(
     const float* __restrict__ a, const float* __restrict__ b,
     const float* __restrict__ c, float* __restrict__ out, uint32_t n,
     uint32_t C, F f) {
-  uint32_t n4 = n >> 2;
-  uint32_t gid = blockIdx.x * blockDim.x + threadIdx.x;
-  uint32_t stride = gridDim.x * blockDim.x;
-  for (uint32_t v = gid; v < n4; v += stride) {
-    uint32_t i = v << 2;
-    float4 xa = ld4<KA>(a, i, C);
-    float4 xb = NIN > 1 ? ld4<KB>(b, i, C) : xa;
-    float4 xc = NIN > 2 ? ld4<KC>(c, i, C) : xa;
-    float4 r;
-    r.x = f(xa.x, xb.x, xc.x);
-    r.y = f(xa.y, xb.y, xc.y);
-    r.z = f(xa.z, xb.z, xc.z);
-    r.w = f(xa.w, xb.w, xc.w);
-    *reinterpret_cast<float4*>(out + i) = r;
+  const uint32_t n4 = n >> 2;
+  const uint32_t stride = gridDim.x * blockDim.x * kUnroll;
+  for (uint32_t v0 = blockIdx.x * blockDim.x * kUnroll + threadIdx.x; v0 < n4; v0 += stride) {
+    float4 xa[kUnroll], xb[kUnroll], xc[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const uint32_t v = v0 + u * blockDim.x;
+      if (v < n4) {
+        const uint32_t i = v << 2;
+        xa[u] = ld4<KA>(a, i, C);
+        xb[u] = NIN > 1 ? ld4<KB>(b, i, C) : xa[u];
+        xc[u] = NIN > 2 ? ld4<KC>(c, i, C) : xa[u];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const uint32_t v = v0 + u * blockDim.x;
+      if (v < n4) {
+        float4 r;
+        r.x = f(xa[u].x, xb[u].x, xc[u].x);
+        r.y = f(xa[u].y, xb[u].y, xc[u].y);
+        r.z = f(xa[u].z, xb[u].z, xc[u].z);
+        r.w = f(xa[u].w, xb[u].w, xc[u].w);
+        *reinterpret_cast<float4*>(out + (v << 2)) = r;
+      }
+    }
   }
-  uint32_t tail = n - (n4 << 2);
+  const uint32_t gid = blockIdx.x * blockDim.x + threadIdx.x;
+  const uint32_t tail = n - (n4 << 2);
   if (gid < tail) {
     uint32_t i = (n4 << 2) + gid;
     float xa = ld1<KA>(a, i, C);
@@ -402,7 +419,7 @@ template <int NIN, int KA, int KB, int KC, class F>
 void launch_vec_kinds(const float* a, const float* b, const float* c, float* out,
                       int64_t n, int64_t C, bool vec, F f) {
   if (vec) {
-    int g = grid_for(cdiv(n, 4));
+    int g = grid_for(cdiv(n, 4 * kUnroll));
     hipLaunchKernelGGL((k_vec<NIN, KA, KB, KC, F>), dim3(g), dim3(kBlock), 0,
                        stream(), a, b, c, out, (uint32_t)n, (uint32_t)C, f);
   } else {
@@ -533,9 +550,12 @@ __global__ __launch_bounds__(kBlock) void k_fill(T* __restrict__ out, int64_t n,
 }
 
 __global__ __launch_bounds__(kBlock) void k_fill4(float4* __restrict__ out, int64_t n4, float v) {
-  int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  float4 q = make_float4(v, v, v, v);
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride) out[i] = q;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x * kUnroll;
+  const float4 q = make_float4(v, v, v, v);
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x * kUnroll + threadIdx.x; i < n4; i += stride)
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u)
+      if (i + u * blockDim.x < n4) out[i + u * blockDim.x] = q;
 }
 
 __device__ __forceinline__ uint32_t xorshift32(uint32_t x) {
@@ -639,7 +659,7 @@ int tjh_fill_f32(float* out, int64_t n, float value) {
   if (n == 0) return TJH_OK;
   KernelScope ks("fill");
   if (aligned16(out) && n % 4 == 0) {
-    hipLaunchKernelGGL(k_fill4, dim3(grid_for(n / 4)), dim3(kBlock), 0, stream(),
+    hipLaunchKernelGGL(k_fill4, dim3(grid_for(cdiv(n / 4, kUnroll))), dim3(kBlock), 0, stream(),
                        reinterpret_cast<float4*>(out), n / 4, value);
   } else {
     hipLaunchKernelGGL(k_fill<float>, dim3(grid_for(n)), dim3(kBlock), 0, stream(), out, n, value);

@@ -507,12 +507,19 @@ int tjh::gemm(const char* family, int transA, int transB, int64_t M, int64_t N, 
   if (Mm > 0 && Nm > 0)
     rc = run_block(plan.tile, sub(gk, transA, transB, 0, Mm, 0, Nm, 0, Km), transA, transB,
                    plan.splits, batch, false, cus);
-  if (rc == TJH_OK && Nm < N)  // right strip (all rows)
-    rc = run_block(plan.tile, sub(gk, transA, transB, 0, M, Nm, N - Nm, 0, Km), transA, transB,
-                   1, batch, true, cus);
-  if (rc == TJH_OK && Mm < M && Nm > 0)  // bottom strip (interior columns)
-    rc = run_block(plan.tile, sub(gk, transA, transB, Mm, M - Mm, 0, Nm, 0, Km), transA, transB,
-                   1, batch, true, cus);
+  // Edge strips pick their own tile and K split: a thin strip of a long-K
+  // product (the 81 leftover rows of a 50257-row weight gradient) would
+  // otherwise run on a dozen workgroups for the whole K range.
+  if (rc == TJH_OK && Nm < N) {  // right strip (all rows)
+    const Plan ps = choose_plan(M, N - Nm, Km, batch, cus, transA, transB);
+    rc = run_block(ps.tile, sub(gk, transA, transB, 0, M, Nm, N - Nm, 0, Km), transA, transB,
+                   ps.splits, batch, true, cus);
+  }
+  if (rc == TJH_OK && Mm < M && Nm > 0) {  // bottom strip (interior columns)
+    const Plan ps = choose_plan(M - Mm, Nm, Km, batch, cus, transA, transB);
+    rc = run_block(ps.tile, sub(gk, transA, transB, Mm, M - Mm, 0, Nm, 0, Km), transA, transB,
+                   ps.splits, batch, true, cus);
+  }
   if (rc == TJH_OK && Kr > 0) {
     GemmArgs gr = sub(g, transA, transB, 0, M, 0, N, Km, Kr);
     gr.beta = 1.0f;

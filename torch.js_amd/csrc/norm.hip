@@ -14,7 +14,7 @@
 // whose stride is odd (ld = 50257) peel a scalar prefix up to the next
 // 16-byte boundary, stream float4s, and finish with a scalar tail.
 
-#include "common.h"
+#include "colsum.h"
 
 #include <float.h>
 
@@ -732,10 +732,10 @@ int tjh_layer_norm_backward(const float* dy, const float* x, const float* gamma,
              (!gamma || aligned16(gamma));
   int v4 = cols <= 64 * 4 * 3 ? 3 : (cols <= 64 * 4 * 6 ? 6 : (cols <= 64 * 4 * 12 ? 12 : 0));
   if (vec && v4) {
-    // rows per block: ~2 blocks per CU, >= 16 rows each (fewer partials)
+    // rows per block: ~4 blocks per CU, >= 8 rows each
     int cus = num_cus() > 0 ? num_cus() : 256;
-    int64_t rpb = cdiv(rows, 2LL * cus);
-    if (rpb < 16) rpb = 16;
+    int64_t rpb = cdiv(rows, 4LL * cus);
+    if (rpb < 8) rpb = 8;
     int64_t nb = cdiv(rows, rpb);
     Scratch part(want_p ? (size_t)(2 * nb * cols) * sizeof(float) : 0);
     if (want_p && !part.ok()) return set_error(TJH_ERR_OOM, "layer_norm_backward: no scratch");
@@ -754,8 +754,14 @@ int tjh_layer_norm_backward(const float* dy, const float* x, const float* gamma,
                            gamma, mean, rstd, dx, pg, pb, rows, cols, rpb);
       int rc = check_launch("layer_norm_backward");
       if (rc != TJH_OK) return rc;
+      if (want_p) {
+        // dgamma and dbeta from the per-workgroup partial rows, one launch
+        float* parts[2] = {pg, pb};
+        float* outs[2] = {dgamma, dbeta};
+        rc = colsum_final(parts, outs, 2, nb, cols, accumulate, 1.0f);
+        if (rc != TJH_OK) return rc;
+      }
     }
-    if (want_p) return sum_partials(pg, pb, nb, cols, dgamma, dbeta, accumulate);
     return TJH_OK;
   }
   // general path: partials per row, then column sums

@@ -16,7 +16,7 @@
 // Split reductions write partials and finish with a second pass.  Every
 // split point and combine order is fixed, so results are deterministic.
 
-#include "common.h"
+#include "colsum.h"
 
 #include <float.h>
 
@@ -145,6 +145,95 @@ __global__ __launch_bounds__(kBlock) void k_reduce_cols(const float* __restrict_
   }
 }
 
+// Column sums of x viewed [outer][r][inner]: workgroup (b, o) sums rows
+// [b*rchunk, (b+1)*rchunk) of every column of o (compensated) into the
+// partial row part[o][b]; colsum_final adds the partial rows.
+template <bool VEC>
+__global__ __launch_bounds__(kBlock) void k_colsum(const float* __restrict__ x, int64_t r,
+                                                   int64_t inner, int64_t rchunk,
+                                                   float* __restrict__ part) {
+  const int64_t o = blockIdx.y;
+  const int64_t nb = gridDim.x, b = blockIdx.x;
+  const float* __restrict__ base = x + o * r * inner;
+  const int64_t r0 = b * rchunk, r1 = r0 + rchunk < r ? r0 + rchunk : r;
+  float* __restrict__ prow = part + (o * nb + b) * inner;
+  // rows are fetched kBatch at a time before they are accumulated, so the
+  // loads of a batch are in flight together
+  if (VEC) {
+    for (int64_t c4 = threadIdx.x; c4 * 4 < inner; c4 += kBlock) {
+      Kahan kx, ky, kz, kw;
+      const float4* __restrict__ col = reinterpret_cast<const float4*>(base + c4 * 4);
+      const int64_t st = inner / 4;
+      for (int64_t k = r0; k < r1; k += kBatch) {
+        float4 v[kBatch];
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u)
+          v[u] = k + u < r1 ? col[(k + u) * st] : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+          kx.add(v[u].x); ky.add(v[u].y); kz.add(v[u].z); kw.add(v[u].w);
+        }
+      }
+      *reinterpret_cast<float4*>(prow + c4 * 4) = make_float4(kx.s, ky.s, kz.s, kw.s);
+    }
+  } else {
+    for (int64_t cc = threadIdx.x; cc < inner; cc += kBlock) {
+      Kahan kc;
+      for (int64_t k = r0; k < r1; k += kBatch) {
+        float v[kBatch];
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) v[u] = k + u < r1 ? base[(k + u) * inner + cc] : 0.f;
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) kc.add(v[u]);
+      }
+      prow[cc] = kc.s;
+    }
+  }
+}
+
+// Final pass: workgroup (x, i) owns 64 columns of output i; wave w of 16
+// sums partial rows w, w+16, ... (compensated, fetched kBatch at a time)
+// and the 16 wave sums are added in wave order.
+constexpr int kFinalWaves = 16;
+
+struct FinalArgs {
+  const float* part[kFinalMax];
+  float* out[kFinalMax];
+};
+
+__global__ __launch_bounds__(64 * kFinalWaves) void k_colsum_final(FinalArgs fa, int64_t nb,
+                                                                   int64_t cols, int accumulate,
+                                                                   float scale) {
+  __shared__ float red[kFinalWaves][64];
+  const int i = blockIdx.y;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t c = (int64_t)blockIdx.x * 64 + lane;
+  float* __restrict__ out = fa.out[i];
+  const float* __restrict__ p = fa.part[i];
+  Kahan k;
+  if (c < cols) {
+    for (int64_t b = w; b < nb; b += kFinalWaves * kBatch) {
+      float v[kBatch];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const int64_t bb = b + (int64_t)u * kFinalWaves;
+        v[u] = bb < nb ? p[bb * cols + c] : 0.f;
+      }
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) k.add(v[u]);
+    }
+  }
+  red[w][lane] = k.s;
+  __syncthreads();
+  if (w == 0 && c < cols) {
+    float s = 0.f;
+#pragma unroll
+    for (int q = 0; q < kFinalWaves; ++q) s += red[q][lane];
+    s *= scale;
+    out[c] = accumulate ? out[c] + s : s;
+  }
+}
+
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 template <int OP>
@@ -186,9 +275,50 @@ int reduce_rows(const float* x, int64_t outer, int64_t r, float* out, float scal
   return reduce_rows<OP>(part, outer, splits, out, scale);
 }
 
+// SUM / MEAN over the middle axis: partial rows (k_colsum), then their
+// fixed-order sum (colsum_final).
+int colsum_launch(const float* x, int64_t outer, int64_t r, int64_t inner, float* out,
+                  float scale) {
+  const int cus = num_cus() > 0 ? num_cus() : 256;
+  const bool vec = aligned16(x) && (inner % 4) == 0;
+  const int64_t col_waves = cdiv(vec ? inner / 4 : inner, kBlock);
+  // ~2 workgroups per CU in total, >= 16 rows each
+  int64_t nb = cdiv(2LL * cus, outer * col_waves);
+  if (nb > cdiv(r, 16)) nb = cdiv(r, 16);
+  if (nb < 1) nb = 1;
+  const int64_t rchunk = cdiv(r, nb);
+  nb = cdiv(r, rchunk);
+  Scratch part((size_t)(outer * nb * inner) * sizeof(float));
+  if (!part.ok()) return set_error(TJH_ERR_OOM, "reduce: no scratch memory");
+  dim3 grid((unsigned)nb, (unsigned)outer);
+  if (vec)
+    hipLaunchKernelGGL(k_colsum<true>, grid, dim3(kBlock), 0, stream(), x, r, inner, rchunk,
+                       part.as<float>());
+  else
+    hipLaunchKernelGGL(k_colsum<false>, grid, dim3(kBlock), 0, stream(), x, r, inner, rchunk,
+                       part.as<float>());
+  int rc = check_launch("reduce_colsum");
+  if (rc != TJH_OK) return rc;
+  // the [outer][nb][inner] partials are outer*inner columns of nb rows only
+  // when outer == 1; otherwise finish each o separately
+  for (int64_t o = 0; o < outer && rc == TJH_OK; o += kFinalMax) {
+    float* parts[kFinalMax];
+    float* outs[kFinalMax];
+    const int np = (int)(outer - o < kFinalMax ? outer - o : kFinalMax);
+    for (int i = 0; i < np; ++i) {
+      parts[i] = part.as<float>() + (o + i) * nb * inner;
+      outs[i] = out + (o + i) * inner;
+    }
+    rc = colsum_final(parts, outs, np, nb, inner, 0, scale);
+  }
+  return rc;
+}
+
 template <int OP>
 int reduce_cols(const float* x, int64_t outer, int64_t r, int64_t inner, float* out,
                 float scale) {
+  if ((OP == TJH_REDUCE_SUM || OP == TJH_REDUCE_MEAN) && outer <= 64 && r >= 64)
+    return colsum_launch(x, outer, r, inner, out, scale);
   int cus = num_cus() > 0 ? num_cus() : 256;
   bool vec = aligned16(x) && aligned16(out) && (inner % 4) == 0;
   int64_t lanes = vec ? inner / 4 : inner;
@@ -287,6 +417,24 @@ __global__ __launch_bounds__(kBlock) void k_argmax_cols(const float* __restrict_
 }
 
 }  // namespace
+
+int colsum_final(float* const* part, float* const* out, int np, int64_t nb, int64_t cols,
+                 int accumulate, float scale) {
+  TJH_ARG(np >= 1 && np <= kFinalMax, "colsum_final: %d outputs", np);
+  FinalArgs fa{};
+  int used = 0;
+  for (int i = 0; i < np; ++i) {
+    if (!out[i]) continue;
+    fa.part[used] = part[i];
+    fa.out[used] = out[i];
+    ++used;
+  }
+  if (used == 0) return TJH_OK;
+  hipLaunchKernelGGL(k_colsum_final, dim3((unsigned)cdiv(cols, 64), (unsigned)used),
+                     dim3(64 * kFinalWaves), 0, stream(), fa, nb, cols, accumulate, scale);
+  return check_launch("colsum_final");
+}
+
 }  // namespace tjh
 
 using namespace tjh;

@@ -49,6 +49,7 @@ static int g_cus = 0;
 static hipStream_t g_stream = nullptr;
 
 hipStream_t stream() { return g_stream; }
+
 bool initialized() { return g_init; }
 int device_ordinal() { return g_ordinal; }
 int num_cus() { return g_cus; }
