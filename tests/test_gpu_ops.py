@@ -451,6 +451,41 @@ def test_sdpa_flash_gpt2_layout(torch, T, causal):
     check(gqkv, np.concatenate([un(gq), un(gk), un(gv)], -1), rtol=1e-4, atol=1e-4)
 
 
+def test_split_and_narrow_gradients(torch):
+    """Pieces of a split that are unused, overlapping narrows and a reused
+    piece: the input gradient is the sum over every use (zero elsewhere)."""
+    x = f32(np.random.default_rng(11).normal(size=(3, 10, 6)))
+    t = torch.tensor(x, requires_grad=True)
+    a, b, c = t.split([3, 5, 2], dim=1)
+    n1 = t.narrow(1, 2, 4)  # overlaps a and b
+    loss = (a * 2.0).sum() + (b * b).sum() + (n1 * 3.0).sum() + a.sum()  # c unused, a twice
+    loss.backward()
+    want = np.zeros(x.shape)
+    want[:, 0:3] += 3.0
+    want[:, 3:8] += 2.0 * x[:, 3:8]
+    want[:, 2:6] += 3.0
+    check(t.grad.numpy(), want, **EW)
+    # a split whose pieces all flow back tiles the input exactly
+    t2 = torch.tensor(x, requires_grad=True)
+    p, q, r = t2.split(2, dim=2)
+    ((p * 1.0) + (q * 2.0) + (r * 3.0)).sum().backward()
+    check(t2.grad.numpy(), np.repeat([[[1.0, 1.0, 2.0, 2.0, 3.0, 3.0]]], 3, 0).repeat(10, 1), **EW)
+
+
+def test_sdpa_self_attention_same_tensor(torch):
+    """q = k = v (one tensor used three times): the three gradients must add."""
+    r = np.random.default_rng(16)
+    B, H, T, D = 2, 3, 40, 64
+    x = f32(r.standard_normal((B, H, T, D)))
+    out, g, (gx,) = grad_of(torch, lambda t: torch.F.scaled_dot_product_attention(
+        t, t, t, is_causal=True), x)
+    xd = x.astype(np.float64)
+    o, _ = ops.sdpa(xd, xd, xd, True)
+    check(out, o, rtol=1e-4, atol=1e-5)
+    gq, gk, gv = ops.sdpa_backward(g.astype(np.float64), xd, xd, xd, True)
+    check(gx, gq + gk + gv, rtol=1e-4, atol=1e-4)
+
+
 def test_sdpa_attn_mask_raises(torch):
     q = torch.zeros(1, 1, 2, 4)
     with pytest.raises(NotImplementedError, match="attn_mask not yet implemented"):

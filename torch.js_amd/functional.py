@@ -413,13 +413,46 @@ def scaled_dot_product_attention(query, key, value, attn_mask=None, dropout_p=0.
         buf = empty((Bx, Tx, Hx, Dx))
         return _alias(buf, t.shape, (Tx * Hx * Dx, Dx, Hx * Dx, 1), 0)
 
+    def shared_grads():
+        """dq, dk, dv laid out exactly like q, k, v inside one new buffer when
+        the three are equally strided, disjoint views of one allocation (the
+        fused qkv projection split into heads): the gradient of that
+        projection's output is then that buffer, assembled with no copy."""
+        ts = (q, k, v)
+        if not all(t._storage is q._storage and t._strides == q._strides and
+                   t.shape == q.shape for t in ts):
+            return None
+        # innermost dense run of the layout: each view is a set of runs of
+        # length `run` at offset + multiples of `period`
+        dims = sorted((st, n) for st, n in zip(q._strides, q.shape) if n > 1)
+        run, i = 1, 0
+        while i < len(dims) and dims[i][0] == run:
+            run *= dims[i][1]
+            i += 1
+        outer = [st for st, _ in dims[i:]]
+        if not outer:
+            return None
+        period = min(outer)
+        if run > period or any(st % period for st in outer):
+            return None
+        res = sorted(t._offset % period for t in ts)
+        gaps = [res[1] - res[0], res[2] - res[1], period - (res[2] - res[0])]
+        if min(gaps) < run:
+            return None  # the views share elements
+        ext = [t._offset + sum((n - 1) * st for n, st in zip(t.shape, t._strides)) + 1
+               for t in ts]
+        lo = min(t._offset for t in ts)
+        buf = empty((max(ext) - lo,))
+        return [_alias(buf, t.shape, t._strides, t._offset - lo) for t in ts]
+
     def bwd(g):
         if three:
             g = _alias(g, (g.shape[0], 1) + g.shape[1:], (g._strides[0], 0) + g._strides[1:],
                        g._offset)
         if g._strides[3] != 1:
             g = _k_contiguous(g)
-        dq, dk, dv = grad_like(q), grad_like(k), grad_like(v)
+        shared = shared_grads()
+        dq, dk, dv = shared if shared else (grad_like(q), grad_like(k), grad_like(v))
         arrs = [L.i64arr(t._strides[:3]) for t in (q, k, v, o, g, dq, dk, dv)]
         ptrs = (L.P_i64 * 8)(*[ctypes.cast(a, L.P_i64) for a in arrs])
         L.check(L.lib().tjh_sdpa_backward(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),

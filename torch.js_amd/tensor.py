@@ -1430,13 +1430,7 @@ def narrow(x, dim, start, length):
     shape = x.shape[:d] + (length,) + x.shape[d + 1:]
     out = _alias(x, shape, x._strides, x._offset + start * x._strides[d])
     xs = x.shape
-
-    def bwd(g):
-        z = zeros(xs)
-        dst = _alias(z, g.shape, z._strides, start * z._strides[d])
-        _copy_into(dst, g)
-        return [z]
-    return _record(out, "Narrow", [x], bwd)
+    return _record(out, "Narrow", [x], lambda g: [_SliceGrad(xs, d, [(start, g)])])
 
 
 def select(x, dim, index):
@@ -1791,9 +1785,72 @@ _add_unary_methods()
 # ----------------------------------------------------------------- engine
 
 
+class _SliceGrad:
+    """Gradient of a narrow()/split() output w.r.t. the full input, kept as
+    (start, tensor) pieces along `dim` until the input's own node runs.  The
+    pieces of one split are then assembled in one go: with no zero fill
+    when they tile the input, and with no copy at all when they already sit
+    at their places in one buffer (attention's backward writes dq, dk, dv
+    into the layout of the fused qkv projection)."""
+
+    __slots__ = ("shape", "dim", "pieces")
+
+    def __init__(self, shape, dim, pieces):
+        self.shape = tuple(shape)
+        self.dim = dim
+        self.pieces = pieces
+
+    def merge(self, other):
+        return _SliceGrad(self.shape, self.dim, self.pieces + other.pieces)
+
+    def materialize(self):
+        d, n = self.dim, self.shape[self.dim]
+        pieces = sorted(self.pieces, key=lambda p: p[0])
+        pos, tiles = 0, True
+        for start, g in pieces:
+            if start != pos:
+                tiles = False
+                break
+            pos += g.shape[d]
+        tiles = tiles and pos == n
+        if tiles:
+            # one buffer already holding every piece at its place?
+            g0 = pieces[0][1]
+            st = _contig_strides(self.shape)
+            base = g0._offset
+            if all(g._storage is g0._storage and tuple(g._strides) == st and
+                   g._offset == base + start * st[d] and g._dtype == g0._dtype
+                   for start, g in pieces):
+                return Tensor(g0._storage, self.shape, st, base, g0._dtype)
+            out = empty(self.shape, dtype=g0._dtype)
+        else:
+            out = zeros(self.shape, dtype=pieces[0][1]._dtype)
+        covered = [False] * n
+        for start, g in pieces:
+            ln = g.shape[d]
+            dst = _alias(out, g.shape, out._strides, out._offset + start * out._strides[d])
+            if any(covered[start:start + ln]):
+                _copy_into(dst, _k_binary("add", dst, g))  # overlapping narrows add up
+            else:
+                _copy_into(dst, g)
+            for i in range(start, start + ln):
+                covered[i] = True
+        return out
+
+
+def _dense(g):
+    return g.materialize() if isinstance(g, _SliceGrad) else g
+
+
 def _accumulate(store, key, g):
     prev = store.get(key)
-    store[key] = g if prev is None else _k_binary("add", prev, g)
+    if prev is None:
+        store[key] = g
+    elif (isinstance(prev, _SliceGrad) and isinstance(g, _SliceGrad) and
+          prev.shape == g.shape and prev.dim == g.dim):
+        store[key] = prev.merge(g)
+    else:
+        store[key] = _k_binary("add", _dense(prev), _dense(g))
 
 
 def _toposort(roots):
@@ -1844,7 +1901,7 @@ def run_backward(pairs, retain_graph=False, inputs=None):
             roots.append(t.grad_fn)
         order = _toposort(roots)
         for node in reversed(order):
-            g = grads.pop(id(node), None)
+            g = _dense(grads.pop(id(node), None))
             if g is None:
                 continue
             if node.fn is None:
@@ -1855,6 +1912,9 @@ def run_backward(pairs, retain_graph=False, inputs=None):
             for t, gi in zip(node.inputs, in_grads):
                 if t is None or gi is None:
                     continue
+                if isinstance(gi, _SliceGrad) and (t.grad_fn is None or t._retains_grad or
+                                                   (wanted is not None and id(t) in wanted)):
+                    gi = gi.materialize()
                 if tuple(gi.shape) != t.shape:
                     gi = _sum_to(gi, t.shape) if gi.ndim >= t.ndim else reshape_raw(gi, t.shape)
                 if wanted is not None and id(t) in wanted:
@@ -1871,7 +1931,7 @@ def run_backward(pairs, retain_graph=False, inputs=None):
                 node.fn = None
                 node.inputs = [None] * len(node.inputs)
         if wanted is not None:
-            return [results.get(id(t)) for t in inputs]
+            return [_dense(results.get(id(t))) for t in inputs]
         return None
     finally:
         _grad["enabled"] = prev
