@@ -58,6 +58,8 @@ __device__ __forceinline__ MS wave_ms(MS v) {
 
 // Calls f(index, value) for every element of row[0..n) with 128-bit loads
 // in the aligned middle.  `lane`/`nl` describe the participating lanes.
+constexpr int kRowUnroll = 4;
+
 template <class F>
 __device__ __forceinline__ void row_scan(const float* __restrict__ row, int64_t n, int lane,
                                          int nl, F&& f) {
@@ -67,13 +69,25 @@ __device__ __forceinline__ void row_scan(const float* __restrict__ row, int64_t 
   for (int64_t i = lane; i < pre; i += nl) f(i, row[i]);
   int64_t n4 = (n - pre) / 4;
   const float4* p4 = reinterpret_cast<const float4*>(row + pre);
-  for (int64_t i = lane; i < n4; i += nl) {
-    float4 v = p4[i];
-    int64_t b = pre + 4 * i;
-    f(b, v.x);
-    f(b + 1, v.y);
-    f(b + 2, v.z);
-    f(b + 3, v.w);
+  // kRowUnroll float4 per lane are loaded before any is consumed
+  for (int64_t i0 = lane; i0 < n4; i0 += (int64_t)nl * kRowUnroll) {
+    float4 v[kRowUnroll];
+#pragma unroll
+    for (int u = 0; u < kRowUnroll; ++u) {
+      const int64_t i = i0 + (int64_t)u * nl;
+      if (i < n4) v[u] = p4[i];
+    }
+#pragma unroll
+    for (int u = 0; u < kRowUnroll; ++u) {
+      const int64_t i = i0 + (int64_t)u * nl;
+      if (i < n4) {
+        const int64_t b = pre + 4 * i;
+        f(b, v[u].x);
+        f(b + 1, v[u].y);
+        f(b + 2, v[u].z);
+        f(b + 3, v[u].w);
+      }
+    }
   }
   for (int64_t i = pre + 4 * n4 + lane; i < n; i += nl) f(i, row[i]);
 }
@@ -232,17 +246,29 @@ __global__ __launch_bounds__(kBlock) void k_ce_bwd(const float* __restrict__ x, 
   int64_t n4 = (cols - pre) / 4;
   float4* d4 = reinterpret_cast<float4*>(dr + pre);
   bool xal = (((uintptr_t)(xr + pre)) & 15) == 0;
-  for (int64_t i = lane; i < n4; i += nl) {
-    int64_t b = pre + 4 * i;
-    float4 xv;
-    if (xal) xv = *reinterpret_cast<const float4*>(xr + b);
-    else xv = make_float4(xr[b], xr[b + 1], xr[b + 2], xr[b + 3]);
-    float4 o = make_float4(val(b, xv.x), val(b + 1, xv.y), val(b + 2, xv.z), val(b + 3, xv.w));
-    if (accumulate) {
-      float4 q = d4[i];
-      o.x += q.x; o.y += q.y; o.z += q.z; o.w += q.w;
+  for (int64_t i0 = lane; i0 < n4; i0 += (int64_t)nl * kRowUnroll) {
+    float4 xv[kRowUnroll];
+#pragma unroll
+    for (int u = 0; u < kRowUnroll; ++u) {
+      const int64_t i = i0 + (int64_t)u * nl, b = pre + 4 * i;
+      if (i < n4) {
+        if (xal) xv[u] = ld_nt(xr + b);
+        else xv[u] = make_float4(xr[b], xr[b + 1], xr[b + 2], xr[b + 3]);
+      }
     }
-    d4[i] = o;
+#pragma unroll
+    for (int u = 0; u < kRowUnroll; ++u) {
+      const int64_t i = i0 + (int64_t)u * nl, b = pre + 4 * i;
+      if (i < n4) {
+        float4 o = make_float4(val(b, xv[u].x), val(b + 1, xv[u].y), val(b + 2, xv[u].z),
+                               val(b + 3, xv[u].w));
+        if (accumulate) {
+          float4 q = d4[i];
+          o.x += q.x; o.y += q.y; o.z += q.z; o.w += q.w;
+        }
+        d4[i] = o;
+      }
+    }
   }
   for (int64_t i = pre + 4 * n4 + lane; i < cols; i += nl) {
     float v = val(i, xr[i]);
@@ -422,41 +448,67 @@ __global__ __launch_bounds__(kBlock) void k_ln_bwd_wave(const float* __restrict_
   const float inv_n = 1.0f / (float)cols;
   int64_t r_beg = (int64_t)blockIdx.x * rpb;
   int64_t r_end = r_beg + rpb < rows ? r_beg + rpb : rows;
-  for (int64_t r = r_beg + w; r < r_end; r += kBlock / 64) {
-    const float4* g4 = reinterpret_cast<const float4*>(dy + r * cols);
-    const float4* x4 = reinterpret_cast<const float4*>(x + r * cols);
-    const float mu = mean[r], rs = rstd[r];
-    float4 gv[V4], xh[V4];
-    float s1 = 0.f, s2 = 0.f;
+  // two rows per wave per step: both rows' loads are issued before either
+  // row's reductions
+  constexpr int kPair = 2;
+  constexpr int kStep = kBlock / 64;
+  for (int64_t r0 = r_beg + w; r0 < r_end; r0 += kStep * kPair) {
+    float4 gv[kPair][V4], xh[kPair][V4];
+    float mu[kPair], rs[kPair];
 #pragma unroll
-    for (int j = 0; j < V4; ++j) {
-      int i = lane + 64 * j;
-      if (i < c4) {
-        float4 g = g4[i], xv = x4[i];
-        xh[j] = make_float4((xv.x - mu) * rs, (xv.y - mu) * rs, (xv.z - mu) * rs, (xv.w - mu) * rs);
-        gv[j] = g;
-        float4 gg = make_float4(g.x * gm[j].x, g.y * gm[j].y, g.z * gm[j].z, g.w * gm[j].w);
-        s1 += (gg.x + gg.y) + (gg.z + gg.w);
-        s2 += (gg.x * xh[j].x + gg.y * xh[j].y) + (gg.z * xh[j].z + gg.w * xh[j].w);
-        ag[j].x += g.x * xh[j].x; ag[j].y += g.y * xh[j].y;
-        ag[j].z += g.z * xh[j].z; ag[j].w += g.w * xh[j].w;
-        ab[j].x += g.x; ab[j].y += g.y; ab[j].z += g.z; ab[j].w += g.w;
+    for (int q = 0; q < kPair; ++q) {
+      const int64_t r = r0 + q * kStep;
+      if (r < r_end) {
+        const float4* g4 = reinterpret_cast<const float4*>(dy + r * cols);
+        const float4* x4 = reinterpret_cast<const float4*>(x + r * cols);
+        mu[q] = mean[r];
+        rs[q] = rstd[r];
+#pragma unroll
+        for (int j = 0; j < V4; ++j) {
+          const int i = lane + 64 * j;
+          if (i < c4) {
+            gv[q][j] = ld_nt(reinterpret_cast<const float*>(g4 + i));
+            xh[q][j] = ld_nt(reinterpret_cast<const float*>(x4 + i));
+          }
+        }
       }
     }
-    s1 = wave_sum(s1) * inv_n;
-    s2 = wave_sum(s2) * inv_n;
-    if (dx) {
-      float4* d4 = reinterpret_cast<float4*>(dx + r * cols);
+#pragma unroll
+    for (int q = 0; q < kPair; ++q) {
+      const int64_t r = r0 + q * kStep;
+      if (r >= r_end) continue;  // wave-uniform
+      float s1 = 0.f, s2 = 0.f;
 #pragma unroll
       for (int j = 0; j < V4; ++j) {
-        int i = lane + 64 * j;
+        const int i = lane + 64 * j;
         if (i < c4) {
-          float4 o;
-          o.x = rs * (gv[j].x * gm[j].x - s1 - xh[j].x * s2);
-          o.y = rs * (gv[j].y * gm[j].y - s1 - xh[j].y * s2);
-          o.z = rs * (gv[j].z * gm[j].z - s1 - xh[j].z * s2);
-          o.w = rs * (gv[j].w * gm[j].w - s1 - xh[j].w * s2);
-          d4[i] = o;
+          const float4 g = gv[q][j], xv = xh[q][j];
+          xh[q][j] = make_float4((xv.x - mu[q]) * rs[q], (xv.y - mu[q]) * rs[q],
+                                 (xv.z - mu[q]) * rs[q], (xv.w - mu[q]) * rs[q]);
+          const float4 gg = make_float4(g.x * gm[j].x, g.y * gm[j].y, g.z * gm[j].z,
+                                        g.w * gm[j].w);
+          s1 += (gg.x + gg.y) + (gg.z + gg.w);
+          s2 += (gg.x * xh[q][j].x + gg.y * xh[q][j].y) + (gg.z * xh[q][j].z + gg.w * xh[q][j].w);
+          ag[j].x += g.x * xh[q][j].x; ag[j].y += g.y * xh[q][j].y;
+          ag[j].z += g.z * xh[q][j].z; ag[j].w += g.w * xh[q][j].w;
+          ab[j].x += g.x; ab[j].y += g.y; ab[j].z += g.z; ab[j].w += g.w;
+        }
+      }
+      s1 = wave_sum(s1) * inv_n;
+      s2 = wave_sum(s2) * inv_n;
+      if (dx) {
+        float4* d4 = reinterpret_cast<float4*>(dx + r * cols);
+#pragma unroll
+        for (int j = 0; j < V4; ++j) {
+          const int i = lane + 64 * j;
+          if (i < c4) {
+            float4 o;
+            o.x = rs[q] * (gv[q][j].x * gm[j].x - s1 - xh[q][j].x * s2);
+            o.y = rs[q] * (gv[q][j].y * gm[j].y - s1 - xh[q][j].y * s2);
+            o.z = rs[q] * (gv[q][j].z * gm[j].z - s1 - xh[q][j].z * s2);
+            o.w = rs[q] * (gv[q][j].w * gm[j].w - s1 - xh[q][j].w * s2);
+            d4[i] = o;
+          }
         }
       }
     }

@@ -19,7 +19,7 @@ namespace tjh {
 namespace {
 
 constexpr int kBlock = 256;
-constexpr int kMaxTensors = 32;
+constexpr int kMaxTensors = 56;  // keeps the kernel argument block under 4 KiB
 constexpr int64_t kChunk = kBlock * 4 * 4;  // elements per workgroup
 
 struct AdamTensor {
@@ -34,13 +34,15 @@ struct AdamTensor {
   int vec;
 };
 
-struct AdamBatch {
+struct AdamBatch {  // passed by value: must stay within the 4 KiB kernel argument block
   AdamTensor t[kMaxTensors];
   int count;
   float b1, omb1, b2, omb2, eps, wd;  // fp32 scalars as torch.js's tensor ops see them
   double decay;                        // 1 - lr*wd (AdamW)
   int decoupled;
 };
+static_assert(sizeof(AdamBatch) <= 4000, "AdamBatch exceeds the kernel argument block");
+
 
 // Every fp32 operation is rounded on its own (contraction off; IEEE
 // division and the correctly rounded llvm.sqrt), as the reference's
@@ -66,18 +68,32 @@ __global__ __launch_bounds__(kBlock) void k_adam(AdamBatch B) {
   int64_t beg = (int64_t)(b - T.first_block) * kChunk;
   int64_t end = beg + kChunk < T.n ? beg + kChunk : T.n;
   if (T.vec) {
-    for (int64_t i = beg + 4 * threadIdx.x; i < end; i += 4 * kBlock) {
-      float4 p = *reinterpret_cast<float4*>(T.p + i);
-      float4 g = *reinterpret_cast<const float4*>(T.g + i);
-      float4 m = *reinterpret_cast<float4*>(T.m + i);
-      float4 v = *reinterpret_cast<float4*>(T.v + i);
-      adam_elem(p.x, g.x, m.x, v.x, B, T);
-      adam_elem(p.y, g.y, m.y, v.y, B, T);
-      adam_elem(p.z, g.z, m.z, v.z, B, T);
-      adam_elem(p.w, g.w, m.w, v.w, B, T);
-      *reinterpret_cast<float4*>(T.p + i) = p;
-      *reinterpret_cast<float4*>(T.m + i) = m;
-      *reinterpret_cast<float4*>(T.v + i) = v;
+    // every load of the chunk is issued before the first update, so each
+    // lane has kSteps x 4 float4 in flight
+    constexpr int kSteps = kChunk / (4 * kBlock);
+    float4 p[kSteps], g[kSteps], m[kSteps], v[kSteps];
+#pragma unroll
+    for (int u = 0; u < kSteps; ++u) {
+      const int64_t i = beg + 4 * (threadIdx.x + (int64_t)u * kBlock);
+      if (i < end) {
+        p[u] = ld_nt(T.p + i);
+        g[u] = ld_nt(T.g + i);
+        m[u] = ld_nt(T.m + i);
+        v[u] = ld_nt(T.v + i);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kSteps; ++u) {
+      const int64_t i = beg + 4 * (threadIdx.x + (int64_t)u * kBlock);
+      if (i < end) {
+        adam_elem(p[u].x, g[u].x, m[u].x, v[u].x, B, T);
+        adam_elem(p[u].y, g[u].y, m[u].y, v[u].y, B, T);
+        adam_elem(p[u].z, g[u].z, m[u].z, v[u].z, B, T);
+        adam_elem(p[u].w, g[u].w, m[u].w, v[u].w, B, T);
+        st_nt(T.p + i, p[u]);
+        st_nt(T.m + i, m[u]);
+        st_nt(T.v + i, v[u]);
+      }
     }
   } else {
     for (int64_t i = beg + threadIdx.x; i < end; i += kBlock) {
