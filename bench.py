@@ -18,6 +18,7 @@ and `kernel_ms_per_step` come from an instrumented pass after the timed
 region that brackets every launch.  `cpu_baseline` times the oracle
 (numpy) on a bounded sample of the same workload on the host.
 
+    python bench.py --config mlp|chain|cnn|block   # the other four workloads
     python bench.py --copy-mib 1024      # known-size copy for counter scaling
     python bench.py --summarize-pmc FETCH WRITE COPY_FETCH COPY_WRITE
         # rocprofv3 --pmc output dirs -> profiles/gemm_hbm_traffic_gpt2.json
@@ -180,6 +181,165 @@ def copy_calibration(mib):
     print(json.dumps({"copy_calibration_bytes": n * 4, "launches": 3}), flush=True)
 
 
+# ------------------------------------------------------------ other workloads
+
+CONFIGS = {
+    "mlp": "MLP 784-256-ReLU-10 train step, batch 64, cross_entropy, Adam(lr 1e-3)",
+    "chain": "x[4096,4096] + bias[4096] -> GELU -> * y -> sum(0) -> mean, fwd+bwd",
+    "cnn": "CNN [32,3,64,64]: conv 3->32 3x3 p1, ReLU, conv 32->64 3x3 s2 p1, ReLU, "
+           "avg-pool, Linear(64,10), cross_entropy, fwd+bwd",
+    "block": "pre-LN transformer block B=8 T=1024 d=768 12 heads causal, 4x GELU MLP, "
+             "loss=mean, fwd+bwd",
+}
+
+# algorithmic work per step (the roofline numerators)
+MLP_FLOPS = 2 * 64 * (784 * 256 + 256 * 10) + 2 * 64 * (784 * 256 + 2 * 256 * 10)
+MLP_ADAM_BYTES = 28 * (784 * 256 + 256 + 256 * 10 + 10)
+CHAIN_FUSED_BYTES = 4 * 4096 * 4096 * 4 + 2 * 4096 * 4  # read x, y; write gx, gy; bias, gbias
+CNN_FLOPS = 226492416 + 3 * 1207959552 + 226492416 + 3 * 40960
+BLOCK_FLOPS = 3 * (2 * 8192 * (768 * 2304 + 768 * 768 + 2 * 768 * 3072) +
+                   4 * 8 * 12 * 64 * (1024 * 1025 // 2))
+
+
+def _timed(torch, step, steps, warmup):
+    for _ in range(warmup):
+        step()
+    torch.synchronize()
+    torch.hip.kernel_timing(False)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.synchronize()
+    el = time.perf_counter() - t0
+    # instrumented pass after the timed region: per-family kernel time
+    torch.hip.kernel_timing(True)
+    torch.hip.kernel_timing_reset()
+    for _ in range(steps):
+        step()
+    fams = {f: torch.hip.kernel_time(f) for f in torch.hip.kernel_families()}
+    torch.hip.kernel_timing(False)
+    per = {f: round(ms / steps, 4) for f, (n, ms) in sorted(fams.items(), key=lambda x: -x[1][1])
+           if ms > 0}
+    return el / steps, per
+
+
+def _cpu_time(fn):
+    t0 = time.perf_counter()
+    fn()
+    return time.perf_counter() - t0
+
+
+def run_config(name, steps, warmup, cpu):
+    import __graft_entry__ as ge
+    torch = ge.load_package()
+    from torchjs_amd import workloads as W
+    from oracle import models as om
+    from oracle import ops
+    from oracle.rng import Generator
+    torch.init(0)
+    out = {"metric": name, "config": {"workload": CONFIGS[name]}, "n_gpus": 1, "steps": steps,
+           "warmup": warmup, "dtype": "f32", "data": "synthetic (seeded host generator)"}
+    if name == "mlp":
+        g = Generator(1234)
+        x = g.randn((64, 784))
+        t = g.integers((64,), 10)
+        model = W.mlp()
+        opt = torch.optim.Adam(model.parameters(), lr=1e-3)
+        tx, tt = torch.tensor(x), torch.tensor(t)
+
+        def step():
+            opt.zero_grad()
+            torch.F.cross_entropy(model(tx), tt).backward()
+            opt.step()
+        sec, per = _timed(torch, step, steps, warmup)
+        out.update({"metric": "MLP train step samples/s", "value": round(64 / sec, 1),
+                    "unit": "samples/s", "us_per_step": round(sec * 1e6, 1),
+                    "roofline": {"bound": "launch", "gemm_TFLOP/s": round(MLP_FLOPS / sec / 1e12, 4),
+                                 "adam_GB/s": round(MLP_ADAM_BYTES / sec / 1e9, 2)}})
+        if cpu:
+            p = {k: v.numpy() for k, v in model.named_parameters()}
+
+            def ref():
+                _, gr = om.mlp_loss_and_grads(p, x, t)
+                for k in p:
+                    ops.adam_step(p[k], gr[k], np.zeros_like(p[k]), np.zeros_like(p[k]), 1, lr=1e-3)
+            dt = _cpu_time(ref)
+            out["cpu_baseline"] = {"value": round(64 / dt, 1), "unit": "samples/s", "kind": "port",
+                                   "sample": "oracle (numpy float64), full config, one step"}
+    elif name == "chain":
+        g = Generator(99)
+        n = 4096
+        x, b, y = g.randn((n, n)), g.randn((n,)), g.uniform((n, n), -1, 1)
+        tx, tb, ty = (torch.tensor(a, requires_grad=True) for a in (x, b, y))
+
+        def step():
+            for t_ in (tx, tb, ty):
+                t_.grad = None
+            W.chain_loss(tx, tb, ty).backward()
+        sec, per = _timed(torch, step, steps, warmup)
+        out.update({"metric": "elementwise+reduction fwd+bwd GB/s (fused-minimum bytes)",
+                    "value": round(CHAIN_FUSED_BYTES / sec / 1e9, 1), "unit": "GB/s",
+                    "ms_per_step": round(sec * 1e3, 3),
+                    "roofline": {"bound": "hbm", "achieved": round(CHAIN_FUSED_BYTES / sec / 1e9, 1),
+                                 "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                 "frac": round(CHAIN_FUSED_BYTES / sec / 1e9 / HBM_PEAK_GBS, 3),
+                                 "note": "end to end over the fused minimum (read x, y; write "
+                                         "gx, gy); the unfused pipeline moves ~4.5x that"}})
+        if cpu:
+            dt = _cpu_time(lambda: om.chain_loss_and_grads(x, b, y))
+            out["cpu_baseline"] = {"value": round(CHAIN_FUSED_BYTES / dt / 1e9, 2), "unit": "GB/s",
+                                   "kind": "port", "sample": "oracle (numpy float64), full 4096^2"}
+    elif name == "cnn":
+        g = Generator(7)
+        x = g.randn((32, 3, 64, 64))
+        t = g.integers((32,), 10)
+        model = W.CNN()
+        tx, tt = torch.tensor(x), torch.tensor(t)
+
+        def step():
+            model.zero_grad()
+            torch.F.cross_entropy(model(tx), tt).backward()
+        sec, per = _timed(torch, step, steps, warmup)
+        out.update({"metric": "small CNN fwd+bwd images/s", "value": round(32 / sec, 1),
+                    "unit": "images/s", "ms_per_step": round(sec * 1e3, 3),
+                    "roofline": {"bound": "mfma (conv2) / hbm (conv1)",
+                                 "achieved": round(CNN_FLOPS / sec / 1e12, 2),
+                                 "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                 "frac": round(CNN_FLOPS / sec / 1e12 / FP32_MFMA_PEAK_TFLOPS, 4)}})
+        if cpu:
+            p = {k: v.numpy() for k, v in model.named_parameters()}
+            dt = _cpu_time(lambda: om.cnn_loss_and_grads(p, x, t))
+            out["cpu_baseline"] = {"value": round(32 / dt, 2), "unit": "images/s", "kind": "port",
+                                   "sample": "oracle (numpy float64), full batch 32"}
+    elif name == "block":
+        r = np.random.default_rng(21)
+        p = om.block_params(768, r, std=0.02)
+        x = r.standard_normal((8, 1024, 768)).astype(np.float32)
+        blk = W.Block(768, 12)
+        W.load_params(blk, p)
+        tx = torch.tensor(x, requires_grad=True)
+
+        def step():
+            blk.zero_grad()
+            tx.grad = None
+            blk(tx).mean().backward()
+        sec, per = _timed(torch, step, steps, warmup)
+        out.update({"metric": "transformer block fwd+bwd tokens/s", "value": round(8192 / sec, 1),
+                    "unit": "tokens/s", "ms_per_step": round(sec * 1e3, 3),
+                    "roofline": {"bound": "mfma", "achieved": round(BLOCK_FLOPS / sec / 1e12, 2),
+                                 "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                 "frac": round(BLOCK_FLOPS / sec / 1e12 / FP32_MFMA_PEAK_TFLOPS, 4),
+                                 "flops": "386.58 GFLOP per step (causal-useful attention)"}})
+        if cpu:
+            xs = x[:1, :256]
+            dt = _cpu_time(lambda: om.block_loss_and_grads(p, xs, 12))
+            out["cpu_baseline"] = {"value": round(256 / dt, 1), "unit": "tokens/s", "kind": "port",
+                                   "sample": "oracle (numpy float64) at B=1, T=256 (same code "
+                                             "path, reduced sequence)"}
+    out["kernel_ms_per_step"] = dict(list(per.items())[:10])
+    return out
+
+
 def _pmc_rows(d):
     import csv
     import glob
@@ -235,6 +395,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="only run the copy-kernel calibration of this many MiB")
+    ap.add_argument("--config", default="gpt2", choices=["gpt2"] + sorted(CONFIGS),
+                    help="workload (default: the GPT-2 124M headline)")
     ap.add_argument("--summarize-pmc", nargs=4, metavar="DIR", default=None,
                     help="FETCH WRITE COPY_FETCH COPY_WRITE rocprofv3 --pmc output dirs")
     args = ap.parse_args()
@@ -247,6 +409,10 @@ def main():
         sys.exit(2)
     if args.copy_mib:
         copy_calibration(args.copy_mib)
+        return
+    if args.config != "gpt2":
+        print(json.dumps(run_config(args.config, args.steps, args.warmup,
+                                    not args.no_cpu_baseline)), flush=True)
         return
     elapsed, final_loss, dominant, timing, prof_steps, nparams, mem = run_gpu(args.steps,
                                                                               args.warmup)
