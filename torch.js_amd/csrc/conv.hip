@@ -32,64 +32,61 @@ ConvGeo geo(const tjh_conv2d_desc* d) {
 }
 
 // col[(c*KH+kh)*KW+kw][n*P + p] = x[n][c][oh*sh - ph + kh*dh][ow*sw - pw + kw*dw]
+// Grid (ceil(P/256), C*KH*KW, N): the patch row (c, kh, kw) and the image
+// are per-workgroup constants, threads walk output pixels p (coalesced
+// writes; coalesced reads along ox for unit stride).
 __global__ __launch_bounds__(kBlock) void k_im2col(const float* __restrict__ x, ConvGeo g,
                                                    float* __restrict__ col) {
-  const int64_t P = g.oh * g.ow;
-  const int64_t ncol = g.n * P;
-  const int64_t total = g.c * g.kh * g.kw * ncol;
-  int64_t stride = (int64_t)gridDim.x * kBlock;
-  for (int64_t e = (int64_t)blockIdx.x * kBlock + threadIdx.x; e < total; e += stride) {
-    int64_t j = e % ncol;
-    int64_t row = e / ncol;
-    int64_t kw = row % g.kw;
-    int64_t kh = (row / g.kw) % g.kh;
-    int64_t c = row / (g.kw * g.kh);
-    int64_t n = j / P, p = j % P;
-    int64_t oy = p / g.ow, ox = p % g.ow;
-    int64_t iy = oy * g.sh - g.ph + kh * g.dh;
-    int64_t ix = ox * g.sw - g.pw + kw * g.dw;
-    float v = 0.f;
-    if (iy >= 0 && iy < g.h && ix >= 0 && ix < g.w) v = x[((n * g.c + c) * g.h + iy) * g.w + ix];
-    col[e] = v;
-  }
+  const int P = (int)(g.oh * g.ow);
+  const int p = blockIdx.x * kBlock + threadIdx.x;
+  if (p >= P) return;
+  const int row = blockIdx.y, n = blockIdx.z;
+  const int kw = row % (int)g.kw;
+  const int kh = (row / (int)g.kw) % (int)g.kh;
+  const int c = row / (int)(g.kw * g.kh);
+  const int oy = p / (int)g.ow, ox = p - oy * (int)g.ow;
+  const int iy = oy * (int)g.sh - (int)g.ph + kh * (int)g.dh;
+  const int ix = ox * (int)g.sw - (int)g.pw + kw * (int)g.dw;
+  float v = 0.f;
+  if (iy >= 0 && iy < g.h && ix >= 0 && ix < g.w)
+    v = x[(((int64_t)n * g.c + c) * g.h + iy) * g.w + ix];
+  col[(int64_t)row * (g.n * P) + (int64_t)n * P + p] = v;
 }
 
 // dx[n][c][iy][ix] = sum over (kh, kw) hitting an output pixel of dcol.
+// Grid (ceil(H*W/256), C, N).
 __global__ __launch_bounds__(kBlock) void k_col2im(const float* __restrict__ dcol, ConvGeo g,
                                                    float* __restrict__ dx) {
-  const int64_t P = g.oh * g.ow;
-  const int64_t ncol = g.n * P;
-  const int64_t total = g.n * g.c * g.h * g.w;
-  int64_t stride = (int64_t)gridDim.x * kBlock;
-  for (int64_t e = (int64_t)blockIdx.x * kBlock + threadIdx.x; e < total; e += stride) {
-    int64_t ix = e % g.w;
-    int64_t iy = (e / g.w) % g.h;
-    int64_t c = (e / (g.w * g.h)) % g.c;
-    int64_t n = e / (g.w * g.h * g.c);
-    float acc = 0.f;
-    for (int64_t kh = 0; kh < g.kh; ++kh) {
-      int64_t ty = iy + g.ph - kh * g.dh;
-      if (ty < 0 || ty % g.sh) continue;
-      int64_t oy = ty / g.sh;
-      if (oy >= g.oh) continue;
-      for (int64_t kw = 0; kw < g.kw; ++kw) {
-        int64_t tx = ix + g.pw - kw * g.dw;
-        if (tx < 0 || tx % g.sw) continue;
-        int64_t ox = tx / g.sw;
-        if (ox >= g.ow) continue;
-        int64_t row = (c * g.kh + kh) * g.kw + kw;
-        acc += dcol[row * ncol + n * P + oy * g.ow + ox];
-      }
+  const int HW = (int)(g.h * g.w);
+  const int e = blockIdx.x * kBlock + threadIdx.x;
+  if (e >= HW) return;
+  const int c = blockIdx.y, n = blockIdx.z;
+  const int iy = e / (int)g.w, ix = e - iy * (int)g.w;
+  const int64_t P = g.oh * g.ow, ncol = g.n * P;
+  const float* __restrict__ base = dcol + (int64_t)n * P;
+  float acc = 0.f;
+  for (int kh = 0; kh < (int)g.kh; ++kh) {
+    const int ty = iy + (int)g.ph - kh * (int)g.dh;
+    if (ty < 0 || ty % (int)g.sh) continue;
+    const int oy = ty / (int)g.sh;
+    if (oy >= g.oh) continue;
+    for (int kw = 0; kw < (int)g.kw; ++kw) {
+      const int tx = ix + (int)g.pw - kw * (int)g.dw;
+      if (tx < 0 || tx % (int)g.sw) continue;
+      const int ox = tx / (int)g.sw;
+      if (ox >= g.ow) continue;
+      const int64_t row = ((int64_t)c * g.kh + kh) * g.kw + kw;
+      acc += base[row * ncol + (int64_t)oy * g.ow + ox];
     }
-    dx[e] = acc;
   }
+  dx[((int64_t)n * g.c + c) * HW + e] = acc;
 }
 
-int grid_for(int64_t n) {
-  int64_t g = cdiv(n, kBlock);
-  int64_t cap = (int64_t)(num_cus() > 0 ? num_cus() : 256) * 16;
-  if (g > cap) g = cap;
-  return (int)(g < 1 ? 1 : g);
+int launch_im2col(const float* x, const ConvGeo& g, float* col) {
+  hipLaunchKernelGGL(k_im2col, dim3((unsigned)cdiv(g.oh * g.ow, kBlock),
+                                    (unsigned)(g.c * g.kh * g.kw), (unsigned)g.n),
+                     dim3(kBlock), 0, stream(), x, g, col);
+  return check_launch("im2col");
 }
 
 int check_desc(const tjh_conv2d_desc* d) {
@@ -107,6 +104,9 @@ int check_desc(const tjh_conv2d_desc* d) {
   TJH_ARG(oh == d->oh && ow == d->ow, "conv2d: output size %lldx%lld does not match %lldx%lld",
           (long long)d->oh, (long long)d->ow, (long long)oh, (long long)ow);
   TJH_ARG(oh > 0 && ow > 0, "conv2d: empty output");
+  TJH_ARG(d->h * d->w < (int64_t(1) << 30) && oh * ow < (int64_t(1) << 30) &&
+              d->c * d->kh * d->kw <= 65535 && d->n <= 65535 && d->c <= 65535,
+          "conv2d: sizes beyond this implementation's grid (C*KH*KW, N, C <= 65535)");
   return TJH_OK;
 }
 
@@ -129,10 +129,8 @@ int tjh_conv2d_forward(const tjh_conv2d_desc* d, const float* x, const float* w,
   Scratch col((size_t)(g.c * kk * ncol) * sizeof(float));
   if (!col.ok()) return set_error(TJH_ERR_OOM, "conv2d_forward: no im2col scratch");
   KernelScope ks("conv2d_fwd");
-  int64_t total = g.c * kk * ncol;
-  hipLaunchKernelGGL(k_im2col, dim3(grid_for(total)), dim3(kBlock), 0, stream(), x, g,
-                     col.as<float>());
-  if ((rc = check_launch("im2col")) != TJH_OK) return rc;
+  rc = launch_im2col(x, g, col.as<float>());
+  if (rc != TJH_OK) return rc;
   for (int64_t gi = 0; gi < g.groups; ++gi) {
     // y[n][gi*ocg + o][p] = sum_r W[gi*ocg + o][r] * col[gi*cg*kk + r][n*P + p]
     rc = gemm("conv.gemm", 0, 0, ocg, P, cg * kk, 1.f, w + gi * ocg * cg * kk, cg * kk, 0,
@@ -162,9 +160,8 @@ int tjh_conv2d_backward_input(const tjh_conv2d_desc* d, const float* dy, const f
                   ncol, P, g.n, nullptr, 0);
     if (rc != TJH_OK) return rc;
   }
-  int64_t total = g.n * g.c * g.h * g.w;
-  hipLaunchKernelGGL(k_col2im, dim3(grid_for(total)), dim3(kBlock), 0, stream(), dcol.as<float>(),
-                     g, dx);
+  hipLaunchKernelGGL(k_col2im, dim3((unsigned)cdiv(g.h * g.w, kBlock), (unsigned)g.c,
+                                     (unsigned)g.n), dim3(kBlock), 0, stream(), dcol.as<float>(), g, dx);
   return check_launch("col2im");
 }
 
@@ -184,10 +181,8 @@ int tjh_conv2d_backward_weight(const tjh_conv2d_desc* d, const float* dy, const 
   Scratch dyt((size_t)(g.oc * ncol) * sizeof(float));
   if (!col.ok() || !dyt.ok()) return set_error(TJH_ERR_OOM, "conv2d_backward_weight: no scratch");
   KernelScope ks("conv2d_wgrad");
-  int64_t total = g.c * kk * ncol;
-  hipLaunchKernelGGL(k_im2col, dim3(grid_for(total)), dim3(kBlock), 0, stream(), x, g,
-                     col.as<float>());
-  if ((rc = check_launch("im2col")) != TJH_OK) return rc;
+  rc = launch_im2col(x, g, col.as<float>());
+  if (rc != TJH_OK) return rc;
   // dyt[o][n][p] = dy[n][o][p]
   int64_t shape[3] = {g.oc, g.n, P};
   int64_t sst[3] = {P, g.oc * P, 1};

@@ -145,14 +145,15 @@ __global__ __launch_bounds__(kBlock) void k_reduce_cols(const float* __restrict_
   }
 }
 
-// Column sums of x viewed [outer][r][inner]: workgroup (b, o) sums rows
-// [b*rchunk, (b+1)*rchunk) of every column of o (compensated) into the
-// partial row part[o][b]; colsum_final adds the partial rows.
+// Column sums of x viewed [outer][r][inner]: workgroup (b, cb, o) sums
+// rows [b*rchunk, (b+1)*rchunk) of column block cb (256 lanes of 4 or 1
+// columns) of o, compensated, into the partial row part[o][b]; colsum_final
+// adds the partial rows.
 template <bool VEC>
 __global__ __launch_bounds__(kBlock) void k_colsum(const float* __restrict__ x, int64_t r,
                                                    int64_t inner, int64_t rchunk,
                                                    float* __restrict__ part) {
-  const int64_t o = blockIdx.y;
+  const int64_t o = blockIdx.z;
   const int64_t nb = gridDim.x, b = blockIdx.x;
   const float* __restrict__ base = x + o * r * inner;
   const int64_t r0 = b * rchunk, r1 = r0 + rchunk < r ? r0 + rchunk : r;
@@ -160,7 +161,8 @@ __global__ __launch_bounds__(kBlock) void k_colsum(const float* __restrict__ x, 
   // rows are fetched kBatch at a time before they are accumulated, so the
   // loads of a batch are in flight together
   if (VEC) {
-    for (int64_t c4 = threadIdx.x; c4 * 4 < inner; c4 += kBlock) {
+    const int64_t c4 = (int64_t)blockIdx.y * kBlock + threadIdx.x;
+    if (c4 * 4 < inner) {
       Kahan kx, ky, kz, kw;
       const float4* __restrict__ col = reinterpret_cast<const float4*>(base + c4 * 4);
       const int64_t st = inner / 4;
@@ -177,7 +179,8 @@ __global__ __launch_bounds__(kBlock) void k_colsum(const float* __restrict__ x, 
       *reinterpret_cast<float4*>(prow + c4 * 4) = make_float4(kx.s, ky.s, kz.s, kw.s);
     }
   } else {
-    for (int64_t cc = threadIdx.x; cc < inner; cc += kBlock) {
+    const int64_t cc = (int64_t)blockIdx.y * kBlock + threadIdx.x;
+    if (cc < inner) {
       Kahan kc;
       for (int64_t k = r0; k < r1; k += kBatch) {
         float v[kBatch];
@@ -290,7 +293,7 @@ int colsum_launch(const float* x, int64_t outer, int64_t r, int64_t inner, float
   nb = cdiv(r, rchunk);
   Scratch part((size_t)(outer * nb * inner) * sizeof(float));
   if (!part.ok()) return set_error(TJH_ERR_OOM, "reduce: no scratch memory");
-  dim3 grid((unsigned)nb, (unsigned)outer);
+  dim3 grid((unsigned)nb, (unsigned)col_waves, (unsigned)outer);
   if (vec)
     hipLaunchKernelGGL(k_colsum<true>, grid, dim3(kBlock), 0, stream(), x, r, inner, rchunk,
                        part.as<float>());
