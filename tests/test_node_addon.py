@@ -17,7 +17,15 @@ EXPORTS = ["init", "deviceInfo", "malloc", "h2d", "d2h", "d2hAsync", "synchroniz
            "unaryBackward", "binary", "scalar", "reduce", "softmaxForward", "softmaxBackward",
            "crossEntropyForward", "crossEntropyBackward", "layerNormForward",
            "layerNormBackward", "embeddingForward", "embeddingBackward", "gemm", "sdpaForward",
-           "sdpaBackward", "adamStep", "version"]
+           "sdpaBackward", "adamStep", "version", "isInitialized", "deviceCount", "free",
+           "resetPeak", "d2d", "kprofEnable", "kprofFilter", "kprofReset", "kprofQuery",
+           "kprofNames", "timerStart", "timerStop", "fillI32", "copyStridedI32", "castF32I32",
+           "castI32F32", "ternary", "powScalarBackward", "axpy", "maskedFill", "compare",
+           "argmax", "nllLossForward", "nllLossBackward", "indexSelect", "indexAdd", "gather",
+           "scatterAdd", "oneHot", "oneHotI32", "nonzero", "conv2dForward",
+           "conv2dBackwardInput", "conv2dBackwardWeight"]
+HEADER = os.path.join(ROOT, "include", "torchjs_hip.h")
+SOURCE = os.path.join(ROOT, "torch.js_amd", "node", "torchjs_hip_napi.c")
 
 needs_addon = pytest.mark.skipif(NODE is None or not os.path.exists(ADDON),
                                  reason="node or the built addon is absent")
@@ -34,6 +42,16 @@ def test_addon_exports():
     assert r.returncode == 0, r.stderr
     keys = json.loads(r.stdout)
     assert sorted(keys) == sorted(EXPORTS)
+
+
+def test_addon_binds_every_declared_entry_point():
+    """Every function the C ABI header declares is called by the addon."""
+    import re
+    declared = set(re.findall(r"^(?:int|const char\*)\s+(tjh_\w+)\(", open(HEADER).read(),
+                              re.M))
+    called = set(re.findall(r"(tjh_\w+)\(", open(SOURCE).read()))
+    assert declared, "no declarations parsed"
+    assert not declared - called, sorted(declared - called)
 
 
 @needs_addon

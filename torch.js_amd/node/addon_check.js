@@ -103,6 +103,58 @@ async function main() {
   out.adam_max_abs_err = aErr;
   ok = ok && aErr < 1e-6;
 
+  // conv2d forward (NCHW, stride 2, pad 1, bias) against a direct loop
+  const cn = 2, cc = 3, ch = 9, cw = 7, coc = 4, k = 3, cs = 2, cp = 1;
+  const coh = Math.floor((ch + 2 * cp - k) / cs) + 1, cow = Math.floor((cw + 2 * cp - k) / cs) + 1;
+  const cx = Float32Array.from({ length: cn * cc * ch * cw }, rnd);
+  const cwt = Float32Array.from({ length: coc * cc * k * k }, rnd);
+  const cb = Float32Array.from({ length: coc }, rnd);
+  const dcx = upload(cx), dcw = upload(cwt), dcb = upload(cb);
+  const dcy = hip.malloc(cn * coc * coh * cow * 4);
+  hip.conv2dForward([cn, cc, ch, cw, coc, k, k, cs, cs, cp, cp, 1, 1, 1, coh, cow], dcx.ptr,
+                    dcw.ptr, dcb.ptr, dcy.ptr);
+  const cy = await hip.d2hAsync(dcy.ptr, new Float32Array(cn * coc * coh * cow));
+  let cErr = 0;
+  for (let n = 0; n < cn; ++n)
+    for (let o = 0; o < coc; ++o)
+      for (let y = 0; y < coh; ++y)
+        for (let x = 0; x < cow; ++x) {
+          let s = cb[o];
+          for (let c = 0; c < cc; ++c)
+            for (let a = 0; a < k; ++a)
+              for (let b = 0; b < k; ++b) {
+                const iy = y * cs - cp + a, ix = x * cs - cp + b;
+                if (iy >= 0 && iy < ch && ix >= 0 && ix < cw)
+                  s += cx[((n * cc + c) * ch + iy) * cw + ix] * cwt[((o * cc + c) * k + a) * k + b];
+              }
+          cErr = Math.max(cErr, Math.abs(cy[((n * coc + o) * coh + y) * cow + x] - s));
+        }
+  out.conv_max_abs_err = cErr;
+  ok = ok && cErr < 1e-5;
+
+  // argmax over rows (first index on ties) and index_select of rows
+  const ar = 5, ac = 37;
+  const av = Float32Array.from({ length: ar * ac }, (_, i) => Math.round(8 * rnd()));
+  const dav = upload(av), dai = hip.malloc(ar * 4);
+  hip.argmax(dav.ptr, ar, ac, 1, 0, dai.ptr);
+  const ai = await hip.d2hAsync(dai.ptr, new Int32Array(ar));
+  let argOk = true;
+  for (let r = 0; r < ar; ++r) {
+    let best = 0;
+    for (let c = 1; c < ac; ++c) if (av[r * ac + c] > av[r * ac + best]) best = c;
+    argOk = argOk && ai[r] === best;
+  }
+  const sel = Int32Array.of(4, 0, -1, 2);
+  const dsel = upload(sel), dso = hip.malloc(sel.length * ac * 4);
+  hip.indexSelect(dav.ptr, 1, ar, ac, dsel.ptr, sel.length, dso.ptr);
+  const so = await hip.d2hAsync(dso.ptr, new Float32Array(sel.length * ac));
+  for (let j = 0; j < sel.length; ++j) {
+    const row = sel[j] < 0 ? sel[j] + ar : sel[j];
+    for (let c = 0; c < ac; ++c) argOk = argOk && so[j * ac + c] === av[row * ac + c];
+  }
+  out.argmax_index_select_exact = argOk;
+  ok = ok && argOk;
+
   hip.synchronize();
   out.mem = hip.memoryStats();
   out.ok = ok;

@@ -11,11 +11,11 @@
  * libuv worker (napi_async_work) so readbacks do not block the event loop,
  * the analogue of torch.js's mapAsync readback (buffer.ts:150-206).
  *
- * Bound entry points: the runtime (init, device info, malloc / free,
- * copies, sync, memory stats, timers) and the autograd hot path (fill,
- * random, unary fwd/bwd, binary, scalar, reduce, softmax fwd/bwd,
- * cross_entropy fwd/bwd, layer_norm fwd/bwd, embedding fwd/bwd, gemm,
- * sdpa fwd/bwd, adam_step, copy_strided).
+ * Every entry point of include/torchjs_hip.h is bound (tjh_last_error's
+ * message rides on the thrown Error; tjh_version is the `version`
+ * property): the runtime (init, device info and count, malloc / free,
+ * copies, sync, memory stats, launch timing, timers) and every kernel
+ * entry of the autograd hot path.
  */
 #ifndef NAPI_VERSION
 #define NAPI_VERSION 8
@@ -521,6 +521,289 @@ static napi_value js_adam_step(napi_env env, napi_callback_info info) {
   return undef(env);
 }
 
+/* ------------------------------------------------- remaining entry points */
+
+#define F32(v) ((float*)ptr(env, (v)))
+#define CF32(v) ((const float*)ptr(env, (v)))
+#define I32(v) ((int32_t*)ptr(env, (v)))
+#define CI32(v) ((const int32_t*)ptr(env, (v)))
+
+static napi_value js_is_initialized(napi_env env, napi_callback_info info) {
+  (void)info;
+  return num(env, tjh_is_initialized());
+}
+static napi_value js_device_count(napi_env env, napi_callback_info info) {
+  (void)info;
+  int n = 0;
+  CHECK_RC(tjh_device_count(&n));
+  return num(env, n);
+}
+/* free(ptr): returns a block to the cache now (the GC finalizer of the
+ * allocation's handle must then not run: callers drop the handle). */
+static napi_value js_free(napi_env env, napi_callback_info info) {
+  napi_value a[1];
+  if (!get_args(env, info, 1, a)) return NULL;
+  CHECK_RC(tjh_free(ptr(env, a[0])));
+  return undef(env);
+}
+static napi_value js_reset_peak(napi_env env, napi_callback_info info) {
+  (void)info;
+  CHECK_RC(tjh_reset_peak());
+  return undef(env);
+}
+static napi_value js_d2d(napi_env env, napi_callback_info info) {
+  napi_value a[3];
+  if (!get_args(env, info, 3, a)) return NULL;
+  CHECK_RC(tjh_d2d(ptr(env, a[0]), ptr(env, a[1]), (size_t)i64(env, a[2])));
+  return undef(env);
+}
+static napi_value js_kprof_enable(napi_env env, napi_callback_info info) {
+  napi_value a[1];
+  if (!get_args(env, info, 1, a)) return NULL;
+  CHECK_RC(tjh_kprof_enable((int)i64(env, a[0])));
+  return undef(env);
+}
+static napi_value js_kprof_filter(napi_env env, napi_callback_info info) {
+  napi_value a[1];
+  char buf[256];
+  size_t len = 0;
+  if (!get_args(env, info, 1, a)) return NULL;
+  napi_get_value_string_utf8(env, a[0], buf, sizeof(buf), &len);
+  CHECK_RC(tjh_kprof_filter(buf));
+  return undef(env);
+}
+static napi_value js_kprof_reset(napi_env env, napi_callback_info info) {
+  (void)info;
+  CHECK_RC(tjh_kprof_reset());
+  return undef(env);
+}
+/* kprofQuery(family) -> { launches, ms } */
+static napi_value js_kprof_query(napi_env env, napi_callback_info info) {
+  napi_value a[1], o;
+  char buf[256];
+  size_t len = 0;
+  int64_t n = 0;
+  double ms = 0.0;
+  if (!get_args(env, info, 1, a)) return NULL;
+  napi_get_value_string_utf8(env, a[0], buf, sizeof(buf), &len);
+  CHECK_RC(tjh_kprof_query(buf, &n, &ms));
+  napi_create_object(env, &o);
+  napi_set_named_property(env, o, "launches", num(env, (double)n));
+  napi_set_named_property(env, o, "ms", num(env, ms));
+  return o;
+}
+static napi_value js_kprof_names(napi_env env, napi_callback_info info) {
+  (void)info;
+  static char buf[65536];
+  napi_value s;
+  CHECK_RC(tjh_kprof_names(buf, sizeof(buf)));
+  napi_create_string_utf8(env, buf, NAPI_AUTO_LENGTH, &s);
+  return s;
+}
+static napi_value js_timer_start(napi_env env, napi_callback_info info) {
+  (void)info;
+  int id = 0;
+  CHECK_RC(tjh_timer_start(&id));
+  return num(env, id);
+}
+static napi_value js_timer_stop(napi_env env, napi_callback_info info) {
+  napi_value a[1];
+  double ms = 0.0;
+  if (!get_args(env, info, 1, a)) return NULL;
+  CHECK_RC(tjh_timer_stop((int)i64(env, a[0]), &ms));
+  return num(env, ms);
+}
+static napi_value js_fill_i32(napi_env env, napi_callback_info info) {
+  napi_value a[3];
+  if (!get_args(env, info, 3, a)) return NULL;
+  CHECK_RC(tjh_fill_i32(I32(a[0]), i64(env, a[1]), (int32_t)i64(env, a[2])));
+  return undef(env);
+}
+static napi_value js_copy_strided_i32(napi_env env, napi_callback_info info) {
+  napi_value a[5];
+  int64_t shape[TJH_MAX_DIMS], ss[TJH_MAX_DIMS], ds[TJH_MAX_DIMS];
+  if (!get_args(env, info, 5, a)) return NULL;
+  int nd = i64arr(env, a[0], shape, TJH_MAX_DIMS);
+  i64arr(env, a[2], ss, TJH_MAX_DIMS);
+  i64arr(env, a[4], ds, TJH_MAX_DIMS);
+  CHECK_RC(tjh_copy_strided_i32(nd, shape, CI32(a[1]), ss, I32(a[3]), ds));
+  return undef(env);
+}
+static napi_value js_cast_f32_i32(napi_env env, napi_callback_info info) {
+  napi_value a[3];
+  if (!get_args(env, info, 3, a)) return NULL;
+  CHECK_RC(tjh_cast_f32_i32(CF32(a[0]), I32(a[1]), i64(env, a[2])));
+  return undef(env);
+}
+static napi_value js_cast_i32_f32(napi_env env, napi_callback_info info) {
+  napi_value a[3];
+  if (!get_args(env, info, 3, a)) return NULL;
+  CHECK_RC(tjh_cast_i32_f32(CI32(a[0]), F32(a[1]), i64(env, a[2])));
+  return undef(env);
+}
+/* ternary(op, shape, g, gStrides, a, aStrides, b, bStrides, out) */
+static napi_value js_ternary(napi_env env, napi_callback_info info) {
+  napi_value a[9];
+  int64_t shape[TJH_MAX_DIMS], gs[TJH_MAX_DIMS], as[TJH_MAX_DIMS], bs[TJH_MAX_DIMS];
+  if (!get_args(env, info, 9, a)) return NULL;
+  int nd = i64arr(env, a[1], shape, TJH_MAX_DIMS);
+  i64arr(env, a[3], gs, TJH_MAX_DIMS);
+  i64arr(env, a[5], as, TJH_MAX_DIMS);
+  i64arr(env, a[7], bs, TJH_MAX_DIMS);
+  CHECK_RC(tjh_ternary((int)i64(env, a[0]), nd, shape, CF32(a[2]), gs, CF32(a[4]), as, CF32(a[6]),
+                       bs, F32(a[8])));
+  return undef(env);
+}
+static napi_value js_pow_scalar_backward(napi_env env, napi_callback_info info) {
+  napi_value a[5];
+  if (!get_args(env, info, 5, a)) return NULL;
+  CHECK_RC(tjh_pow_scalar_backward(CF32(a[0]), CF32(a[1]), (float)f64(env, a[2]), F32(a[3]),
+                                   i64(env, a[4])));
+  return undef(env);
+}
+static napi_value js_axpy(napi_env env, napi_callback_info info) {
+  napi_value a[5];
+  if (!get_args(env, info, 5, a)) return NULL;
+  CHECK_RC(tjh_axpy((float)f64(env, a[0]), CF32(a[1]), CF32(a[2]), F32(a[3]), i64(env, a[4])));
+  return undef(env);
+}
+/* maskedFill(shape, x, xStrides, mask(uint8), maskStrides, value, out) */
+static napi_value js_masked_fill(napi_env env, napi_callback_info info) {
+  napi_value a[7];
+  int64_t shape[TJH_MAX_DIMS], xs[TJH_MAX_DIMS], ms[TJH_MAX_DIMS];
+  if (!get_args(env, info, 7, a)) return NULL;
+  int nd = i64arr(env, a[0], shape, TJH_MAX_DIMS);
+  i64arr(env, a[2], xs, TJH_MAX_DIMS);
+  i64arr(env, a[4], ms, TJH_MAX_DIMS);
+  CHECK_RC(tjh_masked_fill(nd, shape, CF32(a[1]), xs, (const uint8_t*)ptr(env, a[3]), ms,
+                           (float)f64(env, a[5]), F32(a[6])));
+  return undef(env);
+}
+/* compare(op, shape, a, aStrides, b, bStrides, out) */
+static napi_value js_compare(napi_env env, napi_callback_info info) {
+  napi_value a[7];
+  int64_t shape[TJH_MAX_DIMS], as[TJH_MAX_DIMS], bs[TJH_MAX_DIMS];
+  if (!get_args(env, info, 7, a)) return NULL;
+  int nd = i64arr(env, a[1], shape, TJH_MAX_DIMS);
+  i64arr(env, a[3], as, TJH_MAX_DIMS);
+  i64arr(env, a[5], bs, TJH_MAX_DIMS);
+  CHECK_RC(tjh_compare((int)i64(env, a[0]), nd, shape, CF32(a[2]), as, CF32(a[4]), bs, F32(a[6])));
+  return undef(env);
+}
+/* argmax(x, outer, r, inner, isMin, out(int32)) */
+static napi_value js_argmax(napi_env env, napi_callback_info info) {
+  napi_value a[6];
+  if (!get_args(env, info, 6, a)) return NULL;
+  CHECK_RC(tjh_argmax(CF32(a[0]), i64(env, a[1]), i64(env, a[2]), i64(env, a[3]),
+                      (int)i64(env, a[4]), I32(a[5])));
+  return undef(env);
+}
+/* nllLossForward(logp, ld, targets, rows, cols, ignore, lossRows, reduction, out) */
+static napi_value js_nll_forward(napi_env env, napi_callback_info info) {
+  napi_value a[9];
+  if (!get_args(env, info, 9, a)) return NULL;
+  CHECK_RC(tjh_nll_loss_forward(CF32(a[0]), i64(env, a[1]), CI32(a[2]), i64(env, a[3]),
+                                i64(env, a[4]), (int32_t)i64(env, a[5]), F32(a[6]),
+                                (int)i64(env, a[7]), F32(a[8])));
+  return undef(env);
+}
+/* nllLossBackward(targets, gradOut, rows, cols, ignore, reduction, dlogp) */
+static napi_value js_nll_backward(napi_env env, napi_callback_info info) {
+  napi_value a[7];
+  if (!get_args(env, info, 7, a)) return NULL;
+  CHECK_RC(tjh_nll_loss_backward(CI32(a[0]), CF32(a[1]), i64(env, a[2]), i64(env, a[3]),
+                                 (int32_t)i64(env, a[4]), (int)i64(env, a[5]), F32(a[6])));
+  return undef(env);
+}
+/* indexSelect(x, outer, srcLen, inner, idx, nIdx, out) */
+static napi_value js_index_select(napi_env env, napi_callback_info info) {
+  napi_value a[7];
+  if (!get_args(env, info, 7, a)) return NULL;
+  CHECK_RC(tjh_index_select(CF32(a[0]), i64(env, a[1]), i64(env, a[2]), i64(env, a[3]), CI32(a[4]),
+                            i64(env, a[5]), F32(a[6])));
+  return undef(env);
+}
+/* indexAdd(dx, outer, srcLen, inner, idx, nIdx, dout) */
+static napi_value js_index_add(napi_env env, napi_callback_info info) {
+  napi_value a[7];
+  if (!get_args(env, info, 7, a)) return NULL;
+  CHECK_RC(tjh_index_add(F32(a[0]), i64(env, a[1]), i64(env, a[2]), i64(env, a[3]), CI32(a[4]),
+                         i64(env, a[5]), CF32(a[6])));
+  return undef(env);
+}
+/* gather(x, outer, srcLen, inner, idx, idxLen, out) */
+static napi_value js_gather(napi_env env, napi_callback_info info) {
+  napi_value a[7];
+  if (!get_args(env, info, 7, a)) return NULL;
+  CHECK_RC(tjh_gather(CF32(a[0]), i64(env, a[1]), i64(env, a[2]), i64(env, a[3]), CI32(a[4]),
+                      i64(env, a[5]), F32(a[6])));
+  return undef(env);
+}
+/* scatterAdd(dx, outer, dstLen, inner, idx, idxLen, src) */
+static napi_value js_scatter_add(napi_env env, napi_callback_info info) {
+  napi_value a[7];
+  if (!get_args(env, info, 7, a)) return NULL;
+  CHECK_RC(tjh_scatter_add(F32(a[0]), i64(env, a[1]), i64(env, a[2]), i64(env, a[3]), CI32(a[4]),
+                           i64(env, a[5]), CF32(a[6])));
+  return undef(env);
+}
+/* oneHot(x(float), n, classes, out) and oneHotI32(x(int32), n, classes, out) */
+static napi_value js_one_hot(napi_env env, napi_callback_info info) {
+  napi_value a[4];
+  if (!get_args(env, info, 4, a)) return NULL;
+  CHECK_RC(tjh_one_hot(CF32(a[0]), i64(env, a[1]), i64(env, a[2]), F32(a[3])));
+  return undef(env);
+}
+static napi_value js_one_hot_i32(napi_env env, napi_callback_info info) {
+  napi_value a[4];
+  if (!get_args(env, info, 4, a)) return NULL;
+  CHECK_RC(tjh_one_hot_i32(CI32(a[0]), i64(env, a[1]), i64(env, a[2]), F32(a[3])));
+  return undef(env);
+}
+/* nonzero(x, shape, out(int32 [maxOut, ndim]), maxOut) -> count */
+static napi_value js_nonzero(napi_env env, napi_callback_info info) {
+  napi_value a[4];
+  int64_t shape[TJH_MAX_DIMS], count = 0;
+  if (!get_args(env, info, 4, a)) return NULL;
+  int nd = i64arr(env, a[1], shape, TJH_MAX_DIMS);
+  CHECK_RC(tjh_nonzero(CF32(a[0]), nd, shape, I32(a[2]), i64(env, a[3]), &count));
+  return num(env, (double)count);
+}
+/* conv descriptor: [n, c, h, w, oc, kh, kw, strideH, strideW, padH, padW,
+ * dilH, dilW, groups, oh, ow] */
+static int conv_desc(napi_env env, napi_value v, tjh_conv2d_desc* d) {
+  int64_t f[16];
+  if (i64arr(env, v, f, 16) != 16) {
+    napi_throw_type_error(env, NULL, "conv2d: descriptor must have 16 numbers");
+    return 0;
+  }
+  d->n = f[0]; d->c = f[1]; d->h = f[2]; d->w = f[3]; d->oc = f[4]; d->kh = f[5]; d->kw = f[6];
+  d->stride_h = f[7]; d->stride_w = f[8]; d->pad_h = f[9]; d->pad_w = f[10]; d->dil_h = f[11];
+  d->dil_w = f[12]; d->groups = f[13]; d->oh = f[14]; d->ow = f[15];
+  return 1;
+}
+static napi_value js_conv_forward(napi_env env, napi_callback_info info) {
+  napi_value a[5];
+  tjh_conv2d_desc d;
+  if (!get_args(env, info, 5, a) || !conv_desc(env, a[0], &d)) return NULL;
+  CHECK_RC(tjh_conv2d_forward(&d, CF32(a[1]), CF32(a[2]), CF32(a[3]), F32(a[4])));
+  return undef(env);
+}
+static napi_value js_conv_backward_input(napi_env env, napi_callback_info info) {
+  napi_value a[4];
+  tjh_conv2d_desc d;
+  if (!get_args(env, info, 4, a) || !conv_desc(env, a[0], &d)) return NULL;
+  CHECK_RC(tjh_conv2d_backward_input(&d, CF32(a[1]), CF32(a[2]), F32(a[3])));
+  return undef(env);
+}
+static napi_value js_conv_backward_weight(napi_env env, napi_callback_info info) {
+  napi_value a[5];
+  tjh_conv2d_desc d;
+  if (!get_args(env, info, 5, a) || !conv_desc(env, a[0], &d)) return NULL;
+  CHECK_RC(tjh_conv2d_backward_weight(&d, CF32(a[1]), CF32(a[2]), F32(a[3]), (int)i64(env, a[4])));
+  return undef(env);
+}
+
 /* ---------------------------------------------------------------- module */
 
 #define FN(name, fn)                                                              \
@@ -542,7 +825,22 @@ static napi_value init_module(napi_env env, napi_value exports) {
       FN("layerNormBackward", js_ln_backward), FN("embeddingForward", js_emb_forward),
       FN("embeddingBackward", js_emb_backward), FN("gemm", js_gemm),
       FN("sdpaForward", js_sdpa_forward), FN("sdpaBackward", js_sdpa_backward),
-      FN("adamStep", js_adam_step),
+      FN("adamStep", js_adam_step), FN("isInitialized", js_is_initialized),
+      FN("deviceCount", js_device_count), FN("free", js_free), FN("resetPeak", js_reset_peak),
+      FN("d2d", js_d2d), FN("kprofEnable", js_kprof_enable), FN("kprofFilter", js_kprof_filter),
+      FN("kprofReset", js_kprof_reset), FN("kprofQuery", js_kprof_query),
+      FN("kprofNames", js_kprof_names), FN("timerStart", js_timer_start),
+      FN("timerStop", js_timer_stop), FN("fillI32", js_fill_i32),
+      FN("copyStridedI32", js_copy_strided_i32), FN("castF32I32", js_cast_f32_i32),
+      FN("castI32F32", js_cast_i32_f32), FN("ternary", js_ternary),
+      FN("powScalarBackward", js_pow_scalar_backward), FN("axpy", js_axpy),
+      FN("maskedFill", js_masked_fill), FN("compare", js_compare), FN("argmax", js_argmax),
+      FN("nllLossForward", js_nll_forward), FN("nllLossBackward", js_nll_backward),
+      FN("indexSelect", js_index_select), FN("indexAdd", js_index_add), FN("gather", js_gather),
+      FN("scatterAdd", js_scatter_add), FN("oneHot", js_one_hot), FN("oneHotI32", js_one_hot_i32),
+      FN("nonzero", js_nonzero), FN("conv2dForward", js_conv_forward),
+      FN("conv2dBackwardInput", js_conv_backward_input),
+      FN("conv2dBackwardWeight", js_conv_backward_weight),
   };
   napi_define_properties(env, exports, sizeof(desc) / sizeof(desc[0]), desc);
   napi_value v;
