@@ -66,10 +66,12 @@ struct GemmArgs {
 // per outer row); TRANS: storage [k][outer] (outer contiguous).
 // EDGE == false: the caller guarantees the tile is in bounds and 16-byte
 // aligned, so every load is an unconditional 128-bit load.  EDGE == true:
-// every element is guarded (tiles on the problem's edge, unaligned data).
+// every 4-run is bounds-checked (tiles on the problem's edge); `vec` (the
+// operand is 16-byte aligned with a row stride divisible by 4) lets runs
+// that are wholly in bounds load as one 128-bit access.
 template <bool TRANS, int OUTER, int V, bool EDGE>
 __device__ __forceinline__ void load_tile(const float* __restrict__ P, int64_t ld, int64_t rows,
-                                          int64_t cols, int64_t r0, int64_t c0,
+                                          int64_t cols, int64_t r0, int64_t c0, bool vec,
                                           floatx4 (&reg)[V]) {
   const int t = threadIdx.x;
 #pragma unroll
@@ -85,10 +87,16 @@ __device__ __forceinline__ void load_tile(const float* __restrict__ P, int64_t l
         reg[i] = *reinterpret_cast<const floatx4*>(P + (c0 + k) * ld + r0 + oq * 4);
       }
     } else {
+      // guarded: a 4-run wholly in bounds of an aligned operand is still
+      // one 128-bit load; only runs that cross an edge go element-wise
       float v[4];
       if (!TRANS) {
         int o = f >> 2, kq = f & 3;
         int64_t go = r0 + o, gk = c0 + kq * 4;
+        if (vec && go < rows && gk + 3 < cols) {
+          reg[i] = *reinterpret_cast<const floatx4*>(P + go * ld + gk);
+          continue;
+        }
 #pragma unroll
         for (int j = 0; j < 4; ++j)
           v[j] = (go < rows && gk + j < cols) ? P[go * ld + gk + j] : 0.f;
@@ -96,6 +104,10 @@ __device__ __forceinline__ void load_tile(const float* __restrict__ P, int64_t l
         constexpr int Q = OUTER / 4;
         int k = f / Q, oq = f % Q;
         int64_t gk = c0 + k, go = r0 + oq * 4;
+        if (vec && gk < cols && go + 3 < rows) {
+          reg[i] = *reinterpret_cast<const floatx4*>(P + gk * ld + go);
+          continue;
+        }
 #pragma unroll
         for (int j = 0; j < 4; ++j)
           v[j] = (gk < cols && go + j < rows) ? P[gk * ld + go + j] : 0.f;
@@ -188,8 +200,8 @@ __global__ __launch_bounds__(kThreads, 2) void k_gemm(GemmArgs g) {
   //    (k contiguous, like !TA) and [K][N] when !TB (n contiguous, like TA).
   const int64_t ktiles = kend > kbeg ? cdiv(kend - kbeg, BK) : 0;
   floatx4 ra[VA], rb[VB];
-  load_tile<TA, BM, VA, EDGE>(A, g.lda, g.M, kend, m0, kbeg, ra);
-  load_tile<!TB, BN, VB, EDGE>(B, g.ldb, g.N, kend, n0, kbeg, rb);
+  load_tile<TA, BM, VA, EDGE>(A, g.lda, g.M, kend, m0, kbeg, g.vecA, ra);
+  load_tile<!TB, BN, VB, EDGE>(B, g.ldb, g.N, kend, n0, kbeg, g.vecB, rb);
   store_tile<TA, BM, VA, LA>(As[0], ra);
   store_tile<!TB, BN, VB, LB>(Bs[0], rb);
   __syncthreads();
@@ -199,8 +211,8 @@ __global__ __launch_bounds__(kThreads, 2) void k_gemm(GemmArgs g) {
     const bool more = kt + 1 < ktiles;
     if (more) {
       const int64_t k0 = kbeg + (kt + 1) * BK;
-      load_tile<TA, BM, VA, EDGE>(A, g.lda, g.M, kend, m0, k0, ra);
-      load_tile<!TB, BN, VB, EDGE>(B, g.ldb, g.N, kend, n0, k0, rb);
+      load_tile<TA, BM, VA, EDGE>(A, g.lda, g.M, kend, m0, k0, g.vecA, ra);
+      load_tile<!TB, BN, VB, EDGE>(B, g.ldb, g.N, kend, n0, k0, g.vecB, rb);
     }
     const float* __restrict__ as = As[cur] + wm * WM + l32;
     const float* __restrict__ bs = Bs[cur] + wn * WN + l32;
@@ -328,11 +340,14 @@ double fill_of(int64_t wgs, int cus) {
   return r / (double)cdiv(wgs, cus);
 }
 
-// Split-K factor for `tiles` output tiles: K slices of >= 256, at most 64,
-// chosen for the best fill once the tiles alone cannot fill the CUs twice.
+// Split-K factor for `tiles` output tiles: K slices of >= 256 (>= 64 when
+// the tiles would occupy fewer than half the CUs), at most 64, chosen for
+// the best fill once the tiles alone cannot fill the CUs twice.
 int64_t choose_splits(int64_t tiles, int64_t K, int cus) {
-  if (tiles >= 2LL * cus || K < 4 * 256) return 1;
-  int64_t smax = K / 256;
+  if (tiles >= 2LL * cus) return 1;
+  const int64_t slice = 2 * tiles < cus ? 64 : 256;
+  if (K < 4 * slice) return 1;
+  int64_t smax = K / slice;
   if (smax > 64) smax = 64;
   int64_t best = 1;
   double best_f = -1.0;
