@@ -327,6 +327,24 @@ def test_gemm_layouts(torch, M, N, K, ta, tb):
     check(got, want, rtol=1e-4, atol=1e-5 * np.sqrt(K) * 4)
 
 
+@pytest.mark.parametrize("tile", ["256x128", "128x128", "128x64", "64x64"])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("M,N,K", [(300, 260, 200), (256, 128, 4096)])
+def test_gemm_every_tile(torch, monkeypatch, tile, ta, tb, M, N, K):
+    # every tile on both kernels: an interior block (K steps of 32), edge
+    # strips and a K remainder (first shape), split-K on one tile (second)
+    monkeypatch.setenv("TJH_GEMM_TILE", tile)
+    r = np.random.default_rng(M + N + K + ta * 2 + tb)
+    A = f32(r.standard_normal((K, M) if ta else (M, K)))
+    B = f32(r.standard_normal((N, K) if tb else (K, N)))
+    bias = f32(r.standard_normal(N))
+    C0 = f32(r.standard_normal((M, N)))
+    want = 0.5 * ((A.T if ta else A).astype(np.float64) @ (B.T if tb else B).astype(np.float64))
+    want += 0.25 * C0 + bias
+    got = _raw_gemm(torch, ta, tb, A, B, M, N, K, alpha=0.5, beta=0.25, C0=C0, bias=bias, bmode=1)
+    check(got, want, rtol=1e-4, atol=1e-5 * np.sqrt(K) * 4)
+
+
 def test_gemm_epilogue(torch):
     r = np.random.default_rng(13)
     M, N, K = 70, 90, 50

@@ -315,13 +315,14 @@ constexpr TileCfg kTiles[] = {{256, 128}, {128, 128}, {128, 64}, {64, 64}};
 constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
 
 // Measured relative per-FLOP throughput of each tile with the CUs full, by
-// operand layout (GPT-2 products on MI355X): with B read k-contiguous
-// (NT, the forward) 128x128 is fastest; with B read n-contiguous (NN dgrad,
-// TN wgrad) the 128x64 tile's higher occupancy wins.
+// operand layout (GPT-2 products on MI355X, every tile forced in turn):
+// 128x128 is fastest or within noise of it for every layout once it fills
+// the CUs (with a K split where K is long); 128x64 is 3-5% slower per FLOP
+// and wins only where 128x128 leaves CUs idle.
 float tile_speed(int ti, int ta, int tb) {
   static const float nt[kNumTiles] = {0.85f, 1.00f, 0.95f, 0.85f};
-  static const float nn[kNumTiles] = {0.80f, 0.91f, 1.00f, 0.85f};
-  static const float tn[kNumTiles] = {0.80f, 0.93f, 1.00f, 0.85f};
+  static const float nn[kNumTiles] = {0.85f, 1.00f, 0.97f, 0.85f};
+  static const float tn[kNumTiles] = {0.85f, 1.00f, 0.97f, 0.85f};
   if (!ta && tb) return nt[ti];
   if (!ta && !tb) return nn[ti];
   if (ta && !tb) return tn[ti];
@@ -365,18 +366,15 @@ int64_t choose_splits(int64_t tiles, int64_t K, int cus) {
 }
 
 // Picks tile and split maximising (useful fraction of padded work) x
-// (CU fill) x tile speed.  TJH_GEMM_TILE=BMxBN forces a tile.
+// (CU fill) x tile speed.  TJH_GEMM_TILE=BMxBN forces a tile (read on every
+// call, so a test can sweep the tiles in one process).
 Plan choose_plan(int64_t M, int64_t N, int64_t K, int64_t batch, int cus, int ta, int tb) {
-  static int forced = -2;
-  if (forced == -2) {
-    forced = -1;
-    const char* e = getenv("TJH_GEMM_TILE");
-    if (e) {
-      for (int i = 0; i < kNumTiles; ++i) {
-        char buf[32];
-        snprintf(buf, sizeof(buf), "%dx%d", kTiles[i].bm, kTiles[i].bn);
-        if (strcmp(buf, e) == 0) forced = i;
-      }
+  int forced = -1;
+  if (const char* e = getenv("TJH_GEMM_TILE")) {
+    for (int i = 0; i < kNumTiles; ++i) {
+      char buf[32];
+      snprintf(buf, sizeof(buf), "%dx%d", kTiles[i].bm, kTiles[i].bn);
+      if (strcmp(buf, e) == 0) forced = i;
     }
   }
   Plan best{1, 1};
