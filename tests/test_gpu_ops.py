@@ -213,6 +213,28 @@ def test_cross_entropy(torch, rows, cols, red):
     check(xt.grad.numpy(), ops.cross_entropy_backward(x, t, gl, red), **RED)
 
 
+@pytest.mark.parametrize("rows,cols,ld", [(37, 50257, 50260), (19, 4100, 4100), (5, 2049, 2052)])
+@pytest.mark.parametrize("red", ["mean", "none"])
+def test_cross_entropy_aligned_rows(torch, rows, cols, ld, red):
+    # logits whose rows start 16-byte aligned (a column slice of a wider
+    # tensor, like the LM head's padded output): the flat backward path
+    r = np.random.default_rng(rows * 3 + cols)
+    full = f32(r.standard_normal((rows, ld)) * 2)
+    t = r.integers(0, cols, rows).astype(np.int32)
+    t[::4] = -100
+    t[1] = cols - 1  # target in the last, partial 4-column chunk
+    ft = torch.tensor(full, requires_grad=True)
+    x = ft[:, :cols]
+    loss = torch.F.cross_entropy(x, torch.tensor(t), reduction=red)
+    gl = f32(r.standard_normal(rows)) if red == "none" else np.float32(0.7)
+    loss.backward(torch.tensor(gl))
+    xs = full[:, :cols]
+    check(loss.numpy(), ops.cross_entropy(xs, t, red), **RED)
+    g = ft.grad.numpy()
+    check(g[:, :cols], ops.cross_entropy_backward(xs, t, gl, red), **RED)
+    assert not g[:, cols:].any()
+
+
 def test_nll_loss(torch):
     r = np.random.default_rng(11)
     lp = ops.log_softmax(r.standard_normal((9, 6))).astype(np.float32)

@@ -276,6 +276,66 @@ __global__ __launch_bounds__(kBlock) void k_ce_bwd(const float* __restrict__ x, 
   }
 }
 
+// Wide rows, flat: the padded matrix is one stream of rows * ld/4 float4;
+// a lane takes 4 at a time (loads issued first), the row comes from one
+// 32-bit division, columns past `cols` (row padding) are skipped.
+__global__ __launch_bounds__(kBlock) void k_ce_bwd_flat(
+    const float* __restrict__ x, uint32_t ld4, uint32_t total4, const int32_t* __restrict__ t,
+    const float* __restrict__ lse, const float* __restrict__ gout,
+    const float* __restrict__ count, int64_t cols, int32_t ignore, int reduction,
+    float* __restrict__ d, int accumulate) {
+  const float inv = count ? 1.0f / count[0] : 1.0f;
+  const uint32_t stride = gridDim.x * kBlock * 4;
+  for (uint32_t v0 = blockIdx.x * kBlock * 4 + threadIdx.x; v0 < total4; v0 += stride) {
+    // loads first: whole in-bounds chunks as one 128-bit access, a chunk
+    // crossing `cols` element-wise (nothing past `cols` is read)
+    float4 xv[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const uint32_t v = v0 + u * kBlock;
+      if (v >= total4) continue;
+      const uint32_t r = v / ld4;
+      const int64_t c = 4 * (int64_t)(v - r * ld4);
+      if (c + 4 <= cols) {
+        xv[u] = ld_nt(x + 4 * (size_t)v);
+      } else if (c < cols) {
+        const float* xp = x + 4 * (size_t)v;
+        xv[u] = make_float4(xp[0], c + 1 < cols ? xp[1] : 0.f, c + 2 < cols ? xp[2] : 0.f, 0.f);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const uint32_t v = v0 + u * kBlock;
+      if (v >= total4) continue;
+      const uint32_t r = v / ld4;
+      const int64_t c = 4 * (int64_t)(v - r * ld4);
+      if (c >= cols) continue;
+      const int32_t tr = t[r];
+      const bool valid = !(tr == ignore || tr < 0 || tr >= cols);
+      const float sc = valid ? ce_scale(gout, reduction, r, inv) : 0.f;
+      const float l = lse[r];
+      float e[4] = {xv[u].x, xv[u].y, xv[u].z, xv[u].w};
+      float o[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        o[j] = (c + j < cols) ? (__expf(e[j] - l) - (c + j == tr ? 1.f : 0.f)) * sc : 0.f;
+      float* dp = d + 4 * (size_t)v;
+      if (c + 4 <= cols) {
+        float4 ov = make_float4(o[0], o[1], o[2], o[3]);
+        if (accumulate) {
+          const float4 q = *reinterpret_cast<const float4*>(dp);
+          ov.x += q.x; ov.y += q.y; ov.z += q.z; ov.w += q.w;
+          *reinterpret_cast<float4*>(dp) = ov;
+        } else {
+          st_nt(dp, ov);
+        }
+      } else {
+        for (int j = 0; j < 4 && c + j < cols; ++j) dp[j] = accumulate ? dp[j] + o[j] : o[j];
+      }
+    }
+  }
+}
+
 // count of valid targets (for mean) into one float.
 __global__ __launch_bounds__(kBlock) void k_count_valid(const int32_t* __restrict__ t, int64_t rows,
                                                         int64_t cols, int32_t ignore,
@@ -318,7 +378,9 @@ __global__ __launch_bounds__(kBlock) void k_nll_bwd(const int32_t* __restrict__ 
 // ------------------------------------------------------------- layer norm
 
 // Wave per row, the row kept in registers: cols % 4 == 0, cols <= 64*4*V4.
-template <int V4>
+// EXACT: cols == 256 * V4, so every lane owns V4 whole float4 and no lane
+// guard is needed (the guards otherwise split the loads across branches).
+template <int V4, bool EXACT>
 __global__ __launch_bounds__(kBlock) void k_ln_fwd_wave(const float* __restrict__ x,
                                                         const float* __restrict__ gamma,
                                                         const float* __restrict__ beta,
@@ -336,7 +398,7 @@ __global__ __launch_bounds__(kBlock) void k_ln_fwd_wave(const float* __restrict_
 #pragma unroll
   for (int j = 0; j < V4; ++j) {
     int i = lane + 64 * j;
-    if (i < c4) {
+    if (EXACT || i < c4) {
       v[j] = xr[i];
       s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
     } else {
@@ -348,7 +410,7 @@ __global__ __launch_bounds__(kBlock) void k_ln_fwd_wave(const float* __restrict_
 #pragma unroll
   for (int j = 0; j < V4; ++j) {
     int i = lane + 64 * j;
-    if (i < c4) {
+    if (EXACT || i < c4) {
       float a = v[j].x - mean, b = v[j].y - mean, c = v[j].z - mean, d = v[j].w - mean;
       q += (a * a + b * b) + (c * c + d * d);
     }
@@ -361,7 +423,7 @@ __global__ __launch_bounds__(kBlock) void k_ln_fwd_wave(const float* __restrict_
 #pragma unroll
   for (int j = 0; j < V4; ++j) {
     int i = lane + 64 * j;
-    if (i < c4) {
+    if (EXACT || i < c4) {
       float4 o;
       o.x = (v[j].x - mean) * rstd;
       o.y = (v[j].y - mean) * rstd;
@@ -422,7 +484,8 @@ __global__ __launch_bounds__(kBlock) void k_ln_fwd_block(const float* __restrict
 // Block b owns rows [b*rpb, (b+1)*rpb); wave w takes rows b*rpb + w + 4k.
 // Lane owns columns 4*(lane + 64*j) .. +3 (cols % 4 == 0, cols <= 256*V4).
 // Partials: pg/pb [nblocks, cols].
-template <int V4>
+// EXACT as for k_ln_fwd_wave.
+template <int V4, bool EXACT>
 __global__ __launch_bounds__(kBlock) void k_ln_bwd_wave(const float* __restrict__ dy,
                                                         const float* __restrict__ x,
                                                         const float* __restrict__ gamma,
@@ -442,15 +505,15 @@ __global__ __launch_bounds__(kBlock) void k_ln_bwd_wave(const float* __restrict_
     ag[j] = make_float4(0.f, 0.f, 0.f, 0.f);
     ab[j] = make_float4(0.f, 0.f, 0.f, 0.f);
     int i = lane + 64 * j;
-    gm[j] = (gamma && i < c4) ? reinterpret_cast<const float4*>(gamma)[i]
+    gm[j] = (gamma && (EXACT || i < c4)) ? reinterpret_cast<const float4*>(gamma)[i]
                               : make_float4(1.f, 1.f, 1.f, 1.f);
   }
   const float inv_n = 1.0f / (float)cols;
   int64_t r_beg = (int64_t)blockIdx.x * rpb;
   int64_t r_end = r_beg + rpb < rows ? r_beg + rpb : rows;
-  // two rows per wave per step: both rows' loads are issued before either
+  // four rows per wave per step: all four rows' loads are issued before any
   // row's reductions
-  constexpr int kPair = 2;
+  constexpr int kPair = 4;
   constexpr int kStep = kBlock / 64;
   for (int64_t r0 = r_beg + w; r0 < r_end; r0 += kStep * kPair) {
     float4 gv[kPair][V4], xh[kPair][V4];
@@ -466,7 +529,7 @@ __global__ __launch_bounds__(kBlock) void k_ln_bwd_wave(const float* __restrict_
 #pragma unroll
         for (int j = 0; j < V4; ++j) {
           const int i = lane + 64 * j;
-          if (i < c4) {
+          if (EXACT || i < c4) {
             gv[q][j] = ld_nt(reinterpret_cast<const float*>(g4 + i));
             xh[q][j] = ld_nt(reinterpret_cast<const float*>(x4 + i));
           }
@@ -481,7 +544,7 @@ __global__ __launch_bounds__(kBlock) void k_ln_bwd_wave(const float* __restrict_
 #pragma unroll
       for (int j = 0; j < V4; ++j) {
         const int i = lane + 64 * j;
-        if (i < c4) {
+        if (EXACT || i < c4) {
           const float4 g = gv[q][j], xv = xh[q][j];
           xh[q][j] = make_float4((xv.x - mu[q]) * rs[q], (xv.y - mu[q]) * rs[q],
                                  (xv.z - mu[q]) * rs[q], (xv.w - mu[q]) * rs[q]);
@@ -501,7 +564,7 @@ __global__ __launch_bounds__(kBlock) void k_ln_bwd_wave(const float* __restrict_
 #pragma unroll
         for (int j = 0; j < V4; ++j) {
           const int i = lane + 64 * j;
-          if (i < c4) {
+          if (EXACT || i < c4) {
             float4 o;
             o.x = rs[q] * (gv[q][j].x * gm[j].x - s1 - xh[q][j].x * s2);
             o.y = rs[q] * (gv[q][j].y * gm[j].y - s1 - xh[q][j].y * s2);
@@ -699,7 +762,15 @@ int tjh_cross_entropy_backward(const float* logits, int64_t ld, const int32_t* t
     hipLaunchKernelGGL(k_ce_bwd<true>, dim3((unsigned)cdiv(rows, 4)), dim3(kBlock), 0, stream(),
                        logits, ld, targets, lse, grad_out, cnt.as<float>(), rows, cols,
                        ignore_index, reduction, dlogits, ldd, accumulate);
-  else
+  else if (ld == ldd && ld % 4 == 0 && aligned16(logits) && aligned16(dlogits) &&
+           rows * (ld / 4) < (int64_t(1) << 31)) {
+    const int64_t total4 = rows * (ld / 4);
+    const int64_t grid = cdiv(total4, (int64_t)kBlock * 4) < 16384 ? cdiv(total4, (int64_t)kBlock * 4)
+                                                                   : 16384;
+    hipLaunchKernelGGL(k_ce_bwd_flat, dim3((unsigned)grid), dim3(kBlock), 0, stream(), logits,
+                       (uint32_t)(ld / 4), (uint32_t)total4, targets, lse, grad_out,
+                       cnt.as<float>(), cols, ignore_index, reduction, dlogits, accumulate);
+  } else
     hipLaunchKernelGGL(k_ce_bwd<false>, dim3((unsigned)rows), dim3(kBlock), 0, stream(), logits,
                        ld, targets, lse, grad_out, cnt.as<float>(), rows, cols, ignore_index,
                        reduction, dlogits, ldd, accumulate);
@@ -754,12 +825,15 @@ int tjh_layer_norm_forward(const float* x, const float* gamma, const float* beta
   bool vec = cols % 4 == 0 && aligned16(x) && aligned16(y) && (!gamma || aligned16(gamma)) &&
              (!beta || aligned16(beta));
   unsigned g = (unsigned)cdiv(rows, 4);
-  if (vec && cols <= 64 * 4 * 4) {
-    hipLaunchKernelGGL(k_ln_fwd_wave<4>, dim3(g), dim3(kBlock), 0, stream(), x, gamma, beta, y,
-                       mean, rstd, rows, cols, eps);
+  if (vec && cols == 64 * 4 * 3) {
+    hipLaunchKernelGGL((k_ln_fwd_wave<3, true>), dim3(g), dim3(kBlock), 0, stream(), x, gamma,
+                       beta, y, mean, rstd, rows, cols, eps);
+  } else if (vec && cols <= 64 * 4 * 4) {
+    hipLaunchKernelGGL((k_ln_fwd_wave<4, false>), dim3(g), dim3(kBlock), 0, stream(), x, gamma,
+                       beta, y, mean, rstd, rows, cols, eps);
   } else if (vec && cols <= 64 * 4 * 16) {
-    hipLaunchKernelGGL(k_ln_fwd_wave<16>, dim3(g), dim3(kBlock), 0, stream(), x, gamma, beta, y,
-                       mean, rstd, rows, cols, eps);
+    hipLaunchKernelGGL((k_ln_fwd_wave<16, false>), dim3(g), dim3(kBlock), 0, stream(), x, gamma,
+                       beta, y, mean, rstd, rows, cols, eps);
   } else {
     hipLaunchKernelGGL(k_ln_fwd_block, dim3((unsigned)rows), dim3(kBlock), 0, stream(), x, gamma,
                        beta, y, mean, rstd, cols, eps);
@@ -784,10 +858,11 @@ int tjh_layer_norm_backward(const float* dy, const float* x, const float* gamma,
              (!gamma || aligned16(gamma));
   int v4 = cols <= 64 * 4 * 3 ? 3 : (cols <= 64 * 4 * 6 ? 6 : (cols <= 64 * 4 * 12 ? 12 : 0));
   if (vec && v4) {
-    // rows per block: ~4 blocks per CU, >= 8 rows each
+    // rows per block: ~2 blocks per CU, >= 16 rows each (fewer partial
+    // rows for the dgamma/dbeta pass; measured faster than 4 per CU)
     int cus = num_cus() > 0 ? num_cus() : 256;
-    int64_t rpb = cdiv(rows, 4LL * cus);
-    if (rpb < 8) rpb = 8;
+    int64_t rpb = cdiv(rows, 2LL * cus);
+    if (rpb < 16) rpb = 16;
     int64_t nb = cdiv(rows, rpb);
     Scratch part(want_p ? (size_t)(2 * nb * cols) * sizeof(float) : 0);
     if (want_p && !part.ok()) return set_error(TJH_ERR_OOM, "layer_norm_backward: no scratch");
@@ -795,15 +870,18 @@ int tjh_layer_norm_backward(const float* dy, const float* x, const float* gamma,
     float* pb = want_p ? part.as<float>() + nb * cols : nullptr;
     {
       KernelScope ks("layer_norm_bwd");
-      if (v4 == 3)
-        hipLaunchKernelGGL(k_ln_bwd_wave<3>, dim3((unsigned)nb), dim3(kBlock), 0, stream(), dy, x,
-                           gamma, mean, rstd, dx, pg, pb, rows, cols, rpb);
+      if (v4 == 3 && cols == 64 * 4 * 3)
+        hipLaunchKernelGGL((k_ln_bwd_wave<3, true>), dim3((unsigned)nb), dim3(kBlock), 0, stream(),
+                           dy, x, gamma, mean, rstd, dx, pg, pb, rows, cols, rpb);
+      else if (v4 == 3)
+        hipLaunchKernelGGL((k_ln_bwd_wave<3, false>), dim3((unsigned)nb), dim3(kBlock), 0, stream(),
+                           dy, x, gamma, mean, rstd, dx, pg, pb, rows, cols, rpb);
       else if (v4 == 6)
-        hipLaunchKernelGGL(k_ln_bwd_wave<6>, dim3((unsigned)nb), dim3(kBlock), 0, stream(), dy, x,
-                           gamma, mean, rstd, dx, pg, pb, rows, cols, rpb);
+        hipLaunchKernelGGL((k_ln_bwd_wave<6, false>), dim3((unsigned)nb), dim3(kBlock), 0, stream(),
+                           dy, x, gamma, mean, rstd, dx, pg, pb, rows, cols, rpb);
       else
-        hipLaunchKernelGGL(k_ln_bwd_wave<12>, dim3((unsigned)nb), dim3(kBlock), 0, stream(), dy, x,
-                           gamma, mean, rstd, dx, pg, pb, rows, cols, rpb);
+        hipLaunchKernelGGL((k_ln_bwd_wave<12, false>), dim3((unsigned)nb), dim3(kBlock), 0,
+                           stream(), dy, x, gamma, mean, rstd, dx, pg, pb, rows, cols, rpb);
       int rc = check_launch("layer_norm_backward");
       if (rc != TJH_OK) return rc;
       if (want_p) {
