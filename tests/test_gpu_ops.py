@@ -552,6 +552,46 @@ def test_conv2d(torch, N, C, H, W, OC, k, s, p, d, grp):
     check(gb, db, rtol=1e-4, atol=2e-3)
 
 
+@pytest.mark.parametrize("N,C,H,W,OC,kh,kw,s,p,d,grp", [
+    (2, 4, 9, 11, 6, 2, 3, (2, 1), (0, 1), (1, 2), 2),   # rectangular everything, groups
+    (3, 5, 8, 8, 7, 3, 1, (3, 2), (2, 0), (2, 1), 1),    # stride 3 skips input rows
+    (1, 6, 13, 5, 6, 3, 3, 1, 1, 1, 6),                  # depthwise
+    (5, 33, 12, 12, 130, 3, 3, 1, 1, 1, 1),              # M, N and K edges of every tile
+    (2, 3, 10, 9, 4, 2, 2, 3, 0, 1, 1),                  # kernel < stride: untouched pixels
+    (3, 8, 15, 14, 5, 5, 3, (2, 3), (2, 1), 1, 1)])      # stride classes of unequal size
+def test_conv2d_shapes(torch, N, C, H, W, OC, kh, kw, s, p, d, grp):
+    r = np.random.default_rng(N * 100 + C + OC)
+    x = f32(r.standard_normal((N, C, H, W)))
+    w = f32(r.standard_normal((OC, C // grp, kh, kw)) * 0.2)
+    b = f32(r.standard_normal(OC))
+    out, g, (gx, gw, gb) = grad_of(
+        torch, lambda a, ww, bb: torch.F.conv2d(a, ww, bb, s, p, d, grp), x, w, b)
+    check(out, ops.conv2d(x, w, b, s, p, d, grp), rtol=1e-4, atol=1e-4)
+    dx, dw, db = ops.conv2d_backward(g, x, w, s, p, d, grp)
+    check(gx, dx, rtol=1e-4, atol=1e-4)
+    check(gw, dw, rtol=1e-4, atol=2e-3)
+    check(gb, db, rtol=1e-4, atol=2e-3)
+
+
+@pytest.mark.parametrize("N,H", [(2, 9), (16, 64)])  # one K slice, and a split K
+def test_conv2d_weight_grad_accumulates(torch, N, H):
+    """tjh_conv2d_backward_weight with accumulate != 0 adds into dW."""
+    import ctypes
+    from torchjs_amd import _lib as L
+    r = np.random.default_rng(N + H)
+    C, OC, k = 3, 8, 3
+    x = f32(r.standard_normal((N, C, H, H)))
+    g = f32(r.standard_normal((N, OC, H, H)))
+    w = f32(r.standard_normal((OC, C, k, k)))
+    dw0 = f32(r.standard_normal((OC, C, k, k)))
+    desc = L.Conv2dDesc(N, C, H, H, OC, k, k, 1, 1, 1, 1, 1, 1, 1, H, H)
+    xt, gt, dwt = torch.tensor(x), torch.tensor(g), torch.tensor(dw0)
+    L.check(L.lib().tjh_conv2d_backward_weight(ctypes.byref(desc), gt.data_ptr(), xt.data_ptr(),
+                                               dwt.data_ptr(), 1), "conv2d_backward_weight")
+    _, want, _ = ops.conv2d_backward(g, x, w, 1, 1, 1, 1)
+    check(dwt.numpy(), dw0 + want, rtol=1e-4, atol=2e-3)
+
+
 # ------------------------------------------------------------------ optimizers
 
 
