@@ -491,6 +491,28 @@ def test_sdpa_flash_gpt2_layout(torch, T, causal):
     check(gqkv, np.concatenate([un(gq), un(gk), un(gv)], -1), rtol=1e-4, atol=1e-4)
 
 
+@pytest.mark.parametrize("Tq,Tk,causal", [(50, 97, True), (130, 64, True), (45, 200, False),
+                                          (257, 33, False)])
+def test_sdpa_flash_cross_lengths(torch, Tq, Tk, causal):
+    """Head dim 64 with different, ragged query and key lengths: the dS
+    blocks the key kernel stores cover exactly what the query kernel reads."""
+    r = np.random.default_rng(Tq * 1000 + Tk)
+    B, H, D = 2, 3, 64
+    q = f32(r.standard_normal((B, H, Tq, D)))
+    k = f32(r.standard_normal((B, H, Tk, D)))
+    v = f32(r.standard_normal((B, H, Tk, D)))
+    out, g, (gq, gk, gv) = grad_of(
+        torch, lambda a, b, c: torch.F.scaled_dot_product_attention(a, b, c, is_causal=causal),
+        q, k, v)
+    f64 = lambda z: z.astype(np.float64)
+    o, _ = ops.sdpa(f64(q), f64(k), f64(v), causal)
+    check(out, o, rtol=1e-4, atol=1e-5)
+    wq, wk, wv = ops.sdpa_backward(f64(g), f64(q), f64(k), f64(v), causal)
+    check(gq, wq, rtol=1e-4, atol=1e-4)
+    check(gk, wk, rtol=1e-4, atol=1e-4)
+    check(gv, wv, rtol=1e-4, atol=1e-4)
+
+
 def test_split_and_narrow_gradients(torch):
     """Pieces of a split that are unused, overlapping narrows and a reused
     piece: the input gradient is the sum over every use (zero elsewhere)."""

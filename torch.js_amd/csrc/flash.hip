@@ -22,8 +22,11 @@
 // Forward: S^T = K Q^T per 32-key block (lane <-> query), online softmax
 //   per query in base 2, O^T += V^T P^T; lse written for the backward.
 // Backward (deterministic, no atomics): D = rowsum(dO*O); a key-block
-//   kernel accumulates dV^T = dO^T P and dK^T = Q^T dS (lane <-> key); a
-//   query-block kernel accumulates dQ^T = K^T dS^T (lane <-> query).
+//   kernel accumulates dV^T = dO^T P and dK^T = Q^T dS (lane <-> key) and
+//   stores each 32x32 block of dS; a query-block kernel accumulates
+//   dQ^T = K^T dS^T (lane <-> query) from those blocks, so S and dP are
+//   computed once (when the blocks cannot be allocated, the query kernel
+//   recomputes them instead).
 // Causal masking (key > query masked, top-left aligned) skips every
 // 32x32 tile that is entirely masked and masks element-wise only on tiles
 // that cross the diagonal or the end of the sequence.
@@ -74,7 +77,18 @@ struct FlashArgs {
   int causal;
   int nblk;           // row blocks per (b, h)
   int cus;            // compute units per XCD
+  // dS blocks written by the key-block kernel for the query-block kernel:
+  // [b*H + h][query tile][key tile][32 x 32], or null (dQ recomputes dS)
+  float* dsblk;
+  int nqt, nkt;       // 32-row query / key tiles per (b, h)
 };
+
+// Column of key offset ko (0..31) inside a dS block row: the query-block
+// kernel's lane (query row, h) reads its 16 keys kappa(j, h), j = 0..15, as
+// one contiguous run at h*16, so key kappa(j, h) sits at h*16 + j.
+__device__ __forceinline__ int ds_col(int ko) {
+  return ((ko >> 2) & 1) * 16 + (((ko >> 3) << 2) | (ko & 3));
+}
 
 // Cost rank of the item a workgroup processes (rank 0 = most expensive).
 // Workgroup w runs on XCD w % 8, and the j-th workgroup an XCD receives
@@ -419,6 +433,16 @@ __global__ __launch_bounds__(256, 2) void k_flash_dkv(FlashArgs a) {
       lds_cols(Qs[cur], l32, h, ct);
 #pragma unroll
       for (int j = 0; j < 16; ++j) dp[j] *= p[j];  // dS
+      if (a.dsblk) {
+        // this lane's key column of the (query tile, key tile) dS block;
+        // masked entries are 0, so the block is complete.  Non-temporal:
+        // the blocks are read once, by the next kernel
+        float* blk = a.dsblk +
+                     (((int64_t)bh * a.nqt + qq0 / TILE) * a.nkt + k0 / TILE) * (TILE * TILE) +
+                     ds_col(l32);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) __builtin_nontemporal_store(dp[j], blk + kappa(j, h) * TILE);
+      }
 #pragma unroll
       for (int s = 0; s < 16; ++s) {  // dK^T += Q^T dS
         dk0 = mfma(ct[0][s], dp[s], dk0);
@@ -525,6 +549,83 @@ __global__ __launch_bounds__(256, 2) void k_flash_dq(FlashArgs a) {
   write_rows(buf, dq0, dq1, a.scale, dqb, a.o1s.t, q0, a.Tq, l32, h, lane);
 }
 
+// Query-block kernel from stored dS: dQ^T = K^T dS^T for 128 queries per
+// workgroup, reading the 32x32 dS blocks the key-block kernel wrote (each
+// lane's 16 values are one contiguous run) instead of recomputing S and dP.
+// GUARD: Tk is not a multiple of 32.
+template <bool GUARD>
+__global__ __launch_bounds__(256, 2) void k_flash_dq_ds(FlashArgs a) {
+  // two K tiles in flight; all four buffers stage the waves' dQ rows at the end
+  __shared__ __attribute__((aligned(16))) float Ks[WAVES][TILE * LDSW];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int l32 = lane & 31, h = lane >> 5;
+  const int64_t nbh = (int64_t)gridDim.x / a.nblk;
+  const int g = balanced_rank(blockIdx.x, gridDim.x, a.cus);
+  const int64_t bh = g % nbh;
+  const int qb = a.nblk - 1 - (int)(g / nbh);
+  const int64_t b = bh / a.H, hh = bh % a.H;
+  const float* K = a.k + b * a.ks.b + hh * a.ks.h;
+  const int q0 = qb * ROWS + w * TILE;
+  const bool wave_in = q0 < a.Tq;
+  // this wave's row of dS blocks; lane (l32, h) reads 16 floats per block
+  const float* dsrow = a.dsblk +
+                       ((int64_t)bh * a.nqt + (wave_in ? q0 / TILE : 0)) * a.nkt * (TILE * TILE) +
+                       l32 * TILE + h * 16;
+  floatx16 dq0 = zero16(), dq1 = zero16();
+
+  int kend = a.Tk;
+  if (a.causal) kend = min(kend, qb * ROWS + ROWS);
+  const int nkb = (kend + TILE - 1) / TILE;
+  // dS blocks this wave reads: key tiles kb < nmine (causal: up to the
+  // wave's last query); each is fetched two tiles ahead of its use
+  int nmine = wave_in ? nkb : 0;
+  if (a.causal && wave_in) nmine = min(nkb, (q0 + TILE - 1) / TILE + 1);
+  auto fetch_ds = [&](int kb, floatx4 (&d)[4]) {
+    if (kb < nmine) {
+      const floatx4* src = reinterpret_cast<const floatx4*>(dsrow + (int64_t)kb * (TILE * TILE));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) d[i] = src[i];
+    }
+  };
+  floatx4 d0[4], d1[4], d2[4];
+  fetch_ds(0, d0);
+  fetch_ds(1, d1);
+  floatx4 rk[2];
+  load_tile<GUARD>(K, a.ks.t, 0, a.Tk, rk);
+  store_tile(Ks[0], rk);
+  __syncthreads();
+  // key tile kb uses register set kb % 3 and fetches tile kb + 2 into set
+  // (kb + 2) % 3; the sets are named statically (a register copy of an
+  // in-flight load would wait for it)
+  auto step = [&](int kb, const floatx4 (&use)[4], floatx4 (&into)[4]) {
+    const int cur = kb & 1;
+    const bool more = kb + 1 < nkb;
+    if (more) load_tile<GUARD>(K, a.ks.t, (kb + 1) * TILE, a.Tk, rk);
+    fetch_ds(kb + 2, into);
+    if (kb < nmine) {  // the key-block kernel wrote exactly these blocks
+      float ct[2][16];
+      lds_cols(Ks[cur], l32, h, ct);
+#pragma unroll
+      for (int s = 0; s < 16; ++s) {  // dQ^T += K^T dS^T
+        const float d = use[s >> 2][s & 3];
+        dq0 = mfma(ct[0][s], d, dq0);
+        dq1 = mfma(ct[1][s], d, dq1);
+      }
+    }
+    if (more) store_tile(Ks[cur ^ 1], rk);
+    __syncthreads();
+  };
+  for (int kb = 0; kb < nkb; kb += 3) {
+    step(kb, d0, d2);
+    if (kb + 1 >= nkb) break;
+    step(kb + 1, d1, d0);
+    if (kb + 2 >= nkb) break;
+    step(kb + 2, d2, d1);
+  }
+  float* dqb = a.out + b * a.o1s.b + hh * a.o1s.h;
+  write_rows(Ks[w], dq0, dq1, a.scale, dqb, a.o1s.t, q0, a.Tq, l32, h, lane);
+}
+
 bool rows_ok(const int64_t* s, const void* p) {
   // D contiguous, 16-byte aligned rows
   return ((uintptr_t)p & 15) == 0 && (s[0] % 4) == 0 && (s[1] % 4) == 0 && (s[2] % 4) == 0;
@@ -586,6 +687,12 @@ int flash_backward(const float* q, const float* k, const float* v, const float* 
   int rc = check_launch("flash_dsum");
   if (rc != TJH_OK) return rc;
   const bool ragged = (Tq % TILE) || (Tk % TILE);
+  // dS blocks for the query-block kernel (about 403 MB for 96 heads of
+  // T = 1024; released once the query kernel is queued)
+  a.nqt = (int)cdiv(Tq, TILE);
+  a.nkt = (int)cdiv(Tk, TILE);
+  Scratch dsb((size_t)(B * H) * a.nqt * a.nkt * (TILE * TILE) * sizeof(float));
+  a.dsblk = dsb.ok() ? dsb.as<float>() : nullptr;
   // keys: dK, dV
   a.nblk = (int)cdiv(Tk, ROWS);
   a.out = dk; a.out2 = dv; a.o1s = s3(st[6]); a.o2s = s3(st[7]);
@@ -596,14 +703,21 @@ int flash_backward(const float* q, const float* k, const float* v, const float* 
     hipLaunchKernelGGL(k_flash_dkv<false>, dim3(gk), dim3(256), 0, stream(), a);
   rc = check_launch("flash_dkv");
   if (rc != TJH_OK) return rc;
-  // queries: dQ
+  // queries: dQ from the stored dS blocks, or recomputed when the blocks
+  // could not be allocated
   a.nblk = (int)cdiv(Tq, ROWS);
   a.out = dq; a.out2 = nullptr; a.o1s = s3(st[5]);
   const unsigned gq = (unsigned)(B * H * a.nblk);
-  if (Tk % TILE)
+  if (a.dsblk) {
+    if (Tk % TILE)
+      hipLaunchKernelGGL(k_flash_dq_ds<true>, dim3(gq), dim3(256), 0, stream(), a);
+    else
+      hipLaunchKernelGGL(k_flash_dq_ds<false>, dim3(gq), dim3(256), 0, stream(), a);
+  } else if (Tk % TILE) {
     hipLaunchKernelGGL(k_flash_dq<true>, dim3(gq), dim3(256), 0, stream(), a);
-  else
+  } else {
     hipLaunchKernelGGL(k_flash_dq<false>, dim3(gq), dim3(256), 0, stream(), a);
+  }
   return check_launch("flash_dq");
 }
 
