@@ -513,6 +513,21 @@ def test_sdpa_flash_cross_lengths(torch, Tq, Tk, causal):
     check(gv, wv, rtol=1e-4, atol=1e-4)
 
 
+@pytest.mark.parametrize("causal", [True, False])
+def test_sdpa_flash_recompute_path(torch, monkeypatch, causal):
+    """The query-block kernel that recomputes S and dP (used when the dS
+    blocks cannot be allocated) agrees with the stored-dS path."""
+    r = np.random.default_rng(5 + causal)
+    q, k, v = (f32(r.standard_normal((1, 2, 97, 64))) for _ in range(3))
+    fn = lambda a, b, c: torch.F.scaled_dot_product_attention(a, b, c, is_causal=causal)
+    _, _, stored = grad_of(torch, fn, q, k, v)
+    monkeypatch.setenv("TJH_SDPA_RECOMPUTE", "1")
+    _, _, recomputed = grad_of(torch, fn, q, k, v)
+    for s_, r_ in zip(stored, recomputed):
+        check(r_, s_, rtol=1e-4, atol=1e-5)
+    assert not np.array_equal(stored[0], recomputed[0])  # two different paths ran
+
+
 def test_split_and_narrow_gradients(torch):
     """Pieces of a split that are unused, overlapping narrows and a reused
     piece: the input gradient is the sum over every use (zero elsewhere)."""

@@ -39,6 +39,7 @@
 #include "common.h"
 
 #include <float.h>
+#include <stdlib.h>
 
 namespace tjh {
 namespace {
@@ -691,7 +692,10 @@ int flash_backward(const float* q, const float* k, const float* v, const float* 
   // T = 1024; released once the query kernel is queued)
   a.nqt = (int)cdiv(Tq, TILE);
   a.nkt = (int)cdiv(Tk, TILE);
-  Scratch dsb((size_t)(B * H) * a.nqt * a.nkt * (TILE * TILE) * sizeof(float));
+  // TJH_SDPA_RECOMPUTE=1 (read on every call) forces the recomputing path
+  const char* rec = getenv("TJH_SDPA_RECOMPUTE");
+  const bool want_blocks = !(rec && rec[0] == '1');
+  Scratch dsb(want_blocks ? (size_t)(B * H) * a.nqt * a.nkt * (TILE * TILE) * sizeof(float) : 0);
   a.dsblk = dsb.ok() ? dsb.as<float>() : nullptr;
   // keys: dK, dV
   a.nblk = (int)cdiv(Tk, ROWS);
