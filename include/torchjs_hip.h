@@ -366,8 +366,10 @@ int tjh_nonzero(const float* x, int ndim, const int64_t* shape,
  * op(X) = X^T when trans != 0.  A is [M,K] (or [K,M] when transA), B is
  * [K,N] (or [N,K] when transB); lda/ldb/ldc are row strides; strides
  * between batch items may be 0 (broadcast).  bias_mode: 0 none, 1 bias[N]
- * added to every row, 2 bias[M] added to every column.  beta == 0 never
- * reads C. */
+ * added to every row, 2 bias[M] added to every column, 3 bias[M] is an
+ * OUTPUT: bias[m] = sum_k op(A)[m][k] (batch 1; the bias gradient of a
+ * Linear layer computed with its weight gradient, which replaces the
+ * separate column sum of dY).  beta == 0 never reads C. */
 int tjh_gemm(int transA, int transB, int64_t M, int64_t N, int64_t K,
              float alpha, const float* A, int64_t lda, int64_t strideA,
              const float* B, int64_t ldb, int64_t strideB, float beta,

@@ -367,6 +367,44 @@ def test_gemm_every_tile(torch, monkeypatch, tile, ta, tb, M, N, K):
     check(got, want, rtol=1e-4, atol=1e-5 * np.sqrt(K) * 4)
 
 
+@pytest.mark.parametrize("tile", ["256x128", "128x128", "128x64", "64x64"])
+@pytest.mark.parametrize("ta", [0, 1])
+@pytest.mark.parametrize("M,N,K", [(300, 260, 200), (256, 128, 4096), (768, 192, 8192), (5, 3, 7)])
+def test_gemm_row_sums(torch, monkeypatch, tile, ta, M, N, K):
+    """bias_mode 3: the GEMM also writes sum_k op(A)[m][k] (a Linear bias
+    gradient) -- interior and edge tiles, a K remainder, split-K."""
+    from torchjs_amd import _lib as L
+    monkeypatch.setenv("TJH_GEMM_TILE", tile)
+    r = np.random.default_rng(M * 3 + N + K + ta)
+    A = f32(r.standard_normal((K, M) if ta else (M, K)))
+    B = f32(r.standard_normal((K, N)))
+    a, b = torch.tensor(A), torch.tensor(B)
+    c = torch.tensor(np.zeros((M, N), np.float32))
+    rs = torch.tensor(np.full(M, 7.0, np.float32))  # written, not accumulated
+    L.check(L.lib().tjh_gemm(ta, 0, M, N, K, 1.0, a.data_ptr(), A.shape[1], 0, b.data_ptr(), N,
+                             0, 0.0, c.data_ptr(), N, 0, 1, rs.data_ptr(), 3), "gemm")
+    opA = (A.T if ta else A).astype(np.float64)
+    check(c.numpy(), opA @ B.astype(np.float64), rtol=1e-4, atol=1e-5 * np.sqrt(K) * 4)
+    check(rs.numpy(), opA.sum(1), rtol=1e-4, atol=1e-5 * np.sqrt(K))
+
+
+def test_gemm_row_sums_unaligned(torch):
+    """bias_mode 3 through the guarded path (operand rows not 16-byte aligned)."""
+    from torchjs_amd import _lib as L
+    r = np.random.default_rng(21)
+    M, N, K = 37, 29, 1001
+    A = f32(r.standard_normal((K, M + 1)))  # row stride M + 1 = 38: unaligned rows
+    B = f32(r.standard_normal((K, N)))
+    a, b = torch.tensor(A), torch.tensor(B)
+    c = torch.tensor(np.zeros((M, N), np.float32))
+    rs = torch.tensor(np.zeros(M, np.float32))
+    L.check(L.lib().tjh_gemm(1, 0, M, N, K, 1.0, a.data_ptr(), M + 1, 0, b.data_ptr(), N, 0, 0.0,
+                             c.data_ptr(), N, 0, 1, rs.data_ptr(), 3), "gemm")
+    opA = A[:, :M].T.astype(np.float64)
+    check(c.numpy(), opA @ B.astype(np.float64), rtol=1e-4, atol=1e-4)
+    check(rs.numpy(), opA.sum(1), rtol=1e-4, atol=1e-4)
+
+
 def test_gemm_epilogue(torch):
     r = np.random.default_rng(13)
     M, N, K = 70, 90, 50

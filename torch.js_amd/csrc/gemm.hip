@@ -27,6 +27,7 @@
 // tiles share B columns, and each XCD receives a contiguous run of that
 // order so the sharing happens inside one L2.
 
+#include "colsum.h"
 #include "common.h"
 
 #include <stdio.h>
@@ -59,6 +60,7 @@ struct GemmArgs {
   int tiles_m, tiles_n;
   int64_t kchunk;  // K range per split (multiple of BK); splits = gridDim.y
   float* ws;       // split-K partials [batch][split][M][N] (nullptr: none)
+  float* rsw;      // split-K partials of the row sums (bias_mode 3/4) [split][M]
 };
 
 // Loads a logical OUTER x BK tile (outer = m for A, n for B) for this lane:
@@ -199,6 +201,12 @@ __global__ __launch_bounds__(kThreads, 2) void k_gemm(GemmArgs g) {
   // B: logical [K][N]; as an "outer = n" tile it is stored [N][K] when TB
   //    (k contiguous, like !TA) and [K][N] when !TB (n contiguous, like TA).
   const int64_t ktiles = kend > kbeg ? cdiv(kend - kbeg, BK) : 0;
+  // bias_mode 3/4: the workgroups of the first column tile also sum the
+  // rows of op(A) over their K range (the bias gradient of a weight
+  // gradient), compensated, RKPT k values per lane and K step
+  constexpr int RKPT = BK * BM / kThreads;
+  const bool row_sums = g.bias_mode >= 3 && tn == 0;
+  Kahan rsum;
   floatx4 ra[VA], rb[VB];
   load_tile<TA, BM, VA, EDGE>(A, g.lda, g.M, kend, m0, kbeg, g.vecA, ra);
   load_tile<!TB, BN, VB, EDGE>(B, g.ldb, g.N, kend, n0, kbeg, g.vecB, rb);
@@ -237,11 +245,34 @@ __global__ __launch_bounds__(kThreads, 2) void k_gemm(GemmArgs g) {
         for (int j = 0; j < FN; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[c][i], bv[c][j], acc[i][j], 0, 0, 0);
     }
+    if (row_sums) {
+      // this lane's k slice of row t % BM of the current A tile
+      const float* col = As[cur] + (threadIdx.x / BM) * RKPT * LA + threadIdx.x % BM;
+#pragma unroll
+      for (int i = 0; i < RKPT; ++i) rsum.add(col[i * LA]);
+    }
     if (more) {
       store_tile<TA, BM, VA, LA>(As[cur ^ 1], ra);
       store_tile<!TB, BN, VB, LB>(Bs[cur ^ 1], rb);
     }
     __syncthreads();
+  }
+
+  if (row_sums) {
+    // lanes t, t + BM, ... hold slices of row t: combined in that order
+    __shared__ float rpart[kThreads];
+    rpart[threadIdx.x] = rsum.s;
+    __syncthreads();
+    const int64_t row = m0 + threadIdx.x;
+    if (threadIdx.x < BM && row < g.M) {
+      float v = 0.f;
+#pragma unroll
+      for (int q = 0; q < kThreads / BM; ++q) v += rpart[threadIdx.x + q * BM];
+      float* out = const_cast<float*>(g.bias);
+      if (g.rsw) g.rsw[(int64_t)blockIdx.y * g.M + row] = v;
+      else if (g.bias_mode == 3) out[row] = v;
+      else out[row] += v;
+    }
   }
 
   // ---- epilogue
@@ -301,6 +332,15 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(GemmArgs g, int splits) {
     if (g.bias_mode == 1) v += g.bias[col];
     else if (g.bias_mode == 2) v += g.bias[row];
     *cp = v;
+  }
+  if (g.rsw && b == 0) {
+    // row sums of op(A) (bias_mode 3/4), splits summed in order
+    float* out = const_cast<float*>(g.bias);
+    for (int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x; r < g.M; r += (int64_t)gridDim.x * 256) {
+      float s = 0.f;
+      for (int q = 0; q < splits; ++q) s += g.rsw[q * g.M + r];
+      out[r] = g.bias_mode == 3 ? s : out[r] + s;
+    }
   }
 }
 
@@ -434,13 +474,16 @@ int run_block(int ti, GemmArgs g, int ta, int tb, int64_t splits, int64_t batch,
   if (g.kchunk < BK) g.kchunk = BK;
   splits = cdiv(g.K, g.kchunk) > 0 ? cdiv(g.K, g.kchunk) : 1;
   g.ws = nullptr;
-  Scratch ws(splits > 1 ? (size_t)(batch * splits * g.M * g.N) * sizeof(float) : 0);
+  g.rsw = nullptr;
+  const int64_t rs_len = g.bias_mode >= 3 ? splits * g.M : 0;
+  Scratch ws(splits > 1 ? (size_t)(batch * splits * g.M * g.N + rs_len) * sizeof(float) : 0);
   if (splits > 1) {
     if (!ws.ok()) {
       splits = 1;
       g.kchunk = g.K > 0 ? cdiv(g.K, BK) * BK : BK;
     } else {
       g.ws = ws.as<float>();
+      if (rs_len) g.rsw = g.ws + batch * splits * g.M * g.N;
     }
   }
   dim3 grid((unsigned)(g.tiles_m * g.tiles_n), (unsigned)splits, (unsigned)batch);
@@ -463,7 +506,7 @@ GemmArgs sub(const GemmArgs& g, int ta, int tb, int64_t m0, int64_t M, int64_t n
   s.B = g.B + (tb ? n0 * g.ldb + k0 : k0 * g.ldb + n0);
   s.C = g.C + m0 * g.ldc + n0;
   if (g.bias_mode == 1) s.bias = g.bias + n0;
-  else if (g.bias_mode == 2) s.bias = g.bias + m0;
+  else if (g.bias_mode >= 2) s.bias = g.bias + m0;
   return s;
 }
 
@@ -478,8 +521,9 @@ int tjh::gemm(const char* family, int transA, int transB, int64_t M, int64_t N, 
               int64_t batch, const float* bias, int bias_mode) {
   TJH_REQUIRE_INIT();
   TJH_ARG(M >= 0 && N >= 0 && K >= 0 && batch >= 0, "tjh_gemm: negative size");
-  TJH_ARG(bias_mode >= 0 && bias_mode <= 2, "tjh_gemm: bad bias_mode %d", bias_mode);
+  TJH_ARG(bias_mode >= 0 && bias_mode <= 3, "tjh_gemm: bad bias_mode %d", bias_mode);
   TJH_ARG(bias_mode == 0 || bias, "tjh_gemm: bias_mode %d needs a bias pointer", bias_mode);
+  TJH_ARG(bias_mode != 3 || batch <= 1, "tjh_gemm: bias_mode 3 needs batch 1");
   if (M == 0 || N == 0 || batch == 0) return TJH_OK;
   TJH_ARG(batch <= 65535, "tjh_gemm: batch %lld exceeds 65535", (long long)batch);
   // row strides must cover the contiguous extent
@@ -498,6 +542,7 @@ int tjh::gemm(const char* family, int transA, int transB, int64_t M, int64_t N, 
   g.tiles_m = g.tiles_n = 0;
   g.kchunk = BK;
   g.ws = nullptr;
+  g.rsw = nullptr;
   KernelScope ks(family);
   const Plan plan = choose_plan(M, N, K, batch, cus, transA, transB);
   const TileCfg& tc = kTiles[plan.tile];
@@ -525,8 +570,9 @@ int tjh::gemm(const char* family, int transA, int transB, int64_t M, int64_t N, 
   // otherwise run on a dozen workgroups for the whole K range.
   if (rc == TJH_OK && Nm < N) {  // right strip (all rows)
     const Plan ps = choose_plan(M, N - Nm, Km, batch, cus, transA, transB);
-    rc = run_block(ps.tile, sub(gk, transA, transB, 0, M, Nm, N - Nm, 0, Km), transA, transB,
-                   ps.splits, batch, true, cus);
+    GemmArgs gs = sub(gk, transA, transB, 0, M, Nm, N - Nm, 0, Km);
+    if (gs.bias_mode == 3 && Nm > 0) gs.bias_mode = 0;  // row sums come from column 0's tiles
+    rc = run_block(ps.tile, gs, transA, transB, ps.splits, batch, true, cus);
   }
   if (rc == TJH_OK && Mm < M && Nm > 0) {  // bottom strip (interior columns)
     const Plan ps = choose_plan(M - Mm, Nm, Km, batch, cus, transA, transB);
@@ -536,8 +582,12 @@ int tjh::gemm(const char* family, int transA, int transB, int64_t M, int64_t N, 
   if (rc == TJH_OK && Kr > 0) {
     GemmArgs gr = sub(g, transA, transB, 0, M, 0, N, Km, Kr);
     gr.beta = 1.0f;
-    gr.bias_mode = 0;
-    gr.bias = nullptr;
+    if (g.bias_mode == 3) {
+      gr.bias_mode = 4;  // add this K range's row sums
+    } else {
+      gr.bias_mode = 0;
+      gr.bias = nullptr;
+    }
     rc = run_block(plan.tile, gr, transA, transB, 1, batch, true, cus);
   }
   return rc;

@@ -282,8 +282,8 @@ def embedding(input, weight):
 
 def linear(x, weight, bias=None):
     """y = x W^T + b (src/nn/linear.ts:43-66) as ONE GEMM with the bias in
-    the epilogue and W^T read in place; backward dx = g W, dW = g^T x
-    (split-K over tokens), db = column sum of g."""
+    the epilogue and W^T read in place; backward dx = g W, and dW = g^T x
+    (split-K over tokens) with db = column sums of g from the same GEMM."""
     if x.dtype != "float32":
         x = x.float()
     out_f, in_f = weight.shape
@@ -303,9 +303,14 @@ def linear(x, weight, bias=None):
     def bwd(g):
         g2 = reshape_raw(g, (M, out_f))
         dx = reshape_raw(_gemm(g2, wd), lead + (in_f,)) if rx else None
-        dw = _gemm(g2.T, x2) if rw else None
-        db = None
-        if rb:
+        dw = db = None
+        if rw and rb:
+            # db = the row sums of g^T, accumulated by the dW GEMM itself
+            db = empty((out_f,))
+            dw = _gemm(g2.T, x2, rowsum_out=db)
+        elif rw:
+            dw = _gemm(g2.T, x2)
+        elif rb:
             gc = g2 if g2.is_contiguous() else _k_contiguous(g2)
             db = _view_raw(_k_reduce("sum", gc, [0]), (out_f,))
         return [dx, dw, db]

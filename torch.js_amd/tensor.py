@@ -1658,8 +1658,14 @@ def _mat_operand(t):
     return None
 
 
-def _gemm(a, b, out=None, alpha=1.0, beta=0.0, bias=None, bias_mode=0):
-    """out[M,N] = alpha*a[M,K] @ b[K,N] (+beta*out) (+bias) for 2-D views."""
+def _gemm(a, b, out=None, alpha=1.0, beta=0.0, bias=None, bias_mode=0, rowsum_out=None):
+    """out[M,N] = alpha*a[M,K] @ b[K,N] (+beta*out) (+bias) for 2-D views.
+    rowsum_out (a contiguous [M] tensor) receives the row sums of `a` from
+    the same launch (bias_mode 3: a Linear layer's bias gradient computed
+    with its weight gradient)."""
+    if rowsum_out is not None:
+        assert bias is None and bias_mode == 0 and rowsum_out.is_contiguous()
+        bias, bias_mode = rowsum_out, 3
     M, K = a.shape
     K2, N = b.shape
     assert K == K2
