@@ -317,29 +317,47 @@ __global__ __launch_bounds__(kThreads, 2) void k_gemm(GemmArgs g) {
 }
 
 // C = alpha * sum_s ws[b][s] + beta*C + bias, in a fixed split order.
+// VEC: N, ldc and C are 16-byte aligned, so a lane sums 4 columns with
+// 128-bit accesses.  Partials are dead after this read (non-temporal).
+template <bool VEC>
 __global__ __launch_bounds__(256) void k_splitk_reduce(GemmArgs g, int splits) {
   const int64_t mn = g.M * g.N;
   const int64_t b = blockIdx.y;
   float* __restrict__ C = g.C + b * g.sC;
   const float* __restrict__ W = g.ws + b * splits * mn;
-  for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < mn; e += (int64_t)gridDim.x * 256) {
-    float s = 0.f;
-    for (int q = 0; q < splits; ++q) s += W[q * mn + e];
-    const int64_t row = e / g.N, col = e % g.N;
-    float v = g.alpha * s;
-    float* cp = C + row * g.ldc + col;
-    if (g.beta != 0.f) v += g.beta * *cp;
-    if (g.bias_mode == 1) v += g.bias[col];
-    else if (g.bias_mode == 2) v += g.bias[row];
-    *cp = v;
+  const uint32_t w = VEC ? (uint32_t)(g.N / 4) : (uint32_t)g.N;  // items per row
+  const uint32_t items = (uint32_t)g.M * w;
+  for (uint32_t e = blockIdx.x * 256 + threadIdx.x; e < items; e += gridDim.x * 256) {
+    const uint32_t row = e / w, c0 = (e - row * w) * (VEC ? 4 : 1);
+    const int64_t off = (int64_t)row * g.N + c0;
+    float s[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int q = 0; q < splits; ++q) {
+      if (VEC) {
+        const float4 v = ld_nt(W + q * mn + off);
+        s[0] += v.x; s[1] += v.y; s[2] += v.z; s[3] += v.w;
+      } else {
+        s[0] += W[q * mn + off];
+      }
+    }
+    float* cp = C + (int64_t)row * g.ldc + c0;
+#pragma unroll
+    for (int j = 0; j < (VEC ? 4 : 1); ++j) {
+      float v = g.alpha * s[j];
+      if (g.beta != 0.f) v += g.beta * cp[j];
+      if (g.bias_mode == 1) v += g.bias[c0 + j];
+      else if (g.bias_mode == 2) v += g.bias[row];
+      s[j] = v;
+    }
+    if (VEC) *reinterpret_cast<float4*>(cp) = make_float4(s[0], s[1], s[2], s[3]);
+    else cp[0] = s[0];
   }
   if (g.rsw && b == 0) {
     // row sums of op(A) (bias_mode 3/4), splits summed in order
     float* out = const_cast<float*>(g.bias);
     for (int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x; r < g.M; r += (int64_t)gridDim.x * 256) {
-      float s = 0.f;
-      for (int q = 0; q < splits; ++q) s += g.rsw[q * g.M + r];
-      out[r] = g.bias_mode == 3 ? s : out[r] + s;
+      float t = 0.f;
+      for (int q = 0; q < splits; ++q) t += g.rsw[q * g.M + r];
+      out[r] = g.bias_mode == 3 ? t : out[r] + t;
     }
   }
 }
@@ -473,6 +491,10 @@ int run_block(int ti, GemmArgs g, int ta, int tb, int64_t splits, int64_t batch,
   g.kchunk = cdiv(cdiv(g.K, splits), BK) * BK;
   if (g.kchunk < BK) g.kchunk = BK;
   splits = cdiv(g.K, g.kchunk) > 0 ? cdiv(g.K, g.kchunk) : 1;
+  if (g.M * g.N >= (int64_t(1) << 32)) {  // the split-K sum indexes elements in 32 bits
+    splits = 1;
+    g.kchunk = g.K > 0 ? cdiv(g.K, BK) * BK : BK;
+  }
   g.ws = nullptr;
   g.rsw = nullptr;
   const int64_t rs_len = g.bias_mode >= 3 ? splits * g.M : 0;
@@ -490,10 +512,15 @@ int run_block(int ti, GemmArgs g, int ta, int tb, int64_t splits, int64_t batch,
   launch_tile(ti, g, grid, ta, tb, edge);
   int rc = check_launch("gemm");
   if (rc != TJH_OK || splits == 1) return rc;
-  int64_t blocks = cdiv(g.M * g.N, 256);
-  if (blocks > 4LL * cus) blocks = 4LL * cus;
-  hipLaunchKernelGGL(k_splitk_reduce, dim3((unsigned)blocks, (unsigned)batch), dim3(256), 0,
-                     stream(), g, (int)splits);
+  const bool vec = g.N % 4 == 0 && g.ldc % 4 == 0 && g.sC % 4 == 0 && aligned16(g.C);
+  int64_t blocks = cdiv(g.M * g.N / (vec ? 4 : 1), 256);
+  if (blocks > 16LL * cus) blocks = 16LL * cus;
+  if (vec)
+    hipLaunchKernelGGL(k_splitk_reduce<true>, dim3((unsigned)blocks, (unsigned)batch), dim3(256),
+                       0, stream(), g, (int)splits);
+  else
+    hipLaunchKernelGGL(k_splitk_reduce<false>, dim3((unsigned)blocks, (unsigned)batch), dim3(256),
+                       0, stream(), g, (int)splits);
   return check_launch("gemm_splitk_reduce");
 }
 
