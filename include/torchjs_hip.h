@@ -375,6 +375,22 @@ int tjh_gemm(int transA, int transB, int64_t M, int64_t N, int64_t K,
              const float* B, int64_t ldb, int64_t strideB, float beta,
              float* C, int64_t ldc, int64_t strideC, int64_t batch,
              const float* bias, int bias_mode);
+/* tjh_gemm (batch 1) with the GELU of the MLP block fused into the
+ * epilogue — the Linear -> GELU -> Linear pattern of torch.js's
+ * transformer MLP (src/nn/activation.ts GELU between src/nn/linear.ts
+ * layers), which otherwise runs GELU as separate elementwise passes over
+ * the [tokens, 4*d] activation (unary.wgsl:246-252 and its backward).
+ * With v the final value of C[m][n] (alpha, beta and bias applied):
+ *   act 1: aux[m*ldaux + n] = v, C = GELU(v)       (forward: keeps the
+ *          pre-activation for the backward)
+ *   act 2: C = v * GELU'(aux[m*ldaux + n])          (backward through GELU)
+ * act 0 is tjh_gemm.  GELU and GELU' are the library's elementwise ones,
+ * so the results equal the unfused sequence bit for bit. */
+int tjh_gemm_act(int transA, int transB, int64_t M, int64_t N, int64_t K,
+                 float alpha, const float* A, int64_t lda, const float* B,
+                 int64_t ldb, float beta, float* C, int64_t ldc,
+                 const float* bias, int bias_mode, float* aux, int64_t ldaux,
+                 int act);
 
 /* ------------------------------------------------------------------ */
 /* Attention — F.scaled_dot_product_attention                           */

@@ -699,3 +699,40 @@ def test_adam_bit_exact(torch, cls, decoupled, wd):
         got = t.numpy()
         assert (got == p).mean() > 0.999
         assert np.max(np.abs(got.astype(np.float64) - p)) <= np.abs(p).max() * 2 ** -23
+
+
+# ------------------------------------------------------------------ fused MLP
+
+
+@pytest.mark.parametrize("B,T,d_in,hid,d_out", [(4, 33, 70, 200, 70),     # edges + K remainder
+                                               (1, 64, 2048, 128, 2048)])  # split K
+@pytest.mark.parametrize("bias", [True, False])
+def test_mlp_gelu_fused_equals_unfused(torch, B, T, d_in, hid, d_out, bias):
+    """The MLP block with GELU fused into the GEMM epilogues reproduces
+    linear -> gelu -> linear bit for bit, forward and backward."""
+    r = np.random.default_rng(B * T + d_in + bias)
+    x = f32(r.standard_normal((B, T, d_in)))
+    w1 = f32(r.standard_normal((hid, d_in)) * 0.05)
+    w2 = f32(r.standard_normal((d_out, hid)) * 0.05)
+    b1 = f32(r.standard_normal(hid)) if bias else None
+    b2 = f32(r.standard_normal(d_out)) if bias else None
+    arrays = [a for a in (x, w1, b1, w2, b2) if a is not None]
+
+    def fused(*ts):
+        xx, ww1, *rest = ts
+        bb1, ww2, bb2 = (rest[0], rest[1], rest[2]) if bias else (None, rest[0], None)
+        return torch.F._mlp_gelu(xx, ww1, bb1, ww2, bb2)
+
+    def unfused(*ts):
+        xx, ww1, *rest = ts
+        bb1, ww2, bb2 = (rest[0], rest[1], rest[2]) if bias else (None, rest[0], None)
+        return torch.F.linear(torch.F.gelu(torch.F.linear(xx, ww1, bb1)), ww2, bb2)
+    y1, g, grads1 = grad_of(torch, fused, *arrays)
+    y2, _, grads2 = grad_of(torch, unfused, *arrays)
+    assert np.array_equal(y1, y2)
+    for a_, b_ in zip(grads1, grads2):
+        assert np.array_equal(a_, b_)
+    # and both match the oracle
+    h = x.astype(np.float64) @ w1.T.astype(np.float64) + (b1 if bias else 0)
+    want = ops.gelu(h) @ w2.T.astype(np.float64) + (b2 if bias else 0)
+    check(y1, want, rtol=1e-4, atol=1e-4)

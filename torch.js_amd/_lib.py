@@ -117,6 +117,8 @@ SIGNATURES = {
     "tjh_nonzero": [c_vp, c_int, P_i64, c_vp, c_i64, P_i64],
     "tjh_gemm": [c_int, c_int, c_i64, c_i64, c_i64, c_f32, c_vp, c_i64, c_i64, c_vp, c_i64, c_i64,
                  c_f32, c_vp, c_i64, c_i64, c_i64, c_vp, c_int],
+    "tjh_gemm_act": [c_int, c_int, c_i64, c_i64, c_i64, c_f32, c_vp, c_i64, c_vp, c_i64, c_f32,
+                     c_vp, c_i64, c_vp, c_int, c_vp, c_i64, c_int],
     "tjh_sdpa_forward": [c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_i64, P_i64,
                          P_i64, P_i64, P_i64, c_f32, c_int],
     "tjh_sdpa_backward": [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64,

@@ -52,12 +52,13 @@ struct Scratch {
   bool ok() const { return p != nullptr; }
 };
 
-// The MFMA GEMM behind tjh_gemm, timed under `family` (so products issued
-// inside attention or convolution are reported apart from tjh_gemm's).
+// The MFMA GEMM behind tjh_gemm / tjh_gemm_act, timed under `family` (so
+// products issued inside attention are reported apart from tjh_gemm's).
+// act: 0 none, 1 GELU (aux <- pre-activation), 2 times GELU'(aux).
 int gemm(const char* family, int transA, int transB, int64_t M, int64_t N, int64_t K,
          float alpha, const float* A, int64_t lda, int64_t strideA, const float* B, int64_t ldb,
          int64_t strideB, float beta, float* C, int64_t ldc, int64_t strideC, int64_t batch,
-         const float* bias, int bias_mode);
+         const float* bias, int bias_mode, float* aux = nullptr, int64_t ldaux = 0, int act = 0);
 
 // Flash attention for head dim 64 (flash.hip).  `flash_supported` checks
 // the head dim and that every tensor has 16-byte aligned, D-contiguous rows.

@@ -29,6 +29,7 @@
 
 #include "colsum.h"
 #include "common.h"
+#include "ops_math.h"
 
 #include <stdio.h>
 #include <stdlib.h>
@@ -61,7 +62,23 @@ struct GemmArgs {
   int64_t kchunk;  // K range per split (multiple of BK); splits = gridDim.y
   float* ws;       // split-K partials [batch][split][M][N] (nullptr: none)
   float* rsw;      // split-K partials of the row sums (bias_mode 3/4) [split][M]
+  // epilogue activation on the final C values (after alpha, beta, bias):
+  // 1: aux <- v, C <- GELU(v);  2: C <- v * GELU'(aux)
+  float* aux;
+  int64_t ldaux;
+  int act;
 };
+
+// The activation epilogue, shared by the GEMM and the split-K sum.
+__device__ __forceinline__ float epilogue_act(const GemmArgs& g, int64_t row, int64_t col,
+                                              float v) {
+  if (g.act == 1) {
+    g.aux[row * g.ldaux + col] = v;
+    return gelu_f(v);
+  }
+  if (g.act == 2) return v * gelu_grad(g.aux[row * g.ldaux + col]);
+  return v;
+}
 
 // Loads a logical OUTER x BK tile (outer = m for A, n for B) for this lane:
 // V float4 per lane.  !TRANS: storage [outer][k] (k contiguous, 4 float4
@@ -309,7 +326,7 @@ __global__ __launch_bounds__(kThreads, 2) void k_gemm(GemmArgs g) {
           if (g.beta != 0.f) v += g.beta * *cp;
           if (g.bias_mode == 1) v += bn;
           else if (g.bias_mode == 2) v += g.bias[row];
-          *cp = v;
+          *cp = epilogue_act(g, row, col, v);
         }
       }
     }
@@ -346,7 +363,7 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(GemmArgs g, int splits) {
       if (g.beta != 0.f) v += g.beta * cp[j];
       if (g.bias_mode == 1) v += g.bias[c0 + j];
       else if (g.bias_mode == 2) v += g.bias[row];
-      s[j] = v;
+      s[j] = epilogue_act(g, row, c0 + j, v);
     }
     if (VEC) *reinterpret_cast<float4*>(cp) = make_float4(s[0], s[1], s[2], s[3]);
     else cp[0] = s[0];
@@ -532,6 +549,7 @@ GemmArgs sub(const GemmArgs& g, int ta, int tb, int64_t m0, int64_t M, int64_t n
   s.A = g.A + (ta ? k0 * g.lda + m0 : m0 * g.lda + k0);
   s.B = g.B + (tb ? n0 * g.ldb + k0 : k0 * g.ldb + n0);
   s.C = g.C + m0 * g.ldc + n0;
+  if (g.aux) s.aux = g.aux + m0 * g.ldaux + n0;
   if (g.bias_mode == 1) s.bias = g.bias + n0;
   else if (g.bias_mode >= 2) s.bias = g.bias + m0;
   return s;
@@ -545,12 +563,15 @@ using namespace tjh;
 int tjh::gemm(const char* family, int transA, int transB, int64_t M, int64_t N, int64_t K,
               float alpha, const float* A, int64_t lda, int64_t strideA, const float* B,
               int64_t ldb, int64_t strideB, float beta, float* C, int64_t ldc, int64_t strideC,
-              int64_t batch, const float* bias, int bias_mode) {
+              int64_t batch, const float* bias, int bias_mode, float* aux, int64_t ldaux, int act) {
   TJH_REQUIRE_INIT();
   TJH_ARG(M >= 0 && N >= 0 && K >= 0 && batch >= 0, "tjh_gemm: negative size");
   TJH_ARG(bias_mode >= 0 && bias_mode <= 3, "tjh_gemm: bad bias_mode %d", bias_mode);
   TJH_ARG(bias_mode == 0 || bias, "tjh_gemm: bias_mode %d needs a bias pointer", bias_mode);
   TJH_ARG(bias_mode != 3 || batch <= 1, "tjh_gemm: bias_mode 3 needs batch 1");
+  TJH_ARG(act >= 0 && act <= 2, "tjh_gemm_act: bad activation %d", act);
+  TJH_ARG(act == 0 || (aux && ldaux >= N && batch <= 1),
+          "tjh_gemm_act: activation %d needs aux (ld >= N) and batch 1", act);
   if (M == 0 || N == 0 || batch == 0) return TJH_OK;
   TJH_ARG(batch <= 65535, "tjh_gemm: batch %lld exceeds 65535", (long long)batch);
   // row strides must cover the contiguous extent
@@ -570,6 +591,9 @@ int tjh::gemm(const char* family, int transA, int transB, int64_t M, int64_t N, 
   g.kchunk = BK;
   g.ws = nullptr;
   g.rsw = nullptr;
+  g.aux = act ? aux : nullptr;
+  g.ldaux = ldaux;
+  g.act = act;
   KernelScope ks(family);
   const Plan plan = choose_plan(M, N, K, batch, cus, transA, transB);
   const TileCfg& tc = kTiles[plan.tile];
@@ -584,6 +608,7 @@ int tjh::gemm(const char* family, int transA, int transB, int64_t M, int64_t N, 
   const int64_t Kr = K - Km;
   GemmArgs gk = g;
   gk.K = Km;
+  if (Kr > 0) gk.act = 0;  // the K remainder pass applies the activation
   int rc = TJH_OK;
   if (Km == 0) {
     // K < 16: one guarded pass does it all
@@ -626,4 +651,12 @@ extern "C" int tjh_gemm(int transA, int transB, int64_t M, int64_t N, int64_t K,
                         int64_t batch, const float* bias, int bias_mode) {
   return tjh::gemm("gemm", transA, transB, M, N, K, alpha, A, lda, strideA, B, ldb, strideB, beta,
                    C, ldc, strideC, batch, bias, bias_mode);
+}
+
+extern "C" int tjh_gemm_act(int transA, int transB, int64_t M, int64_t N, int64_t K, float alpha,
+                            const float* A, int64_t lda, const float* B, int64_t ldb, float beta,
+                            float* C, int64_t ldc, const float* bias, int bias_mode, float* aux,
+                            int64_t ldaux, int act) {
+  return tjh::gemm("gemm", transA, transB, M, N, K, alpha, A, lda, 0, B, ldb, 0, beta, C, ldc, 0,
+                   1, bias, bias_mode, aux, ldaux, act);
 }

@@ -317,6 +317,57 @@ def linear(x, weight, bias=None):
     return _record(out, "Linear", [x, weight, bias], bwd)
 
 
+def _mlp_gelu(x, w1, b1, w2, b2):
+    """linear(gelu(linear(x, w1, b1)), w2, b2) -- the transformer MLP block
+    (nn.Linear, nn.GELU, nn.Linear; src/nn/linear.ts:43-66,
+    src/nn/activation.ts) -- with GELU fused into the GEMM epilogues: the
+    first GEMM writes the pre-activation h and GELU(h), and in the backward
+    the second layer's input-gradient GEMM multiplies by GELU'(h) as it
+    writes.  Every value equals the unfused sequence's bit for bit."""
+    if x.dtype != "float32":
+        x = x.float()
+    hid, d_in = w1.shape
+    d_out = w2.shape[0]
+    if x.shape[-1] != d_in or w2.shape[1] != hid:
+        raise RuntimeError("mlp: shapes %s, %s, %s do not chain" % (x.shape, w1.shape, w2.shape))
+    lead = x.shape[:-1]
+    M = _numel(lead)
+    x2 = reshape(x.detach(), (M, d_in))
+    w1d, w2d = w1.detach(), w2.detach()
+    b1d = b1.detach().contiguous() if b1 is not None else None
+    b2d = b2.detach().contiguous() if b2 is not None else None
+    h = empty((M, hid))
+    a = empty((M, hid))
+    _gemm(x2, w1d.T, out=a, bias=b1d, bias_mode=1 if b1d is not None else 0, aux=h, act=1)
+    y2 = _gemm(a, w2d.T, bias=b2d, bias_mode=1 if b2d is not None else 0)
+    out = reshape_raw(y2, lead + (d_out,))
+    need = [t is not None and t.requires_grad for t in (x, w1, b1, w2, b2)]
+
+    def bwd(g):
+        g2 = reshape_raw(g, (M, d_out))
+        if not g2.is_contiguous():
+            g2 = _k_contiguous(g2)
+        dx = dw1 = db1 = dw2 = db2 = None
+        if need[3] or need[4]:
+            db2 = empty((d_out,)) if need[4] else None
+            if need[3]:
+                dw2 = _gemm(g2.T, a, rowsum_out=db2)
+            else:
+                db2 = _view_raw(_k_reduce("sum", g2, [0]), (d_out,))
+        if need[0] or need[1] or need[2]:
+            dh = empty((M, hid))
+            _gemm(g2, w2d, out=dh, aux=h, act=2)  # (g W2) * GELU'(h)
+            if need[0]:
+                dx = reshape_raw(_gemm(dh, w1d), lead + (d_in,))
+            if need[1]:
+                db1 = empty((hid,)) if need[2] else None
+                dw1 = _gemm(dh.T, x2, rowsum_out=db1)
+            elif need[2]:
+                db1 = _view_raw(_k_reduce("sum", dh, [0]), (hid,))
+        return [dx, dw1, db1, dw2, db2]
+    return _record(out, "MLP", [x, w1, b1, w2, b2], bwd)
+
+
 # ------------------------------------------------------------ convolution
 
 

@@ -455,6 +455,19 @@ static napi_value js_gemm(napi_env env, napi_callback_info info) {
   return undef(env);
 }
 
+/* gemmAct(transA, transB, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, bias, biasMode, aux, ldaux, act) */
+static napi_value js_gemm_act(napi_env env, napi_callback_info info) {
+  napi_value a[18];
+  if (!get_args(env, info, 18, a)) return NULL;
+  CHECK_RC(tjh_gemm_act((int)i64(env, a[0]), (int)i64(env, a[1]), i64(env, a[2]), i64(env, a[3]),
+                        i64(env, a[4]), (float)f64(env, a[5]), (const float*)ptr(env, a[6]),
+                        i64(env, a[7]), (const float*)ptr(env, a[8]), i64(env, a[9]),
+                        (float)f64(env, a[10]), (float*)ptr(env, a[11]), i64(env, a[12]),
+                        (const float*)ptr(env, a[13]), (int)i64(env, a[14]), (float*)ptr(env, a[15]),
+                        i64(env, a[16]), (int)i64(env, a[17])));
+  return undef(env);
+}
+
 /* sdpaForward(q, k, v, o, lse, B, H, Tq, Tk, D, qs[3], ks[3], vs[3], os[3], scale, causal) */
 static napi_value js_sdpa_forward(napi_env env, napi_callback_info info) {
   napi_value a[16];
@@ -823,7 +836,7 @@ static napi_value init_module(napi_env env, napi_value exports) {
       FN("softmaxBackward", js_softmax_backward), FN("crossEntropyForward", js_ce_forward),
       FN("crossEntropyBackward", js_ce_backward), FN("layerNormForward", js_ln_forward),
       FN("layerNormBackward", js_ln_backward), FN("embeddingForward", js_emb_forward),
-      FN("embeddingBackward", js_emb_backward), FN("gemm", js_gemm),
+      FN("embeddingBackward", js_emb_backward), FN("gemm", js_gemm), FN("gemmAct", js_gemm_act),
       FN("sdpaForward", js_sdpa_forward), FN("sdpaBackward", js_sdpa_backward),
       FN("adamStep", js_adam_step), FN("isInitialized", js_is_initialized),
       FN("deviceCount", js_device_count), FN("free", js_free), FN("resetPeak", js_reset_peak),

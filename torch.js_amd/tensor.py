@@ -1658,11 +1658,14 @@ def _mat_operand(t):
     return None
 
 
-def _gemm(a, b, out=None, alpha=1.0, beta=0.0, bias=None, bias_mode=0, rowsum_out=None):
+def _gemm(a, b, out=None, alpha=1.0, beta=0.0, bias=None, bias_mode=0, rowsum_out=None,
+          aux=None, act=0):
     """out[M,N] = alpha*a[M,K] @ b[K,N] (+beta*out) (+bias) for 2-D views.
     rowsum_out (a contiguous [M] tensor) receives the row sums of `a` from
     the same launch (bias_mode 3: a Linear layer's bias gradient computed
-    with its weight gradient)."""
+    with its weight gradient).  act 1 / 2 with aux ([M,N], row stride as
+    out's) fuses GELU into the epilogue: 1 writes the pre-activation to
+    aux and GELU of it to out, 2 multiplies by GELU'(aux)."""
     if rowsum_out is not None:
         assert bias is None and bias_mode == 0 and rowsum_out.is_contiguous()
         bias, bias_mode = rowsum_out, 3
@@ -1680,6 +1683,13 @@ def _gemm(a, b, out=None, alpha=1.0, beta=0.0, bias=None, bias_mode=0, rowsum_ou
     if out is None:
         out = _empty_padded(M, N) if N % 4 else empty((M, N))
     ldc = out._strides[0] if out._strides[0] >= N else N
+    if act:
+        assert aux is not None and aux.shape == (M, N) and aux._strides[1] == 1
+        L.check(L.lib().tjh_gemm_act(1 if oa[2] else 0, 1 if ob[2] else 0, M, N, K, float(alpha),
+                                     oa[0], oa[1], ob[0], ob[1], float(beta), out.data_ptr(), ldc,
+                                     bias.data_ptr() if bias is not None else None, bias_mode,
+                                     aux.data_ptr(), aux._strides[0], act), "gemm_act")
+        return out
     L.check(L.lib().tjh_gemm(1 if oa[2] else 0, 1 if ob[2] else 0, M, N, K, float(alpha), oa[0],
                              oa[1], 0, ob[0], ob[1], 0, float(beta), out.data_ptr(), ldc, 0, 1,
                              bias.data_ptr() if bias is not None else None, bias_mode), "gemm")

@@ -61,7 +61,9 @@ class MLPBlock(nn.Module):
         self.c_proj = nn.Linear(4 * d, d)
 
     def forward(self, x):
-        return self.c_proj(F.gelu(self.c_fc(x)))
+        # c_proj(gelu(c_fc(x))) with GELU fused into the two GEMMs
+        return F._mlp_gelu(x, self.c_fc.weight, self.c_fc.bias, self.c_proj.weight,
+                           self.c_proj.bias)
 
 
 class Block(nn.Module):
