@@ -9,10 +9,12 @@
 //
 // Tiling (one workgroup = 256 lanes = 4 wave64 arranged 2 x 2):
 //   block tile BM x BN in {256x128, 128x128, 128x64, 64x64}, K step 16;
-//   each wave owns a (BM/2) x (BN/2) sub-tile of 32x32 MFMA blocks.  A and
-//   B tiles are staged in LDS k-major (As[k][m], Bs[k][n]) with a 4-float
-//   pad, double-buffered: the next K tile is fetched from HBM into
-//   registers while the MFMAs consume the current LDS tile.
+//   each wave owns a (BM/2) x (BN/2) sub-tile of 32x32 MFMA blocks.  Tiles
+//   are double-buffered in LDS: the next K tile is fetched from HBM into
+//   registers while the MFMAs consume the current LDS tile.  A stored
+//   [M][K] (k contiguous) is staged As[m][k] and read as 128-bit fragments
+//   under a K-step permutation (below); every other operand is staged
+//   k-major (As[k][m], Bs[k][n]) with a 4-float pad.
 // The tile is chosen per call from M, N and the CU count so that the
 // number of workgroups divides evenly over the 256 CUs (an 8192 x 768
 // product has 384 tiles of 128x128 — 1.5 per CU — but 768 of 128x64).
@@ -136,14 +138,21 @@ __device__ __forceinline__ void load_tile(const float* __restrict__ P, int64_t l
   }
 }
 
-// Stores a loaded tile into LDS laid out S[k][outer] (row length W).
-template <bool TRANS, int OUTER, int V, int W>
+// Stores a loaded tile into LDS.  TRANS (outer contiguous in memory):
+// S[k][outer], row length W, one 128-bit store per float4.  !TRANS (k
+// contiguous): KC ? S[outer][k] with row length KS, one 128-bit store per
+// float4 : S[k][outer] (transposed, four 32-bit stores per float4).
+constexpr int KS = BK + 4;  // [outer][k] row length: 16-lane groups of 128-bit reads are conflict free
+template <bool TRANS, bool KC, int OUTER, int V, int W>
 __device__ __forceinline__ void store_tile(float* __restrict__ S, const floatx4 (&reg)[V]) {
   const int t = threadIdx.x;
 #pragma unroll
   for (int i = 0; i < V; ++i) {
     int f = t + kThreads * i;
-    if (!TRANS) {
+    if (!TRANS && KC) {
+      int o = f >> 2, kq = f & 3;
+      *reinterpret_cast<floatx4*>(S + o * KS + kq * 4) = reg[i];
+    } else if (!TRANS) {
       int o = f >> 2, kq = f & 3;
       S[(kq * 4 + 0) * W + o] = reg[i].x;
       S[(kq * 4 + 1) * W + o] = reg[i].y;
@@ -153,6 +162,25 @@ __device__ __forceinline__ void store_tile(float* __restrict__ S, const floatx4 
       constexpr int Q = OUTER / 4;
       int k = f / Q, oq = f % Q;
       *reinterpret_cast<floatx4*>(S + k * W + oq * 4) = reg[i];
+    }
+  }
+}
+
+// Reads this lane's MFMA operand values for K steps 4q .. 4q+3 of a tile: F
+// blocks of 32 outer indices, 4 k values each.  K-step permutation: at MFMA
+// step j the lanes of half h (lane / 32) feed k = 8h + j, so a lane's k
+// values are contiguous in an [outer][k] tile (one 128-bit read per block).
+template <bool KC, int F, int W>
+__device__ __forceinline__ void read_frags(const float* __restrict__ S, int outer0, int l32, int h,
+                                           int q, floatx4 (&fr)[F]) {
+#pragma unroll
+  for (int i = 0; i < F; ++i) {
+    const int o = outer0 + i * 32 + l32;
+    if (KC) {
+      fr[i] = *reinterpret_cast<const floatx4*>(S + o * KS + 8 * h + 4 * q);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) fr[i][j] = S[(8 * h + 4 * q + j) * W + o];
     }
   }
 }
@@ -170,15 +198,20 @@ __device__ __forceinline__ int xcd_tile(int bid, int n) {
 }
 
 template <int BM, int BN, bool TA, bool TB, bool EDGE>
-__global__ __launch_bounds__(kThreads, 2) void k_gemm(GemmArgs g) {
+__global__ __launch_bounds__(kThreads, BM * BN > 128 * 128 ? 2 : 4) void k_gemm(GemmArgs g) {
   constexpr int LA = BM + 4, LB = BN + 4;       // LDS row lengths
   constexpr int WM = BM / 2, WN = BN / 2;       // wave tile
   constexpr int FM = WM / 32, FN = WN / 32;     // MFMA blocks per wave
   constexpr int VA = BM * BK / (kThreads * 4);  // float4 loads per lane
   constexpr int VB = BN * BK / (kThreads * 4);
   static_assert(FM >= 1 && FN >= 1 && VA >= 1 && VB >= 1, "tile too small");
-  __shared__ __attribute__((aligned(16))) float As[2][BK * LA];
-  __shared__ __attribute__((aligned(16))) float Bs[2][BK * LB];
+  // A with k contiguous is staged [m][k] (128-bit stores and reads).  B
+  // stays k-major: staging a k-contiguous B as [n][k] measured slower on
+  // the forward products (A . B^T) of GPT-2's shapes.
+  constexpr bool AKC = !TA, BKC = false;
+  constexpr int SA = AKC ? BM * KS : BK * LA, SB = BKC ? BN * KS : BK * LB;
+  __shared__ __attribute__((aligned(16))) float As[2][SA];
+  __shared__ __attribute__((aligned(16))) float Bs[2][SB];
 
   // ---- tile coordinates (grouped ordering for L2 reuse)
   const int tiles_m = g.tiles_m, tiles_n = g.tiles_n;
@@ -227,8 +260,8 @@ __global__ __launch_bounds__(kThreads, 2) void k_gemm(GemmArgs g) {
   floatx4 ra[VA], rb[VB];
   load_tile<TA, BM, VA, EDGE>(A, g.lda, g.M, kend, m0, kbeg, g.vecA, ra);
   load_tile<!TB, BN, VB, EDGE>(B, g.ldb, g.N, kend, n0, kbeg, g.vecB, rb);
-  store_tile<TA, BM, VA, LA>(As[0], ra);
-  store_tile<!TB, BN, VB, LB>(Bs[0], rb);
+  store_tile<TA, AKC, BM, VA, LA>(As[0], ra);
+  store_tile<!TB, BKC, BN, VB, LB>(Bs[0], rb);
   __syncthreads();
 
   for (int64_t kt = 0; kt < ktiles; ++kt) {
@@ -239,45 +272,63 @@ __global__ __launch_bounds__(kThreads, 2) void k_gemm(GemmArgs g) {
       load_tile<TA, BM, VA, EDGE>(A, g.lda, g.M, kend, m0, k0, g.vecA, ra);
       load_tile<!TB, BN, VB, EDGE>(B, g.ldb, g.N, kend, n0, k0, g.vecB, rb);
     }
-    const float* __restrict__ as = As[cur] + wm * WM + l32;
-    const float* __restrict__ bs = Bs[cur] + wn * WN + l32;
-    // fragments of step kk+2 are read from LDS before the MFMAs of step kk
-    float a[2][FM], bv[2][FN];
+    if (AKC || BKC) {
 #pragma unroll
-    for (int i = 0; i < FM; ++i) a[0][i] = as[h * LA + i * 32];
+      for (int q = 0; q < 2; ++q) {
+        floatx4 a[FM], bv[FN];
+        read_frags<AKC, FM, LA>(As[cur], wm * WM, l32, h, q, a);
+        read_frags<BKC, FN, LB>(Bs[cur], wn * WN, l32, h, q, bv);
 #pragma unroll
-    for (int j = 0; j < FN; ++j) bv[0][j] = bs[h * LB + j * 32];
+        for (int j = 0; j < 4; ++j)
 #pragma unroll
-    for (int kk = 0; kk < BK; kk += 2) {
-      const int c = (kk >> 1) & 1;
-      if (kk + 2 < BK) {
+          for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int i = 0; i < FM; ++i) a[c ^ 1][i] = as[(kk + 2 + h) * LA + i * 32];
-#pragma unroll
-        for (int j = 0; j < FN; ++j) bv[c ^ 1][j] = bs[(kk + 2 + h) * LB + j * 32];
+            for (int jn = 0; jn < FN; ++jn)
+              acc[i][jn] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][j], bv[jn][j], acc[i][jn], 0, 0, 0);
       }
+    } else {
+      const float* __restrict__ as = As[cur] + wm * WM + l32;
+      const float* __restrict__ bs = Bs[cur] + wn * WN + l32;
+      // fragments of step kk+2 are read from LDS before the MFMAs of step kk
+      float a[2][FM], bv[2][FN];
 #pragma unroll
-      for (int i = 0; i < FM; ++i)
+      for (int i = 0; i < FM; ++i) a[0][i] = as[h * LA + i * 32];
 #pragma unroll
-        for (int j = 0; j < FN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[c][i], bv[c][j], acc[i][j], 0, 0, 0);
+      for (int j = 0; j < FN; ++j) bv[0][j] = bs[h * LB + j * 32];
+#pragma unroll
+      for (int kk = 0; kk < BK; kk += 2) {
+        const int c = (kk >> 1) & 1;
+        if (kk + 2 < BK) {
+#pragma unroll
+          for (int i = 0; i < FM; ++i) a[c ^ 1][i] = as[(kk + 2 + h) * LA + i * 32];
+#pragma unroll
+          for (int j = 0; j < FN; ++j) bv[c ^ 1][j] = bs[(kk + 2 + h) * LB + j * 32];
+        }
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int j = 0; j < FN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[c][i], bv[c][j], acc[i][j], 0, 0, 0);
+      }
     }
     if (row_sums) {
       // this lane's k slice of row t % BM of the current A tile
-      const float* col = As[cur] + (threadIdx.x / BM) * RKPT * LA + threadIdx.x % BM;
+      const int rm = threadIdx.x % BM, rk = (threadIdx.x / BM) * RKPT;
 #pragma unroll
-      for (int i = 0; i < RKPT; ++i) rsum.add(col[i * LA]);
+      for (int i = 0; i < RKPT; ++i)
+        rsum.add(AKC ? As[cur][rm * KS + rk + i] : As[cur][(rk + i) * LA + rm]);
     }
     if (more) {
-      store_tile<TA, BM, VA, LA>(As[cur ^ 1], ra);
-      store_tile<!TB, BN, VB, LB>(Bs[cur ^ 1], rb);
+      store_tile<TA, AKC, BM, VA, LA>(As[cur ^ 1], ra);
+      store_tile<!TB, BKC, BN, VB, LB>(Bs[cur ^ 1], rb);
     }
     __syncthreads();
   }
 
   if (row_sums) {
-    // lanes t, t + BM, ... hold slices of row t: combined in that order
-    __shared__ float rpart[kThreads];
+    // lanes t, t + BM, ... hold slices of row t: combined in that order.
+    // The staging tiles are free here (the K loop ended on a barrier).
+    float* rpart = As[0];
     rpart[threadIdx.x] = rsum.s;
     __syncthreads();
     const int64_t row = m0 + threadIdx.x;
