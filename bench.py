@@ -61,10 +61,11 @@ def hbm_bytes_per_step(b, t, nparams):
     return {
         # dlogits = softmax - onehot: read logits, write dlogits
         "cross_entropy_bwd": 2 * tok * V * f,
-        # 25 LayerNorms: read dy, x; write dx (+ mean/rstd, gamma)
-        "layer_norm_bwd": (2 * LAYERS + 1) * (3 * tok * D * f + 2 * tok * f + D * f),
-        # GELU backward per layer: read g, x; write dx over [tok, 4D]
-        "unary_backward": LAYERS * 3 * tok * 4 * D * f,
+        # 25 LayerNorms: read dy, x; write dx (+ mean/rstd, gamma); the 24
+        # in the blocks also read the residual stream's gradient, which they
+        # add into dx (GELU's backward runs in a GEMM epilogue: no kernel)
+        "layer_norm_bwd": (2 * LAYERS + 1) * (3 * tok * D * f + 2 * tok * f + D * f) +
+                          2 * LAYERS * tok * D * f,
         # AdamW: read p, g, m, v; write p, m, v
         "adam": 7 * nparams * f,
         # embedding backward: read the dout rows, write the touched table rows

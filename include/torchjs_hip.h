@@ -311,6 +311,18 @@ int tjh_layer_norm_backward(const float* dy, const float* x,
                             const float* rstd, float* dx, float* dgamma,
                             float* dbeta, int64_t rows, int64_t cols,
                             int accumulate);
+/* tjh_layer_norm_backward with dx = res + the LayerNorm input gradient, in
+ * one pass (res [rows, cols], dx required; res may not overlap dx).  The
+ * pre-LN residual stream x -> x + f(LayerNorm(x)) of torch.js's
+ * transformer blocks gives x two gradient contributions that its autograd
+ * sums with a separate add (accumulateGrad, Tensor.ts:3670-3677); this
+ * entry folds that add into the LayerNorm backward.  Equal bit for bit to
+ * tjh_layer_norm_backward followed by the add. */
+int tjh_layer_norm_backward_res(const float* dy, const float* x,
+                                const float* gamma, const float* mean,
+                                const float* rstd, const float* res,
+                                float* dx, float* dgamma, float* dbeta,
+                                int64_t rows, int64_t cols, int accumulate);
 
 /* ------------------------------------------------------------------ */
 /* Embedding / indexing — embedding.wgsl:13-27, index_select.wgsl,      */
@@ -375,17 +387,21 @@ int tjh_gemm(int transA, int transB, int64_t M, int64_t N, int64_t K,
              const float* B, int64_t ldb, int64_t strideB, float beta,
              float* C, int64_t ldc, int64_t strideC, int64_t batch,
              const float* bias, int bias_mode);
-/* tjh_gemm (batch 1) with the GELU of the MLP block fused into the
- * epilogue — the Linear -> GELU -> Linear pattern of torch.js's
- * transformer MLP (src/nn/activation.ts GELU between src/nn/linear.ts
- * layers), which otherwise runs GELU as separate elementwise passes over
- * the [tokens, 4*d] activation (unary.wgsl:246-252 and its backward).
- * With v the final value of C[m][n] (alpha, beta and bias applied):
+/* tjh_gemm (batch 1) with the elementwise op that follows a Linear layer in
+ * torch.js's transformer fused into the epilogue: the GELU of the
+ * Linear -> GELU -> Linear MLP (src/nn/activation.ts GELU between
+ * src/nn/linear.ts layers), which otherwise runs as separate elementwise
+ * passes over the [tokens, 4*d] activation (unary.wgsl:246-252 and its
+ * backward), and the residual add x + Linear(...) of the pre-LN block
+ * (elementwise.wgsl add).  With v the final value of C[m][n] (alpha, beta
+ * and bias applied):
  *   act 1: aux[m*ldaux + n] = v, C = GELU(v)       (forward: keeps the
  *          pre-activation for the backward)
  *   act 2: C = v * GELU'(aux[m*ldaux + n])          (backward through GELU)
- * act 0 is tjh_gemm.  GELU and GELU' are the library's elementwise ones,
- * so the results equal the unfused sequence bit for bit. */
+ *   act 3: C = aux[m*ldaux + n] + v                 (residual add; aux is
+ *          only read and may not overlap C)
+ * act 0 is tjh_gemm.  GELU, GELU' and the add are the library's
+ * elementwise ones, so the results equal the unfused sequence bit for bit. */
 int tjh_gemm_act(int transA, int transB, int64_t M, int64_t N, int64_t K,
                  float alpha, const float* A, int64_t lda, const float* B,
                  int64_t ldb, float beta, float* C, int64_t ldc,

@@ -736,3 +736,111 @@ def test_mlp_gelu_fused_equals_unfused(torch, B, T, d_in, hid, d_out, bias):
     h = x.astype(np.float64) @ w1.T.astype(np.float64) + (b1 if bias else 0)
     want = ops.gelu(h) @ w2.T.astype(np.float64) + (b2 if bias else 0)
     check(y1, want, rtol=1e-4, atol=1e-4)
+
+
+@pytest.mark.parametrize("B,T,in_f,out_f,bias", [(2, 33, 64, 80, True), (1, 50, 50, 96, False),
+                                                  (1, 64, 4096, 64, True), (2, 64, 768, 768, True)])
+def test_linear_add_equals_unfused(torch, B, T, in_f, out_f, bias):
+    """residual + linear(x) with the add in the GEMM epilogue (K remainder,
+    split-K and edge tiles included) reproduces linear followed by the add
+    bit for bit, forward and backward."""
+    r = np.random.default_rng(B * T + in_f + out_f)
+    x = f32(r.standard_normal((B, T, in_f)))
+    w = f32(r.standard_normal((out_f, in_f)) * 0.05)
+    b = f32(r.standard_normal(out_f)) if bias else None
+    res = f32(r.standard_normal((B, T, out_f)))
+    arrays = [a for a in (x, w, b, res) if a is not None]
+
+    def split(ts):
+        return (ts[0], ts[1], ts[2], ts[3]) if bias else (ts[0], ts[1], None, ts[2])
+
+    def fused(*ts):
+        xx, ww, bb, rr = split(ts)
+        return torch.F._linear_add(xx, ww, bb, rr)
+
+    def unfused(*ts):
+        xx, ww, bb, rr = split(ts)
+        return rr + torch.F.linear(xx, ww, bb)
+    y1, _, grads1 = grad_of(torch, fused, *arrays)
+    y2, _, grads2 = grad_of(torch, unfused, *arrays)
+    assert np.array_equal(y1, y2)
+    for a_, b_ in zip(grads1, grads2):
+        assert np.array_equal(a_, b_)
+    want = res + x.astype(np.float64) @ w.T.astype(np.float64) + (b if bias else 0)
+    check(y1, want, **RED)
+
+
+@pytest.mark.parametrize("rows,cols", [(64, 768), (37, 300), (19, 1001), (8, 2000)])
+def test_layer_norm_backward_folds_pending_gradient(torch, rows, cols):
+    """x feeding both a LayerNorm and a residual add: the engine hands the
+    add's gradient to the LayerNorm backward, which adds it in the same
+    kernel (fast row kernel, odd widths and the general path); equal bit
+    for bit to the separate add, and to the oracle within tolerance."""
+    from torchjs_amd import tensor as T
+    r = np.random.default_rng(rows + cols)
+    x0 = f32(r.standard_normal((rows, cols)))
+    gm = f32(1 + 0.1 * r.standard_normal(cols))
+    bt = f32(0.1 * r.standard_normal(cols))
+    res = []
+    for fuse in (True, False):
+        T._FUSE_ACC = fuse
+        try:
+            ts = [torch.tensor(a, requires_grad=True) for a in (x0, gm, bt)]
+            x = ts[0] * 2.0                      # non-leaf: its gradient is summed by the engine
+            y = x + torch.F.layer_norm(x, (cols,), ts[1], ts[2])
+            g = np.random.default_rng(5).standard_normal((rows, cols)).astype(np.float32)
+            y.backward(torch.tensor(g))
+            res.append([t.grad.numpy() for t in ts])
+        finally:
+            T._FUSE_ACC = True
+    for a_, b_ in zip(*res):
+        assert np.array_equal(a_, b_)
+    dx, dgm, dbt = ops.layer_norm_backward(g, 2.0 * x0.astype(np.float64), gm)
+    check(res[0][0], 2.0 * (g + dx), **RED)
+    check(res[0][1], dgm, **RED)
+    check(res[0][2], dbt, **RED)
+
+
+def test_block_residual_fusion_equals_unfused(torch):
+    """The pre-LN block with both residual adds in GEMM epilogues and the
+    add of the residual stream's gradients folded into the LayerNorm
+    backward gives the plain op-by-op block's output and gradients bit for
+    bit."""
+    from torchjs_amd import workloads as W
+    from torchjs_amd import tensor as T
+    r = np.random.default_rng(7)
+    Bn, Tn, d, H = 2, 40, 64, 4
+    blk = W.Block(d, H)
+    p0 = {k: f32(r.standard_normal(p.shape) * 0.1) for k, p in blk.named_parameters()}
+    x0 = f32(r.standard_normal((Bn, Tn, d)))
+    g = f32(r.standard_normal((Bn, Tn, d)))
+
+    def plain(m, x):
+        F = torch.F
+        a = m.ln_1(x)
+        q, k, v = m.attn.c_attn(a).split(d, dim=2)
+        q, k, v = (t.view(Bn, Tn, H, d // H).transpose(1, 2) for t in (q, k, v))
+        y = F.scaled_dot_product_attention(q, k, v, is_causal=True)
+        y = y.transpose(1, 2).contiguous().view(Bn, Tn, d)
+        x = x + m.attn.c_proj(y)
+        hdn = F.gelu(m.mlp.c_fc(m.ln_2(x)))
+        return x + m.mlp.c_proj(hdn)
+
+    outs = []
+    for mode in ("fused", "plain", "fused_noacc"):
+        W.load_params(blk, p0)
+        for prm in blk.parameters():
+            prm.grad = None
+        T._FUSE_ACC = mode != "fused_noacc"
+        try:
+            xl = torch.tensor(x0, requires_grad=True)
+            xx = xl * 1.0
+            y = plain(blk, xx) if mode == "plain" else blk(xx)
+            y.backward(torch.tensor(g))
+            outs.append([y.numpy(), xl.grad.numpy()] +
+                        [prm.grad.numpy() for _, prm in blk.named_parameters()])
+        finally:
+            T._FUSE_ACC = True
+    for other in outs[1:]:
+        for a_, b_ in zip(outs[0], other):
+            assert np.array_equal(a_, b_)

@@ -65,7 +65,7 @@ struct GemmArgs {
   float* ws;       // split-K partials [batch][split][M][N] (nullptr: none)
   float* rsw;      // split-K partials of the row sums (bias_mode 3/4) [split][M]
   // epilogue activation on the final C values (after alpha, beta, bias):
-  // 1: aux <- v, C <- GELU(v);  2: C <- v * GELU'(aux)
+  // 1: aux <- v, C <- GELU(v);  2: C <- v * GELU'(aux);  3: C <- aux + v
   float* aux;
   int64_t ldaux;
   int act;
@@ -79,6 +79,7 @@ __device__ __forceinline__ float epilogue_act(const GemmArgs& g, int64_t row, in
     return gelu_f(v);
   }
   if (g.act == 2) return v * gelu_grad(g.aux[row * g.ldaux + col]);
+  if (g.act == 3) return g.aux[row * g.ldaux + col] + v;
   return v;
 }
 
@@ -620,7 +621,7 @@ int tjh::gemm(const char* family, int transA, int transB, int64_t M, int64_t N, 
   TJH_ARG(bias_mode >= 0 && bias_mode <= 3, "tjh_gemm: bad bias_mode %d", bias_mode);
   TJH_ARG(bias_mode == 0 || bias, "tjh_gemm: bias_mode %d needs a bias pointer", bias_mode);
   TJH_ARG(bias_mode != 3 || batch <= 1, "tjh_gemm: bias_mode 3 needs batch 1");
-  TJH_ARG(act >= 0 && act <= 2, "tjh_gemm_act: bad activation %d", act);
+  TJH_ARG(act >= 0 && act <= 3, "tjh_gemm_act: bad activation %d", act);
   TJH_ARG(act == 0 || (aux && ldaux >= N && batch <= 1),
           "tjh_gemm_act: activation %d needs aux (ld >= N) and batch 1", act);
   if (M == 0 || N == 0 || batch == 0) return TJH_OK;

@@ -480,7 +480,8 @@ __global__ __launch_bounds__(kBlock) void k_ln_fwd_block(const float* __restrict
   }
 }
 
-// LayerNorm backward, dx part + per-block partial dgamma/dbeta.
+// LayerNorm backward, dx part + per-block partial dgamma/dbeta.  With res,
+// dx = res + the LayerNorm input gradient (a residual stream's gradient).
 // Block b owns rows [b*rpb, (b+1)*rpb); wave w takes rows b*rpb + w + 4k.
 // Lane owns columns 4*(lane + 64*j) .. +3 (cols % 4 == 0, cols <= 256*V4).
 // Partials: pg/pb [nblocks, cols].
@@ -491,6 +492,7 @@ __global__ __launch_bounds__(kBlock) void k_ln_bwd_wave(const float* __restrict_
                                                         const float* __restrict__ gamma,
                                                         const float* __restrict__ mean,
                                                         const float* __restrict__ rstd,
+                                                        const float* __restrict__ res,
                                                         float* __restrict__ dx,
                                                         float* __restrict__ pg,
                                                         float* __restrict__ pb, int64_t rows,
@@ -557,6 +559,16 @@ __global__ __launch_bounds__(kBlock) void k_ln_bwd_wave(const float* __restrict_
           ab[j].x += g.x; ab[j].y += g.y; ab[j].z += g.z; ab[j].w += g.w;
         }
       }
+      // the residual row's loads go out before the row reductions
+      float4 rv[V4];
+      if (dx && res) {
+        const float4* r4 = reinterpret_cast<const float4*>(res + r * cols);
+#pragma unroll
+        for (int j = 0; j < V4; ++j) {
+          const int i = lane + 64 * j;
+          if (EXACT || i < c4) rv[j] = ld_nt(reinterpret_cast<const float*>(r4 + i));
+        }
+      }
       s1 = wave_sum(s1) * inv_n;
       s2 = wave_sum(s2) * inv_n;
       if (dx) {
@@ -570,6 +582,10 @@ __global__ __launch_bounds__(kBlock) void k_ln_bwd_wave(const float* __restrict_
             o.y = rs[q] * (gv[q][j].y * gm[j].y - s1 - xh[q][j].y * s2);
             o.z = rs[q] * (gv[q][j].z * gm[j].z - s1 - xh[q][j].z * s2);
             o.w = rs[q] * (gv[q][j].w * gm[j].w - s1 - xh[q][j].w * s2);
+            if (res) {
+              o.x = rv[j].x + o.x; o.y = rv[j].y + o.y;
+              o.z = rv[j].z + o.z; o.w = rv[j].w + o.w;
+            }
             d4[i] = o;
           }
         }
@@ -616,6 +632,7 @@ __global__ __launch_bounds__(kBlock) void k_ln_bwd_block(const float* __restrict
                                                          const float* __restrict__ gamma,
                                                          const float* __restrict__ mean,
                                                          const float* __restrict__ rstd,
+                                                         const float* __restrict__ res,
                                                          float* __restrict__ dx,
                                                          float* __restrict__ pg,
                                                          float* __restrict__ pb, int64_t cols) {
@@ -639,7 +656,8 @@ __global__ __launch_bounds__(kBlock) void k_ln_bwd_block(const float* __restrict
     for (int64_t i = threadIdx.x; i < cols; i += kBlock) {
       float gg = g[i] * (gamma ? gamma[i] : 1.f);
       float xh = (xr[i] - mu) * rs;
-      dx[r * cols + i] = rs * (gg - s1 - xh * s2);
+      const float o = rs * (gg - s1 - xh * s2);
+      dx[r * cols + i] = res ? res[r * cols + i] + o : o;
     }
   }
 }
@@ -844,8 +862,17 @@ int tjh_layer_norm_forward(const float* x, const float* gamma, const float* beta
 int tjh_layer_norm_backward(const float* dy, const float* x, const float* gamma,
                             const float* mean, const float* rstd, float* dx, float* dgamma,
                             float* dbeta, int64_t rows, int64_t cols, int accumulate) {
+  return tjh_layer_norm_backward_res(dy, x, gamma, mean, rstd, nullptr, dx, dgamma, dbeta, rows,
+                                     cols, accumulate);
+}
+
+int tjh_layer_norm_backward_res(const float* dy, const float* x, const float* gamma,
+                                const float* mean, const float* rstd, const float* res,
+                                float* dx, float* dgamma, float* dbeta, int64_t rows,
+                                int64_t cols, int accumulate) {
   TJH_REQUIRE_INIT();
   TJH_ARG(rows >= 0 && cols > 0, "tjh_layer_norm_backward: bad sizes");
+  TJH_ARG(!res || dx, "tjh_layer_norm_backward_res: res needs dx");
   if (rows == 0) {
     if (!accumulate) {
       if (dgamma) { int rc = tjh_fill_f32(dgamma, cols, 0.f); if (rc) return rc; }
@@ -855,7 +882,7 @@ int tjh_layer_norm_backward(const float* dy, const float* x, const float* gamma,
   }
   bool want_p = dgamma || dbeta;
   bool vec = cols % 4 == 0 && aligned16(x) && aligned16(dy) && (!dx || aligned16(dx)) &&
-             (!gamma || aligned16(gamma));
+             (!gamma || aligned16(gamma)) && (!res || aligned16(res));
   int v4 = cols <= 64 * 4 * 3 ? 3 : (cols <= 64 * 4 * 6 ? 6 : (cols <= 64 * 4 * 12 ? 12 : 0));
   if (vec && v4) {
     // rows per block: ~2 blocks per CU, >= 16 rows each (fewer partial
@@ -872,16 +899,16 @@ int tjh_layer_norm_backward(const float* dy, const float* x, const float* gamma,
       KernelScope ks("layer_norm_bwd");
       if (v4 == 3 && cols == 64 * 4 * 3)
         hipLaunchKernelGGL((k_ln_bwd_wave<3, true>), dim3((unsigned)nb), dim3(kBlock), 0, stream(),
-                           dy, x, gamma, mean, rstd, dx, pg, pb, rows, cols, rpb);
+                           dy, x, gamma, mean, rstd, res, dx, pg, pb, rows, cols, rpb);
       else if (v4 == 3)
         hipLaunchKernelGGL((k_ln_bwd_wave<3, false>), dim3((unsigned)nb), dim3(kBlock), 0, stream(),
-                           dy, x, gamma, mean, rstd, dx, pg, pb, rows, cols, rpb);
+                           dy, x, gamma, mean, rstd, res, dx, pg, pb, rows, cols, rpb);
       else if (v4 == 6)
         hipLaunchKernelGGL((k_ln_bwd_wave<6, false>), dim3((unsigned)nb), dim3(kBlock), 0, stream(),
-                           dy, x, gamma, mean, rstd, dx, pg, pb, rows, cols, rpb);
+                           dy, x, gamma, mean, rstd, res, dx, pg, pb, rows, cols, rpb);
       else
         hipLaunchKernelGGL((k_ln_bwd_wave<12, false>), dim3((unsigned)nb), dim3(kBlock), 0,
-                           stream(), dy, x, gamma, mean, rstd, dx, pg, pb, rows, cols, rpb);
+                           stream(), dy, x, gamma, mean, rstd, res, dx, pg, pb, rows, cols, rpb);
       int rc = check_launch("layer_norm_backward");
       if (rc != TJH_OK) return rc;
       if (want_p) {
@@ -902,7 +929,7 @@ int tjh_layer_norm_backward(const float* dy, const float* x, const float* gamma,
   {
     KernelScope ks("layer_norm_bwd");
     hipLaunchKernelGGL(k_ln_bwd_block, dim3((unsigned)rows), dim3(kBlock), 0, stream(), dy, x,
-                       gamma, mean, rstd, dx, pg, pb, cols);
+                       gamma, mean, rstd, res, dx, pg, pb, cols);
     int rc = check_launch("layer_norm_backward");
     if (rc != TJH_OK) return rc;
   }

@@ -237,18 +237,25 @@ def layer_norm(x, normalized_shape, weight=None, bias=None, eps=1e-5):
     rw = weight is not None and weight.requires_grad
     rb = bias is not None and bias.requires_grad
 
-    def bwd(g):
+    def bwd(g, pending=None):
+        # pending: a gradient already accumulated for x (the residual
+        # stream's identity path), added to dx by the same kernel
         g = g.contiguous()
         dx = empty(x.shape) if rx else None
         dw = empty(normalized_shape) if rw else None
         db = empty(normalized_shape) if rb else None
-        L.check(L.lib().tjh_layer_norm_backward(
-            g.data_ptr(), xc.data_ptr(), w.data_ptr() if w is not None else None,
-            mean.data_ptr(), rstd.data_ptr(), dx.data_ptr() if dx is not None else None,
-            dw.data_ptr() if dw is not None else None, db.data_ptr() if db is not None else None,
-            rows, cols, 0), "layer_norm_backward")
+        args = (g.data_ptr(), xc.data_ptr(), w.data_ptr() if w is not None else None,
+                mean.data_ptr(), rstd.data_ptr())
+        outs = (dx.data_ptr() if dx is not None else None,
+                dw.data_ptr() if dw is not None else None,
+                db.data_ptr() if db is not None else None, rows, cols, 0)
+        if pending is not None and dx is not None:
+            L.check(L.lib().tjh_layer_norm_backward_res(*args, pending.data_ptr(), *outs),
+                    "layer_norm_backward_res")
+        else:
+            L.check(L.lib().tjh_layer_norm_backward(*args, *outs), "layer_norm_backward")
         return [dx, dw, db]
-    return _record(y, "LayerNorm", [x, weight, bias], bwd)
+    return _record(y, "LayerNorm", [x, weight, bias], bwd, acc_slot=0)
 
 
 # ------------------------------------------------------------ embedding / linear
@@ -317,13 +324,58 @@ def linear(x, weight, bias=None):
     return _record(out, "Linear", [x, weight, bias], bwd)
 
 
-def _mlp_gelu(x, w1, b1, w2, b2):
+def _linear_add(x, weight, bias, residual):
+    """residual + linear(x, weight, bias) -- the residual add that follows
+    the attention projection of a pre-LN transformer block -- as one GEMM
+    whose epilogue adds the residual.  Equal bit for bit to the unfused
+    add; the residual's gradient is the incoming gradient itself."""
+    if residual is None:
+        return linear(x, weight, bias)
+    if x.dtype != "float32":
+        x = x.float()
+    out_f, in_f = weight.shape
+    lead = x.shape[:-1]
+    if x.shape[-1] != in_f or residual.shape != lead + (out_f,):
+        raise RuntimeError("linear_add: shapes %s, %s, %s do not match"
+                           % (list(x.shape), list(weight.shape), list(residual.shape)))
+    M = _numel(lead)
+    x2 = reshape(x.detach(), (M, in_f))
+    wd = weight.detach()
+    bd = bias.detach().contiguous() if bias is not None else None
+    r = residual.detach()
+    r2 = reshape(r if r.dtype == "float32" and r.is_contiguous() else r.float().contiguous(),
+                 (M, out_f))
+    out2 = empty((M, out_f))
+    _gemm(x2, wd.T, out=out2, bias=bd, bias_mode=1 if bd is not None else 0, aux=r2, act=3)
+    out = reshape_raw(out2, lead + (out_f,))
+    rx, rw = x.requires_grad, weight.requires_grad
+    rb = bias is not None and bias.requires_grad
+
+    def bwd(g):
+        g2 = reshape_raw(g, (M, out_f))
+        dx = reshape_raw(_gemm(g2, wd), lead + (in_f,)) if rx else None
+        dw = db = None
+        if rw and rb:
+            db = empty((out_f,))
+            dw = _gemm(g2.T, x2, rowsum_out=db)
+        elif rw:
+            dw = _gemm(g2.T, x2)
+        elif rb:
+            gc = g2 if g2.is_contiguous() else _k_contiguous(g2)
+            db = _view_raw(_k_reduce("sum", gc, [0]), (out_f,))
+        return [dx, dw, db, g]
+    return _record(out, "LinearAdd", [x, weight, bias, residual], bwd)
+
+
+def _mlp_gelu(x, w1, b1, w2, b2, residual=None):
     """linear(gelu(linear(x, w1, b1)), w2, b2) -- the transformer MLP block
     (nn.Linear, nn.GELU, nn.Linear; src/nn/linear.ts:43-66,
     src/nn/activation.ts) -- with GELU fused into the GEMM epilogues: the
     first GEMM writes the pre-activation h and GELU(h), and in the backward
     the second layer's input-gradient GEMM multiplies by GELU'(h) as it
-    writes.  Every value equals the unfused sequence's bit for bit."""
+    writes.  With `residual`, returns residual + MLP(x), the add done by
+    the second GEMM's epilogue.  Every value equals the unfused sequence's
+    bit for bit."""
     if x.dtype != "float32":
         x = x.float()
     hid, d_in = w1.shape
@@ -336,10 +388,20 @@ def _mlp_gelu(x, w1, b1, w2, b2):
     w1d, w2d = w1.detach(), w2.detach()
     b1d = b1.detach().contiguous() if b1 is not None else None
     b2d = b2.detach().contiguous() if b2 is not None else None
+    if residual is not None and residual.shape != lead + (d_out,):
+        raise RuntimeError("mlp: residual shape %s != output shape %s"
+                           % (list(residual.shape), list(lead + (d_out,))))
     h = empty((M, hid))
     a = empty((M, hid))
     _gemm(x2, w1d.T, out=a, bias=b1d, bias_mode=1 if b1d is not None else 0, aux=h, act=1)
-    y2 = _gemm(a, w2d.T, bias=b2d, bias_mode=1 if b2d is not None else 0)
+    if residual is None:
+        y2 = _gemm(a, w2d.T, bias=b2d, bias_mode=1 if b2d is not None else 0)
+    else:
+        r = residual.detach()
+        r2 = reshape(r if r.dtype == "float32" and r.is_contiguous() else r.float().contiguous(),
+                     (M, d_out))
+        y2 = empty((M, d_out))
+        _gemm(a, w2d.T, out=y2, bias=b2d, bias_mode=1 if b2d is not None else 0, aux=r2, act=3)
     out = reshape_raw(y2, lead + (d_out,))
     need = [t is not None and t.requires_grad for t in (x, w1, b1, w2, b2)]
 
@@ -364,8 +426,8 @@ def _mlp_gelu(x, w1, b1, w2, b2):
                 dw1 = _gemm(dh.T, x2, rowsum_out=db1)
             elif need[2]:
                 db1 = _view_raw(_k_reduce("sum", dh, [0]), (hid,))
-        return [dx, dw1, db1, dw2, db2]
-    return _record(out, "MLP", [x, w1, b1, w2, b2], bwd)
+        return [dx, dw1, db1, dw2, db2, g]
+    return _record(out, "MLP", [x, w1, b1, w2, b2, residual], bwd)
 
 
 # ------------------------------------------------------------ convolution

@@ -424,6 +424,18 @@ static napi_value js_ln_backward(napi_env env, napi_callback_info info) {
   return undef(env);
 }
 
+/* layerNormBackwardRes(dy, x, gamma, mean, rstd, res, dx, dgamma, dbeta, rows, cols, accumulate) */
+static napi_value js_ln_backward_res(napi_env env, napi_callback_info info) {
+  napi_value a[12];
+  if (!get_args(env, info, 12, a)) return NULL;
+  CHECK_RC(tjh_layer_norm_backward_res(
+      (const float*)ptr(env, a[0]), (const float*)ptr(env, a[1]), (const float*)ptr(env, a[2]),
+      (const float*)ptr(env, a[3]), (const float*)ptr(env, a[4]), (const float*)ptr(env, a[5]),
+      (float*)ptr(env, a[6]), (float*)ptr(env, a[7]), (float*)ptr(env, a[8]), i64(env, a[9]),
+      i64(env, a[10]), (int)i64(env, a[11])));
+  return undef(env);
+}
+
 static napi_value js_emb_forward(napi_env env, napi_callback_info info) {
   napi_value a[6];
   if (!get_args(env, info, 6, a)) return NULL;
@@ -835,7 +847,8 @@ static napi_value init_module(napi_env env, napi_value exports) {
       FN("reduce", js_reduce), FN("softmaxForward", js_softmax_forward),
       FN("softmaxBackward", js_softmax_backward), FN("crossEntropyForward", js_ce_forward),
       FN("crossEntropyBackward", js_ce_backward), FN("layerNormForward", js_ln_forward),
-      FN("layerNormBackward", js_ln_backward), FN("embeddingForward", js_emb_forward),
+      FN("layerNormBackward", js_ln_backward),
+      FN("layerNormBackwardRes", js_ln_backward_res), FN("embeddingForward", js_emb_forward),
       FN("embeddingBackward", js_emb_backward), FN("gemm", js_gemm), FN("gemmAct", js_gemm_act),
       FN("sdpaForward", js_sdpa_forward), FN("sdpaBackward", js_sdpa_backward),
       FN("adamStep", js_adam_step), FN("isInitialized", js_is_initialized),

@@ -205,14 +205,21 @@ def _wrap_dim(d, ndim):
 class Node:
     """grad_fn: the vector-Jacobian product of one recorded op
     (GradFn, src/tensor/types.ts:13-17).  `inputs` are the op's tensor
-    arguments; `fn(grad)` returns one gradient (or None) per input."""
+    arguments; `fn(grad)` returns one gradient (or None) per input.
 
-    __slots__ = ("name", "inputs", "fn", "__weakref__")
+    `acc_slot`: index of an input whose gradient the VJP can add to a
+    gradient already pending for that input, in the same kernel: the
+    engine then calls `fn(grad, pending)` and takes the returned gradient
+    as the input's whole gradient (the residual stream of a pre-LN block
+    sums the identity path and the LayerNorm path this way)."""
 
-    def __init__(self, name, inputs, fn):
+    __slots__ = ("name", "inputs", "fn", "acc_slot", "__weakref__")
+
+    def __init__(self, name, inputs, fn, acc_slot=None):
         self.name = name
         self.inputs = inputs
         self.fn = fn
+        self.acc_slot = acc_slot
 
     def __repr__(self):
         return "<%sBackward>" % self.name
@@ -223,11 +230,11 @@ class Node:
         return [t for t in self.inputs if t is not None]
 
 
-def _record(out, name, inputs, fn):
+def _record(out, name, inputs, fn, acc_slot=None):
     if _grad["enabled"] and any(t is not None and t.requires_grad for t in inputs):
         out.requires_grad = True
         out.grad_fn = Node(name, [t if (t is not None and t.requires_grad) else None
-                                  for t in inputs], fn)
+                                  for t in inputs], fn, acc_slot)
     return out
 
 
@@ -1663,9 +1670,10 @@ def _gemm(a, b, out=None, alpha=1.0, beta=0.0, bias=None, bias_mode=0, rowsum_ou
     """out[M,N] = alpha*a[M,K] @ b[K,N] (+beta*out) (+bias) for 2-D views.
     rowsum_out (a contiguous [M] tensor) receives the row sums of `a` from
     the same launch (bias_mode 3: a Linear layer's bias gradient computed
-    with its weight gradient).  act 1 / 2 with aux ([M,N], row stride as
-    out's) fuses GELU into the epilogue: 1 writes the pre-activation to
-    aux and GELU of it to out, 2 multiplies by GELU'(aux)."""
+    with its weight gradient).  act 1 / 2 / 3 with aux ([M,N], row stride
+    as out's) fuses an elementwise op into the epilogue: 1 writes the
+    pre-activation to aux and GELU of it to out, 2 multiplies by
+    GELU'(aux), 3 adds aux (a residual; must not overlap out)."""
     if rowsum_out is not None:
         assert bias is None and bias_mode == 0 and rowsum_out.is_contiguous()
         bias, bias_mode = rowsum_out, 3
@@ -1923,10 +1931,14 @@ def run_backward(pairs, retain_graph=False, inputs=None):
             if node.fn is None:
                 raise RuntimeError("Trying to backward through the graph a second time; "
                                    "pass retain_graph=True the first time")
-            in_grads = node.fn(g)
+            acc = _pending_for(node, grads, wanted)
+            in_grads = node.fn(g) if acc is None else node.fn(g, acc)
             del g
-            for t, gi in zip(node.inputs, in_grads):
+            for slot, (t, gi) in enumerate(zip(node.inputs, in_grads)):
                 if t is None or gi is None:
+                    continue
+                if acc is not None and slot == node.acc_slot:
+                    grads[id(t.grad_fn)] = gi  # already holds the pending gradient
                     continue
                 if isinstance(gi, _SliceGrad) and (t.grad_fn is None or t._retains_grad or
                                                    (wanted is not None and id(t) in wanted)):
@@ -1951,6 +1963,31 @@ def run_backward(pairs, retain_graph=False, inputs=None):
         return None
     finally:
         _grad["enabled"] = prev
+
+
+def _pending_for(node, grads, wanted):
+    """The gradient pending for input `node.acc_slot`, when the VJP may fold
+    it in: a non-leaf input that retains no grad, is not asked for by
+    autograd.grad, and whose pending gradient is one dense contiguous
+    float32 tensor of the input's shape."""
+    k = node.acc_slot
+    if k is None or not _FUSE_ACC:
+        return None
+    t = node.inputs[k]
+    if t is None or t.grad_fn is None or t._retains_grad:
+        return None
+    if wanted is not None and id(t) in wanted:
+        return None
+    prev = grads.get(id(t.grad_fn))
+    if (prev is None or isinstance(prev, _SliceGrad) or prev.shape != t.shape or
+            prev._dtype != "float32" or not prev.is_contiguous()):
+        return None
+    return prev
+
+
+# folding pending gradients into VJPs (acc_slot); off only to compare with
+# the plain sum in tests
+_FUSE_ACC = True
 
 
 def _leaf_accumulate(t, g, owned, force_copy=False):

@@ -42,7 +42,9 @@ class CausalSelfAttention(nn.Module):
         self.c_attn = nn.Linear(d, 3 * d)
         self.c_proj = nn.Linear(d, d)
 
-    def forward(self, x):
+    def forward(self, x, residual=None):
+        """attention(x), or residual + attention(x) with the add done by the
+        output projection's GEMM epilogue."""
         B, T, C = x.shape
         hd = C // self.heads
         q, k, v = self.c_attn(x).split(C, dim=2)
@@ -51,7 +53,7 @@ class CausalSelfAttention(nn.Module):
         v = v.view(B, T, self.heads, hd).transpose(1, 2)
         y = F.scaled_dot_product_attention(q, k, v, is_causal=True)
         y = y.transpose(1, 2).contiguous().view(B, T, C)
-        return self.c_proj(y)
+        return F._linear_add(y, self.c_proj.weight, self.c_proj.bias, residual)
 
 
 class MLPBlock(nn.Module):
@@ -60,10 +62,11 @@ class MLPBlock(nn.Module):
         self.c_fc = nn.Linear(d, 4 * d)
         self.c_proj = nn.Linear(4 * d, d)
 
-    def forward(self, x):
-        # c_proj(gelu(c_fc(x))) with GELU fused into the two GEMMs
+    def forward(self, x, residual=None):
+        # c_proj(gelu(c_fc(x))) (+ residual) with GELU and the add fused
+        # into the two GEMMs
         return F._mlp_gelu(x, self.c_fc.weight, self.c_fc.bias, self.c_proj.weight,
-                           self.c_proj.bias)
+                           self.c_proj.bias, residual)
 
 
 class Block(nn.Module):
@@ -77,8 +80,10 @@ class Block(nn.Module):
         self.mlp = MLPBlock(d)
 
     def forward(self, x):
-        x = x + self.attn(self.ln_1(x))
-        return x + self.mlp(self.ln_2(x))
+        # x + attn(ln_1(x)), then x + mlp(ln_2(x)); each residual add runs in
+        # the epilogue of the branch's last GEMM
+        x = self.attn(self.ln_1(x), residual=x)
+        return self.mlp(self.ln_2(x), residual=x)
 
 
 class GPT2(nn.Module):
