@@ -268,8 +268,12 @@ def test_layer_norm(torch, rows, cols):
 # ------------------------------------------------------------------ embedding / indexing
 
 
-@pytest.mark.parametrize("V,D,n", [(50257, 768, 8192), (7, 4, 6), (1000, 9, 20000), (3, 64, 1)])
+@pytest.mark.parametrize("V,D,n", [(50257, 768, 8192), (7, 4, 6), (1000, 9, 20000), (3, 64, 1),
+                                   (70, 16, 16384), (300000, 8, 16384)])
 def test_embedding(torch, V, D, n):
+    """Lookup and deterministic scatter-add backward; n <= 16384 with
+    V * n <= 2^32 sorts the (id, position) keys by rank in one launch, the
+    rest by the bitonic network."""
     r = np.random.default_rng(V + n)
     w = f32(r.standard_normal((V, D)))
     ids = r.integers(0, V, n).astype(np.int32)
@@ -289,6 +293,35 @@ def test_embedding(torch, V, D, n):
     out2 = torch.F.embedding(torch.tensor(ids), wt)
     out2.backward(torch.tensor(g))
     assert np.array_equal(wt.grad.numpy(), got)
+
+
+def test_embedding_tied_to_lm_head(torch):
+    """A table used by an embedding lookup and as the weight of the output
+    projection (GPT-2's tied wte): the embedding backward adds its rows into
+    the projection's weight gradient in place; the result matches the sum
+    of both gradients (and the unfused path) within tolerance."""
+    from torchjs_amd import tensor as T
+    r = np.random.default_rng(31)
+    V, D, n = 500, 32, 300
+    w = f32(r.standard_normal((V, D)) * 0.1)
+    ids = r.integers(0, V, n).astype(np.int32)
+    g = f32(r.standard_normal((n, V)))
+    got = []
+    for fuse in (True, False):
+        T._FUSE_ACC = fuse
+        try:
+            wt = torch.tensor(w, requires_grad=True)
+            x = torch.F.embedding(torch.tensor(ids), wt)
+            y = torch.F.linear(x * 1.5, wt)
+            y.backward(torch.tensor(g))
+            got.append(wt.grad.numpy())
+        finally:
+            T._FUSE_ACC = True
+    xd = 1.5 * w[ids].astype(np.float64)
+    d_head = g.astype(np.float64).T @ xd
+    d_emb = ops.embedding_backward(1.5 * (g.astype(np.float64) @ w.astype(np.float64)), ids, V)
+    check(got[0], d_head + d_emb, **RED)
+    check(got[0], got[1], **RED)
 
 
 def test_embedding_clamps_ids(torch):

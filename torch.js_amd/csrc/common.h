@@ -71,6 +71,9 @@ int flash_backward(const float* q, const float* k, const float* v, const float* 
                    int64_t B, int64_t H, int64_t Tq, int64_t Tk, const int64_t* const* strides,
                    float scale, int causal);
 
+// 16-byte alignment of a device pointer (128-bit access paths).
+inline bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
 // Streaming (non-temporal) 128-bit global loads and stores, for data that
 // is dead after the access (optimizer state, logits read by the loss
 // backward): on MI355X they lift a 1 GiB copy from 5.7 to 6.2 TB/s, but a

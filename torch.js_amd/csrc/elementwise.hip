@@ -99,8 +99,6 @@ bool out_contiguous(const Layout& L) {
   return true;
 }
 
-bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
-
 int grid_for(int64_t work_items) {
   int64_t g = cdiv(work_items, kBlock);
   int64_t cap = (int64_t)num_cus() * 32;

@@ -431,8 +431,6 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(GemmArgs g, int splits) {
   }
 }
 
-bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
-
 // ------------------------------------------------------------ tile choice
 
 struct TileCfg {

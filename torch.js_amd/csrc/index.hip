@@ -58,6 +58,37 @@ __global__ __launch_bounds__(kBlock) void k_make_keys(const int32_t* __restrict_
   keys[i] = i < n ? (((uint64_t)clamp_id(ids[i], num)) << 32) | (uint64_t)i : ~0ull;
 }
 
+// Sorting the keys of a short index list by rank: key i lands at
+// #{j : key_j < key_i}.  Keys are distinct (the position is part of the
+// key), so the ranks are a permutation and the result is the sorted key
+// array, in one launch.  Here a key is packed in 32 bits as
+// clamp(id) * n + position (the caller checks num * n <= 2^32); all n of
+// them sit in LDS, padded to a multiple of 4 with 0xffffffff, which is
+// never below a key.  A workgroup ranks 16 keys; the 16 lanes of a key
+// split the comparisons and combine their counts with shuffles.
+constexpr int kRankMax = 16384;
+__global__ __launch_bounds__(256) void k_rank_keys(const int32_t* __restrict__ ids, int64_t n,
+                                                   int64_t num, uint64_t* __restrict__ keys) {
+  __shared__ __attribute__((aligned(16))) uint32_t sk[kRankMax];
+  const uint32_t nn = (uint32_t)n;
+  const int n4 = (int)((n + 3) >> 2);
+  for (int j = threadIdx.x; j < 4 * n4; j += 256)
+    sk[j] = j < n ? (uint32_t)clamp_id(ids[j], num) * nn + (uint32_t)j : 0xffffffffu;
+  __syncthreads();
+  const int64_t i = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+  const int part = threadIdx.x & 15;
+  const uint32_t ki = i < n ? sk[i] : 0u;
+  uint32_t cnt = 0;
+  const uint4* s4 = reinterpret_cast<const uint4*>(sk);
+  for (int j = part; j < n4; j += 16) {
+    const uint4 v = s4[j];
+    cnt += (v.x < ki) + (v.y < ki) + (v.z < ki) + (v.w < ki);
+  }
+#pragma unroll
+  for (int off = 8; off >= 1; off >>= 1) cnt += __shfl_xor(cnt, off, 16);
+  if (i < n && part == 0) keys[cnt] = ((uint64_t)(ki / nn) << 32) | (uint64_t)(ki % nn);
+}
+
 constexpr int kSortChunk = 2048;  // elements per LDS stage (1024 lanes x 2)
 constexpr int kSortThreads = 1024;
 
@@ -314,24 +345,32 @@ int tjh_embedding_backward(const float* dout, const int32_t* ids, int64_t n, int
     if (rc != TJH_OK) return rc;
   }
   if (n == 0 || dim == 0) return TJH_OK;
+  // short lists (a batch of token positions) are sorted by rank in one
+  // launch; longer ones by the bitonic network
+  const bool by_rank = n <= kRankMax && (uint64_t)num * (uint64_t)n <= (1ull << 32);
   int64_t npad = 1;
   while (npad < n) npad <<= 1;
   if (npad < 2) npad = 2;
-  Scratch keys_s((size_t)npad * sizeof(uint64_t));
+  Scratch keys_s((size_t)(by_rank ? n : npad) * sizeof(uint64_t));
   if (!keys_s.ok()) return set_error(TJH_ERR_OOM, "embedding_backward: no scratch");
   uint64_t* keys = keys_s.as<uint64_t>();
   KernelScope ks("embedding_bwd");
-  hipLaunchKernelGGL(k_make_keys, dim3((unsigned)cdiv(npad, kBlock)), dim3(kBlock), 0, stream(),
-                     ids, n, num, npad, keys);
-  unsigned chunks = (unsigned)cdiv(npad, kSortChunk);
-  hipLaunchKernelGGL(k_bitonic_local<true>, dim3(chunks), dim3(kSortThreads), 0, stream(), keys,
-                     npad, (int64_t)0);
-  for (int64_t k = 2 * kSortChunk; k <= npad; k <<= 1) {
-    for (int64_t j = k >> 1; j >= kSortChunk; j >>= 1)
-      hipLaunchKernelGGL(k_bitonic_global, dim3((unsigned)cdiv(npad / 2, kBlock)), dim3(kBlock), 0,
-                         stream(), keys, npad, k, j);
-    hipLaunchKernelGGL(k_bitonic_local<false>, dim3(chunks), dim3(kSortThreads), 0, stream(), keys,
-                       npad, k);
+  if (by_rank) {
+    hipLaunchKernelGGL(k_rank_keys, dim3((unsigned)cdiv(n, 16)), dim3(256), 0, stream(), ids, n,
+                       num, keys);
+  } else {
+    hipLaunchKernelGGL(k_make_keys, dim3((unsigned)cdiv(npad, kBlock)), dim3(kBlock), 0, stream(),
+                       ids, n, num, npad, keys);
+    unsigned chunks = (unsigned)cdiv(npad, kSortChunk);
+    hipLaunchKernelGGL(k_bitonic_local<true>, dim3(chunks), dim3(kSortThreads), 0, stream(), keys,
+                       npad, (int64_t)0);
+    for (int64_t k = 2 * kSortChunk; k <= npad; k <<= 1) {
+      for (int64_t j = k >> 1; j >= kSortChunk; j >>= 1)
+        hipLaunchKernelGGL(k_bitonic_global, dim3((unsigned)cdiv(npad / 2, kBlock)), dim3(kBlock),
+                           0, stream(), keys, npad, k, j);
+      hipLaunchKernelGGL(k_bitonic_local<false>, dim3(chunks), dim3(kSortThreads), 0, stream(),
+                         keys, npad, k);
+    }
   }
   int rc = check_launch("embedding_backward_sort");
   if (rc != TJH_OK) return rc;

@@ -685,8 +685,6 @@ int sum_partials(const float* pg, const float* pb, int64_t nb, int64_t cols, flo
   return TJH_OK;
 }
 
-bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
-
 }  // namespace
 }  // namespace tjh
 

@@ -115,8 +115,6 @@ __global__ __launch_bounds__(kBlock) void k_adam(AdamBatch B) {
   }
 }
 
-bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
-
 }  // namespace
 }  // namespace tjh
 

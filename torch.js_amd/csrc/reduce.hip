@@ -237,8 +237,6 @@ __global__ __launch_bounds__(64 * kFinalWaves) void k_colsum_final(FinalArgs fa,
   }
 }
 
-bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
-
 template <int OP>
 int reduce_rows(const float* x, int64_t outer, int64_t r, float* out, float scale) {
   // a single reduction level: split long rows over several workgroups

@@ -278,13 +278,18 @@ def embedding(input, weight):
     L.check(L.lib().tjh_embedding_forward(w.data_ptr(), V, D, ids.data_ptr(), n, out.data_ptr()),
             "embedding")
 
-    def bwd(g):
+    def bwd(g, pending=None):
+        # pending: the table's gradient so far in this backward pass (a table
+        # tied to the LM head already holds that layer's weight gradient);
+        # the rows are then added into it in place, with no zero fill of a
+        # second [V, D] table and no add of the two
         g = g.contiguous()
-        dw = empty((V, D))
+        dw = pending if pending is not None else empty((V, D))
         L.check(L.lib().tjh_embedding_backward(g.data_ptr(), ids.data_ptr(), n, D, dw.data_ptr(),
-                                               V, 0), "embedding_backward")
+                                               V, 1 if pending is not None else 0),
+                "embedding_backward")
         return [dw]
-    return _record(out, "Embedding", [weight], bwd)
+    return _record(out, "Embedding", [weight], bwd, acc_slot=0)
 
 
 def linear(x, weight, bias=None):

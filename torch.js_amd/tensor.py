@@ -1931,14 +1931,18 @@ def run_backward(pairs, retain_graph=False, inputs=None):
             if node.fn is None:
                 raise RuntimeError("Trying to backward through the graph a second time; "
                                    "pass retain_graph=True the first time")
-            acc = _pending_for(node, grads, wanted)
+            acc = _pending_for(node, grads, wanted, owned)
             in_grads = node.fn(g) if acc is None else node.fn(g, acc)
             del g
             for slot, (t, gi) in enumerate(zip(node.inputs, in_grads)):
                 if t is None or gi is None:
                     continue
                 if acc is not None and slot == node.acc_slot:
-                    grads[id(t.grad_fn)] = gi  # already holds the pending gradient
+                    # gi already holds the pending gradient
+                    if t.grad_fn is None:
+                        t._grad = gi
+                    else:
+                        grads[id(t.grad_fn)] = gi
                     continue
                 if isinstance(gi, _SliceGrad) and (t.grad_fn is None or t._retains_grad or
                                                    (wanted is not None and id(t) in wanted)):
@@ -1965,20 +1969,32 @@ def run_backward(pairs, retain_graph=False, inputs=None):
         _grad["enabled"] = prev
 
 
-def _pending_for(node, grads, wanted):
+def _pending_for(node, grads, wanted, owned):
     """The gradient pending for input `node.acc_slot`, when the VJP may fold
-    it in: a non-leaf input that retains no grad, is not asked for by
-    autograd.grad, and whose pending gradient is one dense contiguous
-    float32 tensor of the input's shape."""
+    it in: one dense contiguous float32 tensor of the input's shape, and
+    either the pending gradient of a non-leaf that retains no grad, or the
+    .grad of a leaf that this backward pass created and that no pending
+    gradient shares storage with (the VJP may then add into it in place, as
+    the embedding backward of a table tied to the LM head does).  Inputs
+    asked for by autograd.grad never take part."""
     k = node.acc_slot
     if k is None or not _FUSE_ACC:
         return None
     t = node.inputs[k]
-    if t is None or t.grad_fn is None or t._retains_grad:
+    if t is None or (wanted is not None):
         return None
-    if wanted is not None and id(t) in wanted:
-        return None
-    prev = grads.get(id(t.grad_fn))
+    if t.grad_fn is None:
+        prev = t._grad
+        if prev is None or id(prev._storage) not in owned:
+            return None
+        for p in grads.values():
+            pieces = p.pieces if isinstance(p, _SliceGrad) else [(0, p)]
+            if any(q._storage is prev._storage for _, q in pieces):
+                return None
+    else:
+        if t._retains_grad:
+            return None
+        prev = grads.get(id(t.grad_fn))
     if (prev is None or isinstance(prev, _SliceGrad) or prev.shape != t.shape or
             prev._dtype != "float32" or not prev.is_contiguous()):
         return None
