@@ -312,17 +312,26 @@ int tjh_layer_norm_backward(const float* dy, const float* x,
                             float* dbeta, int64_t rows, int64_t cols,
                             int accumulate);
 /* tjh_layer_norm_backward with dx = res + the LayerNorm input gradient, in
- * one pass (res [rows, cols], dx required; res may not overlap dx).  The
- * pre-LN residual stream x -> x + f(LayerNorm(x)) of torch.js's
- * transformer blocks gives x two gradient contributions that its autograd
- * sums with a separate add (accumulateGrad, Tensor.ts:3670-3677); this
- * entry folds that add into the LayerNorm backward.  Equal bit for bit to
- * tjh_layer_norm_backward followed by the add. */
+ * one pass (res [rows, cols] or NULL; with res, dx is required and may not
+ * overlap it).  The pre-LN residual stream x -> x + f(LayerNorm(x)) of
+ * torch.js's transformer blocks gives x two gradient contributions that
+ * its autograd sums with a separate add (accumulateGrad,
+ * Tensor.ts:3670-3677); this entry folds that add into the LayerNorm
+ * backward, equal bit for bit to tjh_layer_norm_backward followed by the
+ * add.  flags: bit 0 (1) accumulates dgamma/dbeta as `accumulate` does;
+ * TJH_LN_DEFER lets the library postpone the dgamma/dbeta finishing pass
+ * to the next tjh_flush_deferred, which finishes every postponed
+ * LayerNorm in one launch (dx is final on return; dgamma/dbeta are not
+ * until the flush).  An autograd pass over a model with many LayerNorms
+ * (25 in GPT-2 124M) defers them all and flushes once at its end. */
+enum { TJH_LN_DEFER = 2 };
 int tjh_layer_norm_backward_res(const float* dy, const float* x,
                                 const float* gamma, const float* mean,
                                 const float* rstd, const float* res,
                                 float* dx, float* dgamma, float* dbeta,
-                                int64_t rows, int64_t cols, int accumulate);
+                                int64_t rows, int64_t cols, int flags);
+/* Runs the finishing passes postponed by TJH_LN_DEFER (none: no launch). */
+int tjh_flush_deferred(void);
 
 /* ------------------------------------------------------------------ */
 /* Embedding / indexing — embedding.wgsl:13-27, index_select.wgsl,      */

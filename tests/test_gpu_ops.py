@@ -877,3 +877,51 @@ def test_block_residual_fusion_equals_unfused(torch):
     for other in outs[1:]:
         for a_, b_ in zip(outs[0], other):
             assert np.array_equal(a_, b_)
+
+
+def test_layer_norm_deferred_weight_grads(torch):
+    """LayerNorm weight gradients whose finishing pass the engine defers to
+    one batched launch at the end of backward: a LayerNorm applied twice
+    (its gamma/beta receive two contributions, forcing an early flush), a
+    chain of LayerNorms and leaves with a .grad from an earlier backward;
+    bit-identical to the undeferred engine, and to the oracle."""
+    from torchjs_amd import tensor as T
+    r = np.random.default_rng(17)
+    rows, cols = 96, 768
+    x0 = f32(r.standard_normal((rows, cols)))
+    gms = [f32(1 + 0.1 * r.standard_normal(cols)) for _ in range(3)]
+    bts = [f32(0.1 * r.standard_normal(cols)) for _ in range(3)]
+    g = f32(r.standard_normal((rows, cols)))
+    runs = []
+    for fuse in (True, False):
+        T._FUSE_ACC = fuse
+        try:
+            ps = [torch.tensor(a, requires_grad=True) for a in gms + bts]
+            x = torch.tensor(x0, requires_grad=True)
+            F = torch.F
+            h = F.layer_norm(x * 1.0, (cols,), ps[0], ps[3])
+            h = F.layer_norm(h * 2.0, (cols,), ps[1], ps[4])
+            h = F.layer_norm(h + x, (cols,), ps[0], ps[3])  # gamma/beta 0 used twice
+            y = F.layer_norm(h, (cols,), ps[2], ps[5])
+            y.backward(torch.tensor(g))
+            first = [p.grad.numpy() for p in ps] + [x.grad.numpy()]
+            y2 = F.layer_norm(F.layer_norm(x * 1.0, (cols,), ps[1], ps[4]), (cols,), ps[2], ps[5])
+            y2.backward(torch.tensor(g))  # accumulates into existing .grad
+            runs.append(first + [p.grad.numpy() for p in ps])
+        finally:
+            T._FUSE_ACC = True
+    for a_, b_ in zip(*runs):
+        assert np.array_equal(a_, b_)
+    # last LayerNorm's gamma / beta gradients against the oracle
+    hd = runs[0]  # first backward's grads
+    _, dgm, dbt = ops.layer_norm_backward(g, _ln_chain_input(x0, gms, bts), gms[2])
+    check(hd[2], dgm, rtol=1e-4, atol=1e-3)
+    check(hd[5], dbt, rtol=1e-4, atol=1e-3)
+
+
+def _ln_chain_input(x0, gms, bts):
+    """The input of the last LayerNorm in test_layer_norm_deferred_weight_grads."""
+    x = x0.astype(np.float64)
+    h = ops.layer_norm(x, gms[0], bts[0])[0]
+    h = ops.layer_norm(2.0 * h, gms[1], bts[1])[0]
+    return ops.layer_norm(h + x, gms[0], bts[0])[0]

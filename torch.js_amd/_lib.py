@@ -108,6 +108,7 @@ SIGNATURES = {
                                 c_int],
     "tjh_layer_norm_backward_res": [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64,
                                     c_i64, c_int],
+    "tjh_flush_deferred": [],
     "tjh_embedding_forward": [c_vp, c_i64, c_i64, c_vp, c_i64, c_vp],
     "tjh_embedding_backward": [c_vp, c_vp, c_i64, c_i64, c_vp, c_i64, c_int],
     "tjh_index_select": [c_vp, c_i64, c_i64, c_i64, c_vp, c_i64, c_vp],

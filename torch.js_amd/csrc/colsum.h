@@ -27,7 +27,7 @@ struct Kahan {
   }
 };
 
-constexpr int kFinalMax = 8;  // outputs one colsum_final launch can finish
+constexpr int kFinalMax = 64;  // outputs one colsum_final launch can finish
 constexpr int kBatch = 8;     // rows fetched before they are accumulated
 
 // out[i][c] (=|+=) scale * sum_b part[i][b][c] for i < np (out[i] may be

@@ -50,6 +50,12 @@ struct Scratch {
   ~Scratch() { if (p) scratch_free(p); }
   template <typename T> T* as() const { return static_cast<T*>(p); }
   bool ok() const { return p != nullptr; }
+  // hands the block to the caller, who scratch_free()s it later
+  void* release() {
+    void* q = p;
+    p = nullptr;
+    return q;
+  }
 };
 
 // The MFMA GEMM behind tjh_gemm / tjh_gemm_act, timed under `family` (so

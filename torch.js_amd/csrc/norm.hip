@@ -16,6 +16,8 @@
 
 #include "colsum.h"
 
+#include <vector>
+
 #include <float.h>
 
 namespace tjh {
@@ -690,6 +692,26 @@ int sum_partials(const float* pg, const float* pb, int64_t nb, int64_t cols, flo
 
 using namespace tjh;
 
+namespace tjh {
+namespace {
+
+// LayerNorm backwards whose dgamma/dbeta finishing pass waits for
+// tjh_flush_deferred: the partial-row scratch block and the outputs.
+struct DeferredSums {
+  void* part;  // [2][nb][cols]: dgamma rows, then dbeta rows
+  float* outs[2];
+  int64_t nb, cols;
+  int accumulate;
+};
+
+std::vector<DeferredSums>& deferred_sums() {
+  static std::vector<DeferredSums> q;
+  return q;
+}
+
+}  // namespace
+}  // namespace tjh
+
 extern "C" {
 
 int tjh_softmax_forward(const float* x, int64_t ldx, float* y, int64_t ldy, int64_t rows,
@@ -861,16 +883,19 @@ int tjh_layer_norm_backward(const float* dy, const float* x, const float* gamma,
                             const float* mean, const float* rstd, float* dx, float* dgamma,
                             float* dbeta, int64_t rows, int64_t cols, int accumulate) {
   return tjh_layer_norm_backward_res(dy, x, gamma, mean, rstd, nullptr, dx, dgamma, dbeta, rows,
-                                     cols, accumulate);
+                                     cols, accumulate ? 1 : 0);
 }
 
 int tjh_layer_norm_backward_res(const float* dy, const float* x, const float* gamma,
                                 const float* mean, const float* rstd, const float* res,
                                 float* dx, float* dgamma, float* dbeta, int64_t rows,
-                                int64_t cols, int accumulate) {
+                                int64_t cols, int flags) {
   TJH_REQUIRE_INIT();
   TJH_ARG(rows >= 0 && cols > 0, "tjh_layer_norm_backward: bad sizes");
   TJH_ARG(!res || dx, "tjh_layer_norm_backward_res: res needs dx");
+  TJH_ARG((flags & ~3) == 0, "tjh_layer_norm_backward: bad flags %d", flags);
+  const int accumulate = flags & 1;
+  const bool defer = (flags & TJH_LN_DEFER) != 0;
   if (rows == 0) {
     if (!accumulate) {
       if (dgamma) { int rc = tjh_fill_f32(dgamma, cols, 0.f); if (rc) return rc; }
@@ -909,7 +934,12 @@ int tjh_layer_norm_backward_res(const float* dy, const float* x, const float* ga
                            stream(), dy, x, gamma, mean, rstd, res, dx, pg, pb, rows, cols, rpb);
       int rc = check_launch("layer_norm_backward");
       if (rc != TJH_OK) return rc;
-      if (want_p) {
+      if (want_p && defer) {
+        // dgamma and dbeta wait for tjh_flush_deferred, which finishes
+        // every queued LayerNorm in one launch
+        deferred_sums().push_back(DeferredSums{part.release(), {dgamma, dbeta}, nb, cols,
+                                               accumulate});
+      } else if (want_p) {
         // dgamma and dbeta from the per-workgroup partial rows, one launch
         float* parts[2] = {pg, pb};
         float* outs[2] = {dgamma, dbeta};
@@ -933,6 +963,37 @@ int tjh_layer_norm_backward_res(const float* dy, const float* x, const float* ga
   }
   if (want_p) return sum_partials(pg, pb, rows, cols, dgamma, dbeta, accumulate);
   return TJH_OK;
+}
+
+int tjh_flush_deferred(void) {
+  TJH_REQUIRE_INIT();
+  std::vector<DeferredSums>& q = deferred_sums();
+  int rc = TJH_OK;
+  {
+    KernelScope ks("layer_norm_bwd");
+    // one colsum_final launch per run of entries with the same shape
+    size_t i = 0;
+    while (i < q.size() && rc == TJH_OK) {
+      float* parts[kFinalMax];
+      float* outs[kFinalMax];
+      int np = 0;
+      size_t j = i;
+      while (j < q.size() && np + 2 <= kFinalMax && q[j].nb == q[i].nb &&
+             q[j].cols == q[i].cols && q[j].accumulate == q[i].accumulate) {
+        float* base = static_cast<float*>(q[j].part);
+        parts[np] = base;
+        outs[np++] = q[j].outs[0];
+        parts[np] = base + q[j].nb * q[j].cols;
+        outs[np++] = q[j].outs[1];
+        ++j;
+      }
+      rc = colsum_final(parts, outs, np, q[i].nb, q[i].cols, q[i].accumulate, 1.0f);
+      i = j;
+    }
+  }
+  for (DeferredSums& e : q) scratch_free(e.part);
+  q.clear();
+  return rc;
 }
 
 }  // extern "C"

@@ -211,6 +211,9 @@ def mse_loss(input, target, reduction="mean"):
 # ------------------------------------------------------------ normalisation
 
 
+_LN_DEFER = 2  # TJH_LN_DEFER
+
+
 def layer_norm(x, normalized_shape, weight=None, bias=None, eps=1e-5):
     """nn.LayerNorm forward (layernorm.wgsl:14-42: biased variance, eps
     inside the sqrt) and backward dx, dgamma, dbeta (torch.js has none, D10)."""
@@ -237,9 +240,11 @@ def layer_norm(x, normalized_shape, weight=None, bias=None, eps=1e-5):
     rw = weight is not None and weight.requires_grad
     rb = bias is not None and bias.requires_grad
 
-    def bwd(g, pending=None):
+    def bwd(g, pending=None, defer=False):
         # pending: a gradient already accumulated for x (the residual
-        # stream's identity path), added to dx by the same kernel
+        # stream's identity path), added to dx by the same kernel.  defer:
+        # the engine will call tjh_flush_deferred before anything reads dw
+        # / db, so their finishing pass may wait and run batched
         g = g.contiguous()
         dx = empty(x.shape) if rx else None
         dw = empty(normalized_shape) if rw else None
@@ -248,14 +253,16 @@ def layer_norm(x, normalized_shape, weight=None, bias=None, eps=1e-5):
                 mean.data_ptr(), rstd.data_ptr())
         outs = (dx.data_ptr() if dx is not None else None,
                 dw.data_ptr() if dw is not None else None,
-                db.data_ptr() if db is not None else None, rows, cols, 0)
-        if pending is not None and dx is not None:
-            L.check(L.lib().tjh_layer_norm_backward_res(*args, pending.data_ptr(), *outs),
-                    "layer_norm_backward_res")
+                db.data_ptr() if db is not None else None, rows, cols,
+                _LN_DEFER if defer else 0)
+        if (pending is not None and dx is not None) or defer:
+            L.check(L.lib().tjh_layer_norm_backward_res(
+                *args, pending.data_ptr() if pending is not None else None, *outs),
+                "layer_norm_backward_res")
         else:
             L.check(L.lib().tjh_layer_norm_backward(*args, *outs), "layer_norm_backward")
         return [dx, dw, db]
-    return _record(y, "LayerNorm", [x, weight, bias], bwd, acc_slot=0)
+    return _record(y, "LayerNorm", [x, weight, bias], bwd, acc_slot=0, defer_slots=(1, 2))
 
 
 # ------------------------------------------------------------ embedding / linear

@@ -436,6 +436,13 @@ static napi_value js_ln_backward_res(napi_env env, napi_callback_info info) {
   return undef(env);
 }
 
+/* flushDeferred() */
+static napi_value js_flush_deferred(napi_env env, napi_callback_info info) {
+  (void)info;
+  CHECK_RC(tjh_flush_deferred());
+  return undef(env);
+}
+
 static napi_value js_emb_forward(napi_env env, napi_callback_info info) {
   napi_value a[6];
   if (!get_args(env, info, 6, a)) return NULL;
@@ -848,7 +855,7 @@ static napi_value init_module(napi_env env, napi_value exports) {
       FN("softmaxBackward", js_softmax_backward), FN("crossEntropyForward", js_ce_forward),
       FN("crossEntropyBackward", js_ce_backward), FN("layerNormForward", js_ln_forward),
       FN("layerNormBackward", js_ln_backward),
-      FN("layerNormBackwardRes", js_ln_backward_res), FN("embeddingForward", js_emb_forward),
+      FN("layerNormBackwardRes", js_ln_backward_res), FN("flushDeferred", js_flush_deferred), FN("embeddingForward", js_emb_forward),
       FN("embeddingBackward", js_emb_backward), FN("gemm", js_gemm), FN("gemmAct", js_gemm_act),
       FN("sdpaForward", js_sdpa_forward), FN("sdpaBackward", js_sdpa_backward),
       FN("adamStep", js_adam_step), FN("isInitialized", js_is_initialized),

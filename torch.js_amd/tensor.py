@@ -209,17 +209,24 @@ class Node:
 
     `acc_slot`: index of an input whose gradient the VJP can add to a
     gradient already pending for that input, in the same kernel: the
-    engine then calls `fn(grad, pending)` and takes the returned gradient
-    as the input's whole gradient (the residual stream of a pre-LN block
-    sums the identity path and the LayerNorm path this way)."""
+    engine then calls `fn(grad, pending=...)` and takes the returned
+    gradient as the input's whole gradient (the residual stream of a pre-LN
+    block sums the identity path and the LayerNorm path this way).
 
-    __slots__ = ("name", "inputs", "fn", "acc_slot", "__weakref__")
+    `defer_slots`: inputs whose gradients the VJP may leave unfinished
+    until the library's tjh_flush_deferred (`fn(grad, defer=True)`); the
+    engine allows it when each of them is a leaf receiving its first
+    gradient of the pass, and flushes before any of those gradients is
+    read (a second contribution, the end of the pass)."""
 
-    def __init__(self, name, inputs, fn, acc_slot=None):
+    __slots__ = ("name", "inputs", "fn", "acc_slot", "defer_slots", "__weakref__")
+
+    def __init__(self, name, inputs, fn, acc_slot=None, defer_slots=()):
         self.name = name
         self.inputs = inputs
         self.fn = fn
         self.acc_slot = acc_slot
+        self.defer_slots = defer_slots
 
     def __repr__(self):
         return "<%sBackward>" % self.name
@@ -230,11 +237,11 @@ class Node:
         return [t for t in self.inputs if t is not None]
 
 
-def _record(out, name, inputs, fn, acc_slot=None):
+def _record(out, name, inputs, fn, acc_slot=None, defer_slots=()):
     if _grad["enabled"] and any(t is not None and t.requires_grad for t in inputs):
         out.requires_grad = True
         out.grad_fn = Node(name, [t if (t is not None and t.requires_grad) else None
-                                  for t in inputs], fn, acc_slot)
+                                  for t in inputs], fn, acc_slot, defer_slots)
     return out
 
 
@@ -1908,6 +1915,7 @@ def run_backward(pairs, retain_graph=False, inputs=None):
         wanted = {id(t): t for t in inputs} if inputs is not None else None
         results = {}
         owned = set()  # storages already handed to a leaf in this pass
+        deferred = set()  # ids of leaves whose .grad awaits tjh_flush_deferred
         for t, g in pairs:
             if g.shape != t.shape:
                 if g.numel() == t.numel():
@@ -1931,11 +1939,25 @@ def run_backward(pairs, retain_graph=False, inputs=None):
             if node.fn is None:
                 raise RuntimeError("Trying to backward through the graph a second time; "
                                    "pass retain_graph=True the first time")
+            if deferred and any(t is not None and id(t) in deferred for t in node.inputs):
+                _flush_deferred(deferred)  # this node may read or add to such a .grad
             acc = _pending_for(node, grads, wanted, owned)
-            in_grads = node.fn(g) if acc is None else node.fn(g, acc)
+            defer = _can_defer(node, wanted)
+            kw = {}
+            if acc is not None:
+                kw["pending"] = acc
+            if defer:
+                kw["defer"] = True
+            in_grads = node.fn(g, **kw)
             del g
             for slot, (t, gi) in enumerate(zip(node.inputs, in_grads)):
                 if t is None or gi is None:
+                    continue
+                if defer and slot in node.defer_slots:
+                    # a leaf's first gradient, finished by the next flush
+                    t._grad = gi
+                    owned.add(id(gi._storage))
+                    deferred.add(id(t))
                     continue
                 if acc is not None and slot == node.acc_slot:
                     # gi already holds the pending gradient
@@ -1962,11 +1984,37 @@ def run_backward(pairs, retain_graph=False, inputs=None):
                 # cannot be replayed (torch.js nulls grad_fn, Tensor.ts:3735-3739)
                 node.fn = None
                 node.inputs = [None] * len(node.inputs)
+        if deferred:
+            _flush_deferred(deferred)
         if wanted is not None:
             return [_dense(results.get(id(t))) for t in inputs]
         return None
     finally:
+        if deferred:
+            _flush_deferred(deferred)
         _grad["enabled"] = prev
+
+
+def _can_defer(node, wanted):
+    """Whether the VJP may leave the gradients of node.defer_slots for the
+    library's next flush: each such input is a leaf that has no .grad yet
+    (so the gradient is only stored, never read, until the flush)."""
+    if not node.defer_slots or not _FUSE_ACC or wanted is not None:
+        return False
+    present = False
+    for k in node.defer_slots:
+        t = node.inputs[k]
+        if t is None:
+            continue
+        if t.grad_fn is not None or t._grad is not None or not t.requires_grad:
+            return False
+        present = True
+    return present
+
+
+def _flush_deferred(deferred):
+    L.check(L.lib().tjh_flush_deferred(), "flush_deferred")
+    deferred.clear()
 
 
 def _pending_for(node, grads, wanted, owned):
