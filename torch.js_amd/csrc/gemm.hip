@@ -7,9 +7,12 @@
 //
 // C[b] = alpha * op(A[b]) op(B[b]) + beta * C[b] (+ bias), row-major.
 //
-// Tiling (one workgroup = 256 lanes = 4 wave64 arranged 2 x 2):
+// Tiling (one workgroup = 4 wave64 arranged 2 x 2, or 8 arranged 4 x 2 for
+// 256-row tiles):
 //   block tile BM x BN in {256x128, 128x128, 128x64, 64x64}, K step 16;
-//   each wave owns a (BM/2) x (BN/2) sub-tile of 32x32 MFMA blocks.  Tiles
+//   each wave owns a (BM/2 or 64) x (BN/2) sub-tile of 32x32 MFMA blocks;
+//   the 8-wave 256x128 tile shares each B tile among four row waves (a
+//   quarter fewer global loads and LDS stores per FLOP than 128x128).  Tiles
 //   are double-buffered in LDS: the next K tile is fetched from HBM into
 //   registers while the MFMAs consume the current LDS tile.  A stored
 //   [M][K] (k contiguous) is staged As[m][k] and read as 128-bit fragments
@@ -41,7 +44,6 @@ namespace tjh {
 namespace {
 
 constexpr int BK = 16;
-constexpr int kThreads = 256;
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 // Staging registers are native 4-wide vectors: a struct float4 copied out
@@ -91,14 +93,14 @@ __device__ __forceinline__ float epilogue_act(const GemmArgs& g, int64_t row, in
 // every 4-run is bounds-checked (tiles on the problem's edge); `vec` (the
 // operand is 16-byte aligned with a row stride divisible by 4) lets runs
 // that are wholly in bounds load as one 128-bit access.
-template <bool TRANS, int OUTER, int V, bool EDGE>
+template <bool TRANS, int OUTER, int V, bool EDGE, int T>
 __device__ __forceinline__ void load_tile(const float* __restrict__ P, int64_t ld, int64_t rows,
                                           int64_t cols, int64_t r0, int64_t c0, bool vec,
                                           floatx4 (&reg)[V]) {
   const int t = threadIdx.x;
 #pragma unroll
   for (int i = 0; i < V; ++i) {
-    int f = t + kThreads * i;
+    int f = t + T * i;
     if (!EDGE) {
       if (!TRANS) {
         int o = f >> 2, kq = f & 3;
@@ -144,12 +146,12 @@ __device__ __forceinline__ void load_tile(const float* __restrict__ P, int64_t l
 // contiguous): KC ? S[outer][k] with row length KS, one 128-bit store per
 // float4 : S[k][outer] (transposed, four 32-bit stores per float4).
 constexpr int KS = BK + 4;  // [outer][k] row length: 16-lane groups of 128-bit reads are conflict free
-template <bool TRANS, bool KC, int OUTER, int V, int W>
+template <bool TRANS, bool KC, int OUTER, int V, int W, int T>
 __device__ __forceinline__ void store_tile(float* __restrict__ S, const floatx4 (&reg)[V]) {
   const int t = threadIdx.x;
 #pragma unroll
   for (int i = 0; i < V; ++i) {
-    int f = t + kThreads * i;
+    int f = t + T * i;
     if (!TRANS && KC) {
       int o = f >> 2, kq = f & 3;
       *reinterpret_cast<floatx4*>(S + o * KS + kq * 4) = reg[i];
@@ -191,6 +193,10 @@ __device__ __forceinline__ void read_frags(const float* __restrict__ S, int oute
 // receives the contiguous run [x*n/8, (x+1)*n/8) of the grouped tile order
 // keeps the tiles that share A rows and B columns on one L2.  A bijection on
 // [0, n): ids past the last multiple of 8 keep their number.
+// Lanes per workgroup: 2 x 2 waves, or 4 x 2 waves for 256-row tiles
+// (each wave keeps a 64 x BN/2 sub-tile; B is shared by four waves).
+constexpr int gemm_threads(int bm) { return bm >= 256 ? 512 : 256; }
+
 constexpr int kXcds = 8;
 __device__ __forceinline__ int xcd_tile(int bid, int n) {
   const int full = n - n % kXcds;
@@ -199,12 +205,13 @@ __device__ __forceinline__ int xcd_tile(int bid, int n) {
 }
 
 template <int BM, int BN, bool TA, bool TB, bool EDGE>
-__global__ __launch_bounds__(kThreads, BM * BN > 128 * 128 ? 2 : 4) void k_gemm(GemmArgs g) {
+__global__ __launch_bounds__(gemm_threads(BM), 4) void k_gemm(GemmArgs g) {
   constexpr int LA = BM + 4, LB = BN + 4;       // LDS row lengths
-  constexpr int WM = BM / 2, WN = BN / 2;       // wave tile
+  constexpr int WM = BM / (gemm_threads(BM) / 128), WN = BN / 2;  // wave tile: (T/128) x 2 waves
   constexpr int FM = WM / 32, FN = WN / 32;     // MFMA blocks per wave
-  constexpr int VA = BM * BK / (kThreads * 4);  // float4 loads per lane
-  constexpr int VB = BN * BK / (kThreads * 4);
+  constexpr int T = gemm_threads(BM);
+  constexpr int VA = BM * BK / (T * 4);  // float4 loads per lane
+  constexpr int VB = BN * BK / (T * 4);
   static_assert(FM >= 1 && FN >= 1 && VA >= 1 && VB >= 1, "tile too small");
   // A with k contiguous is staged [m][k] (128-bit stores and reads).  B
   // stays k-major: staging a k-contiguous B as [n][k] measured slower on
@@ -255,14 +262,14 @@ __global__ __launch_bounds__(kThreads, BM * BN > 128 * 128 ? 2 : 4) void k_gemm(
   // bias_mode 3/4: the workgroups of the first column tile also sum the
   // rows of op(A) over their K range (the bias gradient of a weight
   // gradient), compensated, RKPT k values per lane and K step
-  constexpr int RKPT = BK * BM / kThreads;
+  constexpr int RKPT = BK * BM / T;
   const bool row_sums = g.bias_mode >= 3 && tn == 0;
   Kahan rsum;
   floatx4 ra[VA], rb[VB];
-  load_tile<TA, BM, VA, EDGE>(A, g.lda, g.M, kend, m0, kbeg, g.vecA, ra);
-  load_tile<!TB, BN, VB, EDGE>(B, g.ldb, g.N, kend, n0, kbeg, g.vecB, rb);
-  store_tile<TA, AKC, BM, VA, LA>(As[0], ra);
-  store_tile<!TB, BKC, BN, VB, LB>(Bs[0], rb);
+  load_tile<TA, BM, VA, EDGE, T>(A, g.lda, g.M, kend, m0, kbeg, g.vecA, ra);
+  load_tile<!TB, BN, VB, EDGE, T>(B, g.ldb, g.N, kend, n0, kbeg, g.vecB, rb);
+  store_tile<TA, AKC, BM, VA, LA, T>(As[0], ra);
+  store_tile<!TB, BKC, BN, VB, LB, T>(Bs[0], rb);
   __syncthreads();
 
   for (int64_t kt = 0; kt < ktiles; ++kt) {
@@ -270,8 +277,8 @@ __global__ __launch_bounds__(kThreads, BM * BN > 128 * 128 ? 2 : 4) void k_gemm(
     const bool more = kt + 1 < ktiles;
     if (more) {
       const int64_t k0 = kbeg + (kt + 1) * BK;
-      load_tile<TA, BM, VA, EDGE>(A, g.lda, g.M, kend, m0, k0, g.vecA, ra);
-      load_tile<!TB, BN, VB, EDGE>(B, g.ldb, g.N, kend, n0, k0, g.vecB, rb);
+      load_tile<TA, BM, VA, EDGE, T>(A, g.lda, g.M, kend, m0, k0, g.vecA, ra);
+      load_tile<!TB, BN, VB, EDGE, T>(B, g.ldb, g.N, kend, n0, k0, g.vecB, rb);
     }
     if (AKC || BKC) {
 #pragma unroll
@@ -320,8 +327,8 @@ __global__ __launch_bounds__(kThreads, BM * BN > 128 * 128 ? 2 : 4) void k_gemm(
         rsum.add(AKC ? As[cur][rm * KS + rk + i] : As[cur][(rk + i) * LA + rm]);
     }
     if (more) {
-      store_tile<TA, AKC, BM, VA, LA>(As[cur ^ 1], ra);
-      store_tile<!TB, BKC, BN, VB, LB>(Bs[cur ^ 1], rb);
+      store_tile<TA, AKC, BM, VA, LA, T>(As[cur ^ 1], ra);
+      store_tile<!TB, BKC, BN, VB, LB, T>(Bs[cur ^ 1], rb);
     }
     __syncthreads();
   }
@@ -336,7 +343,7 @@ __global__ __launch_bounds__(kThreads, BM * BN > 128 * 128 ? 2 : 4) void k_gemm(
     if (threadIdx.x < BM && row < g.M) {
       float v = 0.f;
 #pragma unroll
-      for (int q = 0; q < kThreads / BM; ++q) v += rpart[threadIdx.x + q * BM];
+      for (int q = 0; q < T / BM; ++q) v += rpart[threadIdx.x + q * BM];
       float* out = const_cast<float*>(g.bias);
       if (g.rsw) g.rsw[(int64_t)blockIdx.y * g.M + row] = v;
       else if (g.bias_mode == 3) out[row] = v;
@@ -440,14 +447,14 @@ constexpr TileCfg kTiles[] = {{256, 128}, {128, 128}, {128, 64}, {64, 64}};
 constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
 
 // Measured relative per-FLOP throughput of each tile with the CUs full, by
-// operand layout (GPT-2 products on MI355X, every tile forced in turn):
-// 128x128 is fastest or within noise of it for every layout once it fills
-// the CUs (with a K split where K is long); 128x64 is 3-5% slower per FLOP
-// and wins only where 128x128 leaves CUs idle.
+// operand layout (GPT-2 products on MI355X, every tile forced in turn): the
+// 8-wave 256x128 tile is 3-8% faster than 128x128 on products that fill the
+// CUs with it (the LM head's three, the 3072-wide ones); 128x64 is 3-5%
+// slower per FLOP and wins only where the larger tiles leave CUs idle.
 float tile_speed(int ti, int ta, int tb) {
-  static const float nt[kNumTiles] = {0.85f, 1.00f, 0.95f, 0.85f};
-  static const float nn[kNumTiles] = {0.85f, 1.00f, 0.97f, 0.85f};
-  static const float tn[kNumTiles] = {0.85f, 1.00f, 0.97f, 0.85f};
+  static const float nt[kNumTiles] = {1.04f, 1.00f, 0.95f, 0.85f};
+  static const float nn[kNumTiles] = {1.03f, 1.00f, 0.97f, 0.85f};
+  static const float tn[kNumTiles] = {1.03f, 1.00f, 0.97f, 0.85f};
   if (!ta && tb) return nt[ti];
   if (!ta && !tb) return nn[ti];
   if (ta && !tb) return tn[ti];
@@ -492,8 +499,15 @@ int64_t choose_splits(int64_t tiles, int64_t K, int cus) {
 
 // Picks tile and split maximising (useful fraction of padded work) x
 // (CU fill) x tile speed.  TJH_GEMM_TILE=BMxBN forces a tile (read on every
-// call, so a test can sweep the tiles in one process).
-Plan choose_plan(int64_t M, int64_t N, int64_t K, int64_t batch, int cus, int ta, int tb) {
+// call, so a test can sweep the tiles in one process).  The 8-wave 256x128
+// tile runs two workgroups per CU, so a heavy epilogue (GELU) stalls half
+// the CU at once, and needing more K splits than 128x128 doubles the
+// split-sum traffic: it is taken only with no activation and either no K
+// split or K >= 16384 (measured in the GPT-2 step: the MLP's GELU GEMMs and
+// the split weight gradients ran 3-10% slower with it, the LM head's three
+// products 2-5% faster).
+Plan choose_plan(int64_t M, int64_t N, int64_t K, int64_t batch, int cus, int ta, int tb,
+                 int act) {
   int forced = -1;
   if (const char* e = getenv("TJH_GEMM_TILE")) {
     for (int i = 0; i < kNumTiles; ++i) {
@@ -511,6 +525,7 @@ Plan choose_plan(int64_t M, int64_t N, int64_t K, int64_t batch, int cus, int ta
     double useful = (double)(M * N) / (double)(tm * t.bm * tn * t.bn);
     int64_t tiles = tm * tn * batch;
     int64_t s = choose_splits(tiles, K, cus);
+    if (t.bm >= 256 && forced < 0 && (act != 0 || (s > 1 && K < 16384))) continue;
     double score = useful * fill_of(tiles * s, cus) * tile_speed(i, ta, tb);
     if (tiles * s < cus) score *= (double)(tiles * s) / cus;
     if (score > best_score + 1e-9) {
@@ -524,13 +539,13 @@ Plan choose_plan(int64_t M, int64_t N, int64_t K, int64_t batch, int cus, int ta
 template <int BM, int BN, bool EDGE>
 void launch_e(const GemmArgs& g, dim3 grid, int ta, int tb) {
   if (!ta && !tb)
-    hipLaunchKernelGGL((k_gemm<BM, BN, false, false, EDGE>), grid, dim3(kThreads), 0, stream(), g);
+    hipLaunchKernelGGL((k_gemm<BM, BN, false, false, EDGE>), grid, dim3(gemm_threads(BM)), 0, stream(), g);
   else if (!ta && tb)
-    hipLaunchKernelGGL((k_gemm<BM, BN, false, true, EDGE>), grid, dim3(kThreads), 0, stream(), g);
+    hipLaunchKernelGGL((k_gemm<BM, BN, false, true, EDGE>), grid, dim3(gemm_threads(BM)), 0, stream(), g);
   else if (ta && !tb)
-    hipLaunchKernelGGL((k_gemm<BM, BN, true, false, EDGE>), grid, dim3(kThreads), 0, stream(), g);
+    hipLaunchKernelGGL((k_gemm<BM, BN, true, false, EDGE>), grid, dim3(gemm_threads(BM)), 0, stream(), g);
   else
-    hipLaunchKernelGGL((k_gemm<BM, BN, true, true, EDGE>), grid, dim3(kThreads), 0, stream(), g);
+    hipLaunchKernelGGL((k_gemm<BM, BN, true, true, EDGE>), grid, dim3(gemm_threads(BM)), 0, stream(), g);
 }
 
 template <int BM, int BN>
@@ -645,7 +660,7 @@ int tjh::gemm(const char* family, int transA, int transB, int64_t M, int64_t N, 
   g.ldaux = ldaux;
   g.act = act;
   KernelScope ks(family);
-  const Plan plan = choose_plan(M, N, K, batch, cus, transA, transB);
+  const Plan plan = choose_plan(M, N, K, batch, cus, transA, transB, act);
   const TileCfg& tc = kTiles[plan.tile];
   if (!(g.vecA && g.vecB)) {
     // unaligned operands: guarded loads everywhere
@@ -671,13 +686,13 @@ int tjh::gemm(const char* family, int transA, int transB, int64_t M, int64_t N, 
   // product (the 81 leftover rows of a 50257-row weight gradient) would
   // otherwise run on a dozen workgroups for the whole K range.
   if (rc == TJH_OK && Nm < N) {  // right strip (all rows)
-    const Plan ps = choose_plan(M, N - Nm, Km, batch, cus, transA, transB);
+    const Plan ps = choose_plan(M, N - Nm, Km, batch, cus, transA, transB, act);
     GemmArgs gs = sub(gk, transA, transB, 0, M, Nm, N - Nm, 0, Km);
     if (gs.bias_mode == 3 && Nm > 0) gs.bias_mode = 0;  // row sums come from column 0's tiles
     rc = run_block(ps.tile, gs, transA, transB, ps.splits, batch, true, cus);
   }
   if (rc == TJH_OK && Mm < M && Nm > 0) {  // bottom strip (interior columns)
-    const Plan ps = choose_plan(M - Mm, Nm, Km, batch, cus, transA, transB);
+    const Plan ps = choose_plan(M - Mm, Nm, Km, batch, cus, transA, transB, act);
     rc = run_block(ps.tile, sub(gk, transA, transB, Mm, M - Mm, 0, Nm, 0, Km), transA, transB,
                    ps.splits, batch, true, cus);
   }
