@@ -500,14 +500,12 @@ int64_t choose_splits(int64_t tiles, int64_t K, int cus) {
 // Picks tile and split maximising (useful fraction of padded work) x
 // (CU fill) x tile speed.  TJH_GEMM_TILE=BMxBN forces a tile (read on every
 // call, so a test can sweep the tiles in one process).  The 8-wave 256x128
-// tile runs two workgroups per CU, so a heavy epilogue (GELU) stalls half
-// the CU at once, and needing more K splits than 128x128 doubles the
-// split-sum traffic: it is taken only with no activation and either no K
-// split or K >= 16384 (measured in the GPT-2 step: the MLP's GELU GEMMs and
-// the split weight gradients ran 3-10% slower with it, the LM head's three
-// products 2-5% faster).
-Plan choose_plan(int64_t M, int64_t N, int64_t K, int64_t batch, int cus, int ta, int tb,
-                 int act) {
+// tile needs more K splits than 128x128 for the same fill, which doubles
+// the split-sum traffic: it is taken only with no K split or K >= 16384
+// (measured in the GPT-2 step: the split weight gradients and 768-wide
+// input gradients ran 3-8% slower with it; the LM head's three products and
+// the MLP's 3072-wide GEMMs 2-5% faster).
+Plan choose_plan(int64_t M, int64_t N, int64_t K, int64_t batch, int cus, int ta, int tb) {
   int forced = -1;
   if (const char* e = getenv("TJH_GEMM_TILE")) {
     for (int i = 0; i < kNumTiles; ++i) {
@@ -525,7 +523,7 @@ Plan choose_plan(int64_t M, int64_t N, int64_t K, int64_t batch, int cus, int ta
     double useful = (double)(M * N) / (double)(tm * t.bm * tn * t.bn);
     int64_t tiles = tm * tn * batch;
     int64_t s = choose_splits(tiles, K, cus);
-    if (t.bm >= 256 && forced < 0 && (act != 0 || (s > 1 && K < 16384))) continue;
+    if (t.bm >= 256 && forced < 0 && (s > 1 && K < 16384)) continue;
     double score = useful * fill_of(tiles * s, cus) * tile_speed(i, ta, tb);
     if (tiles * s < cus) score *= (double)(tiles * s) / cus;
     if (score > best_score + 1e-9) {
@@ -660,7 +658,7 @@ int tjh::gemm(const char* family, int transA, int transB, int64_t M, int64_t N, 
   g.ldaux = ldaux;
   g.act = act;
   KernelScope ks(family);
-  const Plan plan = choose_plan(M, N, K, batch, cus, transA, transB, act);
+  const Plan plan = choose_plan(M, N, K, batch, cus, transA, transB);
   const TileCfg& tc = kTiles[plan.tile];
   if (!(g.vecA && g.vecB)) {
     // unaligned operands: guarded loads everywhere
@@ -686,13 +684,13 @@ int tjh::gemm(const char* family, int transA, int transB, int64_t M, int64_t N, 
   // product (the 81 leftover rows of a 50257-row weight gradient) would
   // otherwise run on a dozen workgroups for the whole K range.
   if (rc == TJH_OK && Nm < N) {  // right strip (all rows)
-    const Plan ps = choose_plan(M, N - Nm, Km, batch, cus, transA, transB, act);
+    const Plan ps = choose_plan(M, N - Nm, Km, batch, cus, transA, transB);
     GemmArgs gs = sub(gk, transA, transB, 0, M, Nm, N - Nm, 0, Km);
     if (gs.bias_mode == 3 && Nm > 0) gs.bias_mode = 0;  // row sums come from column 0's tiles
     rc = run_block(ps.tile, gs, transA, transB, ps.splits, batch, true, cus);
   }
   if (rc == TJH_OK && Mm < M && Nm > 0) {  // bottom strip (interior columns)
-    const Plan ps = choose_plan(M - Mm, Nm, Km, batch, cus, transA, transB, act);
+    const Plan ps = choose_plan(M - Mm, Nm, Km, batch, cus, transA, transB);
     rc = run_block(ps.tile, sub(gk, transA, transB, Mm, M - Mm, 0, Nm, 0, Km), transA, transB,
                    ps.splits, batch, true, cus);
   }
