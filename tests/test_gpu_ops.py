@@ -925,3 +925,43 @@ def _ln_chain_input(x0, gms, bts):
     h = ops.layer_norm(x, gms[0], bts[0])[0]
     h = ops.layer_norm(2.0 * h, gms[1], bts[1])[0]
     return ops.layer_norm(h + x, gms[0], bts[0])[0]
+
+
+@pytest.mark.parametrize("tile", ["256x128", "128x128", "128x64", "64x64"])
+def test_gemm_epilogue_activations_every_tile(torch, monkeypatch, tile):
+    """The fused epilogues on every tile (interior, edge strips, K
+    remainder): act 1 writes the pre-activation and GELU of it, act 2
+    multiplies by GELU' of aux, act 3 adds aux; each equals the plain GEMM
+    followed by the library's elementwise op, bit for bit."""
+    from torchjs_amd import _lib as L
+    monkeypatch.setenv("TJH_GEMM_TILE", tile)
+    r = np.random.default_rng(5)
+    M, N, K = 300, 260, 200
+    A = f32(r.standard_normal((M, K)))
+    B = f32(r.standard_normal((K, N)))
+    bias = f32(r.standard_normal(N))
+    aux0 = f32(r.standard_normal((M, N)))
+    a, b, bt = torch.tensor(A), torch.tensor(B), torch.tensor(bias)
+
+    def gemm(act, aux):
+        c = torch.tensor(np.zeros((M, N), np.float32))
+        if act:
+            L.check(L.lib().tjh_gemm_act(0, 0, M, N, K, 1.0, a.data_ptr(), K, b.data_ptr(), N, 0.0,
+                                         c.data_ptr(), N, bt.data_ptr(), 1, aux.data_ptr(), N, act),
+                    "gemm_act")
+        else:
+            L.check(L.lib().tjh_gemm(0, 0, M, N, K, 1.0, a.data_ptr(), K, 0, b.data_ptr(), N, 0,
+                                     0.0, c.data_ptr(), N, 0, 1, bt.data_ptr(), 1), "gemm")
+        return c
+    plain = gemm(0, None)
+    h = torch.tensor(np.zeros((M, N), np.float32))
+    y1 = gemm(1, h)
+    assert np.array_equal(h.numpy(), plain.numpy())
+    assert np.array_equal(y1.numpy(), torch.F.gelu(plain).numpy())
+    aux = torch.tensor(aux0)
+    y2 = gemm(2, aux)
+    dg = torch.tensor(aux0, requires_grad=True)
+    torch.F.gelu(dg).backward(plain)
+    assert np.array_equal(y2.numpy(), dg.grad.numpy())
+    y3 = gemm(3, aux)
+    assert np.array_equal(y3.numpy(), (aux + plain).numpy())
