@@ -126,10 +126,11 @@ __device__ __forceinline__ floatx16 zero16() {
 // lane of a 256-lane workgroup.  GUARD: rows >= T read as zero.
 template <bool GUARD>
 __device__ __forceinline__ void load_tile(const float* __restrict__ base, int64_t st, int r0, int T,
-                                          floatx4 (&reg)[2]) {
+                                          floatx4 (&reg)[2], int tid = -1) {
+  if (tid < 0) tid = threadIdx.x;
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
-    const int f = threadIdx.x + 256 * i;
+    const int f = tid + 256 * i;
     const int row = f >> 4, c4 = f & 15;
     const int r = r0 + row;
     if (!GUARD || r < T)
@@ -139,10 +140,12 @@ __device__ __forceinline__ void load_tile(const float* __restrict__ base, int64_
   }
 }
 
-__device__ __forceinline__ void store_tile(float* __restrict__ S, const floatx4 (&reg)[2]) {
+__device__ __forceinline__ void store_tile(float* __restrict__ S, const floatx4 (&reg)[2],
+                                           int tid = -1) {
+  if (tid < 0) tid = threadIdx.x;
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
-    const int f = threadIdx.x + 256 * i;
+    const int f = tid + 256 * i;
     const int row = f >> 4, c4 = f & 15;
     *reinterpret_cast<floatx4*>(S + row * LDSW + c4 * 4) = reg[i];
   }
@@ -646,6 +649,106 @@ __global__ __launch_bounds__(256, 2) void k_flash_dq_ds(FlashArgs a) {
   write_rows(Ks[w], dq0, dq1, a.scale, dqb, a.o1s.t, q0, a.Tq, l32, h, lane);
 }
 
+// The same with 8 waves: two groups of four take the even and the odd key
+// tiles of the workgroup's 128 queries, so the longest (causal) query block
+// runs half as many steps; the groups' dQ accumulators are added through
+// LDS in a fixed order (even + odd), so the result is deterministic.
+template <bool GUARD>
+__global__ __launch_bounds__(512, 1) void k_flash_dq_ds8(FlashArgs a) {
+  // group g stages its K tiles in Ks[2g], Ks[2g+1]; the combine and the
+  // dQ row staging reuse all four
+  __shared__ __attribute__((aligned(16))) float Ks[WAVES][TILE * LDSW];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int grp = wv >> 2, w = wv & 3, gt = threadIdx.x & 255;
+  const int l32 = lane & 31, h = lane >> 5;
+  const int64_t nbh = (int64_t)gridDim.x / a.nblk;
+  const int g = balanced_rank(blockIdx.x, gridDim.x, a.cus);
+  const int64_t bh = g % nbh;
+  const int qb = a.nblk - 1 - (int)(g / nbh);
+  const int64_t b = bh / a.H, hh = bh % a.H;
+  const float* K = a.k + b * a.ks.b + hh * a.ks.h;
+  const int q0 = qb * ROWS + w * TILE;
+  const bool wave_in = q0 < a.Tq;
+  const float* dsrow = a.dsblk +
+                       ((int64_t)bh * a.nqt + (wave_in ? q0 / TILE : 0)) * a.nkt * (TILE * TILE) +
+                       l32 * TILE + h * 16;
+  floatx16 dq0 = zero16(), dq1 = zero16();
+
+  int kend = a.Tk;
+  if (a.causal) kend = min(kend, qb * ROWS + ROWS);
+  const int nkb = (kend + TILE - 1) / TILE;
+  int nmine = wave_in ? nkb : 0;
+  if (a.causal && wave_in) nmine = min(nkb, (q0 + TILE - 1) / TILE + 1);
+  // this group's key tiles: kb = grp + 2t; both groups run nst0 steps (the
+  // odd group's last one may be empty) so their barriers pair up
+  const int nst0 = (nkb + 1) / 2;
+  auto kb_of = [&](int t) { return grp + 2 * t; };
+  auto fetch_ds = [&](int t, floatx4 (&d)[4]) {
+    const int kb = kb_of(t);
+    if (t < nst0 && kb < nmine) {
+      const floatx4* src = reinterpret_cast<const floatx4*>(dsrow + (int64_t)kb * (TILE * TILE));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) d[i] = src[i];
+    }
+  };
+  floatx4 d0[4], d1[4], d2[4];
+  fetch_ds(0, d0);
+  fetch_ds(1, d1);
+  floatx4 rk[2];
+  if (kb_of(0) < nkb) load_tile<GUARD>(K, a.ks.t, kb_of(0) * TILE, a.Tk, rk, gt);
+  if (kb_of(0) < nkb) store_tile(Ks[2 * grp], rk, gt);
+  __syncthreads();
+  auto step = [&](int t, const floatx4 (&use)[4], floatx4 (&into)[4]) {
+    const int cur = 2 * grp + (t & 1);
+    const int kb = kb_of(t);
+    const bool more = kb + 2 < nkb;
+    if (more) load_tile<GUARD>(K, a.ks.t, (kb + 2) * TILE, a.Tk, rk, gt);
+    fetch_ds(t + 2, into);
+    if (kb < nmine) {
+      float ct[2][16];
+      lds_cols(Ks[cur], l32, h, ct);
+#pragma unroll
+      for (int s = 0; s < 16; ++s) {  // dQ^T += K^T dS^T
+        const float d = use[s >> 2][s & 3];
+        dq0 = mfma(ct[0][s], d, dq0);
+        dq1 = mfma(ct[1][s], d, dq1);
+      }
+    }
+    if (more) store_tile(Ks[2 * grp + ((t + 1) & 1)], rk, gt);
+    __syncthreads();
+  };
+  for (int t = 0; t < nst0; t += 3) {
+    step(t, d0, d2);
+    if (t + 1 >= nst0) break;
+    step(t + 1, d1, d0);
+    if (t + 2 >= nst0) break;
+    step(t + 2, d2, d1);
+  }
+  // dQ = even-group sum + odd-group sum
+  float* red = &Ks[0][0] + w * (32 * 64);
+  if (grp == 1) {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      red[j * 64 + lane] = dq0[j];
+      red[(16 + j) * 64 + lane] = dq1[j];
+    }
+  }
+  __syncthreads();
+  if (grp == 0) {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      dq0[j] = dq0[j] + red[j * 64 + lane];
+      dq1[j] = dq1[j] + red[(16 + j) * 64 + lane];
+    }
+  }
+  __syncthreads();
+  float* dqb = a.out + b * a.o1s.b + hh * a.o1s.h;
+  if (grp == 0)
+    write_rows(Ks[w], dq0, dq1, a.scale, dqb, a.o1s.t, q0, a.Tq, l32, h, lane);
+  else
+    __syncthreads();  // the one barrier inside write_rows
+}
+
 bool rows_ok(const int64_t* s, const void* p) {
   // D contiguous, 16-byte aligned rows
   return ((uintptr_t)p & 15) == 0 && (s[0] % 4) == 0 && (s[1] % 4) == 0 && (s[2] % 4) == 0;
@@ -739,9 +842,9 @@ int flash_backward(const float* q, const float* k, const float* v, const float* 
   const unsigned gq = (unsigned)(B * H * a.nblk);
   if (a.dsblk) {
     if (Tk % TILE)
-      hipLaunchKernelGGL(k_flash_dq_ds<true>, dim3(gq), dim3(256), 0, stream(), a);
+      hipLaunchKernelGGL(k_flash_dq_ds8<true>, dim3(gq), dim3(512), 0, stream(), a);
     else
-      hipLaunchKernelGGL(k_flash_dq_ds<false>, dim3(gq), dim3(256), 0, stream(), a);
+      hipLaunchKernelGGL(k_flash_dq_ds8<false>, dim3(gq), dim3(512), 0, stream(), a);
   } else if (Tk % TILE) {
     hipLaunchKernelGGL(k_flash_dq<true>, dim3(gq), dim3(256), 0, stream(), a);
   } else {
