@@ -575,84 +575,11 @@ __global__ __launch_bounds__(256, 2) void k_flash_dq(FlashArgs a) {
 // Query-block kernel from stored dS: dQ^T = K^T dS^T for 128 queries per
 // workgroup, reading the 32x32 dS blocks the key-block kernel wrote (each
 // lane's 16 values are one contiguous run) instead of recomputing S and dP.
-// GUARD: Tk is not a multiple of 32.
-template <bool GUARD>
-__global__ __launch_bounds__(256, 2) void k_flash_dq_ds(FlashArgs a) {
-  // two K tiles in flight; all four buffers stage the waves' dQ rows at the end
-  __shared__ __attribute__((aligned(16))) float Ks[WAVES][TILE * LDSW];
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int l32 = lane & 31, h = lane >> 5;
-  const int64_t nbh = (int64_t)gridDim.x / a.nblk;
-  const int g = balanced_rank(blockIdx.x, gridDim.x, a.cus);
-  const int64_t bh = g % nbh;
-  const int qb = a.nblk - 1 - (int)(g / nbh);
-  const int64_t b = bh / a.H, hh = bh % a.H;
-  const float* K = a.k + b * a.ks.b + hh * a.ks.h;
-  const int q0 = qb * ROWS + w * TILE;
-  const bool wave_in = q0 < a.Tq;
-  // this wave's row of dS blocks; lane (l32, h) reads 16 floats per block
-  const float* dsrow = a.dsblk +
-                       ((int64_t)bh * a.nqt + (wave_in ? q0 / TILE : 0)) * a.nkt * (TILE * TILE) +
-                       l32 * TILE + h * 16;
-  floatx16 dq0 = zero16(), dq1 = zero16();
-
-  int kend = a.Tk;
-  if (a.causal) kend = min(kend, qb * ROWS + ROWS);
-  const int nkb = (kend + TILE - 1) / TILE;
-  // dS blocks this wave reads: key tiles kb < nmine (causal: up to the
-  // wave's last query); each is fetched two tiles ahead of its use
-  int nmine = wave_in ? nkb : 0;
-  if (a.causal && wave_in) nmine = min(nkb, (q0 + TILE - 1) / TILE + 1);
-  auto fetch_ds = [&](int kb, floatx4 (&d)[4]) {
-    if (kb < nmine) {
-      const floatx4* src = reinterpret_cast<const floatx4*>(dsrow + (int64_t)kb * (TILE * TILE));
-#pragma unroll
-      for (int i = 0; i < 4; ++i) d[i] = src[i];
-    }
-  };
-  floatx4 d0[4], d1[4], d2[4];
-  fetch_ds(0, d0);
-  fetch_ds(1, d1);
-  floatx4 rk[2];
-  load_tile<GUARD>(K, a.ks.t, 0, a.Tk, rk);
-  store_tile(Ks[0], rk);
-  __syncthreads();
-  // key tile kb uses register set kb % 3 and fetches tile kb + 2 into set
-  // (kb + 2) % 3; the sets are named statically (a register copy of an
-  // in-flight load would wait for it)
-  auto step = [&](int kb, const floatx4 (&use)[4], floatx4 (&into)[4]) {
-    const int cur = kb & 1;
-    const bool more = kb + 1 < nkb;
-    if (more) load_tile<GUARD>(K, a.ks.t, (kb + 1) * TILE, a.Tk, rk);
-    fetch_ds(kb + 2, into);
-    if (kb < nmine) {  // the key-block kernel wrote exactly these blocks
-      float ct[2][16];
-      lds_cols(Ks[cur], l32, h, ct);
-#pragma unroll
-      for (int s = 0; s < 16; ++s) {  // dQ^T += K^T dS^T
-        const float d = use[s >> 2][s & 3];
-        dq0 = mfma(ct[0][s], d, dq0);
-        dq1 = mfma(ct[1][s], d, dq1);
-      }
-    }
-    if (more) store_tile(Ks[cur ^ 1], rk);
-    __syncthreads();
-  };
-  for (int kb = 0; kb < nkb; kb += 3) {
-    step(kb, d0, d2);
-    if (kb + 1 >= nkb) break;
-    step(kb + 1, d1, d0);
-    if (kb + 2 >= nkb) break;
-    step(kb + 2, d2, d1);
-  }
-  float* dqb = a.out + b * a.o1s.b + hh * a.o1s.h;
-  write_rows(Ks[w], dq0, dq1, a.scale, dqb, a.o1s.t, q0, a.Tq, l32, h, lane);
-}
-
-// The same with 8 waves: two groups of four take the even and the odd key
-// tiles of the workgroup's 128 queries, so the longest (causal) query block
-// runs half as many steps; the groups' dQ accumulators are added through
-// LDS in a fixed order (even + odd), so the result is deterministic.
+// 8 waves: two groups of four take the even and the odd key tiles of the
+// 128 queries, so the longest (causal) query block runs half as many steps
+// (measured faster than 4 waves over all tiles); the groups' dQ
+// accumulators are added through LDS in a fixed order (even + odd), so the
+// result is deterministic.  GUARD: Tk is not a multiple of 32.
 template <bool GUARD>
 __global__ __launch_bounds__(512, 1) void k_flash_dq_ds8(FlashArgs a) {
   // group g stages its K tiles in Ks[2g], Ks[2g+1]; the combine and the
