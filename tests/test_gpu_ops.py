@@ -919,6 +919,21 @@ def test_layer_norm_deferred_weight_grads(torch):
     check(hd[5], dbt, rtol=1e-4, atol=1e-3)
 
 
+def test_layer_norm_same_tensor_as_weight_and_bias(torch):
+    """gamma and beta given as one tensor: its gradient is the sum of both
+    (the engine does not defer a tensor that fills two of a node's slots)."""
+    r = np.random.default_rng(23)
+    rows, cols = 40, 768
+    x0 = f32(r.standard_normal((rows, cols)))
+    w0 = f32(1 + 0.1 * r.standard_normal(cols))
+    g = f32(r.standard_normal((rows, cols)))
+    x = torch.tensor(x0, requires_grad=True)
+    w = torch.tensor(w0, requires_grad=True)
+    torch.F.layer_norm(x * 1.0, (cols,), w, w).backward(torch.tensor(g))
+    _, dgm, dbt = ops.layer_norm_backward(g, x0.astype(np.float64), w0)
+    check(w.grad.numpy(), dgm + dbt, rtol=1e-4, atol=1e-3)
+
+
 def _ln_chain_input(x0, gms, bts):
     """The input of the last LayerNorm in test_layer_norm_deferred_weight_grads."""
     x = x0.astype(np.float64)

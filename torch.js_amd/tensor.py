@@ -1909,13 +1909,13 @@ def run_backward(pairs, retain_graph=False, inputs=None):
     gradients instead of accumulating into leaves (autograd.grad)."""
     prev = _grad["enabled"]
     _grad["enabled"] = False
+    deferred = set()  # ids of leaves whose .grad awaits tjh_flush_deferred
     try:
         grads = {}
         roots = []
         wanted = {id(t): t for t in inputs} if inputs is not None else None
         results = {}
         owned = set()  # storages already handed to a leaf in this pass
-        deferred = set()  # ids of leaves whose .grad awaits tjh_flush_deferred
         for t, g in pairs:
             if g.shape != t.shape:
                 if g.numel() == t.numel():
@@ -1997,19 +1997,21 @@ def run_backward(pairs, retain_graph=False, inputs=None):
 
 def _can_defer(node, wanted):
     """Whether the VJP may leave the gradients of node.defer_slots for the
-    library's next flush: each such input is a leaf that has no .grad yet
-    (so the gradient is only stored, never read, until the flush)."""
+    library's next flush: each such input is a distinct leaf that has no
+    .grad yet (so the gradient is only stored, never read, until the
+    flush)."""
     if not node.defer_slots or not _FUSE_ACC or wanted is not None:
         return False
-    present = False
+    seen = set()
     for k in node.defer_slots:
         t = node.inputs[k]
         if t is None:
             continue
-        if t.grad_fn is not None or t._grad is not None or not t.requires_grad:
+        if (t.grad_fn is not None or t._grad is not None or not t.requires_grad or
+                id(t) in seen):
             return False
-        present = True
-    return present
+        seen.add(id(t))
+    return bool(seen)
 
 
 def _flush_deferred(deferred):
