@@ -111,6 +111,17 @@ int tjh_reset_peak(void);
 int tjh_h2d(void* dst, const void* src, size_t bytes);
 int tjh_d2h(void* dst, const void* src, size_t bytes);
 int tjh_d2d(void* dst, const void* src, size_t bytes);
+/* Asynchronous readback, the mapAsync path of readBuffer
+ * (src/backend/webgpu/buffer.ts:150-206, Tensor.toArray, Tensor.ts:253-257):
+ * tjh_d2h_start enqueues the copy of `bytes` from `src` into pinned staging
+ * owned by the library, in stream order at the time of the call (it sees
+ * every earlier call; later calls, including frees and kernels writing
+ * `src`, cannot change what it reads), and returns a ticket.
+ * tjh_d2h_finish waits for that copy, writes the bytes to `dst` and
+ * releases the ticket; it may run on another thread (a Node-API worker)
+ * while the caller keeps launching work. */
+int tjh_d2h_start(const void* src, size_t bytes, uint64_t* ticket);
+int tjh_d2h_finish(uint64_t ticket, void* dst);
 
 /* ------------------------------------------------------------------ */
 /* Timing — device-side counterpart of the profiler's record_function   */
@@ -263,34 +274,49 @@ int tjh_softmax_forward(const float* x, int64_t ldx, float* y, int64_t ldy,
 /* dx from y and dy: softmax: y*(dy - sum(dy*y)); log: dy - exp(y)*sum(dy). */
 int tjh_softmax_backward(const float* dy, const float* y, float* dx,
                          int64_t rows, int64_t cols, int log);
-/* Fused cross entropy over logits [rows, cols] (row stride ld) with int32
- * targets: lse[r] = logsumexp(x[r]); loss_rows[r] = lse - x[r, t_r]
- * (0 for ignore_index).  `out` (1 float) receives the reduction:
- * 0 none (out unused), 1 mean over non-ignored rows, 2 sum. */
+/* Reductions of the losses (apply_reduction, losses.ts:18-32):
+ *   0 none      per-row losses
+ *   1 mean      sum / (number of valid rows, or the sum of their targets'
+ *               class weights when `weight` is given: PyTorch's weighted mean)
+ *   2 sum
+ *   3 batchmean sum / rows
+ * A row is valid when its target is not ignore_index and lies in [0, cols).
+ *
+ * Fused cross entropy over logits [rows, cols] (row stride ld) with int32
+ * targets (F.cross_entropy, losses.ts:129-168): lse[r] = logsumexp(x[r]);
+ * for a valid row with target t, eps = label_smoothing and w the optional
+ * class weights [cols] (w = 1 when NULL),
+ *   loss_rows[r] = (1-eps) w_t (lse - x[r,t]) + (eps/cols) sum_c w_c (lse - x[r,c])
+ * (0 for invalid rows); `out` (1 float) receives the reduction. */
 int tjh_cross_entropy_forward(const float* logits, int64_t ld,
                               const int32_t* targets, int64_t rows,
                               int64_t cols, int32_t ignore_index,
+                              const float* weight, float label_smoothing,
                               float* lse, float* loss_rows, int reduction,
                               float* out);
-/* dlogits[r,c] = (exp(x - lse) - [c == t_r]) * scale_r, where scale_r =
- * grad_out[0]/count (mean), grad_out[0] (sum) or grad_out[r] (none); rows
- * with the ignore target get 0.  dlogits row stride ldd.  accumulate != 0
- * adds into dlogits. */
+/* dlogits[r,c] = s_r [((1-eps) w_t + (eps/cols) W) p_c - (1-eps) w_t [c == t]
+ *                     - (eps/cols) w_c ],
+ * p = exp(x - lse), W = sum_c w_c, s_r = grad_out[r] (none) or grad_out[0]
+ * divided as the reduction divides (mean, batchmean) or not (sum); invalid
+ * rows get 0.  Without weights and smoothing this is (softmax - onehot) * s_r.
+ * dlogits row stride ldd; accumulate != 0 adds into dlogits. */
 int tjh_cross_entropy_backward(const float* logits, int64_t ld,
-                               const int32_t* targets, const float* lse,
+                               const int32_t* targets, const float* weight,
+                               float label_smoothing, const float* lse,
                                const float* grad_out, int64_t rows,
                                int64_t cols, int32_t ignore_index,
                                int reduction, float* dlogits, int64_t ldd,
                                int accumulate);
-/* nll over log-probs [rows, cols]: loss_rows[r] = -logp[r, t_r]. */
+/* nll over log-probs [rows, cols] (F.nll_loss, losses.ts:63-94):
+ * loss_rows[r] = -w_t logp[r, t] for valid rows, else 0. */
 int tjh_nll_loss_forward(const float* logp, int64_t ld,
                          const int32_t* targets, int64_t rows, int64_t cols,
-                         int32_t ignore_index, float* loss_rows,
-                         int reduction, float* out);
-/* dlogp = 0 except dlogp[r, t_r] = -scale_r (same scale rule as above). */
-int tjh_nll_loss_backward(const int32_t* targets, const float* grad_out,
-                          int64_t rows, int64_t cols, int32_t ignore_index,
-                          int reduction, float* dlogp);
+                         int32_t ignore_index, const float* weight,
+                         float* loss_rows, int reduction, float* out);
+/* dlogp = 0 except dlogp[r, t] = -w_t s_r (same scale rule as above). */
+int tjh_nll_loss_backward(const int32_t* targets, const float* weight,
+                          const float* grad_out, int64_t rows, int64_t cols,
+                          int32_t ignore_index, int reduction, float* dlogp);
 
 /* ------------------------------------------------------------------ */
 /* LayerNorm — layernorm.wgsl:14-42, nn.LayerNorm                       */
@@ -348,8 +374,12 @@ int tjh_embedding_backward(const float* dout, const int32_t* ids,
                            int64_t n, int64_t dim, float* dweight,
                            int64_t num, int accumulate);
 /* x viewed [outer, src_len, inner]; out [outer, n_idx, inner] =
- * x[:, idx[j], :]; negative indices wrap once; out-of-range is an error
- * reported by the host check (index_select.wgsl:20-55). */
+ * x[:, idx[j], :] (index_select.wgsl:20-55).  Valid indices are
+ * 0 <= idx[j] < src_len, PyTorch's contract for index_select: the host
+ * layer raises for any other value (the WGSL casts a negative i32 to u32
+ * and reads out of bounds).  The kernel itself never reads outside x: an
+ * out-of-range index yields a zero row here and contributes nothing in
+ * tjh_index_add. */
 int tjh_index_select(const float* x, int64_t outer, int64_t src_len,
                      int64_t inner, const int32_t* idx, int64_t n_idx,
                      float* out);

@@ -186,6 +186,25 @@ def reduce(op, x, dims=None, keepdim=False):
     return f(x, axis=ax, keepdims=keepdim)
 
 
+def reduce_backward(op, g, shape, dims=None, keepdim=False):
+    """Gradient of sum / mean over `dims`: g with the reduced dims restored
+    as size 1, broadcast to `shape`, divided by the reduced count for mean
+    (the contract; torch.js expands without restoring them, D13,
+    Tensor.ts:2416-2424)."""
+    shape = tuple(shape)
+    dims = tuple(range(len(shape))) if dims is None else tuple(d % len(shape) for d in dims)
+    g = np.asarray(g, dtype=F64)
+    if not keepdim:
+        for d in sorted(dims):
+            g = np.expand_dims(g, d)
+    out = np.broadcast_to(g, shape).astype(F64)
+    if op == "mean":
+        out = out / int(np.prod([shape[d] for d in dims]))
+    elif op != "sum":
+        raise ValueError(op)
+    return out
+
+
 def argmax(x, dim=None, is_min=False):
     """First index of the max (min) — Tensor.ts:2568 keeps the first on ties
     (`val > maxVal`)."""
@@ -231,63 +250,96 @@ def _valid(t, cols, ignore_index):
     return (t != ignore_index) & (t >= 0) & (t < cols)
 
 
-def cross_entropy(x, t, reduction="mean", ignore_index=-100):
-    """mean_i -log_softmax(x_i)[t_i] over rows whose target is not ignored
-    (src/nn/losses.ts:130-145 = nll_loss(log_softmax), losses.ts:63-94)."""
-    x = np.asarray(x, dtype=F64)
-    t = np.asarray(t, dtype=np.int64)
-    ok = _valid(t, x.shape[1], ignore_index)
-    lp = log_softmax(x)
-    rows = np.where(ok, -lp[np.arange(len(t)), np.where(ok, t, 0)], 0.0)
+def _denominator(reduction, ok, wt):
+    """Divisor of the reduction (apply_reduction, losses.ts:18-32): mean ->
+    sum of the valid rows' target weights (their count without weights,
+    PyTorch's weighted mean), batchmean -> rows, sum / none -> 1."""
+    if reduction == "mean":
+        return np.where(ok, wt, 0.0).sum()
+    if reduction == "batchmean":
+        return float(len(ok))
+    return 1.0
+
+
+def _reduce_rows(rows, reduction, ok, wt):
     if reduction == "none":
         return rows
-    if reduction == "sum":
-        return rows.sum()
-    return rows.sum() / ok.sum()
+    return rows.sum() / _denominator(reduction, ok, wt)
 
 
-def cross_entropy_backward(x, t, g=1.0, reduction="mean", ignore_index=-100):
-    """(softmax - onehot) * scale per valid row (nll_loss_backward.wgsl +
-    the log_softmax VJP)."""
+def _row_scale(g, reduction, ok, wt):
+    g = np.asarray(g, dtype=F64)
+    if reduction == "none":
+        sc = g.reshape(-1) * np.ones(len(ok))
+    else:
+        sc = np.full(len(ok), float(g) / _denominator(reduction, ok, wt))
+    return np.where(ok, sc, 0.0)
+
+
+def _class_weights(weight, cols):
+    return np.ones(cols) if weight is None else np.asarray(weight, dtype=F64)
+
+
+def cross_entropy(x, t, reduction="mean", ignore_index=-100, weight=None, label_smoothing=0.0):
+    """F.cross_entropy (src/nn/losses.ts:129-168 = nll_loss(log_softmax),
+    losses.ts:63-94) under PyTorch's contract: for a valid row with target
+    t and smoothing eps, loss = (1-eps) w_t (-logp_t) + (eps/C) sum_c w_c
+    (-logp_c); 'mean' divides by the sum of the valid rows' target weights
+    (the row count without weights), 'batchmean' by the row count."""
     x = np.asarray(x, dtype=F64)
     t = np.asarray(t, dtype=np.int64)
-    ok = _valid(t, x.shape[1], ignore_index)
+    C = x.shape[1]
+    ok = _valid(t, C, ignore_index)
+    w = _class_weights(weight, C)
+    ts = np.where(ok, t, 0)
+    wt = w[ts]
+    lp = log_softmax(x)
+    eps = float(label_smoothing)
+    rows = (1.0 - eps) * wt * -lp[np.arange(len(t)), ts] + (eps / C) * (-(lp * w)).sum(axis=1)
+    rows = np.where(ok, rows, 0.0)
+    return _reduce_rows(rows, reduction, ok, wt)
+
+
+def cross_entropy_backward(x, t, g=1.0, reduction="mean", ignore_index=-100, weight=None,
+                           label_smoothing=0.0):
+    """d loss / d x of cross_entropy: row scale s times
+    ((1-eps) w_t (p - onehot_t) + (eps/C) (W p - w)), W = sum_c w_c; the
+    plain case is (softmax - onehot) * s (nll_loss_backward.wgsl + the
+    log_softmax VJP)."""
+    x = np.asarray(x, dtype=F64)
+    t = np.asarray(t, dtype=np.int64)
+    C = x.shape[1]
+    ok = _valid(t, C, ignore_index)
+    w = _class_weights(weight, C)
+    ts = np.where(ok, t, 0)
+    wt = w[ts]
+    eps = float(label_smoothing)
     p = softmax(x)
-    p[np.arange(len(t))[ok], t[ok]] -= 1.0
-    g = np.asarray(g, dtype=F64)
-    if reduction == "mean":
-        sc = np.full(len(t), g / ok.sum())
-    elif reduction == "sum":
-        sc = np.full(len(t), float(g))
-    else:
-        sc = g.reshape(-1)
-    return p * np.where(ok, sc, 0.0)[:, None]
+    oh = np.zeros_like(p)
+    oh[np.arange(len(t)), ts] = 1.0
+    d = (1.0 - eps) * wt[:, None] * (p - oh) + (eps / C) * (w.sum() * p - w[None, :])
+    return d * _row_scale(g, reduction, ok, wt)[:, None]
 
 
-def nll_loss(lp, t, reduction="mean", ignore_index=-100):
+def nll_loss(lp, t, reduction="mean", ignore_index=-100, weight=None):
+    """F.nll_loss (losses.ts:63-94): -w_t logp[i, t] per valid row."""
     lp = np.asarray(lp, dtype=F64)
     t = np.asarray(t, dtype=np.int64)
     ok = _valid(t, lp.shape[1], ignore_index)
-    rows = np.where(ok, -lp[np.arange(len(t)), np.where(ok, t, 0)], 0.0)
-    if reduction == "none":
-        return rows
-    if reduction == "sum":
-        return rows.sum()
-    return rows.sum() / ok.sum()
+    ts = np.where(ok, t, 0)
+    wt = _class_weights(weight, lp.shape[1])[ts]
+    rows = np.where(ok, -wt * lp[np.arange(len(t)), ts], 0.0)
+    return _reduce_rows(rows, reduction, ok, wt)
 
 
-def nll_loss_backward(lp_shape, t, g=1.0, reduction="mean", ignore_index=-100):
+def nll_loss_backward(lp_shape, t, g=1.0, reduction="mean", ignore_index=-100, weight=None):
     t = np.asarray(t, dtype=np.int64)
     ok = _valid(t, lp_shape[1], ignore_index)
+    ts = np.where(ok, t, 0)
+    wt = _class_weights(weight, lp_shape[1])[ts]
     d = np.zeros(lp_shape)
-    g = np.asarray(g, dtype=F64)
-    if reduction == "mean":
-        sc = np.full(len(t), g / ok.sum())
-    elif reduction == "sum":
-        sc = np.full(len(t), float(g))
-    else:
-        sc = g.reshape(-1)
-    d[np.arange(len(t))[ok], t[ok]] = -sc[ok]
+    sc = _row_scale(g, reduction, ok, wt)
+    d[np.arange(len(t))[ok], t[ok]] = -(wt * sc)[ok]
     return d
 
 
@@ -348,17 +400,27 @@ def embedding_backward(g, ids, num):
     return dw
 
 
+def _check_index_range(idx, n):
+    """index_select's contract is PyTorch's (the @pytorch tag of
+    Tensor.ts:1242): every index in [0, n), else IndexError.  torch.js's
+    index_select.wgsl:32-52 casts the i32 index to u32, so a negative one
+    reads out of bounds there; no wrap is defined."""
+    if idx.size and (idx.min() < 0 or idx.max() >= n):
+        raise IndexError("index_select: index out of range for dimension of size %d" % n)
+
+
 def index_select(x, dim, idx):
-    """x.index_select(dim, idx) (Tensor.ts:1242-1287); negative wraps once."""
+    """x.index_select(dim, idx) (Tensor.ts:1242-1287, index_select.wgsl:20-55)."""
     x = np.asarray(x, dtype=F64)
     idx = np.asarray(idx, dtype=np.int64)
-    idx = np.where(idx < 0, idx + x.shape[dim], idx)
+    _check_index_range(idx, x.shape[dim])
     return np.take(x, idx, axis=dim)
 
 
 def index_select_backward(g, shape, dim, idx):
+    """index_add of g into zeros: repeated indices sum."""
     idx = np.asarray(idx, dtype=np.int64)
-    idx = np.where(idx < 0, idx + shape[dim], idx)
+    _check_index_range(idx, shape[dim])
     out = np.zeros(shape)
     gm = np.moveaxis(np.asarray(g, dtype=F64), dim, 0)
     om = np.moveaxis(out, dim, 0)

@@ -39,6 +39,7 @@ def unary_ops(rng):
         "gelu": (lambda v: torch.nn.functional.gelu(v), x), "square": (torch.square, x),
         "reciprocal": (torch.reciprocal, xp), "erf": (torch.erf, x), "abs": (torch.abs, x),
         "sin": (torch.sin, x), "cos": (torch.cos, x), "silu": (torch.nn.functional.silu, x),
+        "softplus": (torch.nn.functional.softplus, x),
     }
     for name, (fn, inp) in fns.items():
         a = t(inp, True)
@@ -72,7 +73,9 @@ def reductions(rng):
     d["max_2"] = t(x).amax(2)
     d["argmax_1"] = t(x).argmax(1).to(torch.int32)
     ta = t(x, True)
-    ta.mean((0, 2)).backward(t(rng.standard_normal(5)))
+    up = rng.standard_normal(5)
+    ta.mean((0, 2)).backward(t(up))
+    d["up_mean_02"] = up
     d["g_mean_02"] = ta.grad
     save("reduce", **d)
 
@@ -259,7 +262,35 @@ def models(rng):
     save("models", **d)
 
 
+def losses_ext(rng):
+    """cross_entropy with class weights and / or label smoothing and
+    nll_loss with class weights, every reduction, one ignored row."""
+    x = rng.standard_normal((7, 9)) * 2
+    tgt = np.array([3, 0, 8, -100, 5, 1, 3])
+    w = rng.uniform(0.2, 2.0, 9)
+    d = {"x": x, "t": tgt, "w": w}
+    for tag, kw in (("w", dict(weight=t(w))), ("ls", dict(label_smoothing=0.15)),
+                    ("wls", dict(weight=t(w), label_smoothing=0.3))):
+        for red in ("mean", "sum", "none"):
+            a = t(x, True)
+            loss = torch.nn.functional.cross_entropy(a, torch.tensor(tgt), reduction=red, **kw)
+            gl = t(rng.standard_normal(7)) if red == "none" else t(0.8)
+            loss.backward(gl)
+            k = "ce_%s_%s" % (tag, red)
+            d[k], d[k + "_g"], d[k + "_dx"] = loss, gl, a.grad
+    lp = torch.log_softmax(t(x), -1).detach()
+    for red in ("mean", "sum", "none"):
+        a = lp.clone().requires_grad_(True)
+        loss = torch.nn.functional.nll_loss(a, torch.tensor(tgt), weight=t(w), reduction=red)
+        gl = t(rng.standard_normal(7)) if red == "none" else t(1.3)
+        loss.backward(gl)
+        k = "nll_w_" + red
+        d["lp"], d[k], d[k + "_g"], d[k + "_dx"] = lp, loss, gl, a.grad
+    save("losses_ext", **d)
+
+
 def main():
+    losses_ext(np.random.default_rng(20261202))
     rng = np.random.default_rng(20261201)
     unary_ops(rng)
     binary_ops(rng)

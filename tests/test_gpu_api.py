@@ -1,0 +1,309 @@
+"""The operator surface above the kernels on the MI355X: torch.autograd's
+grad / vjp / jvp / Function (the literal tests of torch.js's
+tests/compatibility/autograd/autograd.test.ts), cat / stack / expand and
+their gradients, cross_entropy with class weights and label smoothing,
+and nn.init.  Values are checked against the oracle or the reference's
+literal expectations."""
+import math
+
+import numpy as np
+import pytest
+
+from oracle import ops, rng
+
+pytestmark = pytest.mark.gpu
+
+RED = dict(rtol=1e-4, atol=1e-5)
+EW = dict(rtol=1e-5, atol=1e-6)
+
+
+def f32(a):
+    return np.asarray(a, dtype=np.float32)
+
+
+def check(got, want, **tol):
+    np.testing.assert_allclose(np.asarray(got, dtype=np.float64), np.asarray(want, dtype=np.float64),
+                               **tol)
+
+
+# ------------------------------------------------------------ torch.autograd
+# autograd.test.ts:11-56 (grad), :59-105 (vjp), :107-150 (jvp), :153-228
+# (Function); toBeCloseTo(v, 4) is |got - v| < 5e-5.
+
+def close4(got, want):
+    assert np.all(np.abs(np.asarray(got, dtype=np.float64) - np.asarray(want)) < 5e-5), (got, want)
+
+
+def test_autograd_grad_literals(torch):
+    x = torch.tensor([2.0, 3.0], requires_grad=True)
+    (g,) = torch.autograd.grad(x.pow(2).sum(), x)
+    close4(g.toArray(), [4.0, 6.0])                       # :12-20
+    x = torch.tensor([2.0, 3.0], requires_grad=True)
+    (g,) = torch.autograd.grad(x.pow(2), x, torch.tensor([1.0, 2.0]))
+    close4(g.toArray(), [4.0, 12.0])                      # :22-31
+    x = torch.tensor([1.0, 2.0], requires_grad=True)
+    w = torch.tensor([3.0, 4.0], requires_grad=True)
+    gx, gw = torch.autograd.grad(x.mul(w).sum(), [x, w])
+    close4(gx.toArray(), [3.0, 4.0])                      # :33-45
+    close4(gw.toArray(), [1.0, 2.0])
+    # grad leaves .grad untouched
+    assert x.grad is None and w.grad is None
+    # second order needs create_graph, which the hip path does not build
+    # (autograd.test.ts:47-55): a clear error, not a wrong number
+    x = torch.tensor([2.0], requires_grad=True)
+    with pytest.raises(NotImplementedError):
+        torch.autograd.grad(x.pow(3), x, torch.ones_like(x), True, True)
+
+
+def test_autograd_vjp_literals(torch):
+    out, v = torch.autograd.vjp(lambda t: t.pow(2), torch.tensor([1.0, 2.0], requires_grad=True),
+                                torch.tensor([1.0, 1.0]))
+    close4(out.toArray(), [1.0, 4.0])                     # :60-75
+    close4(v.toArray(), [2.0, 4.0])
+
+    def f(t):  # [x0 + x1, x1 + x2]
+        return torch.cat([t[0:2].sum(-1, True), t[1:3].sum(-1, True)])
+    _, v = torch.autograd.vjp(f, torch.tensor([1.0, 2.0, 3.0], requires_grad=True),
+                              torch.tensor([1.0, 1.0]))
+    close4(v.toArray(), [1.0, 2.0, 1.0])                  # :77-91
+    _, v = torch.autograd.vjp(lambda t: t.pow(3), torch.tensor([2.0], requires_grad=True),
+                              torch.tensor([1.0]), True)
+    close4(v.toArray(), [12.0])                           # :93-105
+
+
+def test_autograd_jvp_literals(torch):
+    out, j = torch.autograd.jvp(lambda t: t.pow(2), torch.tensor([1.0, 2.0], requires_grad=True),
+                                torch.tensor([3.0, 4.0]))
+    close4(out.toArray(), [1.0, 4.0])                     # :108-122
+    close4(j.toArray(), [6.0, 16.0])
+    _, j = torch.autograd.jvp(lambda t: t.sum(-1, True), torch.tensor([1.0, 2.0, 3.0]),
+                              torch.tensor([1.0, 1.0, 1.0]))
+    close4(j.toArray(), [3.0])                            # :124-135
+    _, j = torch.autograd.jvp(lambda t: t.pow(2).sum(-1, True), torch.tensor([2.0, 3.0]),
+                              torch.tensor([1.0, 0.0]))
+    close4(j.toArray(), [4.0])                            # :137-149
+
+
+def test_autograd_function_literals(torch):
+    class DoubleFn(torch.autograd.Function):
+        @staticmethod
+        def forward(ctx, x):
+            ctx.save_for_backward(x)
+            return x.mul(2)
+
+        @staticmethod
+        def backward(ctx, g):
+            return g.mul(2)
+
+    x = torch.tensor([1.0, 2.0, 3.0], requires_grad=True)
+    DoubleFn.apply(x).sum().backward()
+    close4(x.grad.toArray(), [2.0, 2.0, 2.0])             # :153-175
+
+    class ReLUFn(torch.autograd.Function):
+        @staticmethod
+        def forward(ctx, x):
+            ctx.save_for_backward(x)
+            return x.clamp_min(0)
+
+        @staticmethod
+        def backward(ctx, g):
+            (x,) = ctx.saved_tensors
+            return g.mul(x.gt(0))
+
+    x = torch.tensor([-1.0, 0.0, 2.0, 5.0], requires_grad=True)
+    y = ReLUFn.apply(x)
+    close4(y.toArray(), [0.0, 0.0, 2.0, 5.0])
+    y.sum().backward()
+    close4(x.grad.toArray(), [0.0, 0.0, 1.0, 1.0])        # :177-200
+
+    class MulAddFn(torch.autograd.Function):
+        @staticmethod
+        def forward(ctx, x, y):
+            ctx.save_for_backward(x, y)
+            return x.mul(y).add(x)
+
+        @staticmethod
+        def backward(ctx, g):
+            x, y = ctx.saved_tensors
+            return [g.mul(y.add(1)), g.mul(x)]
+
+    x = torch.tensor([2.0, 3.0], requires_grad=True)
+    y = torch.tensor([4.0, 5.0], requires_grad=True)
+    MulAddFn.apply(x, y).sum().backward()
+    close4(x.grad.toArray(), [5.0, 6.0])                  # :202-228
+    close4(y.grad.toArray(), [2.0, 3.0])
+
+
+def test_clamp_gradient_includes_bounds(torch):
+    x = torch.tensor([-2.0, -1.0, 0.0, 0.5, 1.0, 3.0], requires_grad=True)
+    y = x.clamp(-1.0, 1.0)
+    assert y.toArray() == [-1.0, -1.0, 0.0, 0.5, 1.0, 1.0]
+    y.sum().backward()
+    assert x.grad.toArray() == [0.0, 1.0, 1.0, 1.0, 1.0, 0.0]
+
+
+# ------------------------------------------------------------ cat / stack / expand
+
+
+@pytest.mark.parametrize("dim", [0, 1, 2, -1])
+def test_cat_forward_backward(torch, dim):
+    """cat (Tensor.ts:152-235): values and the split gradient, ragged sizes
+    along `dim`, one input a transposed view."""
+    r = np.random.default_rng(40 + dim)
+    shapes = []
+    for k in (3, 1, 5):
+        s = [4, 6, 7]
+        s[dim] = k
+        shapes.append(tuple(s))
+    arrs = [f32(r.standard_normal(s)) for s in shapes]
+    ts = [torch.tensor(a, requires_grad=True) for a in arrs]
+    # the middle input enters as a non-contiguous view of its transpose
+    tt = torch.tensor(np.ascontiguousarray(np.swapaxes(arrs[1], 0, 2)), requires_grad=True)
+    mid = tt.transpose(0, 2)
+    out = torch.cat([ts[0], mid, ts[2]], dim)
+    want = np.concatenate(arrs, axis=dim)
+    assert np.array_equal(out.numpy(), want)
+    g = f32(r.standard_normal(want.shape))
+    out.backward(torch.tensor(g))
+    pieces = np.split(g, np.cumsum([s[dim] for s in shapes])[:-1], axis=dim)
+    assert np.array_equal(ts[0].grad.numpy(), pieces[0])
+    assert np.array_equal(tt.grad.numpy(), np.swapaxes(pieces[1], 0, 2))
+    assert np.array_equal(ts[2].grad.numpy(), pieces[2])
+
+
+@pytest.mark.parametrize("dim", [0, 1, 2])
+def test_stack_forward_backward(torch, dim):
+    """stack (src/ops/creation.ts:416-437): a new axis, gradients unstacked."""
+    r = np.random.default_rng(50 + dim)
+    arrs = [f32(r.standard_normal((5, 3))) for _ in range(4)]
+    ts = [torch.tensor(a, requires_grad=True) for a in arrs]
+    out = torch.stack(ts, dim)
+    want = np.stack(arrs, axis=dim)
+    assert np.array_equal(out.numpy(), want)
+    g = f32(r.standard_normal(want.shape))
+    out.backward(torch.tensor(g))
+    for i, t in enumerate(ts):
+        assert np.array_equal(t.grad.numpy(), np.take(g, i, axis=dim))
+
+
+def test_cat_int32_and_empty_piece(torch):
+    a = torch.tensor(np.array([[1, 2]], dtype=np.int32))
+    b = torch.tensor(np.zeros((0, 2), dtype=np.int32))
+    c = torch.tensor(np.array([[3, 4], [5, 6]], dtype=np.int32))
+    out = torch.cat([a, b, c], 0)
+    assert out.dtype == "int32" and out.numpy().tolist() == [[1, 2], [3, 4], [5, 6]]
+
+
+@pytest.mark.parametrize("src,target", [((4096,), (64, 4096)), ((1, 7, 1), (3, 7, 5)),
+                                        ((6, 1), (2, 6, 9)), ((), (3, 4)), ((5,), (5,))])
+def test_expand_backward_sums_broadcast_dims(torch, src, target):
+    """expand's gradient is the sum over every expanded dim (torch.js
+    records none, D12, Tensor.ts:1541-1601)."""
+    r = np.random.default_rng(len(src) * 10 + len(target))
+    x = f32(r.standard_normal(src))
+    g = f32(r.standard_normal(target))
+    t = torch.tensor(x, requires_grad=True)
+    e = t.expand(*target)
+    assert np.array_equal(e.numpy(), np.broadcast_to(x, target))
+    e.backward(torch.tensor(g))
+    check(t.grad.numpy(), ops.sum_to(g, src), **RED)
+    # -1 keeps a size; expand_as; a materialised copy of the view is still a view's grad
+    t2 = torch.tensor(x, requires_grad=True)
+    e2 = t2.expand_as(torch.zeros(*target)).contiguous()
+    e2.backward(torch.tensor(g))
+    check(t2.grad.numpy(), ops.sum_to(g, src), **RED)
+
+
+# ------------------------------------------------------------ losses
+
+
+@pytest.mark.parametrize("rows,cols", [(7, 9), (33, 1000), (6, 50257)])
+@pytest.mark.parametrize("kind", ["w", "ls", "wls"])
+@pytest.mark.parametrize("red", ["mean", "sum", "none", "batchmean"])
+def test_cross_entropy_weights_and_smoothing(torch, rows, cols, kind, red):
+    """F.cross_entropy(input, target, weight, reduction, label_smoothing)
+    (losses.ts:129-168, positional as torch.js orders them) against the
+    oracle, with an ignored row."""
+    r = np.random.default_rng(rows * 7 + cols + len(kind))
+    x = f32(r.standard_normal((rows, cols)) * 2)
+    t = r.integers(0, cols, rows).astype(np.int32)
+    t[2] = -100
+    w = f32(r.uniform(0.2, 2.0, cols)) if "w" in kind else None
+    eps = {"w": 0.0, "ls": 0.1, "wls": 0.25}[kind]
+    xt = torch.tensor(x, requires_grad=True)
+    loss = torch.F.cross_entropy(xt, torch.tensor(t), torch.tensor(w) if w is not None else None,
+                                 red, eps)
+    gl = f32(r.standard_normal(rows)) if red == "none" else np.float32(1.1)
+    loss.backward(torch.tensor(gl))
+    kw = dict(weight=w, label_smoothing=eps)
+    check(loss.numpy(), ops.cross_entropy(x, t, red, **kw), **RED)
+    check(xt.grad.numpy(), ops.cross_entropy_backward(x, t, gl, red, **kw), **RED)
+
+
+def test_cross_entropy_module_and_keyword_ignore_index(torch):
+    r = np.random.default_rng(3)
+    x = f32(r.standard_normal((5, 4)))
+    t = np.array([1, 0, 3, 7, 2], dtype=np.int32)
+    w = f32([1.0, 2.0, 0.5, 1.5])
+    loss = torch.nn.CrossEntropyLoss(torch.tensor(w), "mean", 0.2, ignore_index=7)(
+        torch.tensor(x), torch.tensor(t))
+    check(loss.item(), ops.cross_entropy(x, t, "mean", 7, weight=w, label_smoothing=0.2), **RED)
+    with pytest.raises(ValueError):
+        torch.F.cross_entropy(torch.tensor(x), torch.tensor(t), None, "bogus")
+
+
+@pytest.mark.parametrize("red", ["mean", "sum", "none", "batchmean"])
+def test_nll_loss_weighted(torch, red):
+    r = np.random.default_rng(17)
+    lp = f32(ops.log_softmax(r.standard_normal((9, 6))))
+    t = r.integers(0, 6, 9).astype(np.int32)
+    t[4] = -100
+    w = f32(r.uniform(0.1, 3.0, 6))
+    xt = torch.tensor(lp, requires_grad=True)
+    loss = torch.F.nll_loss(xt, torch.tensor(t), torch.tensor(w), red)
+    gl = f32(r.standard_normal(9)) if red == "none" else np.float32(0.9)
+    loss.backward(torch.tensor(gl))
+    check(loss.numpy(), ops.nll_loss(lp, t, red, weight=w), **RED)
+    check(xt.grad.numpy(), ops.nll_loss_backward(lp.shape, t, gl, red, weight=w), **RED)
+
+
+# ------------------------------------------------------------ nn.init
+
+
+def test_nn_init_seeded_and_bounded(torch):
+    """nn.init (init.ts:10-144) over the seeded device generator: each fill is
+    one rand / randn call of the manual_seed stream (creation.ts:921), so the
+    values are the oracle's stream scaled."""
+    init = torch.nn.init
+    torch.manual_seed(77)
+    seeds = []
+    s = 77
+    for _ in range(4):
+        s = rng.lcg_next(s)
+        seeds.append(s)
+    w = torch.nn.Parameter.create(torch.zeros(64, 48))
+    init.normal_(w, 0.5, 0.02)
+    check(w.numpy(), 0.5 + 0.02 * rng.randn(64 * 48, seeds[0]).reshape(64, 48), rtol=1e-5,
+          atol=1e-6)
+    assert w.is_leaf and w.requires_grad
+    init.uniform_(w, -0.3, 0.7)
+    check(w.numpy(), -0.3 + 1.0 * rng.rand(64 * 48, seeds[1]).reshape(64, 48), **EW)
+    init.kaiming_uniform_(w, a=math.sqrt(5))  # PyTorch's Linear default
+    bound = math.sqrt(2.0 / (1 + 5)) / math.sqrt(48) * math.sqrt(3)
+    u = rng.rand(64 * 48, seeds[2]).reshape(64, 48).astype(np.float64)
+    check(w.numpy(), -bound + 2 * bound * u, **EW)
+    assert np.abs(w.numpy()).max() <= bound
+    conv = torch.zeros(8, 3, 3, 3)
+    init.xavier_normal_(conv)  # fan_in 27, fan_out 72 (PyTorch's rule)
+    std = math.sqrt(2.0 / (27 + 72))
+    check(conv.numpy(), std * rng.randn(8 * 27, seeds[3]).reshape(8, 3, 3, 3), rtol=1e-5,
+          atol=1e-6)
+    e = torch.zeros(3, 5)
+    init.eye_(e)
+    assert np.array_equal(e.numpy(), np.eye(3, 5, dtype=np.float32))
+    init.constant_(e, 2.5)
+    assert (e.numpy() == 2.5).all()
+    assert init.calculate_gain("tanh") == 5.0 / 3.0
+    assert abs(init.calculate_gain("leaky_relu", 0.2) - math.sqrt(2 / 1.04)) < 1e-15
+    with pytest.raises(ValueError):
+        init.xavier_uniform_(torch.zeros(5))

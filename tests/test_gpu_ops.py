@@ -59,14 +59,60 @@ def test_roundtrip_and_allocator(torch):
     assert torch.tensor([-0.0, 1.5]).toArray() == [0.0, 1.5]
 
 
+def test_async_readback_is_stream_ordered(torch):
+    """tjh_d2h_start copies in submission order: a fill launched after it
+    cannot change what tjh_d2h_finish delivers, even when finish runs on
+    another thread while the caller keeps launching."""
+    import threading
+    from torchjs_amd import _lib as L
+    n = 1 << 20
+    src = (np.arange(n) % 977).astype(np.float32)
+    t = torch.tensor(src)
+    tickets = []
+    for _ in range(3):
+        tk = ctypes.c_uint64(0)
+        L.check(L.lib().tjh_d2h_start(t.data_ptr(), n * 4, ctypes.byref(tk)), "d2h_start")
+        tickets.append(tk.value)
+        t.fill_(7.0)  # lands after the copy just enqueued
+    outs = [np.empty(n, np.float32) for _ in tickets]
+    errs = []
+
+    def finish(tk, out):
+        rc = L.lib().tjh_d2h_finish(tk, out.ctypes.data)
+        if rc:
+            errs.append(L.lib().tjh_last_error())
+    th = [threading.Thread(target=finish, args=(tk, o)) for tk, o in zip(tickets, outs)]
+    for x in th:
+        x.start()
+    for x in th:
+        x.join()
+    assert not errs, errs
+    assert np.array_equal(outs[0], src)
+    assert (outs[1] == 7.0).all() and (outs[2] == 7.0).all()
+    # a released ticket is unknown afterwards
+    assert L.lib().tjh_d2h_finish(tickets[0], outs[0].ctypes.data) != 0
+
+
 def test_rng_matches_oracle_stream(torch):
+    """Six successive rand / randn calls after manual_seed(1234): the seeds
+    are creation.ts:921's JS-double LCG states (233191843, 128476320,
+    85706848, ...: the third is where exact integer arithmetic would
+    diverge), each element the xorshift32 state of random.wgsl."""
     torch.manual_seed(1234)
-    u = torch.rand(10007).numpy()
-    n = torch.randn(4099).numpy()
-    s1 = rng.lcg_next(1234)
-    s2 = rng.lcg_next(s1)
-    assert np.array_equal(u, rng.rand(10007, s1))  # integer stream + exact scaling
-    check(n, rng.randn(4099, s2), rtol=1e-5, atol=2e-6)
+    sizes = [10007, 4099, 513, 1 << 16, 7, 2049]
+    normal = [False, True, False, True, False, True]
+    got = [(torch.randn if nm else torch.rand)(n).numpy() for n, nm in zip(sizes, normal)]
+    s = 1234
+    seeds = []
+    for _ in sizes:
+        s = rng.lcg_next(s)
+        seeds.append(s)
+    assert seeds[:4] == [233191843, 128476320, 85706848, 2116141344]
+    for g, n, nm, sd in zip(got, sizes, normal, seeds):
+        if nm:  # Box-Muller in float32 on the device, float64 in the oracle
+            check(g, rng.randn(n, sd), rtol=1e-5, atol=2e-6)
+        else:  # integer stream + exact scaling: bit-exact
+            assert np.array_equal(g, rng.rand(n, sd))
 
 
 # ------------------------------------------------------------------ elementwise
@@ -334,10 +380,17 @@ def test_embedding_clamps_ids(torch):
 def test_index_select_gather_nonzero_one_hot(torch):
     r = np.random.default_rng(12)
     x = f32(r.standard_normal((4, 5, 3)))
-    idx = np.array([4, 0, 4, -1], dtype=np.int32)
+    idx = np.array([4, 0, 4, 2], dtype=np.int32)
     out, g, (gx,) = grad_of(torch, lambda t: t.index_select(1, torch.tensor(idx)), x)
     assert np.array_equal(out, ops.index_select(x, 1, idx).astype(np.float32))
     check(gx, ops.index_select_backward(g, x.shape, 1, idx), **RED)
+    # PyTorch's contract: negative or too large indices raise (no kernel runs)
+    for bad in ([0, -1], [5]):
+        with pytest.raises(IndexError):
+            torch.tensor(x).index_select(1, torch.tensor(np.array(bad, dtype=np.int32)))
+    # advanced indexing still wraps negatives once
+    assert np.array_equal(torch.tensor(x)[torch.tensor(np.array([-1, 0], dtype=np.int32))].numpy(),
+                          x[[-1, 0]])
     gidx = r.integers(-5, 5, (4, 6, 3)).astype(np.int32)
     out, g, (gx,) = grad_of(torch, lambda t: t.gather(1, torch.tensor(gidx)), x)
     assert np.array_equal(out, ops.gather(x, 1, gidx).astype(np.float32))
@@ -932,6 +985,53 @@ def test_layer_norm_same_tensor_as_weight_and_bias(torch):
     torch.F.layer_norm(x * 1.0, (cols,), w, w).backward(torch.tensor(g))
     _, dgm, dbt = ops.layer_norm_backward(g, x0.astype(np.float64), w0)
     check(w.grad.numpy(), dgm + dbt, rtol=1e-4, atol=1e-3)
+
+
+def test_layer_norm_same_tensor_as_input_and_weight(torch):
+    """layer_norm(w, (n,), w, b): the weight gradient is not deferred, since
+    w also receives the input gradient from the same node; w.grad is the
+    sum of both."""
+    r = np.random.default_rng(29)
+    n = 768
+    w0 = f32(1 + 0.1 * r.standard_normal(n))
+    b0 = f32(0.1 * r.standard_normal(n))
+    g = f32(r.standard_normal(n))
+    w = torch.tensor(w0, requires_grad=True)
+    b = torch.tensor(b0, requires_grad=True)
+    torch.F.layer_norm(w, (n,), w, b).backward(torch.tensor(g))
+    dx, dgm, dbt = ops.layer_norm_backward(g[None], w0[None].astype(np.float64), w0)
+    check(w.grad.numpy(), dx[0] + dgm, **RED)
+    check(b.grad.numpy(), dbt, **RED)
+
+
+@pytest.mark.parametrize("emb_first", [True, False])
+def test_embedding_fold_never_writes_a_shared_gradient(torch, emb_first):
+    """A non-leaf table W = 1.5 * W0 feeds both (W + L) * C and
+    embedding(ids, W).  The add's VJP hands one gradient tensor to W and to
+    the leaf L; the embedding's in-place row add may not use it, or L.grad
+    would pick up the embedding rows."""
+    r = np.random.default_rng(31)
+    V, D, n = 37, 16, 50
+    w0 = f32(r.standard_normal((V, D)))
+    l0 = f32(r.standard_normal((V, D)))
+    c0 = f32(r.standard_normal((V, D)))
+    ids = r.integers(0, V, n).astype(np.int32)
+    g1 = f32(r.standard_normal((V, D)))
+    g2 = f32(r.standard_normal((n, D)))
+    W0 = torch.tensor(w0, requires_grad=True)
+    L = torch.tensor(l0, requires_grad=True)
+    W = W0 * 1.5
+    if emb_first:
+        e = torch.F.embedding(torch.tensor(ids), W)
+        a = (W + L) * torch.tensor(c0)
+    else:
+        a = (W + L) * torch.tensor(c0)
+        e = torch.F.embedding(torch.tensor(ids), W)
+    loss = (a * torch.tensor(g1)).sum() + (e * torch.tensor(g2)).sum()
+    loss.backward()
+    gw = c0.astype(np.float64) * g1 + ops.embedding_backward(g2, ids, V)
+    check(L.grad.numpy(), c0.astype(np.float64) * g1, **RED)
+    check(W0.grad.numpy(), 1.5 * gw, **RED)
 
 
 def _ln_chain_input(x0, gms, bts):

@@ -66,7 +66,12 @@ def test_addon_error_before_init():
 @pytest.mark.gpu
 @needs_addon
 def test_addon_end_to_end():
-    r = subprocess.run([NODE, CHECK], capture_output=True, text=True, timeout=120, cwd=ROOT)
+    r = subprocess.run([NODE, "--expose-gc", CHECK], capture_output=True, text=True, timeout=120,
+                       cwd=ROOT)
     assert r.returncode == 0, r.stdout + r.stderr
     out = json.loads(r.stdout.strip().splitlines()[-1])
     assert out["ok"] and out["device"].startswith("gfx950")
+    # a readback enqueued before a fill and a free returns the old bytes
+    assert out["d2h_async_submission_order"] is True
+    # free() followed by GC never returns a block twice
+    assert out["free_then_gc"]["distinct"] and out["free_then_gc"]["doubleFreeThrows"], out

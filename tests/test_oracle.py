@@ -24,7 +24,7 @@ def close(a, b, rtol=RT, atol=AT):
 def test_unary_golden():
     z = golden("unary")
     for op in ["neg", "exp", "log", "sqrt", "rsqrt", "tanh", "sigmoid", "relu", "square",
-               "reciprocal", "abs", "sin", "cos", "silu"]:
+               "reciprocal", "abs", "sin", "cos", "silu", "softplus"]:
         x = z["xp"] if op in ("log", "sqrt", "rsqrt", "reciprocal") else z["x"]
         close(ops.unary(op, x), z["fwd_" + op])
         close(ops.unary_backward(op, z["g"], x), z["bwd_" + op])
@@ -49,6 +49,7 @@ def test_reduce_golden():
     close(ops.reduce("sum", z["x"]), z["sum_all"])
     close(ops.reduce("sum", z["x"], [1]), z["sum_1"])
     close(ops.reduce("mean", z["x"], [0, 2]), z["mean_02"])
+    close(ops.reduce_backward("mean", z["up_mean_02"], z["x"].shape, [0, 2]), z["g_mean_02"])
     close(ops.reduce("max", z["x"], [2]), z["max_2"])
     assert np.array_equal(ops.argmax(z["x"], 1), z["argmax_1"])
 
@@ -67,6 +68,32 @@ def test_softmax_losses_golden():
     close(ops.nll_loss(ly, z["t"]), z["nll"])
     d = ops.nll_loss_backward(ly.shape, z["t"])
     close(ops.log_softmax_backward(d, ly), z["nll_dx"])
+
+
+@pytest.mark.parametrize("tag", ["w", "ls", "wls"])
+@pytest.mark.parametrize("red", ["mean", "sum", "none"])
+def test_weighted_smoothed_losses_golden(tag, red):
+    """Class weights (weighted mean) and label smoothing, PyTorch's contract."""
+    z = golden("losses_ext")
+    kw = {"w": dict(weight=z["w"]), "ls": dict(label_smoothing=0.15),
+          "wls": dict(weight=z["w"], label_smoothing=0.3)}[tag]
+    k = "ce_%s_%s" % (tag, red)
+    close(ops.cross_entropy(z["x"], z["t"], red, **kw), z[k])
+    close(ops.cross_entropy_backward(z["x"], z["t"], z[k + "_g"], red, **kw), z[k + "_dx"])
+    k = "nll_w_" + red
+    close(ops.nll_loss(z["lp"], z["t"], red, weight=z["w"]), z[k])
+    close(ops.nll_loss_backward(z["lp"].shape, z["t"], z[k + "_g"], red, weight=z["w"]),
+          z[k + "_dx"])
+
+
+def test_batchmean_is_sum_over_rows():
+    """apply_reduction's 'batchmean' (losses.ts:27-28): sum / rows, against
+    the pinned 'sum' vectors."""
+    z = golden("losses_ext")
+    rows = len(z["t"])
+    close(ops.cross_entropy(z["x"], z["t"], "batchmean", weight=z["w"]), z["ce_w_sum"] / rows)
+    close(ops.cross_entropy_backward(z["x"], z["t"], 0.8 * rows, "batchmean", weight=z["w"]),
+          z["ce_w_sum_dx"])
 
 
 def test_layer_norm_golden():
@@ -214,6 +241,19 @@ def test_literal_argmax_first_on_ties():
     assert ops.argmax(np.array([[3., 3.], [1., 4.]]), 1).tolist() == [0, 1]
 
 
+def test_index_select_rejects_out_of_range():
+    """index_select follows PyTorch's contract (Tensor.ts:1242's @pytorch
+    tag): indices outside [0, n) raise, negatives included (torch.js's WGSL
+    reinterprets them as u32)."""
+    x = np.arange(6.0).reshape(2, 3)
+    with pytest.raises(IndexError):
+        ops.index_select(x, 1, np.array([0, -1]))
+    with pytest.raises(IndexError):
+        ops.index_select(x, 0, np.array([2]))
+    with pytest.raises(IndexError):
+        ops.index_select_backward(np.ones((2, 1)), x.shape, 1, np.array([3]))
+
+
 def test_literal_gather_negative_wrap():
     """Tensor.ts:2686-2687 wraps negative gather indices."""
     x = np.array([[1., 2., 3.]])
@@ -339,15 +379,36 @@ def test_finite_differences_cnn_mlp():
 # ------------------------------------------------------------------ rng
 
 
-def test_rng_integer_streams():
-    """random.wgsl:9-15 xorshift32 and creation.ts:921 LCG, by hand."""
+def test_lcg_known_answers_js_doubles():
+    """creation.ts:921 evaluated as JavaScript does.  The expected states are
+    those of the IEEE-double definition: globalSeed*1103515245 is rounded to
+    a double (it exceeds 2^53 from the third draw on), 12345 is added in
+    double precision, ToInt32 and & 0x7fffffff keep the low 31 bits.  From
+    manual_seed(1234) that gives 233191843, 128476320, 85706848,
+    2116141344; exact integer arithmetic would give 85706841 third."""
+    s, seen = 1234, []
+    for _ in range(4):
+        s = rng.lcg_next(s)
+        seen.append(s)
+    assert seen == [233191843, 128476320, 85706848, 2116141344]
+    assert (128476320 * 1103515245 + 12345) & 0x7FFFFFFF == 85706841  # the integer result
     assert rng.lcg_next(0) == 12345
-    assert rng.lcg_next(1) == (1103515245 + 12345) & 0x7FFFFFFF
-    x = 1
-    x ^= (x << 13) & 0xFFFFFFFF
-    x ^= x >> 17
-    x ^= (x << 5) & 0xFFFFFFFF
-    assert int(rng.xorshift32(1)) == x
+    # the generator's seed stream follows the same steps
+    g = rng.Generator(1234)
+    assert [g._next() for _ in range(4)] == seen
+
+
+def test_xorshift32_published_known_answer():
+    """Marsaglia, "Xorshift RNGs" (J. Stat. Softw. 8(14), 2003): the (13,17,5)
+    generator from y = 2463534242 returns 723471715 first; random.wgsl:9-15
+    uses the same shifts."""
+    assert int(rng.xorshift32(2463534242)) == 723471715
+    # shifts, not rotations: the top bits fall off (x=2^31 -> 2^31 ^ 2^14 ^ ...)
+    assert int(rng.xorshift32(0)) == 0
+
+
+def test_rng_integer_streams():
+    """Per-element states and the float maps of random.wgsl:17-46."""
     u = rng.rand(1000, 42)
     assert u.min() >= 0 and u.max() < 1 and abs(u.mean() - 0.5) < 0.05
     n = rng.randn(20000, 7)

@@ -70,6 +70,8 @@ SIGNATURES = {
     "tjh_h2d": [c_vp, c_vp, c_sz],
     "tjh_d2h": [c_vp, c_vp, c_sz],
     "tjh_d2d": [c_vp, c_vp, c_sz],
+    "tjh_d2h_start": [c_vp, ctypes.c_size_t, ctypes.POINTER(ctypes.c_uint64)],
+    "tjh_d2h_finish": [ctypes.c_uint64, c_vp],
     "tjh_kprof_enable": [c_int],
     "tjh_kprof_filter": [ctypes.c_char_p],
     "tjh_kprof_reset": [],
@@ -97,12 +99,13 @@ SIGNATURES = {
     "tjh_argmax": [c_vp, c_i64, c_i64, c_i64, c_int, c_vp],
     "tjh_softmax_forward": [c_vp, c_i64, c_vp, c_i64, c_i64, c_i64, c_int],
     "tjh_softmax_backward": [c_vp, c_vp, c_vp, c_i64, c_i64, c_int],
-    "tjh_cross_entropy_forward": [c_vp, c_i64, c_vp, c_i64, c_i64, ctypes.c_int32, c_vp, c_vp,
-                                  c_int, c_vp],
-    "tjh_cross_entropy_backward": [c_vp, c_i64, c_vp, c_vp, c_vp, c_i64, c_i64, ctypes.c_int32,
-                                   c_int, c_vp, c_i64, c_int],
-    "tjh_nll_loss_forward": [c_vp, c_i64, c_vp, c_i64, c_i64, ctypes.c_int32, c_vp, c_int, c_vp],
-    "tjh_nll_loss_backward": [c_vp, c_vp, c_i64, c_i64, ctypes.c_int32, c_int, c_vp],
+    "tjh_cross_entropy_forward": [c_vp, c_i64, c_vp, c_i64, c_i64, ctypes.c_int32, c_vp, c_f32,
+                                  c_vp, c_vp, c_int, c_vp],
+    "tjh_cross_entropy_backward": [c_vp, c_i64, c_vp, c_vp, c_f32, c_vp, c_vp, c_i64, c_i64,
+                                   ctypes.c_int32, c_int, c_vp, c_i64, c_int],
+    "tjh_nll_loss_forward": [c_vp, c_i64, c_vp, c_i64, c_i64, ctypes.c_int32, c_vp, c_vp, c_int,
+                             c_vp],
+    "tjh_nll_loss_backward": [c_vp, c_vp, c_vp, c_i64, c_i64, ctypes.c_int32, c_int, c_vp],
     "tjh_layer_norm_forward": [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_f32],
     "tjh_layer_norm_backward": [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64,
                                 c_int],

@@ -42,14 +42,46 @@ def backward(tensors, grad_tensors=None, retain_graph=False):
     run_backward(_pairs(tensors, grad_tensors), retain_graph=retain_graph)
 
 
-def vjp(func, inputs, v=None):
-    """autograd.functional.vjp (src/autograd.ts:74-105): (func(inputs), v^T J)."""
+def vjp(func, inputs, v=None, create_graph=False):
+    """autograd.functional.vjp (src/autograd.ts:74-86): (func(inputs), v^T J).
+    The product is computed the same with create_graph; it is returned
+    without a graph of its own (double backward is not on the hip path)."""
     single = isinstance(inputs, Tensor)
     ins = [inputs] if single else list(inputs)
     ins = [i.detach().requires_grad_(True) for i in ins]
     out = func(*ins)
     g = grad(out, ins, grad_outputs=v, allow_unused=True)
     return out.detach(), (g[0] if single else g)
+
+
+def jvp(func, inputs, v, create_graph=False):
+    """autograd.functional.jvp (src/autograd.ts:88-137): (func(x), J v) for
+    one input tensor, by reverse mode as torch.js computes it: element i of
+    J v is <d out_i / dx, v>, one retained backward pass per output element
+    (a scalar output takes one).  The dot products and the result stay on
+    the device (torch.js reads each one back)."""
+    from .tensor import _k_reduce, _k_binary, _view_raw, cat, reshape_raw, zeros
+    if not isinstance(inputs, Tensor):
+        raise TypeError("jvp: one input tensor is supported")
+    x = inputs.detach().requires_grad_(True)
+    out = func(x)
+    vf = reshape_raw(v.contiguous(), (v.numel(),))
+    n = out.numel()
+    parts = []
+    for i in range(n):
+        e = zeros(out.shape)
+        if n > 1:
+            _view_raw(e, (n,))[i].fill_(1.0)
+        else:
+            e.fill_(1.0)
+        (gi,) = grad(out, x, grad_outputs=e, retain_graph=True, allow_unused=True)
+        if gi is None:
+            parts.append(zeros((1,)))
+            continue
+        prod = _k_binary("mul", reshape_raw(gi.contiguous(), (gi.numel(),)), vf)
+        parts.append(_view_raw(_k_reduce("sum", prod, [0]), (1,)))
+    res = cat(parts, 0) if parts else zeros((0,))
+    return out.detach(), reshape_raw(res, out.shape)
 
 
 class _Ctx:

@@ -195,12 +195,12 @@ __global__ __launch_bounds__(kBlock) void k_index_select(const float* __restrict
     int64_t i = e % inner;
     int64_t j = (e / inner) % n_idx;
     int64_t o = e / (inner * n_idx);
-    int64_t s = wrap_idx(idx[j], src_len);
+    int64_t s = idx[j];  // no wrap: the host rejects indices outside [0, src_len)
     out[e] = (s >= 0 && s < src_len) ? x[(o * src_len + s) * inner + i] : 0.f;
   }
 }
 
-// dx[o, s, i] += sum_{j : wrap(idx[j]) == s} dout[o, j, i]  (j increasing)
+// dx[o, s, i] += sum_{j : idx[j] == s} dout[o, j, i]  (j increasing)
 __global__ __launch_bounds__(kBlock) void k_index_add(float* __restrict__ dx, int64_t outer,
                                                       int64_t src_len, int64_t inner,
                                                       const int32_t* __restrict__ idx,
@@ -214,7 +214,7 @@ __global__ __launch_bounds__(kBlock) void k_index_add(float* __restrict__ dx, in
     int64_t o = e / (inner * src_len);
     float acc = dx[e];
     for (int64_t j = 0; j < n_idx; ++j)
-      if (wrap_idx(idx[j], src_len) == s) acc += dout[(o * n_idx + j) * inner + i];
+      if ((int64_t)idx[j] == s) acc += dout[(o * n_idx + j) * inner + i];
     dx[e] = acc;
   }
 }

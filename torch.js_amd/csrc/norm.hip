@@ -188,9 +188,12 @@ __global__ __launch_bounds__(kBlock) void k_ce_fwd(const float* __restrict__ x, 
   }
 }
 
-// Final reduction of per-row losses: mean over valid rows or sum.  One block.
+// Final reduction of per-row losses.  reduction 1: sum / (sum over valid
+// rows of the target's class weight, 1 without weights), 2: sum,
+// 3 ('batchmean', losses.ts:27-28): sum / rows.  One block.
 __global__ __launch_bounds__(kBlock) void k_loss_reduce(const float* __restrict__ loss_rows,
                                                         const int32_t* __restrict__ t,
+                                                        const float* __restrict__ w,
                                                         int64_t rows, int64_t cols,
                                                         int32_t ignore, int reduction,
                                                         float* __restrict__ out) {
@@ -199,17 +202,19 @@ __global__ __launch_bounds__(kBlock) void k_loss_reduce(const float* __restrict_
   for (int64_t i = threadIdx.x; i < rows; i += kBlock) {
     s += loss_rows[i];
     int32_t tr = t[i];
-    c += (tr == ignore || tr < 0 || tr >= cols) ? 0.f : 1.f;
+    c += (tr == ignore || tr < 0 || tr >= cols) ? 0.f : (w ? w[tr] : 1.f);
   }
   s = block_sum(s, sm);
   c = block_sum(c, sm);
-  if (threadIdx.x == 0) out[0] = reduction == 1 ? s / c : s;
+  if (threadIdx.x == 0) out[0] = reduction == 1 ? s / c : reduction == 3 ? s / (float)rows : s;
 }
 
+// Gradient scale of row r: grad_out[r] (none), grad_out[0] / denominator
+// (mean, batchmean: the denominator k_count_valid wrote), grad_out[0] (sum).
 __device__ __forceinline__ float ce_scale(const float* __restrict__ gout, int reduction,
                                           int64_t r, float inv_count) {
   if (reduction == 0) return gout[r];
-  if (reduction == 1) return gout[0] * inv_count;
+  if (reduction == 1 || reduction == 3) return gout[0] * inv_count;
   return gout[0];
 }
 
@@ -338,31 +343,121 @@ __global__ __launch_bounds__(kBlock) void k_ce_bwd_flat(
   }
 }
 
-// count of valid targets (for mean) into one float.
+// Denominator of the mean reductions into one float: the number of valid
+// targets, or the sum of their class weights (reduction 1), or the row
+// count ('batchmean', reduction 3).  When `wsum` is given, also the sum of
+// every class weight (C without weights), which label smoothing needs.
 __global__ __launch_bounds__(kBlock) void k_count_valid(const int32_t* __restrict__ t, int64_t rows,
                                                         int64_t cols, int32_t ignore,
-                                                        float* __restrict__ out) {
+                                                        const float* __restrict__ w, int reduction,
+                                                        float* __restrict__ out,
+                                                        float* __restrict__ wsum) {
   __shared__ float sm[kBlock / 64];
   float c = 0.f;
   for (int64_t i = threadIdx.x; i < rows; i += kBlock) {
     int32_t tr = t[i];
-    c += (tr == ignore || tr < 0 || tr >= cols) ? 0.f : 1.f;
+    c += (tr == ignore || tr < 0 || tr >= cols) ? 0.f : (w ? w[tr] : 1.f);
   }
   c = block_sum(c, sm);
-  if (threadIdx.x == 0) out[0] = c;
+  if (wsum) {
+    float ws = 0.f;
+    for (int64_t i = threadIdx.x; i < cols; i += kBlock) ws += w ? w[i] : 1.f;
+    ws = block_sum(ws, sm);
+    if (threadIdx.x == 0) wsum[0] = ws;
+  }
+  if (threadIdx.x == 0 && out) out[0] = reduction == 3 ? (float)rows : c;
+}
+
+// ---- cross entropy with class weights and / or label smoothing
+// (losses.ts:129-168 under PyTorch's contract, which its @pytorch tag
+// declares).  Row i with a valid target t, W = sum_c w_c (C without weights),
+// eps the smoothing:
+//   loss_i = (1-eps) w_t (lse - x_t) + (eps/C) sum_c w_c (lse - x_c)
+//   dx_ic  = s_i [ ((1-eps) w_t + (eps/C) W) p_c - (1-eps) w_t [c == t]
+//                  - (eps/C) w_c ]
+// with p = softmax(x_i) and s_i the row's gradient scale.  An ignored row
+// has loss 0 and gradient 0.  The plain case (no weights, eps 0) runs on
+// k_ce_fwd / k_ce_bwd(_flat) instead.
+template <bool WAVE>
+__global__ __launch_bounds__(kBlock) void k_ce_fwd_gen(const float* __restrict__ x, int64_t ld,
+                                                       const int32_t* __restrict__ t, int64_t rows,
+                                                       int64_t cols, int32_t ignore,
+                                                       const float* __restrict__ w, float eps,
+                                                       float* __restrict__ lse_out,
+                                                       float* __restrict__ loss_rows) {
+  __shared__ float sm[2 * kBlock / 64];
+  int64_t r = WAVE ? (int64_t)blockIdx.x * (kBlock / 64) + (threadIdx.x >> 6) : blockIdx.x;
+  int lane = WAVE ? (threadIdx.x & 63) : threadIdx.x;
+  int nl = WAVE ? 64 : kBlock;
+  if (r >= rows) return;
+  const float* xr = x + r * ld;
+  MS ms{-INFINITY, 0.f};
+  row_scan(xr, cols, lane, nl, [&](int64_t, float v) { ms = ms_add(ms, v); });
+  ms = WAVE ? wave_ms(ms) : block_ms(ms, sm);
+  const float lse = ms.m + logf(ms.s);
+  // smoothing term: sum_c w_c (lse - x_c), every term >= 0 (no cancellation)
+  float sm_term = 0.f;
+  if (eps != 0.f) {
+    row_scan(xr, cols, lane, nl,
+             [&](int64_t i, float v) { sm_term += (w ? w[i] : 1.f) * (lse - v); });
+    sm_term = WAVE ? wave_sum(sm_term) : block_sum(sm_term, sm);
+  }
+  if (lane == 0) {
+    int32_t tr = t[r];
+    lse_out[r] = lse;
+    float l = 0.f;
+    if (!(tr == ignore || tr < 0 || tr >= cols)) {
+      const float wt = w ? w[tr] : 1.f;
+      l = (1.f - eps) * wt * (lse - xr[tr]);
+      if (eps != 0.f) l += eps / (float)cols * sm_term;
+    }
+    loss_rows[r] = l;
+  }
+}
+
+template <bool WAVE>
+__global__ __launch_bounds__(kBlock) void k_ce_bwd_gen(
+    const float* __restrict__ x, int64_t ld, const int32_t* __restrict__ t,
+    const float* __restrict__ w, float eps, const float* __restrict__ lse,
+    const float* __restrict__ gout, const float* __restrict__ count,
+    const float* __restrict__ wsum, int64_t rows, int64_t cols, int32_t ignore, int reduction,
+    float* __restrict__ d, int64_t ldd, int accumulate) {
+  int64_t r = WAVE ? (int64_t)blockIdx.x * (kBlock / 64) + (threadIdx.x >> 6) : blockIdx.x;
+  int lane = WAVE ? (threadIdx.x & 63) : threadIdx.x;
+  int nl = WAVE ? 64 : kBlock;
+  if (r >= rows) return;
+  const float* xr = x + r * ld;
+  float* dr = d + r * ldd;
+  const int32_t tr = t[r];
+  const bool valid = !(tr == ignore || tr < 0 || tr >= cols);
+  const float sc = valid ? ce_scale(gout, reduction, r, count ? 1.0f / count[0] : 1.0f) : 0.f;
+  const float wt = valid ? (w ? w[tr] : 1.f) : 0.f;
+  const float ec = eps / (float)cols;
+  const float a = ((1.f - eps) * wt + ec * wsum[0]) * sc;  // coefficient of p_c
+  const float b = (1.f - eps) * wt * sc;                   // of [c == t]
+  const float e = ec * sc;                                 // of w_c
+  const float l = lse[r];
+  for (int64_t i = lane; i < cols; i += nl) {
+    const float p = __expf(xr[i] - l);
+    const float v = a * p - (i == tr ? b : 0.f) - e * (w ? w[i] : 1.f);
+    dr[i] = accumulate ? dr[i] + v : v;
+  }
 }
 
 __global__ __launch_bounds__(kBlock) void k_nll_fwd(const float* __restrict__ lp, int64_t ld,
                                                     const int32_t* __restrict__ t, int64_t rows,
                                                     int64_t cols, int32_t ignore,
+                                                    const float* __restrict__ w,
                                                     float* __restrict__ loss_rows) {
   int64_t r = (int64_t)blockIdx.x * kBlock + threadIdx.x;
   if (r >= rows) return;
   int32_t tr = t[r];
-  loss_rows[r] = (tr == ignore || tr < 0 || tr >= cols) ? 0.f : -lp[r * ld + tr];
+  loss_rows[r] = (tr == ignore || tr < 0 || tr >= cols) ? 0.f
+                                                        : -(w ? w[tr] : 1.f) * lp[r * ld + tr];
 }
 
 __global__ __launch_bounds__(kBlock) void k_nll_bwd(const int32_t* __restrict__ t,
+                                                    const float* __restrict__ w,
                                                     const float* __restrict__ gout,
                                                     const float* __restrict__ count,
                                                     int64_t rows, int64_t cols, int32_t ignore,
@@ -373,7 +468,8 @@ __global__ __launch_bounds__(kBlock) void k_nll_bwd(const int32_t* __restrict__ 
   int32_t tr = t[r];
   bool valid = !(tr == ignore || tr < 0 || tr >= cols);
   float v = 0.f;
-  if (valid && c == tr) v = -ce_scale(gout, reduction, r, count ? 1.0f / count[0] : 1.0f);
+  if (valid && c == tr)
+    v = -(w ? w[tr] : 1.f) * ce_scale(gout, reduction, r, count ? 1.0f / count[0] : 1.0f);
   d[i] = v;
 }
 
@@ -747,19 +843,31 @@ int tjh_softmax_backward(const float* dy, const float* y, float* dx, int64_t row
 }
 
 int tjh_cross_entropy_forward(const float* logits, int64_t ld, const int32_t* targets,
-                              int64_t rows, int64_t cols, int32_t ignore_index, float* lse,
+                              int64_t rows, int64_t cols, int32_t ignore_index,
+                              const float* weight, float label_smoothing, float* lse,
                               float* loss_rows, int reduction, float* out) {
   TJH_REQUIRE_INIT();
   TJH_ARG(rows >= 0 && cols > 0 && ld >= cols, "tjh_cross_entropy_forward: bad sizes");
-  TJH_ARG(reduction >= 0 && reduction <= 2, "tjh_cross_entropy_forward: bad reduction");
+  TJH_ARG(reduction >= 0 && reduction <= 3, "tjh_cross_entropy_forward: bad reduction");
   TJH_ARG(reduction == 0 || out, "tjh_cross_entropy_forward: reduction needs `out`");
+  TJH_ARG(label_smoothing >= 0.f && label_smoothing <= 1.f,
+          "tjh_cross_entropy_forward: label_smoothing must lie in [0, 1]");
   if (rows == 0) {
-    if (reduction) return tjh_fill_f32(out, 1, reduction == 1 ? __builtin_nanf("") : 0.f);
+    if (reduction) return tjh_fill_f32(out, 1, reduction == 2 ? 0.f : __builtin_nanf(""));
     return TJH_OK;
   }
+  const bool gen = weight != nullptr || label_smoothing != 0.f;
   {
     KernelScope ks("cross_entropy_fwd");
-    if (cols <= 2048)
+    if (gen && cols <= 2048)
+      hipLaunchKernelGGL(k_ce_fwd_gen<true>, dim3((unsigned)cdiv(rows, 4)), dim3(kBlock), 0,
+                         stream(), logits, ld, targets, rows, cols, ignore_index, weight,
+                         label_smoothing, lse, loss_rows);
+    else if (gen)
+      hipLaunchKernelGGL(k_ce_fwd_gen<false>, dim3((unsigned)rows), dim3(kBlock), 0, stream(),
+                         logits, ld, targets, rows, cols, ignore_index, weight, label_smoothing,
+                         lse, loss_rows);
+    else if (cols <= 2048)
       hipLaunchKernelGGL(k_ce_fwd<true>, dim3((unsigned)cdiv(rows, 4)), dim3(kBlock), 0, stream(),
                          logits, ld, targets, rows, cols, ignore_index, lse, loss_rows);
     else
@@ -770,86 +878,108 @@ int tjh_cross_entropy_forward(const float* logits, int64_t ld, const int32_t* ta
   }
   if (reduction) {
     KernelScope ks("loss_reduce");
-    hipLaunchKernelGGL(k_loss_reduce, dim3(1), dim3(kBlock), 0, stream(), loss_rows, targets, rows,
-                       cols, ignore_index, reduction, out);
+    hipLaunchKernelGGL(k_loss_reduce, dim3(1), dim3(kBlock), 0, stream(), loss_rows, targets,
+                       weight, rows, cols, ignore_index, reduction, out);
     return check_launch("loss_reduce");
   }
   return TJH_OK;
 }
 
 int tjh_cross_entropy_backward(const float* logits, int64_t ld, const int32_t* targets,
-                               const float* lse, const float* grad_out, int64_t rows,
-                               int64_t cols, int32_t ignore_index, int reduction, float* dlogits,
-                               int64_t ldd, int accumulate) {
+                               const float* weight, float label_smoothing, const float* lse,
+                               const float* grad_out, int64_t rows, int64_t cols,
+                               int32_t ignore_index, int reduction, float* dlogits, int64_t ldd,
+                               int accumulate) {
   TJH_REQUIRE_INIT();
   TJH_ARG(rows >= 0 && cols > 0 && ld >= cols && ldd >= cols,
           "tjh_cross_entropy_backward: bad sizes");
-  TJH_ARG(reduction >= 0 && reduction <= 2, "tjh_cross_entropy_backward: bad reduction");
+  TJH_ARG(reduction >= 0 && reduction <= 3, "tjh_cross_entropy_backward: bad reduction");
+  TJH_ARG(label_smoothing >= 0.f && label_smoothing <= 1.f,
+          "tjh_cross_entropy_backward: label_smoothing must lie in [0, 1]");
   if (rows == 0) return TJH_OK;
-  Scratch cnt(reduction == 1 ? sizeof(float) : 0);
-  if (reduction == 1) {
+  const bool gen = weight != nullptr || label_smoothing != 0.f;
+  const bool mean = reduction == 1 || reduction == 3;
+  // [0]: the mean's denominator, [1]: the sum of the class weights
+  Scratch cnt(mean || gen ? 2 * sizeof(float) : 0);
+  if (mean || gen) {
     if (!cnt.ok()) return set_error(TJH_ERR_OOM, "cross_entropy_backward: no scratch");
     KernelScope ks("loss_reduce");
     hipLaunchKernelGGL(k_count_valid, dim3(1), dim3(kBlock), 0, stream(), targets, rows, cols,
-                       ignore_index, cnt.as<float>());
+                       ignore_index, weight, reduction, mean ? cnt.as<float>() : nullptr,
+                       gen ? cnt.as<float>() + 1 : nullptr);
     int rc = check_launch("count_valid");
     if (rc != TJH_OK) return rc;
   }
+  const float* count = mean ? cnt.as<float>() : nullptr;
   KernelScope ks("cross_entropy_bwd");
-  if (cols <= 2048)
+  if (gen && cols <= 2048)
+    hipLaunchKernelGGL(k_ce_bwd_gen<true>, dim3((unsigned)cdiv(rows, 4)), dim3(kBlock), 0,
+                       stream(), logits, ld, targets, weight, label_smoothing, lse, grad_out,
+                       count, cnt.as<float>() + 1, rows, cols, ignore_index, reduction, dlogits,
+                       ldd, accumulate);
+  else if (gen)
+    hipLaunchKernelGGL(k_ce_bwd_gen<false>, dim3((unsigned)rows), dim3(kBlock), 0, stream(),
+                       logits, ld, targets, weight, label_smoothing, lse, grad_out, count,
+                       cnt.as<float>() + 1, rows, cols, ignore_index, reduction, dlogits, ldd,
+                       accumulate);
+  else if (cols <= 2048)
     hipLaunchKernelGGL(k_ce_bwd<true>, dim3((unsigned)cdiv(rows, 4)), dim3(kBlock), 0, stream(),
-                       logits, ld, targets, lse, grad_out, cnt.as<float>(), rows, cols,
-                       ignore_index, reduction, dlogits, ldd, accumulate);
+                       logits, ld, targets, lse, grad_out, count, rows, cols, ignore_index,
+                       reduction, dlogits, ldd, accumulate);
   else if (ld == ldd && ld % 4 == 0 && aligned16(logits) && aligned16(dlogits) &&
            rows * (ld / 4) < (int64_t(1) << 31)) {
     const int64_t total4 = rows * (ld / 4);
     const int64_t grid = cdiv(total4, (int64_t)kBlock * 4) < 16384 ? cdiv(total4, (int64_t)kBlock * 4)
                                                                    : 16384;
     hipLaunchKernelGGL(k_ce_bwd_flat, dim3((unsigned)grid), dim3(kBlock), 0, stream(), logits,
-                       (uint32_t)(ld / 4), (uint32_t)total4, targets, lse, grad_out,
-                       cnt.as<float>(), cols, ignore_index, reduction, dlogits, accumulate);
+                       (uint32_t)(ld / 4), (uint32_t)total4, targets, lse, grad_out, count, cols,
+                       ignore_index, reduction, dlogits, accumulate);
   } else
     hipLaunchKernelGGL(k_ce_bwd<false>, dim3((unsigned)rows), dim3(kBlock), 0, stream(), logits,
-                       ld, targets, lse, grad_out, cnt.as<float>(), rows, cols, ignore_index,
-                       reduction, dlogits, ldd, accumulate);
+                       ld, targets, lse, grad_out, count, rows, cols, ignore_index, reduction,
+                       dlogits, ldd, accumulate);
   return check_launch("cross_entropy_backward");
 }
 
 int tjh_nll_loss_forward(const float* logp, int64_t ld, const int32_t* targets, int64_t rows,
-                         int64_t cols, int32_t ignore_index, float* loss_rows, int reduction,
-                         float* out) {
+                         int64_t cols, int32_t ignore_index, const float* weight,
+                         float* loss_rows, int reduction, float* out) {
   TJH_REQUIRE_INIT();
   TJH_ARG(rows >= 0 && cols > 0 && ld >= cols, "tjh_nll_loss_forward: bad sizes");
-  TJH_ARG(reduction >= 0 && reduction <= 2, "tjh_nll_loss_forward: bad reduction");
+  TJH_ARG(reduction >= 0 && reduction <= 3, "tjh_nll_loss_forward: bad reduction");
+  TJH_ARG(reduction == 0 || out, "tjh_nll_loss_forward: reduction needs `out`");
   if (rows == 0) {
-    if (reduction) return tjh_fill_f32(out, 1, reduction == 1 ? __builtin_nanf("") : 0.f);
+    if (reduction) return tjh_fill_f32(out, 1, reduction == 2 ? 0.f : __builtin_nanf(""));
     return TJH_OK;
   }
   KernelScope ks("nll_loss_fwd");
   hipLaunchKernelGGL(k_nll_fwd, dim3((unsigned)cdiv(rows, kBlock)), dim3(kBlock), 0, stream(),
-                     logp, ld, targets, rows, cols, ignore_index, loss_rows);
+                     logp, ld, targets, rows, cols, ignore_index, weight, loss_rows);
   int rc = check_launch("nll_loss_forward");
   if (rc != TJH_OK || !reduction) return rc;
-  hipLaunchKernelGGL(k_loss_reduce, dim3(1), dim3(kBlock), 0, stream(), loss_rows, targets, rows,
-                     cols, ignore_index, reduction, out);
+  hipLaunchKernelGGL(k_loss_reduce, dim3(1), dim3(kBlock), 0, stream(), loss_rows, targets,
+                     weight, rows, cols, ignore_index, reduction, out);
   return check_launch("loss_reduce");
 }
 
-int tjh_nll_loss_backward(const int32_t* targets, const float* grad_out, int64_t rows,
-                          int64_t cols, int32_t ignore_index, int reduction, float* dlogp) {
+int tjh_nll_loss_backward(const int32_t* targets, const float* weight, const float* grad_out,
+                          int64_t rows, int64_t cols, int32_t ignore_index, int reduction,
+                          float* dlogp) {
   TJH_REQUIRE_INIT();
   TJH_ARG(rows >= 0 && cols > 0, "tjh_nll_loss_backward: bad sizes");
+  TJH_ARG(reduction >= 0 && reduction <= 3, "tjh_nll_loss_backward: bad reduction");
   if (rows == 0) return TJH_OK;
-  Scratch cnt(reduction == 1 ? sizeof(float) : 0);
-  if (reduction == 1) {
+  const bool mean = reduction == 1 || reduction == 3;
+  Scratch cnt(mean ? sizeof(float) : 0);
+  if (mean) {
     if (!cnt.ok()) return set_error(TJH_ERR_OOM, "nll_loss_backward: no scratch");
     hipLaunchKernelGGL(k_count_valid, dim3(1), dim3(kBlock), 0, stream(), targets, rows, cols,
-                       ignore_index, cnt.as<float>());
+                       ignore_index, weight, reduction, cnt.as<float>(), nullptr);
   }
   KernelScope ks("nll_loss_bwd");
   hipLaunchKernelGGL(k_nll_bwd, dim3((unsigned)cdiv(rows * cols, kBlock)), dim3(kBlock), 0,
-                     stream(), targets, grad_out, cnt.as<float>(), rows, cols, ignore_index,
-                     reduction, dlogp);
+                     stream(), targets, weight, grad_out, cnt.as<float>(), rows, cols,
+                     ignore_index, reduction, dlogp);
   return check_launch("nll_loss_backward");
 }
 

@@ -259,6 +259,38 @@ KernelScope::~KernelScope() {
   }
 }
 
+// ---------------------------------------------------------------- readbacks
+//
+// tjh_d2h_start enqueues a device-to-host copy into pinned staging on the
+// library stream at call time (so it sees every earlier call and no later
+// one), records an event and hands out a ticket; tjh_d2h_finish, on any
+// thread, waits for that event and copies the staging out.  Staging
+// blocks are cached (hipHostMalloc is slow) and never returned to HIP.
+
+namespace {
+
+struct Readback {
+  void* staging;
+  size_t cap;
+  size_t bytes;
+  hipEvent_t ev;
+};
+
+struct Readbacks {
+  std::mutex mu;
+  std::multimap<size_t, void*> pinned;  // capacity -> staging block
+  std::unordered_map<uint64_t, Readback> live;
+  std::vector<hipEvent_t> events;
+  uint64_t next = 1;
+};
+
+Readbacks& readbacks() {
+  static Readbacks* r = new Readbacks();
+  return *r;
+}
+
+}  // namespace
+
 }  // namespace tjh
 
 using namespace tjh;
@@ -396,6 +428,74 @@ int tjh_d2h(void* dst, const void* src, size_t bytes) {
   TJH_ARG(dst && src, "tjh_d2h: NULL pointer");
   TJH_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, g_stream));
   TJH_HIP(hipStreamSynchronize(g_stream));
+  return TJH_OK;
+}
+
+int tjh_d2h_start(const void* src, size_t bytes, uint64_t* ticket) {
+  TJH_REQUIRE_INIT();
+  TJH_ARG(ticket, "tjh_d2h_start: ticket is NULL");
+  TJH_ARG(src || bytes == 0, "tjh_d2h_start: NULL source");
+  Readbacks& R = readbacks();
+  std::lock_guard<std::mutex> lk(R.mu);
+  Readback rb{nullptr, 0, bytes, nullptr};
+  if (bytes) {
+    auto it = R.pinned.lower_bound(bytes);
+    if (it != R.pinned.end() && it->first <= 2 * bytes + (size_t(64) << 10)) {
+      rb.cap = it->first;
+      rb.staging = it->second;
+      R.pinned.erase(it);
+    } else {
+      rb.cap = (bytes + 4095) / 4096 * 4096;
+      TJH_HIP(hipHostMalloc(&rb.staging, rb.cap, hipHostMallocDefault));
+    }
+    hipError_t e = hipMemcpyAsync(rb.staging, src, bytes, hipMemcpyDeviceToHost, g_stream);
+    if (e != hipSuccess) {
+      R.pinned.emplace(rb.cap, rb.staging);
+      return hip_fail(e, "tjh_d2h_start: hipMemcpyAsync");
+    }
+  }
+  if (!R.events.empty()) {
+    rb.ev = R.events.back();
+    R.events.pop_back();
+  } else {
+    hipError_t e = hipEventCreateWithFlags(&rb.ev, hipEventDisableTiming);
+    if (e != hipSuccess) {
+      if (rb.staging) R.pinned.emplace(rb.cap, rb.staging);
+      TJH_HIP(hipStreamSynchronize(g_stream));  // the copy may still be reading staging
+      return hip_fail(e, "tjh_d2h_start: hipEventCreate");
+    }
+  }
+  TJH_HIP(hipEventRecord(rb.ev, g_stream));
+  uint64_t t = R.next++;
+  R.live.emplace(t, rb);
+  *ticket = t;
+  return TJH_OK;
+}
+
+int tjh_d2h_finish(uint64_t ticket, void* dst) {
+  Readback rb;
+  {
+    Readbacks& R = readbacks();
+    std::lock_guard<std::mutex> lk(R.mu);
+    auto it = R.live.find(ticket);
+    TJH_ARG(it != R.live.end(), "tjh_d2h_finish: unknown ticket %llu",
+            (unsigned long long)ticket);
+    rb = it->second;
+    R.live.erase(it);
+  }
+  // wait outside the lock: other threads may start readbacks meanwhile
+  hipError_t e = hipEventSynchronize(rb.ev);
+  if (e == hipSuccess && rb.bytes) {
+    if (dst) memcpy(dst, rb.staging, rb.bytes);
+  }
+  {
+    Readbacks& R = readbacks();
+    std::lock_guard<std::mutex> lk(R.mu);
+    if (rb.staging) R.pinned.emplace(rb.cap, rb.staging);
+    R.events.push_back(rb.ev);
+  }
+  if (e != hipSuccess) return hip_fail(e, "tjh_d2h_finish: hipEventSynchronize");
+  TJH_ARG(dst || rb.bytes == 0, "tjh_d2h_finish: NULL destination (the ticket is released)");
   return TJH_OK;
 }
 

@@ -104,7 +104,13 @@ def log_softmax(x, dim=-1):
 
 # ------------------------------------------------------------ losses
 
-_RED = {"none": 0, "mean": 1, "sum": 2}
+_RED = {"none": 0, "mean": 1, "sum": 2, "batchmean": 3}
+
+
+def _reduction_code(reduction):
+    if reduction not in _RED:
+        raise ValueError("%s is not a valid value for reduction" % (reduction,))
+    return _RED[reduction]
 
 
 def _class_last_2d(x, target):
@@ -126,15 +132,39 @@ def _class_last_2d(x, target):
     return x, t
 
 
-def cross_entropy(input, target, weight=None, reduction="mean", ignore_index=-100,
-                  label_smoothing=0.0):
-    """F.cross_entropy (src/nn/losses.ts:130-145) = nll_loss(log_softmax),
-    fused: one pass computes logsumexp and the per-row loss, the backward
-    writes (softmax - onehot) * scale in one pass (torch.js's nll_loss
-    reinterprets int targets as floats, D9)."""
-    if weight is not None or label_smoothing:
-        raise NotImplementedError("cross_entropy: class weights / label smoothing are not on the hip path")
-    red = _RED[reduction]
+def _class_weight(weight, cols):
+    """Class weights as a contiguous float32 [C] tensor (no gradient flows to
+    them, as in PyTorch), or None."""
+    if weight is None:
+        return None
+    if not isinstance(weight, Tensor):
+        from .tensor import tensor as _tensor
+        weight = _tensor(np.asarray(weight, dtype=np.float32))
+    w = weight.detach()
+    w = w.float() if w.dtype != "float32" else w
+    if w.shape != (cols,):
+        raise ValueError("weight should be a 1-D tensor of %d class weights, got shape %s"
+                         % (cols, list(w.shape)))
+    return w.contiguous()
+
+
+def cross_entropy(input, target, weight=None, reduction="mean", label_smoothing=0.0, *,
+                  ignore_index=-100):
+    """F.cross_entropy(input, target, weight, reduction, label_smoothing)
+    (src/nn/losses.ts:129-168; the positional order is torch.js's) =
+    nll_loss(log_softmax) fused: one pass computes logsumexp and the per-row
+    loss, the backward writes the logits' gradient in one pass (torch.js's
+    nll_loss reinterprets int targets as floats, D9).  Class weights,
+    label smoothing and the 'mean' over weights follow PyTorch's contract,
+    which torch.js's @pytorch tag declares: loss_i = (1-eps) w_t (-logp_t)
+    + (eps/C) sum_c w_c (-logp_c), and 'mean' divides by the sum of the
+    valid rows' target weights (torch.js averages over rows).  'batchmean'
+    (losses.ts:27-28) divides the sum by the number of rows.
+    `ignore_index` (PyTorch's; torch.js has none) is keyword-only."""
+    red = _reduction_code(reduction)
+    eps = float(label_smoothing)
+    if not 0.0 <= eps <= 1.0:
+        raise ValueError("label_smoothing must lie in [0, 1], got %r" % (label_smoothing,))
     x, t = _class_last_2d(input, target)
     if x.dtype != "float32":
         x = x.float()
@@ -144,19 +174,23 @@ def cross_entropy(input, target, weight=None, reduction="mean", ignore_index=-10
         xd = _k_contiguous(xd)
         rv = _rows_view(xd)
     rows, cols = x.shape
+    w = _class_weight(weight, cols)
+    wp = w.data_ptr() if w is not None else None
     lse = empty((rows,))
     loss_rows = empty((rows,))
     out = empty(()) if red else loss_rows
     L.check(L.lib().tjh_cross_entropy_forward(rv[0], rv[1], t.data_ptr(), rows, cols,
-                                              int(ignore_index), lse.data_ptr(),
+                                              int(ignore_index), wp, eps, lse.data_ptr(),
                                               loss_rows.data_ptr(), red,
                                               out.data_ptr() if red else None),
             "cross_entropy")
+
     def bwd(g):
         g = g.contiguous()
         d = _empty_padded(rows, cols) if cols % 4 else empty((rows, cols))
         xp, ld = _rows_view(xd)
-        L.check(L.lib().tjh_cross_entropy_backward(xp, ld, t.data_ptr(), lse.data_ptr(),
+        wb = w.data_ptr() if w is not None else None  # keeps w alive with the graph
+        L.check(L.lib().tjh_cross_entropy_backward(xp, ld, t.data_ptr(), wb, eps, lse.data_ptr(),
                                                    g.data_ptr(), rows, cols, int(ignore_index),
                                                    red, d.data_ptr(), d._strides[0], 0),
                 "cross_entropy_backward")
@@ -167,11 +201,11 @@ def cross_entropy(input, target, weight=None, reduction="mean", ignore_index=-10
     return res
 
 
-def nll_loss(input, target, weight=None, reduction="mean", ignore_index=-100):
-    """F.nll_loss (src/nn/losses.ts:63-94, nll_loss(_backward).wgsl)."""
-    if weight is not None:
-        raise NotImplementedError("nll_loss: class weights are not on the hip path")
-    red = _RED[reduction]
+def nll_loss(input, target, weight=None, reduction="mean", *, ignore_index=-100):
+    """F.nll_loss(input, target, weight, reduction) (src/nn/losses.ts:63-94,
+    nll_loss(_backward).wgsl): loss_i = -w_t logp[i, t]; 'mean' divides by
+    the sum of the valid rows' target weights (PyTorch's contract)."""
+    red = _reduction_code(reduction)
     x, t = _class_last_2d(input, target)
     if x.dtype != "float32":
         x = x.float()
@@ -181,16 +215,19 @@ def nll_loss(input, target, weight=None, reduction="mean", ignore_index=-100):
         xd = _k_contiguous(xd)
         rv = _rows_view(xd)
     rows, cols = x.shape
+    w = _class_weight(weight, cols)
+    wp = w.data_ptr() if w is not None else None
     loss_rows = empty((rows,))
     out = empty(()) if red else loss_rows
     L.check(L.lib().tjh_nll_loss_forward(rv[0], rv[1], t.data_ptr(), rows, cols, int(ignore_index),
-                                         loss_rows.data_ptr(), red,
+                                         wp, loss_rows.data_ptr(), red,
                                          out.data_ptr() if red else None), "nll_loss")
 
     def bwd(g):
         g = g.contiguous()
         d = empty((rows, cols))
-        L.check(L.lib().tjh_nll_loss_backward(t.data_ptr(), g.data_ptr(), rows, cols,
+        wb = w.data_ptr() if w is not None else None  # keeps w alive with the graph
+        L.check(L.lib().tjh_nll_loss_backward(t.data_ptr(), wb, g.data_ptr(), rows, cols,
                                               int(ignore_index), red, d.data_ptr()),
                 "nll_loss_backward")
         return [d]

@@ -280,25 +280,30 @@ class ModuleList(Module):
 
 
 class CrossEntropyLoss(Module):
-    """nn.CrossEntropyLoss (src/nn/losses.ts:100-124)."""
+    """nn.CrossEntropyLoss(weight, reduction, label_smoothing)
+    (src/nn/losses.ts:100-124; torch.js's positional order, ignore_index
+    keyword-only)."""
 
-    def __init__(self, weight=None, reduction="mean", ignore_index=-100, label_smoothing=0.0):
+    def __init__(self, weight=None, reduction="mean", label_smoothing=0.0, *, ignore_index=-100):
         super().__init__()
         self.weight, self.reduction = weight, reduction
         self.ignore_index, self.label_smoothing = ignore_index, label_smoothing
 
     def forward(self, input, target):
-        return F.cross_entropy(input, target, self.weight, self.reduction, self.ignore_index,
-                               self.label_smoothing)
+        return F.cross_entropy(input, target, self.weight, self.reduction, self.label_smoothing,
+                               ignore_index=self.ignore_index)
 
 
 class NLLLoss(Module):
-    def __init__(self, weight=None, reduction="mean", ignore_index=-100):
+    """nn.NLLLoss(weight, reduction) (src/nn/losses.ts:38-57)."""
+
+    def __init__(self, weight=None, reduction="mean", *, ignore_index=-100):
         super().__init__()
         self.weight, self.reduction, self.ignore_index = weight, reduction, ignore_index
 
     def forward(self, input, target):
-        return F.nll_loss(input, target, self.weight, self.reduction, self.ignore_index)
+        return F.nll_loss(input, target, self.weight, self.reduction,
+                          ignore_index=self.ignore_index)
 
 
 class MSELoss(Module):
@@ -310,33 +315,123 @@ class MSELoss(Module):
         return F.mse_loss(input, target, self.reduction)
 
 
+def _fans(t):
+    """(fan_in, fan_out) of a weight [out, in, *receptive] (PyTorch's rule;
+    torch.js's getFanOut drops the receptive field, init.ts:219-228)."""
+    if t.ndim < 2:
+        raise ValueError("Fan in and fan out can not be computed for tensor with fewer than "
+                         "2 dimensions")
+    rf = 1
+    for s in t.shape[2:]:
+        rf *= s
+    return t.shape[1] * rf, t.shape[0] * rf
+
+
+def calculate_gain(nonlinearity, param=None):
+    """nn.init.calculate_gain (init.ts:194-207)."""
+    if nonlinearity in ("linear", "conv1d", "conv2d", "conv3d", "conv_transpose1d",
+                        "conv_transpose2d", "conv_transpose3d", "sigmoid"):
+        return 1.0
+    if nonlinearity == "tanh":
+        return 5.0 / 3.0
+    if nonlinearity == "relu":
+        return math.sqrt(2.0)
+    if nonlinearity == "leaky_relu":
+        slope = 0.01 if param is None else float(param)
+        return math.sqrt(2.0 / (1.0 + slope * slope))
+    if nonlinearity == "selu":
+        return 3.0 / 4.0
+    raise ValueError("unsupported nonlinearity %s" % (nonlinearity,))
+
+
 class init:
-    """nn.init (src/nn/init.ts:58-126) over the device RNG."""
+    """nn.init (src/nn/init.ts:10-160) over the device generator: every
+    random fill draws one seeded rand / randn call (the LCG seed stream of
+    manual_seed, creation.ts:921), so initialisation is reproducible
+    (torch.js's uniform_ uses unseeded Math.random, init.ts:69-79).  The
+    fills run under no_grad and keep the tensor's identity (leaf
+    parameters stay leaves)."""
+
+    calculate_gain = staticmethod(calculate_gain)
+    calculateGain = staticmethod(calculate_gain)
+
+    @staticmethod
+    def _assign(t, src):
+        from .tensor import _copy_into, no_grad
+        with no_grad():
+            _copy_into(t, src)
+        return t
+
+    @staticmethod
+    def constant_(t, val):
+        from .tensor import no_grad
+        with no_grad():
+            t.fill_(float(val))
+        return t
 
     @staticmethod
     def zeros_(t):
-        from .tensor import no_grad
-        with no_grad():
-            t.zero_()
-        return t
+        return init.constant_(t, 0.0)
 
     @staticmethod
     def ones_(t):
-        from .tensor import no_grad
-        with no_grad():
-            t.fill_(1.0)
-        return t
+        return init.constant_(t, 1.0)
 
     @staticmethod
-    def constant_(t, v):
-        from .tensor import no_grad
+    def eye_(t):
+        """Identity into a 2-D tensor (init.ts:44-52; PyTorch also takes
+        non-square ones)."""
+        from .tensor import Tensor, no_grad
+        if t.ndim != 2:
+            raise ValueError("eye_ requires a 2-D tensor")
         with no_grad():
-            t.fill_(v)
+            t.zero_()
+            n = min(t.shape)
+            diag = Tensor(t._storage, (n,), (t._strides[0] + t._strides[1],), t._offset,
+                          t._dtype)
+            diag.fill_(1.0)
         return t
 
     @staticmethod
     def normal_(t, mean=0.0, std=1.0):
-        from .tensor import _copy_into, no_grad
+        """mean + std * randn (init.ts:58-63)."""
+        if std < 0:
+            raise ValueError("normal_: std must be non-negative")
+        from .tensor import no_grad
         with no_grad():
-            _copy_into(t, randn(*t.shape).mul(std).add(mean))
-        return t
+            return init._assign(t, randn(*t.shape).mul(float(std)).add(float(mean)))
+
+    @staticmethod
+    def uniform_(t, a=0.0, b=1.0):
+        """a + (b - a) * rand (init.ts:69-79), from the seeded device stream."""
+        from .tensor import no_grad, rand
+        with no_grad():
+            return init._assign(t, rand(*t.shape).mul(float(b) - float(a)).add(float(a)))
+
+    @staticmethod
+    def xavier_uniform_(t, gain=1.0):
+        """U(-a, a), a = gain * sqrt(6 / (fan_in + fan_out)) (init.ts:85-92)."""
+        fi, fo = _fans(t)
+        a = gain * math.sqrt(2.0 / (fi + fo)) * math.sqrt(3.0)
+        return init.uniform_(t, -a, a)
+
+    @staticmethod
+    def xavier_normal_(t, gain=1.0):
+        """N(0, gain^2 * 2 / (fan_in + fan_out)) (init.ts:98-104)."""
+        fi, fo = _fans(t)
+        return init.normal_(t, 0.0, gain * math.sqrt(2.0 / (fi + fo)))
+
+    @staticmethod
+    def kaiming_uniform_(t, a=0.0, mode="fan_in", nonlinearity="leaky_relu"):
+        """U(-b, b), b = gain * sqrt(3 / fan) (init.ts:110-124)."""
+        fi, fo = _fans(t)
+        fan = fi if mode == "fan_in" else fo
+        bound = calculate_gain(nonlinearity, a) / math.sqrt(fan) * math.sqrt(3.0)
+        return init.uniform_(t, -bound, bound)
+
+    @staticmethod
+    def kaiming_normal_(t, a=0.0, mode="fan_in", nonlinearity="leaky_relu"):
+        """N(0, gain^2 / fan) (init.ts:130-144)."""
+        fi, fo = _fans(t)
+        fan = fi if mode == "fan_in" else fo
+        return init.normal_(t, 0.0, calculate_gain(nonlinearity, a) / math.sqrt(fan))

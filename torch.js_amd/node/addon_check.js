@@ -55,10 +55,12 @@ async function main() {
   tg[3] = -100;  // ignore_index
   const dL = upload(logits), dT = upload(tg);
   const dLse = hip.malloc(R * 4), dRows = hip.malloc(R * 4), dLoss = hip.malloc(4);
-  hip.crossEntropyForward(dL.ptr, V, dT.ptr, R, V, -100, dLse.ptr, dRows.ptr, 1, dLoss.ptr);
+  hip.crossEntropyForward(dL.ptr, V, dT.ptr, R, V, -100, null, 0, dLse.ptr, dRows.ptr, 1,
+                          dLoss.ptr);
   const one = upload(Float32Array.of(1));
   const dG = hip.malloc(R * V * 4);
-  hip.crossEntropyBackward(dL.ptr, V, dT.ptr, dLse.ptr, one.ptr, R, V, -100, 1, dG.ptr, V, 0);
+  hip.crossEntropyBackward(dL.ptr, V, dT.ptr, null, 0, dLse.ptr, one.ptr, R, V, -100, 1, dG.ptr,
+                           V, 0);
   const loss = (await hip.d2hAsync(dLoss.ptr, new Float32Array(1)))[0];
   const grad = await hip.d2hAsync(dG.ptr, new Float32Array(R * V));
   let ref = 0, valid = 0, gErr = 0;
@@ -144,16 +146,62 @@ async function main() {
     for (let c = 1; c < ac; ++c) if (av[r * ac + c] > av[r * ac + best]) best = c;
     argOk = argOk && ai[r] === best;
   }
-  const sel = Int32Array.of(4, 0, -1, 2);
+  const sel = Int32Array.of(4, 0, 3, 2);
   const dsel = upload(sel), dso = hip.malloc(sel.length * ac * 4);
   hip.indexSelect(dav.ptr, 1, ar, ac, dsel.ptr, sel.length, dso.ptr);
   const so = await hip.d2hAsync(dso.ptr, new Float32Array(sel.length * ac));
   for (let j = 0; j < sel.length; ++j) {
-    const row = sel[j] < 0 ? sel[j] + ar : sel[j];
+    const row = sel[j];
     for (let c = 0; c < ac; ++c) argOk = argOk && so[j * ac + c] === av[row * ac + c];
   }
   out.argmax_index_select_exact = argOk;
   ok = ok && argOk;
+
+  // d2hAsync copies in submission order: a fill launched right after the
+  // call, and a free of the source, cannot change what the Promise returns
+  const NS = 1 << 20;
+  const src = Float32Array.from({ length: NS }, (_, i) => i % 977);
+  const dsrc = upload(src);
+  const pending = hip.d2hAsync(dsrc.ptr, new Float32Array(NS), dsrc);
+  hip.fill(dsrc.ptr, NS, 7.0);
+  const later = hip.d2hAsync(dsrc.ptr, new Float32Array(NS));
+  hip.free(dsrc);
+  const reuse = hip.malloc(NS * 4);  // the freed block, handed out again
+  hip.fill(reuse.ptr, NS, -1.0);
+  const [old, filled] = await Promise.all([pending, later]);
+  let orderOk = true;
+  for (let i = 0; i < NS; ++i) orderOk = orderOk && old[i] === src[i] && filled[i] === 7.0;
+  out.d2h_async_submission_order = orderOk;
+  ok = ok && orderOk;
+
+  // free() then GC: the finalizer of a freed allocation must not return the
+  // block again (it may belong to a newer allocation by then)
+  if (typeof global.gc === 'function') {
+    const blk = 1 << 16;
+    const s0 = hip.memoryStats();
+    let a = hip.malloc(blk);
+    const pa = a.ptr;
+    hip.free(a);
+    let doubleFreeThrows = false;
+    try { hip.free(a); } catch (e) { doubleFreeThrows = /already freed/.test(e.message); }
+    a = null;
+    const b = hip.malloc(blk);  // reuses the block `a` had
+    global.gc();
+    await new Promise((r) => setImmediate(r));
+    global.gc();
+    await new Promise((r) => setImmediate(r));
+    const c = hip.malloc(blk);
+    const s1 = hip.memoryStats();
+    const gcOk = b.ptr === pa && c.ptr !== b.ptr && doubleFreeThrows &&
+        s1.activeBytes - s0.activeBytes === 2 * blk;
+    out.free_then_gc = { reused: b.ptr === pa, distinct: c.ptr !== b.ptr, doubleFreeThrows,
+                         activeDelta: s1.activeBytes - s0.activeBytes };
+    ok = ok && gcOk;
+    hip.free(b);
+    hip.free(c);
+  } else {
+    out.free_then_gc = 'skipped (run node with --expose-gc)';
+  }
 
   hip.synchronize();
   out.mem = hip.memoryStats();

@@ -5,11 +5,17 @@
  * Device pointers cross into JavaScript as BigInt (so views can add byte
  * offsets); an allocation is owned by an External whose finalizer returns
  * it to the library's stream-ordered cache, which is safe whenever the GC
- * runs because every later use is ordered on the library stream.
+ * runs because every later use is ordered on the library stream.  An
+ * explicit free(allocation) returns the block at once and marks the
+ * External, so its finalizer does nothing later (the block may by then
+ * belong to another allocation).
  * Every failing call throws an Error carrying tjh_last_error().
- * Host data moves through TypedArrays; d2hAsync resolves a Promise from a
- * libuv worker (napi_async_work) so readbacks do not block the event loop,
- * the analogue of torch.js's mapAsync readback (buffer.ts:150-206).
+ * Host data moves through TypedArrays.  d2hAsync enqueues its copy on the
+ * library stream when it is called (tjh_d2h_start: submission order is
+ * execution order, as on torch.js's single WebGPU queue), and a libuv
+ * worker (napi_async_work) waits for it and resolves the Promise
+ * (tjh_d2h_finish), so readbacks do not block the event loop: the
+ * analogue of torch.js's mapAsync readback (buffer.ts:150-206).
  *
  * Every entry point of include/torchjs_hip.h is bound (tjh_last_error's
  * message rides on the thrown Error; tjh_version is the `version`
@@ -145,10 +151,19 @@ static napi_value js_device_info(napi_env env, napi_callback_info info) {
   return o;
 }
 
+/* What an allocation's External holds: the block, and whether free() has
+ * already returned it (then the GC finalizer must not). */
+typedef struct {
+  void* p;
+  int freed;
+} Block;
+
 static void free_ext(napi_env env, void* data, void* hint) {
   (void)env;
   (void)hint;
-  tjh_free(data);
+  Block* b = (Block*)data;
+  if (!b->freed) tjh_free(b->p);
+  free(b);
 }
 
 /* malloc(bytes) -> { ptr: BigInt, handle: External (frees on GC) } */
@@ -157,12 +172,41 @@ static napi_value js_malloc(napi_env env, napi_callback_info info) {
   if (!get_args(env, info, 1, a)) return NULL;
   void* p = NULL;
   CHECK_RC(tjh_malloc((size_t)i64(env, a[0]), &p));
+  Block* b = (Block*)malloc(sizeof(Block));
+  if (!b) {
+    tjh_free(p);
+    napi_throw_error(env, NULL, "malloc: out of host memory");
+    return NULL;
+  }
+  b->p = p;
+  b->freed = 0;
   napi_value o, ext;
   napi_create_object(env, &o);
-  napi_create_external(env, p, free_ext, NULL, &ext);
+  if (napi_create_external(env, b, free_ext, NULL, &ext) != napi_ok) {
+    tjh_free(p);
+    free(b);
+    napi_throw_error(env, NULL, "malloc: napi_create_external failed");
+    return NULL;
+  }
   napi_set_named_property(env, o, "ptr", bigint(env, p));
   napi_set_named_property(env, o, "handle", ext);
   return o;
+}
+
+/* The Block behind an allocation object { ptr, handle } or its handle. */
+static Block* block_of(napi_env env, napi_value v) {
+  napi_valuetype t;
+  napi_typeof(env, v, &t);
+  if (t == napi_object) {
+    napi_value h;
+    if (napi_get_named_property(env, v, "handle", &h) != napi_ok) return NULL;
+    v = h;
+    napi_typeof(env, v, &t);
+  }
+  if (t != napi_external) return NULL;
+  void* data = NULL;
+  if (napi_get_value_external(env, v, &data) != napi_ok) return NULL;
+  return (Block*)data;
 }
 
 static int typed(napi_env env, napi_value v, void** data, size_t* bytes) {
@@ -210,10 +254,10 @@ static napi_value js_d2h(napi_env env, napi_callback_info info) {
 typedef struct {
   napi_async_work work;
   napi_deferred deferred;
-  napi_ref keep;  /* the destination TypedArray */
+  napi_ref keep;      /* the destination TypedArray */
+  napi_ref keep_src;  /* the source allocation, when given (or NULL) */
   void* dst;
-  const void* src;
-  size_t bytes;
+  uint64_t ticket;
   int rc;
   char msg[1024];
 } D2HJob;
@@ -221,7 +265,7 @@ typedef struct {
 static void d2h_exec(napi_env env, void* data) {
   (void)env;
   D2HJob* j = (D2HJob*)data;
-  j->rc = tjh_d2h(j->dst, j->src, j->bytes);
+  j->rc = tjh_d2h_finish(j->ticket, j->dst);
   if (j->rc) snprintf(j->msg, sizeof(j->msg), "%s", tjh_last_error());
 }
 
@@ -239,24 +283,47 @@ static void d2h_done(napi_env env, napi_status status, void* data) {
     napi_reject_deferred(env, j->deferred, e);
   }
   napi_delete_reference(env, j->keep);
+  if (j->keep_src) napi_delete_reference(env, j->keep_src);
   napi_delete_async_work(env, j->work);
   free(j);
 }
 
-/* d2hAsync(ptr, typedArray) -> Promise<typedArray> */
+/* d2hAsync(ptr, typedArray[, allocation]) -> Promise<typedArray>.  The copy
+ * is enqueued now, in submission order: kernels launched after this call,
+ * or a free of the source, cannot change the bytes it reads.  The optional
+ * allocation object is kept alive until the Promise settles. */
 static napi_value js_d2h_async(napi_env env, napi_callback_info info) {
-  napi_value a[2];
-  if (!get_args(env, info, 2, a)) return NULL;
+  size_t argc = 3;
+  napi_value a[3];
+  if (napi_get_cb_info(env, info, &argc, a, NULL, NULL) != napi_ok) return NULL;
+  if (argc < 2) {
+    napi_throw_type_error(env, NULL, "d2hAsync(ptr, typedArray[, allocation])");
+    return NULL;
+  }
   D2HJob* j = (D2HJob*)calloc(1, sizeof(D2HJob));
-  if (!typed(env, a[1], &j->dst, &j->bytes)) {
+  if (!j) {
+    napi_throw_error(env, NULL, "d2hAsync: out of host memory");
+    return NULL;
+  }
+  size_t bytes = 0;
+  if (!typed(env, a[1], &j->dst, &bytes)) {
     free(j);
     napi_throw_type_error(env, NULL, "d2hAsync: expected a TypedArray");
     return NULL;
   }
-  j->src = ptr(env, a[0]);
+  int rc = tjh_d2h_start(ptr(env, a[0]), bytes, &j->ticket);
+  if (rc != 0) {
+    free(j);
+    return throw_last(env, rc);
+  }
   napi_value promise, name;
   napi_create_promise(env, &j->deferred, &promise);
   napi_create_reference(env, a[1], 1, &j->keep);
+  if (argc >= 3) {
+    napi_valuetype t;
+    napi_typeof(env, a[2], &t);
+    if (t == napi_object || t == napi_external) napi_create_reference(env, a[2], 1, &j->keep_src);
+  }
   napi_create_string_utf8(env, "tjh_d2h", NAPI_AUTO_LENGTH, &name);
   napi_create_async_work(env, NULL, name, d2h_exec, d2h_done, j, &j->work);
   napi_queue_async_work(env, j->work);
@@ -379,27 +446,30 @@ static napi_value js_softmax_backward(napi_env env, napi_callback_info info) {
   return undef(env);
 }
 
-/* crossEntropyForward(logits, ld, targets, rows, cols, ignore, lse, lossRows, reduction, out) */
+/* crossEntropyForward(logits, ld, targets, rows, cols, ignore, weight, labelSmoothing, lse,
+ *                     lossRows, reduction, out); weight may be null */
 static napi_value js_ce_forward(napi_env env, napi_callback_info info) {
-  napi_value a[10];
-  if (!get_args(env, info, 10, a)) return NULL;
+  napi_value a[12];
+  if (!get_args(env, info, 12, a)) return NULL;
   CHECK_RC(tjh_cross_entropy_forward((const float*)ptr(env, a[0]), i64(env, a[1]),
                                      (const int32_t*)ptr(env, a[2]), i64(env, a[3]), i64(env, a[4]),
-                                     (int32_t)i64(env, a[5]), (float*)ptr(env, a[6]),
-                                     (float*)ptr(env, a[7]), (int)i64(env, a[8]),
-                                     (float*)ptr(env, a[9])));
+                                     (int32_t)i64(env, a[5]), (const float*)ptr(env, a[6]),
+                                     (float)f64(env, a[7]), (float*)ptr(env, a[8]),
+                                     (float*)ptr(env, a[9]), (int)i64(env, a[10]),
+                                     (float*)ptr(env, a[11])));
   return undef(env);
 }
 
-/* crossEntropyBackward(logits, ld, targets, lse, gradOut, rows, cols, ignore, reduction, d, ldd, acc) */
+/* crossEntropyBackward(logits, ld, targets, weight, labelSmoothing, lse, gradOut, rows, cols,
+ *                      ignore, reduction, d, ldd, acc) */
 static napi_value js_ce_backward(napi_env env, napi_callback_info info) {
-  napi_value a[12];
-  if (!get_args(env, info, 12, a)) return NULL;
+  napi_value a[14];
+  if (!get_args(env, info, 14, a)) return NULL;
   CHECK_RC(tjh_cross_entropy_backward(
       (const float*)ptr(env, a[0]), i64(env, a[1]), (const int32_t*)ptr(env, a[2]),
-      (const float*)ptr(env, a[3]), (const float*)ptr(env, a[4]), i64(env, a[5]), i64(env, a[6]),
-      (int32_t)i64(env, a[7]), (int)i64(env, a[8]), (float*)ptr(env, a[9]), i64(env, a[10]),
-      (int)i64(env, a[11])));
+      (const float*)ptr(env, a[3]), (float)f64(env, a[4]), (const float*)ptr(env, a[5]),
+      (const float*)ptr(env, a[6]), i64(env, a[7]), i64(env, a[8]), (int32_t)i64(env, a[9]),
+      (int)i64(env, a[10]), (float*)ptr(env, a[11]), i64(env, a[12]), (int)i64(env, a[13])));
   return undef(env);
 }
 
@@ -570,12 +640,23 @@ static napi_value js_device_count(napi_env env, napi_callback_info info) {
   CHECK_RC(tjh_device_count(&n));
   return num(env, n);
 }
-/* free(ptr): returns a block to the cache now (the GC finalizer of the
- * allocation's handle must then not run: callers drop the handle). */
+/* free(allocation): returns the block of an allocation object from malloc
+ * (or its handle) to the cache now, in stream order; the handle's GC
+ * finalizer then does nothing.  Freeing an allocation twice throws. */
 static napi_value js_free(napi_env env, napi_callback_info info) {
   napi_value a[1];
   if (!get_args(env, info, 1, a)) return NULL;
-  CHECK_RC(tjh_free(ptr(env, a[0])));
+  Block* b = block_of(env, a[0]);
+  if (!b) {
+    napi_throw_type_error(env, NULL, "free: expected the allocation returned by malloc");
+    return NULL;
+  }
+  if (b->freed) {
+    napi_throw_error(env, NULL, "free: allocation already freed");
+    return NULL;
+  }
+  CHECK_RC(tjh_free(b->p));
+  b->freed = 1;
   return undef(env);
 }
 static napi_value js_reset_peak(napi_env env, napi_callback_info info) {
@@ -730,21 +811,22 @@ static napi_value js_argmax(napi_env env, napi_callback_info info) {
                       (int)i64(env, a[4]), I32(a[5])));
   return undef(env);
 }
-/* nllLossForward(logp, ld, targets, rows, cols, ignore, lossRows, reduction, out) */
+/* nllLossForward(logp, ld, targets, rows, cols, ignore, weight, lossRows, reduction, out) */
 static napi_value js_nll_forward(napi_env env, napi_callback_info info) {
-  napi_value a[9];
-  if (!get_args(env, info, 9, a)) return NULL;
+  napi_value a[10];
+  if (!get_args(env, info, 10, a)) return NULL;
   CHECK_RC(tjh_nll_loss_forward(CF32(a[0]), i64(env, a[1]), CI32(a[2]), i64(env, a[3]),
-                                i64(env, a[4]), (int32_t)i64(env, a[5]), F32(a[6]),
-                                (int)i64(env, a[7]), F32(a[8])));
+                                i64(env, a[4]), (int32_t)i64(env, a[5]), CF32(a[6]), F32(a[7]),
+                                (int)i64(env, a[8]), F32(a[9])));
   return undef(env);
 }
-/* nllLossBackward(targets, gradOut, rows, cols, ignore, reduction, dlogp) */
+/* nllLossBackward(targets, weight, gradOut, rows, cols, ignore, reduction, dlogp) */
 static napi_value js_nll_backward(napi_env env, napi_callback_info info) {
-  napi_value a[7];
-  if (!get_args(env, info, 7, a)) return NULL;
-  CHECK_RC(tjh_nll_loss_backward(CI32(a[0]), CF32(a[1]), i64(env, a[2]), i64(env, a[3]),
-                                 (int32_t)i64(env, a[4]), (int)i64(env, a[5]), F32(a[6])));
+  napi_value a[8];
+  if (!get_args(env, info, 8, a)) return NULL;
+  CHECK_RC(tjh_nll_loss_backward(CI32(a[0]), CF32(a[1]), CF32(a[2]), i64(env, a[3]),
+                                 i64(env, a[4]), (int32_t)i64(env, a[5]), (int)i64(env, a[6]),
+                                 F32(a[7])));
   return undef(env);
 }
 /* indexSelect(x, outer, srcLen, inner, idx, nIdx, out) */

@@ -564,6 +564,17 @@ class Tensor:
     def argmax(self, dim=None, keepdim=False):
         return argmax(self, dim, keepdim)
 
+    def clamp(self, min=None, max=None):
+        return clamp(self, min, max)
+
+    def clamp_min(self, min):
+        return clamp(self, min, None)
+
+    def clamp_max(self, max):
+        return clamp(self, None, max)
+
+    clip = clamp
+
     def argmin(self, dim=None, keepdim=False):
         return argmax(self, dim, keepdim, is_min=True)
 
@@ -790,9 +801,13 @@ def manual_seed(seed):
 def _next_seed():
     # torch.js seeds each rand/randn call with an LCG step of a global seed
     # (src/ops/creation.ts:921); an unset seed starts from a random value.
+    # The step is JavaScript arithmetic: the product and the sum are IEEE
+    # doubles (products above 2^53 round before the mask), then ToInt32 and
+    # `& 0x7fffffff` keep the low 31 bits of the rounded integer.
     if _state["seed"] is None:
         _state["seed"] = int(np.random.randint(0, 2147483647))
-    _state["seed"] = (_state["seed"] * 1103515245 + 12345) & 0x7FFFFFFF
+    v = float(_state["seed"]) * 1103515245.0 + 12345.0
+    _state["seed"] = int(v) & 0x7FFFFFFF
     return _state["seed"]
 
 
@@ -1164,6 +1179,34 @@ def compare(a, b, op):
     return compare_raw(a, b, op)
 
 
+def clamp(x, min=None, max=None):
+    """clamp / clamp_min / clamp_max (clamp.wgsl): max(x, min) then
+    min(., max); the gradient passes where min <= x <= max (PyTorch's
+    rule, the bounds included)."""
+    if min is None and max is None:
+        raise RuntimeError("clamp: at least one of min and max must be given")
+    if x.dtype != "float32":
+        x = x.float()
+    out = x.contiguous().detach()
+    if min is not None:
+        out = _k_scalar("maximum", out, float(min))
+    if max is not None:
+        out = _k_scalar("minimum", out, float(max))
+    if out is x:
+        out = _k_contiguous(x)
+    xd = x.detach()
+
+    def bwd(g):
+        m = None
+        if min is not None:
+            m = compare_raw(xd, float(min), "ge")
+        if max is not None:
+            mx = compare_raw(xd, float(max), "le")
+            m = mx if m is None else _k_binary("mul", m, mx)
+        return [_k_binary("mul", g, m)]
+    return _record(out, "Clamp", [x], bwd)
+
+
 # ------------------------------------------------------------ reductions
 
 
@@ -1502,7 +1545,13 @@ def _getitem(x, idx):
             d += 1
             continue
         if isinstance(it, Tensor):
-            out = index_select(out, d, it.reshape(-1))
+            # advanced indexing wraps negative indices once (index_select
+            # itself rejects them)
+            ih = it.reshape(-1).to("int32").numpy()
+            n = out.shape[d]
+            if ih.size and (ih.min() < -n or ih.max() >= n):
+                raise IndexError("index out of range for dimension of size %d" % n)
+            out = index_select(out, d, np.where(ih < 0, ih + n, ih).astype(np.int32))
             d += 1
             continue
         raise TypeError("unsupported index %r" % (it,))
@@ -1588,7 +1637,10 @@ def _idx32(index):
 
 def index_select(x, dim, index):
     """index_select (Tensor.ts:1242-1287) for any rank; backward is an
-    ordered index_add (torch.js has none)."""
+    ordered index_add (torch.js has none).  Indices must lie in [0, n):
+    PyTorch's index_select raises for anything else, negatives included
+    (torch.js's index_select.wgsl:32-52 casts them to u32 and reads out of
+    bounds), and so does this one."""
     d = _wrap_dim(dim, x.ndim)
     index = _idx32(index)
     if index.ndim != 1:
@@ -1597,8 +1649,10 @@ def index_select(x, dim, index):
     outer, src, inner = _numel(xc.shape[:d]), xc.shape[d], _numel(xc.shape[d + 1:])
     n = index.numel()
     host = index.numpy()
-    if n and (host.max() >= src or host.min() < -src):
-        raise IndexError("index_select: index out of range for dimension of size %d" % src)
+    if n and (host.max() >= src or host.min() < 0):
+        bad = int(host.min()) if host.min() < 0 else int(host.max())
+        raise IndexError("index_select: index %d is out of range for dimension of size %d"
+                         % (bad, src))
     oshape = xc.shape[:d] + (n,) + xc.shape[d + 1:]
     out = empty(oshape)
     L.check(L.lib().tjh_index_select(xc.data_ptr(), outer, src, inner, index.data_ptr(), n,
@@ -2010,6 +2064,10 @@ def _can_defer(node, wanted):
         if (t.grad_fn is not None or t._grad is not None or not t.requires_grad or
                 id(t) in seen):
             return False
+        # the same tensor in another slot (layer_norm(w, (n,), w, b)) gets a
+        # second contribution from this node, which a deferred .grad would lose
+        if any(j != k and u is t for j, u in enumerate(node.inputs)):
+            return False
         seen.add(id(t))
     return bool(seen)
 
@@ -2037,17 +2095,26 @@ def _pending_for(node, grads, wanted, owned):
         prev = t._grad
         if prev is None or id(prev._storage) not in owned:
             return None
-        for p in grads.values():
-            pieces = p.pieces if isinstance(p, _SliceGrad) else [(0, p)]
-            if any(q._storage is prev._storage for _, q in pieces):
-                return None
+        others = [p for p in grads.values()]
     else:
         if t._retains_grad:
             return None
         prev = grads.get(id(t.grad_fn))
+        if prev is None or isinstance(prev, _SliceGrad):
+            return None
+        # a pending gradient may be the very tensor an add / sub / scalar-add
+        # VJP also handed to another input, a leaf's .grad among them: the
+        # VJP may add into it in place only if nothing else holds it
+        if id(prev._storage) in owned:
+            return None
+        others = [p for key, p in grads.items() if key != id(t.grad_fn)]
     if (prev is None or isinstance(prev, _SliceGrad) or prev.shape != t.shape or
             prev._dtype != "float32" or not prev.is_contiguous()):
         return None
+    for p in others:
+        pieces = p.pieces if isinstance(p, _SliceGrad) else [(0, p)]
+        if any(q._storage is prev._storage for _, q in pieces):
+            return None
     return prev
 
 
