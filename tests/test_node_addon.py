@@ -74,4 +74,5 @@ def test_addon_end_to_end():
     # a readback enqueued before a fill and a free returns the old bytes
     assert out["d2h_async_submission_order"] is True
     # free() followed by GC never returns a block twice
-    assert out["free_then_gc"]["distinct"] and out["free_then_gc"]["doubleFreeThrows"], out
+    fg = out["free_then_gc"]
+    assert fg["distinct"] and fg["doubleFreeThrows"] and fg["intact"], out

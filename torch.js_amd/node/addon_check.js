@@ -178,7 +178,6 @@ async function main() {
   // block again (it may belong to a newer allocation by then)
   if (typeof global.gc === 'function') {
     const blk = 1 << 16;
-    const s0 = hip.memoryStats();
     let a = hip.malloc(blk);
     const pa = a.ptr;
     hip.free(a);
@@ -191,11 +190,14 @@ async function main() {
     global.gc();
     await new Promise((r) => setImmediate(r));
     const c = hip.malloc(blk);
-    const s1 = hip.memoryStats();
-    const gcOk = b.ptr === pa && c.ptr !== b.ptr && doubleFreeThrows &&
-        s1.activeBytes - s0.activeBytes === 2 * blk;
+    // b's block still belongs to b alone: c's writes do not reach it
+    hip.fill(b.ptr, blk / 4, 1.0);
+    hip.fill(c.ptr, blk / 4, 2.0);
+    const bv = await hip.d2hAsync(b.ptr, new Float32Array(blk / 4), b);
+    const intact = bv.every((v) => v === 1.0);
+    const gcOk = b.ptr === pa && c.ptr !== b.ptr && doubleFreeThrows && intact;
     out.free_then_gc = { reused: b.ptr === pa, distinct: c.ptr !== b.ptr, doubleFreeThrows,
-                         activeDelta: s1.activeBytes - s0.activeBytes };
+                         intact };
     ok = ok && gcOk;
     hip.free(b);
     hip.free(c);
