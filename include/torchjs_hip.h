@@ -358,6 +358,25 @@ int tjh_layer_norm_backward_res(const float* dy, const float* x,
                                 int64_t rows, int64_t cols, int flags);
 /* Runs the finishing passes postponed by TJH_LN_DEFER (none: no launch). */
 int tjh_flush_deferred(void);
+/* tjh_layer_norm_backward_res (flags = accumulate & 1, no deferral) that
+ * allocates nothing.  No counterpart in the reference: it is for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight
+ * serving or training loops, harnesses that forbid hipMalloc).  The
+ * dgamma / dbeta partial rows live in a static 12 MiB device array of the
+ * library (2 x 512 rows of up to 3072 floats, enough for any row count on
+ * a 256-CU MI355X) instead of the caching allocator; the kernels and the
+ * results are those of tjh_layer_norm_backward_res, bit for bit.  Takes
+ * cols a multiple of 4 up to 3072 with 16-byte aligned operands (else
+ * TJH_ERR_UNSUPPORTED) and rejects a request whose partials would exceed
+ * the array (TJH_ERR_INVALID).  Every call on a GPU shares that GPU's
+ * array: calls run in order on the library stream, but a captured graph
+ * replayed concurrently with another call on the same GPU races on it. */
+int tjh_layer_norm_backward_noalloc(const float* dy, const float* x,
+                                    const float* gamma, const float* mean,
+                                    const float* rstd, const float* res,
+                                    float* dx, float* dgamma, float* dbeta,
+                                    int64_t rows, int64_t cols,
+                                    int accumulate);
 
 /* ------------------------------------------------------------------ */
 /* Embedding / indexing — embedding.wgsl:13-27, index_select.wgsl,      */

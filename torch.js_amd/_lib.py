@@ -112,6 +112,8 @@ SIGNATURES = {
     "tjh_layer_norm_backward_res": [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64,
                                     c_i64, c_int],
     "tjh_flush_deferred": [],
+    "tjh_layer_norm_backward_noalloc": [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,
+                                        c_i64, c_i64, c_int],
     "tjh_embedding_forward": [c_vp, c_i64, c_i64, c_vp, c_i64, c_vp],
     "tjh_embedding_backward": [c_vp, c_vp, c_i64, c_i64, c_vp, c_i64, c_int],
     "tjh_index_select": [c_vp, c_i64, c_i64, c_i64, c_vp, c_i64, c_vp],

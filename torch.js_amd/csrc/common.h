@@ -19,6 +19,9 @@ hipStream_t stream();
 bool initialized();
 int device_ordinal();
 int num_cus();
+// Takes the device address of the allocation-free entry points' static
+// scratch (norm.hip) for the current device; tjh_init calls it once.
+int noalloc_setup(int ordinal);
 
 // Returns TJH_ERR_NOT_INITIALIZED (with message) unless tjh_init succeeded.
 int require_init();

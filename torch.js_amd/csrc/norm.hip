@@ -791,6 +791,49 @@ using namespace tjh;
 namespace tjh {
 namespace {
 
+// The register-resident LayerNorm backward (k_ln_bwd_wave) takes rows
+// whose length is a multiple of 4 and at most 3072, with 16-byte aligned
+// operands; returns its V4 (float4 per lane), or 0 for the general path.
+int ln_bwd_v4(const float* dy, const float* x, const float* gamma, const float* res,
+              const float* dx, int64_t cols) {
+  const bool vec = cols % 4 == 0 && aligned16(x) && aligned16(dy) && (!dx || aligned16(dx)) &&
+                   (!gamma || aligned16(gamma)) && (!res || aligned16(res));
+  if (!vec) return 0;
+  return cols <= 64 * 4 * 3 ? 3 : (cols <= 64 * 4 * 6 ? 6 : (cols <= 64 * 4 * 12 ? 12 : 0));
+}
+
+// Rows per workgroup: ~2 workgroups per CU, >= 16 rows each (fewer partial
+// rows for the dgamma/dbeta pass; measured faster than 4 per CU).  So
+// nb <= max(2 * CUs, ...) and nb <= 512 on a 256-CU MI355X.
+void ln_bwd_blocks(int64_t rows, int64_t& rpb, int64_t& nb) {
+  const int cus = num_cus() > 0 ? num_cus() : 256;
+  rpb = cdiv(rows, 2LL * cus);
+  if (rpb < 16) rpb = 16;
+  nb = cdiv(rows, rpb);
+}
+
+// Launches k_ln_bwd_wave: dx (optionally plus res) and, with pg / pb, the
+// per-workgroup partial rows [nb, cols] of dgamma / dbeta (every row
+// written whole).
+int ln_bwd_wave_launch(int v4, const float* dy, const float* x, const float* gamma,
+                       const float* mean, const float* rstd, const float* res, float* dx,
+                       float* pg, float* pb, int64_t rows, int64_t cols, int64_t rpb,
+                       int64_t nb) {
+  if (v4 == 3 && cols == 64 * 4 * 3)
+    hipLaunchKernelGGL((k_ln_bwd_wave<3, true>), dim3((unsigned)nb), dim3(kBlock), 0, stream(),
+                       dy, x, gamma, mean, rstd, res, dx, pg, pb, rows, cols, rpb);
+  else if (v4 == 3)
+    hipLaunchKernelGGL((k_ln_bwd_wave<3, false>), dim3((unsigned)nb), dim3(kBlock), 0, stream(),
+                       dy, x, gamma, mean, rstd, res, dx, pg, pb, rows, cols, rpb);
+  else if (v4 == 6)
+    hipLaunchKernelGGL((k_ln_bwd_wave<6, false>), dim3((unsigned)nb), dim3(kBlock), 0, stream(),
+                       dy, x, gamma, mean, rstd, res, dx, pg, pb, rows, cols, rpb);
+  else
+    hipLaunchKernelGGL((k_ln_bwd_wave<12, false>), dim3((unsigned)nb), dim3(kBlock), 0, stream(),
+                       dy, x, gamma, mean, rstd, res, dx, pg, pb, rows, cols, rpb);
+  return check_launch("layer_norm_backward");
+}
+
 // LayerNorm backwards whose dgamma/dbeta finishing pass waits for
 // tjh_flush_deferred: the partial-row scratch block and the outputs.
 struct DeferredSums {
@@ -1034,35 +1077,18 @@ int tjh_layer_norm_backward_res(const float* dy, const float* x, const float* ga
     return TJH_OK;
   }
   bool want_p = dgamma || dbeta;
-  bool vec = cols % 4 == 0 && aligned16(x) && aligned16(dy) && (!dx || aligned16(dx)) &&
-             (!gamma || aligned16(gamma)) && (!res || aligned16(res));
-  int v4 = cols <= 64 * 4 * 3 ? 3 : (cols <= 64 * 4 * 6 ? 6 : (cols <= 64 * 4 * 12 ? 12 : 0));
-  if (vec && v4) {
-    // rows per block: ~2 blocks per CU, >= 16 rows each (fewer partial
-    // rows for the dgamma/dbeta pass; measured faster than 4 per CU)
-    int cus = num_cus() > 0 ? num_cus() : 256;
-    int64_t rpb = cdiv(rows, 2LL * cus);
-    if (rpb < 16) rpb = 16;
-    int64_t nb = cdiv(rows, rpb);
+  const int v4 = ln_bwd_v4(dy, x, gamma, res, dx, cols);
+  if (v4) {
+    int64_t rpb, nb;
+    ln_bwd_blocks(rows, rpb, nb);
     Scratch part(want_p ? (size_t)(2 * nb * cols) * sizeof(float) : 0);
     if (want_p && !part.ok()) return set_error(TJH_ERR_OOM, "layer_norm_backward: no scratch");
     float* pg = want_p ? part.as<float>() : nullptr;
     float* pb = want_p ? part.as<float>() + nb * cols : nullptr;
     {
       KernelScope ks("layer_norm_bwd");
-      if (v4 == 3 && cols == 64 * 4 * 3)
-        hipLaunchKernelGGL((k_ln_bwd_wave<3, true>), dim3((unsigned)nb), dim3(kBlock), 0, stream(),
-                           dy, x, gamma, mean, rstd, res, dx, pg, pb, rows, cols, rpb);
-      else if (v4 == 3)
-        hipLaunchKernelGGL((k_ln_bwd_wave<3, false>), dim3((unsigned)nb), dim3(kBlock), 0, stream(),
-                           dy, x, gamma, mean, rstd, res, dx, pg, pb, rows, cols, rpb);
-      else if (v4 == 6)
-        hipLaunchKernelGGL((k_ln_bwd_wave<6, false>), dim3((unsigned)nb), dim3(kBlock), 0, stream(),
-                           dy, x, gamma, mean, rstd, res, dx, pg, pb, rows, cols, rpb);
-      else
-        hipLaunchKernelGGL((k_ln_bwd_wave<12, false>), dim3((unsigned)nb), dim3(kBlock), 0,
-                           stream(), dy, x, gamma, mean, rstd, res, dx, pg, pb, rows, cols, rpb);
-      int rc = check_launch("layer_norm_backward");
+      int rc = ln_bwd_wave_launch(v4, dy, x, gamma, mean, rstd, res, dx, pg, pb, rows, cols, rpb,
+                                  nb);
       if (rc != TJH_OK) return rc;
       if (want_p && defer) {
         // dgamma and dbeta wait for tjh_flush_deferred, which finishes
@@ -1093,6 +1119,87 @@ int tjh_layer_norm_backward_res(const float* dy, const float* x, const float* ga
   }
   if (want_p) return sum_partials(pg, pb, rows, cols, dgamma, dbeta, accumulate);
   return TJH_OK;
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------- no-alloc
+//
+// tjh_layer_norm_backward_noalloc keeps the dgamma / dbeta partial rows in
+// this file-scope device array instead of the caching allocator: 2 x 512
+// partial rows of up to 3072 floats, the most k_ln_bwd_wave writes on a
+// 256-CU MI355X (12 MiB, held by every GPU the library runs on until the
+// process ends).  Host code never passes `scratch` itself to a kernel: its
+// name is a host-side stand-in there.  Its device address comes from
+// hipGetSymbolAddress, taken once per device by tjh_init.
+
+static constexpr int64_t kNoAllocFloats = 2 * 512 * 3072;
+static __device__ __align__(256) float scratch[kNoAllocFloats];
+
+namespace tjh {
+namespace {
+constexpr int kMaxDevices = 64;
+float* g_noalloc_scratch[kMaxDevices] = {};  // device address of `scratch`, per device
+}  // namespace
+
+int noalloc_setup(int ordinal) {
+  if (ordinal < 0 || ordinal >= kMaxDevices)
+    return set_error(TJH_ERR_UNSUPPORTED, "device ordinal %d beyond %d", ordinal, kMaxDevices);
+  if (g_noalloc_scratch[ordinal]) return TJH_OK;
+  void* p = nullptr;
+  hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || !p) {
+    (void)hipGetLastError();
+    return hip_fail(e, "hipGetSymbolAddress(scratch)");
+  }
+  g_noalloc_scratch[ordinal] = static_cast<float*>(p);
+  return TJH_OK;
+}
+}  // namespace tjh
+
+extern "C" {
+
+int tjh_layer_norm_backward_noalloc(const float* dy, const float* x, const float* gamma,
+                                    const float* mean, const float* rstd, const float* res,
+                                    float* dx, float* dgamma, float* dbeta, int64_t rows,
+                                    int64_t cols, int accumulate) {
+  TJH_REQUIRE_INIT();
+  TJH_ARG(rows >= 0 && cols > 0, "tjh_layer_norm_backward_noalloc: bad sizes");
+  TJH_ARG(!res || dx, "tjh_layer_norm_backward_noalloc: res needs dx");
+  TJH_ARG(mean && rstd && dy && x, "tjh_layer_norm_backward_noalloc: NULL input");
+  const int dev = device_ordinal();
+  float* sp = (dev >= 0 && dev < kMaxDevices) ? g_noalloc_scratch[dev] : nullptr;
+  if (!sp)
+    return set_error(TJH_ERR_NOT_INITIALIZED,
+                     "tjh_layer_norm_backward_noalloc: no scratch address for device %d", dev);
+  if (rows == 0) {
+    if (!accumulate) {
+      if (dgamma) { int rc = tjh_fill_f32(dgamma, cols, 0.f); if (rc) return rc; }
+      if (dbeta) { int rc = tjh_fill_f32(dbeta, cols, 0.f); if (rc) return rc; }
+    }
+    return TJH_OK;
+  }
+  const int v4 = ln_bwd_v4(dy, x, gamma, res, dx, cols);
+  if (!v4)
+    return set_error(TJH_ERR_UNSUPPORTED,
+                     "tjh_layer_norm_backward_noalloc: rows of %lld floats need a multiple of 4 "
+                     "up to 3072 and 16-byte aligned operands (tjh_layer_norm_backward takes "
+                     "any layout)", (long long)cols);
+  const bool want_p = dgamma || dbeta;
+  int64_t rpb, nb;
+  ln_bwd_blocks(rows, rpb, nb);
+  if (want_p && 2 * nb * cols > kNoAllocFloats)
+    return set_error(TJH_ERR_INVALID,
+                     "tjh_layer_norm_backward_noalloc: %lld partial floats exceed the %lld-float "
+                     "scratch", (long long)(2 * nb * cols), (long long)kNoAllocFloats);
+  // the kernel overwrites every partial row it owns: nothing to clear
+  float* pg = want_p ? sp : nullptr;
+  float* pb = want_p ? sp + nb * cols : nullptr;
+  int rc = ln_bwd_wave_launch(v4, dy, x, gamma, mean, rstd, res, dx, pg, pb, rows, cols, rpb, nb);
+  if (rc != TJH_OK || !want_p) return rc;
+  float* parts[2] = {pg, pb};
+  float* outs[2] = {dgamma, dbeta};
+  return colsum_final(parts, outs, 2, nb, cols, accumulate ? 1 : 0, 1.0f);
 }
 
 int tjh_flush_deferred(void) {

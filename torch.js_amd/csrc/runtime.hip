@@ -340,6 +340,12 @@ int tjh_init(int ordinal) {
     return set_error(TJH_ERR_UNSUPPORTED,
                      "tjh_init: device %d is %s; this library is built for gfx950 only",
                      ordinal, prop.gcnArchName);
+  // the static scratch of the allocation-free entry points, addressed per
+  // device with this device current
+  {
+    int rc = noalloc_setup(ordinal);
+    if (rc != TJH_OK) return rc;
+  }
   // default priority stream, non-blocking w.r.t. the legacy null stream
   TJH_HIP(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking));
   g_cus = prop.multiProcessorCount;

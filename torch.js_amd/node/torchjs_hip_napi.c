@@ -506,6 +506,19 @@ static napi_value js_ln_backward_res(napi_env env, napi_callback_info info) {
   return undef(env);
 }
 
+/* layerNormBackwardNoalloc(dy, x, gamma, mean, rstd, res, dx, dgamma, dbeta, rows, cols, acc):
+ * the allocation-free variant (partials in the library's static scratch) */
+static napi_value js_ln_backward_noalloc(napi_env env, napi_callback_info info) {
+  napi_value a[12];
+  if (!get_args(env, info, 12, a)) return NULL;
+  CHECK_RC(tjh_layer_norm_backward_noalloc(
+      (const float*)ptr(env, a[0]), (const float*)ptr(env, a[1]), (const float*)ptr(env, a[2]),
+      (const float*)ptr(env, a[3]), (const float*)ptr(env, a[4]), (const float*)ptr(env, a[5]),
+      (float*)ptr(env, a[6]), (float*)ptr(env, a[7]), (float*)ptr(env, a[8]), i64(env, a[9]),
+      i64(env, a[10]), (int)i64(env, a[11])));
+  return undef(env);
+}
+
 /* flushDeferred() */
 static napi_value js_flush_deferred(napi_env env, napi_callback_info info) {
   (void)info;
@@ -937,7 +950,9 @@ static napi_value init_module(napi_env env, napi_value exports) {
       FN("softmaxBackward", js_softmax_backward), FN("crossEntropyForward", js_ce_forward),
       FN("crossEntropyBackward", js_ce_backward), FN("layerNormForward", js_ln_forward),
       FN("layerNormBackward", js_ln_backward),
-      FN("layerNormBackwardRes", js_ln_backward_res), FN("flushDeferred", js_flush_deferred), FN("embeddingForward", js_emb_forward),
+      FN("layerNormBackwardRes", js_ln_backward_res),
+      FN("layerNormBackwardNoalloc", js_ln_backward_noalloc),
+      FN("flushDeferred", js_flush_deferred), FN("embeddingForward", js_emb_forward),
       FN("embeddingBackward", js_emb_backward), FN("gemm", js_gemm), FN("gemmAct", js_gemm_act),
       FN("sdpaForward", js_sdpa_forward), FN("sdpaBackward", js_sdpa_backward),
       FN("adamStep", js_adam_step), FN("isInitialized", js_is_initialized),
