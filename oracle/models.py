@@ -167,8 +167,9 @@ def block_loss_and_grads(p, x, heads):
     return loss, grads
 
 
-def gpt2_loss_and_grads(cfg, p, ids, targets):
-    """GPT-2 (tied embeddings) next-token cross_entropy and all grads."""
+def gpt2_loss_and_grads(cfg, p, ids, targets, return_dlogits=False):
+    """GPT-2 (tied embeddings) next-token cross_entropy and all grads (and
+    the logits' gradient [B*T, vocab] with return_dlogits)."""
     ids = np.asarray(ids)
     B, T = ids.shape
     p = {k: np.asarray(v, dtype=F64) for k, v in p.items()}
@@ -191,6 +192,8 @@ def gpt2_loss_and_grads(cfg, p, ids, targets):
     grads["wte.weight"] = dwte_head + ops.embedding_backward(dx, ids, cfg.vocab)
     grads["wpe.weight"] = np.zeros_like(p["wpe.weight"], dtype=F64)
     grads["wpe.weight"][:T] = dx.sum(axis=0)
+    if return_dlogits:
+        return loss, grads, dlog.reshape(B * T, cfg.vocab)
     return loss, grads
 
 

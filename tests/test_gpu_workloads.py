@@ -17,6 +17,24 @@ def check(got, want, rtol=1e-4, atol=1e-5):
                                rtol=rtol, atol=atol)
 
 
+# Reductions, GEMM, attention, conv: north_star's rtol 1e-4 / atol 1e-5 per
+# element, and a scale-free bound on the whole tensor, since atol 1e-5 is
+# loose for gradients of 1e-3: ||got - want|| / ||want|| <= 1e-5.  Measured
+# at GPT-2 124M (B=1, T=1024): <= 1.8e-6 on the GPU, <= 1.05e-6 for
+# PyTorch's CPU float32 path on the same inputs (the fp32 floor).
+RELNORM = 1e-5
+
+
+def check_red(got, want, name=""):
+    got = np.asarray(got, dtype=np.float64)
+    want = np.asarray(want, dtype=np.float64)
+    check(got, want, rtol=1e-4, atol=1e-5)
+    den = np.linalg.norm(want)
+    if den > 0:
+        rel = np.linalg.norm(got - want) / den
+        assert rel <= RELNORM, (name, rel)
+
+
 def _params(model):
     return {k: p.numpy() for k, p in model.named_parameters()}
 
@@ -69,12 +87,12 @@ def test_chain_full_config(torch, n):
     check(tb.grad.numpy(), tx.grad.numpy().astype(np.float64).sum(0), rtol=1e-4, atol=1e-7)
 
 
-def test_cnn_reduced_batch(torch):
-    """The small CNN at batch 4 (full spatial size 64x64) against the oracle."""
+def test_cnn_full_batch(torch):
+    """The small CNN at its full config (batch 32, 3x64x64) against the oracle."""
     from torchjs_amd import workloads as W
     g = Generator(7)
-    x = g.randn((4, 3, 64, 64))
-    t = g.integers((4,), 10)
+    x = g.randn((32, 3, 64, 64))
+    t = g.integers((32,), 10)
     p = {"conv1.weight": g.uniform((32, 3, 3, 3), -0.19, 0.19), "conv1.bias": g.uniform((32,), -0.19, 0.19),
          "conv2.weight": g.uniform((64, 32, 3, 3), -0.059, 0.059), "conv2.bias": g.uniform((64,), -0.059, 0.059),
          "fc.weight": g.uniform((10, 64), -0.125, 0.125), "fc.bias": g.uniform((10,), -0.125, 0.125)}
@@ -83,28 +101,29 @@ def test_cnn_reduced_batch(torch):
     loss = torch.F.cross_entropy(model(torch.tensor(x)), torch.tensor(t))
     loss.backward()
     ref, rg = om.cnn_loss_and_grads(p, x, t)
-    check(loss.item(), ref)
+    check_red(loss.item(), ref, "loss")
     for k, prm in model.named_parameters():
-        check(prm.grad.numpy(), rg[k], rtol=1e-4, atol=1e-5)
+        check_red(prm.grad.numpy(), rg[k], k)
 
 
-def test_transformer_block_reduced(torch):
-    """Pre-LN block (d=768, 12 heads, causal) at B=2, T=128; loss = mean(out)."""
+@pytest.mark.parametrize("B,T", [(2, 128), (1, 1024)])
+def test_transformer_block(torch, B, T):
+    """Pre-LN block (d=768, 12 heads, causal, 4x GELU MLP); loss = mean(out);
+    at T=1024 the full per-sequence shape of the block workload."""
     from torchjs_amd import workloads as W
     r = np.random.default_rng(21)
     p = om.block_params(768, r, std=0.02)
-    x = r.standard_normal((2, 128, 768)).astype(np.float32)
+    x = r.standard_normal((B, T, 768)).astype(np.float32)
     blk = W.Block(768, 12)
     W.load_params(blk, p)
     tx = torch.tensor(x, requires_grad=True)
     loss = blk(tx).mean()
     loss.backward()
     ref, rg = om.block_loss_and_grads(p, x, 12)
-    check(loss.item(), ref, rtol=1e-4, atol=1e-6)
-    check(tx.grad.numpy(), rg["x"], rtol=1e-4, atol=1e-8)
+    check_red(loss.item(), ref, "loss")
+    check_red(tx.grad.numpy(), rg["x"], "x")
     for k, prm in blk.named_parameters():
-        scale = np.abs(rg[k]).max()
-        check(prm.grad.numpy(), rg[k], rtol=1e-3, atol=1e-4 * scale + 1e-9)
+        check_red(prm.grad.numpy(), rg[k], k)
 
 
 def test_gpt2_tiny_train_step(torch):
@@ -123,13 +142,47 @@ def test_gpt2_tiny_train_step(torch):
     ref, rg = om.gpt2_loss_and_grads(cfg, p, ids[:, :-1], ids[:, 1:])
     check(loss.item(), ref, rtol=1e-5, atol=1e-6)
     for k, prm in model.named_parameters():
-        scale = np.abs(rg[k]).max()
-        check(prm.grad.numpy(), rg[k], rtol=1e-3, atol=1e-4 * scale + 1e-9)
+        check_red(prm.grad.numpy(), rg[k], k)
     opt.step()
     new = om.adamw_step(p, {k: prm.grad.numpy() for k, prm in model.named_parameters()},
                         lr=6e-4, wd=0.1, step=1)
     for k, prm in model.named_parameters():
         check(prm.numpy(), new[k], rtol=0, atol=2e-7)
+
+
+def test_gpt2_124m_full_shape_against_oracle(torch):
+    """GPT-2 small itself (12 layers, 12 heads, d 768, vocab 50257, tied
+    embeddings) on a full 1024-token sequence: the loss, the logits'
+    gradient, every parameter's gradient (wte / wpe, every layer, ln_f) and
+    the AdamW(lr 6e-4, wd 0.1) step, against the float64 oracle at
+    north_star's tolerances."""
+    from torchjs_amd import workloads as W
+    cfg = om.Config()
+    r = np.random.default_rng(11)
+    p = om.init_params(cfg, r)
+    ids = r.integers(0, cfg.vocab, (1, cfg.ctx + 1)).astype(np.int32)
+    model = W.GPT2()
+    W.load_params(model, p)
+    logits = model(torch.tensor(ids[:, :-1]))
+    lv = logits.view(-1, cfg.vocab)
+    lv.retain_grad()
+    loss = torch.F.cross_entropy(lv, torch.tensor(ids[:, 1:]).reshape(-1))
+    loss.backward()
+    ref, rg, rdl = om.gpt2_loss_and_grads(cfg, p, ids[:, :-1], ids[:, 1:], return_dlogits=True)
+    check(loss.item(), ref, rtol=1e-5, atol=1e-6)
+    dl = lv.grad.numpy()
+    for rows in (slice(0, 4), slice(510, 514), slice(1020, 1024)):
+        check_red(dl[rows], rdl[rows], "dlogits")
+    grads = {k: prm.grad.numpy() for k, prm in model.named_parameters()}
+    for k in rg:
+        check_red(grads[k], rg[k], k)
+    torch.optim.AdamW(model.parameters(), lr=6e-4, weight_decay=0.1).step()
+    new = om.adamw_step({k: p[k] for k in ("wte.weight", "h.0.attn.c_attn.weight",
+                                          "h.11.mlp.c_proj.weight", "ln_f.bias")},
+                        grads, lr=6e-4, wd=0.1, step=1)
+    params = dict(model.named_parameters())
+    for k, v in new.items():
+        check(params[k].numpy(), v, rtol=0, atol=2e-7)
 
 
 def test_gpt2_full_shape_step_properties(torch):
