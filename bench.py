@@ -10,13 +10,21 @@ next-token cross_entropy; full backward; AdamW(lr 6e-4, wd 0.1).
 Prints ONE JSON line.  `value` = tokens/s over exactly K timed steps
 (inputs resident in HBM, device synchronised on both sides of the timed
 region).  `roofline` reports the dominant kernel family (the MFMA GEMMs of
-the Linear layers) from HIP events recorded on the library stream around
-each of its launches during the timed steps (no other launch is bracketed
-there); `roofline.traffic` is the HBM bytes per launch measured by
-rocprofv3 counters (profiles/gemm_hbm_traffic_gpt2.json).  `hbm_kernels`
-and `kernel_ms_per_step` come from an instrumented pass after the timed
-region that brackets every launch.  `cpu_baseline` times the oracle
-(numpy) on a bounded sample of the same workload on the host.
+the Linear layers) from the start / stop timestamps of each of its
+kernels' own dispatches (hipExtLaunchKernel events: no marker packets
+between launches) over K more steps right after the timed region, the
+same work (the timestamps cost ~10 us of issue time per launch, so they
+stay out of the region that gives `value`); `roofline.traffic` is the HBM bytes
+per launch measured by rocprofv3 counters
+(profiles/gemm_hbm_traffic_gpt2.json).  `hbm_kernels` and
+`kernel_ms_per_step` come from a pass after the timed region in which
+every kernel carries such timestamps (the sums are kernel execution time,
+as a kernel trace reports it).  `public_api` times the same model written
+with the public operators only (nn.Linear, F.gelu, `+`), which do not
+reach the fused GEMM epilogues.  `workloads` holds the four other
+configurations' lines (MLP, elementwise chain, CNN, transformer block).
+`cpu_baseline` times the oracle (numpy) on a bounded sample of the same
+workload on the host.
 
     python bench.py --config mlp|chain|cnn|block   # the other four workloads
     python bench.py --copy-mib 1024      # known-size copy for counter scaling
@@ -53,7 +61,7 @@ def linear_flops_per_step(b, t):
     return 3 * fwd
 
 
-def hbm_bytes_per_step(b, t, nparams):
+def hbm_bytes_per_step(b, t, nparams, distinct_ids):
     """Algorithmic HBM bytes (inputs read once + outputs written once) per
     step for the memory-bound backward kernel families."""
     tok = b * t
@@ -68,8 +76,12 @@ def hbm_bytes_per_step(b, t, nparams):
                           2 * LAYERS * tok * D * f,
         # AdamW: read p, g, m, v; write p, m, v
         "adam": 7 * nparams * f,
-        # embedding backward: read the dout rows, write the touched table rows
-        "embedding_bwd": 2 * (tok * D * f) + 2 * tok * 4,
+        # embedding backward, both tables: wte reads the token rows of dout
+        # and adds them into its distinct rows of the tied head gradient
+        # (read + write each); wpe reads the batch-summed [T, D] gradient
+        # and writes its T rows (read + write into the zeroed table); ids
+        "embedding_bwd": (tok * D * f + 2 * distinct_ids * D * f + tok * 4) +
+                         (t * D * f + 2 * t * D * f + t * 4),
     }
 
 
@@ -80,6 +92,7 @@ def run_gpu(steps, warmup):
     torch.init(0)
     torch.manual_seed(1234)
     model = W.GPT2(V, CTX, D, H, LAYERS)
+    print("gpt2: model built", file=sys.stderr, flush=True)
     with torch.no_grad():
         for name, p in model.named_parameters():
             if name.endswith(("ln_1.weight", "ln_2.weight")) or name == "ln_f.weight":
@@ -106,9 +119,9 @@ def run_gpu(steps, warmup):
         loss = step()
         print("warmup %d loss %.4f" % (i, loss.item()), file=sys.stderr, flush=True)
     torch.synchronize()
-    # timed region: only the dominant kernel family is bracketed by events
-    torch.hip.kernel_timing(True, only=DOMINANT)
-    torch.hip.kernel_timing_reset()
+    # timed region: K steps with no instrumentation (a timestamped dispatch
+    # costs ~10 us of issue time, 2.5% of a step when every GEMM carries one)
+    torch.hip.kernel_timing(False)
     torch.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps):
@@ -116,9 +129,15 @@ def run_gpu(steps, warmup):
     torch.synchronize()
     elapsed = time.perf_counter() - t0
     final_loss = loss.item()
+    # roofline pass: the same K steps again, the dominant family's kernels
+    # carrying their dispatch start / stop timestamps
+    torch.hip.kernel_timing(True, only=DOMINANT)
+    torch.hip.kernel_timing_reset()
+    for _ in range(steps):
+        step()
     dominant = torch.hip.kernel_time(DOMINANT)
-    # instrumented pass after the timed region: every family, for the
-    # per-kernel breakdown (events between all launches cost ~4% of a step)
+    # pass after the timed region with every kernel timestamped, for the
+    # per-family breakdown
     prof_steps = max(1, min(steps, 5))
     torch.hip.kernel_timing(True)
     torch.hip.kernel_timing_reset()
@@ -128,18 +147,68 @@ def run_gpu(steps, warmup):
     timing = {f: torch.hip.kernel_time(f) for f in fams}
     torch.hip.kernel_timing(False)
     mem = torch.hip.memory_stats()
-    return elapsed, final_loss, dominant, timing, prof_steps, nparams, mem
+    public = public_api_rate(torch, W, model, ids, tgt, min(steps, 5))
+    distinct = int(np.unique(toks[:, :-1]).size)
+    return elapsed, final_loss, dominant, timing, prof_steps, nparams, mem, public, distinct
+
+
+def public_api_rate(torch, W, fused_model, ids, tgt, steps):
+    """The same GPT-2 step with the model written in the public operators
+    only (nn.Linear, F.gelu, `+`): the GELU and residual adds run as their
+    own kernels instead of in the GEMM epilogues."""
+    model = W.GPT2(V, CTX, D, H, LAYERS, fused=False)
+    model.load_state_dict(fused_model.state_dict())
+    opt = torch.optim.AdamW(model.parameters(), lr=6e-4, weight_decay=0.1)
+
+    def step():
+        opt.zero_grad()
+        loss = model.loss(ids, tgt)
+        loss.backward()
+        opt.step()
+        return loss
+    for _ in range(2):
+        step()
+    torch.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.synchronize()
+    el = time.perf_counter() - t0
+    print("gpt2 public API: %.1f tokens/s" % (B * T * steps / el), file=sys.stderr, flush=True)
+    return {"value": round(B * T * steps / el, 1), "unit": "tokens/s", "steps": steps,
+            "ms_per_step": round(1000.0 * el / steps, 3),
+            "model": "GPT-2 124M from nn.Linear, F.gelu and `+` (no epilogue fusion)"}
+
+
+def _host():
+    """Host CPU facts for the CPU baseline."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except AttributeError:
+        avail = os.cpu_count() or 1
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+    except Exception:
+        threads = 1
+    return {"host_cores": os.cpu_count() or 1, "host_cores_available": avail, "cpu_model": model,
+            "threads_used": int(threads)}
 
 
 def cpu_baseline():
     """The oracle (numpy) on a bounded sample: GPT-2 small at B=1, T=1024,
     full 12 layers and vocabulary, fwd + bwd + AdamW."""
     from oracle import models as om
-    try:
-        from threadpoolctl import threadpool_info
-        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
-    except Exception:
-        threads = 1
+    host = _host()
     cfg = om.Config()
     r = np.random.default_rng(0)
     p = om.init_params(cfg, r)
@@ -149,9 +218,12 @@ def cpu_baseline():
     _, g = om.gpt2_loss_and_grads(cfg, p, ids[:, :-1], ids[:, 1:])
     om.adamw_step(p, g, lr=6e-4, wd=0.1, step=1)
     dt = time.perf_counter() - t0
-    return {"value": tb * tt / dt, "unit": "tokens/s", "cores": int(threads), "kind": "port",
-            "sample": "oracle (numpy float64) GPT-2 124M fwd+bwd+AdamW at B=1, T=1024 (1024 "
-                      "tokens, full 12 layers and 50257 vocab), %.1f s" % dt}
+    out = {"value": round(tb * tt / dt, 2), "unit": "tokens/s", "cores": host["threads_used"],
+           "kind": "port",
+           "sample": "oracle (numpy float64, multithreaded BLAS) GPT-2 124M fwd+bwd+AdamW at "
+                     "B=1, T=1024 (1024 tokens, full 12 layers and 50257 vocab), %.1f s" % dt}
+    out.update(host)
+    return out
 
 
 def traffic_per_launch():
@@ -192,6 +264,9 @@ CONFIGS = {
     "block": "pre-LN transformer block B=8 T=1024 d=768 12 heads causal, 4x GELU MLP, "
              "loss=mean, fwd+bwd",
 }
+
+# timed steps of each workload inside the default run (each well under a second)
+WORKLOAD_STEPS = {"mlp": 50, "chain": 20, "cnn": 20, "block": 10}
 
 # algorithmic work per step (the roofline numerators)
 MLP_FLOPS = 2 * 64 * (784 * 256 + 256 * 10) + 2 * 64 * (784 * 256 + 2 * 256 * 10)
@@ -338,6 +413,10 @@ def run_config(name, steps, warmup, cpu):
                                    "sample": "oracle (numpy float64) at B=1, T=256 (same code "
                                              "path, reduced sequence)"}
     out["kernel_ms_per_step"] = dict(list(per.items())[:10])
+    if "cpu_baseline" in out:
+        host = _host()
+        out["cpu_baseline"]["cores"] = host["threads_used"]
+        out["cpu_baseline"].update(host)
     return out
 
 
@@ -394,6 +473,8 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-workloads", action="store_true",
+                    help="skip the MLP / chain / CNN / block lines of the default run")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="only run the copy-kernel calibration of this many MiB")
     ap.add_argument("--config", default="gpt2", choices=["gpt2"] + sorted(CONFIGS),
@@ -415,8 +496,8 @@ def main():
         print(json.dumps(run_config(args.config, args.steps, args.warmup,
                                     not args.no_cpu_baseline)), flush=True)
         return
-    elapsed, final_loss, dominant, timing, prof_steps, nparams, mem = run_gpu(args.steps,
-                                                                              args.warmup)
+    elapsed, final_loss, dominant, timing, prof_steps, nparams, mem, public, distinct = run_gpu(
+        args.steps, args.warmup)
     tokens = B * T * args.steps
     ms_step = 1000.0 * elapsed / args.steps
     # dominant kernel: the Linear GEMMs (MFMA), timed inside the timed region
@@ -431,7 +512,7 @@ def main():
                 "flop_per_launch": round(flops / max(n_g, 1)),
                 "share_of_step": round(ms_g / (ms_step * args.steps), 3)}
     hbm = {}
-    for fam, byts in hbm_bytes_per_step(B, T, nparams).items():
+    for fam, byts in hbm_bytes_per_step(B, T, nparams, distinct).items():
         n, ms = timing.get(fam, (0, 0.0))
         if ms:
             gbs = byts * prof_steps / (ms / 1000.0) / 1e9
@@ -450,9 +531,16 @@ def main():
         "roofline": roofline, "hbm_kernels": hbm,
         "kernel_ms_per_step": {f: round(ms, 3) for ms, f in top},
         "final_loss": round(final_loss, 4), "peak_mem_GB": round(mem["peak_bytes"] / 1e9, 2),
+        "public_api": public,
     }
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline()
+    if not args.no_workloads:
+        out["workloads"] = {}
+        for name in ("mlp", "chain", "cnn", "block"):
+            print("workload %s" % name, file=sys.stderr, flush=True)
+            out["workloads"][name] = run_config(name, WORKLOAD_STEPS[name], 3,
+                                                not args.no_cpu_baseline)
     print(json.dumps(out), flush=True)
 
 

@@ -134,7 +134,7 @@ int tjh_sdpa_forward(const float* q, const float* k, const float* v, float* o, f
     int rc = gemm("sdpa.gemm", 0, 1, Tq, Tk, D, scale, q + b * qs[0], qs[2], qs[1], k + b * ks[0], ks[2],
                       ks[1], 0.f, s, Tk, Tq * Tk, H, nullptr, 0);
     if (rc != TJH_OK) return rc;
-    hipLaunchKernelGGL(k_attn_softmax, dim3((unsigned)cdiv(H * Tq, 4)), dim3(kBlock), 0, stream(),
+    tjh_launch(k_attn_softmax, dim3((unsigned)cdiv(H * Tq, 4)), dim3(kBlock), 0, stream(),
                        s, H * Tq, Tq, Tk, causal, lse + b * H * Tq);
     rc = check_launch("sdpa_softmax");
     if (rc != TJH_OK) return rc;
@@ -182,7 +182,7 @@ int tjh_sdpa_backward(const float* q, const float* k, const float* v, const floa
     int rc = gemm("sdpa.gemm", 0, 1, Tq, Tk, D, scale, qb, qs[2], qs[1], kb, ks[2], ks[1], 0.f, P, Tk,
                       Tq * Tk, H, nullptr, 0);
     if (rc != TJH_OK) return rc;
-    hipLaunchKernelGGL(k_attn_p, dim3(grows), dim3(kBlock), 0, stream(), P, H * Tq, Tq, Tk, causal,
+    tjh_launch(k_attn_p, dim3(grows), dim3(kBlock), 0, stream(), P, H * Tq, Tq, Tk, causal,
                        lse + b * H * Tq);
     if ((rc = check_launch("sdpa_p")) != TJH_OK) return rc;
     // dV = P^T dO
@@ -194,9 +194,9 @@ int tjh_sdpa_backward(const float* q, const float* k, const float* v, const floa
                   nullptr, 0);
     if (rc != TJH_OK) return rc;
     // D = rowsum(dO * O); dS = P * (dP - D) * scale
-    hipLaunchKernelGGL(k_attn_rowdot, dim3(grows), dim3(kBlock), 0, stream(), gb, ob, H, Tq, D,
+    tjh_launch(k_attn_rowdot, dim3(grows), dim3(kBlock), 0, stream(), gb, ob, H, Tq, D,
                        gs[1], gs[2], os[1], os[2], Dr);
-    hipLaunchKernelGGL(k_attn_ds, dim3(grows), dim3(kBlock), 0, stream(), P, dP, H * Tq, Tk, Dr,
+    tjh_launch(k_attn_ds, dim3(grows), dim3(kBlock), 0, stream(), P, dP, H * Tq, Tk, Dr,
                        scale);
     if ((rc = check_launch("sdpa_ds")) != TJH_OK) return rc;
     // dQ = dS K ; dK = dS^T Q

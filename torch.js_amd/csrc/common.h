@@ -3,6 +3,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 #include <stdint.h>
 #include <stddef.h>
 
@@ -29,14 +30,34 @@ int require_init();
 // Maps a HIP error to TJH_ERR_HIP with the call site in the message.
 int hip_fail(hipError_t e, const char* what);
 
-// Per-family launch timing.  `KernelScope` records a start event before
-// the launch and an end event after it when timing is enabled.
+// Per-family launch timing.  A `KernelScope` names the family of the
+// kernels launched while it is open and counts one call of that family;
+// when timing is enabled (tjh_kprof_enable) each kernel launched through
+// tjh_launch inside it carries a start / stop event pair on its own
+// dispatch (hipExtLaunchKernel), so the family's time is the sum of its
+// kernels' execution times, with no marker packets between launches.
 struct KernelScope {
   int slot;
-  void* start;  // hipEvent_t of the opening record
+  int prev;  // the enclosing scope's slot, restored on close
   explicit KernelScope(const char* family);
   ~KernelScope();
 };
+
+// Two timing events for the next kernel of the open scope, or false when
+// that kernel is not timed.
+bool launch_events(hipEvent_t* start, hipEvent_t* stop);
+
+// Launches a kernel on `s` (the library stream), timed by its dispatch
+// timestamps when the open KernelScope is being timed.
+template <typename... Args, typename F = void (*)(Args...)>
+inline void tjh_launch(F kernel, const dim3& grid, const dim3& block, uint32_t shmem,
+                       hipStream_t s, Args... args) {
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  if (launch_events(&e0, &e1))
+    hipExtLaunchKernelGGL(kernel, grid, block, shmem, s, e0, e1, 0, args...);
+  else
+    hipLaunchKernelGGL(kernel, grid, block, shmem, s, args...);
+}
 
 // Checks hipGetLastError after a launch; returns TJH_OK or TJH_ERR_HIP.
 int check_launch(const char* kernel);

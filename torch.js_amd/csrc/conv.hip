@@ -515,11 +515,11 @@ int choose_cfg(uint32_t M, uint32_t N) {
 template <int MODE>
 void launch_cfg(int cfg, const ConvArgs& a, dim3 grid) {
   if (cfg == 0)
-    hipLaunchKernelGGL((k_conv_igemm<MODE, 32, 128>), grid, dim3(kThreads), 0, stream(), a);
+    tjh_launch((k_conv_igemm<MODE, 32, 128>), grid, dim3(kThreads), 0, stream(), a);
   else if (cfg == 1)
-    hipLaunchKernelGGL((k_conv_igemm<MODE, 64, 64>), grid, dim3(kThreads), 0, stream(), a);
+    tjh_launch((k_conv_igemm<MODE, 64, 64>), grid, dim3(kThreads), 0, stream(), a);
   else
-    hipLaunchKernelGGL((k_conv_igemm<MODE, 128, 32>), grid, dim3(kThreads), 0, stream(), a);
+    tjh_launch((k_conv_igemm<MODE, 128, 32>), grid, dim3(kThreads), 0, stream(), a);
 }
 
 ConvArgs make_args(const tjh_conv2d_desc* d) {

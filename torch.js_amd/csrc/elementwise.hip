@@ -418,11 +418,11 @@ void launch_vec_kinds(const float* a, const float* b, const float* c, float* out
                       int64_t n, int64_t C, bool vec, F f) {
   if (vec) {
     int g = grid_for(cdiv(n, 4 * kUnroll));
-    hipLaunchKernelGGL((k_vec<NIN, KA, KB, KC, F>), dim3(g), dim3(kBlock), 0,
+    tjh_launch((k_vec<NIN, KA, KB, KC, F>), dim3(g), dim3(kBlock), 0,
                        stream(), a, b, c, out, (uint32_t)n, (uint32_t)C, f);
   } else {
     int g = grid_for(n);
-    hipLaunchKernelGGL((k_scalar1<NIN, KA, KB, KC, F>), dim3(g), dim3(kBlock), 0,
+    tjh_launch((k_scalar1<NIN, KA, KB, KC, F>), dim3(g), dim3(kBlock), 0,
                        stream(), a, b, c, out, (uint32_t)n, (uint32_t)C, f);
   }
 }
@@ -488,10 +488,10 @@ void launch_strided(const Layout& L, const float* a, const float* b,
   for (int o = 0; o <= NIN && small; ++o) small = max_offset(L, o) < (int64_t(1) << 31);
   int g = grid_for(n);
   if (small) {
-    hipLaunchKernelGGL((k_strided<NIN, uint32_t, F>), dim3(g), dim3(kBlock), 0,
+    tjh_launch((k_strided<NIN, uint32_t, F>), dim3(g), dim3(kBlock), 0,
                        stream(), a, b, c, out, L, (uint32_t)n, f);
   } else {
-    hipLaunchKernelGGL((k_strided<NIN, int64_t, F>), dim3(g), dim3(kBlock), 0,
+    tjh_launch((k_strided<NIN, int64_t, F>), dim3(g), dim3(kBlock), 0,
                        stream(), a, b, c, out, L, n, f);
   }
 }
@@ -657,10 +657,10 @@ int tjh_fill_f32(float* out, int64_t n, float value) {
   if (n == 0) return TJH_OK;
   KernelScope ks("fill");
   if (aligned16(out) && n % 4 == 0) {
-    hipLaunchKernelGGL(k_fill4, dim3(grid_for(cdiv(n / 4, kUnroll))), dim3(kBlock), 0, stream(),
+    tjh_launch(k_fill4, dim3(grid_for(cdiv(n / 4, kUnroll))), dim3(kBlock), 0, stream(),
                        reinterpret_cast<float4*>(out), n / 4, value);
   } else {
-    hipLaunchKernelGGL(k_fill<float>, dim3(grid_for(n)), dim3(kBlock), 0, stream(), out, n, value);
+    tjh_launch(k_fill<float>, dim3(grid_for(n)), dim3(kBlock), 0, stream(), out, n, value);
   }
   return check_launch("fill");
 }
@@ -670,7 +670,7 @@ int tjh_fill_i32(int32_t* out, int64_t n, int32_t value) {
   TJH_ARG(n >= 0 && (out || n == 0), "tjh_fill_i32: bad arguments");
   if (n == 0) return TJH_OK;
   KernelScope ks("fill");
-  hipLaunchKernelGGL(k_fill<int32_t>, dim3(grid_for(n)), dim3(kBlock), 0, stream(), out, n, value);
+  tjh_launch(k_fill<int32_t>, dim3(grid_for(n)), dim3(kBlock), 0, stream(), out, n, value);
   return check_launch("fill_i32");
 }
 
@@ -679,7 +679,7 @@ int tjh_random(float* out, int64_t n, uint32_t seed, int normal) {
   TJH_ARG(n >= 0 && (out || n == 0), "tjh_random: bad arguments");
   if (n == 0) return TJH_OK;
   KernelScope ks("random");
-  hipLaunchKernelGGL(k_random, dim3(grid_for(n)), dim3(kBlock), 0, stream(), out, n, seed, normal);
+  tjh_launch(k_random, dim3(grid_for(n)), dim3(kBlock), 0, stream(), out, n, seed, normal);
   return check_launch("random");
 }
 
@@ -702,7 +702,7 @@ int tjh_copy_strided_i32(int ndim, const int64_t* shape, const int32_t* src,
   int64_t n = make_layout(L, ndim, shape, 2, st);
   if (n == 0) return TJH_OK;
   KernelScope ks("copy_strided_i32");
-  hipLaunchKernelGGL(k_copy_i32, dim3(grid_for(n)), dim3(kBlock), 0, stream(), src, dst, L, n);
+  tjh_launch(k_copy_i32, dim3(grid_for(n)), dim3(kBlock), 0, stream(), src, dst, L, n);
   return check_launch("copy_strided_i32");
 }
 
@@ -710,7 +710,7 @@ int tjh_cast_f32_i32(const float* src, int32_t* dst, int64_t n) {
   TJH_REQUIRE_INIT();
   if (n <= 0) return TJH_OK;
   KernelScope ks("cast");
-  hipLaunchKernelGGL(k_f2i, dim3(grid_for(n)), dim3(kBlock), 0, stream(), src, dst, n);
+  tjh_launch(k_f2i, dim3(grid_for(n)), dim3(kBlock), 0, stream(), src, dst, n);
   return check_launch("cast_f32_i32");
 }
 
@@ -718,7 +718,7 @@ int tjh_cast_i32_f32(const int32_t* src, float* dst, int64_t n) {
   TJH_REQUIRE_INIT();
   if (n <= 0) return TJH_OK;
   KernelScope ks("cast");
-  hipLaunchKernelGGL(k_i2f, dim3(grid_for(n)), dim3(kBlock), 0, stream(), src, dst, n);
+  tjh_launch(k_i2f, dim3(grid_for(n)), dim3(kBlock), 0, stream(), src, dst, n);
   return check_launch("cast_i32_f32");
 }
 
@@ -831,7 +831,7 @@ int tjh_masked_fill(int ndim, const int64_t* shape, const float* x, const int64_
   int64_t n = make_layout(L, ndim, shape, 3, st);
   if (n == 0) return TJH_OK;
   KernelScope ks("masked_fill");
-  hipLaunchKernelGGL(k_masked_fill, dim3(grid_for(n)), dim3(kBlock), 0, stream(), x, mask, out, L,
+  tjh_launch(k_masked_fill, dim3(grid_for(n)), dim3(kBlock), 0, stream(), x, mask, out, L,
                      n, value);
   return check_launch("masked_fill");
 }

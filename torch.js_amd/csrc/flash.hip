@@ -711,9 +711,9 @@ int flash_forward(const float* q, const float* k, const float* v, float* o, floa
   TJH_ARG(grid < (int64_t(1) << 31), "sdpa: grid too large");
   KernelScope ks_("sdpa_fwd");
   if (Tk % TILE)
-    hipLaunchKernelGGL(k_flash_fwd<true>, dim3((unsigned)grid), dim3(256), 0, stream(), a);
+    tjh_launch(k_flash_fwd<true>, dim3((unsigned)grid), dim3(256), 0, stream(), a);
   else
-    hipLaunchKernelGGL(k_flash_fwd<false>, dim3((unsigned)grid), dim3(256), 0, stream(), a);
+    tjh_launch(k_flash_fwd<false>, dim3((unsigned)grid), dim3(256), 0, stream(), a);
   return check_launch("flash_forward");
 }
 
@@ -735,10 +735,10 @@ int flash_backward(const float* q, const float* k, const float* v, const float* 
   const bool v4 = aligned16(dout) && aligned16(o) && a.gs.b % 4 == 0 && a.gs.h % 4 == 0 &&
                   a.gs.t % 4 == 0 && a.os.b % 4 == 0 && a.os.h % 4 == 0 && a.os.t % 4 == 0;
   if (v4)
-    hipLaunchKernelGGL(k_flash_dsum4, dim3((unsigned)cdiv(rows, 16)), dim3(256), 0, stream(), a,
+    tjh_launch(k_flash_dsum4, dim3((unsigned)cdiv(rows, 16)), dim3(256), 0, stream(), a,
                        ds.as<float>(), rows);
   else
-    hipLaunchKernelGGL(k_flash_dsum, dim3((unsigned)cdiv(rows, 4)), dim3(256), 0, stream(), a,
+    tjh_launch(k_flash_dsum, dim3((unsigned)cdiv(rows, 4)), dim3(256), 0, stream(), a,
                        ds.as<float>(), rows);
   int rc = check_launch("flash_dsum");
   if (rc != TJH_OK) return rc;
@@ -757,9 +757,9 @@ int flash_backward(const float* q, const float* k, const float* v, const float* 
   a.out = dk; a.out2 = dv; a.o1s = s3(st[6]); a.o2s = s3(st[7]);
   const unsigned gk = (unsigned)(B * H * a.nblk);
   if (ragged)
-    hipLaunchKernelGGL(k_flash_dkv<true>, dim3(gk), dim3(256), 0, stream(), a);
+    tjh_launch(k_flash_dkv<true>, dim3(gk), dim3(256), 0, stream(), a);
   else
-    hipLaunchKernelGGL(k_flash_dkv<false>, dim3(gk), dim3(256), 0, stream(), a);
+    tjh_launch(k_flash_dkv<false>, dim3(gk), dim3(256), 0, stream(), a);
   rc = check_launch("flash_dkv");
   if (rc != TJH_OK) return rc;
   // queries: dQ from the stored dS blocks, or recomputed when the blocks
@@ -769,13 +769,13 @@ int flash_backward(const float* q, const float* k, const float* v, const float* 
   const unsigned gq = (unsigned)(B * H * a.nblk);
   if (a.dsblk) {
     if (Tk % TILE)
-      hipLaunchKernelGGL(k_flash_dq_ds8<true>, dim3(gq), dim3(512), 0, stream(), a);
+      tjh_launch(k_flash_dq_ds8<true>, dim3(gq), dim3(512), 0, stream(), a);
     else
-      hipLaunchKernelGGL(k_flash_dq_ds8<false>, dim3(gq), dim3(512), 0, stream(), a);
+      tjh_launch(k_flash_dq_ds8<false>, dim3(gq), dim3(512), 0, stream(), a);
   } else if (Tk % TILE) {
-    hipLaunchKernelGGL(k_flash_dq<true>, dim3(gq), dim3(256), 0, stream(), a);
+    tjh_launch(k_flash_dq<true>, dim3(gq), dim3(256), 0, stream(), a);
   } else {
-    hipLaunchKernelGGL(k_flash_dq<false>, dim3(gq), dim3(256), 0, stream(), a);
+    tjh_launch(k_flash_dq<false>, dim3(gq), dim3(256), 0, stream(), a);
   }
   return check_launch("flash_dq");
 }

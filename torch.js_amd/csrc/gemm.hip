@@ -537,13 +537,13 @@ Plan choose_plan(int64_t M, int64_t N, int64_t K, int64_t batch, int cus, int ta
 template <int BM, int BN, bool EDGE>
 void launch_e(const GemmArgs& g, dim3 grid, int ta, int tb) {
   if (!ta && !tb)
-    hipLaunchKernelGGL((k_gemm<BM, BN, false, false, EDGE>), grid, dim3(gemm_threads(BM)), 0, stream(), g);
+    tjh_launch((k_gemm<BM, BN, false, false, EDGE>), grid, dim3(gemm_threads(BM)), 0, stream(), g);
   else if (!ta && tb)
-    hipLaunchKernelGGL((k_gemm<BM, BN, false, true, EDGE>), grid, dim3(gemm_threads(BM)), 0, stream(), g);
+    tjh_launch((k_gemm<BM, BN, false, true, EDGE>), grid, dim3(gemm_threads(BM)), 0, stream(), g);
   else if (ta && !tb)
-    hipLaunchKernelGGL((k_gemm<BM, BN, true, false, EDGE>), grid, dim3(gemm_threads(BM)), 0, stream(), g);
+    tjh_launch((k_gemm<BM, BN, true, false, EDGE>), grid, dim3(gemm_threads(BM)), 0, stream(), g);
   else
-    hipLaunchKernelGGL((k_gemm<BM, BN, true, true, EDGE>), grid, dim3(gemm_threads(BM)), 0, stream(), g);
+    tjh_launch((k_gemm<BM, BN, true, true, EDGE>), grid, dim3(gemm_threads(BM)), 0, stream(), g);
 }
 
 template <int BM, int BN>
@@ -596,10 +596,10 @@ int run_block(int ti, GemmArgs g, int ta, int tb, int64_t splits, int64_t batch,
   int64_t blocks = cdiv(g.M * g.N / (vec ? 4 : 1), 256);
   if (blocks > 16LL * cus) blocks = 16LL * cus;
   if (vec)
-    hipLaunchKernelGGL(k_splitk_reduce<true>, dim3((unsigned)blocks, (unsigned)batch), dim3(256),
+    tjh_launch(k_splitk_reduce<true>, dim3((unsigned)blocks, (unsigned)batch), dim3(256),
                        0, stream(), g, (int)splits);
   else
-    hipLaunchKernelGGL(k_splitk_reduce<false>, dim3((unsigned)blocks, (unsigned)batch), dim3(256),
+    tjh_launch(k_splitk_reduce<false>, dim3((unsigned)blocks, (unsigned)batch), dim3(256),
                        0, stream(), g, (int)splits);
   return check_launch("gemm_splitk_reduce");
 }

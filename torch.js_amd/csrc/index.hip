@@ -58,35 +58,95 @@ __global__ __launch_bounds__(kBlock) void k_make_keys(const int32_t* __restrict_
   keys[i] = i < n ? (((uint64_t)clamp_id(ids[i], num)) << 32) | (uint64_t)i : ~0ull;
 }
 
-// Sorting the keys of a short index list by rank: key i lands at
-// #{j : key_j < key_i}.  Keys are distinct (the position is part of the
-// key), so the ranks are a permutation and the result is the sorted key
-// array, in one launch.  Here a key is packed in 32 bits as
-// clamp(id) * n + position (the caller checks num * n <= 2^32); all n of
-// them sit in LDS, padded to a multiple of 4 with 0xffffffff, which is
-// never below a key.  A workgroup ranks 16 keys; the 16 lanes of a key
-// split the comparisons and combine their counts with shuffles.
-constexpr int kRankMax = 16384;
-__global__ __launch_bounds__(256) void k_rank_keys(const int32_t* __restrict__ ids, int64_t n,
-                                                   int64_t num, uint64_t* __restrict__ keys) {
-  __shared__ __attribute__((aligned(16))) uint32_t sk[kRankMax];
-  const uint32_t nn = (uint32_t)n;
-  const int n4 = (int)((n + 3) >> 2);
-  for (int j = threadIdx.x; j < 4 * n4; j += 256)
-    sk[j] = j < n ? (uint32_t)clamp_id(ids[j], num) * nn + (uint32_t)j : 0xffffffffu;
+// Sorting a short index list in one workgroup: an LSD radix sort of
+// 32-bit keys clamp(id) << pos_bits | position, held in LDS, over the id
+// bits only, 8 bits per pass.  A pass is stable: each of the 16 waves owns
+// a contiguous block of positions; per-wave digit histograms are scanned in
+// (digit, wave) order, and each wave scatters its block in position order,
+// 64 keys at a time, a key's rank among same-digit lanes coming from
+// ballots.  So equal ids keep increasing positions (the summation order of
+// the backward) and the result is the same on every run.  n <= 16384 and
+// pos_bits + id bits <= 32 (vocabularies up to 2^18 at n = 16384).
+constexpr int kLdsSortMax = 16384;
+constexpr int kLdsSortThreads = 1024;
+constexpr int kLdsSortWaves = kLdsSortThreads / 64;
+
+__global__ __launch_bounds__(kLdsSortThreads) void k_sort_ids_lds(
+    const int32_t* __restrict__ ids, int n, int64_t num, int pos_bits, int passes,
+    uint64_t* __restrict__ keys_out) {
+  __shared__ uint32_t buf[2][kLdsSortMax];
+  __shared__ uint32_t hist[kLdsSortWaves][256];
+  __shared__ uint32_t wsum[kLdsSortWaves];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  for (int i = tid; i < n; i += kLdsSortThreads)
+    buf[0][i] = ((uint32_t)clamp_id(ids[i], num) << pos_bits) | (uint32_t)i;
+  // wave w owns positions [beg, end), a multiple of 64 long
+  const int per = ((n + kLdsSortWaves - 1) / kLdsSortWaves + 63) & ~63;
+  const int beg = w * per < n ? w * per : n;
+  const int end = beg + per < n ? beg + per : n;
+  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  int src = 0;
   __syncthreads();
-  const int64_t i = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
-  const int part = threadIdx.x & 15;
-  const uint32_t ki = i < n ? sk[i] : 0u;
-  uint32_t cnt = 0;
-  const uint4* s4 = reinterpret_cast<const uint4*>(sk);
-  for (int j = part; j < n4; j += 16) {
-    const uint4 v = s4[j];
-    cnt += (v.x < ki) + (v.y < ki) + (v.z < ki) + (v.w < ki);
-  }
+  for (int p = 0; p < passes; ++p) {
+    const int shift = pos_bits + 8 * p;
+    const uint32_t* a = buf[src];
+    uint32_t* b = buf[src ^ 1];
+    for (int d = lane; d < 256; d += 64) hist[w][d] = 0;
+    __syncthreads();
+    for (int e = beg + lane; e < end; e += 64) atomicAdd(&hist[w][(a[e] >> shift) & 255u], 1u);
+    __syncthreads();
+    // exclusive scan in (digit, wave) order: entry q = d * 16 + wave
+    uint32_t v[4], t = 0;
 #pragma unroll
-  for (int off = 8; off >= 1; off >>= 1) cnt += __shfl_xor(cnt, off, 16);
-  if (i < n && part == 0) keys[cnt] = ((uint64_t)(ki / nn) << 32) | (uint64_t)(ki % nn);
+    for (int k = 0; k < 4; ++k) {
+      const int q = 4 * tid + k;
+      v[k] = hist[q & (kLdsSortWaves - 1)][q >> 4];
+      t += v[k];
+    }
+    uint32_t incl = t;  // inclusive scan of the thread totals within the wave
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const uint32_t o = __shfl_up(incl, off, 64);
+      if (lane >= off) incl += o;
+    }
+    if (lane == 63) wsum[w] = incl;
+    __syncthreads();
+    uint32_t wbase = 0;
+    for (int k = 0; k < w; ++k) wbase += wsum[k];
+    uint32_t run = wbase + incl - t;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int q = 4 * tid + k;
+      hist[q & (kLdsSortWaves - 1)][q >> 4] = run;
+      run += v[k];
+    }
+    __syncthreads();
+    // stable scatter of the wave's block, 64 keys at a time, in order
+    for (int c = beg; c < end; c += 64) {
+      const int e = c + lane;
+      const bool valid = e < end;
+      const uint32_t key = valid ? a[e] : 0u;
+      const uint32_t d = (key >> shift) & 255u;
+      uint64_t peers = __ballot(valid);
+#pragma unroll
+      for (int bit = 0; bit < 8; ++bit) {
+        const uint64_t m = __ballot(valid && ((d >> bit) & 1u));
+        peers &= ((d >> bit) & 1u) ? m : ~m;
+      }
+      const uint32_t rank = (uint32_t)__popcll(peers & lt_mask);
+      const uint32_t base = valid ? hist[w][d] : 0u;
+      if (valid) b[base + rank] = key;
+      // the lowest peer advances the digit's cursor (every peer has read it)
+      if (valid && (peers & lt_mask) == 0) hist[w][d] = base + (uint32_t)__popcll(peers);
+    }
+    __syncthreads();
+    src ^= 1;
+  }
+  const uint32_t pmask = (1u << pos_bits) - 1u;
+  for (int i = tid; i < n; i += kLdsSortThreads) {
+    const uint32_t k = buf[src][i];
+    keys_out[i] = ((uint64_t)(k >> pos_bits) << 32) | (uint64_t)(k & pmask);
+  }
 }
 
 constexpr int kSortChunk = 2048;  // elements per LDS stage (1024 lanes x 2)
@@ -327,10 +387,10 @@ int tjh_embedding_forward(const float* weight, int64_t num, int64_t dim, const i
   unsigned g = (unsigned)cdiv(n, kBlock / 64);
   bool vec = dim % 4 == 0 && ((uintptr_t)weight & 15) == 0 && ((uintptr_t)out & 15) == 0;
   if (vec)
-    hipLaunchKernelGGL(k_emb_fwd<true>, dim3(g), dim3(kBlock), 0, stream(), weight, num, dim, ids,
+    tjh_launch(k_emb_fwd<true>, dim3(g), dim3(kBlock), 0, stream(), weight, num, dim, ids,
                        n, out);
   else
-    hipLaunchKernelGGL(k_emb_fwd<false>, dim3(g), dim3(kBlock), 0, stream(), weight, num, dim, ids,
+    tjh_launch(k_emb_fwd<false>, dim3(g), dim3(kBlock), 0, stream(), weight, num, dim, ids,
                        n, out);
   return check_launch("embedding_forward");
 }
@@ -345,30 +405,33 @@ int tjh_embedding_backward(const float* dout, const int32_t* ids, int64_t n, int
     if (rc != TJH_OK) return rc;
   }
   if (n == 0 || dim == 0) return TJH_OK;
-  // short lists (a batch of token positions) are sorted by rank in one
-  // launch; longer ones by the bitonic network
-  const bool by_rank = n <= kRankMax && (uint64_t)num * (uint64_t)n <= (1ull << 32);
+  // short lists (a batch of token positions) are radix-sorted in LDS by one
+  // workgroup; longer ones (or ids too wide to pack) by the bitonic network
+  int pos_bits = 1, id_bits = 1;
+  while ((int64_t(1) << pos_bits) < n) ++pos_bits;
+  while ((int64_t(1) << id_bits) < num) ++id_bits;
+  const bool lds_sort = n <= kLdsSortMax && pos_bits + id_bits <= 32;
   int64_t npad = 1;
   while (npad < n) npad <<= 1;
   if (npad < 2) npad = 2;
-  Scratch keys_s((size_t)(by_rank ? n : npad) * sizeof(uint64_t));
+  Scratch keys_s((size_t)(lds_sort ? n : npad) * sizeof(uint64_t));
   if (!keys_s.ok()) return set_error(TJH_ERR_OOM, "embedding_backward: no scratch");
   uint64_t* keys = keys_s.as<uint64_t>();
   KernelScope ks("embedding_bwd");
-  if (by_rank) {
-    hipLaunchKernelGGL(k_rank_keys, dim3((unsigned)cdiv(n, 16)), dim3(256), 0, stream(), ids, n,
-                       num, keys);
+  if (lds_sort) {
+    tjh_launch(k_sort_ids_lds, dim3(1), dim3(kLdsSortThreads), 0, stream(), ids, (int)n, num,
+               pos_bits, (id_bits + 7) / 8, keys);
   } else {
-    hipLaunchKernelGGL(k_make_keys, dim3((unsigned)cdiv(npad, kBlock)), dim3(kBlock), 0, stream(),
+    tjh_launch(k_make_keys, dim3((unsigned)cdiv(npad, kBlock)), dim3(kBlock), 0, stream(),
                        ids, n, num, npad, keys);
     unsigned chunks = (unsigned)cdiv(npad, kSortChunk);
-    hipLaunchKernelGGL(k_bitonic_local<true>, dim3(chunks), dim3(kSortThreads), 0, stream(), keys,
+    tjh_launch(k_bitonic_local<true>, dim3(chunks), dim3(kSortThreads), 0, stream(), keys,
                        npad, (int64_t)0);
     for (int64_t k = 2 * kSortChunk; k <= npad; k <<= 1) {
       for (int64_t j = k >> 1; j >= kSortChunk; j >>= 1)
-        hipLaunchKernelGGL(k_bitonic_global, dim3((unsigned)cdiv(npad / 2, kBlock)), dim3(kBlock),
+        tjh_launch(k_bitonic_global, dim3((unsigned)cdiv(npad / 2, kBlock)), dim3(kBlock),
                            0, stream(), keys, npad, k, j);
-      hipLaunchKernelGGL(k_bitonic_local<false>, dim3(chunks), dim3(kSortThreads), 0, stream(),
+      tjh_launch(k_bitonic_local<false>, dim3(chunks), dim3(kSortThreads), 0, stream(),
                          keys, npad, k);
     }
   }
@@ -377,10 +440,10 @@ int tjh_embedding_backward(const float* dout, const int32_t* ids, int64_t n, int
   bool vec = dim % 4 == 0 && ((uintptr_t)dout & 15) == 0 && ((uintptr_t)dweight & 15) == 0;
   unsigned g = (unsigned)cdiv(n, kBlock / 64);
   if (vec)
-    hipLaunchKernelGGL(k_emb_bwd_runs<true>, dim3(g), dim3(kBlock), 0, stream(), keys, n, dout, dim,
+    tjh_launch(k_emb_bwd_runs<true>, dim3(g), dim3(kBlock), 0, stream(), keys, n, dout, dim,
                        dweight, 1);
   else
-    hipLaunchKernelGGL(k_emb_bwd_runs<false>, dim3(g), dim3(kBlock), 0, stream(), keys, n, dout,
+    tjh_launch(k_emb_bwd_runs<false>, dim3(g), dim3(kBlock), 0, stream(), keys, n, dout,
                        dim, dweight, 1);
   return check_launch("embedding_backward");
 }
@@ -394,7 +457,7 @@ int tjh_index_select(const float* x, int64_t outer, int64_t src_len, int64_t inn
   KernelScope ks("index_select");
   int64_t g = cdiv(total, kBlock);
   if (g > 65536) g = 65536;
-  hipLaunchKernelGGL(k_index_select, dim3((unsigned)g), dim3(kBlock), 0, stream(), x, outer,
+  tjh_launch(k_index_select, dim3((unsigned)g), dim3(kBlock), 0, stream(), x, outer,
                      src_len, inner, idx, n_idx, out);
   return check_launch("index_select");
 }
@@ -408,7 +471,7 @@ int tjh_index_add(float* dx, int64_t outer, int64_t src_len, int64_t inner, cons
   KernelScope ks("index_add");
   int64_t g = cdiv(total, kBlock);
   if (g > 65536) g = 65536;
-  hipLaunchKernelGGL(k_index_add, dim3((unsigned)g), dim3(kBlock), 0, stream(), dx, outer, src_len,
+  tjh_launch(k_index_add, dim3((unsigned)g), dim3(kBlock), 0, stream(), dx, outer, src_len,
                      inner, idx, n_idx, dout);
   return check_launch("index_add");
 }
@@ -422,7 +485,7 @@ int tjh_gather(const float* x, int64_t outer, int64_t src_len, int64_t inner, co
   KernelScope ks("gather");
   int64_t g = cdiv(total, kBlock);
   if (g > 65536) g = 65536;
-  hipLaunchKernelGGL(k_gather, dim3((unsigned)g), dim3(kBlock), 0, stream(), x, outer, src_len,
+  tjh_launch(k_gather, dim3((unsigned)g), dim3(kBlock), 0, stream(), x, outer, src_len,
                      inner, idx, idx_len, out);
   return check_launch("gather");
 }
@@ -433,7 +496,7 @@ int tjh_scatter_add(float* dx, int64_t outer, int64_t dst_len, int64_t inner, co
   TJH_ARG(outer >= 0 && dst_len >= 0 && inner >= 0 && idx_len >= 0, "tjh_scatter_add: bad sizes");
   if (outer * inner == 0 || idx_len == 0) return TJH_OK;
   KernelScope ks("scatter_add");
-  hipLaunchKernelGGL(k_scatter_add, dim3((unsigned)cdiv(outer * inner, kBlock)), dim3(kBlock), 0,
+  tjh_launch(k_scatter_add, dim3((unsigned)cdiv(outer * inner, kBlock)), dim3(kBlock), 0,
                      stream(), dx, outer, dst_len, inner, idx, idx_len, src);
   return check_launch("scatter_add");
 }
@@ -445,7 +508,7 @@ int tjh_one_hot(const float* x, int64_t n, int64_t classes, float* out) {
   KernelScope ks("one_hot");
   int64_t g = cdiv(n * classes, kBlock);
   if (g > 65536) g = 65536;
-  hipLaunchKernelGGL(k_one_hot<float>, dim3((unsigned)g), dim3(kBlock), 0, stream(), x, n, classes,
+  tjh_launch(k_one_hot<float>, dim3((unsigned)g), dim3(kBlock), 0, stream(), x, n, classes,
                      out);
   return check_launch("one_hot");
 }
@@ -457,7 +520,7 @@ int tjh_one_hot_i32(const int32_t* x, int64_t n, int64_t classes, float* out) {
   KernelScope ks("one_hot");
   int64_t g = cdiv(n * classes, kBlock);
   if (g > 65536) g = 65536;
-  hipLaunchKernelGGL(k_one_hot<int32_t>, dim3((unsigned)g), dim3(kBlock), 0, stream(), x, n,
+  tjh_launch(k_one_hot<int32_t>, dim3((unsigned)g), dim3(kBlock), 0, stream(), x, n,
                      classes, out);
   return check_launch("one_hot_i32");
 }
@@ -479,7 +542,7 @@ int tjh_nonzero(const float* x, int ndim, const int64_t* shape, int32_t* out, in
   Scratch cs((size_t)chunks * sizeof(int64_t));
   if (!cs.ok()) return set_error(TJH_ERR_OOM, "nonzero: no scratch");
   KernelScope ks("nonzero");
-  hipLaunchKernelGGL(k_nz_count, dim3((unsigned)chunks), dim3(kBlock), 0, stream(), x, n,
+  tjh_launch(k_nz_count, dim3((unsigned)chunks), dim3(kBlock), 0, stream(), x, n,
                      cs.as<int64_t>());
   int rc = check_launch("nonzero_count");
   if (rc != TJH_OK) return rc;
@@ -502,7 +565,7 @@ int tjh_nonzero(const float* x, int ndim, const int64_t* shape, int32_t* out, in
     if (e == hipSuccess) e = hipStreamSynchronize(stream());
     delete[] hc;
     if (e != hipSuccess) return hip_fail(e, "nonzero offsets upload");
-    hipLaunchKernelGGL(k_nz_write, dim3((unsigned)chunks), dim3(64), 0, stream(), x, n, ndim, sh,
+    tjh_launch(k_nz_write, dim3((unsigned)chunks), dim3(64), 0, stream(), x, n, ndim, sh,
                        cs.as<int64_t>(), out, max_out);
     return check_launch("nonzero_write");
   }

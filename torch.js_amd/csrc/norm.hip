@@ -820,16 +820,16 @@ int ln_bwd_wave_launch(int v4, const float* dy, const float* x, const float* gam
                        float* pg, float* pb, int64_t rows, int64_t cols, int64_t rpb,
                        int64_t nb) {
   if (v4 == 3 && cols == 64 * 4 * 3)
-    hipLaunchKernelGGL((k_ln_bwd_wave<3, true>), dim3((unsigned)nb), dim3(kBlock), 0, stream(),
+    tjh_launch((k_ln_bwd_wave<3, true>), dim3((unsigned)nb), dim3(kBlock), 0, stream(),
                        dy, x, gamma, mean, rstd, res, dx, pg, pb, rows, cols, rpb);
   else if (v4 == 3)
-    hipLaunchKernelGGL((k_ln_bwd_wave<3, false>), dim3((unsigned)nb), dim3(kBlock), 0, stream(),
+    tjh_launch((k_ln_bwd_wave<3, false>), dim3((unsigned)nb), dim3(kBlock), 0, stream(),
                        dy, x, gamma, mean, rstd, res, dx, pg, pb, rows, cols, rpb);
   else if (v4 == 6)
-    hipLaunchKernelGGL((k_ln_bwd_wave<6, false>), dim3((unsigned)nb), dim3(kBlock), 0, stream(),
+    tjh_launch((k_ln_bwd_wave<6, false>), dim3((unsigned)nb), dim3(kBlock), 0, stream(),
                        dy, x, gamma, mean, rstd, res, dx, pg, pb, rows, cols, rpb);
   else
-    hipLaunchKernelGGL((k_ln_bwd_wave<12, false>), dim3((unsigned)nb), dim3(kBlock), 0, stream(),
+    tjh_launch((k_ln_bwd_wave<12, false>), dim3((unsigned)nb), dim3(kBlock), 0, stream(),
                        dy, x, gamma, mean, rstd, res, dx, pg, pb, rows, cols, rpb);
   return check_launch("layer_norm_backward");
 }
@@ -860,10 +860,10 @@ int tjh_softmax_forward(const float* x, int64_t ldx, float* y, int64_t ldy, int6
   if (rows == 0 || cols == 0) return TJH_OK;
   KernelScope ks(log ? "log_softmax_fwd" : "softmax_fwd");
   if (cols <= 2048) {
-    hipLaunchKernelGGL(k_softmax_fwd<true>, dim3((unsigned)cdiv(rows, 4)), dim3(kBlock), 0,
+    tjh_launch(k_softmax_fwd<true>, dim3((unsigned)cdiv(rows, 4)), dim3(kBlock), 0,
                        stream(), x, ldx, y, ldy, rows, cols, log);
   } else {
-    hipLaunchKernelGGL(k_softmax_fwd<false>, dim3((unsigned)rows), dim3(kBlock), 0, stream(), x,
+    tjh_launch(k_softmax_fwd<false>, dim3((unsigned)rows), dim3(kBlock), 0, stream(), x,
                        ldx, y, ldy, rows, cols, log);
   }
   return check_launch("softmax_forward");
@@ -876,10 +876,10 @@ int tjh_softmax_backward(const float* dy, const float* y, float* dx, int64_t row
   if (rows == 0 || cols == 0) return TJH_OK;
   KernelScope ks(log ? "log_softmax_bwd" : "softmax_bwd");
   if (cols <= 2048) {
-    hipLaunchKernelGGL(k_softmax_bwd<true>, dim3((unsigned)cdiv(rows, 4)), dim3(kBlock), 0,
+    tjh_launch(k_softmax_bwd<true>, dim3((unsigned)cdiv(rows, 4)), dim3(kBlock), 0,
                        stream(), dy, y, dx, rows, cols, log);
   } else {
-    hipLaunchKernelGGL(k_softmax_bwd<false>, dim3((unsigned)rows), dim3(kBlock), 0, stream(), dy,
+    tjh_launch(k_softmax_bwd<false>, dim3((unsigned)rows), dim3(kBlock), 0, stream(), dy,
                        y, dx, rows, cols, log);
   }
   return check_launch("softmax_backward");
@@ -903,25 +903,25 @@ int tjh_cross_entropy_forward(const float* logits, int64_t ld, const int32_t* ta
   {
     KernelScope ks("cross_entropy_fwd");
     if (gen && cols <= 2048)
-      hipLaunchKernelGGL(k_ce_fwd_gen<true>, dim3((unsigned)cdiv(rows, 4)), dim3(kBlock), 0,
+      tjh_launch(k_ce_fwd_gen<true>, dim3((unsigned)cdiv(rows, 4)), dim3(kBlock), 0,
                          stream(), logits, ld, targets, rows, cols, ignore_index, weight,
                          label_smoothing, lse, loss_rows);
     else if (gen)
-      hipLaunchKernelGGL(k_ce_fwd_gen<false>, dim3((unsigned)rows), dim3(kBlock), 0, stream(),
+      tjh_launch(k_ce_fwd_gen<false>, dim3((unsigned)rows), dim3(kBlock), 0, stream(),
                          logits, ld, targets, rows, cols, ignore_index, weight, label_smoothing,
                          lse, loss_rows);
     else if (cols <= 2048)
-      hipLaunchKernelGGL(k_ce_fwd<true>, dim3((unsigned)cdiv(rows, 4)), dim3(kBlock), 0, stream(),
+      tjh_launch(k_ce_fwd<true>, dim3((unsigned)cdiv(rows, 4)), dim3(kBlock), 0, stream(),
                          logits, ld, targets, rows, cols, ignore_index, lse, loss_rows);
     else
-      hipLaunchKernelGGL(k_ce_fwd<false>, dim3((unsigned)rows), dim3(kBlock), 0, stream(), logits,
+      tjh_launch(k_ce_fwd<false>, dim3((unsigned)rows), dim3(kBlock), 0, stream(), logits,
                          ld, targets, rows, cols, ignore_index, lse, loss_rows);
     int rc = check_launch("cross_entropy_forward");
     if (rc != TJH_OK) return rc;
   }
   if (reduction) {
     KernelScope ks("loss_reduce");
-    hipLaunchKernelGGL(k_loss_reduce, dim3(1), dim3(kBlock), 0, stream(), loss_rows, targets,
+    tjh_launch(k_loss_reduce, dim3(1), dim3(kBlock), 0, stream(), loss_rows, targets,
                        weight, rows, cols, ignore_index, reduction, out);
     return check_launch("loss_reduce");
   }
@@ -947,7 +947,7 @@ int tjh_cross_entropy_backward(const float* logits, int64_t ld, const int32_t* t
   if (mean || gen) {
     if (!cnt.ok()) return set_error(TJH_ERR_OOM, "cross_entropy_backward: no scratch");
     KernelScope ks("loss_reduce");
-    hipLaunchKernelGGL(k_count_valid, dim3(1), dim3(kBlock), 0, stream(), targets, rows, cols,
+    tjh_launch(k_count_valid, dim3(1), dim3(kBlock), 0, stream(), targets, rows, cols,
                        ignore_index, weight, reduction, mean ? cnt.as<float>() : nullptr,
                        gen ? cnt.as<float>() + 1 : nullptr);
     int rc = check_launch("count_valid");
@@ -956,17 +956,17 @@ int tjh_cross_entropy_backward(const float* logits, int64_t ld, const int32_t* t
   const float* count = mean ? cnt.as<float>() : nullptr;
   KernelScope ks("cross_entropy_bwd");
   if (gen && cols <= 2048)
-    hipLaunchKernelGGL(k_ce_bwd_gen<true>, dim3((unsigned)cdiv(rows, 4)), dim3(kBlock), 0,
+    tjh_launch(k_ce_bwd_gen<true>, dim3((unsigned)cdiv(rows, 4)), dim3(kBlock), 0,
                        stream(), logits, ld, targets, weight, label_smoothing, lse, grad_out,
                        count, cnt.as<float>() + 1, rows, cols, ignore_index, reduction, dlogits,
                        ldd, accumulate);
   else if (gen)
-    hipLaunchKernelGGL(k_ce_bwd_gen<false>, dim3((unsigned)rows), dim3(kBlock), 0, stream(),
+    tjh_launch(k_ce_bwd_gen<false>, dim3((unsigned)rows), dim3(kBlock), 0, stream(),
                        logits, ld, targets, weight, label_smoothing, lse, grad_out, count,
                        cnt.as<float>() + 1, rows, cols, ignore_index, reduction, dlogits, ldd,
                        accumulate);
   else if (cols <= 2048)
-    hipLaunchKernelGGL(k_ce_bwd<true>, dim3((unsigned)cdiv(rows, 4)), dim3(kBlock), 0, stream(),
+    tjh_launch(k_ce_bwd<true>, dim3((unsigned)cdiv(rows, 4)), dim3(kBlock), 0, stream(),
                        logits, ld, targets, lse, grad_out, count, rows, cols, ignore_index,
                        reduction, dlogits, ldd, accumulate);
   else if (ld == ldd && ld % 4 == 0 && aligned16(logits) && aligned16(dlogits) &&
@@ -974,11 +974,11 @@ int tjh_cross_entropy_backward(const float* logits, int64_t ld, const int32_t* t
     const int64_t total4 = rows * (ld / 4);
     const int64_t grid = cdiv(total4, (int64_t)kBlock * 4) < 16384 ? cdiv(total4, (int64_t)kBlock * 4)
                                                                    : 16384;
-    hipLaunchKernelGGL(k_ce_bwd_flat, dim3((unsigned)grid), dim3(kBlock), 0, stream(), logits,
+    tjh_launch(k_ce_bwd_flat, dim3((unsigned)grid), dim3(kBlock), 0, stream(), logits,
                        (uint32_t)(ld / 4), (uint32_t)total4, targets, lse, grad_out, count, cols,
                        ignore_index, reduction, dlogits, accumulate);
   } else
-    hipLaunchKernelGGL(k_ce_bwd<false>, dim3((unsigned)rows), dim3(kBlock), 0, stream(), logits,
+    tjh_launch(k_ce_bwd<false>, dim3((unsigned)rows), dim3(kBlock), 0, stream(), logits,
                        ld, targets, lse, grad_out, count, rows, cols, ignore_index, reduction,
                        dlogits, ldd, accumulate);
   return check_launch("cross_entropy_backward");
@@ -996,11 +996,11 @@ int tjh_nll_loss_forward(const float* logp, int64_t ld, const int32_t* targets, 
     return TJH_OK;
   }
   KernelScope ks("nll_loss_fwd");
-  hipLaunchKernelGGL(k_nll_fwd, dim3((unsigned)cdiv(rows, kBlock)), dim3(kBlock), 0, stream(),
+  tjh_launch(k_nll_fwd, dim3((unsigned)cdiv(rows, kBlock)), dim3(kBlock), 0, stream(),
                      logp, ld, targets, rows, cols, ignore_index, weight, loss_rows);
   int rc = check_launch("nll_loss_forward");
   if (rc != TJH_OK || !reduction) return rc;
-  hipLaunchKernelGGL(k_loss_reduce, dim3(1), dim3(kBlock), 0, stream(), loss_rows, targets,
+  tjh_launch(k_loss_reduce, dim3(1), dim3(kBlock), 0, stream(), loss_rows, targets,
                      weight, rows, cols, ignore_index, reduction, out);
   return check_launch("loss_reduce");
 }
@@ -1016,11 +1016,11 @@ int tjh_nll_loss_backward(const int32_t* targets, const float* weight, const flo
   Scratch cnt(mean ? sizeof(float) : 0);
   if (mean) {
     if (!cnt.ok()) return set_error(TJH_ERR_OOM, "nll_loss_backward: no scratch");
-    hipLaunchKernelGGL(k_count_valid, dim3(1), dim3(kBlock), 0, stream(), targets, rows, cols,
+    tjh_launch(k_count_valid, dim3(1), dim3(kBlock), 0, stream(), targets, rows, cols,
                        ignore_index, weight, reduction, cnt.as<float>(), nullptr);
   }
   KernelScope ks("nll_loss_bwd");
-  hipLaunchKernelGGL(k_nll_bwd, dim3((unsigned)cdiv(rows * cols, kBlock)), dim3(kBlock), 0,
+  tjh_launch(k_nll_bwd, dim3((unsigned)cdiv(rows * cols, kBlock)), dim3(kBlock), 0,
                      stream(), targets, weight, grad_out, cnt.as<float>(), rows, cols,
                      ignore_index, reduction, dlogp);
   return check_launch("nll_loss_backward");
@@ -1037,16 +1037,16 @@ int tjh_layer_norm_forward(const float* x, const float* gamma, const float* beta
              (!beta || aligned16(beta));
   unsigned g = (unsigned)cdiv(rows, 4);
   if (vec && cols == 64 * 4 * 3) {
-    hipLaunchKernelGGL((k_ln_fwd_wave<3, true>), dim3(g), dim3(kBlock), 0, stream(), x, gamma,
+    tjh_launch((k_ln_fwd_wave<3, true>), dim3(g), dim3(kBlock), 0, stream(), x, gamma,
                        beta, y, mean, rstd, rows, cols, eps);
   } else if (vec && cols <= 64 * 4 * 4) {
-    hipLaunchKernelGGL((k_ln_fwd_wave<4, false>), dim3(g), dim3(kBlock), 0, stream(), x, gamma,
+    tjh_launch((k_ln_fwd_wave<4, false>), dim3(g), dim3(kBlock), 0, stream(), x, gamma,
                        beta, y, mean, rstd, rows, cols, eps);
   } else if (vec && cols <= 64 * 4 * 16) {
-    hipLaunchKernelGGL((k_ln_fwd_wave<16, false>), dim3(g), dim3(kBlock), 0, stream(), x, gamma,
+    tjh_launch((k_ln_fwd_wave<16, false>), dim3(g), dim3(kBlock), 0, stream(), x, gamma,
                        beta, y, mean, rstd, rows, cols, eps);
   } else {
-    hipLaunchKernelGGL(k_ln_fwd_block, dim3((unsigned)rows), dim3(kBlock), 0, stream(), x, gamma,
+    tjh_launch(k_ln_fwd_block, dim3((unsigned)rows), dim3(kBlock), 0, stream(), x, gamma,
                        beta, y, mean, rstd, cols, eps);
   }
   return check_launch("layer_norm_forward");
@@ -1112,7 +1112,7 @@ int tjh_layer_norm_backward_res(const float* dy, const float* x, const float* ga
   float* pb = want_p ? part.as<float>() + rows * cols : nullptr;
   {
     KernelScope ks("layer_norm_bwd");
-    hipLaunchKernelGGL(k_ln_bwd_block, dim3((unsigned)rows), dim3(kBlock), 0, stream(), dy, x,
+    tjh_launch(k_ln_bwd_block, dim3((unsigned)rows), dim3(kBlock), 0, stream(), dy, x,
                        gamma, mean, rstd, res, dx, pg, pb, cols);
     int rc = check_launch("layer_norm_backward");
     if (rc != TJH_OK) return rc;

@@ -165,7 +165,7 @@ extern "C" int tjh_adam_step(int n_tensors, float* const* params, const float* c
     }
     if (B.count == 0) break;
     TJH_ARG(blocks < (int64_t(1) << 31), "tjh_adam_step: tensors too large");
-    hipLaunchKernelGGL(k_adam, dim3((unsigned)blocks), dim3(kBlock), 0, stream(), B);
+    tjh_launch(k_adam, dim3((unsigned)blocks), dim3(kBlock), 0, stream(), B);
     int rc = check_launch("adam_step");
     if (rc != TJH_OK) return rc;
   }

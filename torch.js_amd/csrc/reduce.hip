@@ -243,7 +243,7 @@ int reduce_rows(const float* x, int64_t outer, int64_t r, float* out, float scal
   int cus = num_cus() > 0 ? num_cus() : 256;
   if (r <= 4096 && outer >= 4) {
     int64_t g = cdiv(outer, kBlock / 64);
-    hipLaunchKernelGGL(k_reduce_rows_wave<OP>, dim3((unsigned)g), dim3(kBlock), 0, stream(), x,
+    tjh_launch(k_reduce_rows_wave<OP>, dim3((unsigned)g), dim3(kBlock), 0, stream(), x,
                        outer, r, out, scale);
     return check_launch("reduce_rows_wave");
   }
@@ -268,9 +268,9 @@ int reduce_rows(const float* x, int64_t outer, int64_t r, float* out, float scal
   dim3 grid((unsigned)outer, (unsigned)splits);
   float s1 = splits > 1 ? 1.0f : scale;
   if (vec)
-    hipLaunchKernelGGL((k_reduce_rows<OP, true>), grid, dim3(kBlock), 0, stream(), x, r, chunk, part, s1);
+    tjh_launch((k_reduce_rows<OP, true>), grid, dim3(kBlock), 0, stream(), x, r, chunk, part, s1);
   else
-    hipLaunchKernelGGL((k_reduce_rows<OP, false>), grid, dim3(kBlock), 0, stream(), x, r, chunk, part, s1);
+    tjh_launch((k_reduce_rows<OP, false>), grid, dim3(kBlock), 0, stream(), x, r, chunk, part, s1);
   int rc = check_launch("reduce_rows");
   if (rc != TJH_OK || splits == 1) return rc;
   return reduce_rows<OP>(part, outer, splits, out, scale);
@@ -293,10 +293,10 @@ int colsum_launch(const float* x, int64_t outer, int64_t r, int64_t inner, float
   if (!part.ok()) return set_error(TJH_ERR_OOM, "reduce: no scratch memory");
   dim3 grid((unsigned)nb, (unsigned)col_waves, (unsigned)outer);
   if (vec)
-    hipLaunchKernelGGL(k_colsum<true>, grid, dim3(kBlock), 0, stream(), x, r, inner, rchunk,
+    tjh_launch(k_colsum<true>, grid, dim3(kBlock), 0, stream(), x, r, inner, rchunk,
                        part.as<float>());
   else
-    hipLaunchKernelGGL(k_colsum<false>, grid, dim3(kBlock), 0, stream(), x, r, inner, rchunk,
+    tjh_launch(k_colsum<false>, grid, dim3(kBlock), 0, stream(), x, r, inner, rchunk,
                        part.as<float>());
   int rc = check_launch("reduce_colsum");
   if (rc != TJH_OK) return rc;
@@ -344,10 +344,10 @@ int reduce_cols(const float* x, int64_t outer, int64_t r, int64_t inner, float* 
   dim3 grid((unsigned)(gx * outer), (unsigned)splits);
   float s1 = splits > 1 ? 1.0f : scale;
   if (vec)
-    hipLaunchKernelGGL((k_reduce_cols<OP, true>), grid, dim3(kBlock), 0, stream(), x, r, inner,
+    tjh_launch((k_reduce_cols<OP, true>), grid, dim3(kBlock), 0, stream(), x, r, inner,
                        rchunk, gx, part, s1);
   else
-    hipLaunchKernelGGL((k_reduce_cols<OP, false>), grid, dim3(kBlock), 0, stream(), x, r, inner,
+    tjh_launch((k_reduce_cols<OP, false>), grid, dim3(kBlock), 0, stream(), x, r, inner,
                        rchunk, gx, part, s1);
   int rc = check_launch("reduce_cols");
   if (rc != TJH_OK || splits == 1) return rc;
@@ -431,7 +431,7 @@ int colsum_final(float* const* part, float* const* out, int np, int64_t nb, int6
     ++used;
   }
   if (used == 0) return TJH_OK;
-  hipLaunchKernelGGL(k_colsum_final, dim3((unsigned)cdiv(cols, 64), (unsigned)used),
+  tjh_launch(k_colsum_final, dim3((unsigned)cdiv(cols, 64), (unsigned)used),
                      dim3(64 * kFinalWaves), 0, stream(), fa, nb, cols, accumulate, scale);
   return check_launch("colsum_final");
 }
@@ -473,15 +473,15 @@ int tjh_argmax(const float* x, int64_t outer, int64_t r, int64_t inner, int is_m
   KernelScope ks("argmax");
   if (inner == 1) {
     if (is_min)
-      hipLaunchKernelGGL(k_argmax_rows<true>, dim3((unsigned)outer), dim3(kBlock), 0, stream(), x, r, out);
+      tjh_launch(k_argmax_rows<true>, dim3((unsigned)outer), dim3(kBlock), 0, stream(), x, r, out);
     else
-      hipLaunchKernelGGL(k_argmax_rows<false>, dim3((unsigned)outer), dim3(kBlock), 0, stream(), x, r, out);
+      tjh_launch(k_argmax_rows<false>, dim3((unsigned)outer), dim3(kBlock), 0, stream(), x, r, out);
   } else {
     unsigned g = (unsigned)cdiv(outer * inner, kBlock);
     if (is_min)
-      hipLaunchKernelGGL(k_argmax_cols<true>, dim3(g), dim3(kBlock), 0, stream(), x, outer, r, inner, out);
+      tjh_launch(k_argmax_cols<true>, dim3(g), dim3(kBlock), 0, stream(), x, outer, r, inner, out);
     else
-      hipLaunchKernelGGL(k_argmax_cols<false>, dim3(g), dim3(kBlock), 0, stream(), x, outer, r, inner, out);
+      tjh_launch(k_argmax_cols<false>, dim3(g), dim3(kBlock), 0, stream(), x, outer, r, inner, out);
   }
   return check_launch("argmax");
 }

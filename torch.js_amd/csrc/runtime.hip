@@ -225,38 +225,55 @@ void drain(Prof& P) {
 
 }  // namespace
 
-KernelScope::KernelScope(const char* family) : slot(-1), start(nullptr) {
+static thread_local int g_open_slot = -1;  // family of the open KernelScope (-1: untimed)
+
+KernelScope::KernelScope(const char* family) : slot(-1), prev(g_open_slot) {
   Prof& P = prof();
-  if (!P.on) return;
+  if (!P.on) {
+    g_open_slot = -1;
+    return;
+  }
   std::lock_guard<std::mutex> lk(P.mu);
-  if (!P.only.empty() && P.only != family) return;
+  if (!P.only.empty() && P.only != family) {
+    g_open_slot = -1;
+    return;
+  }
   auto it = P.index.find(family);
   if (it == P.index.end()) {
     P.fams.push_back(Family{family, {}, 0, 0.0});
     it = P.index.emplace(family, (int)P.fams.size() - 1).first;
   }
   slot = it->second;
-  hipEvent_t s = take_event(P);
-  if (!s) { slot = -1; return; }
-  (void)hipEventRecord(s, g_stream);
-  start = (void*)s;
+  P.fams[slot].launches++;
+  g_open_slot = slot;
 }
 
-KernelScope::~KernelScope() {
-  if (slot < 0) return;
+KernelScope::~KernelScope() { g_open_slot = prev; }
+
+bool launch_events(hipEvent_t* start, hipEvent_t* stop) {
+  if (g_open_slot < 0) return false;
   Prof& P = prof();
   std::lock_guard<std::mutex> lk(P.mu);
+  if (!P.on || g_open_slot >= (int)P.fams.size()) return false;
+  hipEvent_t s = take_event(P);
+  if (!s) return false;
   hipEvent_t e = take_event(P);
-  if (!e) return;
-  (void)hipEventRecord(e, g_stream);
-  Family& f = P.fams[slot];
-  f.pending.emplace_back((hipEvent_t)start, e);
-  f.launches++;
+  if (!e) {
+    P.spare.push_back(s);
+    return false;
+  }
+  Family& f = P.fams[g_open_slot];
+  f.pending.emplace_back(s, e);
   // keep the number of outstanding events bounded
   if (f.pending.size() > 4096) {
+    f.pending.pop_back();
     (void)hipStreamSynchronize(g_stream);
     drain(P);
+    f.pending.emplace_back(s, e);
   }
+  *start = s;
+  *stop = e;
+  return true;
 }
 
 // ---------------------------------------------------------------- readbacks

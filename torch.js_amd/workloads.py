@@ -36,15 +36,16 @@ class CNN(nn.Module):
 
 
 class CausalSelfAttention(nn.Module):
-    def __init__(self, d, heads):
+    def __init__(self, d, heads, fused=True):
         super().__init__()
-        self.d, self.heads = d, heads
+        self.d, self.heads, self.fused = d, heads, fused
         self.c_attn = nn.Linear(d, 3 * d)
         self.c_proj = nn.Linear(d, d)
 
     def forward(self, x, residual=None):
-        """attention(x), or residual + attention(x) with the add done by the
-        output projection's GEMM epilogue."""
+        """attention(x), or residual + attention(x) (with `fused`, the add is
+        done by the output projection's GEMM epilogue; without, it is the
+        public `+`)."""
         B, T, C = x.shape
         hd = C // self.heads
         q, k, v = self.c_attn(x).split(C, dim=2)
@@ -53,35 +54,44 @@ class CausalSelfAttention(nn.Module):
         v = v.view(B, T, self.heads, hd).transpose(1, 2)
         y = F.scaled_dot_product_attention(q, k, v, is_causal=True)
         y = y.transpose(1, 2).contiguous().view(B, T, C)
-        return F._linear_add(y, self.c_proj.weight, self.c_proj.bias, residual)
+        if self.fused:
+            return F._linear_add(y, self.c_proj.weight, self.c_proj.bias, residual)
+        out = self.c_proj(y)
+        return out if residual is None else residual + out
 
 
 class MLPBlock(nn.Module):
-    def __init__(self, d):
+    def __init__(self, d, fused=True):
         super().__init__()
+        self.fused = fused
         self.c_fc = nn.Linear(d, 4 * d)
         self.c_proj = nn.Linear(4 * d, d)
 
     def forward(self, x, residual=None):
-        # c_proj(gelu(c_fc(x))) (+ residual) with GELU and the add fused
-        # into the two GEMMs
-        return F._mlp_gelu(x, self.c_fc.weight, self.c_fc.bias, self.c_proj.weight,
-                           self.c_proj.bias, residual)
+        if self.fused:
+            # c_proj(gelu(c_fc(x))) (+ residual) with GELU and the add fused
+            # into the two GEMMs
+            return F._mlp_gelu(x, self.c_fc.weight, self.c_fc.bias, self.c_proj.weight,
+                               self.c_proj.bias, residual)
+        out = self.c_proj(F.gelu(self.c_fc(x)))
+        return out if residual is None else residual + out
 
 
 class Block(nn.Module):
-    """Pre-LayerNorm transformer block."""
+    """Pre-LayerNorm transformer block.  fused=False writes it with the
+    public operators only (nn.Linear, F.gelu, `+`), as a torch.js program
+    would; fused=True routes the GELU and the residual adds through the
+    GEMM epilogues (the same values, bit for bit)."""
 
-    def __init__(self, d, heads):
+    def __init__(self, d, heads, fused=True):
         super().__init__()
         self.ln_1 = nn.LayerNorm(d)
-        self.attn = CausalSelfAttention(d, heads)
+        self.attn = CausalSelfAttention(d, heads, fused)
         self.ln_2 = nn.LayerNorm(d)
-        self.mlp = MLPBlock(d)
+        self.mlp = MLPBlock(d, fused)
 
     def forward(self, x):
-        # x + attn(ln_1(x)), then x + mlp(ln_2(x)); each residual add runs in
-        # the epilogue of the branch's last GEMM
+        # x + attn(ln_1(x)), then x + mlp(ln_2(x))
         x = self.attn(self.ln_1(x), residual=x)
         return self.mlp(self.ln_2(x), residual=x)
 
@@ -89,12 +99,12 @@ class Block(nn.Module):
 class GPT2(nn.Module):
     """GPT-2 with the LM head tied to the token embedding."""
 
-    def __init__(self, vocab=50257, ctx=1024, d=768, heads=12, layers=12):
+    def __init__(self, vocab=50257, ctx=1024, d=768, heads=12, layers=12, fused=True):
         super().__init__()
         self.vocab, self.ctx = vocab, ctx
         self.wte = nn.Embedding(vocab, d)
         self.wpe = nn.Embedding(ctx, d)
-        self.h = nn.ModuleList([Block(d, heads) for _ in range(layers)])
+        self.h = nn.ModuleList([Block(d, heads, fused) for _ in range(layers)])
         self.ln_f = nn.LayerNorm(d)
 
     def forward(self, ids):
