@@ -169,6 +169,25 @@ int tjh_copy_strided_i32(int ndim, const int64_t* shape,
 /* float <-> int32 conversions (Tensor.to(dtype)); f2i truncates toward 0 */
 int tjh_cast_f32_i32(const float* src, int32_t* dst, int64_t n);
 int tjh_cast_i32_f32(const int32_t* src, float* dst, int64_t n);
+/* Element types of tjh_cast: float32, int32, uint8 and bool (one byte per
+ * element, 0 / 1) — the dtypes torch.js keeps (src/dtype.ts:7-15). */
+enum { TJH_DTYPE_F32 = 0, TJH_DTYPE_I32, TJH_DTYPE_U8, TJH_DTYPE_BOOL, TJH_DTYPE_COUNT };
+/* Tensor.to(dtype) / .bool() / .float() / .int() between any two of them:
+ * to bool is `!= 0`; float to an integer type truncates toward zero; to
+ * uint8 keeps the low 8 bits of that integer. */
+int tjh_cast(int src_dtype, int dst_dtype, const void* src, void* dst,
+             int64_t n);
+/* uint8 / bool fills and strided copies (masks, Tensor.bool()). */
+int tjh_fill_u8(uint8_t* out, int64_t n, uint8_t value);
+int tjh_copy_strided_u8(int ndim, const int64_t* shape,
+                        const uint8_t* src, const int64_t* src_strides,
+                        uint8_t* dst, const int64_t* dst_strides);
+/* Tensor.triu / tril (triu.wgsl, tril.wgsl) of `batch` contiguous
+ * [rows, cols] matrices: element (r, c) is kept when c - r >= diagonal
+ * (upper != 0) or c - r <= diagonal, else 0.  Also the backward (the
+ * same mask applied to the gradient). */
+int tjh_triangle(const float* x, float* out, int64_t batch, int64_t rows,
+                 int64_t cols, int64_t diagonal, int upper);
 
 /* ------------------------------------------------------------------ */
 /* Elementwise — elementwise.wgsl:5-31, broadcast.wgsl:28-175,          */
@@ -426,6 +445,19 @@ int tjh_one_hot_i32(const int32_t* x, int64_t n, int64_t classes,
  * (blocking), out [nnz, ndim] int32 must hold max_out rows. */
 int tjh_nonzero(const float* x, int ndim, const int64_t* shape,
                 int32_t* out, int64_t max_out, int64_t* count);
+
+/* Tensor.multinomial (src/tensor/Tensor.ts:271-359) on the device: out
+ * [rows, num_samples] int32 category indices drawn from each row of probs
+ * [rows, cols] (contiguous).  Row weights are max(0, x) (NaN as 0),
+ * normalised by their sum; a row summing to <= 0 samples uniformly.  With
+ * replacement, a draw u picks the first index whose running sum of the
+ * normalised weights exceeds u; without it, each draw renormalises over
+ * the indices not yet taken (num_samples <= cols, cols <= 2^18).  Draw s
+ * of row r uses the uniform of element r * num_samples + s of tjh_random
+ * with the same seed, so callers can replay every draw. */
+int tjh_multinomial(const float* probs, int64_t rows, int64_t cols,
+                    int64_t num_samples, int replacement, uint32_t seed,
+                    int32_t* out);
 
 /* ------------------------------------------------------------------ */
 /* Dense contractions — matmul.wgsl:17-50 / Tensor.matmul, bmm, Linear  */

@@ -639,3 +639,59 @@ def adam_step(p, g, m, v, step, lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_de
         pd *= 1.0 - lr * weight_decay
     pd -= upd
     return pd.astype(F32), m, v
+
+
+# ------------------------------------------------------------------ sampling
+
+
+def multinomial(x, num_samples, replacement, u):
+    """Tensor.multinomial (src/tensor/Tensor.ts:271-359) given the draws
+    u[row, s] in [0, 1): weights p = max(0, x) (NaN as 0), uniform when
+    their sum is not positive (Tensor.ts:331-339).  With replacement, the
+    first index whose running sum of p / sum exceeds u (the last index when
+    none does, Tensor.ts:344-356).  Without replacement, each draw picks
+    the first untaken index whose running sum of p exceeds u times the
+    untaken mass (the last untaken index when none does): the distribution
+    of the reference's redraw-until-new loop (Tensor.ts:331-343), one draw
+    per sample.  Float64 running sums, in index order."""
+    x = np.asarray(x, dtype=F64)
+    one = x.ndim == 1
+    x = np.atleast_2d(x)
+    u = np.asarray(u, dtype=F64).reshape(x.shape[0], num_samples)
+    rows, C = x.shape
+    out = np.zeros((rows, num_samples), dtype=np.int32)
+    for r in range(rows):
+        p = np.where(x[r] > 0, x[r], 0.0)
+        total = p.sum()
+        if not total > 0:
+            p = np.ones(C)
+            total = float(C)
+        taken = np.zeros(C, dtype=bool)
+        for s in range(num_samples):
+            if replacement:
+                c, idx = 0.0, C - 1
+                for i in range(C):
+                    c += p[i] / total
+                    if u[r, s] < c:
+                        idx = i
+                        break
+            else:
+                mass = 0.0
+                for i in range(C):
+                    if not taken[i]:
+                        mass += p[i]
+                target = u[r, s] * mass
+                c, idx = 0.0, -1
+                for i in range(C):
+                    if taken[i] or p[i] <= 0:
+                        continue
+                    c += p[i]
+                    if target < c:
+                        idx = i
+                        break
+                if idx < 0:
+                    idx = int(np.flatnonzero(~taken)[-1])
+                taken[idx] = True
+            out[r, s] = idx
+    return out[0] if one else out
+

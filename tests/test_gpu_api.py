@@ -307,3 +307,173 @@ def test_nn_init_seeded_and_bounded(torch):
     assert abs(init.calculate_gain("leaky_relu", 0.2) - math.sqrt(2 / 1.04)) < 1e-15
     with pytest.raises(ValueError):
         init.xavier_uniform_(torch.zeros(5))
+
+
+# ------------------------------------------------------------ dtypes, masks, triu / tril
+
+
+def test_casts_on_device(torch):
+    """Tensor.to / .bool() between float32, int32, uint8 and bool run on the
+    device: bool is `!= 0` (NaN included), float to integer truncates toward
+    zero, uint8 keeps the low 8 bits."""
+    x = np.array([-2.7, -0.0, 0.0, 0.4, 1.0, 3.9, 255.0, 300.5, np.nan], np.float32)
+    t = torch.tensor(x)
+    assert t.bool().numpy().tolist() == [1, 0, 0, 1, 1, 1, 1, 1, 1]
+    assert t.bool().dtype == "bool"
+    assert t[:8].int().numpy().tolist() == [-2, 0, 0, 0, 1, 3, 255, 300]
+    assert t[:8].to("uint8").numpy().tolist() == [254, 0, 0, 0, 1, 3, 255, 44]
+    i = torch.tensor(np.array([-1, 0, 7, 256], np.int32))
+    assert i.bool().numpy().tolist() == [1, 0, 1, 1]
+    assert i.to("uint8").numpy().tolist() == [255, 0, 7, 0]
+    assert i.float().numpy().tolist() == [-1.0, 0.0, 7.0, 256.0]
+    b = torch.tensor(np.array([[1, 0], [0, 1]], np.bool_))
+    assert b.dtype == "bool" and b.float().numpy().tolist() == [[1.0, 0.0], [0.0, 1.0]]
+    # a strided bool view copied on the device
+    assert b.T.contiguous().numpy().tolist() == [[1, 0], [0, 1]]
+    u = torch.zeros(5, dtype="uint8")
+    u.fill_(300)
+    assert u.numpy().tolist() == [44] * 5
+
+
+@pytest.mark.parametrize("diag", [-2, -1, 0, 1, 3])
+def test_triu_tril_forward_backward(torch, diag):
+    r = np.random.default_rng(60 + diag)
+    x = f32(r.standard_normal((2, 5, 7)))
+    g = f32(r.standard_normal((2, 5, 7)))
+    for upper, fn in ((True, np.triu), (False, np.tril)):
+        t = torch.tensor(x, requires_grad=True)
+        y = t.triu(diag) if upper else t.tril(diag)
+        assert np.array_equal(y.numpy(), fn(x, diag))
+        y.backward(torch.tensor(g))
+        assert np.array_equal(t.grad.numpy(), fn(g, diag))
+
+
+def test_gpt2_inference_ops_literal(torch):
+    """tests/gpt2.test.ts:24-100: a causal mask from ones.triu(1).bool(),
+    4-D batched Q @ K^T, masked_fill(mask, -1e9), softmax, probs @ V, and
+    the transpose / contiguous / reshape of the output, against numpy."""
+    r = np.random.default_rng(70)
+    B, H, T, hd = 1, 4, 8, 16
+    q = f32(r.standard_normal((B, H, T, hd)))
+    k = f32(r.standard_normal((B, H, hd, T)))
+    v = f32(r.standard_normal((B, H, T, hd)))
+    mask = torch.ones(T, T).triu(1).bool()
+    assert mask.shape == (T, T) and mask.dtype == "bool"
+    att = torch.tensor(q).matmul(torch.tensor(k)).mul(1.0 / np.sqrt(hd))
+    assert att.shape == (B, H, T, T)
+    probs = att.masked_fill(mask, -1e9).softmax(-1)
+    out = probs.matmul(torch.tensor(v))
+    s = (q.astype(np.float64) @ k) / np.sqrt(hd)
+    s = np.where(np.triu(np.ones((T, T)), 1) > 0, -1e9, s)
+    want = ops.softmax(s) @ v
+    check(out.numpy(), want, **RED)
+    o = out.transpose(1, 2).contiguous().reshape(B, T, H * hd)
+    assert o.shape == (B, T, H * hd)
+    check(o.numpy(), want.transpose(0, 2, 1, 3).reshape(B, T, H * hd), **RED)
+
+
+# ------------------------------------------------------------ sampling
+
+
+@pytest.mark.parametrize("rows,cols,ns,repl", [(1, 10, 1, False), (3, 1000, 7, True),
+                                               (2, 50257, 3, True), (4, 37, 37, False),
+                                               (5, 300, 20, False), (2, 9, 500, True)])
+def test_multinomial_replays_oracle(torch, rows, cols, ns, repl):
+    """The device sampler draws u from the seeded stream (element
+    r * num_samples + s of rand's generator, seed = the next LCG state):
+    replaying those u through the oracle gives the same indices."""
+    r = np.random.default_rng(rows * 1000 + cols + ns)
+    x = f32(r.random((rows, cols)) ** 3)
+    x[0, ::4] = 0.0
+    if rows > 2:
+        x[1] = -1.0  # no positive weight: uniform
+        x[2, 5] = np.nan  # counts as 0
+    torch.manual_seed(4321)
+    got = torch.tensor(x).multinomial(ns, repl).numpy()
+    seed = rng.lcg_next(4321)
+    u = rng.rand(rows * ns, seed).reshape(rows, ns)
+    want = ops.multinomial(np.nan_to_num(x, nan=0.0), ns, repl, u)
+    assert got.shape == (rows, ns) and got.dtype == np.int32
+    assert np.array_equal(got, want)
+    if not repl:
+        assert all(len(set(row)) == ns for row in got.tolist())
+
+
+def test_multinomial_literal_and_errors(torch):
+    """tests/gpt2.test.ts:123-131: softmax of 100 logits, one draw, an index
+    in [0, 100); and the reference's error without replacement."""
+    probs = torch.randn(100).softmax(0)
+    tok = probs.multinomial(1)
+    assert tok.shape == (1,) and 0 <= tok.item() < 100
+    with pytest.raises(RuntimeError):
+        torch.tensor([0.5, 0.5]).multinomial(3)
+
+
+# ------------------------------------------------------------ attention masks, KV cache
+
+
+@pytest.mark.parametrize("kind", ["bool", "float"])
+def test_sdpa_attn_mask(torch, kind):
+    """attn_mask (PyTorch's contract; torch.js throws): bool True attends,
+    float is added to the scores; gradients through the composite path."""
+    r = np.random.default_rng(80)
+    B, H, Tq, Tk, D = 2, 3, 5, 7, 16
+    q, k, v = (f32(r.standard_normal((B, H, t, D))) for t in (Tq, Tk, Tk))
+    if kind == "bool":
+        m = r.random((Tq, Tk)) > 0.3
+        m[:, 0] = True  # every query keeps one key
+        mt = torch.tensor(m)
+        add = np.where(m, 0.0, -np.inf)
+    else:
+        add = f32(r.standard_normal((Tq, Tk)))
+        mt = torch.tensor(add)
+    g = f32(r.standard_normal((B, H, Tq, D)))
+    ts = [torch.tensor(a, requires_grad=True) for a in (q, k, v)]
+    out = torch.F.scaled_dot_product_attention(*ts, attn_mask=mt)
+    out.backward(torch.tensor(g))
+    q64, k64, v64 = (a.astype(np.float64) for a in (q, k, v))
+    s = q64 @ k64.transpose(0, 1, 3, 2) / np.sqrt(D) + add
+    p = ops.softmax(s)
+    check(out.numpy(), p @ v64, **RED)
+    g64 = g.astype(np.float64)
+    dp = g64 @ v64.transpose(0, 1, 3, 2)
+    ds = p * (dp - (dp * p).sum(-1, keepdims=True)) / np.sqrt(D)
+    check(ts[0].grad.numpy(), ds @ k64, **RED)
+    check(ts[1].grad.numpy(), ds.transpose(0, 1, 3, 2) @ q64, **RED)
+    check(ts[2].grad.numpy(), p.transpose(0, 1, 3, 2) @ g64, **RED)
+
+
+def test_gpt2_kv_cache_matches_full_forward(torch):
+    """Decoding with the KV cache gives, at every new position, the logits of
+    the full forward over the whole sequence; generate() with a fixed seed
+    draws the tokens the oracle sampler picks from those logits."""
+    from oracle import models as om
+    from torchjs_amd import workloads as W
+    cfg = om.Config(vocab=211, ctx=64, d=128, heads=4, layers=2)
+    r = np.random.default_rng(90)
+    p = om.init_params(cfg, r, std=0.2)
+    model = W.GPT2(cfg.vocab, cfg.ctx, cfg.d, cfg.heads, cfg.layers)
+    W.load_params(model, p)
+    prompt = r.integers(0, cfg.vocab, (2, 9)).astype(np.int32)
+    torch.manual_seed(77)
+    seq = model.generate(torch.tensor(prompt), 12, temperature=0.8).numpy()
+    assert seq.shape == (2, 21) and np.array_equal(seq[:, :9], prompt)
+    with torch.no_grad():
+        full = model(torch.tensor(seq)).numpy()
+    # every sampled token replays through the oracle sampler on the full
+    # forward's probabilities at the previous position
+    s = 77
+    for j in range(12):
+        s = rng.lcg_next(s)
+        u = rng.rand(2, s).reshape(2, 1)
+        logits = full[:, 8 + j].astype(np.float64) / 0.8
+        want = ops.multinomial(ops.softmax(logits), 1, True, u)
+        assert np.array_equal(seq[:, 9 + j], want[:, 0]), j
+    # the cached decode's logits equal the full forward's
+    with torch.no_grad():
+        cache = model.new_cache(2, 21)
+        first = model.forward_cached(torch.tensor(seq[:, :9]), cache, 0).numpy()
+        check(first, full[:, :9], **RED)
+        for j in range(9, 21):
+            step = model.forward_cached(torch.tensor(seq[:, j:j + 1]), cache, j).numpy()
+            check(step[:, 0], full[:, j], **RED)

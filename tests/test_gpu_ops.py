@@ -702,10 +702,15 @@ def test_sdpa_self_attention_same_tensor(torch):
     check(gx, gq + gk + gv, **RED)
 
 
-def test_sdpa_attn_mask_raises(torch):
+def test_sdpa_attn_mask_errors(torch):
+    """attn_mask together with is_causal is refused (PyTorch's contract), and
+    a mask that does not broadcast against the scores raises."""
     q = torch.zeros(1, 1, 2, 4)
-    with pytest.raises(NotImplementedError, match="attn_mask not yet implemented"):
-        torch.F.scaled_dot_product_attention(q, q, q, attn_mask=q)
+    with pytest.raises(RuntimeError, match="either attn_mask or is_causal"):
+        torch.F.scaled_dot_product_attention(q, q, q, attn_mask=torch.ones(2, 2).bool(),
+                                             is_causal=True)
+    with pytest.raises(ValueError, match="not broadcastable"):
+        torch.F.scaled_dot_product_attention(q, q, q, attn_mask=torch.zeros(3, 5))
 
 
 # ------------------------------------------------------------------ conv

@@ -23,7 +23,8 @@ EXPORTS = ["init", "deviceInfo", "malloc", "h2d", "d2h", "d2hAsync", "synchroniz
            "castI32F32", "ternary", "powScalarBackward", "axpy", "maskedFill", "compare",
            "argmax", "nllLossForward", "nllLossBackward", "indexSelect", "indexAdd", "gather",
            "scatterAdd", "oneHot", "oneHotI32", "nonzero", "conv2dForward",
-           "conv2dBackwardInput", "conv2dBackwardWeight"]
+           "conv2dBackwardInput", "conv2dBackwardWeight", "cast", "fillU8", "copyStridedU8",
+           "triangle", "multinomial"]
 HEADER = os.path.join(ROOT, "include", "torchjs_hip.h")
 SOURCE = os.path.join(ROOT, "torch.js_amd", "node", "torchjs_hip_napi.c")
 

@@ -413,3 +413,53 @@ def test_rng_integer_streams():
     assert u.min() >= 0 and u.max() < 1 and abs(u.mean() - 0.5) < 0.05
     n = rng.randn(20000, 7)
     assert abs(n.mean()) < 0.05 and abs(n.std() - 1) < 0.05
+
+
+# ------------------------------------------------------------------ sampling
+
+
+def test_multinomial_inverse_cdf_against_searchsorted():
+    """With replacement the oracle is the inverse CDF of the normalised
+    weights: numpy's searchsorted on their cumulative sum (a library
+    routine) gives the same indices."""
+    r = np.random.default_rng(9)
+    x = r.random((4, 37))
+    x[1, ::3] = -1.0  # negative weights count as 0
+    u = r.random((4, 25))
+    got = ops.multinomial(x, 25, True, u)
+    for i in range(4):
+        p = np.where(x[i] > 0, x[i], 0.0)
+        want = np.searchsorted(np.cumsum(p / p.sum()), u[i], side="right")
+        assert np.array_equal(got[i], np.minimum(want, 36))
+
+
+def test_multinomial_closed_forms():
+    # a one-hot row always draws its index; an all-zero row is uniform:
+    # draw u lands in bucket floor(u * C)
+    u = np.array([[0.0, 0.3, 0.99999]])
+    assert ops.multinomial(np.eye(5)[3], 3, True, u).tolist() == [3, 3, 3]
+    assert ops.multinomial(np.zeros(4), 3, True, u).tolist() == [0, 1, 3]
+    # without replacement: distinct indices; all C of them is a permutation
+    r = np.random.default_rng(4)
+    x = r.random((3, 9))
+    perm = ops.multinomial(x, 9, False, r.random((3, 9)))
+    assert all(sorted(row) == list(range(9)) for row in perm.tolist())
+    # zero-weight categories come last without replacement
+    x = np.array([0.0, 2.0, 0.0, 1.0])
+    got = ops.multinomial(x, 4, False, np.array([0.1, 0.9, 0.5, 0.5]))
+    assert sorted(got[:2].tolist()) == [1, 3] and sorted(got[2:].tolist()) == [0, 2]
+    # the reference's literal test (tests/gpt2.test.ts:123-131): an index in [0, vocab)
+    p = ops.softmax(np.random.default_rng(1).standard_normal(100))
+    t = int(ops.multinomial(p, 1, False, np.array([0.42]))[0])
+    assert 0 <= t < 100
+
+
+def test_multinomial_distribution():
+    """Many draws reproduce the weights (chi-square, 5 dof, p ~ 1e-6 bound)."""
+    r = np.random.default_rng(2)
+    w = np.array([1.0, 2.0, 3.0, 0.5, 0.5, 3.0])
+    draws = ops.multinomial(w, 20000, True, r.random(20000))
+    cnt = np.bincount(draws, minlength=6)
+    exp = 20000 * w / w.sum()
+    assert ((cnt - exp) ** 2 / exp).sum() < 35.0
+

@@ -20,8 +20,8 @@ from . import _lib
 from . import autograd, functional, nn, optim
 from .tensor import (Tensor, arange, cat, chunk, enable_grad, from_numpy, full, full_like,
                      inference_mode, init, is_grad_enabled, is_initialized, manual_seed, matmul,
-                     no_grad, ones, ones_like, rand, randn, set_grad_enabled, split, stack,
-                     synchronize, tensor, zeros, zeros_like, empty)
+                     multinomial, no_grad, ones, ones_like, rand, randn, set_grad_enabled, split,
+                     stack, synchronize, tensor, tril, triu, zeros, zeros_like, empty)
 
 nn.functional = functional
 F = functional
@@ -29,8 +29,9 @@ F = functional
 __all__ = [
     "Tensor", "arange", "autograd", "cat", "chunk", "empty", "enable_grad", "from_numpy", "full",
     "full_like", "hip", "inference_mode", "init", "is_grad_enabled", "is_initialized",
-    "manual_seed", "matmul", "nn", "no_grad", "ones", "ones_like", "optim", "rand", "randn",
-    "set_grad_enabled", "split", "stack", "synchronize", "tensor", "zeros", "zeros_like",
+    "manual_seed", "matmul", "multinomial", "nn", "no_grad", "ones", "ones_like", "optim", "rand",
+    "randn", "set_grad_enabled", "split", "stack", "synchronize", "tensor", "tril", "triu",
+    "zeros", "zeros_like",
 ]
 
 

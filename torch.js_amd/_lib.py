@@ -134,6 +134,11 @@ SIGNATURES = {
     "tjh_conv2d_forward": [ctypes.POINTER(Conv2dDesc), c_vp, c_vp, c_vp, c_vp],
     "tjh_conv2d_backward_input": [ctypes.POINTER(Conv2dDesc), c_vp, c_vp, c_vp],
     "tjh_conv2d_backward_weight": [ctypes.POINTER(Conv2dDesc), c_vp, c_vp, c_vp, c_int],
+    "tjh_cast": [c_int, c_int, c_vp, c_vp, c_i64],
+    "tjh_fill_u8": [c_vp, c_i64, ctypes.c_uint8],
+    "tjh_copy_strided_u8": [c_int, P_i64, c_vp, P_i64, c_vp, P_i64],
+    "tjh_triangle": [c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_int],
+    "tjh_multinomial": [c_vp, c_i64, c_i64, c_i64, c_int, c_u32, c_vp],
     "tjh_adam_step": [c_int, ctypes.POINTER(c_vp), ctypes.POINTER(c_vp), ctypes.POINTER(c_vp),
                       ctypes.POINTER(c_vp), P_i64, P_i64, c_f64, c_f64, c_f64, c_f64, c_f64,
                       c_int],
@@ -150,6 +155,7 @@ TERNARY = {"div_b": 0, "pow_a": 1, "pow_b": 2, "mul3": 3}
 SCALAR = {"add": 0, "sub": 1, "mul": 2, "div": 3, "pow": 4, "maximum": 5, "minimum": 6}
 REDUCE = {"sum": 0, "mean": 1, "max": 2, "min": 3, "prod": 4}
 COMPARE = {"eq": 0, "ne": 1, "lt": 2, "le": 3, "gt": 4, "ge": 5}
+DTYPE = {"float32": 0, "int32": 1, "uint8": 2, "bool": 3}
 
 _lib = None
 _lock = threading.Lock()

@@ -584,11 +584,11 @@ __global__ __launch_bounds__(kBlock) void k_random(float* __restrict__ out, int6
   }
 }
 
-// ------------------------------------------------------------ int32 copies
+// ------------------------------------------------------------ int32 / uint8 copies
 
-__global__ __launch_bounds__(kBlock) void k_copy_i32(const int32_t* __restrict__ src,
-                                                     int32_t* __restrict__ dst, Layout L,
-                                                     int64_t n) {
+template <typename T>
+__global__ __launch_bounds__(kBlock) void k_copy_t(const T* __restrict__ src, T* __restrict__ dst,
+                                                   Layout L, int64_t n) {
   int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
     int64_t rem = i, so = 0, dof = 0;
@@ -599,6 +599,35 @@ __global__ __launch_bounds__(kBlock) void k_copy_i32(const int32_t* __restrict__
       so += coord * L.st[1][d];
     }
     dst[dof] = src[so];
+  }
+}
+
+// dtype conversions between float32, int32, uint8 and bool (stored as
+// uint8): to bool is `!= 0`; float to integer truncates toward zero; to
+// uint8 keeps the low 8 bits of that integer.
+template <typename S, typename D, bool TO_BOOL>
+__global__ __launch_bounds__(kBlock) void k_cast(const S* __restrict__ s, D* __restrict__ d,
+                                                 int64_t n) {
+  int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const S v = s[i];
+    if (TO_BOOL) d[i] = (D)(v != (S)0 ? 1 : 0);
+    else if (sizeof(D) == 1 && sizeof(S) == 4) d[i] = (D)(uint32_t)(int32_t)v;
+    else d[i] = (D)v;
+  }
+}
+
+// triu / tril of a batch of [rows, cols] matrices (contiguous): element
+// (r, c) is kept when c - r >= diagonal (upper) or c - r <= diagonal.
+__global__ __launch_bounds__(kBlock) void k_triangle(const float* __restrict__ x,
+                                                     float* __restrict__ out, int64_t n,
+                                                     int64_t rows, int64_t cols,
+                                                     int64_t diagonal, int upper) {
+  int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const int64_t c = i % cols, r = (i / cols) % rows;
+    const bool keep = upper ? (c - r >= diagonal) : (c - r <= diagonal);
+    out[i] = keep ? x[i] : 0.f;
   }
 }
 
@@ -702,8 +731,78 @@ int tjh_copy_strided_i32(int ndim, const int64_t* shape, const int32_t* src,
   int64_t n = make_layout(L, ndim, shape, 2, st);
   if (n == 0) return TJH_OK;
   KernelScope ks("copy_strided_i32");
-  tjh_launch(k_copy_i32, dim3(grid_for(n)), dim3(kBlock), 0, stream(), src, dst, L, n);
+  tjh_launch(k_copy_t<int32_t>, dim3(grid_for(n)), dim3(kBlock), 0, stream(), src, dst, L, n);
   return check_launch("copy_strided_i32");
+}
+
+int tjh_copy_strided_u8(int ndim, const int64_t* shape, const uint8_t* src,
+                        const int64_t* src_strides, uint8_t* dst, const int64_t* dst_strides) {
+  TJH_REQUIRE_INIT();
+  TJH_ARG(ndim >= 0 && ndim <= TJH_MAX_DIMS, "tjh_copy_strided_u8: ndim out of range");
+  int64_t one = 1, unit = 1;
+  if (ndim == 0) { shape = &one; src_strides = &unit; dst_strides = &unit; ndim = 1; }
+  const int64_t* st[2] = {dst_strides, src_strides};
+  Layout L;
+  int64_t n = make_layout(L, ndim, shape, 2, st);
+  if (n == 0) return TJH_OK;
+  KernelScope ks("copy_strided_u8");
+  tjh_launch(k_copy_t<uint8_t>, dim3(grid_for(n)), dim3(kBlock), 0, stream(), src, dst, L, n);
+  return check_launch("copy_strided_u8");
+}
+
+int tjh_fill_u8(uint8_t* out, int64_t n, uint8_t value) {
+  TJH_REQUIRE_INIT();
+  TJH_ARG(n >= 0 && (out || n == 0), "tjh_fill_u8: bad arguments");
+  if (n == 0) return TJH_OK;
+  KernelScope ks("fill");
+  tjh_launch(k_fill<uint8_t>, dim3(grid_for(n)), dim3(kBlock), 0, stream(), out, n, value);
+  return check_launch("fill_u8");
+}
+
+int tjh_cast(int src_dtype, int dst_dtype, const void* src, void* dst, int64_t n) {
+  TJH_REQUIRE_INIT();
+  TJH_ARG(src_dtype >= 0 && src_dtype < TJH_DTYPE_COUNT && dst_dtype >= 0 &&
+              dst_dtype < TJH_DTYPE_COUNT, "tjh_cast: unknown dtype %d -> %d", src_dtype,
+          dst_dtype);
+  TJH_ARG(n >= 0 && ((src && dst) || n == 0), "tjh_cast: bad arguments");
+  if (n == 0) return TJH_OK;
+  KernelScope ks("cast");
+  const dim3 g(grid_for(n)), b(kBlock);
+  const bool to_bool = dst_dtype == TJH_DTYPE_BOOL;
+  const int sk = src_dtype == TJH_DTYPE_BOOL ? TJH_DTYPE_U8 : src_dtype;
+  const int dk = to_bool ? TJH_DTYPE_U8 : dst_dtype;
+  const float* sf = static_cast<const float*>(src);
+  const int32_t* si = static_cast<const int32_t*>(src);
+  const uint8_t* su = static_cast<const uint8_t*>(src);
+  float* df = static_cast<float*>(dst);
+  int32_t* di = static_cast<int32_t*>(dst);
+  uint8_t* du = static_cast<uint8_t*>(dst);
+  if (sk == TJH_DTYPE_F32 && dk == TJH_DTYPE_F32) tjh_launch(k_cast<float, float, false>, g, b, 0, stream(), sf, df, n);
+  else if (sk == TJH_DTYPE_F32 && dk == TJH_DTYPE_I32) tjh_launch(k_cast<float, int32_t, false>, g, b, 0, stream(), sf, di, n);
+  else if (sk == TJH_DTYPE_F32 && to_bool) tjh_launch(k_cast<float, uint8_t, true>, g, b, 0, stream(), sf, du, n);
+  else if (sk == TJH_DTYPE_F32) tjh_launch(k_cast<float, uint8_t, false>, g, b, 0, stream(), sf, du, n);
+  else if (sk == TJH_DTYPE_I32 && dk == TJH_DTYPE_F32) tjh_launch(k_cast<int32_t, float, false>, g, b, 0, stream(), si, df, n);
+  else if (sk == TJH_DTYPE_I32 && dk == TJH_DTYPE_I32) tjh_launch(k_cast<int32_t, int32_t, false>, g, b, 0, stream(), si, di, n);
+  else if (sk == TJH_DTYPE_I32 && to_bool) tjh_launch(k_cast<int32_t, uint8_t, true>, g, b, 0, stream(), si, du, n);
+  else if (sk == TJH_DTYPE_I32) tjh_launch(k_cast<int32_t, uint8_t, false>, g, b, 0, stream(), si, du, n);
+  else if (dk == TJH_DTYPE_F32) tjh_launch(k_cast<uint8_t, float, false>, g, b, 0, stream(), su, df, n);
+  else if (dk == TJH_DTYPE_I32) tjh_launch(k_cast<uint8_t, int32_t, false>, g, b, 0, stream(), su, di, n);
+  else if (to_bool) tjh_launch(k_cast<uint8_t, uint8_t, true>, g, b, 0, stream(), su, du, n);
+  else tjh_launch(k_cast<uint8_t, uint8_t, false>, g, b, 0, stream(), su, du, n);
+  return check_launch("cast");
+}
+
+int tjh_triangle(const float* x, float* out, int64_t batch, int64_t rows, int64_t cols,
+                 int64_t diagonal, int upper) {
+  TJH_REQUIRE_INIT();
+  TJH_ARG(batch >= 0 && rows >= 0 && cols >= 0, "tjh_triangle: bad sizes");
+  const int64_t n = batch * rows * cols;
+  if (n == 0) return TJH_OK;
+  TJH_ARG(x && out, "tjh_triangle: NULL pointer");
+  KernelScope ks("triangle");
+  tjh_launch(k_triangle, dim3(grid_for(n)), dim3(kBlock), 0, stream(), x, out, n, rows, cols,
+             diagonal, upper);
+  return check_launch("triangle");
 }
 
 int tjh_cast_f32_i32(const float* src, int32_t* dst, int64_t n) {

@@ -551,13 +551,20 @@ def _bhtd(t):
 
 def scaled_dot_product_attention(query, key, value, attn_mask=None, dropout_p=0.0,
                                  is_causal=False, scale=None):
-    """softmax(Q K^T * scale [causal]) V (src/nn/functional.ts:866-890).
-    torch.js ignores is_causal and throws on attn_mask; the causal mask is
-    implemented here, attn_mask still raises.  The output is laid out
-    [B, T, H, D] in memory and returned as a [B, H, T, D] view, so the usual
-    transpose(1, 2) that follows is free."""
+    """softmax(Q K^T * scale [causal] [mask]) V (src/nn/functional.ts:866-890).
+    torch.js ignores is_causal and throws on attn_mask; both follow
+    PyTorch's contract here.  Without a mask the flash kernels run (O(T)
+    memory); the output is laid out [B, T, H, D] in memory and returned as
+    a [B, H, T, D] view, so the usual transpose(1, 2) that follows is free.
+    With attn_mask (bool: True takes part in attention; float: added to
+    the scores, broadcast over the leading dims) the scores are formed
+    explicitly from the library's batched GEMM, masked and softmaxed, so
+    autograd runs through those ops."""
     if attn_mask is not None:
-        raise NotImplementedError("scaled_dot_product_attention: attn_mask not yet implemented")
+        if is_causal:
+            raise RuntimeError("scaled_dot_product_attention: pass either attn_mask or "
+                               "is_causal, not both")
+        return _sdpa_masked(query, key, value, attn_mask, scale)
     if dropout_p:
         raise NotImplementedError("scaled_dot_product_attention: dropout is not on the hip path")
     three = query.ndim == 3
@@ -634,6 +641,27 @@ def scaled_dot_product_attention(query, key, value, attn_mask=None, dropout_p=0.
     if three:
         out = _alias(ob, (B, Tq, D), (Tq * D, D, 1), 0)
     return _record(out, "SDPA", [query, key, value], bwd)
+
+
+def _sdpa_masked(query, key, value, attn_mask, scale):
+    """SDPA with an explicit mask from differentiable ops: scores = Q K^T *
+    scale (batched GEMM), then masked_fill(-inf) where a bool mask is False
+    or + a float mask, softmax over keys, times V."""
+    from .tensor import compare_raw, masked_fill as _masked_fill, matmul as _matmul
+    D = query.shape[-1]
+    sc = float(scale) if scale is not None else 1.0 / math.sqrt(D)
+    kt = key.transpose(-2, -1)
+    scores = mul(_matmul(query, kt), sc)
+    m = attn_mask
+    if not isinstance(m, Tensor):
+        from .tensor import tensor as _tensor
+        m = _tensor(np.asarray(m))
+    if m.dtype in ("bool", "uint8"):
+        drop = compare_raw(m.float(), 0.0, "eq")  # 1 where the key is masked out
+        scores = _masked_fill(scores, drop, float("-inf"))
+    else:
+        scores = scores + m.float() if m.dtype != "float32" else scores + m
+    return _matmul(softmax(scores, -1), value)
 
 
 # ------------------------------------------------------------ one_hot

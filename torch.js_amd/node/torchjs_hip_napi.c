@@ -842,6 +842,49 @@ static napi_value js_nll_backward(napi_env env, napi_callback_info info) {
                                  F32(a[7])));
   return undef(env);
 }
+/* cast(srcDtype, dstDtype, src, dst, n): dtypes 0 f32, 1 i32, 2 u8, 3 bool */
+static napi_value js_cast(napi_env env, napi_callback_info info) {
+  napi_value a[5];
+  if (!get_args(env, info, 5, a)) return NULL;
+  CHECK_RC(tjh_cast((int)i64(env, a[0]), (int)i64(env, a[1]), ptr(env, a[2]), ptr(env, a[3]),
+                    i64(env, a[4])));
+  return undef(env);
+}
+/* fillU8(ptr, n, value) */
+static napi_value js_fill_u8(napi_env env, napi_callback_info info) {
+  napi_value a[3];
+  if (!get_args(env, info, 3, a)) return NULL;
+  CHECK_RC(tjh_fill_u8((uint8_t*)ptr(env, a[0]), i64(env, a[1]), (uint8_t)i64(env, a[2])));
+  return undef(env);
+}
+/* copyStridedU8(shape, src, srcStrides, dst, dstStrides) */
+static napi_value js_copy_strided_u8(napi_env env, napi_callback_info info) {
+  napi_value a[5];
+  int64_t shape[TJH_MAX_DIMS], ss[TJH_MAX_DIMS], ds[TJH_MAX_DIMS];
+  if (!get_args(env, info, 5, a)) return NULL;
+  int nd = i64arr(env, a[0], shape, TJH_MAX_DIMS);
+  i64arr(env, a[2], ss, TJH_MAX_DIMS);
+  i64arr(env, a[4], ds, TJH_MAX_DIMS);
+  CHECK_RC(tjh_copy_strided_u8(nd, shape, (const uint8_t*)ptr(env, a[1]), ss,
+                               (uint8_t*)ptr(env, a[3]), ds));
+  return undef(env);
+}
+/* triangle(x, out, batch, rows, cols, diagonal, upper) */
+static napi_value js_triangle(napi_env env, napi_callback_info info) {
+  napi_value a[7];
+  if (!get_args(env, info, 7, a)) return NULL;
+  CHECK_RC(tjh_triangle(CF32(a[0]), F32(a[1]), i64(env, a[2]), i64(env, a[3]), i64(env, a[4]),
+                        i64(env, a[5]), (int)i64(env, a[6])));
+  return undef(env);
+}
+/* multinomial(probs, rows, cols, numSamples, replacement, seed, out) */
+static napi_value js_multinomial(napi_env env, napi_callback_info info) {
+  napi_value a[7];
+  if (!get_args(env, info, 7, a)) return NULL;
+  CHECK_RC(tjh_multinomial(CF32(a[0]), i64(env, a[1]), i64(env, a[2]), i64(env, a[3]),
+                           (int)i64(env, a[4]), (uint32_t)i64(env, a[5]), I32(a[6])));
+  return undef(env);
+}
 /* indexSelect(x, outer, srcLen, inner, idx, nIdx, out) */
 static napi_value js_index_select(napi_env env, napi_callback_info info) {
   napi_value a[7];
@@ -971,6 +1014,8 @@ static napi_value init_module(napi_env env, napi_value exports) {
       FN("nonzero", js_nonzero), FN("conv2dForward", js_conv_forward),
       FN("conv2dBackwardInput", js_conv_backward_input),
       FN("conv2dBackwardWeight", js_conv_backward_weight),
+      FN("cast", js_cast), FN("fillU8", js_fill_u8), FN("copyStridedU8", js_copy_strided_u8),
+      FN("triangle", js_triangle), FN("multinomial", js_multinomial),
   };
   napi_define_properties(env, exports, sizeof(desc) / sizeof(desc[0]), desc);
   napi_value v;

@@ -427,6 +427,9 @@ class Tensor:
             return self
         return _k_cast(self, dt)
 
+    def bool(self):
+        return self.to("bool")
+
     def float(self):
         return self.to("float32")
 
@@ -563,6 +566,15 @@ class Tensor:
 
     def argmax(self, dim=None, keepdim=False):
         return argmax(self, dim, keepdim)
+
+    def triu(self, diagonal=0):
+        return triangle(self, diagonal, True)
+
+    def tril(self, diagonal=0):
+        return triangle(self, diagonal, False)
+
+    def multinomial(self, num_samples=1, replacement=False):
+        return multinomial(self, num_samples, replacement)
 
     def clamp(self, min=None, max=None):
         return clamp(self, min, max)
@@ -716,8 +728,8 @@ def _fill_view(t, value):
         elif t._dtype == "int32":
             L.check(lib.tjh_fill_i32(t.data_ptr(), t.numel(), int(value)), "fill")
         else:
-            tmp = np.full(t._shape, value, dtype=np.uint8)
-            L.check(lib.tjh_h2d(t.data_ptr(), tmp.ctypes.data, tmp.nbytes), "h2d")
+            v = (1 if value else 0) if t._dtype == "bool" else int(value) & 0xFF
+            L.check(lib.tjh_fill_u8(t.data_ptr(), t.numel(), v), "fill")
         return
     src = full((1,), value, dtype=t._dtype).expand(t._shape)
     _copy_into(t, src)
@@ -870,24 +882,17 @@ def _copy_into(dst, src):
         L.check(lib.tjh_copy_strided_i32(nd, shp, src.data_ptr(), L.i64arr(src._strides),
                                          dst.data_ptr(), L.i64arr(dst._strides)), "copy")
     else:
-        a = src.numpy()
-        if not dst.is_contiguous():
-            raise RuntimeError("strided uint8 copies are not supported")
-        L.check(lib.tjh_h2d(dst.data_ptr(), np.ascontiguousarray(a).ctypes.data, a.nbytes), "h2d")
+        L.check(lib.tjh_copy_strided_u8(nd, shp, src.data_ptr(), L.i64arr(src._strides),
+                                        dst.data_ptr(), L.i64arr(dst._strides)), "copy")
 
 
 def _k_cast(x, dtype):
+    """Tensor.to(dtype) on the device (float32 / int32 / uint8 / bool)."""
     x = x.contiguous()
     out = empty(x._shape, dtype)
-    n = x.numel()
-    lib = L.lib()
-    if x._dtype == "float32" and dtype == "int32":
-        L.check(lib.tjh_cast_f32_i32(x.data_ptr(), out.data_ptr(), n), "cast")
-    elif x._dtype == "int32" and dtype == "float32":
-        L.check(lib.tjh_cast_i32_f32(x.data_ptr(), out.data_ptr(), n), "cast")
-    else:
-        a = x.numpy().astype(_DT[dtype][1])
-        return from_numpy(a, dtype=dtype)
+    if x.numel():
+        L.check(L.lib().tjh_cast(L.DTYPE[x._dtype], L.DTYPE[dtype], x.data_ptr(), out.data_ptr(),
+                                 x.numel()), "cast")
     return out
 
 
@@ -1177,6 +1182,63 @@ def compare_raw(a, b, op):
 def compare(a, b, op):
     """eq/ne/lt/le/gt/ge producing float 0/1 (compare.wgsl); no gradient."""
     return compare_raw(a, b, op)
+
+
+def triangle(x, diagonal=0, upper=True):
+    """triu / tril (triu.wgsl, tril.wgsl) over the last two dims; the
+    gradient is the same mask applied to the incoming gradient."""
+    if x.ndim < 2:
+        raise RuntimeError("triu/tril: expected a tensor with at least 2 dimensions")
+    dt = x.dtype
+    xf = x if dt == "float32" else x.float()
+    xc = xf.contiguous()
+    rows, cols = x.shape[-2], x.shape[-1]
+    batch = _numel(x.shape[:-2])
+    out = empty(x.shape)
+    L.check(L.lib().tjh_triangle(xc.data_ptr(), out.data_ptr(), batch, rows, cols, int(diagonal),
+                                 1 if upper else 0), "triangle")
+    if dt != "float32":
+        return out.to(dt)
+
+    def bwd(g):
+        gc = g.contiguous()
+        o = empty(g.shape)
+        L.check(L.lib().tjh_triangle(gc.data_ptr(), o.data_ptr(), batch, rows, cols,
+                                     int(diagonal), 1 if upper else 0), "triangle_backward")
+        return [o]
+    return _record(out, "Triu" if upper else "Tril", [x], bwd)
+
+
+def triu(x, diagonal=0):
+    return triangle(x, diagonal, True)
+
+
+def tril(x, diagonal=0):
+    return triangle(x, diagonal, False)
+
+
+def multinomial(x, num_samples=1, replacement=False):
+    """Tensor.multinomial (Tensor.ts:271-359) on the device: int32 indices,
+    [num_samples] for a 1-D input, [rows, num_samples] for a 2-D one.
+    Weights are max(0, x) normalised by their sum (uniform when it is not
+    positive); the draws come from the seeded stream (one LCG step of the
+    manual_seed state per call, like rand), not Math.random."""
+    if x.ndim not in (1, 2):
+        raise RuntimeError("multinomial: expected a 1-D or 2-D tensor of probabilities")
+    cols = x.shape[-1]
+    rows = 1 if x.ndim == 1 else x.shape[0]
+    if cols == 0:
+        raise RuntimeError("multinomial: no categories")
+    if not replacement and num_samples > cols:
+        raise RuntimeError("Cannot sample %d values from %d categories without replacement"
+                           % (num_samples, cols))
+    xc = (x if x.dtype == "float32" else x.float()).contiguous()
+    out = empty((rows, num_samples) if x.ndim == 2 else (num_samples,), "int32")
+    if rows and num_samples:
+        L.check(L.lib().tjh_multinomial(xc.data_ptr(), rows, cols, int(num_samples),
+                                        1 if replacement else 0, _next_seed(), out.data_ptr()),
+                "multinomial")
+    return out
 
 
 def clamp(x, min=None, max=None):
@@ -1546,12 +1608,8 @@ def _getitem(x, idx):
             continue
         if isinstance(it, Tensor):
             # advanced indexing wraps negative indices once (index_select
-            # itself rejects them)
-            ih = it.reshape(-1).to("int32").numpy()
-            n = out.shape[d]
-            if ih.size and (ih.min() < -n or ih.max() >= n):
-                raise IndexError("index out of range for dimension of size %d" % n)
-            out = index_select(out, d, np.where(ih < 0, ih + n, ih).astype(np.int32))
+            # itself rejects them): a gather along d, whose kernel wraps
+            out = _take_along(out, d, it)
             d += 1
             continue
         raise TypeError("unsupported index %r" % (it,))
@@ -1620,8 +1678,8 @@ def masked_fill(x, mask, value):
 
 
 def _to_mask(t):
-    a = (t.numpy() != 0).astype(np.uint8)
-    return from_numpy(a, dtype="uint8")
+    """A bool (one byte per element) view of t != 0, on the device."""
+    return t if t._dtype == "bool" else _k_cast(t, "bool")
 
 
 # ------------------------------------------------------------ indexing
@@ -1694,6 +1752,23 @@ def gather(x, dim, index):
                                         g.data_ptr()), "scatter_add")
         return [z]
     return _record(out, "Gather", [x], bwd)
+
+
+def _take_along(x, d, index):
+    """x[..., index, ...] along dim d for a 1-D index whose negative entries
+    wrap once (advanced indexing): a gather with the index broadcast over
+    the other dims, so the wrap happens on the device; the backward is the
+    gather's ordered scatter-add."""
+    idx = _idx32(index).reshape(-1)
+    n = x.shape[d]
+    host = idx.numpy()  # range check only (as index_select does)
+    if host.size and (host.min() < -n or host.max() >= n):
+        raise IndexError("index out of range for dimension of size %d" % n)
+    shape = x.shape[:d] + (idx.numel(),) + x.shape[d + 1:]
+    st = [0] * len(shape)
+    st[d] = 1
+    full_idx = _k_contiguous(Tensor(idx._storage, shape, tuple(st), idx._offset, "int32"))
+    return gather(x, d, full_idx)
 
 
 def nonzero(x):

@@ -11,7 +11,7 @@ user would write it (nn modules, functional ops, backward(), optimizers):
 """
 from . import functional as F
 from . import nn
-from .tensor import arange, from_numpy
+from .tensor import arange, from_numpy, no_grad, zeros
 
 
 def mlp():
@@ -54,6 +54,32 @@ class CausalSelfAttention(nn.Module):
         v = v.view(B, T, self.heads, hd).transpose(1, 2)
         y = F.scaled_dot_product_attention(q, k, v, is_causal=True)
         y = y.transpose(1, 2).contiguous().view(B, T, C)
+        return self._project(y, residual)
+
+    def forward_cached(self, x, cache, layer, pos, residual=None):
+        """Attention of the new positions [pos, pos + T) of x against the
+        cached keys / values of positions [0, pos) plus their own; the new
+        keys and values are appended to the cache.  A prompt (pos 0) is
+        causal over itself; a single new token attends to every cached
+        position."""
+        B, T, C = x.shape
+        hd = C // self.heads
+        q, k, v = self.c_attn(x).split(C, dim=2)
+        q = q.view(B, T, self.heads, hd).transpose(1, 2)
+        k = k.view(B, T, self.heads, hd).transpose(1, 2)
+        v = v.view(B, T, self.heads, hd).transpose(1, 2)
+        keys, values = cache.append(layer, k, v, pos)
+        if pos == 0:
+            y = F.scaled_dot_product_attention(q, keys, values, is_causal=True)
+        elif T == 1:
+            y = F.scaled_dot_product_attention(q, keys, values, is_causal=False)
+        else:
+            raise NotImplementedError("KV cache: prompts start at position 0, then one token "
+                                      "per step")
+        y = y.transpose(1, 2).contiguous().view(B, T, C)
+        return self._project(y, residual)
+
+    def _project(self, y, residual):
         if self.fused:
             return F._linear_add(y, self.c_proj.weight, self.c_proj.bias, residual)
         out = self.c_proj(y)
@@ -95,6 +121,32 @@ class Block(nn.Module):
         x = self.attn(self.ln_1(x), residual=x)
         return self.mlp(self.ln_2(x), residual=x)
 
+    def forward_cached(self, x, cache, layer, pos):
+        x = self.attn.forward_cached(self.ln_1(x), cache, layer, pos, residual=x)
+        return self.mlp(self.ln_2(x), residual=x)
+
+
+class KVCache:
+    """Keys and values of every layer for positions [0, max_len): one
+    [B, H, max_len, head_dim] buffer each, filled as positions arrive; the
+    attention of a decoding step reads the prefix [0, pos] as a strided
+    view (no copy)."""
+
+    def __init__(self, layers, batch, heads, max_len, head_dim):
+        self.max_len = max_len
+        self.k = [zeros(batch, heads, max_len, head_dim) for _ in range(layers)]
+        self.v = [zeros(batch, heads, max_len, head_dim) for _ in range(layers)]
+
+    def append(self, layer, k, v, pos):
+        T = k.shape[2]
+        if pos + T > self.max_len:
+            raise RuntimeError("KV cache: position %d beyond its length %d" % (pos + T,
+                                                                              self.max_len))
+        with no_grad():
+            self.k[layer][:, :, pos:pos + T].copy_(k)
+            self.v[layer][:, :, pos:pos + T].copy_(v)
+        return self.k[layer][:, :, :pos + T], self.v[layer][:, :, :pos + T]
+
 
 class GPT2(nn.Module):
     """GPT-2 with the LM head tied to the token embedding."""
@@ -119,6 +171,50 @@ class GPT2(nn.Module):
     def loss(self, ids, targets):
         logits = self(ids)
         return F.cross_entropy(logits.view(-1, self.vocab), targets.reshape(-1))
+
+    def new_cache(self, batch, max_len=None):
+        blk = self.h[0].attn
+        return KVCache(len(self.h), batch, blk.heads, max_len or self.ctx, blk.d // blk.heads)
+
+    def forward_cached(self, ids, cache, pos):
+        """Logits of positions [pos, pos + T) of ids [B, T], the keys and
+        values of earlier positions read from (and these appended to) the
+        cache."""
+        B, T = ids.shape
+        p = arange(pos, pos + T, dtype="int32")
+        x = self.wte(ids) + self.wpe(p)
+        for i, blk in enumerate(self.h):
+            x = blk.forward_cached(x, cache, i, pos)
+        x = self.ln_f(x)
+        return F.linear(x, self.wte.weight)
+
+    def generate(self, ids, max_new_tokens, temperature=1.0, greedy=False):
+        """Autoregressive decoding with a KV cache (the inference side of the
+        GPT-2 path, tests/gpt2.test.ts): the prompt runs once, then each
+        new token is one cached step; the next token is drawn by
+        multinomial from softmax(logits / temperature) (or argmax when
+        greedy).  Returns the [B, T + max_new_tokens] int32 ids."""
+        from .tensor import cat
+        B, T = ids.shape
+        total = T + max_new_tokens
+        if total > self.ctx:
+            raise ValueError("generate: %d positions exceed the context of %d" % (total, self.ctx))
+        with no_grad():
+            cache = self.new_cache(B, total)
+            logits = self.forward_cached(ids, cache, 0)
+            out = [ids]
+            pos = T
+            for _ in range(max_new_tokens):
+                last = logits[:, -1, :]
+                if greedy:
+                    nxt = last.argmax(-1, keepdim=True)
+                else:
+                    probs = F.softmax(last * (1.0 / temperature), -1)
+                    nxt = probs.multinomial(1)
+                out.append(nxt)
+                logits = self.forward_cached(nxt, cache, pos)
+                pos += 1
+            return cat(out, 1)
 
 
 def load_params(model, params):
