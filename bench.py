@@ -108,11 +108,17 @@ def run_gpu(steps, warmup):
     ids = torch.tensor(toks[:, :-1])
     tgt = torch.tensor(toks[:, 1:])
 
+    rf = torch.profiler.record_function
+
     def step():
+        # the phases are roctx ranges (rocprofv3 --marker-trace shows them)
         opt.zero_grad()
-        loss = model.loss(ids, tgt)
-        loss.backward()
-        opt.step()
+        with rf("gpt2.forward"):
+            loss = model.loss(ids, tgt)
+        with rf("gpt2.backward"):
+            loss.backward()
+        with rf("gpt2.adamw"):
+            opt.step()
         return loss
 
     for i in range(warmup):

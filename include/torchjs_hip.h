@@ -144,6 +144,19 @@ int tjh_kprof_names(char* buf, size_t buflen);
 /* Wall timer on the stream: returns an id; tjh_timer_stop gives ms. */
 int tjh_timer_start(int* id);
 int tjh_timer_stop(int id, double* ms);
+/* The same timer closed without waiting (tjh_timer_end records the end on
+ * the stream) and read later (tjh_timer_read waits for that end and
+ * releases the id): the device time of a record_function block. */
+int tjh_timer_end(int id);
+int tjh_timer_read(int id, double* ms);
+/* Named ranges and marks on the ROCm tracer's marker timeline (roctx),
+ * the device-side counterpart of record_function
+ * (src/profiler/index.ts:145-166): `rocprofv3 --marker-trace` shows each
+ * range around the kernels launched while it is open.  Cheap no-ops when
+ * no tracer is attached. */
+int tjh_range_push(const char* name);
+int tjh_range_pop(void);
+int tjh_mark(const char* name);
 
 /* ------------------------------------------------------------------ */
 /* Fill / RNG / copies — fill.wgsl, random.wgsl:9-46 (with the LCG seed */

@@ -7,6 +7,7 @@ small and seeded; every file holds inputs and expected outputs only.
 
     python tests/golden/make_golden.py
 """
+import collections
 import math
 import os
 
@@ -289,7 +290,60 @@ def losses_ext(rng):
     save("losses_ext", **d)
 
 
+def serialization_fixtures():
+    """A PyTorch state_dict archive (torch.save) and a torch.js archive laid
+    out as src/serialization/common.ts:22-75 writes it, each with the
+    values a loader must produce (float32 / int32 / uint8 after the device's
+    dtype mapping)."""
+    import io
+    import json
+    import zipfile
+    g = torch.Generator().manual_seed(5)
+    base = torch.randn(10, generator=g, dtype=torch.float32)
+    w = torch.nn.Parameter(torch.randn(3, 4, generator=g, dtype=torch.float32))
+    tr = torch.randn(4, 3, generator=g, dtype=torch.float32).t()  # strides (1, 3)
+    sd = collections.OrderedDict([
+        ("layer.weight", w), ("ids", torch.arange(5, dtype=torch.int64) - 2),
+        ("transposed", tr), ("slice", base[3:7]), ("half", torch.tensor([1.5, -2.25, 65504.0]).half()),
+        ("bf16", torch.tensor([1.0, -3.140625, 0.0078125]).bfloat16()),
+        ("mask", torch.tensor([True, False, True])),
+        ("nested", {"list": [torch.ones(2, dtype=torch.float32), 7, "name"], "scale": 0.5})])
+    buf = io.BytesIO()
+    torch.save(sd, buf)
+    with open(os.path.join(OUT, "state_dict.pt"), "wb") as f:
+        f.write(buf.getvalue())
+    exp = {"layer.weight": w.detach().numpy().astype(np.float32),
+           "ids": (np.arange(5) - 2).astype(np.int32),
+           "transposed": tr.numpy().astype(np.float32),
+           "slice": base[3:7].numpy().astype(np.float32),
+           "half": np.array([1.5, -2.25, 65504.0], np.float32),
+           "bf16": np.array([1.0, -3.140625, 0.0078125], np.float32),
+           "mask": np.array([1, 0, 1], np.uint8),
+           "nested.list.0": np.ones(2, np.float32)}
+    np.savez_compressed(os.path.join(OUT, "state_dict_expected.npz"), **exp)
+    # torch.js layout: model.json with tensor metadata, tensors/<id>.bin
+    meta = lambda i, shape, dt, rg=False: {"__tensor__": True, "id": str(i), "shape": shape,
+                                          "dtype": dt, "requires_grad": rg, "device": "webgpu"}
+    doc = {"model": {"fc.weight": meta(0, [2, 3], "float32", True),
+                     "fc.bias": meta(1, [2], "float32", True)},
+           "step": 12, "ids": meta(2, [4], "int32"), "h": meta(3, [2], "float16"),
+           "flags": meta(4, [3], "bool"), "u": meta(5, [2], "uint32"),
+           "hist": [meta(6, [2, 2], "int8"), "tag"]}
+    bins = [np.arange(6, dtype="<f4").reshape(2, 3) / 4, np.array([-1.5, 2.0], "<f4"),
+            np.array([3, -7, 0, 2 ** 30], "<i4"), np.array([0.5, -1.0], "<f4"),
+            np.array([1, 0, 1], "u1"), np.array([7, 2 ** 31 - 1], "<u4"),
+            np.array([[-128, 5], [0, 127]], "i1")]
+    zb = io.BytesIO()
+    with zipfile.ZipFile(zb, "w", zipfile.ZIP_DEFLATED) as z:
+        z.writestr("model.json", json.dumps(doc, indent=2))
+        for i, a in enumerate(bins):
+            z.writestr("tensors/%d.bin" % i, a.tobytes())
+    with open(os.path.join(OUT, "torchjs_archive.zip"), "wb") as f:
+        f.write(zb.getvalue())
+
+
 def main():
+    serialization_fixtures()
     losses_ext(np.random.default_rng(20261202))
     rng = np.random.default_rng(20261201)
     unary_ops(rng)

@@ -477,3 +477,77 @@ def test_gpt2_kv_cache_matches_full_forward(torch):
         for j in range(9, 21):
             step = model.forward_cached(torch.tensor(seq[:, j:j + 1]), cache, j).numpy()
             check(step[:, 0], full[:, j], **RED)
+
+
+# ------------------------------------------------------------ profiler
+
+
+def test_profiler_record_function(torch):
+    """record_function (src/profiler/index.ts:155-210): the context-manager,
+    fn and decorator forms record host and device time and the allocator
+    delta while a profiler is active; outside one they only run the block
+    (and its roctx range)."""
+    P = torch.profiler
+    assert P.record_function("idle", lambda: 41 + 1) == 42  # no profiler: just runs
+    with P.profile() as prof:
+        with P.record_function("matmul_block"):
+            a = torch.randn(1024, 1024)
+            b = a @ a
+        s = P.record_function("fn_form", lambda: (b * 2.0).sum())
+
+        @P.record_function("decorated")
+        def twice(x):
+            return x * 2.0
+        twice(a)
+        P.mark("checkpoint")
+    assert isinstance(s, torch.Tensor)
+    ev = {e["name"]: e for e in prof.get_events()}
+    assert set(ev) == {"matmul_block", "fn_form", "decorated"}
+    for e in ev.values():
+        assert e["duration"] > 0 and e["device_duration"] > 0 and e["activity"] == "hip"
+    assert ev["matmul_block"]["memory_usage"] >= 2 * 1024 * 1024 * 4
+    tab = prof.key_averages().table(sort_by="device_duration")
+    assert "matmul_block" in tab and "Device Time" in tab
+    out = P.profile(lambda p: P.record_function("inner", lambda: torch.ones(8).sum()))
+    assert [e["name"] for e in out.get_events()] == ["inner"]
+
+
+# ------------------------------------------------------------ weight I/O
+
+
+def test_save_load_round_trip_on_device(torch, tmp_path):
+    """torch.save of a model's state_dict (torch.js's zip layout) and
+    torch.load back into a fresh model: every parameter byte for byte; a
+    strided view is saved as its values."""
+    from torchjs_amd import workloads as W
+    torch.manual_seed(5)
+    src = W.GPT2(211, 64, 128, 4, 2)
+    path = str(tmp_path / "gpt2.zip")
+    extra = torch.randn(6, 4).T  # a transposed view
+    torch.save({"state": src.state_dict(), "extra": extra, "step": 3}, path)
+    obj = torch.load(path)
+    assert obj["step"] == 3 and obj["extra"].shape == (4, 6)
+    assert np.array_equal(obj["extra"].numpy(), extra.numpy())
+    dst = W.GPT2(211, 64, 128, 4, 2)
+    dst.load_state_dict(obj["state"])
+    for (k, a), (k2, b) in zip(src.named_parameters(), dst.named_parameters()):
+        assert k == k2 and a.numpy().tobytes() == b.numpy().tobytes(), k
+    assert torch.save(extra)[:2] == b"PK"  # bytes when no file is given
+
+
+def test_load_pytorch_state_dict_to_device(torch):
+    """A torch.save archive (PyTorch's layout: data.pkl + data/N, read with
+    the weights-only unpickler, strides and offsets applied) becomes 'hip'
+    tensors holding the saved values."""
+    import os
+    from conftest import GOLDEN
+    obj = torch.load(os.path.join(GOLDEN, "state_dict.pt"))
+    with np.load(os.path.join(GOLDEN, "state_dict_expected.npz")) as z:
+        for k in ("layer.weight", "ids", "transposed", "slice", "half", "bf16", "mask"):
+            t = obj[k]
+            assert isinstance(t, torch.Tensor), k
+            assert np.array_equal(t.numpy(), z[k]), k
+        assert np.array_equal(obj["nested"]["list"][0].numpy(), z["nested.list.0"])
+    assert obj["layer.weight"].requires_grad and obj["mask"].dtype == "bool"
+    same = torch.serialization.load_pytorch_zip(os.path.join(GOLDEN, "state_dict.pt"))
+    assert np.array_equal(same["transposed"].numpy(), obj["transposed"].numpy())

@@ -17,7 +17,8 @@ for gfx950.  Usage mirrors torch.js:
 import ctypes
 
 from . import _lib
-from . import autograd, functional, nn, optim
+from . import autograd, functional, nn, optim, profiler, serialization
+from .serialization import load, save
 from .tensor import (Tensor, arange, cat, chunk, enable_grad, from_numpy, full, full_like,
                      inference_mode, init, is_grad_enabled, is_initialized, manual_seed, matmul,
                      multinomial, no_grad, ones, ones_like, rand, randn, set_grad_enabled, split,
@@ -28,9 +29,11 @@ F = functional
 
 __all__ = [
     "Tensor", "arange", "autograd", "cat", "chunk", "empty", "enable_grad", "from_numpy", "full",
-    "full_like", "hip", "inference_mode", "init", "is_grad_enabled", "is_initialized",
-    "manual_seed", "matmul", "multinomial", "nn", "no_grad", "ones", "ones_like", "optim", "rand",
-    "randn", "set_grad_enabled", "split", "stack", "synchronize", "tensor", "tril", "triu",
+    "full_like", "hip", "inference_mode", "init", "is_grad_enabled", "is_initialized", "load",
+    "manual_seed", "matmul", "multinomial", "nn", "no_grad", "ones", "ones_like", "optim",
+    "profiler", "rand",
+    "randn", "save", "set_grad_enabled", "split", "stack", "synchronize", "tensor", "tril",
+    "triu",
     "zeros", "zeros_like",
 ]
 

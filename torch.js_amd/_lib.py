@@ -134,6 +134,11 @@ SIGNATURES = {
     "tjh_conv2d_forward": [ctypes.POINTER(Conv2dDesc), c_vp, c_vp, c_vp, c_vp],
     "tjh_conv2d_backward_input": [ctypes.POINTER(Conv2dDesc), c_vp, c_vp, c_vp],
     "tjh_conv2d_backward_weight": [ctypes.POINTER(Conv2dDesc), c_vp, c_vp, c_vp, c_int],
+    "tjh_timer_end": [c_int],
+    "tjh_timer_read": [c_int, ctypes.POINTER(c_f64)],
+    "tjh_range_push": [ctypes.c_char_p],
+    "tjh_range_pop": [],
+    "tjh_mark": [ctypes.c_char_p],
     "tjh_cast": [c_int, c_int, c_vp, c_vp, c_i64],
     "tjh_fill_u8": [c_vp, c_i64, ctypes.c_uint8],
     "tjh_copy_strided_u8": [c_int, P_i64, c_vp, P_i64, c_vp, P_i64],

@@ -24,6 +24,7 @@ ADDON = os.path.join(PKG, "node", "torchjs_hip.node")
 INCLUDE = os.path.join(os.path.dirname(PKG), "include")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ROCM_LIB = "/opt/rocm/lib"
 HIP_FLAGS = [
     "--offload-arch=gfx950",
     "-O3",
@@ -59,7 +60,9 @@ def build_library(jobs=None):
     with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as ex:
         objs = list(ex.map(_compile, sources))
     tmp = LIB + ".tmp"
-    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp] + objs)
+    # roctx (rocprofiler-sdk) for the named ranges of record_function
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp] + objs +
+         ["-L" + ROCM_LIB, "-lrocprofiler-sdk-roctx", "-Wl,-rpath," + ROCM_LIB])
     os.replace(tmp, LIB)
     return LIB
 

@@ -9,6 +9,7 @@
 
 #include "common.h"
 
+#include <rocprofiler-sdk-roctx/roctx.h>
 #include <stdarg.h>
 #include <stdio.h>
 #include <string.h>
@@ -192,6 +193,7 @@ struct Prof {
   std::unordered_map<std::string, int> index;
   std::vector<hipEvent_t> spare;
   std::vector<hipEvent_t> timers;  // start events of wall timers
+  std::unordered_map<int, hipEvent_t> timer_ends;  // end events recorded by tjh_timer_end
 };
 
 Prof& prof() {
@@ -600,8 +602,74 @@ int tjh_timer_start(int* id) {
   hipEvent_t e = take_event(P);
   if (!e) return set_error(TJH_ERR_HIP, "tjh_timer_start: hipEventCreate failed");
   TJH_HIP(hipEventRecord(e, g_stream));
-  P.timers.push_back(e);
-  *id = (int)P.timers.size() - 1;
+  int slot = -1;
+  for (int i = 0; i < (int)P.timers.size(); ++i)
+    if (!P.timers[i]) { slot = i; break; }
+  if (slot < 0) {
+    P.timers.push_back(e);
+    slot = (int)P.timers.size() - 1;
+  } else {
+    P.timers[slot] = e;
+  }
+  *id = slot;
+  return TJH_OK;
+}
+
+int tjh_timer_end(int id) {
+  TJH_REQUIRE_INIT();
+  Prof& P = prof();
+  std::lock_guard<std::mutex> lk(P.mu);
+  TJH_ARG(id >= 0 && id < (int)P.timers.size() && P.timers[id],
+          "tjh_timer_end: unknown timer %d", id);
+  TJH_ARG(P.timer_ends.find(id) == P.timer_ends.end(), "tjh_timer_end: timer %d already ended",
+          id);
+  hipEvent_t e = take_event(P);
+  if (!e) return set_error(TJH_ERR_HIP, "tjh_timer_end: hipEventCreate failed");
+  TJH_HIP(hipEventRecord(e, g_stream));
+  P.timer_ends[id] = e;
+  return TJH_OK;
+}
+
+int tjh_timer_read(int id, double* ms) {
+  TJH_REQUIRE_INIT();
+  TJH_ARG(ms, "tjh_timer_read: ms is NULL");
+  hipEvent_t s0, e;
+  {
+    Prof& P = prof();
+    std::lock_guard<std::mutex> lk(P.mu);
+    auto it = P.timer_ends.find(id);
+    TJH_ARG(id >= 0 && id < (int)P.timers.size() && P.timers[id] && it != P.timer_ends.end(),
+            "tjh_timer_read: timer %d was not ended", id);
+    s0 = P.timers[id];
+    e = it->second;
+  }
+  TJH_HIP(hipEventSynchronize(e));
+  float t = 0.f;
+  TJH_HIP(hipEventElapsedTime(&t, s0, e));
+  *ms = t;
+  Prof& P = prof();
+  std::lock_guard<std::mutex> lk(P.mu);
+  P.timer_ends.erase(id);
+  P.spare.push_back(s0);
+  P.spare.push_back(e);
+  P.timers[id] = nullptr;
+  return TJH_OK;
+}
+
+int tjh_range_push(const char* name) {
+  TJH_ARG(name, "tjh_range_push: name is NULL");
+  roctxRangePushA(name);
+  return TJH_OK;
+}
+
+int tjh_range_pop(void) {
+  roctxRangePop();
+  return TJH_OK;
+}
+
+int tjh_mark(const char* name) {
+  TJH_ARG(name, "tjh_mark: name is NULL");
+  roctxMarkA(name);
   return TJH_OK;
 }
 

@@ -739,6 +739,43 @@ static napi_value js_timer_stop(napi_env env, napi_callback_info info) {
   CHECK_RC(tjh_timer_stop((int)i64(env, a[0]), &ms));
   return num(env, ms);
 }
+static napi_value js_timer_end(napi_env env, napi_callback_info info) {
+  napi_value a[1];
+  if (!get_args(env, info, 1, a)) return NULL;
+  CHECK_RC(tjh_timer_end((int)i64(env, a[0])));
+  return undef(env);
+}
+static napi_value js_timer_read(napi_env env, napi_callback_info info) {
+  napi_value a[1];
+  double ms = 0.0;
+  if (!get_args(env, info, 1, a)) return NULL;
+  CHECK_RC(tjh_timer_read((int)i64(env, a[0]), &ms));
+  return num(env, ms);
+}
+/* rangePush(name) / rangePop() / mark(name): roctx ranges for record_function */
+static napi_value js_range_push(napi_env env, napi_callback_info info) {
+  napi_value a[1];
+  char buf[512];
+  size_t len = 0;
+  if (!get_args(env, info, 1, a)) return NULL;
+  napi_get_value_string_utf8(env, a[0], buf, sizeof(buf), &len);
+  CHECK_RC(tjh_range_push(buf));
+  return undef(env);
+}
+static napi_value js_range_pop(napi_env env, napi_callback_info info) {
+  (void)info;
+  CHECK_RC(tjh_range_pop());
+  return undef(env);
+}
+static napi_value js_mark(napi_env env, napi_callback_info info) {
+  napi_value a[1];
+  char buf[512];
+  size_t len = 0;
+  if (!get_args(env, info, 1, a)) return NULL;
+  napi_get_value_string_utf8(env, a[0], buf, sizeof(buf), &len);
+  CHECK_RC(tjh_mark(buf));
+  return undef(env);
+}
 static napi_value js_fill_i32(napi_env env, napi_callback_info info) {
   napi_value a[3];
   if (!get_args(env, info, 3, a)) return NULL;
@@ -1016,6 +1053,8 @@ static napi_value init_module(napi_env env, napi_value exports) {
       FN("conv2dBackwardWeight", js_conv_backward_weight),
       FN("cast", js_cast), FN("fillU8", js_fill_u8), FN("copyStridedU8", js_copy_strided_u8),
       FN("triangle", js_triangle), FN("multinomial", js_multinomial),
+      FN("timerEnd", js_timer_end), FN("timerRead", js_timer_read),
+      FN("rangePush", js_range_push), FN("rangePop", js_range_pop), FN("mark", js_mark),
   };
   napi_define_properties(env, exports, sizeof(desc) / sizeof(desc[0]), desc);
   napi_value v;
