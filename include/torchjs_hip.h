@@ -24,8 +24,18 @@
 #ifndef TORCHJS_HIP_H
 #define TORCHJS_HIP_H
 
+/* runtime-compiled kernels (hipRTC) include this header for its op codes;
+ * hipRTC defines the fixed-width integer types itself */
+#ifndef __HIPCC_RTC__
 #include <stddef.h>
 #include <stdint.h>
+#else
+typedef __hip_internal::uint8_t uint8_t;
+typedef __hip_internal::int32_t int32_t;
+typedef __hip_internal::uint32_t uint32_t;
+typedef __hip_internal::int64_t int64_t;
+typedef __hip_internal::uint64_t uint64_t;
+#endif
 
 #ifdef __cplusplus
 extern "C" {
@@ -292,6 +302,68 @@ int tjh_reduce(int op, const float* x, int64_t outer, int64_t r,
  * index (Tensor.ts:2568). */
 int tjh_argmax(const float* x, int64_t outer, int64_t r, int64_t inner,
                int is_min, int32_t* out);
+
+/* ------------------------------------------------------------------ */
+/* Fused elementwise expressions — one launch for a chain of the unary / */
+/* binary / scalar / ternary ops above, which the reference runs as one */
+/* submit each (Tensor.ts _unaryOp / _binaryOp / _broadcastBinaryOp /   */
+/* _scalarOp, 3409-3656, 3742-3792), and for the broadcast-gradient     */
+/* column sum of such a chain (Tensor.ts:3560-3591).                    */
+/* ------------------------------------------------------------------ */
+
+#define TJH_EXPR_MAX_INS 48
+#define TJH_EXPR_MAX_LEAVES 8
+#define TJH_EXPR_MAX_REGS 16
+#define TJH_EXPR_NONE 255 /* absent optional register operand */
+
+/* instruction kinds: dst <- ...
+ *  LOAD       leaf[a]
+ *  CONST      f
+ *  UNARY      unary op `code` of r[a] (alpha f)
+ *  UNARY_BWD  tjh_unary_backward's value for op `code`: g = r[a], x = r[b],
+ *             y = r[c] (b / c may be TJH_EXPR_NONE when the op does not
+ *             read them), alpha f
+ *  BINARY     binary op `code` of r[a], r[b]
+ *  TERNARY    ternary op `code` of g = r[a], a = r[b], b = r[c]
+ *  SCALAR     scalar op `code`: r[a] (op) f;  SCALAR_REV: f (op) r[a]
+ *  AXPY       f * r[a] + r[b]                                            */
+enum { TJH_EXPR_LOAD = 0, TJH_EXPR_CONST, TJH_EXPR_UNARY, TJH_EXPR_UNARY_BWD,
+       TJH_EXPR_BINARY, TJH_EXPR_TERNARY, TJH_EXPR_SCALAR, TJH_EXPR_SCALAR_REV,
+       TJH_EXPR_AXPY, TJH_EXPR_OPS };
+/* how leaf k is indexed at output element e: CONTIG e, ROW e % period,
+ * COL e / period, SCALAR 0 */
+enum { TJH_LEAF_CONTIG = 0, TJH_LEAF_ROW, TJH_LEAF_COL, TJH_LEAF_SCALAR };
+
+typedef struct {
+  uint8_t op, code, dst, a, b, c, pad0, pad1;
+  float f;
+} tjh_expr_ins;
+
+/* A program: n_ins instructions in order over TJH_EXPR_MAX_REGS
+ * registers (each source defined by an earlier instruction); the value of
+ * output element e is r[result] after the last one.  Every instruction
+ * computes exactly what the single-op entry points compute. */
+typedef struct {
+  int32_t n_ins, n_leaves, result, pad;
+  tjh_expr_ins ins[TJH_EXPR_MAX_INS];
+  const float* leaf[TJH_EXPR_MAX_LEAVES];
+  int64_t period[TJH_EXPR_MAX_LEAVES];
+  int32_t kind[TJH_EXPR_MAX_LEAVES];
+} tjh_expr;
+
+/* out[e] = value(e), e in [0, n). */
+int tjh_expr_eval(const tjh_expr* prog, int64_t n, float* out);
+/* Value viewed as contiguous [outer, r, inner]: out[outer, inner] = sum
+ * over r, bit-identical to tjh_reduce(TJH_REDUCE_SUM) of the materialised
+ * value (16-byte aligned, inner % 4 == 0) and of the same determinism;
+ * `values` (may be NULL) also receives the value.  Needs outer <= 64,
+ * r >= 64, inner >= 2 (else TJH_ERR_UNSUPPORTED). */
+int tjh_expr_colsum(const tjh_expr* prog, int64_t outer, int64_t r, int64_t inner,
+                    float* out, float* values);
+/* Validates `prog` and compiles the kernel tjh_expr_eval (colsum == 0) or
+ * tjh_expr_colsum (colsum != 0) would run for n elements, without a
+ * device (kernels are compiled at run time, once per program shape). */
+int tjh_expr_compile(const tjh_expr* prog, int64_t n, int colsum);
 
 /* ------------------------------------------------------------------ */
 /* Softmax / losses — log_softmax.wgsl, log_softmax_backward.wgsl,      */

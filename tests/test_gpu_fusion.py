@@ -1,0 +1,225 @@
+"""Deferred elementwise chains on the device: every fused value, column sum
+and gradient equals the op-by-op kernels bit for bit (the same ops with
+deferral off), chains really run as one kernel, and in-place writes never
+leak into a deferred value that read the written memory."""
+import sys
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def T(torch):
+    import __graft_entry__ as ge
+    return sys.modules[ge.PKG_NAME + ".tensor"]
+
+
+def _mode(T, on):
+    T._LAZY["on"] = on
+
+
+@pytest.fixture
+def both(torch, T):
+    """Runs fn with deferral on and off; returns the two results."""
+    def run(fn):
+        out = []
+        for on in (True, False):
+            _mode(T, on)
+            try:
+                out.append(fn())
+            finally:
+                _mode(T, True)
+        return out
+    return run
+
+
+def _np(x):
+    return x.numpy() if x is not None else None
+
+
+def _same(a, b):
+    if isinstance(a, (list, tuple)):
+        assert len(a) == len(b)
+        for u, v in zip(a, b):
+            _same(u, v)
+        return
+    assert a.shape == b.shape and a.dtype == b.dtype
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), np.max(np.abs(a - b))
+
+
+def _rand(shape, seed, lo=-2.0, hi=2.0):
+    return np.random.default_rng(seed).uniform(lo, hi, shape).astype(np.float32)
+
+
+def test_chain_fwd_bwd_bitwise_and_fused(torch, T, both):
+    """The C2 chain: ((x + bias).gelu() * y).sum(0).mean(), forward and
+    backward, fused against op by op; with deferral the chain's forward is
+    one column-sum launch and no elementwise kernel writes an intermediate."""
+    R, C = 512, 2048
+    xs, bs, ys = _rand((R, C), 1), _rand((C,), 2), _rand((R, C), 3, -1, 1)
+
+    def step():
+        x = torch.tensor(xs, requires_grad=True)
+        b = torch.tensor(bs, requires_grad=True)
+        y = torch.tensor(ys, requires_grad=True)
+        loss = ((x + b).gelu() * y).sum(0).mean()
+        loss.backward()
+        return [_np(loss), _np(x.grad), _np(b.grad), _np(y.grad)]
+
+    fused, plain = both(step)
+    _same(fused, plain)
+    # launch accounting with deferral on
+    torch.hip.kernel_timing(True)
+    torch.hip.kernel_timing_reset()
+    try:
+        step()
+        fams = dict((f, torch.hip.kernel_time(f)[0]) for f in torch.hip.kernel_families())
+    finally:
+        torch.hip.kernel_timing(False)
+    assert fams.get("expr_colsum", 0) >= 2, fams     # forward sum(0) and the bias gradient
+    assert fams.get("unary", 0) == 0 and fams.get("binary", 0) == 0, fams
+
+
+@pytest.mark.parametrize("op", ["neg", "exp", "log", "sqrt", "rsqrt", "tanh", "sigmoid", "relu",
+                                "gelu", "square", "reciprocal", "erf", "abs", "sin", "cos",
+                                "silu", "leaky_relu", "elu", "softplus", "sign"])
+def test_unary_fwd_bwd_bitwise(torch, T, both, op):
+    positive = op in ("log", "sqrt", "rsqrt", "reciprocal")
+    xs = _rand((300, 257), 10 + len(op), 0.1 if positive else -3.0, 3.0)
+
+    def run():
+        x = torch.tensor(xs, requires_grad=True)
+        z = T.unary(op, x * 1.25 + 0.125 if not positive else x * 1.25, 0.2)
+        w = (z * z + x).sum()
+        w.backward()
+        return [_np(z), _np(w), _np(x.grad)]
+
+    fused, plain = both(run)
+    _same(fused, plain)
+
+
+def test_binary_scalar_ternary_broadcast_bitwise(torch, T, both):
+    a_, row_, col_, s_ = _rand((256, 512), 21, 0.5, 2.0), _rand((512,), 22, 0.5, 2.0), \
+        _rand((256, 1), 23, 0.5, 2.0), _rand((), 24, 0.5, 2.0)
+
+    def run():
+        a = torch.tensor(a_, requires_grad=True)
+        row = torch.tensor(row_, requires_grad=True)
+        col = torch.tensor(col_, requires_grad=True)
+        s = torch.tensor(s_, requires_grad=True)
+        t = (a - row) * col / (s + 1.0)
+        t = t.maximum(a * 0.5) - row.minimum(col)
+        t = t ** 2 + (a ** row) / 3.0
+        t = 2.0 - t + 1.0 / (a + 3.0)
+        out = (t * a).sum()
+        out.backward()
+        return [_np(t), _np(out), _np(a.grad), _np(row.grad), _np(col.grad), _np(s.grad)]
+
+    fused, plain = both(run)
+    _same(fused, plain)
+
+
+@pytest.mark.parametrize("shape,dims", [((512, 1024), (0,)), ((8, 128, 256), (0, 1)),
+                                        ((16, 96, 64), (1,)), ((64, 2048), (0,))])
+@pytest.mark.parametrize("red", ["sum", "mean"])
+def test_column_sums_of_deferred_values(torch, T, both, shape, dims, red):
+    xs, ys = _rand(shape, 31), _rand(shape[-1:], 32)
+
+    def run():
+        x = torch.tensor(xs)
+        y = torch.tensor(ys)
+        v = (x * y).exp() - x
+        r = getattr(v, red)(dims if len(dims) > 1 else dims[0])
+        return [_np(r)]
+
+    fused, plain = both(run)
+    _same(fused, plain)
+
+
+def test_column_sum_keeps_value(torch, T):
+    """The broadcast add's backward evaluates the incoming gradient while
+    summing its columns: both results equal the unfused ones."""
+    R, C = 256, 1024
+    xs, bs = _rand((R, C), 41), _rand((C,), 42)
+
+    def run(on):
+        _mode(T, on)
+        try:
+            x = torch.tensor(xs, requires_grad=True)
+            b = torch.tensor(bs, requires_grad=True)
+            ((x + b).tanh() * 3.0).sum().backward()
+            return [_np(x.grad), _np(b.grad)]
+        finally:
+            _mode(T, True)
+
+    _same(run(True), run(False))
+
+
+def test_inplace_writes_do_not_reach_deferred_values(torch, T):
+    xs = _rand((512, 512), 51)
+    x = torch.tensor(xs)
+    y = x * 2.0                       # deferred, reads x
+    z = (y + 1.0).exp()               # deferred, reads y
+    assert T._is_lazy(y) and T._is_lazy(z)
+    x.fill_(7.0)                      # evaluates y and z first
+    np.testing.assert_array_equal(y.numpy(), xs * np.float32(2.0))
+    ref_z = (torch.tensor(xs) * 2.0 + 1.0).exp().numpy()
+    _same(z.numpy(), ref_z)
+    # copy_ / zero_ into a tensor a deferred value reads, and into the
+    # deferred value itself
+    a = torch.tensor(xs)
+    b = a.sigmoid()
+    c = b * 3.0
+    a.copy_(torch.tensor(np.zeros_like(xs)))
+    b.zero_()
+    assert np.all(b.numpy() == 0)
+    ref_c = (torch.tensor(xs).sigmoid() * 3.0).numpy()
+    _same(c.numpy(), ref_c)
+
+
+def test_optimizer_step_after_deferred_read(torch, T):
+    ps = _rand((256, 512), 61)
+    p = torch.tensor(ps, requires_grad=True)
+    with torch.no_grad():
+        w = p * 3.0                   # deferred, reads the parameter
+    (p * p).sum().backward()
+    opt = torch.optim.SGD([p], lr=0.5)
+    opt.step()
+    np.testing.assert_array_equal(w.numpy(), ps * np.float32(3.0))
+
+
+def test_views_detach_and_alignment(torch, T, both):
+    xs = _rand((384, 520), 71)
+
+    def run():
+        x = torch.tensor(xs)
+        v = x.exp() * 0.5
+        d = v.detach()
+        outs = [v.reshape(520, 384), v.t().contiguous(), v[3:7, 10:200], d * 2.0]
+        # a leaf at an odd element offset takes the 1-wide kernel
+        off = torch.tensor(xs.reshape(-1))[1:1 + 384 * 519].reshape(384, 519)
+        outs.append(off.tanh() + 1.0)
+        return [_np(o) for o in outs] + [np.array(d.data_ptr() == v.data_ptr())]
+
+    fused, plain = both(run)
+    _same(fused[:-1], plain[:-1])
+    assert fused[-1] and plain[-1]
+
+
+def test_long_chains_and_many_leaves(torch, T, both):
+    xs = [_rand((256, 256), 80 + k) for k in range(12)]
+
+    def run():
+        ts = [torch.tensor(a) for a in xs]
+        t = ts[0]
+        for k in range(70):  # beyond one program's instruction limit
+            t = (t * 0.999 + 0.001).tanh() if k % 2 else t - ts[k % 12] * 0.01
+        u = ts[0]
+        for a in ts[1:]:     # 12 leaves: beyond one program's leaf limit
+            u = u + a * 0.5
+        return [_np(t), _np(u)]
+
+    fused, plain = both(run)
+    _same(fused, plain)

@@ -53,6 +53,31 @@ class Conv2dDesc(ctypes.Structure):
         "dil_h", "dil_w", "groups", "oh", "ow")]
 
 
+# fused elementwise expression programs (tjh_expr, include/torchjs_hip.h)
+EXPR_MAX_INS = 48
+EXPR_MAX_LEAVES = 8
+EXPR_MAX_REGS = 16
+EXPR_NONE = 255
+EXPR_OP = {"load": 0, "const": 1, "unary": 2, "unary_bwd": 3, "binary": 4, "ternary": 5,
+           "scalar": 6, "scalar_rev": 7, "axpy": 8}
+LEAF = {"contig": 0, "row": 1, "col": 2, "scalar": 3}
+
+
+class ExprIns(ctypes.Structure):
+    _fields_ = [("op", ctypes.c_uint8), ("code", ctypes.c_uint8), ("dst", ctypes.c_uint8),
+                ("a", ctypes.c_uint8), ("b", ctypes.c_uint8), ("c", ctypes.c_uint8),
+                ("pad0", ctypes.c_uint8), ("pad1", ctypes.c_uint8), ("f", ctypes.c_float)]
+
+
+class Expr(ctypes.Structure):
+    _fields_ = [("n_ins", ctypes.c_int32), ("n_leaves", ctypes.c_int32),
+                ("result", ctypes.c_int32), ("pad", ctypes.c_int32),
+                ("ins", ExprIns * EXPR_MAX_INS),
+                ("leaf", ctypes.c_void_p * EXPR_MAX_LEAVES),
+                ("period", ctypes.c_int64 * EXPR_MAX_LEAVES),
+                ("kind", ctypes.c_int32 * EXPR_MAX_LEAVES)]
+
+
 # name -> argtypes (all functions return int status unless listed in _RESTYPE)
 SIGNATURES = {
     "tjh_last_error": [],
@@ -96,6 +121,9 @@ SIGNATURES = {
     "tjh_masked_fill": [c_int, P_i64, c_vp, P_i64, c_vp, P_i64, c_f32, c_vp],
     "tjh_compare": [c_int, c_int, P_i64, c_vp, P_i64, c_vp, P_i64, c_vp],
     "tjh_reduce": [c_int, c_vp, c_i64, c_i64, c_i64, c_vp],
+    "tjh_expr_eval": [c_vp, c_i64, c_vp],
+    "tjh_expr_colsum": [c_vp, c_i64, c_i64, c_i64, c_vp, c_vp],
+    "tjh_expr_compile": [c_vp, c_i64, c_int],
     "tjh_argmax": [c_vp, c_i64, c_i64, c_i64, c_int, c_vp],
     "tjh_softmax_forward": [c_vp, c_i64, c_vp, c_i64, c_i64, c_i64, c_int],
     "tjh_softmax_backward": [c_vp, c_vp, c_vp, c_i64, c_i64, c_int],
@@ -194,6 +222,9 @@ def load(path=None):
 
 def lib():
     return _lib if _lib is not None else load()
+
+
+ERR_UNSUPPORTED = 5  # TJH_ERR_UNSUPPORTED
 
 
 def check(rc, what=""):

@@ -60,9 +60,10 @@ def build_library(jobs=None):
     with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as ex:
         objs = list(ex.map(_compile, sources))
     tmp = LIB + ".tmp"
-    # roctx (rocprofiler-sdk) for the named ranges of record_function
+    # roctx (rocprofiler-sdk) for the named ranges of record_function,
+    # hipRTC for the fused expression kernels compiled at run time
     _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp] + objs +
-         ["-L" + ROCM_LIB, "-lrocprofiler-sdk-roctx", "-Wl,-rpath," + ROCM_LIB])
+         ["-L" + ROCM_LIB, "-lrocprofiler-sdk-roctx", "-lhiprtc", "-Wl,-rpath," + ROCM_LIB])
     os.replace(tmp, LIB)
     return LIB
 

@@ -10,22 +10,9 @@
 #pragma once
 
 #include "common.h"
+#include "kahan.h"
 
 namespace tjh {
-
-// Compensated (Kahan) accumulation: s + c carries the running sum with the
-// low-order bits lost by each fp32 addition kept in c, so a long sum of
-// cancelling terms stays within a few ulp of its exact value.
-struct Kahan {
-  float s = 0.f, c = 0.f;
-  __device__ __forceinline__ void add(float x) {
-#pragma clang fp contract(off)
-    const float y = x - c;
-    const float t = s + y;
-    c = (t - s) - y;
-    s = t;
-  }
-};
 
 constexpr int kFinalMax = 64;  // outputs one colsum_final launch can finish
 constexpr int kBatch = 8;     // rows fetched before they are accumulated
@@ -34,5 +21,11 @@ constexpr int kBatch = 8;     // rows fetched before they are accumulated
 // nullptr: skipped), np <= kFinalMax.  One launch on the library stream.
 int colsum_final(float* const* part, float* const* out, int np, int64_t nb, int64_t cols,
                  int accumulate, float scale);
+
+// Row partition of a column sum over r of [outer][r][inner] (about two
+// workgroups per CU, >= 16 rows each): nb slices of rchunk rows.  `vec`:
+// the column blocks hold 4 columns per lane.
+void colsum_plan(int64_t outer, int64_t r, int64_t inner, bool vec, int64_t* nb,
+                 int64_t* rchunk);
 
 }  // namespace tjh

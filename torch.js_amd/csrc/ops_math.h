@@ -2,7 +2,10 @@
 // kernels.
 #pragma once
 
+// Runtime-compiled kernels (hipRTC) have the HIP device API built in.
+#ifndef __HIPCC_RTC__
 #include <hip/hip_runtime.h>
+#endif
 
 namespace tjh {
 

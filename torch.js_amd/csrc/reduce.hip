@@ -276,19 +276,31 @@ int reduce_rows(const float* x, int64_t outer, int64_t r, float* out, float scal
   return reduce_rows<OP>(part, outer, splits, out, scale);
 }
 
-// SUM / MEAN over the middle axis: partial rows (k_colsum), then their
-// fixed-order sum (colsum_final).
-int colsum_launch(const float* x, int64_t outer, int64_t r, int64_t inner, float* out,
-                  float scale) {
+}  // namespace
+
+void colsum_plan(int64_t outer, int64_t r, int64_t inner, bool vec, int64_t* nb_out,
+                 int64_t* rchunk_out) {
   const int cus = num_cus() > 0 ? num_cus() : 256;
-  const bool vec = aligned16(x) && (inner % 4) == 0;
   const int64_t col_waves = cdiv(vec ? inner / 4 : inner, kBlock);
   // ~2 workgroups per CU in total, >= 16 rows each
   int64_t nb = cdiv(2LL * cus, outer * col_waves);
   if (nb > cdiv(r, 16)) nb = cdiv(r, 16);
   if (nb < 1) nb = 1;
   const int64_t rchunk = cdiv(r, nb);
-  nb = cdiv(r, rchunk);
+  *nb_out = cdiv(r, rchunk);
+  *rchunk_out = rchunk;
+}
+
+namespace {
+
+// SUM / MEAN over the middle axis: partial rows (k_colsum), then their
+// fixed-order sum (colsum_final).
+int colsum_launch(const float* x, int64_t outer, int64_t r, int64_t inner, float* out,
+                  float scale) {
+  const bool vec = aligned16(x) && (inner % 4) == 0;
+  const int64_t col_waves = cdiv(vec ? inner / 4 : inner, kBlock);
+  int64_t nb = 0, rchunk = 0;
+  colsum_plan(outer, r, inner, vec, &nb, &rchunk);
   Scratch part((size_t)(outer * nb * inner) * sizeof(float));
   if (!part.ok()) return set_error(TJH_ERR_OOM, "reduce: no scratch memory");
   dim3 grid((unsigned)nb, (unsigned)col_waves, (unsigned)outer);

@@ -429,6 +429,82 @@ static napi_value js_reduce(napi_env env, napi_callback_info info) {
   return undef(env);
 }
 
+/* Fused expression program from a JS object
+ *   { ins: [[op, code, dst, a, b, c, f], ...],
+ *     leaves: [[devicePtr (BigInt), kind, period], ...], result }
+ * (tjh_expr; a / b / c of an absent operand are 255).  Returns 0 and throws
+ * on a malformed object. */
+static int get_expr(napi_env env, napi_value obj, tjh_expr* P) {
+  memset(P, 0, sizeof(*P));
+  napi_value ins, leaves, res;
+  uint32_t n = 0, nl = 0;
+  if (napi_get_named_property(env, obj, "ins", &ins) != napi_ok ||
+      napi_get_named_property(env, obj, "leaves", &leaves) != napi_ok ||
+      napi_get_named_property(env, obj, "result", &res) != napi_ok ||
+      napi_get_array_length(env, ins, &n) != napi_ok ||
+      napi_get_array_length(env, leaves, &nl) != napi_ok || n > TJH_EXPR_MAX_INS ||
+      nl > TJH_EXPR_MAX_LEAVES) {
+    napi_throw_error(env, NULL, "expression: {ins, leaves, result} within the program limits");
+    return 0;
+  }
+  P->n_ins = (int32_t)n;
+  P->n_leaves = (int32_t)nl;
+  P->result = (int32_t)i64(env, res);
+  for (uint32_t i = 0; i < n; ++i) {
+    napi_value row, e[7];
+    napi_get_element(env, ins, i, &row);
+    for (uint32_t k = 0; k < 7; ++k) napi_get_element(env, row, k, &e[k]);
+    tjh_expr_ins* in = &P->ins[i];
+    in->op = (uint8_t)i64(env, e[0]);
+    in->code = (uint8_t)i64(env, e[1]);
+    in->dst = (uint8_t)i64(env, e[2]);
+    in->a = (uint8_t)i64(env, e[3]);
+    in->b = (uint8_t)i64(env, e[4]);
+    in->c = (uint8_t)i64(env, e[5]);
+    in->f = (float)f64(env, e[6]);
+  }
+  for (uint32_t k = 0; k < nl; ++k) {
+    napi_value row, e[3];
+    napi_get_element(env, leaves, k, &row);
+    for (uint32_t j = 0; j < 3; ++j) napi_get_element(env, row, j, &e[j]);
+    P->leaf[k] = (const float*)ptr(env, e[0]);
+    P->kind[k] = (int32_t)i64(env, e[1]);
+    P->period[k] = i64(env, e[2]);
+  }
+  return 1;
+}
+
+/* exprEval(program, n, out) */
+static napi_value js_expr_eval(napi_env env, napi_callback_info info) {
+  napi_value a[3];
+  if (!get_args(env, info, 3, a)) return NULL;
+  tjh_expr P;
+  if (!get_expr(env, a[0], &P)) return NULL;
+  CHECK_RC(tjh_expr_eval(&P, i64(env, a[1]), (float*)ptr(env, a[2])));
+  return undef(env);
+}
+
+/* exprCompile(program, n, colsum) */
+static napi_value js_expr_compile(napi_env env, napi_callback_info info) {
+  napi_value a[3];
+  if (!get_args(env, info, 3, a)) return NULL;
+  tjh_expr P;
+  if (!get_expr(env, a[0], &P)) return NULL;
+  CHECK_RC(tjh_expr_compile(&P, i64(env, a[1]), (int)i64(env, a[2])));
+  return undef(env);
+}
+
+/* exprColsum(program, outer, r, inner, out, values | null) */
+static napi_value js_expr_colsum(napi_env env, napi_callback_info info) {
+  napi_value a[6];
+  if (!get_args(env, info, 6, a)) return NULL;
+  tjh_expr P;
+  if (!get_expr(env, a[0], &P)) return NULL;
+  CHECK_RC(tjh_expr_colsum(&P, i64(env, a[1]), i64(env, a[2]), i64(env, a[3]),
+                           (float*)ptr(env, a[4]), (float*)ptr(env, a[5])));
+  return undef(env);
+}
+
 static napi_value js_softmax_forward(napi_env env, napi_callback_info info) {
   napi_value a[7];
   if (!get_args(env, info, 7, a)) return NULL;
@@ -1026,7 +1102,9 @@ static napi_value init_module(napi_env env, napi_value exports) {
       FN("emptyCache", js_empty_cache), FN("fill", js_fill), FN("random", js_random),
       FN("copyStrided", js_copy_strided), FN("unary", js_unary),
       FN("unaryBackward", js_unary_backward), FN("binary", js_binary), FN("scalar", js_scalar),
-      FN("reduce", js_reduce), FN("softmaxForward", js_softmax_forward),
+      FN("reduce", js_reduce), FN("exprEval", js_expr_eval), FN("exprColsum", js_expr_colsum),
+      FN("exprCompile", js_expr_compile),
+      FN("softmaxForward", js_softmax_forward),
       FN("softmaxBackward", js_softmax_backward), FN("crossEntropyForward", js_ce_forward),
       FN("crossEntropyBackward", js_ce_backward), FN("layerNormForward", js_ln_forward),
       FN("layerNormBackward", js_ln_backward),

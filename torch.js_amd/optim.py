@@ -6,7 +6,7 @@ and updates in a JS loop, adam.ts:104-120), plus plain SGD.
 import ctypes
 
 from . import _lib as L
-from .tensor import Tensor, _k_contiguous, zeros
+from .tensor import Tensor, _before_write, _k_contiguous, zeros
 
 
 class Optimizer:
@@ -63,6 +63,9 @@ class Adam(Optimizer):
 
     def step(self):
         lib = L.lib()
+        # the step writes parameters (and their moments) in place: deferred
+        # values that read them are evaluated first
+        _before_write(*[p for g in self.param_groups for p in g["params"]])
         for g in self.param_groups:
             b1, b2 = g["betas"]
             ps, gs, ms, vs, ns, steps = [], [], [], [], [], []
@@ -115,6 +118,9 @@ class SGD(Optimizer):
 
     def step(self):
         lib = L.lib()
+        # parameters (and, with weight decay, gradients) are written in place
+        ps = [p for g in self.param_groups for p in g["params"]]
+        _before_write(*ps, *[p.grad for p in ps if p.grad is not None])
         for g in self.param_groups:
             for p in g["params"]:
                 if p.grad is None:

@@ -22,6 +22,8 @@ PyTorch semantics torch.js declares:
 import ctypes
 import math
 import numbers
+import os
+import weakref
 
 import numpy as np
 
@@ -251,12 +253,13 @@ def _record(out, name, inputs, fn, acc_slot=None, defer_slots=()):
 class Tensor:
     """A strided view of device memory on the 'hip' device."""
 
-    __slots__ = ("_storage", "_offset", "_shape", "_strides", "_dtype", "requires_grad",
+    __slots__ = ("_st", "_lz", "_offset", "_shape", "_strides", "_dtype", "requires_grad",
                  "_grad", "grad_fn", "_retains_grad", "__weakref__")
 
     def __init__(self, storage, shape, strides=None, offset=0, dtype="float32",
                  requires_grad=False):
-        self._storage = storage
+        self._st = storage
+        self._lz = None  # a deferred elementwise op (_Lz) while _st is None
         self._shape = tuple(int(s) for s in shape)
         self._strides = tuple(strides) if strides is not None else _contig_strides(self._shape)
         self._offset = int(offset)
@@ -267,6 +270,15 @@ class Tensor:
         self._retains_grad = False
 
     # ------------------------------------------------------------ metadata
+    @property
+    def _storage(self):
+        """The device allocation; a deferred elementwise value is computed
+        (one fused kernel) the first time anything needs its memory."""
+        st = self._st
+        if st is None:
+            st = _realize(self)
+        return st
+
     @property
     def shape(self):
         return self._shape
@@ -388,6 +400,8 @@ class Tensor:
         run_backward([(self, gradient)], retain_graph=retain_graph)
 
     def detach(self):
+        if self._st is None:  # stays deferred, sharing the value
+            return _lazy("alias", 0, 0.0, (self,), self._shape)
         return Tensor(self._storage, self._shape, self._strides, self._offset, self._dtype)
 
     def detach_(self):
@@ -719,6 +733,7 @@ def _empty_padded(rows, cols):
 
 
 def _fill_view(t, value):
+    _before_write(t)
     lib = L.lib()
     if t.numel() == 0:
         return
@@ -736,6 +751,7 @@ def _fill_view(t, value):
 
 
 def _require_writable(t):
+    _before_write(t)
     if _grad["enabled"] and t.requires_grad and t.is_leaf:
         raise RuntimeError("a leaf Variable that requires grad is being used in an in-place operation.")
 
@@ -858,6 +874,324 @@ def _as_tensor(x, like=None):
     return full((), float(x), dtype=dt)
 
 
+# ----------------------------------------------------------------- deferred elementwise ops
+# torch.js runs each elementwise op as its own submit (Tensor.ts _unaryOp /
+# _binaryOp / _scalarOp, 3409-3656, 3742-3792).  Here an elementwise op on
+# a float32 tensor of at least _LAZY["min"] elements returns a tensor whose
+# value is deferred: it records the op and its inputs.  A chain of such ops
+# is evaluated by one fused kernel (tjh_expr_eval) the first time anything
+# needs the memory of a value in it (a GEMM, a readback, a view), and a
+# column sum of a deferred value (`sum(0)`, the bias gradient of a
+# broadcast add) reads the chain's inputs directly (tjh_expr_colsum), so
+# the intermediates of the chain are never written.  The autograd VJPs use
+# the same ops, so a backward through such a chain is deferred too and
+# recomputes the forward intermediates from their inputs.
+#
+# Values are those of the op-by-op kernels, bit for bit.  Writes: before
+# any in-place write to a storage, every deferred value that reads it is
+# evaluated (_before_write), so a deferred value never sees a later write.
+# TJH_LAZY=0 turns deferral off.
+
+_LAZY = {"on": os.environ.get("TJH_LAZY", "1") != "0", "min": 1 << 16}
+_PENDING = weakref.WeakSet()  # deferred tensors not yet evaluated
+_EXPR_KIND = {"u": "unary", "ub": "unary_bwd", "b": "binary", "t": "ternary", "s": "scalar",
+              "sr": "scalar_rev", "axpy": "axpy"}
+
+
+class _Lz:
+    """A deferred op: kind ('u' unary, 'ub' unary backward, 'b' binary,
+    't' ternary, 's' / 'sr' scalar, 'axpy', 'alias'), op code, scalar
+    operand, input tensors, and `deps`: ids of the storages and deferred
+    tensors its value reads (transitively)."""
+
+    __slots__ = ("kind", "code", "f", "args", "deps")
+
+    def __init__(self, kind, code, f, args, deps):
+        self.kind, self.code, self.f, self.args, self.deps = kind, code, f, args, deps
+
+
+def _is_lazy(t):
+    return t._st is None
+
+
+def _skey(t):
+    """Identity of t's storage without evaluating it: a deferred value that
+    is not an alias has no storage yet, so it shares none."""
+    while t._st is None:
+        lz = t._lz
+        if lz.kind != "alias":
+            return ("deferred", id(t))
+        t = lz.args[0]
+    return id(t._st)
+
+
+def _lazy(kind, code, f, args, shape):
+    deps = set()
+    for a in args:
+        if a is None:
+            continue
+        if a._st is None:
+            deps.add(id(a))
+            deps |= a._lz.deps
+        else:
+            deps.add(id(a._st))
+    t = Tensor.__new__(Tensor)
+    t._st = None
+    t._lz = _Lz(kind, code, float(f), tuple(args), deps)
+    t._shape = tuple(shape)
+    t._strides = _contig_strides(t._shape)
+    t._offset = 0
+    t._dtype = "float32"
+    t.requires_grad = False
+    t._grad = None
+    t.grad_fn = None
+    t._retains_grad = False
+    _PENDING.add(t)
+    return t
+
+
+def _leaf_kind(shape, bst):
+    """How a leaf with strides `bst` (broadcast to `shape`) is indexed at
+    flat output element e: ('contig', 0) e, ('row', P) e % P, ('col', Q)
+    e / Q, ('scalar', 0); None for other layouts."""
+    dims = [d for d in range(len(shape)) if shape[d] != 1]
+    if not dims:
+        return ("contig", 0)
+    if all(bst[d] == 0 for d in dims):
+        return ("scalar", 0)
+    cs = _contig_strides(shape)
+    if all(bst[d] == cs[d] for d in dims):
+        return ("contig", 0)
+    # row: leading broadcast dims, then contiguous over the trailing ones
+    z = 0
+    while z < len(dims) and bst[dims[z]] == 0:
+        z += 1
+    if 0 < z < len(dims):
+        trail = dims[z:]
+        inner = _contig_strides([shape[d] for d in trail])
+        if all(bst[d] == st for d, st in zip(trail, inner)):
+            return ("row", _numel([shape[d] for d in trail]))
+    # col: contiguous over the leading dims, broadcast over the trailing ones
+    z = 0
+    while z < len(dims) and bst[dims[len(dims) - 1 - z]] == 0:
+        z += 1
+    if 0 < z < len(dims):
+        lead = dims[:len(dims) - z]
+        outer = _contig_strides([shape[d] for d in lead])
+        if all(bst[d] == st for d, st in zip(lead, outer)):
+            return ("col", _numel([shape[d] for d in dims[len(dims) - z:]]))
+    return None
+
+
+def _lazy_ok(shape, args):
+    """Whether an op with output `shape` over `args` may be deferred."""
+    if not _LAZY["on"] or _numel(shape) < _LAZY["min"]:
+        return False
+    for a in args:
+        if a is None:
+            continue
+        if a._dtype != "float32":
+            return False
+        if a._st is None:
+            if a._shape != tuple(shape) and _leaf_kind(shape, _bstrides_of(a._shape, _contig_strides(a._shape), shape)) is None:
+                return False
+        elif _leaf_kind(shape, _bstrides(a, shape)) is None:
+            return False
+    return True
+
+
+def _bstrides_of(tshape, tstrides, shape):
+    nd = len(shape)
+    off = nd - len(tshape)
+    st = []
+    for d in range(nd):
+        if d < off:
+            st.append(0)
+        else:
+            sz = tshape[d - off]
+            st.append(0 if (sz == 1 and shape[d] != 1) else tstrides[d - off])
+    return st
+
+
+class _TooBig(Exception):
+    pass
+
+
+def _program(root):
+    """The tjh_expr program of deferred tensor `root` and the tensors it
+    keeps alive.  Inputs of another shape, evaluated inputs and views are
+    leaves; deferred inputs of the same shape are inlined."""
+    shape = root._shape
+    leaves, leaf_ix, code, memo = [], {}, [], {}
+
+    def leaf(a):
+        if a._st is None:
+            a._storage  # a deferred input of another shape: evaluate it
+        kind = _leaf_kind(shape, _bstrides(a, shape))
+        if kind is None:
+            a = _k_contiguous(a.expand(shape))
+            kind = ("contig", 0)
+        key = (id(a._st), a._offset, a._strides, a._shape)
+        if key not in leaf_ix:
+            if len(leaves) >= L.EXPR_MAX_LEAVES:
+                raise _TooBig()
+            leaf_ix[key] = len(leaves)
+            leaves.append((a, kind))
+        i = leaf_ix[key]
+        mk = ("leaf", i)
+        if mk not in memo:
+            code.append(("load", 0, i, None, None, 0.0))
+            memo[mk] = len(code) - 1
+        return memo[mk]
+
+    def emit(t):
+        while t._st is None and t._lz.kind == "alias":
+            t = t._lz.args[0]
+        if t._st is not None or t._shape != shape:
+            return leaf(t)
+        if id(t) in memo:
+            return memo[id(t)]
+        lz = t._lz
+        ops = [None if a is None else emit(a) for a in lz.args]
+        code.append((_EXPR_KIND[lz.kind], lz.code) + tuple(ops + [None] * (3 - len(ops))) +
+                    (lz.f,))
+        if len(code) > L.EXPR_MAX_INS:
+            raise _TooBig()
+        memo[id(t)] = len(code) - 1
+        return memo[id(t)]
+
+    result = emit(root)
+    # registers: a value's register is freed after its last use
+    last = {}
+    for i, ins in enumerate(code):
+        for v in (ins[3:5] if ins[0] == "load" else ins[2:5]):  # a load's `a` is a leaf index
+            if v is not None:
+                last[v] = i
+    free = list(range(L.EXPR_MAX_REGS))
+    reg = {}
+    prog = L.Expr()
+    for i, (op, c, a, b, cc, f) in enumerate(code):
+        srcs = [a, b, cc] if op != "load" else [b, cc]
+        for v in set(x for x in srcs if x is not None):
+            if last.get(v) == i and v != result:
+                free.append(reg[v])
+        if not free:
+            raise _TooBig()
+        free.sort()
+        r = free.pop(0)
+        reg[i] = r
+        ins = prog.ins[i]
+        ins.op = L.EXPR_OP[op]
+        ins.code = c
+        ins.dst = r
+        if op == "load":
+            ins.a = a
+            ins.b = ins.c = L.EXPR_NONE
+        else:
+            ins.a = reg[a] if a is not None else L.EXPR_NONE
+            ins.b = reg[b] if b is not None else L.EXPR_NONE
+            ins.c = reg[cc] if cc is not None else L.EXPR_NONE
+        ins.f = f
+        if last.get(i) is None and i != result:
+            free.append(r)  # never read
+    prog.n_ins = len(code)
+    prog.n_leaves = len(leaves)
+    prog.result = reg[result]
+    for k, (a, (kind, per)) in enumerate(leaves):
+        prog.leaf[k] = a.data_ptr()
+        prog.kind[k] = L.LEAF[kind]
+        prog.period[k] = per
+    return prog, [a for a, _ in leaves]
+
+
+def _program_fit(t):
+    """_program(t), evaluating the largest inlined inputs first until the
+    program fits the instruction, leaf and register limits."""
+    while True:
+        try:
+            return _program(t)
+        except _TooBig:
+            cands = [a for a in t._lz.args if a is not None and a._st is None and
+                     a._shape == t._shape]
+            if not cands:
+                raise RuntimeError("elementwise expression too large to fuse")
+            max(cands, key=lambda a: len(a._lz.deps))._storage
+
+
+def _settle(t, st):
+    """t's value now lives in `st`: record it and let the deferred values
+    that read t know its storage."""
+    t._st = st
+    t._lz = None
+    _PENDING.discard(t)
+    key = id(t)
+    for p in list(_PENDING):
+        lz = p._lz
+        if lz is not None and key in lz.deps:
+            lz.deps.add(id(st))
+
+
+def _realize(t):
+    lz = t._lz
+    if lz.kind == "alias":
+        st = lz.args[0]._storage
+        _settle(t, st)
+        return st
+    out = empty(t._shape)
+    prog, keep = _program_fit(t)
+    L.check(L.lib().tjh_expr_eval(ctypes.byref(prog), out.numel(), out.data_ptr()), "expr")
+    del keep
+    _settle(t, out._st)
+    return out._st
+
+
+def _before_write(*ts):
+    """Evaluates every deferred value that reads the storage of (or is) one
+    of `ts`, before that memory is written in place."""
+    if not _PENDING:
+        return
+    keys = set()
+    for t in ts:
+        if t is None:
+            continue
+        keys.add(id(t))
+        if t._st is not None:
+            keys.add(id(t._st))
+    for p in list(_PENDING):
+        lz = p._lz
+        if p._st is None and lz is not None and not keys.isdisjoint(lz.deps):
+            p._storage
+
+
+def _lazy_colsum(x, dims, keep=False):
+    """Sum of deferred x over one run of adjacent dims with a fused kernel
+    (keepdim layout), or None when the shape does not suit it.  With
+    `keep`, x's value is written in the same pass."""
+    shape = list(x._shape)
+    dims = sorted(set(dims))
+    if not dims or dims != list(range(dims[0], dims[-1] + 1)):
+        return None
+    beg, end = dims[0], dims[-1] + 1
+    outer, r, inner = _numel(shape[:beg]), _numel(shape[beg:end]), _numel(shape[end:])
+    if outer > 64 or r < 64 or inner < 2:
+        return None
+    try:
+        prog, keep_alive = _program_fit(x)
+    except RuntimeError:
+        return None
+    out = empty(shape[:beg] + [1] * (end - beg) + shape[end:])
+    vals = empty(x._shape) if keep else None
+    rc = L.lib().tjh_expr_colsum(ctypes.byref(prog), outer, r, inner, out.data_ptr(),
+                                 vals.data_ptr() if vals is not None else None)
+    if rc == L.ERR_UNSUPPORTED:
+        return None
+    L.check(rc, "expr_colsum")
+    del keep_alive
+    if vals is not None:
+        _settle(x, vals._st)
+    return out
+
+
 # ----------------------------------------------------------------- raw kernels
 # Non-differentiable helpers: allocate the output and launch.
 
@@ -872,6 +1206,7 @@ def _copy_into(dst, src):
     """dst[...] = src[...] for equal shapes, any strides."""
     if dst.numel() == 0:
         return
+    _before_write(dst)
     lib = L.lib()
     shp = L.i64arr(dst._shape)
     nd = len(dst._shape)
@@ -897,6 +1232,8 @@ def _k_cast(x, dtype):
 
 
 def _k_unary(op, x, alpha=0.0):
+    if _lazy_ok(x._shape, (x,)):
+        return _lazy("u", L.UNARY[op], alpha, (x,), x._shape)
     x = x.contiguous()
     out = empty(x._shape)
     L.check(L.lib().tjh_unary(L.UNARY[op], x.data_ptr(), out.data_ptr(), x.numel(), float(alpha)),
@@ -905,6 +1242,8 @@ def _k_unary(op, x, alpha=0.0):
 
 
 def _k_unary_bwd(op, g, x, y, alpha=0.0):
+    if _lazy_ok(g._shape, (g, x, y)):
+        return _lazy("ub", L.UNARY[op], alpha, (g, x, y), g._shape)
     g = g.contiguous()
     out = empty(g._shape)
     L.check(L.lib().tjh_unary_backward(
@@ -930,6 +1269,8 @@ def _bstrides(t, shape):
 
 def _k_binary(op, a, b):
     shape = _broadcast_shapes(a._shape, b._shape)
+    if _lazy_ok(shape, (a, b)):
+        return _lazy("b", L.BINARY[op], 0.0, (a, b), shape)
     out = empty(shape)
     if out.numel():
         L.check(L.lib().tjh_binary(L.BINARY[op], len(shape), L.i64arr(shape), a.data_ptr(),
@@ -939,6 +1280,9 @@ def _k_binary(op, a, b):
 
 
 def _k_ternary(op, g, a, b, shape):
+    shape = tuple(shape)
+    if _lazy_ok(shape, (g, a, b)):
+        return _lazy("t", L.TERNARY[op], 0.0, (g, a, b), shape)
     out = empty(shape)
     if out.numel():
         L.check(L.lib().tjh_ternary(L.TERNARY[op], len(shape), L.i64arr(shape), g.data_ptr(),
@@ -949,6 +1293,8 @@ def _k_ternary(op, g, a, b, shape):
 
 
 def _k_scalar(op, x, s, reverse=False):
+    if _lazy_ok(x._shape, (x,)):
+        return _lazy("sr" if reverse else "s", L.SCALAR[op], s, (x,), x._shape)
     x = x.contiguous()
     out = empty(x._shape)
     L.check(L.lib().tjh_scalar(L.SCALAR[op], x.data_ptr(), float(s), 1 if reverse else 0,
@@ -958,6 +1304,8 @@ def _k_scalar(op, x, s, reverse=False):
 
 def _k_axpy(alpha, x, y):
     """alpha*x + y (same shape)."""
+    if x._shape == y._shape and _lazy_ok(x._shape, (x, y)):
+        return _lazy("axpy", 0, alpha, (x, y), x._shape)
     x = x.contiguous()
     y = y.contiguous()
     out = empty(x._shape)
@@ -977,8 +1325,17 @@ def _reduce_runs(shape, dims):
     return runs
 
 
-def _k_reduce(op, x, dims):
-    """Reduces the given dims of x (keepdim=True layout), fp32."""
+def _k_reduce(op, x, dims, keep=False):
+    """Reduces the given dims of x (keepdim=True layout), fp32.  A sum /
+    mean of a deferred x reads x's inputs directly (and, with `keep`,
+    writes x's value in the same pass)."""
+    if op in ("sum", "mean") and _is_lazy(x) and x._lz.kind != "alias":
+        r = _lazy_colsum(x, dims, keep)
+        if r is not None:
+            if op == "mean":
+                total_r = _numel([x._shape[d] for d in set(dims)])
+                r = _k_scalar("mul", r, 1.0 / total_r if total_r else float("nan"))
+            return r
     x = x.contiguous()
     shape = list(x._shape)
     dims = sorted(set(dims))
@@ -1005,16 +1362,17 @@ def _k_reduce(op, x, dims):
     return cur
 
 
-def _sum_to(g, shape):
+def _sum_to(g, shape, keep=False):
     """Sums a broadcast gradient back to `shape` (torch.js only handles 1-D
-    against 2-D, Tensor.ts:3560-3591)."""
+    against 2-D, Tensor.ts:3560-3591).  `keep`: a deferred g is also
+    evaluated by the same pass."""
     shape = tuple(shape)
     if g._shape == shape:
         return g
     nd = g.ndim
     off = nd - len(shape)
     dims = [d for d in range(nd) if d < off or (shape[d - off] == 1 and g._shape[d] != 1)]
-    r = _k_reduce("sum", g, dims) if dims else g
+    r = _k_reduce("sum", g, dims, keep) if dims else g
     return _view_raw(r.contiguous(), shape)
 
 
@@ -1063,6 +1421,11 @@ def _binary_op(op, a, b):
     ra, rb = a.requires_grad, b.requires_grad
     if op == "add":
         def bwd(g):
+            if ra and rb and _is_lazy(g) and g.shape == ash and ash != bsh:
+                # the broadcast operand's column sum evaluates g in the same pass
+                return [g, _sum_to(g, bsh, keep=True)]
+            if ra and rb and _is_lazy(g) and g.shape == bsh and ash != bsh:
+                return [_sum_to(g, ash, keep=True), g]
             return [_sum_to(g, ash) if ra else None, _sum_to(g, bsh) if rb else None]
     elif op == "sub":
         def bwd(g):
@@ -2085,7 +2448,7 @@ def run_backward(pairs, retain_graph=False, inputs=None):
                 if defer and slot in node.defer_slots:
                     # a leaf's first gradient, finished by the next flush
                     t._grad = gi
-                    owned.add(id(gi._storage))
+                    owned.add(_skey(gi))
                     deferred.add(id(t))
                     continue
                 if acc is not None and slot == node.acc_slot:
@@ -2168,7 +2531,7 @@ def _pending_for(node, grads, wanted, owned):
         return None
     if t.grad_fn is None:
         prev = t._grad
-        if prev is None or id(prev._storage) not in owned:
+        if prev is None or _skey(prev) not in owned:
             return None
         others = [p for p in grads.values()]
     else:
@@ -2180,16 +2543,19 @@ def _pending_for(node, grads, wanted, owned):
         # a pending gradient may be the very tensor an add / sub / scalar-add
         # VJP also handed to another input, a leaf's .grad among them: the
         # VJP may add into it in place only if nothing else holds it
-        if id(prev._storage) in owned:
+        if _skey(prev) in owned:
             return None
         others = [p for key, p in grads.items() if key != id(t.grad_fn)]
     if (prev is None or isinstance(prev, _SliceGrad) or prev.shape != t.shape or
             prev._dtype != "float32" or not prev.is_contiguous()):
         return None
+    pk = _skey(prev)
     for p in others:
         pieces = p.pieces if isinstance(p, _SliceGrad) else [(0, p)]
-        if any(q._storage is prev._storage for _, q in pieces):
+        if any(_skey(q) == pk for _, q in pieces):
             return None
+    # the VJP adds into prev in place: deferred values reading it go first
+    _before_write(prev)
     return prev
 
 
@@ -2202,10 +2568,12 @@ def _leaf_accumulate(t, g, owned, force_copy=False):
     """Accumulates into t.grad.  A gradient tensor handed to a leaf is never
     shared with another leaf (the same incoming grad can flow to several
     inputs of an add), so later in-place edits of one .grad stay local."""
-    if force_copy or not g.is_contiguous() or id(g._storage) in owned:
+    if _is_lazy(g) and g._lz.kind != "alias" and not force_copy:
+        g._storage  # a deferred gradient evaluates into memory nothing else holds
+    elif force_copy or not g.is_contiguous() or _skey(g) in owned:
         g = _k_contiguous(g)
     if t._grad is None:
-        owned.add(id(g._storage))
+        owned.add(_skey(g))
         t._grad = Tensor(g._storage, g._shape, g._strides, g._offset, g._dtype)
     else:
         t._grad = _k_binary("add", t._grad, g)
