@@ -216,15 +216,36 @@ int compile_code(const std::string& src, std::string* code_out) {
   return TJH_OK;
 }
 
-// The kernel for `src` on the current device, compiled on first use.
-int get_kernel(const std::string& src, hipFunction_t* fn) {
-  const std::string key = std::to_string(device_ordinal()) + "\n" + src;
+// Compact key of everything the generated source depends on: device,
+// width, entry point, instructions (not their constants) and leaf kinds.
+std::string signature(const tjh_expr* P, int W, Mode mode) {
+  std::string k;
+  k.reserve(16 + 6 * P->n_ins + P->n_leaves);
+  k.push_back((char)device_ordinal());
+  k.push_back((char)W);
+  k.push_back((char)mode);
+  k.push_back((char)P->n_ins);
+  k.push_back((char)P->n_leaves);
+  k.push_back((char)P->result);
+  for (int i = 0; i < P->n_ins; ++i) {
+    const tjh_expr_ins& in = P->ins[i];
+    const char b[6] = {(char)in.op, (char)in.code, (char)in.dst, (char)in.a, (char)in.b, (char)in.c};
+    k.append(b, 6);
+  }
+  for (int j = 0; j < P->n_leaves; ++j) k.push_back((char)P->kind[j]);
+  return k;
+}
+
+// The kernel of program P on the current device, compiled on first use.
+int get_kernel(const tjh_expr* P, int W, Mode mode, hipFunction_t* fn) {
+  const std::string key = signature(P, W, mode);
   std::lock_guard<std::mutex> lock(g_jit_mu);
   auto it = jit_cache().find(key);
   if (it != jit_cache().end()) {
     *fn = it->second.fn;
     return TJH_OK;
   }
+  const std::string src = generate(P, W, mode);
   std::string code;
   const int rc = compile_code(src, &code);
   if (rc != TJH_OK) return rc;
@@ -275,7 +296,7 @@ int tjh_expr_eval(const tjh_expr* prog, int64_t n, float* out) {
   if (n == 0) return TJH_OK;
   TJH_ARG(out != nullptr, "tjh_expr_eval: NULL output");
   hipFunction_t fn;
-  int rc = get_kernel(generate(prog, W, kEval), &fn);
+  int rc = get_kernel(prog, W, kEval, &fn);
   if (rc != TJH_OK) return rc;
   KernelScope ks("expr");
   jit::Args a = make_args(prog);
@@ -307,7 +328,7 @@ int tjh_expr_colsum(const tjh_expr* prog, int64_t outer, int64_t r, int64_t inne
   TJH_ARG(out != nullptr, "tjh_expr_colsum: NULL output");
   if (inner % 4) W = 1;
   hipFunction_t fn;
-  int rc = get_kernel(generate(prog, W, kColsum), &fn);
+  int rc = get_kernel(prog, W, kColsum, &fn);
   if (rc != TJH_OK) return rc;
   KernelScope ks("expr_colsum");
   // the partition of the unfused sum of the materialised (aligned) value

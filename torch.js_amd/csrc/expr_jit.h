@@ -158,7 +158,7 @@ __device__ __forceinline__ void colsum_body(const F& f, const Args& a) {
   const long long c = ((long long)blockIdx.y * kBlock + threadIdx.x) * W;
   if (c >= a.inner) return;
   Kahan acc[W];
-  constexpr int U = 2;  // rows whose loads are in flight together
+  constexpr int U = 4;  // rows whose loads are in flight together
   for (long long k = r0; k < r1; k += U) {
     V<W> v[U];
 #pragma unroll

@@ -20,9 +20,11 @@ PyTorch semantics torch.js declares:
     buffer of every alias, Tensor.ts:241-251).
 """
 import ctypes
+import functools
 import math
 import numbers
 import os
+import struct
 import weakref
 
 import numpy as np
@@ -164,13 +166,18 @@ class Storage:
             self.ptr = 0
 
 
-def _contig_strides(shape):
+@functools.lru_cache(maxsize=4096)
+def _contig_strides_t(shape):
     st = [1] * len(shape)
     s = 1
     for d in range(len(shape) - 1, -1, -1):
         st[d] = s
         s *= shape[d]
     return tuple(st)
+
+
+def _contig_strides(shape):
+    return _contig_strides_t(shape if type(shape) is tuple else tuple(shape))
 
 
 def _numel(shape):
@@ -260,7 +267,7 @@ class Tensor:
                  requires_grad=False):
         self._st = storage
         self._lz = None  # a deferred elementwise op (_Lz) while _st is None
-        self._shape = tuple(int(s) for s in shape)
+        self._shape = tuple(map(int, shape))
         self._strides = tuple(strides) if strides is not None else _contig_strides(self._shape)
         self._offset = int(offset)
         self._dtype = dtype
@@ -328,7 +335,10 @@ class Tensor:
         self._grad = g
 
     def data_ptr(self):
-        return self._storage.ptr + self._offset * self.itemsize
+        st = self._st
+        if st is None:
+            st = _realize(self)
+        return st.ptr + self._offset * _DT[self._dtype][0]
 
     def is_contiguous(self):
         return self._strides == _contig_strides(self._shape) or self.numel() <= 1 or \
@@ -893,7 +903,16 @@ def _as_tensor(x, like=None):
 # TJH_LAZY=0 turns deferral off.
 
 _LAZY = {"on": os.environ.get("TJH_LAZY", "1") != "0", "min": 1 << 16}
-_PENDING = weakref.WeakSet()  # deferred tensors not yet evaluated
+_PENDING = {}  # id -> weakref of each deferred tensor not yet evaluated
+
+
+def _pend(t):
+    key = id(t)
+    _PENDING[key] = weakref.ref(t, lambda _r, k=key: _PENDING.pop(k, None))
+
+
+def _pending_tensors():
+    return [p for p in (r() for r in list(_PENDING.values())) if p is not None]
 _EXPR_KIND = {"u": "unary", "ub": "unary_bwd", "b": "binary", "t": "ternary", "s": "scalar",
               "sr": "scalar_rev", "axpy": "axpy"}
 
@@ -904,10 +923,11 @@ class _Lz:
     operand, input tensors, and `deps`: ids of the storages and deferred
     tensors its value reads (transitively)."""
 
-    __slots__ = ("kind", "code", "f", "args", "deps")
+    __slots__ = ("kind", "code", "f", "args", "kinds", "deps")
 
-    def __init__(self, kind, code, f, args, deps):
-        self.kind, self.code, self.f, self.args, self.deps = kind, code, f, args, deps
+    def __init__(self, kind, code, f, args, kinds, deps):
+        self.kind, self.code, self.f, self.args, self.kinds, self.deps = kind, code, f, args, \
+            kinds, deps
 
 
 def _is_lazy(t):
@@ -925,7 +945,12 @@ def _skey(t):
     return id(t._st)
 
 
-def _lazy(kind, code, f, args, shape):
+def _lazy(kind, code, f, args, shape, kinds=None):
+    """A deferred op over `args` with output `shape`; `kinds[i]` is how a
+    leaf argument is indexed (None: a deferred argument of the same shape,
+    inlined)."""
+    if kinds is None:
+        kinds = [None] * len(args)
     deps = set()
     for a in args:
         if a is None:
@@ -937,7 +962,7 @@ def _lazy(kind, code, f, args, shape):
             deps.add(id(a._st))
     t = Tensor.__new__(Tensor)
     t._st = None
-    t._lz = _Lz(kind, code, float(f), tuple(args), deps)
+    t._lz = _Lz(kind, code, float(f), tuple(args), tuple(kinds), deps)
     t._shape = tuple(shape)
     t._strides = _contig_strides(t._shape)
     t._offset = 0
@@ -946,7 +971,7 @@ def _lazy(kind, code, f, args, shape):
     t._grad = None
     t.grad_fn = None
     t._retains_grad = False
-    _PENDING.add(t)
+    _pend(t)
     return t
 
 
@@ -984,20 +1009,32 @@ def _leaf_kind(shape, bst):
 
 
 def _lazy_ok(shape, args):
-    """Whether an op with output `shape` over `args` may be deferred."""
+    """The leaf kinds of `args` when an op with output `shape` may be
+    deferred over them, else None."""
     if not _LAZY["on"] or _numel(shape) < _LAZY["min"]:
-        return False
+        return None
+    shape = tuple(shape)
+    kinds = []
     for a in args:
         if a is None:
+            kinds.append(None)
             continue
         if a._dtype != "float32":
-            return False
-        if a._st is None:
-            if a._shape != tuple(shape) and _leaf_kind(shape, _bstrides_of(a._shape, _contig_strides(a._shape), shape)) is None:
-                return False
-        elif _leaf_kind(shape, _bstrides(a, shape)) is None:
-            return False
-    return True
+            return None
+        if a._st is None and a._shape == shape:
+            kinds.append(None)
+            continue
+        k = _kind_of(shape, a._shape, a._strides)
+        if k is None:
+            return None
+        kinds.append(k)
+    return kinds
+
+
+@functools.lru_cache(maxsize=8192)
+def _kind_of(shape, tshape, tstrides):
+    """_leaf_kind of a (tshape, tstrides) tensor broadcast to `shape`."""
+    return _leaf_kind(shape, _bstrides_of(tshape, tstrides, shape))
 
 
 def _bstrides_of(tshape, tstrides, shape):
@@ -1023,45 +1060,73 @@ def _program(root):
     leaves; deferred inputs of the same shape are inlined."""
     shape = root._shape
     leaves, leaf_ix, code, memo = [], {}, [], {}
+    max_ins = L.EXPR_MAX_INS
 
-    def leaf(a):
-        if a._st is None:
-            a._storage  # a deferred input of another shape: evaluate it
-        kind = _leaf_kind(shape, _bstrides(a, shape))
+    def emit(t, kind):
+        st = t._st
+        while st is None:
+            lz = t._lz
+            if lz.kind != "alias":
+                break
+            t = lz.args[0]
+            st = t._st
+        if st is None and t._shape == shape:
+            v = memo.get(id(t))
+            if v is not None:
+                return v
+            lz = t._lz
+            args, kinds = lz.args, lz.kinds
+            ops = [None if a is None else emit(a, k) for a, k in zip(args, kinds)]
+            ops += [None] * (3 - len(ops))
+            code.append((_EXPR_KIND[lz.kind], lz.code, ops[0], ops[1], ops[2], lz.f))
+            if len(code) > max_ins:
+                raise _TooBig()
+            v = memo[id(t)] = len(code) - 1
+            return v
+        # a leaf: an evaluated tensor, or a deferred one of another shape
+        if st is None:
+            st = t._storage
         if kind is None:
-            a = _k_contiguous(a.expand(shape))
-            kind = ("contig", 0)
-        key = (id(a._st), a._offset, a._strides, a._shape)
-        if key not in leaf_ix:
+            kind = _kind_of(shape, t._shape, t._strides)
+            if kind is None:
+                t = _k_contiguous(t.expand(shape))
+                st, kind = t._st, ("contig", 0)
+        key = (id(st), t._offset, t._strides, t._shape)
+        i = leaf_ix.get(key)
+        if i is None:
             if len(leaves) >= L.EXPR_MAX_LEAVES:
                 raise _TooBig()
-            leaf_ix[key] = len(leaves)
-            leaves.append((a, kind))
-        i = leaf_ix[key]
-        mk = ("leaf", i)
-        if mk not in memo:
+            i = leaf_ix[key] = len(leaves)
+            leaves.append((t, kind))
+        v = memo.get(("leaf", i))
+        if v is None:
             code.append(("load", 0, i, None, None, 0.0))
-            memo[mk] = len(code) - 1
-        return memo[mk]
+            v = memo[("leaf", i)] = len(code) - 1
+        return v
 
-    def emit(t):
-        while t._st is None and t._lz.kind == "alias":
-            t = t._lz.args[0]
-        if t._st is not None or t._shape != shape:
-            return leaf(t)
-        if id(t) in memo:
-            return memo[id(t)]
-        lz = t._lz
-        ops = [None if a is None else emit(a) for a in lz.args]
-        code.append((_EXPR_KIND[lz.kind], lz.code) + tuple(ops + [None] * (3 - len(ops))) +
-                    (lz.f,))
-        if len(code) > L.EXPR_MAX_INS:
-            raise _TooBig()
-        memo[id(t)] = len(code) - 1
-        return memo[id(t)]
+    result = emit(root, None)
+    sig = (tuple(code), result, tuple(k for _, k in leaves))
+    hit = _PROGRAMS.get(sig)
+    if hit is None:
+        hit = _PROGRAMS[sig] = _pack_code(code, result)
+        if len(_PROGRAMS) > 512:
+            _PROGRAMS.pop(next(iter(_PROGRAMS)))
+    buf = bytearray(hit)
+    nl = len(leaves)
+    _EXPR_NLEAF.pack_into(buf, 4, nl)
+    if nl:
+        struct.pack_into("<%dQ" % nl, buf, _EXPR_LEAF_OFF, *[a.data_ptr() for a, _ in leaves])
+        struct.pack_into("<%dq" % nl, buf, _EXPR_PER_OFF, *[k[1] for _, k in leaves])
+        struct.pack_into("<%di" % nl, buf, _EXPR_KIND_OFF, *[L.LEAF[k[0]] for _, k in leaves])
+    return L.Expr.from_buffer(buf), [a for a, _ in leaves]
 
-    result = emit(root)
-    # registers: a value's register is freed after its last use
+
+_PROGRAMS = {}  # (code, result, leaf kinds) -> packed program without its leaves
+
+
+def _pack_code(code, result):
+    """Packs instructions with registers allocated: a value's register is
+    freed after its last use."""
     last = {}
     for i, ins in enumerate(code):
         for v in (ins[3:5] if ins[0] == "load" else ins[2:5]):  # a load's `a` is a leaf index
@@ -1069,10 +1134,11 @@ def _program(root):
                 last[v] = i
     free = list(range(L.EXPR_MAX_REGS))
     reg = {}
-    prog = L.Expr()
+    buf = bytearray(_EXPR_SIZE)
+    none = L.EXPR_NONE
+    op_ids = L.EXPR_OP
     for i, (op, c, a, b, cc, f) in enumerate(code):
-        srcs = [a, b, cc] if op != "load" else [b, cc]
-        for v in set(x for x in srcs if x is not None):
+        for v in set(x for x in ((a, b, cc) if op != "load" else (b, cc)) if x is not None):
             if last.get(v) == i and v != result:
                 free.append(reg[v])
         if not free:
@@ -1080,28 +1146,28 @@ def _program(root):
         free.sort()
         r = free.pop(0)
         reg[i] = r
-        ins = prog.ins[i]
-        ins.op = L.EXPR_OP[op]
-        ins.code = c
-        ins.dst = r
         if op == "load":
-            ins.a = a
-            ins.b = ins.c = L.EXPR_NONE
+            ra, rb, rc = a, none, none
         else:
-            ins.a = reg[a] if a is not None else L.EXPR_NONE
-            ins.b = reg[b] if b is not None else L.EXPR_NONE
-            ins.c = reg[cc] if cc is not None else L.EXPR_NONE
-        ins.f = f
+            ra = reg[a] if a is not None else none
+            rb = reg[b] if b is not None else none
+            rc = reg[cc] if cc is not None else none
+        _EXPR_INS.pack_into(buf, _EXPR_INS_OFF + _EXPR_INS.size * i, op_ids[op], c, r, ra, rb, rc, f)
         if last.get(i) is None and i != result:
             free.append(r)  # never read
-    prog.n_ins = len(code)
-    prog.n_leaves = len(leaves)
-    prog.result = reg[result]
-    for k, (a, (kind, per)) in enumerate(leaves):
-        prog.leaf[k] = a.data_ptr()
-        prog.kind[k] = L.LEAF[kind]
-        prog.period[k] = per
-    return prog, [a for a, _ in leaves]
+    _EXPR_HDR.pack_into(buf, 0, len(code), 0, reg[result], 0)
+    return bytes(buf)
+
+
+_EXPR_SIZE = ctypes.sizeof(L.Expr)
+_EXPR_HDR = struct.Struct("<4i")
+_EXPR_NLEAF = struct.Struct("<i")
+_EXPR_INS = struct.Struct("<6B2xf")
+_EXPR_INS_OFF = L.Expr.ins.offset
+_EXPR_LEAF_OFF = L.Expr.leaf.offset
+_EXPR_PER_OFF = L.Expr.period.offset
+_EXPR_KIND_OFF = L.Expr.kind.offset
+assert _EXPR_INS.size == ctypes.sizeof(L.ExprIns)
 
 
 def _program_fit(t):
@@ -1123,9 +1189,9 @@ def _settle(t, st):
     that read t know its storage."""
     t._st = st
     t._lz = None
-    _PENDING.discard(t)
     key = id(t)
-    for p in list(_PENDING):
+    _PENDING.pop(key, None)
+    for p in _pending_tensors():
         lz = p._lz
         if lz is not None and key in lz.deps:
             lz.deps.add(id(st))
@@ -1157,7 +1223,7 @@ def _before_write(*ts):
         keys.add(id(t))
         if t._st is not None:
             keys.add(id(t._st))
-    for p in list(_PENDING):
+    for p in _pending_tensors():
         lz = p._lz
         if p._st is None and lz is not None and not keys.isdisjoint(lz.deps):
             p._storage
@@ -1232,8 +1298,9 @@ def _k_cast(x, dtype):
 
 
 def _k_unary(op, x, alpha=0.0):
-    if _lazy_ok(x._shape, (x,)):
-        return _lazy("u", L.UNARY[op], alpha, (x,), x._shape)
+    k = _lazy_ok(x._shape, (x,))
+    if k is not None:
+        return _lazy("u", L.UNARY[op], alpha, (x,), x._shape, k)
     x = x.contiguous()
     out = empty(x._shape)
     L.check(L.lib().tjh_unary(L.UNARY[op], x.data_ptr(), out.data_ptr(), x.numel(), float(alpha)),
@@ -1242,8 +1309,9 @@ def _k_unary(op, x, alpha=0.0):
 
 
 def _k_unary_bwd(op, g, x, y, alpha=0.0):
-    if _lazy_ok(g._shape, (g, x, y)):
-        return _lazy("ub", L.UNARY[op], alpha, (g, x, y), g._shape)
+    k = _lazy_ok(g._shape, (g, x, y))
+    if k is not None:
+        return _lazy("ub", L.UNARY[op], alpha, (g, x, y), g._shape, k)
     g = g.contiguous()
     out = empty(g._shape)
     L.check(L.lib().tjh_unary_backward(
@@ -1269,8 +1337,9 @@ def _bstrides(t, shape):
 
 def _k_binary(op, a, b):
     shape = _broadcast_shapes(a._shape, b._shape)
-    if _lazy_ok(shape, (a, b)):
-        return _lazy("b", L.BINARY[op], 0.0, (a, b), shape)
+    k = _lazy_ok(shape, (a, b))
+    if k is not None:
+        return _lazy("b", L.BINARY[op], 0.0, (a, b), shape, k)
     out = empty(shape)
     if out.numel():
         L.check(L.lib().tjh_binary(L.BINARY[op], len(shape), L.i64arr(shape), a.data_ptr(),
@@ -1281,8 +1350,9 @@ def _k_binary(op, a, b):
 
 def _k_ternary(op, g, a, b, shape):
     shape = tuple(shape)
-    if _lazy_ok(shape, (g, a, b)):
-        return _lazy("t", L.TERNARY[op], 0.0, (g, a, b), shape)
+    k = _lazy_ok(shape, (g, a, b))
+    if k is not None:
+        return _lazy("t", L.TERNARY[op], 0.0, (g, a, b), shape, k)
     out = empty(shape)
     if out.numel():
         L.check(L.lib().tjh_ternary(L.TERNARY[op], len(shape), L.i64arr(shape), g.data_ptr(),
@@ -1293,8 +1363,9 @@ def _k_ternary(op, g, a, b, shape):
 
 
 def _k_scalar(op, x, s, reverse=False):
-    if _lazy_ok(x._shape, (x,)):
-        return _lazy("sr" if reverse else "s", L.SCALAR[op], s, (x,), x._shape)
+    k = _lazy_ok(x._shape, (x,))
+    if k is not None:
+        return _lazy("sr" if reverse else "s", L.SCALAR[op], s, (x,), x._shape, k)
     x = x.contiguous()
     out = empty(x._shape)
     L.check(L.lib().tjh_scalar(L.SCALAR[op], x.data_ptr(), float(s), 1 if reverse else 0,
@@ -1304,8 +1375,9 @@ def _k_scalar(op, x, s, reverse=False):
 
 def _k_axpy(alpha, x, y):
     """alpha*x + y (same shape)."""
-    if x._shape == y._shape and _lazy_ok(x._shape, (x, y)):
-        return _lazy("axpy", 0, alpha, (x, y), x._shape)
+    k = _lazy_ok(x._shape, (x, y)) if x._shape == y._shape else None
+    if k is not None:
+        return _lazy("axpy", 0, alpha, (x, y), x._shape, k)
     x = x.contiguous()
     y = y.contiguous()
     out = empty(x._shape)
