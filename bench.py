@@ -283,7 +283,32 @@ BLOCK_FLOPS = 3 * (2 * 8192 * (768 * 2304 + 768 * 768 + 2 * 768 * 3072) +
                    4 * 8 * 12 * 64 * (1024 * 1025 // 2))
 
 
-def _timed(torch, step, steps, warmup):
+def _replayed(torch, step, steps):
+    """Seconds per step of `step` captured in a HIP graph and replayed (all
+    of its kernels, one launch per replay), or None when it cannot be
+    captured."""
+    g = torch.hip.Graph()
+    try:
+        with torch.hip.graph(g):
+            step()
+    except Exception as e:  # a step that reads back to the host stays eager
+        print("graph capture failed: %s" % e, file=sys.stderr, flush=True)
+        return None
+    for _ in range(3):
+        g.replay()
+    torch.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        g.replay()
+    torch.synchronize()
+    el = time.perf_counter() - t0
+    g.reset()
+    return el / steps
+
+
+def _timed(torch, step, steps, warmup, graph=False):
+    """(seconds per step, per-family kernel ms).  With `graph`, the step is
+    also captured and replayed; returns (graph s, per, eager s)."""
     for _ in range(warmup):
         step()
     torch.synchronize()
@@ -293,6 +318,7 @@ def _timed(torch, step, steps, warmup):
         step()
     torch.synchronize()
     el = time.perf_counter() - t0
+    replay = _replayed(torch, step, steps) if graph else None
     # instrumented pass after the timed region: per-family kernel time
     torch.hip.kernel_timing(True)
     torch.hip.kernel_timing_reset()
@@ -302,6 +328,8 @@ def _timed(torch, step, steps, warmup):
     torch.hip.kernel_timing(False)
     per = {f: round(ms / steps, 4) for f, (n, ms) in sorted(fams.items(), key=lambda x: -x[1][1])
            if ms > 0}
+    if graph:
+        return (replay if replay is not None else el / steps), per, el / steps
     return el / steps, per
 
 
@@ -326,16 +354,20 @@ def run_config(name, steps, warmup, cpu):
         x = g.randn((64, 784))
         t = g.integers((64,), 10)
         model = W.mlp()
-        opt = torch.optim.Adam(model.parameters(), lr=1e-3)
+        # device step counters: the same update bit for bit, and capturable
+        opt = torch.optim.Adam(model.parameters(), lr=1e-3, capturable=True)
         tx, tt = torch.tensor(x), torch.tensor(t)
 
         def step():
             opt.zero_grad()
             torch.F.cross_entropy(model(tx), tt).backward()
             opt.step()
-        sec, per = _timed(torch, step, steps, warmup)
+        sec, per, eager = _timed(torch, step, steps, warmup, graph=True)
         out.update({"metric": "MLP train step samples/s", "value": round(64 / sec, 1),
                     "unit": "samples/s", "us_per_step": round(sec * 1e6, 1),
+                    "timing": ("HIP graph replay of the whole step (hip.Graph)" if sec != eager
+                               else "eager (the step could not be captured)"),
+                    "eager": {"value": round(64 / eager, 1), "us_per_step": round(eager * 1e6, 1)},
                     "roofline": {"bound": "launch", "gemm_TFLOP/s": round(MLP_FLOPS / sec / 1e12, 4),
                                  "adam_GB/s": round(MLP_ADAM_BYTES / sec / 1e9, 2)}})
         if cpu:
@@ -358,15 +390,21 @@ def run_config(name, steps, warmup, cpu):
             for t_ in (tx, tb, ty):
                 t_.grad = None
             W.chain_loss(tx, tb, ty).backward()
-        sec, per = _timed(torch, step, steps, warmup)
+        sec, per, eager = _timed(torch, step, steps, warmup, graph=True)
         out.update({"metric": "elementwise+reduction fwd+bwd GB/s (fused-minimum bytes)",
                     "value": round(CHAIN_FUSED_BYTES / sec / 1e9, 1), "unit": "GB/s",
                     "ms_per_step": round(sec * 1e3, 3),
+                    "timing": ("HIP graph replay of the whole step (hip.Graph)" if sec != eager
+                               else "eager (the step could not be captured)"),
+                    "eager": {"value": round(CHAIN_FUSED_BYTES / eager / 1e9, 1),
+                              "ms_per_step": round(eager * 1e3, 3)},
                     "roofline": {"bound": "hbm", "achieved": round(CHAIN_FUSED_BYTES / sec / 1e9, 1),
                                  "peak": HBM_PEAK_GBS, "unit": "GB/s",
                                  "frac": round(CHAIN_FUSED_BYTES / sec / 1e9 / HBM_PEAK_GBS, 3),
                                  "note": "end to end over the fused minimum (read x, y; write "
-                                         "gx, gy); the unfused pipeline moves ~4.5x that"}})
+                                         "gx, gy); the fused chain moves 576 MB: forward column "
+                                         "sum, y's gradient, x's gradient with the bias "
+                                         "column sum"}})
         if cpu:
             dt = _cpu_time(lambda: om.chain_loss_and_grads(x, b, y))
             out["cpu_baseline"] = {"value": round(CHAIN_FUSED_BYTES / dt / 1e9, 2), "unit": "GB/s",
@@ -381,9 +419,12 @@ def run_config(name, steps, warmup, cpu):
         def step():
             model.zero_grad()
             torch.F.cross_entropy(model(tx), tt).backward()
-        sec, per = _timed(torch, step, steps, warmup)
+        sec, per, eager = _timed(torch, step, steps, warmup, graph=True)
         out.update({"metric": "small CNN fwd+bwd images/s", "value": round(32 / sec, 1),
                     "unit": "images/s", "ms_per_step": round(sec * 1e3, 3),
+                    "timing": ("HIP graph replay of the whole step (hip.Graph)" if sec != eager
+                               else "eager (the step could not be captured)"),
+                    "eager": {"value": round(32 / eager, 1), "ms_per_step": round(eager * 1e3, 3)},
                     "roofline": {"bound": "mfma (conv2) / hbm (conv1)",
                                  "achieved": round(CNN_FLOPS / sec / 1e12, 2),
                                  "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",

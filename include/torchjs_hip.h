@@ -304,6 +304,28 @@ int tjh_argmax(const float* x, int64_t outer, int64_t r, int64_t inner,
                int is_min, int32_t* out);
 
 /* ------------------------------------------------------------------ */
+/* HIP graphs — no counterpart in the reference (WebGPU has no command   */
+/* replay): for callers whose steps are bound by host-side launch cost   */
+/* (small MLPs, elementwise chains), the work a step enqueues on the     */
+/* library stream is captured once and replayed with one launch.        */
+/* ------------------------------------------------------------------ */
+
+/* Starts capturing the library stream into a new graph (id in *graph).
+ * While capturing, every entry point enqueues instead of running; host
+ * copies, synchronisation, timers and nonzero are refused
+ * (TJH_ERR_UNSUPPORTED).  Memory allocated or freed during the capture
+ * belongs to the graph: it is never handed to other work until
+ * tjh_graph_destroy, so replays may rewrite it. */
+int tjh_graph_begin(int* graph);
+/* Ends the capture and instantiates the graph. */
+int tjh_graph_end(int graph);
+/* Enqueues one replay on the library stream (same pointers, same
+ * arguments as captured). */
+int tjh_graph_replay(int graph);
+/* Waits for the stream, destroys the graph and releases its memory. */
+int tjh_graph_destroy(int graph);
+
+/* ------------------------------------------------------------------ */
 /* Fused elementwise expressions — one launch for a chain of the unary / */
 /* binary / scalar / ternary ops above, which the reference runs as one */
 /* submit each (Tensor.ts _unaryOp / _binaryOp / _broadcastBinaryOp /   */
@@ -653,6 +675,18 @@ int tjh_adam_step(int n_tensors, float* const* params,
                   const int64_t* steps, double lr, double beta1,
                   double beta2, double eps, double weight_decay,
                   int decoupled);
+/* The same step with each tensor's step count in device memory
+ * (steps[i] -> int64 counter): the call advances every counter by one and
+ * takes the bias corrections of the new count from a table the host fills
+ * with the same pow as tjh_adam_step (bit-identical results), so the step
+ * can be captured in a graph and replayed.  The table for (lr, beta1,
+ * beta2) is made on the first call, which must not be inside a capture. */
+int tjh_adam_step_dev(int n_tensors, float* const* params,
+                      const float* const* grads, float* const* exp_avg,
+                      float* const* exp_avg_sq, const int64_t* numels,
+                      int64_t* const* steps, double lr, double beta1,
+                      double beta2, double eps, double weight_decay,
+                      int decoupled);
 
 #ifdef __cplusplus
 }

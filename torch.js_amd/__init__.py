@@ -19,6 +19,8 @@ import ctypes
 from . import _lib
 from . import autograd, functional, nn, optim, profiler, serialization
 from .serialization import load, save
+from .tensor import Graph as _Graph
+from .tensor import graph as _graph
 from .tensor import (Tensor, arange, cat, chunk, enable_grad, from_numpy, full, full_like,
                      inference_mode, init, is_grad_enabled, is_initialized, manual_seed, matmul,
                      multinomial, no_grad, ones, ones_like, rand, randn, set_grad_enabled, split,
@@ -44,7 +46,10 @@ def library_path():
 
 class hip:
     """Device memory statistics (torch.webgpu.memory_stats & co.,
-    src/webgpu.ts:11-51) and launch timing."""
+    src/webgpu.ts:11-51), launch timing and HIP graphs."""
+
+    Graph = _Graph
+    graph = _graph
 
     @staticmethod
     def memory_stats():

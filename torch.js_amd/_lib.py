@@ -122,6 +122,10 @@ SIGNATURES = {
     "tjh_compare": [c_int, c_int, P_i64, c_vp, P_i64, c_vp, P_i64, c_vp],
     "tjh_reduce": [c_int, c_vp, c_i64, c_i64, c_i64, c_vp],
     "tjh_expr_eval": [c_vp, c_i64, c_vp],
+    "tjh_graph_begin": [ctypes.POINTER(c_int)],
+    "tjh_graph_end": [c_int],
+    "tjh_graph_replay": [c_int],
+    "tjh_graph_destroy": [c_int],
     "tjh_expr_colsum": [c_vp, c_i64, c_i64, c_i64, c_vp, c_vp],
     "tjh_expr_compile": [c_vp, c_i64, c_int],
     "tjh_argmax": [c_vp, c_i64, c_i64, c_i64, c_int, c_vp],
@@ -175,6 +179,9 @@ SIGNATURES = {
     "tjh_adam_step": [c_int, ctypes.POINTER(c_vp), ctypes.POINTER(c_vp), ctypes.POINTER(c_vp),
                       ctypes.POINTER(c_vp), P_i64, P_i64, c_f64, c_f64, c_f64, c_f64, c_f64,
                       c_int],
+    "tjh_adam_step_dev": [c_int, ctypes.POINTER(c_vp), ctypes.POINTER(c_vp),
+                          ctypes.POINTER(c_vp), ctypes.POINTER(c_vp), P_i64,
+                          ctypes.POINTER(c_vp), c_f64, c_f64, c_f64, c_f64, c_f64, c_int],
 }
 
 _RESTYPE = {"tjh_last_error": ctypes.c_char_p, "tjh_version": ctypes.c_char_p}

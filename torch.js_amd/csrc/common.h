@@ -24,6 +24,10 @@ int num_cus();
 // scratch (norm.hip) for the current device; tjh_init calls it once.
 int noalloc_setup(int ordinal);
 
+// Whether the library stream is being captured into a HIP graph (then
+// host copies, synchronisation and timing events are refused).
+bool capturing();
+
 // Returns TJH_ERR_NOT_INITIALIZED (with message) unless tjh_init succeeded.
 int require_init();
 

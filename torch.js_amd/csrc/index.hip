@@ -538,6 +538,8 @@ int tjh_nonzero(const float* x, int ndim, const int64_t* shape, int32_t* out, in
   }
   *count = 0;
   if (n == 0) return TJH_OK;
+  if (capturing())  // the count is read back to the host
+    return set_error(TJH_ERR_UNSUPPORTED, "tjh_nonzero: not allowed while a graph is being captured");
   int64_t chunks = cdiv(n, kNzChunk);
   Scratch cs((size_t)chunks * sizeof(int64_t));
   if (!cs.ok()) return set_error(TJH_ERR_OOM, "nonzero: no scratch");

@@ -92,6 +92,13 @@ struct Allocator {
   std::multimap<size_t, void*> free_blocks;   // size -> ptr
   std::unordered_map<void*, size_t> live;     // ptr -> size
   tjh_mem_stats st{};
+  // HIP graphs: a block allocated or freed while a graph is being captured
+  // belongs to that graph (its kernels may touch it on every replay), so
+  // when free it goes back to the graph's own pool, never to other work,
+  // until the graph is destroyed.
+  int capturing = 0;                                        // graph id, 0 = none
+  std::unordered_map<void*, int> owner;                     // ptr -> graph id
+  std::unordered_map<int, std::multimap<size_t, void*>> gpool;  // graph -> free blocks
 
   void release_cached_locked() {
     for (auto& kv : free_blocks) {
@@ -113,6 +120,22 @@ static int do_malloc(size_t bytes, void** out) {
   Allocator& A = alloc();
   size_t sz = round_size(bytes);
   std::lock_guard<std::mutex> lk(A.mu);
+  if (A.capturing) {
+    // the captured graph's own free blocks first
+    auto& pool = A.gpool[A.capturing];
+    auto gi = pool.lower_bound(sz);
+    if (gi != pool.end() && gi->first <= sz + sz / 8) {
+      void* p = gi->second;
+      size_t bsz = gi->first;
+      pool.erase(gi);
+      A.live[p] = bsz;
+      A.st.active_bytes += bsz;
+      if (A.st.active_bytes > A.st.peak_bytes) A.st.peak_bytes = A.st.active_bytes;
+      A.st.allocations++;
+      *out = p;
+      return TJH_OK;
+    }
+  }
   auto it = A.free_blocks.lower_bound(sz);
   if (it != A.free_blocks.end() && it->first <= sz + sz / 8) {
     void* p = it->second;
@@ -120,6 +143,7 @@ static int do_malloc(size_t bytes, void** out) {
     A.free_blocks.erase(it);
     A.st.pooled_bytes -= bsz;
     A.live[p] = bsz;
+    if (A.capturing) A.owner[p] = A.capturing;
     A.st.active_bytes += bsz;
     if (A.st.active_bytes > A.st.peak_bytes) A.st.peak_bytes = A.st.active_bytes;
     A.st.allocations++;
@@ -128,6 +152,11 @@ static int do_malloc(size_t bytes, void** out) {
   }
   void* p = nullptr;
   hipError_t e = hipMalloc(&p, sz);
+  if (e != hipSuccess && A.capturing) {
+    (void)hipGetLastError();
+    return set_error(TJH_ERR_OOM, "out of device memory allocating %zu bytes while capturing a graph",
+                     sz);
+  }
   if (e != hipSuccess) {
     (void)hipGetLastError();
     // Out of memory: wait for the stream, drop the cache, try once more.
@@ -143,6 +172,7 @@ static int do_malloc(size_t bytes, void** out) {
     }
   }
   A.live[p] = sz;
+  if (A.capturing) A.owner[p] = A.capturing;
   A.st.active_bytes += sz;
   if (A.st.active_bytes > A.st.peak_bytes) A.st.peak_bytes = A.st.active_bytes;
   A.st.allocations++;
@@ -161,9 +191,40 @@ static int do_free(void* p) {
   size_t sz = it->second;
   A.live.erase(it);
   A.st.active_bytes -= sz;
+  int g = A.capturing;  // freed during a capture: the graph may still read it
+  auto oi = A.owner.find(p);
+  if (oi != A.owner.end()) g = oi->second;
+  if (g) {
+    A.owner[p] = g;
+    A.gpool[g].emplace(sz, p);
+    return TJH_OK;
+  }
   A.free_blocks.emplace(sz, p);
   A.st.pooled_bytes += sz;
   return TJH_OK;
+}
+
+// ---------------------------------------------------------------- graphs
+
+namespace {
+
+struct Graphs {
+  std::mutex mu;
+  int next = 1;
+  std::unordered_map<int, hipGraphExec_t> exec;
+};
+
+Graphs& graphs() {
+  static Graphs* g = new Graphs();
+  return *g;
+}
+
+}  // namespace
+
+bool capturing() {
+  Allocator& A = alloc();
+  std::lock_guard<std::mutex> lk(A.mu);
+  return A.capturing != 0;
 }
 
 void* scratch_alloc(size_t bytes) {
@@ -253,7 +314,7 @@ KernelScope::KernelScope(const char* family) : slot(-1), prev(g_open_slot) {
 KernelScope::~KernelScope() { g_open_slot = prev; }
 
 bool launch_events(hipEvent_t* start, hipEvent_t* stop) {
-  if (g_open_slot < 0) return false;
+  if (g_open_slot < 0 || capturing()) return false;
   Prof& P = prof();
   std::lock_guard<std::mutex> lk(P.mu);
   if (!P.on || g_open_slot >= (int)P.fams.size()) return false;
@@ -397,6 +458,8 @@ int tjh_get_device_info(tjh_device_info* out) {
 
 int tjh_synchronize(void) {
   TJH_REQUIRE_INIT();
+  if (capturing())
+    return set_error(TJH_ERR_UNSUPPORTED, "%s: not allowed while a graph is being captured", __func__);
   TJH_HIP(hipStreamSynchronize(g_stream));
   return TJH_OK;
 }
@@ -422,6 +485,8 @@ int tjh_memory_stats(tjh_mem_stats* out) {
 
 int tjh_empty_cache(void) {
   TJH_REQUIRE_INIT();
+  if (capturing())
+    return set_error(TJH_ERR_UNSUPPORTED, "%s: not allowed while a graph is being captured", __func__);
   TJH_HIP(hipStreamSynchronize(g_stream));
   Allocator& A = alloc();
   std::lock_guard<std::mutex> lk(A.mu);
@@ -438,6 +503,8 @@ int tjh_reset_peak(void) {
 
 int tjh_h2d(void* dst, const void* src, size_t bytes) {
   TJH_REQUIRE_INIT();
+  if (capturing())
+    return set_error(TJH_ERR_UNSUPPORTED, "%s: not allowed while a graph is being captured", __func__);
   if (bytes == 0) return TJH_OK;
   TJH_ARG(dst && src, "tjh_h2d: NULL pointer");
   // The source is pageable host memory owned by the caller: wait for the
@@ -449,6 +516,8 @@ int tjh_h2d(void* dst, const void* src, size_t bytes) {
 
 int tjh_d2h(void* dst, const void* src, size_t bytes) {
   TJH_REQUIRE_INIT();
+  if (capturing())
+    return set_error(TJH_ERR_UNSUPPORTED, "%s: not allowed while a graph is being captured", __func__);
   if (bytes == 0) return TJH_OK;
   TJH_ARG(dst && src, "tjh_d2h: NULL pointer");
   TJH_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, g_stream));
@@ -458,6 +527,8 @@ int tjh_d2h(void* dst, const void* src, size_t bytes) {
 
 int tjh_d2h_start(const void* src, size_t bytes, uint64_t* ticket) {
   TJH_REQUIRE_INIT();
+  if (capturing())
+    return set_error(TJH_ERR_UNSUPPORTED, "%s: not allowed while a graph is being captured", __func__);
   TJH_ARG(ticket, "tjh_d2h_start: ticket is NULL");
   TJH_ARG(src || bytes == 0, "tjh_d2h_start: NULL source");
   Readbacks& R = readbacks();
@@ -498,6 +569,8 @@ int tjh_d2h_start(const void* src, size_t bytes, uint64_t* ticket) {
 }
 
 int tjh_d2h_finish(uint64_t ticket, void* dst) {
+  if (capturing())
+    return set_error(TJH_ERR_UNSUPPORTED, "%s: not allowed while a graph is being captured", __func__);
   Readback rb;
   {
     Readbacks& R = readbacks();
@@ -561,6 +634,8 @@ int tjh_kprof_reset(void) {
 }
 
 int tjh_kprof_query(const char* family, int64_t* launches, double* total_ms) {
+  if (capturing())
+    return set_error(TJH_ERR_UNSUPPORTED, "%s: not allowed while a graph is being captured", __func__);
   TJH_REQUIRE_INIT();
   TJH_ARG(family && launches && total_ms, "tjh_kprof_query: NULL argument");
   TJH_HIP(hipStreamSynchronize(g_stream));
@@ -595,6 +670,8 @@ int tjh_kprof_names(char* buf, size_t buflen) {
 }
 
 int tjh_timer_start(int* id) {
+  if (capturing())
+    return set_error(TJH_ERR_UNSUPPORTED, "%s: not allowed while a graph is being captured", __func__);
   TJH_REQUIRE_INIT();
   TJH_ARG(id, "tjh_timer_start: id is NULL");
   Prof& P = prof();
@@ -616,6 +693,8 @@ int tjh_timer_start(int* id) {
 }
 
 int tjh_timer_end(int id) {
+  if (capturing())
+    return set_error(TJH_ERR_UNSUPPORTED, "%s: not allowed while a graph is being captured", __func__);
   TJH_REQUIRE_INIT();
   Prof& P = prof();
   std::lock_guard<std::mutex> lk(P.mu);
@@ -631,6 +710,8 @@ int tjh_timer_end(int id) {
 }
 
 int tjh_timer_read(int id, double* ms) {
+  if (capturing())
+    return set_error(TJH_ERR_UNSUPPORTED, "%s: not allowed while a graph is being captured", __func__);
   TJH_REQUIRE_INIT();
   TJH_ARG(ms, "tjh_timer_read: ms is NULL");
   hipEvent_t s0, e;
@@ -674,6 +755,8 @@ int tjh_mark(const char* name) {
 }
 
 int tjh_timer_stop(int id, double* ms) {
+  if (capturing())
+    return set_error(TJH_ERR_UNSUPPORTED, "%s: not allowed while a graph is being captured", __func__);
   TJH_REQUIRE_INIT();
   TJH_ARG(ms, "tjh_timer_stop: ms is NULL");
   Prof& P = prof();
@@ -690,6 +773,117 @@ int tjh_timer_stop(int id, double* ms) {
   P.spare.push_back(P.timers[id]);
   P.spare.push_back(e);
   P.timers[id] = nullptr;
+  return TJH_OK;
+}
+
+
+// ---------------------------------------------------------------- graphs
+
+int tjh_graph_begin(int* graph) {
+  TJH_REQUIRE_INIT();
+  TJH_ARG(graph, "tjh_graph_begin: graph is NULL");
+  Allocator& A = alloc();
+  {
+    std::lock_guard<std::mutex> lk(A.mu);
+    if (A.capturing) return set_error(TJH_ERR_INVALID, "tjh_graph_begin: a capture is already open");
+  }
+  int id;
+  {
+    Graphs& G = graphs();
+    std::lock_guard<std::mutex> lk(G.mu);
+    id = G.next++;
+  }
+  // relaxed: allocations (hipMalloc) stay legal while the stream captures
+  TJH_HIP(hipStreamBeginCapture(g_stream, hipStreamCaptureModeRelaxed));
+  {
+    std::lock_guard<std::mutex> lk(A.mu);
+    A.capturing = id;
+  }
+  *graph = id;
+  return TJH_OK;
+}
+
+namespace {
+// Returns graph g's free blocks to the general cache and forgets which
+// live blocks it owned (they go to the cache when freed).
+void release_graph_blocks(int g) {
+  Allocator& A = alloc();
+  std::lock_guard<std::mutex> lk(A.mu);
+  auto pi = A.gpool.find(g);
+  if (pi != A.gpool.end()) {
+    for (auto& kv : pi->second) {
+      A.free_blocks.emplace(kv.first, kv.second);
+      A.st.pooled_bytes += kv.first;
+      A.owner.erase(kv.second);
+    }
+    A.gpool.erase(pi);
+  }
+  for (auto it = A.owner.begin(); it != A.owner.end();) {
+    if (it->second == g) it = A.owner.erase(it);
+    else ++it;
+  }
+}
+}  // namespace
+
+int tjh_graph_end(int graph) {
+  TJH_REQUIRE_INIT();
+  Allocator& A = alloc();
+  {
+    std::lock_guard<std::mutex> lk(A.mu);
+    if (A.capturing != graph || graph == 0)
+      return set_error(TJH_ERR_INVALID, "tjh_graph_end: graph %d is not being captured", graph);
+  }
+  hipGraph_t g = nullptr;
+  hipError_t e = hipStreamEndCapture(g_stream, &g);
+  {
+    std::lock_guard<std::mutex> lk(A.mu);
+    A.capturing = 0;
+  }
+  hipGraphExec_t ex = nullptr;
+  if (e == hipSuccess) e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+  if (g) (void)hipGraphDestroy(g);
+  if (e != hipSuccess) {
+    (void)hipStreamSynchronize(g_stream);
+    release_graph_blocks(graph);
+    return hip_fail(e, "tjh_graph_end");
+  }
+  Graphs& G = graphs();
+  std::lock_guard<std::mutex> lk(G.mu);
+  G.exec[graph] = ex;
+  return TJH_OK;
+}
+
+int tjh_graph_replay(int graph) {
+  TJH_REQUIRE_INIT();
+  if (capturing())
+    return set_error(TJH_ERR_UNSUPPORTED, "tjh_graph_replay: not allowed while a graph is being captured");
+  hipGraphExec_t ex = nullptr;
+  {
+    Graphs& G = graphs();
+    std::lock_guard<std::mutex> lk(G.mu);
+    auto it = G.exec.find(graph);
+    if (it == G.exec.end()) return set_error(TJH_ERR_INVALID, "tjh_graph_replay: no graph %d", graph);
+    ex = it->second;
+  }
+  TJH_HIP(hipGraphLaunch(ex, g_stream));
+  return TJH_OK;
+}
+
+int tjh_graph_destroy(int graph) {
+  TJH_REQUIRE_INIT();
+  hipGraphExec_t ex = nullptr;
+  {
+    Graphs& G = graphs();
+    std::lock_guard<std::mutex> lk(G.mu);
+    auto it = G.exec.find(graph);
+    if (it == G.exec.end()) return set_error(TJH_ERR_INVALID, "tjh_graph_destroy: no graph %d", graph);
+    ex = it->second;
+    G.exec.erase(it);
+  }
+  // a replay may still be running: its blocks are released once it is done
+  TJH_HIP(hipStreamSynchronize(g_stream));
+  TJH_HIP(hipGraphExecDestroy(ex));
+  release_graph_blocks(graph);
   return TJH_OK;
 }
 

@@ -484,6 +484,35 @@ static napi_value js_expr_eval(napi_env env, napi_callback_info info) {
   return undef(env);
 }
 
+/* graphBegin() -> id; graphEnd(id); graphReplay(id); graphDestroy(id) */
+static napi_value js_graph_begin(napi_env env, napi_callback_info info) {
+  (void)info;
+  int id = 0;
+  CHECK_RC(tjh_graph_begin(&id));
+  return num(env, id);
+}
+
+static napi_value js_graph_end(napi_env env, napi_callback_info info) {
+  napi_value a[1];
+  if (!get_args(env, info, 1, a)) return NULL;
+  CHECK_RC(tjh_graph_end((int)i64(env, a[0])));
+  return undef(env);
+}
+
+static napi_value js_graph_replay(napi_env env, napi_callback_info info) {
+  napi_value a[1];
+  if (!get_args(env, info, 1, a)) return NULL;
+  CHECK_RC(tjh_graph_replay((int)i64(env, a[0])));
+  return undef(env);
+}
+
+static napi_value js_graph_destroy(napi_env env, napi_callback_info info) {
+  napi_value a[1];
+  if (!get_args(env, info, 1, a)) return NULL;
+  CHECK_RC(tjh_graph_destroy((int)i64(env, a[0])));
+  return undef(env);
+}
+
 /* exprCompile(program, n, colsum) */
 static napi_value js_expr_compile(napi_env env, napi_callback_info info) {
   napi_value a[3];
@@ -707,6 +736,35 @@ static napi_value js_adam_step(napi_env env, napi_callback_info info) {
   }
   int rc = tjh_adam_step((int)n, p, g, m, v, ne, st, f64(env, a[6]), f64(env, a[7]),
                          f64(env, a[8]), f64(env, a[9]), f64(env, a[10]), (int)i64(env, a[11]));
+  free(p); free(g); free(m); free(v); free(ne); free(st);
+  if (rc) return throw_last(env, rc);
+  return undef(env);
+}
+
+/* adamStepDev(params, grads, expAvg, expAvgSq, numels, stepCounters (device
+ * pointers to int64), lr, beta1, beta2, eps, weightDecay, decoupled) */
+static napi_value js_adam_step_dev(napi_env env, napi_callback_info info) {
+  napi_value a[12];
+  if (!get_args(env, info, 12, a)) return NULL;
+  uint32_t n = 0;
+  napi_get_array_length(env, a[0], &n);
+  float** p = (float**)calloc(n ? n : 1, sizeof(float*));
+  const float** g = (const float**)calloc(n ? n : 1, sizeof(float*));
+  float** m = (float**)calloc(n ? n : 1, sizeof(float*));
+  float** v = (float**)calloc(n ? n : 1, sizeof(float*));
+  int64_t* ne = (int64_t*)calloc(n ? n : 1, sizeof(int64_t));
+  int64_t** st = (int64_t**)calloc(n ? n : 1, sizeof(int64_t*));
+  for (uint32_t i = 0; i < n; ++i) {
+    napi_value e;
+    napi_get_element(env, a[0], i, &e); p[i] = (float*)ptr(env, e);
+    napi_get_element(env, a[1], i, &e); g[i] = (const float*)ptr(env, e);
+    napi_get_element(env, a[2], i, &e); m[i] = (float*)ptr(env, e);
+    napi_get_element(env, a[3], i, &e); v[i] = (float*)ptr(env, e);
+    napi_get_element(env, a[4], i, &e); ne[i] = i64(env, e);
+    napi_get_element(env, a[5], i, &e); st[i] = (int64_t*)ptr(env, e);
+  }
+  int rc = tjh_adam_step_dev((int)n, p, g, m, v, ne, st, f64(env, a[6]), f64(env, a[7]),
+                             f64(env, a[8]), f64(env, a[9]), f64(env, a[10]), (int)i64(env, a[11]));
   free(p); free(g); free(m); free(v); free(ne); free(st);
   if (rc) return throw_last(env, rc);
   return undef(env);
@@ -1104,6 +1162,8 @@ static napi_value init_module(napi_env env, napi_value exports) {
       FN("unaryBackward", js_unary_backward), FN("binary", js_binary), FN("scalar", js_scalar),
       FN("reduce", js_reduce), FN("exprEval", js_expr_eval), FN("exprColsum", js_expr_colsum),
       FN("exprCompile", js_expr_compile),
+      FN("graphBegin", js_graph_begin), FN("graphEnd", js_graph_end),
+      FN("graphReplay", js_graph_replay), FN("graphDestroy", js_graph_destroy),
       FN("softmaxForward", js_softmax_forward),
       FN("softmaxBackward", js_softmax_backward), FN("crossEntropyForward", js_ce_forward),
       FN("crossEntropyBackward", js_ce_backward), FN("layerNormForward", js_ln_forward),
@@ -1113,7 +1173,7 @@ static napi_value init_module(napi_env env, napi_value exports) {
       FN("flushDeferred", js_flush_deferred), FN("embeddingForward", js_emb_forward),
       FN("embeddingBackward", js_emb_backward), FN("gemm", js_gemm), FN("gemmAct", js_gemm_act),
       FN("sdpaForward", js_sdpa_forward), FN("sdpaBackward", js_sdpa_backward),
-      FN("adamStep", js_adam_step), FN("isInitialized", js_is_initialized),
+      FN("adamStep", js_adam_step), FN("adamStepDev", js_adam_step_dev), FN("isInitialized", js_is_initialized),
       FN("deviceCount", js_device_count), FN("free", js_free), FN("resetPeak", js_reset_peak),
       FN("d2d", js_d2d), FN("kprofEnable", js_kprof_enable), FN("kprofFilter", js_kprof_filter),
       FN("kprofReset", js_kprof_reset), FN("kprofQuery", js_kprof_query),

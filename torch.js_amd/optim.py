@@ -6,7 +6,7 @@ and updates in a JS loop, adam.ts:104-120), plus plain SGD.
 import ctypes
 
 from . import _lib as L
-from .tensor import Tensor, _before_write, _k_contiguous, zeros
+from .tensor import Tensor, _before_write, _k_contiguous, capturing, zeros
 
 
 class Optimizer:
@@ -56,12 +56,22 @@ class Adam(Optimizer):
 
     def __init__(self, params, options=None, **kwargs):
         o = _opts(options, kwargs, {"lr": 1e-3, "betas": (0.9, 0.999), "eps": 1e-8,
-                                    "weight_decay": self._default_wd, "amsgrad": False})
+                                    "weight_decay": self._default_wd, "amsgrad": False,
+                                    "capturable": False})
         if o["amsgrad"]:
             raise NotImplementedError("AMSGrad not yet fully implemented")  # adam.ts:93
         super().__init__(params, o)
 
     def step(self):
+        """One update (adam.ts:96-120).  With capturable=True every
+        parameter's step count lives in device memory and the step can be
+        captured in a hip.Graph (take one step eagerly first: the moments
+        and the count are created then)."""
+        if capturing() and not all(g.get("capturable") for g in self.param_groups):
+            # the bias corrections use the step count, a host value that a
+            # replay would repeat
+            raise RuntimeError("Adam / AdamW steps are captured in a graph only with "
+                               "capturable=True")
         lib = L.lib()
         # the step writes parameters (and their moments) in place: deferred
         # values that read them are evaluated first
@@ -74,8 +84,12 @@ class Adam(Optimizer):
                     continue
                 st = self.state.get(id(p))
                 if st is None:
+                    if capturing():
+                        raise RuntimeError("take one Adam step before capturing it in a graph")
                     st = {"step": 0, "exp_avg": zeros(p.shape), "exp_avg_sq": zeros(p.shape),
                           "param": p}
+                    if g.get("capturable"):
+                        st["step_dev"] = zeros((2,), dtype="int32")  # one int64 counter
                     self.state[id(p)] = st
                 st["step"] += 1
                 if not p.is_contiguous():
@@ -87,11 +101,18 @@ class Adam(Optimizer):
                 ms.append(st["exp_avg"].data_ptr())
                 vs.append(st["exp_avg_sq"].data_ptr())
                 ns.append(p.numel())
-                steps.append(st["step"])
+                steps.append(st["step_dev"].data_ptr() if g.get("capturable") else st["step"])
             if not ps:
                 continue
             n = len(ps)
             arr = lambda xs: (ctypes.c_void_p * n)(*xs)
+            if g.get("capturable"):
+                L.check(lib.tjh_adam_step_dev(n, arr(ps), arr(gs), arr(ms), arr(vs),
+                                              (ctypes.c_int64 * n)(*ns), arr(steps),
+                                              float(g["lr"]), float(b1), float(b2),
+                                              float(g["eps"]), float(g["weight_decay"]),
+                                              self._decoupled), "adam_step")
+                continue
             L.check(lib.tjh_adam_step(n, arr(ps), arr(gs), arr(ms), arr(vs),
                                       (ctypes.c_int64 * n)(*ns), (ctypes.c_int64 * n)(*steps),
                                       float(g["lr"]), float(b1), float(b2), float(g["eps"]),

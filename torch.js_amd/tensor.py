@@ -923,11 +923,12 @@ class _Lz:
     operand, input tensors, and `deps`: ids of the storages and deferred
     tensors its value reads (transitively)."""
 
-    __slots__ = ("kind", "code", "f", "args", "kinds", "deps")
+    __slots__ = ("kind", "code", "f", "args", "kinds", "deps", "name")
 
-    def __init__(self, kind, code, f, args, kinds, deps):
+    def __init__(self, kind, code, f, args, kinds, deps, name=None):
         self.kind, self.code, self.f, self.args, self.kinds, self.deps = kind, code, f, args, \
             kinds, deps
+        self.name = name  # op name of the single-op kernel
 
 
 def _is_lazy(t):
@@ -945,7 +946,7 @@ def _skey(t):
     return id(t._st)
 
 
-def _lazy(kind, code, f, args, shape, kinds=None):
+def _lazy(kind, code, f, args, shape, kinds=None, name=None):
     """A deferred op over `args` with output `shape`; `kinds[i]` is how a
     leaf argument is indexed (None: a deferred argument of the same shape,
     inlined)."""
@@ -962,7 +963,7 @@ def _lazy(kind, code, f, args, shape, kinds=None):
             deps.add(id(a._st))
     t = Tensor.__new__(Tensor)
     t._st = None
-    t._lz = _Lz(kind, code, float(f), tuple(args), tuple(kinds), deps)
+    t._lz = _Lz(kind, code, float(f), tuple(args), tuple(kinds), deps, name)
     t._shape = tuple(shape)
     t._strides = _contig_strides(t._shape)
     t._offset = 0
@@ -1203,6 +1204,11 @@ def _realize(t):
         st = lz.args[0]._storage
         _settle(t, st)
         return st
+    if lz.name is not None and all(a is None or a._st is not None for a in lz.args):
+        # one op over evaluated inputs: its own single-op kernel
+        out = _EAGER[lz.kind](lz, t._shape)
+        _settle(t, out._st)
+        return out._st
     out = empty(t._shape)
     prog, keep = _program_fit(t)
     L.check(L.lib().tjh_expr_eval(ctypes.byref(prog), out.numel(), out.data_ptr()), "expr")
@@ -1258,6 +1264,88 @@ def _lazy_colsum(x, dims, keep=False):
     return out
 
 
+# ----------------------------------------------------------------- HIP graphs
+
+_CAPTURE = {"on": False}  # a Graph is capturing the library stream
+
+
+def capturing():
+    return _CAPTURE["on"]
+
+
+class Graph:
+    """A HIP graph of the work one region enqueues on the library stream
+    (in the manner of torch.cuda.CUDAGraph; torch.js has no replay): run
+    the region a few times eagerly, capture it once with `graph(g)`, then
+    `g.replay()` re-runs all of its kernels with one launch and no host
+    work.  Tensors the region created keep their memory across replays
+    (replays rewrite it in place), and tensors it read are read again, so
+    new inputs go in with copy_.  Readbacks, host copies and
+    synchronisation inside the region raise."""
+
+    def __init__(self):
+        self._id = None
+
+    def capture_begin(self):
+        if self._id is not None:
+            raise RuntimeError("this graph has already been captured")
+        gid = ctypes.c_int(0)
+        L.check(L.lib().tjh_graph_begin(ctypes.byref(gid)), "graph_begin")
+        self._id = gid.value
+        _CAPTURE["on"] = True
+
+    def capture_end(self):
+        # deferred values the region created are computed inside the graph
+        try:
+            for p in _pending_tensors():
+                if p._st is None:
+                    p._storage
+        finally:
+            _CAPTURE["on"] = False
+        L.check(L.lib().tjh_graph_end(self._id), "graph_end")
+
+    def replay(self):
+        if self._id is None:
+            raise RuntimeError("replay of a graph that was never captured")
+        L.check(L.lib().tjh_graph_replay(self._id), "graph_replay")
+
+    def reset(self):
+        if self._id is not None:
+            gid, self._id = self._id, None
+            L.check(L.lib().tjh_graph_destroy(gid), "graph_destroy")
+
+    def __del__(self):
+        try:
+            self.reset()
+        except Exception:
+            pass
+
+
+class graph:
+    """`with graph(g):` captures the region into Graph g."""
+
+    def __init__(self, g):
+        self.g = g
+
+    def __enter__(self):
+        self.g.capture_begin()
+        return self.g
+
+    def __exit__(self, et, ev, tb):
+        if et is None:
+            self.g.capture_end()
+            return False
+        # a failed capture is ended and dropped; the error propagates
+        _CAPTURE["on"] = False
+        if self.g._id is not None:
+            try:
+                L.lib().tjh_graph_end(self.g._id)
+                L.lib().tjh_graph_destroy(self.g._id)
+            finally:
+                self.g._id = None
+        return False
+
+
 # ----------------------------------------------------------------- raw kernels
 # Non-differentiable helpers: allocate the output and launch.
 
@@ -1300,7 +1388,11 @@ def _k_cast(x, dtype):
 def _k_unary(op, x, alpha=0.0):
     k = _lazy_ok(x._shape, (x,))
     if k is not None:
-        return _lazy("u", L.UNARY[op], alpha, (x,), x._shape, k)
+        return _lazy("u", L.UNARY[op], alpha, (x,), x._shape, k, op)
+    return _e_unary(op, x, alpha)
+
+
+def _e_unary(op, x, alpha=0.0):
     x = x.contiguous()
     out = empty(x._shape)
     L.check(L.lib().tjh_unary(L.UNARY[op], x.data_ptr(), out.data_ptr(), x.numel(), float(alpha)),
@@ -1311,7 +1403,11 @@ def _k_unary(op, x, alpha=0.0):
 def _k_unary_bwd(op, g, x, y, alpha=0.0):
     k = _lazy_ok(g._shape, (g, x, y))
     if k is not None:
-        return _lazy("ub", L.UNARY[op], alpha, (g, x, y), g._shape, k)
+        return _lazy("ub", L.UNARY[op], alpha, (g, x, y), g._shape, k, op)
+    return _e_unary_bwd(op, g, x, y, alpha)
+
+
+def _e_unary_bwd(op, g, x, y, alpha=0.0):
     g = g.contiguous()
     out = empty(g._shape)
     L.check(L.lib().tjh_unary_backward(
@@ -1339,7 +1435,11 @@ def _k_binary(op, a, b):
     shape = _broadcast_shapes(a._shape, b._shape)
     k = _lazy_ok(shape, (a, b))
     if k is not None:
-        return _lazy("b", L.BINARY[op], 0.0, (a, b), shape, k)
+        return _lazy("b", L.BINARY[op], 0.0, (a, b), shape, k, op)
+    return _e_binary(op, a, b, shape)
+
+
+def _e_binary(op, a, b, shape):
     out = empty(shape)
     if out.numel():
         L.check(L.lib().tjh_binary(L.BINARY[op], len(shape), L.i64arr(shape), a.data_ptr(),
@@ -1352,7 +1452,11 @@ def _k_ternary(op, g, a, b, shape):
     shape = tuple(shape)
     k = _lazy_ok(shape, (g, a, b))
     if k is not None:
-        return _lazy("t", L.TERNARY[op], 0.0, (g, a, b), shape, k)
+        return _lazy("t", L.TERNARY[op], 0.0, (g, a, b), shape, k, op)
+    return _e_ternary(op, g, a, b, shape)
+
+
+def _e_ternary(op, g, a, b, shape):
     out = empty(shape)
     if out.numel():
         L.check(L.lib().tjh_ternary(L.TERNARY[op], len(shape), L.i64arr(shape), g.data_ptr(),
@@ -1365,7 +1469,11 @@ def _k_ternary(op, g, a, b, shape):
 def _k_scalar(op, x, s, reverse=False):
     k = _lazy_ok(x._shape, (x,))
     if k is not None:
-        return _lazy("sr" if reverse else "s", L.SCALAR[op], s, (x,), x._shape, k)
+        return _lazy("sr" if reverse else "s", L.SCALAR[op], s, (x,), x._shape, k, op)
+    return _e_scalar(op, x, s, reverse)
+
+
+def _e_scalar(op, x, s, reverse=False):
     x = x.contiguous()
     out = empty(x._shape)
     L.check(L.lib().tjh_scalar(L.SCALAR[op], x.data_ptr(), float(s), 1 if reverse else 0,
@@ -1377,13 +1485,29 @@ def _k_axpy(alpha, x, y):
     """alpha*x + y (same shape)."""
     k = _lazy_ok(x._shape, (x, y)) if x._shape == y._shape else None
     if k is not None:
-        return _lazy("axpy", 0, alpha, (x, y), x._shape, k)
+        return _lazy("axpy", 0, alpha, (x, y), x._shape, k, "axpy")
+    return _e_axpy(alpha, x, y)
+
+
+def _e_axpy(alpha, x, y):
     x = x.contiguous()
     y = y.contiguous()
     out = empty(x._shape)
     L.check(L.lib().tjh_axpy(float(alpha), x.data_ptr(), y.data_ptr(), out.data_ptr(), x.numel()),
             "axpy")
     return out
+
+
+# single-op kernels of deferred ops (by _Lz.kind)
+_EAGER = {
+    "u": lambda lz, shape: _e_unary(lz.name, lz.args[0], lz.f),
+    "ub": lambda lz, shape: _e_unary_bwd(lz.name, *lz.args, alpha=lz.f),
+    "b": lambda lz, shape: _e_binary(lz.name, lz.args[0], lz.args[1], shape),
+    "t": lambda lz, shape: _e_ternary(lz.name, *lz.args, shape),
+    "s": lambda lz, shape: _e_scalar(lz.name, lz.args[0], lz.f, False),
+    "sr": lambda lz, shape: _e_scalar(lz.name, lz.args[0], lz.f, True),
+    "axpy": lambda lz, shape: _e_axpy(lz.f, lz.args[0], lz.args[1]),
+}
 
 
 def _reduce_runs(shape, dims):
