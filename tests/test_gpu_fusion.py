@@ -223,3 +223,36 @@ def test_long_chains_and_many_leaves(torch, T, both):
 
     fused, plain = both(run)
     _same(fused, plain)
+
+
+def test_compile_failure_falls_back_to_single_op_kernels(torch, T, capsys):
+    """When the fused kernels cannot be compiled, deferred values are
+    evaluated op by op with the single-op kernels (same bits) and fusion
+    turns itself off."""
+    import __graft_entry__ as ge
+    L = sys.modules[ge.PKG_NAME + "._lib"]
+    real = L.lib()
+
+    class NoCompiler:
+        def __getattr__(self, name):
+            if name in ("tjh_expr_eval", "tjh_expr_colsum"):
+                return lambda *a: 4  # TJH_ERR_HIP
+            if name == "tjh_last_error":
+                return lambda: b"tjh_expr: compile failed (HIPRTC_ERROR_COMPILATION): test"
+            return getattr(real, name)
+
+    xs, ys = _rand((512, 512), 91), _rand((512,), 92)
+    _mode(T, True)
+    x, y = torch.tensor(xs), torch.tensor(ys)
+    want = [((x + y).tanh() * 2.0).numpy(), ((x * y).exp() - x).sum(0).numpy()]
+    saved_lib, saved = L.lib, dict(T._LAZY)
+    try:
+        L.lib = lambda: NoCompiler()
+        got = [((x + y).tanh() * 2.0).numpy(), ((x * y).exp() - x).sum(0).numpy()]
+        assert T._LAZY["jit"] is False and T._LAZY["on"] is False
+        assert "one kernel each" in capsys.readouterr().err
+    finally:
+        L.lib = saved_lib
+        T._LAZY.clear()
+        T._LAZY.update(saved)
+    _same(got, want)

@@ -902,7 +902,7 @@ def _as_tensor(x, like=None):
 # evaluated (_before_write), so a deferred value never sees a later write.
 # TJH_LAZY=0 turns deferral off.
 
-_LAZY = {"on": os.environ.get("TJH_LAZY", "1") != "0", "min": 1 << 16}
+_LAZY = {"on": os.environ.get("TJH_LAZY", "1") != "0", "min": 1 << 16, "jit": True}
 _PENDING = {}  # id -> weakref of each deferred tensor not yet evaluated
 
 
@@ -1209,10 +1209,40 @@ def _realize(t):
         out = _EAGER[lz.kind](lz, t._shape)
         _settle(t, out._st)
         return out._st
+    if not _LAZY["jit"]:
+        return _realize_op_by_op(t)
     out = empty(t._shape)
     prog, keep = _program_fit(t)
-    L.check(L.lib().tjh_expr_eval(ctypes.byref(prog), out.numel(), out.data_ptr()), "expr")
+    rc = L.lib().tjh_expr_eval(ctypes.byref(prog), out.numel(), out.data_ptr())
+    if rc and _jit_failed(rc):
+        return _realize_op_by_op(t)
+    L.check(rc, "expr")
     del keep
+    _settle(t, out._st)
+    return out._st
+
+
+def _jit_failed(rc):
+    """A fused kernel could not be compiled (hipRTC unavailable): warn once
+    and evaluate deferred values op by op with the single-op kernels."""
+    msg = (L.lib().tjh_last_error() or b"").decode(errors="replace")
+    if "compile failed" not in msg and "hiprtc" not in msg:
+        return False
+    if _LAZY["jit"]:
+        import sys
+        print("torchjs_amd: fused elementwise kernels unavailable (%s); running elementwise "
+              "ops one kernel each" % msg[:200], file=sys.stderr)
+    _LAZY["jit"] = False
+    _LAZY["on"] = False
+    return True
+
+
+def _realize_op_by_op(t):
+    lz = t._lz
+    for a in lz.args:
+        if a is not None and a._st is None:
+            a._storage
+    out = _EAGER[lz.kind](lz, t._shape)
     _settle(t, out._st)
     return out._st
 
@@ -1239,6 +1269,8 @@ def _lazy_colsum(x, dims, keep=False):
     """Sum of deferred x over one run of adjacent dims with a fused kernel
     (keepdim layout), or None when the shape does not suit it.  With
     `keep`, x's value is written in the same pass."""
+    if not _LAZY["jit"]:
+        return None
     shape = list(x._shape)
     dims = sorted(set(dims))
     if not dims or dims != list(range(dims[0], dims[-1] + 1)):
@@ -1255,7 +1287,7 @@ def _lazy_colsum(x, dims, keep=False):
     vals = empty(x._shape) if keep else None
     rc = L.lib().tjh_expr_colsum(ctypes.byref(prog), outer, r, inner, out.data_ptr(),
                                  vals.data_ptr() if vals is not None else None)
-    if rc == L.ERR_UNSUPPORTED:
+    if rc == L.ERR_UNSUPPORTED or (rc and _jit_failed(rc)):
         return None
     L.check(rc, "expr_colsum")
     del keep_alive
