@@ -327,15 +327,19 @@ def test_layer_norm(torch, rows, cols):
 
 
 @pytest.mark.parametrize("V,D,n", [(50257, 768, 8192), (7, 4, 6), (1000, 9, 20000), (3, 64, 1),
-                                   (70, 16, 16384), (300000, 8, 16384)])
+                                   (70, 16, 16384), (300000, 8, 16384), (1024, 768, 1024),
+                                   (5000, 4, 70000)])
 def test_embedding(torch, V, D, n):
-    """Lookup and deterministic scatter-add backward; n <= 16384 with
-    V * n <= 2^32 sorts the (id, position) keys by rank in one launch, the
-    rest by the bitonic network."""
+    """Lookup and deterministic scatter-add backward.  Index lists up to
+    65536 long are summed by workgroups that own row ranges (a row hit more
+    often than one LDS list holds is summed in position chunks), longer ones
+    after the bitonic sort.  Every row is the float32 sum of its dout rows in
+    increasing position order, so the result equals np.add.at's bit for bit
+    and untouched rows are exactly zero."""
     r = np.random.default_rng(V + n)
     w = f32(r.standard_normal((V, D)))
     ids = r.integers(0, V, n).astype(np.int32)
-    ids[: n // 3] = ids[0]  # a long run of one id
+    ids[: n // 3] = ids[0] if n else 0  # a long run of one id
     wt = torch.tensor(w, requires_grad=True)
     out = torch.F.embedding(torch.tensor(ids), wt)
     assert np.array_equal(out.numpy(), w[ids])  # a gather: bit-exact
@@ -347,12 +351,34 @@ def test_embedding(torch, V, D, n):
     assert np.all(got[untouched] == 0)  # exactly the referenced rows are written
     ref32 = np.zeros((V, D), np.float32)
     np.add.at(ref32, ids, g)  # float32 sums in position order
+    assert np.array_equal(got, ref32)
     check_floor(got, want, ref32)
     # deterministic
     wt.grad = None
     out2 = torch.F.embedding(torch.tensor(ids), wt)
     out2.backward(torch.tensor(g))
     assert np.array_equal(wt.grad.numpy(), got)
+
+
+@pytest.mark.parametrize("V,D,n", [(50257, 768, 8192), (1024, 768, 1024), (40, 5, 3000),
+                                   (600, 8, 70000)])
+def test_embedding_backward_accumulates_in_position_order(torch, V, D, n):
+    """tjh_embedding_backward with accumulate = 1 (a table tied to the LM
+    head): each referenced row becomes prior + dout rows in increasing
+    position order, bit for bit; the other rows keep their prior values."""
+    from torchjs_amd import _lib as L
+    r = np.random.default_rng(n + 5)
+    prior = f32(r.standard_normal((V, D)))
+    ids = r.integers(-3, V + 3, n).astype(np.int32)  # out-of-range ids clamp
+    ids[n // 2: n // 2 + n // 4] = V // 2
+    g = f32(r.standard_normal((n, D)))
+    dw = torch.tensor(prior)
+    gt, it = torch.tensor(g), torch.tensor(ids)
+    rc = L.lib().tjh_embedding_backward(gt.data_ptr(), it.data_ptr(), n, D, dw.data_ptr(), V, 1)
+    assert rc == 0, L.lib().tjh_last_error()
+    want = prior.copy()
+    np.add.at(want, np.clip(ids, 0, V - 1), g)
+    assert np.array_equal(dw.numpy(), want)
 
 
 def test_embedding_tied_to_lm_head(torch):

@@ -2,6 +2,7 @@
 
     python torch.js_amd/build.py            # library + addon
     python torch.js_amd/build.py --lib-only
+    python torch.js_amd/build.py --changed  # only sources newer than their objects
 
 Every HIP source under csrc/ is compiled by hipcc for gfx950 into
 _build/*.o (in parallel) and linked into torch.js_amd/libtorchjs_hip.so.
@@ -45,20 +46,37 @@ def _run(cmd):
     return out
 
 
+def _obj(src):
+    return os.path.join(BUILD, os.path.basename(src).replace(".hip", ".o"))
+
+
 def _compile(src):
-    obj = os.path.join(BUILD, os.path.basename(src).replace(".hip", ".o"))
+    obj = _obj(src)
     _run([HIPCC] + HIP_FLAGS + ["-c", src, "-o", obj])
     return obj
 
 
-def build_library(jobs=None):
+def _stale(src, headers_mtime):
+    obj = _obj(src)
+    if not os.path.exists(obj):
+        return True
+    return os.path.getmtime(obj) < max(os.path.getmtime(src), headers_mtime)
+
+
+def build_library(jobs=None, changed_only=False):
     os.makedirs(BUILD, exist_ok=True)
     sources = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
     if not sources:
         raise RuntimeError("no HIP sources under %s" % CSRC)
-    jobs = jobs or min(len(sources), max(1, min(8, os.cpu_count() or 1)))
+    todo = sources
+    if changed_only:
+        hdrs = glob.glob(os.path.join(CSRC, "*.h")) + glob.glob(os.path.join(INCLUDE, "*.h"))
+        hm = max([os.path.getmtime(h) for h in hdrs] or [0.0])
+        todo = [s for s in sources if _stale(s, hm)]
+    jobs = jobs or min(max(1, len(todo)), max(1, min(8, os.cpu_count() or 1)))
     with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(_compile, sources))
+        list(ex.map(_compile, todo))
+    objs = [_obj(s) for s in sources]
     tmp = LIB + ".tmp"
     # roctx (rocprofiler-sdk) for the named ranges of record_function,
     # hipRTC for the fused expression kernels compiled at run time
@@ -83,7 +101,7 @@ def build_addon():
 
 
 def main(argv):
-    lib = build_library()
+    lib = build_library(changed_only="--changed" in argv)
     print("built", lib)
     if "--lib-only" not in argv and os.path.exists(ADDON_SRC):
         addon = build_addon()

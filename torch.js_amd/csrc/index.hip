@@ -10,10 +10,12 @@
 // (Tensor.ts:1323-1345: row-major coordinates).  The reference runs
 // gather / one_hot / nonzero on the host after a readback.
 //
-// Embedding backward is deterministic: (id, position) pairs are sorted as
-// 64-bit keys with a bitonic network (LDS-resident 2048-element stages and
-// global merge stages), then each run of equal ids is summed by one wave
-// in increasing position order.
+// Embedding backward is deterministic: every table row is the sum of its
+// dout rows in increasing position order.  Short index lists are handled by
+// workgroups that each own a range of table rows (k_emb_bwd_owned); long
+// ones sort (id, position) pairs as 64-bit keys with a bitonic network
+// (LDS-resident 2048-element stages and global merge stages) and sum each
+// run of equal ids with one wave.
 
 #include "common.h"
 
@@ -58,94 +60,257 @@ __global__ __launch_bounds__(kBlock) void k_make_keys(const int32_t* __restrict_
   keys[i] = i < n ? (((uint64_t)clamp_id(ids[i], num)) << 32) | (uint64_t)i : ~0ull;
 }
 
-// Sorting a short index list in one workgroup: an LSD radix sort of
-// 32-bit keys clamp(id) << pos_bits | position, held in LDS, over the id
-// bits only, 8 bits per pass.  A pass is stable: each of the 16 waves owns
-// a contiguous block of positions; per-wave digit histograms are scanned in
-// (digit, wave) order, and each wave scatters its block in position order,
-// 64 keys at a time, a key's rank among same-digit lanes coming from
-// ballots.  So equal ids keep increasing positions (the summation order of
-// the backward) and the result is the same on every run.  n <= 16384 and
-// pos_bits + id bits <= 32 (vocabularies up to 2^18 at n = 16384).
-constexpr int kLdsSortMax = 16384;
-constexpr int kLdsSortThreads = 1024;
-constexpr int kLdsSortWaves = kLdsSortThreads / 64;
+// Embedding backward over owned row ranges, for index lists up to
+// kOwnMaxN: workgroup g owns the table rows [g*span, (g+1)*span).  It reads
+// the whole id list (from L2 after the first workgroups), collects the
+// positions that hit its rows in position order into an LDS list (ballot
+// ranks: hits are rare, so a round costs a few instructions per id), orders
+// the list by row with a stable counting sort, and then spreads the (row,
+// column) work of the rows that have entries over all threads: each output
+// element is its prior value (accumulate) or zero plus the row's dout
+// elements in increasing position order.  When not accumulating, rows
+// without entries are written as zeros, so no separate fill runs.  A list
+// longer than the LDS holds is processed in consecutive position chunks,
+// each adding into what the previous chunk stored; a float32 store and
+// reload is exact, so every sum is the one of a single pass in increasing
+// position order, and the result is the same on every run.
+constexpr int kOwnThreads = 256;
+constexpr int kOwnWaves = kOwnThreads / 64;
+constexpr int kOwnCap = 1024;       // list entries per chunk (>= one round's hits)
+constexpr int kOwnMaxSpan = 1024;   // rows per workgroup
+constexpr int kOwnGroups = 1024;    // workgroups while span <= kOwnMaxSpan
+constexpr int64_t kOwnMaxN = 65536;
+constexpr int64_t kOwnMaxScan = int64_t(1) << 25;  // id reads over all workgroups
+constexpr int kOwnRound = 4 * kOwnThreads;          // positions per compaction round
+constexpr int kOwnSub = 8;                          // rounds loaded together
+constexpr int kOwnBatch = 8;                        // output elements per thread in flight
 
-__global__ __launch_bounds__(kLdsSortThreads) void k_sort_ids_lds(
-    const int32_t* __restrict__ ids, int n, int64_t num, int pos_bits, int passes,
-    uint64_t* __restrict__ keys_out) {
-  __shared__ uint32_t buf[2][kLdsSortMax];
-  __shared__ uint32_t hist[kLdsSortWaves][256];
-  __shared__ uint32_t wsum[kLdsSortWaves];
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  for (int i = tid; i < n; i += kLdsSortThreads)
-    buf[0][i] = ((uint32_t)clamp_id(ids[i], num) << pos_bits) | (uint32_t)i;
-  // wave w owns positions [beg, end), a multiple of 64 long
-  const int per = ((n + kLdsSortWaves - 1) / kLdsSortWaves + 63) & ~63;
-  const int beg = w * per < n ? w * per : n;
-  const int end = beg + per < n ? beg + per : n;
-  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  int src = 0;
-  __syncthreads();
-  for (int p = 0; p < passes; ++p) {
-    const int shift = pos_bits + 8 * p;
-    const uint32_t* a = buf[src];
-    uint32_t* b = buf[src ^ 1];
-    for (int d = lane; d < 256; d += 64) hist[w][d] = 0;
-    __syncthreads();
-    for (int e = beg + lane; e < end; e += 64) atomicAdd(&hist[w][(a[e] >> shift) & 255u], 1u);
-    __syncthreads();
-    // exclusive scan in (digit, wave) order: entry q = d * 16 + wave
-    uint32_t v[4], t = 0;
+// ids[p .. p+3] (entries at or past n read as 0, unused); one 128-bit load
+// when the list is 16-byte aligned (p is a multiple of 4)
+__device__ __forceinline__ void load_ids4(const int32_t* __restrict__ ids, int n, int p,
+                                          int vec, int (&v)[4]) {
+  if (vec && p + 3 < n) {
+    const int4 q = *reinterpret_cast<const int4*>(ids + p);
+    v[0] = q.x;
+    v[1] = q.y;
+    v[2] = q.z;
+    v[3] = q.w;
+  } else {
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int q = 4 * tid + k;
-      v[k] = hist[q & (kLdsSortWaves - 1)][q >> 4];
-      t += v[k];
-    }
-    uint32_t incl = t;  // inclusive scan of the thread totals within the wave
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const uint32_t o = __shfl_up(incl, off, 64);
-      if (lane >= off) incl += o;
-    }
-    if (lane == 63) wsum[w] = incl;
-    __syncthreads();
-    uint32_t wbase = 0;
-    for (int k = 0; k < w; ++k) wbase += wsum[k];
-    uint32_t run = wbase + incl - t;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int q = 4 * tid + k;
-      hist[q & (kLdsSortWaves - 1)][q >> 4] = run;
-      run += v[k];
-    }
-    __syncthreads();
-    // stable scatter of the wave's block, 64 keys at a time, in order
-    for (int c = beg; c < end; c += 64) {
-      const int e = c + lane;
-      const bool valid = e < end;
-      const uint32_t key = valid ? a[e] : 0u;
-      const uint32_t d = (key >> shift) & 255u;
-      uint64_t peers = __ballot(valid);
-#pragma unroll
-      for (int bit = 0; bit < 8; ++bit) {
-        const uint64_t m = __ballot(valid && ((d >> bit) & 1u));
-        peers &= ((d >> bit) & 1u) ? m : ~m;
-      }
-      const uint32_t rank = (uint32_t)__popcll(peers & lt_mask);
-      const uint32_t base = valid ? hist[w][d] : 0u;
-      if (valid) b[base + rank] = key;
-      // the lowest peer advances the digit's cursor (every peer has read it)
-      if (valid && (peers & lt_mask) == 0) hist[w][d] = base + (uint32_t)__popcll(peers);
-    }
-    __syncthreads();
-    src ^= 1;
+    for (int k = 0; k < 4; ++k) v[k] = p + k < n ? ids[p + k] : 0;
   }
-  const uint32_t pmask = (1u << pos_bits) - 1u;
-  for (int i = tid; i < n; i += kLdsSortThreads) {
-    const uint32_t k = buf[src][i];
-    keys_out[i] = ((uint64_t)(k >> pos_bits) << 32) | (uint64_t)(k & pmask);
+}
+
+// Lanes below this one whose bit is set in a wave-wide mask.
+__device__ __forceinline__ int lanes_below(uint64_t m) {
+  return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                        __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
+template <bool VEC>
+struct EmbUnit;
+template <>
+struct EmbUnit<true> {
+  typedef float4 T;
+  static __device__ __forceinline__ T zero() { return make_float4(0.f, 0.f, 0.f, 0.f); }
+  static __device__ __forceinline__ void add(T& a, const T& b) {
+    a.x += b.x;
+    a.y += b.y;
+    a.z += b.z;
+    a.w += b.w;
+  }
+};
+template <>
+struct EmbUnit<false> {
+  typedef float T;
+  static __device__ __forceinline__ T zero() { return 0.f; }
+  static __device__ __forceinline__ void add(T& a, const T& b) { a += b; }
+};
+
+template <bool VEC>
+__global__ __launch_bounds__(kOwnThreads) void k_emb_bwd_owned(
+    const int32_t* __restrict__ ids, int n, int ids_vec, int num, int span, int span_bits,
+    const float* __restrict__ dout, int units, float* __restrict__ dw, int accumulate) {
+  typedef EmbUnit<VEC> U;
+  typedef typename U::T T;
+  __shared__ uint32_t lpos[kOwnCap];     // list: positions, in position order
+  __shared__ uint32_t lrow[kOwnCap];     // list: row within the range
+  __shared__ uint32_t spos[kOwnCap];     // positions ordered by (row, position)
+  __shared__ uint32_t cur[kOwnMaxSpan];  // per row: start, then end, of its entries
+  __shared__ uint32_t rows[kOwnMaxSpan]; // the rows to write, in order
+  __shared__ uint32_t wcnt[kOwnSub * kOwnWaves];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int lo = (int)blockIdx.x * span;
+  const int nrows = num - lo < span ? num - lo : span;  // >= 1 by the grid
+  const T* __restrict__ src = reinterpret_cast<const T*>(dout);
+  T* __restrict__ dst = reinterpret_cast<T*>(dw);
+  int scan = 0;
+  for (int chunk = 0;; ++chunk) {
+    // 1. the positions from `scan` on that hit rows [lo, lo + nrows), in
+    // order.  A super-round covers kOwnSub rounds of 1024 positions (four
+    // consecutive ones per thread per round), all loaded at once so the
+    // workgroup waits for one memory latency, and appends them after one
+    // barrier: the rounds whose hits still fit in the list are appended, the
+    // rest are read again by the next chunk (a round has at most kOwnCap
+    // hits, so every chunk makes progress)
+    int L = 0;
+    bool full = false;
+    while (scan < n && !full) {
+      int idv[kOwnSub][4];
+#pragma unroll
+      for (int j = 0; j < kOwnSub; ++j)
+        load_ids4(ids, n, scan + j * kOwnRound + 4 * tid, ids_vec, idv[j]);
+      uint32_t hitm[kOwnSub];
+      int pre[kOwnSub];
+#pragma unroll
+      for (int j = 0; j < kOwnSub; ++j) {
+        const int p0 = scan + j * kOwnRound + 4 * tid;
+        uint32_t m = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int r = min(max(idv[j][k], 0), num - 1) - lo;
+          idv[j][k] = r;
+          m |= (p0 + k < n && (uint32_t)r < (uint32_t)nrows) ? (1u << k) : 0u;
+        }
+        // rank of this thread's first hit: hits of the lower lanes
+        int below = 0, tot = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const uint64_t b = __ballot((m >> k) & 1u);
+          below += lanes_below(b);
+          tot += (int)__popcll(b);
+        }
+        hitm[j] = m;
+        pre[j] = below;
+        if (lane == 0) wcnt[j * kOwnWaves + w] = (uint32_t)tot;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < kOwnSub; ++j) {
+        if (scan >= n) break;  // uniform over the workgroup
+        int before = 0, total = 0;
+#pragma unroll
+        for (int k = 0; k < kOwnWaves; ++k) {
+          const int t = (int)wcnt[j * kOwnWaves + k];
+          before += k < w ? t : 0;
+          total += t;
+        }
+        if (L + total > kOwnCap) {
+          full = true;
+          break;
+        }
+        if (hitm[j]) {
+          const int p0 = scan + 4 * tid;
+          int at = L + before + pre[j];
+#pragma unroll
+          for (int k = 0; k < 4; ++k)
+            if ((hitm[j] >> k) & 1u) {
+              lpos[at] = (uint32_t)(p0 + k);
+              lrow[at] = (uint32_t)idv[j][k];
+              ++at;
+            }
+        }
+        L += total;
+        scan += kOwnRound;
+      }
+      __syncthreads();  // wcnt is written again by the next super-round
+    }
+    const bool acc = accumulate || chunk > 0;
+    if (L == 0 && acc) break;  // nothing (more) hits these rows
+    // 2. stable counting sort of the list by row: counts, then one scan that
+    // gives each row's start and the list of rows to write (rows with
+    // entries; every row when zero rows are written too)
+    for (int i = tid; i < nrows; i += kOwnThreads) cur[i] = 0u;
+    __syncthreads();
+    for (int e = tid; e < L; e += kOwnThreads) atomicAdd(&cur[lrow[e]], 1u);
+    __syncthreads();
+    int nwrite;
+    {
+      const int per = (nrows + kOwnThreads - 1) / kOwnThreads;  // <= 4
+      const int b0 = tid * per;
+      uint32_t v = 0;  // entries (low 16 bits) and rows to write (high 16)
+      for (int i = 0; i < per; ++i)
+        if (b0 + i < nrows) {
+          const uint32_t c = cur[b0 + i];
+          v += c + ((c || !acc) ? 0x10000u : 0u);
+        }
+      uint32_t incl = v;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t o = __shfl_up(incl, off, 64);
+        if (lane >= off) incl += o;
+      }
+      if (lane == 63) wcnt[w] = incl;
+      __syncthreads();
+      uint32_t run = incl - v, all = 0;
+      for (int k = 0; k < kOwnWaves; ++k) {
+        run += k < w ? wcnt[k] : 0u;
+        all += wcnt[k];
+      }
+      nwrite = (int)(all >> 16);
+      for (int i = 0; i < per; ++i)
+        if (b0 + i < nrows) {
+          const uint32_t c = cur[b0 + i];
+          cur[b0 + i] = run & 0xffffu;
+          if (c || !acc) rows[run >> 16] = (uint32_t)(b0 + i);
+          run += c + ((c || !acc) ? 0x10000u : 0u);
+        }
+    }
+    __syncthreads();
+    // scatter by one wave, 64 entries at a time in list order; a lane's rank
+    // among the lanes of the same row comes from ballots over the row bits,
+    // and the lowest such lane advances the row's cursor after every lane
+    // has read it (one wave's LDS accesses execute in program order)
+    if (w == 0) {
+      for (int c = 0; c < L; c += 64) {
+        const int e = c + lane;
+        const bool valid = e < L;
+        const uint32_t r = valid ? lrow[e] : 0u;
+        uint64_t peers = __ballot(valid);
+        for (int bit = 0; bit < span_bits; ++bit) {
+          const uint64_t m = __ballot(valid && ((r >> bit) & 1u));
+          peers &= ((r >> bit) & 1u) ? m : ~m;
+        }
+        const int rank = lanes_below(peers);
+        const uint32_t base = valid ? cur[r] : 0u;
+        if (valid) spos[base + rank] = lpos[e];
+        if (valid && rank == 0) cur[r] = base + (uint32_t)__popcll(peers);
+      }
+    }
+    __syncthreads();
+    // 3. element (row slot, column) of the rows to write, kOwnBatch per
+    // thread in flight; row r's entries are spos[cur[r-1] .. cur[r])
+    const int items = nwrite * units;
+    for (int i0 = tid; i0 < items; i0 += kOwnThreads * kOwnBatch) {
+      T s[kOwnBatch];
+      int beg[kOwnBatch], cnt[kOwnBatch], col[kOwnBatch], row[kOwnBatch];
+      int maxc = 0;
+#pragma unroll
+      for (int b = 0; b < kOwnBatch; ++b) {
+        const int i = i0 + b * kOwnThreads;
+        cnt[b] = -1;
+        s[b] = U::zero();
+        if (i < items) {
+          const int slot = i / units;
+          col[b] = i - slot * units;
+          row[b] = (int)rows[slot];
+          beg[b] = row[b] ? (int)cur[row[b] - 1] : 0;
+          cnt[b] = (int)cur[row[b]] - beg[b];
+          if (acc) s[b] = dst[(int64_t)(lo + row[b]) * units + col[b]];
+          maxc = max(maxc, cnt[b]);
+        }
+      }
+      for (int k = 0; k < maxc; ++k) {
+#pragma unroll
+        for (int b = 0; b < kOwnBatch; ++b)
+          if (k < cnt[b]) U::add(s[b], src[(int64_t)spos[beg[b] + k] * units + col[b]]);
+      }
+#pragma unroll
+      for (int b = 0; b < kOwnBatch; ++b)
+        if (cnt[b] >= 0) dst[(int64_t)(lo + row[b]) * units + col[b]] = s[b];
+    }
+    __syncthreads();  // the LDS lists are rebuilt by the next chunk
+    if (scan >= n) break;
   }
 }
 
@@ -400,51 +565,65 @@ int tjh_embedding_backward(const float* dout, const int32_t* ids, int64_t n, int
   TJH_REQUIRE_INIT();
   TJH_ARG(num > 0 && dim >= 0 && n >= 0, "tjh_embedding_backward: bad sizes");
   TJH_ARG(n < (int64_t(1) << 32), "tjh_embedding_backward: too many indices");
+  if (dim == 0) return TJH_OK;
+  const bool vec = dim % 4 == 0 && ((uintptr_t)dout & 15) == 0 && ((uintptr_t)dweight & 15) == 0;
+  // short lists (a batch of token positions): each workgroup sums the rows
+  // it owns in one launch, zero rows included
+  int64_t span = cdiv(num, (int64_t)kOwnGroups);
+  if (span > kOwnMaxSpan) span = kOwnMaxSpan;
+  const int64_t groups = cdiv(num, span);
+  const int64_t units = vec ? dim / 4 : dim;
+  if (n > 0 && n <= kOwnMaxN && groups * n <= kOwnMaxScan && num < (int64_t(1) << 31) &&
+      span * units < (int64_t(1) << 31)) {
+    int span_bits = 0;
+    while ((int64_t(1) << span_bits) < span) ++span_bits;
+    const int ids_vec = ((uintptr_t)ids & 15) == 0;
+    KernelScope ks("embedding_bwd");
+    if (vec)
+      tjh_launch(k_emb_bwd_owned<true>, dim3((unsigned)groups), dim3(kOwnThreads), 0, stream(),
+                 ids, (int)n, ids_vec, (int)num, (int)span, span_bits, dout, (int)units, dweight,
+                 accumulate);
+    else
+      tjh_launch(k_emb_bwd_owned<false>, dim3((unsigned)groups), dim3(kOwnThreads), 0,
+                 stream(), ids, (int)n, ids_vec, (int)num, (int)span, span_bits, dout,
+                 (int)units, dweight, accumulate);
+    return check_launch("embedding_backward");
+  }
   if (!accumulate) {
     int rc = tjh_fill_f32(dweight, num * dim, 0.f);
     if (rc != TJH_OK) return rc;
   }
-  if (n == 0 || dim == 0) return TJH_OK;
-  // short lists (a batch of token positions) are radix-sorted in LDS by one
-  // workgroup; longer ones (or ids too wide to pack) by the bitonic network
-  int pos_bits = 1, id_bits = 1;
-  while ((int64_t(1) << pos_bits) < n) ++pos_bits;
-  while ((int64_t(1) << id_bits) < num) ++id_bits;
-  const bool lds_sort = n <= kLdsSortMax && pos_bits + id_bits <= 32;
+  if (n == 0) return TJH_OK;
+  // long lists: (id, position) keys sorted by the bitonic network, then one
+  // wave per run of equal ids
   int64_t npad = 1;
   while (npad < n) npad <<= 1;
   if (npad < 2) npad = 2;
-  Scratch keys_s((size_t)(lds_sort ? n : npad) * sizeof(uint64_t));
+  Scratch keys_s((size_t)npad * sizeof(uint64_t));
   if (!keys_s.ok()) return set_error(TJH_ERR_OOM, "embedding_backward: no scratch");
   uint64_t* keys = keys_s.as<uint64_t>();
   KernelScope ks("embedding_bwd");
-  if (lds_sort) {
-    tjh_launch(k_sort_ids_lds, dim3(1), dim3(kLdsSortThreads), 0, stream(), ids, (int)n, num,
-               pos_bits, (id_bits + 7) / 8, keys);
-  } else {
-    tjh_launch(k_make_keys, dim3((unsigned)cdiv(npad, kBlock)), dim3(kBlock), 0, stream(),
-                       ids, n, num, npad, keys);
-    unsigned chunks = (unsigned)cdiv(npad, kSortChunk);
-    tjh_launch(k_bitonic_local<true>, dim3(chunks), dim3(kSortThreads), 0, stream(), keys,
-                       npad, (int64_t)0);
-    for (int64_t k = 2 * kSortChunk; k <= npad; k <<= 1) {
-      for (int64_t j = k >> 1; j >= kSortChunk; j >>= 1)
-        tjh_launch(k_bitonic_global, dim3((unsigned)cdiv(npad / 2, kBlock)), dim3(kBlock),
-                           0, stream(), keys, npad, k, j);
-      tjh_launch(k_bitonic_local<false>, dim3(chunks), dim3(kSortThreads), 0, stream(),
-                         keys, npad, k);
-    }
+  tjh_launch(k_make_keys, dim3((unsigned)cdiv(npad, kBlock)), dim3(kBlock), 0, stream(), ids, n,
+             num, npad, keys);
+  unsigned chunks = (unsigned)cdiv(npad, kSortChunk);
+  tjh_launch(k_bitonic_local<true>, dim3(chunks), dim3(kSortThreads), 0, stream(), keys, npad,
+             (int64_t)0);
+  for (int64_t k = 2 * kSortChunk; k <= npad; k <<= 1) {
+    for (int64_t j = k >> 1; j >= kSortChunk; j >>= 1)
+      tjh_launch(k_bitonic_global, dim3((unsigned)cdiv(npad / 2, kBlock)), dim3(kBlock), 0,
+                 stream(), keys, npad, k, j);
+    tjh_launch(k_bitonic_local<false>, dim3(chunks), dim3(kSortThreads), 0, stream(), keys, npad,
+               k);
   }
   int rc = check_launch("embedding_backward_sort");
   if (rc != TJH_OK) return rc;
-  bool vec = dim % 4 == 0 && ((uintptr_t)dout & 15) == 0 && ((uintptr_t)dweight & 15) == 0;
   unsigned g = (unsigned)cdiv(n, kBlock / 64);
   if (vec)
     tjh_launch(k_emb_bwd_runs<true>, dim3(g), dim3(kBlock), 0, stream(), keys, n, dout, dim,
-                       dweight, 1);
+               dweight, 1);
   else
-    tjh_launch(k_emb_bwd_runs<false>, dim3(g), dim3(kBlock), 0, stream(), keys, n, dout,
-                       dim, dweight, 1);
+    tjh_launch(k_emb_bwd_runs<false>, dim3(g), dim3(kBlock), 0, stream(), keys, n, dout, dim,
+               dweight, 1);
   return check_launch("embedding_backward");
 }
 
