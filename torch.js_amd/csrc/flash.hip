@@ -23,10 +23,12 @@
 //   per query in base 2, O^T += V^T P^T; lse written for the backward.
 // Backward (deterministic, no atomics): D = rowsum(dO*O); a key-block
 //   kernel accumulates dV^T = dO^T P and dK^T = Q^T dS (lane <-> key) and
-//   stores each 32x32 block of dS; a query-block kernel accumulates
-//   dQ^T = K^T dS^T (lane <-> query) from those blocks, so S and dP are
-//   computed once (when the blocks cannot be allocated, the query kernel
-//   recomputes them instead).
+//   stores each 32x32 block of dS, the products of each 32-key group split
+//   over a pair of waves (P and dV / dS and dK); a query-block kernel
+//   accumulates dQ^T = K^T dS^T (lane <-> query) from those blocks, so S
+//   and dP are computed once (when the blocks cannot be allocated, a
+//   four-product key-block kernel runs and the query kernel recomputes S
+//   and dP instead).
 // Causal masking (key > query masked, top-left aligned) skips every
 // 32x32 tile that is entirely masked and masks element-wise only on tiles
 // that cross the diagonal or the end of the sequence.
@@ -82,6 +84,7 @@ struct FlashArgs {
   // [b*H + h][query tile][key tile][32 x 32], or null (dQ recomputes dS)
   float* dsblk;
   int nqt, nkt;       // 32-row query / key tiles per (b, h)
+  int64_t spare_blk;  // index of the spare block after the last one
 };
 
 // Column of key offset ko (0..31) inside a dS block row: the query-block
@@ -369,7 +372,9 @@ __global__ __launch_bounds__(256) void k_flash_dsum4(FlashArgs a, float* __restr
   if (sub == 0) dsum[r] = x;
 }
 
-// Key-block kernel: dK, dV for 128 keys per workgroup (32 per wave).
+// Key-block kernel: dK, dV for 128 keys per workgroup (32 per wave), each
+// wave forming all four products; the path taken when the dS blocks cannot
+// be allocated (the query-block kernel then recomputes S and dP).
 // GUARD: Tq or Tk is not a multiple of 32.
 template <bool GUARD>
 __global__ __launch_bounds__(256, 2) void k_flash_dkv(FlashArgs a) {
@@ -456,16 +461,6 @@ __global__ __launch_bounds__(256, 2) void k_flash_dkv(FlashArgs a) {
       lds_cols(Qs[cur], l32, h, ct);
 #pragma unroll
       for (int j = 0; j < 16; ++j) dp[j] *= p[j];  // dS
-      if (a.dsblk) {
-        // this lane's key column of the (query tile, key tile) dS block;
-        // masked entries are 0, so the block is complete.  Non-temporal:
-        // the blocks are read once, by the next kernel
-        float* blk = a.dsblk +
-                     (((int64_t)bh * a.nqt + qq0 / TILE) * a.nkt + k0 / TILE) * (TILE * TILE) +
-                     ds_col(l32);
-#pragma unroll
-        for (int j = 0; j < 16; ++j) __builtin_nontemporal_store(dp[j], blk + kappa(j, h) * TILE);
-      }
 #pragma unroll
       for (int s = 0; s < 16; ++s) {  // dK^T += Q^T dS
         dk0 = mfma(ct[0][s], dp[s], dk0);
@@ -676,6 +671,163 @@ __global__ __launch_bounds__(512, 1) void k_flash_dq_ds8(FlashArgs a) {
     __syncthreads();  // the one barrier inside write_rows
 }
 
+// Key-block kernel with the work of each 32-key group split over a pair of
+// waves: wave A holds the group's K rows and forms P = exp2(S - lse) (S =
+// Q K^T), hands P over through LDS and accumulates dV^T += dO^T P; wave B
+// holds the V rows, forms dP - D = dO V^T - D, then dS = P * (dP - D),
+// stores the dS block and accumulates dK^T += Q^T dS.  A workgroup of four
+// waves covers 64 keys (two pairs).  Each wave holds half the registers of
+// a wave that does all four products, so three workgroups fit on a CU
+// (three waves per SIMD).  Each query tile takes two barriers: P is
+// written before the middle one and read after it.  B stores its dS block
+// at the end of the step, after the wait for the next tile's prefetch, so
+// that wait never waits for the stores.  GUARD: Tq or Tk is not a multiple
+// of 32.
+constexpr int PROWS = 64;  // keys per workgroup
+template <bool GUARD, bool STORE>
+__global__ __launch_bounds__(256, 3) void k_flash_dkv_pair(FlashArgs a) {
+  __shared__ __attribute__((aligned(16))) float Qs[2][TILE * LDSW];
+  __shared__ __attribute__((aligned(16))) float Gs[2][TILE * LDSW];
+  __shared__ __attribute__((aligned(16))) float Ps[2][16 * 64];
+  // the three workgroups of a CU run at different wave priorities, so they
+  // do not fall into step (identical workgroups sharing the matrix pipe
+  // fairly finish their MFMA phases together and then leave it idle
+  // together): measured 5% faster than equal priorities
+  if (blockIdx.x % 3 == 0) __builtin_amdgcn_s_setprio(2);
+  else if (blockIdx.x % 3 == 1) __builtin_amdgcn_s_setprio(1);
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int role = wv >> 1, pr = wv & 1;  // role 0: A (P, dV), 1: B (dS, dK)
+  const int l32 = lane & 31, h = lane >> 5;
+  const int64_t nbh = (int64_t)gridDim.x / a.nblk;
+  const int g = balanced_rank(blockIdx.x, gridDim.x, a.cus);
+  const int64_t bh = g % nbh;
+  const int kblk = (int)(g / nbh);  // long (causal) blocks rank first
+  const int64_t b = bh / a.H, hh = bh % a.H;
+  const float* Q = a.q + b * a.qs.b + hh * a.qs.h;
+  const float* K = a.k + b * a.ks.b + hh * a.ks.h;
+  const float* V = a.v + b * a.vs.b + hh * a.vs.h;
+  const float* G = a.dout + b * a.gs.b + hh * a.gs.h;
+  const float* L = role == 0 ? a.lse + bh * a.Tq : a.dsum + bh * a.Tq;
+  const int k0 = kblk * PROWS + pr * TILE;  // the pair's first key
+  const int mykey = k0 + l32;
+
+  // A: K rows (scaled to base-2 logits); B: V rows
+  float kv[32];
+  if (role == 0)
+    gl_row32(K, a.ks.t, mykey, a.Tk, h, a.scale * kLog2e, kv);
+  else
+    gl_row32(V, a.vs.t, mykey, a.Tk, h, 1.0f, kv);
+  // complete the loads here: a wait for them inside the loop would also
+  // wait for every step's prefetch
+#pragma unroll
+  for (int i = 0; i < 32; ++i) asm volatile("" : "+v"(kv[i]));
+  floatx16 acc0 = zero16(), acc1 = zero16();  // A: dV^T, B: dK^T
+  const float one = h == 0 ? 1.f : 0.f;
+  // row offset of a query tile: A -lse*log2e, B -D (loaded by every lane,
+  // the index clamped into range, with the tile; formed after the step)
+  const float omul = role == 0 ? -kLog2e : -1.f;
+  auto row_raw = [&](int qq0) { return L[min(qq0 + l32, a.Tq - 1)]; };
+  auto row_fix = [&](int qq0, float raw) {
+    const bool in = !GUARD || qq0 + l32 < a.Tq;
+    return (h == 0 && in) ? raw * omul : 0.f;
+  };
+
+  const int qstart = a.causal ? kblk * PROWS : 0;
+  const int nqb = qstart < a.Tq ? (a.Tq - qstart + TILE - 1) / TILE : 0;
+  floatx4 rq[2], rg[2];
+  float off = 0.f, raw_n = 0.f;
+  if (nqb > 0) {
+    load_tile<GUARD>(Q, a.qs.t, qstart, a.Tq, rq);
+    load_tile<GUARD>(G, a.gs.t, qstart, a.Tq, rg);
+    raw_n = row_raw(qstart);
+    store_tile(Qs[0], rq);
+    store_tile(Gs[0], rg);
+    off = row_fix(qstart, raw_n);
+  }
+  __syncthreads();
+  float* pbuf = Ps[pr];
+  for (int qi = 0; qi < nqb; ++qi) {
+    const int cur = qi & 1;
+    const bool more = qi + 1 < nqb;
+    const int qq0 = qstart + qi * TILE;
+    if (more) {
+      load_tile<GUARD>(Q, a.qs.t, qq0 + TILE, a.Tq, rq);
+      load_tile<GUARD>(G, a.gs.t, qq0 + TILE, a.Tq, rg);
+      raw_n = row_raw(qq0 + TILE);
+    }
+    const bool skip = (a.causal && qq0 + TILE - 1 < k0) || k0 >= a.Tk;
+    const bool edge = (a.causal && qq0 < k0 + TILE - 1) || (GUARD && qq0 + TILE > a.Tq);
+    floatx16 x = zero16();  // A: P; B: dP - D, then dS
+    if (!skip) {
+      float xa[32];
+      // A: S[q][key] - lse[q] from Q rows; B: dP[q][key] - D[q] from dO rows
+      lds_row32(role == 0 ? Qs[cur] : Gs[cur], l32, h, xa);
+      x = chain(off, one, xa, kv);
+      if (role == 0) {
+        if (edge) {
+#pragma unroll
+          for (int j = 0; j < 16; ++j) {
+            const int q = qq0 + kappa(j, h);
+            const bool ok = (!GUARD || q < a.Tq) && (!a.causal || mykey <= q);
+            x[j] = ok ? exp2_hw(x[j]) : 0.f;
+          }
+        } else {
+#pragma unroll
+          for (int j = 0; j < 16; ++j) x[j] = exp2_hw(x[j]);
+        }
+#pragma unroll
+        for (int j = 0; j < 16; ++j) pbuf[j * 64 + lane] = x[j];
+      }
+    }
+    __syncthreads();
+    if (!skip) {
+      float ct[2][16];
+      if (role == 0) {
+        lds_cols(Gs[cur], l32, h, ct);
+#pragma unroll
+        for (int s = 0; s < 16; ++s) {  // dV^T += dO^T P
+          acc0 = mfma(ct[0][s], x[s], acc0);
+          acc1 = mfma(ct[1][s], x[s], acc1);
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) x[j] *= pbuf[j * 64 + lane];  // dS (0 where masked)
+        lds_cols(Qs[cur], l32, h, ct);
+#pragma unroll
+        for (int s = 0; s < 16; ++s) {  // dK^T += Q^T dS
+          acc0 = mfma(ct[0][s], x[s], acc0);
+          acc1 = mfma(ct[1][s], x[s], acc1);
+        }
+      }
+    }
+    if (more) {
+      store_tile(Qs[cur ^ 1], rq);
+      store_tile(Gs[cur ^ 1], rg);
+      off = row_fix(qq0 + TILE, raw_n);
+    }
+    if (STORE && role == 1) {
+      // this lane's key column of the (query tile, key tile) dS block, on
+      // every step (masked blocks hold zeros; a pair past the last key
+      // writes the spare block).  Non-temporal: read once, by the
+      // query-block kernel
+      const int64_t blk_id = k0 < a.Tk ? ((int64_t)bh * a.nqt + qq0 / TILE) * a.nkt + k0 / TILE
+                                       : a.spare_blk;
+      float* blk = a.dsblk + blk_id * (TILE * TILE) + ds_col(l32);
+#pragma unroll
+      for (int j = 0; j < 16; ++j) __builtin_nontemporal_store(x[j], blk + kappa(j, h) * TILE);
+    }
+    __syncthreads();
+  }
+  float* buf = (wv < 2 ? Qs[wv] : Gs[wv - 2]);
+  if (role == 0) {
+    float* dvb = a.out2 + b * a.o2s.b + hh * a.o2s.h;
+    write_rows(buf, acc0, acc1, 1.0f, dvb, a.o2s.t, k0, a.Tk, l32, h, lane);
+  } else {
+    float* dkb = a.out + b * a.o1s.b + hh * a.o1s.h;
+    write_rows(buf, acc0, acc1, a.scale, dkb, a.o1s.t, k0, a.Tk, l32, h, lane);
+  }
+}
+
 bool rows_ok(const int64_t* s, const void* p) {
   // D contiguous, 16-byte aligned rows
   return ((uintptr_t)p & 15) == 0 && (s[0] % 4) == 0 && (s[1] % 4) == 0 && (s[2] % 4) == 0;
@@ -750,16 +902,27 @@ int flash_backward(const float* q, const float* k, const float* v, const float* 
   // TJH_SDPA_RECOMPUTE=1 (read on every call) forces the recomputing path
   const char* rec = getenv("TJH_SDPA_RECOMPUTE");
   const bool want_blocks = !(rec && rec[0] == '1');
-  Scratch dsb(want_blocks ? (size_t)(B * H) * a.nqt * a.nkt * (TILE * TILE) * sizeof(float) : 0);
+  a.spare_blk = (int64_t)(B * H) * a.nqt * a.nkt;
+  Scratch dsb(want_blocks ? (size_t)(a.spare_blk + 1) * (TILE * TILE) * sizeof(float) : 0);
   a.dsblk = dsb.ok() ? dsb.as<float>() : nullptr;
-  // keys: dK, dV
-  a.nblk = (int)cdiv(Tk, ROWS);
+  // keys: dK, dV (the paired-wave kernel, which also stores the dS blocks;
+  // without blocks, the four-product kernel)
   a.out = dk; a.out2 = dv; a.o1s = s3(st[6]); a.o2s = s3(st[7]);
-  const unsigned gk = (unsigned)(B * H * a.nblk);
-  if (ragged)
-    tjh_launch(k_flash_dkv<true>, dim3(gk), dim3(256), 0, stream(), a);
-  else
-    tjh_launch(k_flash_dkv<false>, dim3(gk), dim3(256), 0, stream(), a);
+  if (a.dsblk) {
+    a.nblk = (int)cdiv(Tk, PROWS);
+    const unsigned gk = (unsigned)(B * H * a.nblk);
+    if (ragged)
+      tjh_launch(k_flash_dkv_pair<true, true>, dim3(gk), dim3(256), 0, stream(), a);
+    else
+      tjh_launch(k_flash_dkv_pair<false, true>, dim3(gk), dim3(256), 0, stream(), a);
+  } else {
+    a.nblk = (int)cdiv(Tk, ROWS);
+    const unsigned gk = (unsigned)(B * H * a.nblk);
+    if (ragged)
+      tjh_launch(k_flash_dkv<true>, dim3(gk), dim3(256), 0, stream(), a);
+    else
+      tjh_launch(k_flash_dkv<false>, dim3(gk), dim3(256), 0, stream(), a);
+  }
   rc = check_launch("flash_dkv");
   if (rc != TJH_OK) return rc;
   // queries: dQ from the stored dS blocks, or recomputed when the blocks
