@@ -501,10 +501,11 @@ int64_t choose_splits(int64_t tiles, int64_t K, int cus) {
 // (CU fill) x tile speed.  TJH_GEMM_TILE=BMxBN forces a tile (read on every
 // call, so a test can sweep the tiles in one process).  The 8-wave 256x128
 // tile needs more K splits than 128x128 for the same fill, which doubles
-// the split-sum traffic: it is taken only with no K split or K >= 16384
-// (measured in the GPT-2 step: the split weight gradients and 768-wide
-// input gradients ran 3-8% slower with it; the LM head's three products and
-// the MLP's 3072-wide GEMMs 2-5% faster).
+// the split-sum traffic: it is taken only with no K split (measured on the
+// GPT-2 products, the best of three interleaved runs each: the split
+// weight gradients and 768-wide input gradients run 3-8% slower with it,
+// the LM head's K-split input gradient (K = 50257) 3.4% slower, 6.45
+// against 6.23 ms; the MLP's 3072-wide GEMMs 2-5% faster).
 Plan choose_plan(int64_t M, int64_t N, int64_t K, int64_t batch, int cus, int ta, int tb) {
   int forced = -1;
   if (const char* e = getenv("TJH_GEMM_TILE")) {
@@ -523,7 +524,7 @@ Plan choose_plan(int64_t M, int64_t N, int64_t K, int64_t batch, int cus, int ta
     double useful = (double)(M * N) / (double)(tm * t.bm * tn * t.bn);
     int64_t tiles = tm * tn * batch;
     int64_t s = choose_splits(tiles, K, cus);
-    if (t.bm >= 256 && forced < 0 && (s > 1 && K < 16384)) continue;
+    if (t.bm >= 256 && forced < 0 && s > 1) continue;
     double score = useful * fill_of(tiles * s, cus) * tile_speed(i, ta, tb);
     if (tiles * s < cus) score *= (double)(tiles * s) / cus;
     if (score > best_score + 1e-9) {
