@@ -649,6 +649,13 @@ int tjh_conv2d_backward_input(const tjh_conv2d_desc* d, const float* dy,
 /* dw (+)= correlation of x and dy; accumulate != 0 adds. */
 int tjh_conv2d_backward_weight(const tjh_conv2d_desc* d, const float* dy,
                                const float* x, float* dw, int accumulate);
+/* The same, plus the bias gradient db[oc] (+)= sum over images and output
+ * pixels of dy (the bias grad of F.conv2d, functional.ts:438-660) when db
+ * is not NULL, taken from the dy tiles the weight-gradient product stages
+ * (no second pass over dy).  With db NULL it is tjh_conv2d_backward_weight. */
+int tjh_conv2d_backward_weight_bias(const tjh_conv2d_desc* d, const float* dy,
+                                    const float* x, float* dw, float* db,
+                                    int accumulate);
 
 /* ------------------------------------------------------------------ */
 /* Optimizers — Adam.step / AdamW.step (src/optim/adam.ts:46-133,       */

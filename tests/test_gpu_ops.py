@@ -810,6 +810,43 @@ def test_conv2d_weight_grad_accumulates(torch, N, H):
     check(dwt.numpy(), dw0 + want, **RED)
 
 
+@pytest.mark.parametrize("N,C,H,OC,s,grp,acc", [(2, 3, 9, 8, 1, 1, 0), (16, 3, 64, 32, 1, 1, 1),
+                                                 (8, 32, 32, 64, 2, 1, 0), (4, 8, 17, 12, 2, 4, 1)])
+def test_conv2d_weight_and_bias_grad_in_one_pass(torch, N, C, H, OC, s, grp, acc):
+    """tjh_conv2d_backward_weight_bias: dW bit-identical to
+    tjh_conv2d_backward_weight (the same product), db = dy summed over
+    images and pixels (the row sums of the product's dy operand, in split
+    order), with one K slice and with a split K, groups, and accumulate."""
+    import ctypes
+    from torchjs_amd import _lib as L
+    r = np.random.default_rng(N * 7 + OC + s)
+    k = 3
+    oh = (H + 2 - k) // s + 1
+    x = f32(r.standard_normal((N, C, H, H)))
+    g = f32(r.standard_normal((N, OC, oh, oh)))
+    dw0 = f32(r.standard_normal((OC, C // grp, k, k)))
+    db0 = f32(r.standard_normal(OC))
+    desc = L.Conv2dDesc(N, C, H, H, OC, k, k, s, s, 1, 1, 1, 1, grp, oh, oh)
+    xt, gt = torch.tensor(x), torch.tensor(g)
+    dwa, dwb, dbt = torch.tensor(dw0), torch.tensor(dw0), torch.tensor(db0)
+    L.check(L.lib().tjh_conv2d_backward_weight(ctypes.byref(desc), gt.data_ptr(), xt.data_ptr(),
+                                               dwa.data_ptr(), acc), "conv2d_backward_weight")
+    L.check(L.lib().tjh_conv2d_backward_weight_bias(ctypes.byref(desc), gt.data_ptr(),
+                                                    xt.data_ptr(), dwb.data_ptr(),
+                                                    dbt.data_ptr(), acc),
+            "conv2d_backward_weight_bias")
+    assert np.array_equal(dwa.numpy(), dwb.numpy())
+    want = g.astype(np.float64).sum(axis=(0, 2, 3)) + (db0 if acc else 0)
+    check(dbt.numpy(), want, **RED)
+    # deterministic
+    dbt2 = torch.tensor(db0)
+    L.check(L.lib().tjh_conv2d_backward_weight_bias(ctypes.byref(desc), gt.data_ptr(),
+                                                    xt.data_ptr(), dwb.data_ptr(),
+                                                    dbt2.data_ptr(), acc),
+            "conv2d_backward_weight_bias")
+    assert np.array_equal(dbt.numpy(), dbt2.numpy())
+
+
 # ------------------------------------------------------------------ optimizers
 
 

@@ -23,7 +23,7 @@ EXPORTS = ["init", "deviceInfo", "malloc", "h2d", "d2h", "d2hAsync", "synchroniz
            "castI32F32", "ternary", "powScalarBackward", "axpy", "maskedFill", "compare",
            "argmax", "nllLossForward", "nllLossBackward", "indexSelect", "indexAdd", "gather",
            "scatterAdd", "oneHot", "oneHotI32", "nonzero", "conv2dForward",
-           "conv2dBackwardInput", "conv2dBackwardWeight", "cast", "fillU8", "copyStridedU8",
+           "conv2dBackwardInput", "conv2dBackwardWeight", "conv2dBackwardWeightBias", "cast", "fillU8", "copyStridedU8",
            "triangle", "multinomial", "timerEnd", "timerRead", "rangePush", "rangePop",
            "mark", "exprEval", "exprColsum", "exprCompile", "graphBegin", "graphEnd", "graphReplay",
            "graphDestroy", "adamStepDev"]

@@ -166,6 +166,7 @@ SIGNATURES = {
     "tjh_conv2d_forward": [ctypes.POINTER(Conv2dDesc), c_vp, c_vp, c_vp, c_vp],
     "tjh_conv2d_backward_input": [ctypes.POINTER(Conv2dDesc), c_vp, c_vp, c_vp],
     "tjh_conv2d_backward_weight": [ctypes.POINTER(Conv2dDesc), c_vp, c_vp, c_vp, c_int],
+    "tjh_conv2d_backward_weight_bias": [ctypes.POINTER(Conv2dDesc), c_vp, c_vp, c_vp, c_vp, c_int],
     "tjh_timer_end": [c_int],
     "tjh_timer_read": [c_int, ctypes.POINTER(c_f64)],
     "tjh_range_push": [ctypes.c_char_p],

@@ -21,6 +21,10 @@ constexpr int kBatch = 8;     // rows fetched before they are accumulated
 // nullptr: skipped), np <= kFinalMax.  One launch on the library stream.
 int colsum_final(float* const* part, float* const* out, int np, int64_t nb, int64_t cols,
                  int accumulate, float scale);
+// The same with a row length per output (outputs of different widths in
+// one launch).
+int colsum_final_cols(float* const* part, float* const* out, const int64_t* cols, int np,
+                      int64_t nb, int accumulate, float scale);
 
 // Row partition of a column sum over r of [outer][r][inner] (about two
 // workgroups per CU, >= 16 rows each): nb slices of rchunk rows.  `vec`:

@@ -24,7 +24,10 @@
 //             K = OC/g * ceil(KH/sh) * ceil(KW/sw) and no skipped taps
 //   wgrad   : dW[oc][r]        = sum_j  dy[n][oc][p]            * x(r; n,p)
 //             M = OC/g, N = C/g * KH*KW, K = images * OH*OW (split over
-//             workgroups, partials summed in split order by colsum_final)
+//             workgroups, partials summed in split order by colsum_final);
+//             the bias gradient db[oc] = sum_j dy[n][oc][p] is the row sum
+//             of that A operand, taken by the first column tile's
+//             workgroups while they stage it
 // with r = (c*KH + kh)*KW + kw, p = oy*OW + ox, e = iy*W + ix and
 // x(r; n,p) = x[n][c][oy*sh - ph + kh*dh][ox*sw - pw + kw*dw] (0 outside).
 //
@@ -39,6 +42,7 @@
 
 #include "colsum.h"
 #include "common.h"
+#include "kahan.h"
 
 namespace tjh {
 namespace {
@@ -80,7 +84,9 @@ struct ConvArgs {
   const float* bias;  // forward only, may be null
   float* out;         // y, dx or dW
   float* ws;          // wgrad split partials [groups][splits][M][N], or null
-  int accumulate;     // wgrad without split: dW += instead of =
+  float* db;          // wgrad: the bias gradient (row sums of dy), or null
+  float* rsw;         // wgrad split partials of db [groups][splits][M], or null
+  int accumulate;     // wgrad without split: dW (and db) += instead of =
   uint32_t n, c, h, w, oc, kh, kw, sh, sw, ph, pw, dh, dw, oh, ow;
   uint32_t cg, ocg, kk;      // channels per group, KH*KW
   uint32_t M, N, K;          // GEMM sizes per group
@@ -93,9 +99,20 @@ struct ConvArgs {
   // dgrad by stride class (dilation 1): input pixels iy = ry + sh*qy,
   // ix = rx + sw*qx (qy < qh, qx < qw) take taps kh = rkh + sh*ta,
   // kw = rkw + sw*tb (ta < th, tb < tw) from dy[oy = qy + oyc - ta][ox =
-  // qx + oxc - tb]; BK = c_oc*th*tw + c_a*tw + c_b
+  // qx + oxc - tb]; BK = c_oc*th*tw + c_a*tw + c_b.  The fields describe
+  // one class; a launch over several classes carries them in `cls`, one
+  // class per grid row (blockIdx.y), and the kernel reads its own
   uint32_t ry, rx, rkh, rkw, th, tw, oyc, oxc, qh, qw, c_oc, c_a, c_b;
   FastDiv f_tt, f_tw, f_qq, f_qw;
+};
+
+constexpr int kMaxClasses = 4;  // stride classes per dgrad launch
+struct ClassArgs {
+  uint32_t ry, rx, rkh, rkw, th, tw, oyc, oxc, qh, qw, c_oc, c_a, c_b, N, K;
+  FastDiv f_tt, f_tw, f_qq, f_qw;
+};
+struct ClassSet {
+  ClassArgs c[kMaxClasses];
 };
 
 // Operand cursors.  A lane stages the same (o, k - k0) positions of every
@@ -367,8 +384,19 @@ __device__ __forceinline__ void tile_pos(int idx, uint32_t& o, uint32_t& k) {
   }
 }
 
+// The fields of one stride class written into a.
+__device__ __forceinline__ void apply_class(ConvArgs& a, const ClassArgs& c) {
+  a.ry = c.ry; a.rx = c.rx; a.rkh = c.rkh; a.rkw = c.rkw; a.th = c.th; a.tw = c.tw;
+  a.oyc = c.oyc; a.oxc = c.oxc; a.qh = c.qh; a.qw = c.qw;
+  a.c_oc = c.c_oc; a.c_a = c.c_a; a.c_b = c.c_b; a.N = c.N; a.K = c.K;
+  a.f_tt = c.f_tt; a.f_tw = c.f_tw; a.f_qq = c.f_qq; a.f_qw = c.f_qw;
+}
+
 template <int MODE, int BM, int BN>
-__global__ __launch_bounds__(kThreads, 2) void k_conv_igemm(ConvArgs a) {
+__global__ __launch_bounds__(kThreads, 2) void k_conv_igemm(ConvArgs a0, ClassSet cs) {
+  // class dgrad: grid row y is a stride class (these launches never split K)
+  ConvArgs a = a0;
+  if (MODE == kDgradClass) apply_class(a, cs.c[blockIdx.y]);
   constexpr int WGM = BM / 32, WGN = BN / 32;  // wave grid
   static_assert(WGM * WGN == 4, "four waves of 32x32");
   constexpr int LA = BM + 4, LB = BN + 4;
@@ -381,7 +409,8 @@ __global__ __launch_bounds__(kThreads, 2) void k_conv_igemm(ConvArgs a) {
   const uint32_t tile = blockIdx.x;
   const uint32_t tm = tile % a.tiles_m, tn = tile / a.tiles_m;
   const uint32_t m0 = tm * BM, n0 = tn * BN;
-  const uint32_t kbeg = blockIdx.y * a.kchunk;
+  if (MODE == kDgradClass && n0 >= a.N) return;  // a smaller class's grid row
+  const uint32_t kbeg = MODE == kDgradClass ? 0u : blockIdx.y * a.kchunk;
   const uint32_t kend = kbeg + a.kchunk < a.K ? kbeg + a.kchunk : a.K;
   const uint32_t ktiles = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
 
@@ -446,13 +475,43 @@ __global__ __launch_bounds__(kThreads, 2) void k_conv_igemm(ConvArgs a) {
     stage(0, ra0, rb0);
   }
   __syncthreads();
+  // wgrad with a bias gradient: the first column tile's workgroups also sum
+  // the rows of their dy tiles (db[oc] = sum over images and pixels of dy),
+  // compensated, RKPT k values per lane and K step
+  constexpr int RKPT = BK * BM / kThreads;
+  const bool row_sums = MODE == kWgrad && a.db != nullptr && tn == 0;
+  Kahan rsum;
   for (uint32_t kt = 0; kt < ktiles; ++kt) {
     const int cur = kt & 1;
     const bool more = kt + 1 < ktiles;
     if (more) fetch(ra0, rb0);
     compute(cur);
+    if (row_sums) {
+      const int rm = t % BM, rk = (t / BM) * RKPT;
+#pragma unroll
+      for (int i = 0; i < RKPT; ++i) rsum.add(As[cur][(rk + i) * LA + rm]);
+    }
     if (more) stage(cur ^ 1, ra0, rb0);
     __syncthreads();
+  }
+  if (MODE == kWgrad && row_sums) {
+    // lanes t, t + BM, ... hold slices of row t: combined in that order (the
+    // staging tiles are free: the K loop ended on a barrier)
+    float* rpart = As[0];
+    rpart[t] = rsum.s;
+    __syncthreads();
+    const uint32_t row = m0 + (uint32_t)t;
+    if (t < BM && row < a.M) {
+      float v = 0.f;
+#pragma unroll
+      for (int q = 0; q < kThreads / BM; ++q) v += rpart[t + q * BM];
+      if (a.rsw) {
+        a.rsw[((size_t)g * gridDim.y + blockIdx.y) * a.M + row] = v;
+      } else {
+        float* o = a.db + g * a.ocg + row;
+        *o = a.accumulate ? *o + v : v;
+      }
+    }
   }
 
   // epilogue: accumulator register r of lane (l32, h) holds tile row
@@ -513,13 +572,13 @@ int choose_cfg(uint32_t M, uint32_t N) {
 }
 
 template <int MODE>
-void launch_cfg(int cfg, const ConvArgs& a, dim3 grid) {
+void launch_cfg(int cfg, const ConvArgs& a, const ClassSet& cs, dim3 grid) {
   if (cfg == 0)
-    tjh_launch((k_conv_igemm<MODE, 32, 128>), grid, dim3(kThreads), 0, stream(), a);
+    tjh_launch((k_conv_igemm<MODE, 32, 128>), grid, dim3(kThreads), 0, stream(), a, cs);
   else if (cfg == 1)
-    tjh_launch((k_conv_igemm<MODE, 64, 64>), grid, dim3(kThreads), 0, stream(), a);
+    tjh_launch((k_conv_igemm<MODE, 64, 64>), grid, dim3(kThreads), 0, stream(), a, cs);
   else
-    tjh_launch((k_conv_igemm<MODE, 128, 32>), grid, dim3(kThreads), 0, stream(), a);
+    tjh_launch((k_conv_igemm<MODE, 128, 32>), grid, dim3(kThreads), 0, stream(), a, cs);
 }
 
 ConvArgs make_args(const tjh_conv2d_desc* d) {
@@ -546,7 +605,8 @@ ConvArgs make_args(const tjh_conv2d_desc* d) {
 
 // One implicit-GEMM launch of `mode` over all groups; wgrad splits K when
 // the output tiles alone cannot fill the CUs.
-int run_conv(int mode, ConvArgs a, int64_t groups) {
+int run_conv(int mode, ConvArgs a, int64_t groups, const ClassSet* cs = nullptr,
+             int nclass = 1) {
   if (a.M == 0 || a.N == 0) return TJH_OK;
   const int cfg = choose_cfg(a.M, a.N);
   a.tiles_m = (uint32_t)cdiv(a.M, kCfgs[cfg].bm);
@@ -562,28 +622,42 @@ int run_conv(int mode, ConvArgs a, int64_t groups) {
   }
   a.kchunk = a.K > 0 ? (uint32_t)(cdiv(cdiv(a.K, splits), BK) * BK) : BK;
   splits = a.K > 0 ? cdiv(a.K, a.kchunk) : 1;  // K = 0: one pass writes zeros
-  Scratch ws(splits > 1 ? (size_t)(groups * splits * a.M * a.N) * sizeof(float) : 0);
+  const int64_t rs_len = (mode == kWgrad && a.db) ? groups * splits * a.M : 0;
+  Scratch ws(splits > 1 ? (size_t)(groups * splits * a.M * a.N + rs_len) * sizeof(float) : 0);
   if (splits > 1 && !ws.ok()) return set_error(TJH_ERR_OOM, "conv2d: no split-K scratch");
   a.ws = splits > 1 ? ws.as<float>() : nullptr;
+  a.rsw = (splits > 1 && rs_len) ? ws.as<float>() + groups * splits * a.M * a.N : nullptr;
   TJH_ARG(tiles < (int64_t(1) << 31) && groups <= 65535, "conv2d: grid too large");
-  const dim3 grid((unsigned)tiles, (unsigned)splits, (unsigned)groups);
-  if (mode == kFwd) launch_cfg<kFwd>(cfg, a, grid);
-  else if (mode == kDgrad) launch_cfg<kDgrad>(cfg, a, grid);
-  else if (mode == kDgradClass) launch_cfg<kDgradClass>(cfg, a, grid);
-  else launch_cfg<kWgrad>(cfg, a, grid);
+  const dim3 grid((unsigned)tiles, (unsigned)(mode == kDgradClass ? nclass : splits),
+                  (unsigned)groups);
+  const ClassSet none{};
+  if (mode == kFwd) launch_cfg<kFwd>(cfg, a, none, grid);
+  else if (mode == kDgrad) launch_cfg<kDgrad>(cfg, a, none, grid);
+  else if (mode == kDgradClass) launch_cfg<kDgradClass>(cfg, a, *cs, grid);
+  else launch_cfg<kWgrad>(cfg, a, none, grid);
   int rc = check_launch("conv2d_igemm");
   if (rc != TJH_OK || splits == 1) return rc;
-  // dW[g] (+)= the splits' partial rows summed in split order (compensated)
+  // dW[g] (+)= the splits' partial rows summed in split order (compensated),
+  // and db[g] (+)= the splits' partial row sums, in one launch
   const int64_t mn = (int64_t)a.M * a.N;
-  for (int64_t g0 = 0; g0 < groups; g0 += kFinalMax) {
+  const int per = a.rsw ? 2 : 1;
+  for (int64_t g0 = 0; g0 < groups; g0 += kFinalMax / per) {
     float* parts[kFinalMax];
     float* outs[kFinalMax];
-    const int np = (int)(groups - g0 < kFinalMax ? groups - g0 : kFinalMax);
-    for (int i = 0; i < np; ++i) {
-      parts[i] = a.ws + (g0 + i) * splits * mn;
-      outs[i] = a.out + (g0 + i) * mn;
+    int64_t cols[kFinalMax];
+    const int64_t ng = groups - g0 < kFinalMax / per ? groups - g0 : kFinalMax / per;
+    int np = 0;
+    for (int64_t i = 0; i < ng; ++i) {
+      parts[np] = a.ws + (g0 + i) * splits * mn;
+      outs[np] = a.out + (g0 + i) * mn;
+      cols[np++] = mn;
+      if (a.rsw) {
+        parts[np] = a.rsw + (g0 + i) * splits * a.M;
+        outs[np] = a.db + (g0 + i) * a.ocg;
+        cols[np++] = a.M;
+      }
     }
-    rc = colsum_final(parts, outs, np, splits, mn, a.accumulate, 1.0f);
+    rc = colsum_final_cols(parts, outs, cols, np, splits, a.accumulate, 1.0f);
     if (rc != TJH_OK) return rc;
   }
   return TJH_OK;
@@ -655,10 +729,26 @@ int tjh_conv2d_backward_input(const tjh_conv2d_desc* d, const float* dy, const f
     a.K = a.ocg * a.kk;
     return run_conv(kDgrad, a, d->groups);
   }
-  // one exact GEMM per stride class of input pixels (sh*sw launches)
+  // one exact GEMM per stride class of input pixels, up to kMaxClasses
+  // classes per launch (one per grid row; the grid is sized for the
+  // largest, the others' extra workgroups return at once)
+  ClassSet cs{};
+  int nc = 0;
+  uint32_t maxN = 0, maxK = 0;
+  auto flush = [&]() -> int {
+    if (nc == 0) return TJH_OK;
+    ConvArgs b = a;
+    b.N = maxN;
+    b.K = maxK;
+    const int r = run_conv(kDgradClass, b, d->groups, &cs, nc);
+    nc = 0;
+    maxN = maxK = 0;
+    return r;
+  };
   for (uint32_t ry = 0; ry < a.sh && ry < a.h; ++ry) {
     for (uint32_t rx = 0; rx < a.sw && rx < a.w; ++rx) {
-      ConvArgs b = a;
+      ClassArgs& b = cs.c[nc];
+      b = ClassArgs{};
       b.ry = ry; b.rx = rx;
       b.rkh = (ry + a.ph) % a.sh;
       b.rkw = (rx + a.pw) % a.sw;
@@ -680,30 +770,41 @@ int tjh_conv2d_backward_input(const tjh_conv2d_desc* d, const float* dy, const f
       }
       b.N = (uint32_t)d->n * b.qh * b.qw;
       b.K = a.ocg * tt;
-      rc = run_conv(kDgradClass, b, d->groups);
-      if (rc != TJH_OK) return rc;
+      if (b.N > maxN) maxN = b.N;
+      if (b.K > maxK) maxK = b.K;
+      if (++nc == kMaxClasses) {
+        rc = flush();
+        if (rc != TJH_OK) return rc;
+      }
     }
   }
-  return TJH_OK;
+  return flush();
 }
 
-int tjh_conv2d_backward_weight(const tjh_conv2d_desc* d, const float* dy, const float* x,
-                               float* dw, int accumulate) {
+int tjh_conv2d_backward_weight_bias(const tjh_conv2d_desc* d, const float* dy, const float* x,
+                                    float* dw, float* db, int accumulate) {
   TJH_REQUIRE_INIT();
   int rc = check_desc(d);
   if (rc != TJH_OK) return rc;
   const int64_t cg = d->c / d->groups, kk = d->kh * d->kw;
   if (d->n == 0) {
-    if (!accumulate) return tjh_fill_f32(dw, d->oc * cg * kk, 0.f);
-    return TJH_OK;
+    if (accumulate) return TJH_OK;
+    rc = tjh_fill_f32(dw, d->oc * cg * kk, 0.f);
+    if (rc == TJH_OK && db) rc = tjh_fill_f32(db, d->oc, 0.f);
+    return rc;
   }
   ConvArgs a = make_args(d);
-  a.dy = dy; a.x = x; a.out = dw; a.accumulate = accumulate ? 1 : 0;
+  a.dy = dy; a.x = x; a.out = dw; a.db = db; a.accumulate = accumulate ? 1 : 0;
   a.M = a.ocg;
   a.N = a.cg * a.kk;
   a.K = (uint32_t)(d->n * d->oh * d->ow);
   KernelScope ks("conv2d_wgrad");
   return run_conv(kWgrad, a, d->groups);
+}
+
+int tjh_conv2d_backward_weight(const tjh_conv2d_desc* d, const float* dy, const float* x,
+                               float* dw, int accumulate) {
+  return tjh_conv2d_backward_weight_bias(d, dy, x, dw, nullptr, accumulate);
 }
 
 }  // extern "C"

@@ -202,13 +202,14 @@ constexpr int kFinalWaves = 16;
 struct FinalArgs {
   const float* part[kFinalMax];
   float* out[kFinalMax];
+  int64_t cols[kFinalMax];  // row length of each output
 };
 
 __global__ __launch_bounds__(64 * kFinalWaves) void k_colsum_final(FinalArgs fa, int64_t nb,
-                                                                   int64_t cols, int accumulate,
-                                                                   float scale) {
+                                                                   int accumulate, float scale) {
   __shared__ float red[kFinalWaves][64];
   const int i = blockIdx.y;
+  const int64_t cols = fa.cols[i];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int64_t c = (int64_t)blockIdx.x * 64 + lane;
   float* __restrict__ out = fa.out[i];
@@ -431,21 +432,31 @@ __global__ __launch_bounds__(kBlock) void k_argmax_cols(const float* __restrict_
 
 }  // namespace
 
-int colsum_final(float* const* part, float* const* out, int np, int64_t nb, int64_t cols,
-                 int accumulate, float scale) {
+int colsum_final_cols(float* const* part, float* const* out, const int64_t* cols, int np,
+                      int64_t nb, int accumulate, float scale) {
   TJH_ARG(np >= 1 && np <= kFinalMax, "colsum_final: %d outputs", np);
   FinalArgs fa{};
   int used = 0;
+  int64_t maxc = 0;
   for (int i = 0; i < np; ++i) {
     if (!out[i]) continue;
     fa.part[used] = part[i];
     fa.out[used] = out[i];
+    fa.cols[used] = cols[i];
+    if (cols[i] > maxc) maxc = cols[i];
     ++used;
   }
-  if (used == 0) return TJH_OK;
-  tjh_launch(k_colsum_final, dim3((unsigned)cdiv(cols, 64), (unsigned)used),
-                     dim3(64 * kFinalWaves), 0, stream(), fa, nb, cols, accumulate, scale);
+  if (used == 0 || maxc == 0) return TJH_OK;
+  tjh_launch(k_colsum_final, dim3((unsigned)cdiv(maxc, 64), (unsigned)used),
+             dim3(64 * kFinalWaves), 0, stream(), fa, nb, accumulate, scale);
   return check_launch("colsum_final");
+}
+
+int colsum_final(float* const* part, float* const* out, int np, int64_t nb, int64_t cols,
+                 int accumulate, float scale) {
+  int64_t cs[kFinalMax];
+  for (int i = 0; i < np && i < kFinalMax; ++i) cs[i] = cols;
+  return colsum_final_cols(part, out, cs, np, nb, accumulate, scale);
 }
 
 }  // namespace tjh

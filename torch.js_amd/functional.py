@@ -524,11 +524,14 @@ def conv2d(input, weight, bias=None, stride=1, padding=0, dilation=1, groups=1):
                                                       wc.data_ptr(), dx.data_ptr()),
                     "conv2d_backward_input")
         if rw:
+            # the bias gradient (dy summed over images and pixels) comes out
+            # of the weight-gradient product, which stages dy anyway
             dwt = empty(weight.shape)
-            L.check(L.lib().tjh_conv2d_backward_weight(ctypes.byref(desc), g.data_ptr(),
-                                                       xc.data_ptr(), dwt.data_ptr(), 0),
-                    "conv2d_backward_weight")
-        if rb:
+            db = empty((oc,)) if rb else None
+            L.check(L.lib().tjh_conv2d_backward_weight_bias(
+                ctypes.byref(desc), g.data_ptr(), xc.data_ptr(), dwt.data_ptr(),
+                db.data_ptr() if db is not None else None, 0), "conv2d_backward_weight")
+        elif rb:
             db = _view_raw(_k_reduce("sum", g, [0, 2, 3]), (oc,))
         return [dx, dwt, db]
     return _record(y, "Conv2d", [x, weight, bias], bwd)

@@ -1144,6 +1144,15 @@ static napi_value js_conv_backward_weight(napi_env env, napi_callback_info info)
   CHECK_RC(tjh_conv2d_backward_weight(&d, CF32(a[1]), CF32(a[2]), F32(a[3]), (int)i64(env, a[4])));
   return undef(env);
 }
+/* conv2dBackwardWeightBias(desc, dy, x, dw, db|null, accumulate) */
+static napi_value js_conv_backward_weight_bias(napi_env env, napi_callback_info info) {
+  napi_value a[6];
+  tjh_conv2d_desc d;
+  if (!get_args(env, info, 6, a) || !conv_desc(env, a[0], &d)) return NULL;
+  CHECK_RC(tjh_conv2d_backward_weight_bias(&d, CF32(a[1]), CF32(a[2]), F32(a[3]), F32(a[4]),
+                                           (int)i64(env, a[5])));
+  return undef(env);
+}
 
 /* ---------------------------------------------------------------- module */
 
@@ -1189,6 +1198,7 @@ static napi_value init_module(napi_env env, napi_value exports) {
       FN("nonzero", js_nonzero), FN("conv2dForward", js_conv_forward),
       FN("conv2dBackwardInput", js_conv_backward_input),
       FN("conv2dBackwardWeight", js_conv_backward_weight),
+      FN("conv2dBackwardWeightBias", js_conv_backward_weight_bias),
       FN("cast", js_cast), FN("fillU8", js_fill_u8), FN("copyStridedU8", js_copy_strided_u8),
       FN("triangle", js_triangle), FN("multinomial", js_multinomial),
       FN("timerEnd", js_timer_end), FN("timerRead", js_timer_read),
