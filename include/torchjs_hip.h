@@ -488,8 +488,8 @@ int tjh_flush_deferred(void);
  * allocates nothing.  No counterpart in the reference: it is for callers
  * that cannot allocate device memory (code under HIP graph capture, tight
  * serving or training loops, harnesses that forbid hipMalloc).  The
- * dgamma / dbeta partial rows live in a static 12 MiB device array of the
- * library (2 x 512 rows of up to 3072 floats, enough for any row count on
+ * dgamma / dbeta partial rows live in a static 6 MiB device array of the
+ * library (2 x 256 rows of up to 3072 floats, enough for any row count on
  * a 256-CU MI355X) instead of the caching allocator; the kernels and the
  * results are those of tjh_layer_norm_backward_res, bit for bit.  Takes
  * cols a multiple of 4 up to 3072 with 16-byte aligned operands (else

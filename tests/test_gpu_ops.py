@@ -1066,6 +1066,49 @@ def test_layer_norm_deferred_weight_grads(torch):
     check(hd[5], dbt, **RED)
 
 
+def test_layer_norm_batched_finish_wide_rows(torch):
+    """Eight LayerNorms of 3072 columns (the widest rows of the
+    register-resident kernel): the batched finishing pass for their 16
+    weight gradients and the per-LayerNorm passes of the undeferred engine
+    agree bit for bit, also when a second backward accumulates into the
+    existing .grad; the last LayerNorm's against the oracle."""
+    from torchjs_amd import tensor as T
+    r = np.random.default_rng(23)
+    rows, cols, n = 40, 3072, 8
+    x0 = f32(r.standard_normal((rows, cols)))
+    gms = [f32(1 + 0.1 * r.standard_normal(cols)) for _ in range(n)]
+    bts = [f32(0.1 * r.standard_normal(cols)) for _ in range(n)]
+    g = f32(r.standard_normal((rows, cols)))
+    runs = []
+    for fuse in (True, False):
+        T._FUSE_ACC = fuse
+        try:
+            ps = [torch.tensor(a, requires_grad=True) for a in gms + bts]
+            x = torch.tensor(x0, requires_grad=True)
+            F = torch.F
+            h = x * 1.0
+            for i in range(n):
+                h = F.layer_norm(h, (cols,), ps[i], ps[n + i])
+            h.backward(torch.tensor(g))
+            first = [p.grad.numpy() for p in ps]
+            h = x * 1.0
+            for i in range(n):
+                h = F.layer_norm(h, (cols,), ps[i], ps[n + i])
+            h.backward(torch.tensor(g))
+            runs.append(first + [p.grad.numpy() for p in ps] + [x.grad.numpy()])
+        finally:
+            T._FUSE_ACC = True
+    for a_, b_ in zip(*runs):
+        assert np.array_equal(a_, b_)
+    # the last LayerNorm's gamma / beta gradients against the oracle
+    h = x0.astype(np.float64)
+    for i in range(n - 1):
+        h = ops.layer_norm(h, gms[i], bts[i])[0]
+    _, dgm, dbt = ops.layer_norm_backward(g, h, gms[n - 1])
+    check(runs[0][n - 1], dgm, **RED)
+    check(runs[0][2 * n - 1], dbt, **RED)
+
+
 def test_layer_norm_same_tensor_as_weight_and_bias(torch):
     """gamma and beta given as one tensor: its gradient is the sum of both
     (the engine does not defer a tensor that fills two of a node's slots)."""

@@ -24,6 +24,7 @@ namespace tjh {
 namespace {
 
 constexpr int kBlock = 256;
+constexpr int kLnBwdWaves = 8;  // waves per k_ln_bwd_wave workgroup
 
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
@@ -580,12 +581,13 @@ __global__ __launch_bounds__(kBlock) void k_ln_fwd_block(const float* __restrict
 
 // LayerNorm backward, dx part + per-block partial dgamma/dbeta.  With res,
 // dx = res + the LayerNorm input gradient (a residual stream's gradient).
-// Block b owns rows [b*rpb, (b+1)*rpb); wave w takes rows b*rpb + w + 4k.
+// Block b (NW waves) owns rows [b*rpb, (b+1)*rpb); wave w takes rows
+// b*rpb + w + NW*k.
 // Lane owns columns 4*(lane + 64*j) .. +3 (cols % 4 == 0, cols <= 256*V4).
 // Partials: pg/pb [nblocks, cols].
 // EXACT as for k_ln_fwd_wave.
 template <int V4, bool EXACT>
-__global__ __launch_bounds__(kBlock) void k_ln_bwd_wave(const float* __restrict__ dy,
+__global__ __launch_bounds__(64 * kLnBwdWaves) void k_ln_bwd_wave(const float* __restrict__ dy,
                                                         const float* __restrict__ x,
                                                         const float* __restrict__ gamma,
                                                         const float* __restrict__ mean,
@@ -595,7 +597,8 @@ __global__ __launch_bounds__(kBlock) void k_ln_bwd_wave(const float* __restrict_
                                                         float* __restrict__ pg,
                                                         float* __restrict__ pb, int64_t rows,
                                                         int64_t cols, int64_t rpb) {
-  __shared__ float4 red[2][kBlock / 64][64 * 3];  // partial combine across waves
+  constexpr int NW = kLnBwdWaves;
+  __shared__ float4 red[2][NW][64 * 3];  // partial combine across waves
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int c4 = (int)(cols >> 2);
   float4 ag[V4], ab[V4];
@@ -614,7 +617,7 @@ __global__ __launch_bounds__(kBlock) void k_ln_bwd_wave(const float* __restrict_
   // four rows per wave per step: all four rows' loads are issued before any
   // row's reductions
   constexpr int kPair = 4;
-  constexpr int kStep = kBlock / 64;
+  constexpr int kStep = NW;
   for (int64_t r0 = r_beg + w; r0 < r_end; r0 += kStep * kPair) {
     float4 gv[kPair][V4], xh[kPair][V4];
     float mu[kPair], rs[kPair];
@@ -690,7 +693,7 @@ __global__ __launch_bounds__(kBlock) void k_ln_bwd_wave(const float* __restrict_
       }
     }
   }
-  // combine the 4 waves' column partials (fixed order) and write
+  // combine the NW waves' column partials (fixed order) and write
   if (pg) {
     for (int j0 = 0; j0 < V4; j0 += 3) {
 #pragma unroll
@@ -710,7 +713,7 @@ __global__ __launch_bounds__(kBlock) void k_ln_bwd_wave(const float* __restrict_
           int i = lane + 64 * j;
           if (j < V4 && i < c4) {
             float4 s = red[w][0][lane + 64 * jj];
-            for (int q = 1; q < kBlock / 64; ++q) {
+            for (int q = 1; q < NW; ++q) {
               float4 t = red[w][q][lane + 64 * jj];
               s.x += t.x; s.y += t.y; s.z += t.z; s.w += t.w;
             }
@@ -802,13 +805,14 @@ int ln_bwd_v4(const float* dy, const float* x, const float* gamma, const float* 
   return cols <= 64 * 4 * 3 ? 3 : (cols <= 64 * 4 * 6 ? 6 : (cols <= 64 * 4 * 12 ? 12 : 0));
 }
 
-// Rows per workgroup: ~2 workgroups per CU, >= 16 rows each (fewer partial
-// rows for the dgamma/dbeta pass; measured faster than 4 per CU).  So
-// nb <= max(2 * CUs, ...) and nb <= 512 on a 256-CU MI355X.
+// Rows per workgroup: one 8-wave workgroup per CU, >= 32 rows each (four
+// per wave: the same waves in flight as two 4-wave workgroups of 16 rows,
+// half the partial rows for the dgamma/dbeta pass, and measured 3% faster).
+// So nb <= max(CUs, ...) and nb <= 256 on a 256-CU MI355X.
 void ln_bwd_blocks(int64_t rows, int64_t& rpb, int64_t& nb) {
   const int cus = num_cus() > 0 ? num_cus() : 256;
-  rpb = cdiv(rows, 2LL * cus);
-  if (rpb < 16) rpb = 16;
+  rpb = cdiv(rows, 1LL * cus);
+  if (rpb < 32) rpb = 32;
   nb = cdiv(rows, rpb);
 }
 
@@ -820,16 +824,16 @@ int ln_bwd_wave_launch(int v4, const float* dy, const float* x, const float* gam
                        float* pg, float* pb, int64_t rows, int64_t cols, int64_t rpb,
                        int64_t nb) {
   if (v4 == 3 && cols == 64 * 4 * 3)
-    tjh_launch((k_ln_bwd_wave<3, true>), dim3((unsigned)nb), dim3(kBlock), 0, stream(),
+    tjh_launch((k_ln_bwd_wave<3, true>), dim3((unsigned)nb), dim3(64 * kLnBwdWaves), 0, stream(),
                        dy, x, gamma, mean, rstd, res, dx, pg, pb, rows, cols, rpb);
   else if (v4 == 3)
-    tjh_launch((k_ln_bwd_wave<3, false>), dim3((unsigned)nb), dim3(kBlock), 0, stream(),
+    tjh_launch((k_ln_bwd_wave<3, false>), dim3((unsigned)nb), dim3(64 * kLnBwdWaves), 0, stream(),
                        dy, x, gamma, mean, rstd, res, dx, pg, pb, rows, cols, rpb);
   else if (v4 == 6)
-    tjh_launch((k_ln_bwd_wave<6, false>), dim3((unsigned)nb), dim3(kBlock), 0, stream(),
+    tjh_launch((k_ln_bwd_wave<6, false>), dim3((unsigned)nb), dim3(64 * kLnBwdWaves), 0, stream(),
                        dy, x, gamma, mean, rstd, res, dx, pg, pb, rows, cols, rpb);
   else
-    tjh_launch((k_ln_bwd_wave<12, false>), dim3((unsigned)nb), dim3(kBlock), 0, stream(),
+    tjh_launch((k_ln_bwd_wave<12, false>), dim3((unsigned)nb), dim3(64 * kLnBwdWaves), 0, stream(),
                        dy, x, gamma, mean, rstd, res, dx, pg, pb, rows, cols, rpb);
   return check_launch("layer_norm_backward");
 }
@@ -1126,14 +1130,14 @@ int tjh_layer_norm_backward_res(const float* dy, const float* x, const float* ga
 // ---------------------------------------------------------------- no-alloc
 //
 // tjh_layer_norm_backward_noalloc keeps the dgamma / dbeta partial rows in
-// this file-scope device array instead of the caching allocator: 2 x 512
+// this file-scope device array instead of the caching allocator: 2 x 256
 // partial rows of up to 3072 floats, the most k_ln_bwd_wave writes on a
-// 256-CU MI355X (12 MiB, held by every GPU the library runs on until the
-// process ends).  Host code never passes `scratch` itself to a kernel: its
+// 256-CU MI355X (one partial row per CU; 6 MiB, held by every GPU the
+// library runs on until the process ends).  Host code never passes `scratch` itself to a kernel: its
 // name is a host-side stand-in there.  Its device address comes from
 // hipGetSymbolAddress, taken once per device by tjh_init.
 
-static constexpr int64_t kNoAllocFloats = 2 * 512 * 3072;
+static constexpr int64_t kNoAllocFloats = 2 * 256 * 3072;
 static __device__ __align__(256) float scratch[kNoAllocFloats];
 
 namespace tjh {
