@@ -605,13 +605,17 @@ __global__ __launch_bounds__(512, 1) void k_flash_dq_ds8(FlashArgs a) {
   // odd group's last one may be empty) so their barriers pair up
   const int nst0 = (nkb + 1) / 2;
   auto kb_of = [&](int t) { return grp + 2 * t; };
+  // Every prefetch is issued, from a block clamped into this wave's range
+  // when it would be past it (its values are then never used): loads on
+  // conditional paths leave the compiler unable to count the loads in
+  // flight, and its in-order vmcnt waits then wait for the newest
+  // prefetch before the current tile's MFMAs.
   auto fetch_ds = [&](int t, floatx4 (&d)[4]) {
-    const int kb = kb_of(t);
-    if (t < nst0 && kb < nmine) {
-      const floatx4* src = reinterpret_cast<const floatx4*>(dsrow + (int64_t)kb * (TILE * TILE));
+    int kb = kb_of(t);
+    if (kb >= nmine) kb = nmine > 0 ? nmine - 1 : 0;
+    const floatx4* src = reinterpret_cast<const floatx4*>(dsrow + (int64_t)kb * (TILE * TILE));
 #pragma unroll
-      for (int i = 0; i < 4; ++i) d[i] = src[i];
-    }
+    for (int i = 0; i < 4; ++i) d[i] = src[i];
   };
   floatx4 d0[4], d1[4], d2[4];
   fetch_ds(0, d0);
@@ -624,7 +628,7 @@ __global__ __launch_bounds__(512, 1) void k_flash_dq_ds8(FlashArgs a) {
     const int cur = 2 * grp + (t & 1);
     const int kb = kb_of(t);
     const bool more = kb + 2 < nkb;
-    if (more) load_tile<GUARD>(K, a.ks.t, (kb + 2) * TILE, a.Tk, rk, gt);
+    load_tile<GUARD>(K, a.ks.t, (more ? kb + 2 : nkb - 1) * TILE, a.Tk, rk, gt);
     fetch_ds(t + 2, into);
     if (kb < nmine) {
       float ct[2][16];
