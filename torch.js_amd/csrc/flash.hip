@@ -353,23 +353,33 @@ __global__ __launch_bounds__(256) void k_flash_dsum(FlashArgs a, float* __restri
   if (lane == 0) dsum[r] = x;
 }
 
-// The same with 128-bit loads: 16 lanes per 64-wide row, 16 rows per
-// workgroup; O is read here only (non-temporal), dO stays cached for the
-// two kernels that follow.  Needs 16-byte aligned rows.
+// The same with 128-bit loads: 16 lanes per 64-wide row, four rows per
+// 16-lane group with all eight loads issued first (64 rows per workgroup;
+// 9% faster than one row per group); O is read here only (non-temporal),
+// dO stays cached for the two kernels that follow.  Needs 16-byte aligned
+// rows.
 __global__ __launch_bounds__(256) void k_flash_dsum4(FlashArgs a, float* __restrict__ dsum,
                                                      int64_t rows) {
-  const int64_t r = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+  constexpr int R = 4;  // rows per 16-lane group, all loads issued first
+  const int64_t r0 = ((int64_t)blockIdx.x * 16 + (threadIdx.x >> 4)) * R;
   const int sub = threadIdx.x & 15;
-  if (r >= rows) return;  // uniform over each 16-lane row group
-  const int64_t bh = r / a.Tq, q = r % a.Tq;
-  const int64_t b = bh / a.H, hh = bh % a.H;
-  const float4 g = *reinterpret_cast<const float4*>(a.dout + b * a.gs.b + hh * a.gs.h +
-                                                    q * a.gs.t + 4 * sub);
-  const float4 o = ld_nt(a.o + b * a.os.b + hh * a.os.h + q * a.os.t + 4 * sub);
-  float x = (g.x * o.x + g.y * o.y) + (g.z * o.z + g.w * o.w);
+  float4 g[R], o[R];
 #pragma unroll
-  for (int off = 8; off >= 1; off >>= 1) x += __shfl_xor(x, off, 16);
-  if (sub == 0) dsum[r] = x;
+  for (int i = 0; i < R; ++i) {
+    const int64_t r = min(r0 + i, rows - 1);
+    const int64_t bh = r / a.Tq, q = r % a.Tq;
+    const int64_t b = bh / a.H, hh = bh % a.H;
+    g[i] = *reinterpret_cast<const float4*>(a.dout + b * a.gs.b + hh * a.gs.h + q * a.gs.t +
+                                            4 * sub);
+    o[i] = ld_nt(a.o + b * a.os.b + hh * a.os.h + q * a.os.t + 4 * sub);
+  }
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    float x = (g[i].x * o[i].x + g[i].y * o[i].y) + (g[i].z * o[i].z + g[i].w * o[i].w);
+#pragma unroll
+    for (int off = 8; off >= 1; off >>= 1) x += __shfl_xor(x, off, 16);
+    if (sub == 0 && r0 + i < rows) dsum[r0 + i] = x;
+  }
 }
 
 // Key-block kernel: dK, dV for 128 keys per workgroup (32 per wave), each
@@ -891,7 +901,7 @@ int flash_backward(const float* q, const float* k, const float* v, const float* 
   const bool v4 = aligned16(dout) && aligned16(o) && a.gs.b % 4 == 0 && a.gs.h % 4 == 0 &&
                   a.gs.t % 4 == 0 && a.os.b % 4 == 0 && a.os.h % 4 == 0 && a.os.t % 4 == 0;
   if (v4)
-    tjh_launch(k_flash_dsum4, dim3((unsigned)cdiv(rows, 16)), dim3(256), 0, stream(), a,
+    tjh_launch(k_flash_dsum4, dim3((unsigned)cdiv(rows, 64)), dim3(256), 0, stream(), a,
                        ds.as<float>(), rows);
   else
     tjh_launch(k_flash_dsum, dim3((unsigned)cdiv(rows, 4)), dim3(256), 0, stream(), a,
