@@ -433,6 +433,14 @@ int tjh_cross_entropy_backward(const float* logits, int64_t ld,
                                int64_t cols, int32_t ignore_index,
                                int reduction, float* dlogits, int64_t ldd,
                                int accumulate);
+/* row_scale[r] = s_r for a valid row, 0 otherwise: the factor of row r
+ * in tjh_cross_entropy_backward's gradient without weights and smoothing,
+ * (softmax - onehot) * s_r.  For tjh_gemm_ce, which forms that gradient
+ * while loading it instead of reading a stored dlogits. */
+int tjh_cross_entropy_row_scale(const int32_t* targets,
+                                const float* grad_out, int64_t rows,
+                                int64_t cols, int32_t ignore_index,
+                                int reduction, float* row_scale);
 /* nll over log-probs [rows, cols] (F.nll_loss, losses.ts:63-94):
  * loss_rows[r] = -w_t logp[r, t] for valid rows, else 0. */
 int tjh_nll_loss_forward(const float* logp, int64_t ld,
@@ -604,6 +612,20 @@ int tjh_gemm_act(int transA, int transB, int64_t M, int64_t N, int64_t K,
                  int64_t ldb, float beta, float* C, int64_t ldc,
                  const float* bias, int bias_mode, float* aux, int64_t ldaux,
                  int act);
+/* The products of torch.js's LM head backward (Linear.backward of
+ * src/nn/linear.ts:43-66 fed by cross_entropy's gradient, losses.ts:129-168)
+ * without the stored cross-entropy gradient: C[M,N] = op(D) B[K,N] (row
+ * stride ldb, not transposed), where D[r][c] = (exp(logits[r][c] - lse[r])
+ * - [c == targets[r]]) * row_scale[r] is tjh_cross_entropy_backward's
+ * dlogits (no weights, no smoothing) formed while the A tiles are loaded.
+ * transA 0: D is [M rows, K classes] (dx = dlogits W); transA 1: op(D) =
+ * D^T with D [K rows, M classes] (dW = dlogits^T x).  Logits row stride
+ * ld; row_scale from tjh_cross_entropy_row_scale.  Equal bit for bit to
+ * tjh_cross_entropy_backward followed by tjh_gemm. */
+int tjh_gemm_ce(int transA, int64_t M, int64_t N, int64_t K,
+                const float* logits, int64_t ld, const float* lse,
+                const int32_t* targets, const float* row_scale,
+                const float* B, int64_t ldb, float* C, int64_t ldc);
 
 /* ------------------------------------------------------------------ */
 /* Attention — F.scaled_dot_product_attention                           */

@@ -36,6 +36,14 @@ def check_floor(got, want, ref32, k=3.0):
     check(got, want, rtol=1e-4, atol=max(1e-5, k * floor))
 
 
+def _tensor_module():
+    """The package's tensor module (its engine switches live there);
+    `from torchjs_amd import tensor` would return the tensor() factory that
+    the package exports under the same name."""
+    import sys
+    return sys.modules["torchjs_amd.tensor"]
+
+
 def grad_of(torch, fn, *arrays):
     """Runs fn on leaf tensors, backprops a seeded upstream grad, returns
     (output, upstream, grads)."""
@@ -386,7 +394,7 @@ def test_embedding_tied_to_lm_head(torch):
     projection (GPT-2's tied wte): the embedding backward adds its rows into
     the projection's weight gradient in place; the result matches the sum
     of both gradients (and the unfused path) within tolerance."""
-    from torchjs_amd import tensor as T
+    T = _tensor_module()
     r = np.random.default_rng(31)
     V, D, n = 500, 32, 300
     w = f32(r.standard_normal((V, D)) * 0.1)
@@ -956,7 +964,7 @@ def test_layer_norm_backward_folds_pending_gradient(torch, rows, cols):
     add's gradient to the LayerNorm backward, which adds it in the same
     kernel (fast row kernel, odd widths and the general path); equal bit
     for bit to the separate add, and to the oracle within tolerance."""
-    from torchjs_amd import tensor as T
+    T = _tensor_module()
     r = np.random.default_rng(rows + cols)
     x0 = f32(r.standard_normal((rows, cols)))
     gm = f32(1 + 0.1 * r.standard_normal(cols))
@@ -987,7 +995,7 @@ def test_block_residual_fusion_equals_unfused(torch):
     backward gives the plain op-by-op block's output and gradients bit for
     bit."""
     from torchjs_amd import workloads as W
-    from torchjs_amd import tensor as T
+    T = _tensor_module()
     r = np.random.default_rng(7)
     Bn, Tn, d, H = 2, 40, 64, 4
     blk = W.Block(d, H)
@@ -1032,7 +1040,7 @@ def test_layer_norm_deferred_weight_grads(torch):
     (its gamma/beta receive two contributions, forcing an early flush), a
     chain of LayerNorms and leaves with a .grad from an earlier backward;
     bit-identical to the undeferred engine, and to the oracle."""
-    from torchjs_amd import tensor as T
+    T = _tensor_module()
     r = np.random.default_rng(17)
     rows, cols = 96, 768
     x0 = f32(r.standard_normal((rows, cols)))
@@ -1072,7 +1080,7 @@ def test_layer_norm_batched_finish_wide_rows(torch):
     weight gradients and the per-LayerNorm passes of the undeferred engine
     agree bit for bit, also when a second backward accumulates into the
     existing .grad; the last LayerNorm's against the oracle."""
-    from torchjs_amd import tensor as T
+    T = _tensor_module()
     r = np.random.default_rng(23)
     rows, cols, n = 40, 3072, 8
     x0 = f32(r.standard_normal((rows, cols)))
@@ -1177,6 +1185,112 @@ def _ln_chain_input(x0, gms, bts):
     h = ops.layer_norm(x, gms[0], bts[0])[0]
     h = ops.layer_norm(2.0 * h, gms[1], bts[1])[0]
     return ops.layer_norm(h + x, gms[0], bts[0])[0]
+
+
+@pytest.mark.parametrize("tile", ["256x128", "128x128", "128x64", "64x64"])
+@pytest.mark.parametrize("red", ["mean", "sum", "none"])
+def test_gemm_ce_equals_stored_gradient(torch, monkeypatch, tile, red):
+    """tjh_gemm_ce in both orientations (dx = dlogits W, dW = dlogits^T x)
+    on every tile, with edge strips and a K remainder, padded logits rows,
+    ignored and out-of-range targets: bit for bit tjh_cross_entropy_backward
+    followed by tjh_gemm, and the oracle's products."""
+    from torchjs_amd import _lib as L
+    monkeypatch.setenv("TJH_GEMM_TILE", tile)
+    r = np.random.default_rng(len(tile) * 10 + len(red))
+    rows, cols, ld, N = 300, 1030, 1032, 200
+    logits = f32(r.standard_normal((rows, ld)) * 2)
+    t = r.integers(0, cols, rows).astype(np.int32)
+    t[::7] = -100
+    t[3] = cols + 5  # out of range: a zero row, like an ignored one
+    t[4] = cols - 1
+    W = f32(r.standard_normal((cols, N)))
+    X = f32(r.standard_normal((rows, N)))
+    gl = f32(r.standard_normal(rows)) if red == "none" else f32([0.7])
+    rc = {"none": 0, "mean": 1, "sum": 2}[red]
+    xt, tt, wt, xx, gt = (torch.tensor(logits), torch.tensor(t), torch.tensor(W), torch.tensor(X),
+                          torch.tensor(gl))
+    lse, lrow, out = torch.empty((rows,)), torch.empty((rows,)), torch.empty(())
+    L.check(L.lib().tjh_cross_entropy_forward(xt.data_ptr(), ld, tt.data_ptr(), rows, cols, -100,
+                                              None, 0.0, lse.data_ptr(), lrow.data_ptr(), rc,
+                                              out.data_ptr() if rc else None), "cross_entropy")
+    d = torch.tensor(np.zeros((rows, ld), np.float32))
+    L.check(L.lib().tjh_cross_entropy_backward(xt.data_ptr(), ld, tt.data_ptr(), None, 0.0,
+                                               lse.data_ptr(), gt.data_ptr(), rows, cols, -100, rc,
+                                               d.data_ptr(), ld, 0), "cross_entropy_backward")
+    rs = torch.empty((rows,))
+    L.check(L.lib().tjh_cross_entropy_row_scale(tt.data_ptr(), gt.data_ptr(), rows, cols, -100, rc,
+                                                rs.data_ptr()), "cross_entropy_row_scale")
+
+    def stored(ta, M, K, b):
+        c = torch.tensor(np.zeros((M, N), np.float32))
+        L.check(L.lib().tjh_gemm(ta, 0, M, N, K, 1.0, d.data_ptr(), ld, 0, b.data_ptr(), N, 0, 0.0,
+                                 c.data_ptr(), N, 0, 1, None, 0), "gemm")
+        return c.numpy()
+
+    def formed(ta, M, K, b):
+        c = torch.tensor(np.full((M, N), 7.0, np.float32))  # beta 0: overwritten
+        L.check(L.lib().tjh_gemm_ce(ta, M, N, K, xt.data_ptr(), ld, lse.data_ptr(), tt.data_ptr(),
+                                    rs.data_ptr(), b.data_ptr(), N, c.data_ptr(), N), "gemm_ce")
+        return c.numpy()
+    dx = formed(0, rows, cols, wt)
+    dw = formed(1, cols, rows, xx)
+    assert np.array_equal(dx, stored(0, rows, cols, wt))
+    assert np.array_equal(dw, stored(1, cols, rows, xx))
+    to = t.copy()
+    to[3] = -100
+    D = ops.cross_entropy_backward(logits[:, :cols], to, gl if red == "none" else gl[0], red)
+    D32 = np.asarray(D, np.float32)
+    check_floor(dx, D @ W.astype(np.float64), D32 @ W)
+    check_floor(dw, D.T @ X.astype(np.float64), D32.T @ X)
+
+
+@pytest.mark.parametrize("red", ["mean", "sum", "none"])
+def test_lm_head_cross_entropy_formed_in_gemms(torch, monkeypatch, red):
+    """A Linear LM head whose weight is also the input embedding (GPT-2's
+    tied table) under cross_entropy: with the cross-entropy gradient formed
+    inside the head's two GEMMs the input and table gradients equal those
+    through the stored gradient bit for bit; autograd.grad and logits read
+    by anything but a Linear take the stored gradient."""
+    T = _tensor_module()
+    r = np.random.default_rng(31 + len(red))
+    B, Tn, D, V = 2, 50, 64, 1030
+    ids = r.integers(0, V, (B, Tn)).astype(np.int32)
+    tg = r.integers(0, V, (B * Tn,)).astype(np.int32)
+    tg[::6] = -100
+    W0 = f32(r.standard_normal((V, D)) * 0.1)
+    h0 = f32(r.standard_normal((B, Tn, D)))
+    calls = []
+    real = T._gemm_ce
+    monkeypatch.setattr(T, "_gemm_ce", lambda *a: calls.append(a[2]) or real(*a))
+    F = torch.F
+
+    def loss_of(W, h, head):
+        x = F.embedding(torch.tensor(ids), W) + h
+        logits = head(x, W)
+        loss = F.cross_entropy(logits.view(-1, V), torch.tensor(tg), reduction=red)
+        return loss.sum() if red == "none" else loss
+
+    runs = []
+    prev = T._FUSE_CE
+    for fuse in (True, False):
+        T._FUSE_CE = fuse
+        try:
+            W = torch.tensor(W0, requires_grad=True)
+            h = torch.tensor(h0, requires_grad=True)
+            loss_of(W, h, F.linear).backward()
+            W2 = torch.tensor(W0, requires_grad=True)
+            h2 = torch.tensor(h0, requires_grad=True)
+            gh = torch.autograd.grad(loss_of(W2, h2, F.linear), [h2])[0]
+            W3 = torch.tensor(W0, requires_grad=True)
+            h3 = torch.tensor(h0, requires_grad=True)
+            loss_of(W3, h3, lambda x, w: F.linear(x, w) * 1.0).backward()
+            runs.append([W.grad.numpy(), h.grad.numpy(), gh.numpy(), W3.grad.numpy(),
+                         h3.grad.numpy()])
+        finally:
+            T._FUSE_CE = prev
+    assert sorted(calls) == [False, False, True, True]  # dx and dW, two formed backwards
+    for a, b in zip(*runs):
+        assert np.array_equal(a, b)
 
 
 @pytest.mark.parametrize("tile", ["256x128", "128x128", "128x64", "64x64"])

@@ -135,6 +135,7 @@ SIGNATURES = {
                                   c_vp, c_vp, c_int, c_vp],
     "tjh_cross_entropy_backward": [c_vp, c_i64, c_vp, c_vp, c_f32, c_vp, c_vp, c_i64, c_i64,
                                    ctypes.c_int32, c_int, c_vp, c_i64, c_int],
+    "tjh_cross_entropy_row_scale": [c_vp, c_vp, c_i64, c_i64, ctypes.c_int32, c_int, c_vp],
     "tjh_nll_loss_forward": [c_vp, c_i64, c_vp, c_i64, c_i64, ctypes.c_int32, c_vp, c_vp, c_int,
                              c_vp],
     "tjh_nll_loss_backward": [c_vp, c_vp, c_vp, c_i64, c_i64, ctypes.c_int32, c_int, c_vp],
@@ -159,6 +160,8 @@ SIGNATURES = {
                  c_f32, c_vp, c_i64, c_i64, c_i64, c_vp, c_int],
     "tjh_gemm_act": [c_int, c_int, c_i64, c_i64, c_i64, c_f32, c_vp, c_i64, c_vp, c_i64, c_f32,
                      c_vp, c_i64, c_vp, c_int, c_vp, c_i64, c_int],
+    "tjh_gemm_ce": [c_int, c_i64, c_i64, c_i64, c_vp, c_i64, c_vp, c_vp, c_vp, c_vp, c_i64, c_vp,
+                    c_i64],
     "tjh_sdpa_forward": [c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_i64, P_i64,
                          P_i64, P_i64, P_i64, c_f32, c_int],
     "tjh_sdpa_backward": [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64,

@@ -92,7 +92,8 @@ struct Scratch {
 int gemm(const char* family, int transA, int transB, int64_t M, int64_t N, int64_t K,
          float alpha, const float* A, int64_t lda, int64_t strideA, const float* B, int64_t ldb,
          int64_t strideB, float beta, float* C, int64_t ldc, int64_t strideC, int64_t batch,
-         const float* bias, int bias_mode, float* aux = nullptr, int64_t ldaux = 0, int act = 0);
+         const float* bias, int bias_mode, float* aux = nullptr, int64_t ldaux = 0, int act = 0,
+         const float* ce_rows = nullptr);
 
 // Flash attention for head dim 64 (flash.hip).  `flash_supported` checks
 // the head dim and that every tensor has 16-byte aligned, D-contiguous rows.

@@ -71,6 +71,13 @@ struct GemmArgs {
   float* aux;
   int64_t ldaux;
   int act;
+  // A formed on load from logits (k_gemm<..., XF>): A's element at logits
+  // row r, class c is (exp(logits[r][c] - lse_r) - (c == t_r)) * s_r, the
+  // cross-entropy gradient, with xrow[r] = {lse_r, s_r, t_r (int bits), 0};
+  // xm0 / xk0 locate this (sub-)product in the logits (rows = m without
+  // TA, k with TA)
+  const floatx4* xrow;
+  int64_t xm0, xk0;
 };
 
 // The activation epilogue, shared by the GEMM and the split-K sum.
@@ -169,6 +176,83 @@ __device__ __forceinline__ void store_tile(float* __restrict__ S, const floatx4 
   }
 }
 
+// The logits row (and class offset) of float4 i of this lane's A tile
+// load, and whether that row lies inside the product.
+template <bool TRANS, int OUTER, bool EDGE, int T>
+__device__ __forceinline__ bool ce_row(const GemmArgs& g, int64_t rows, int64_t cols, int64_t r0,
+                                       int64_t c0, int i, int64_t& lr, int64_t& rel) {
+  const int f = threadIdx.x + T * i;
+  if (!TRANS) {
+    const int64_t go = r0 + (f >> 2), gk = c0 + (f & 3) * 4;
+    lr = g.xm0 + go;
+    rel = g.xk0 + gk;
+    return !EDGE || go < rows;
+  }
+  constexpr int Q = OUTER / 4;
+  const int64_t gk = c0 + f / Q, go = r0 + (f % Q) * 4;
+  lr = g.xk0 + gk;
+  rel = g.xm0 + go;
+  return !EDGE || gk < cols;
+}
+
+// The per-row records the A tile's float4s need (lse, scale, target),
+// issued with the tile's own loads.  Without TA a lane's rows are the same
+// for every K tile, so they are fetched once.
+template <bool TRANS, int OUTER, int V, bool EDGE, int T>
+__device__ __forceinline__ void ce_fetch(const GemmArgs& g, int64_t rows, int64_t cols,
+                                         int64_t r0, int64_t c0, float (&cl)[V], float (&cs)[V],
+                                         int (&ct)[V]) {
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    int64_t lr, rel;
+    if (ce_row<TRANS, OUTER, EDGE, T>(g, rows, cols, r0, c0, i, lr, rel)) {
+      const floatx4 v = g.xrow[lr];
+      cl[i] = v.x;
+      cs[i] = v.y;
+      ct[i] = __float_as_int(v.z);
+    } else {
+      cl[i] = cs[i] = 0.f;
+      ct[i] = -1;
+    }
+  }
+}
+
+// Turns a loaded A tile of logits into the cross-entropy gradient, element
+// for element the expression of the cross-entropy backward kernel, so the
+// product equals the one over the stored gradient bit for bit.  Elements
+// outside the product stay zero.
+template <bool TRANS, int OUTER, int V, bool EDGE, int T>
+__device__ __forceinline__ void ce_apply(const GemmArgs& g, int64_t rows, int64_t cols,
+                                         int64_t r0, int64_t c0, const float (&cl)[V],
+                                         const float (&cs)[V], const int (&ct)[V],
+                                         floatx4 (&reg)[V]) {
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    int64_t lr, rel;
+    if (!ce_row<TRANS, OUTER, EDGE, T>(g, rows, cols, r0, c0, i, lr, rel)) continue;
+    const int tc = ct[i] - (int)rel;  // classes are int32
+    const int f = threadIdx.x + T * i;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      bool in = true;
+      if (EDGE) {
+        if (!TRANS) in = c0 + (f & 3) * 4 + j < cols;
+        else in = r0 + (f % (OUTER / 4)) * 4 + j < rows;
+      }
+      reg[i][j] = in ? (__expf(reg[i][j] - cl[i]) - (tc == j ? 1.f : 0.f)) * cs[i] : 0.f;
+    }
+  }
+}
+
+// xrow[r] = {lse[r], scale[r], targets[r] (int bits), 0} for k_gemm<..., XF>.
+__global__ __launch_bounds__(256) void k_ce_rows(const float* __restrict__ lse,
+                                                 const int32_t* __restrict__ t,
+                                                 const float* __restrict__ sc, int64_t rows,
+                                                 floatx4* __restrict__ xrow) {
+  const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (r < rows) xrow[r] = floatx4{lse[r], sc[r], __int_as_float(t[r]), 0.f};
+}
+
 // Reads this lane's MFMA operand values for K steps 4q .. 4q+3 of a tile: F
 // blocks of 32 outer indices, 4 k values each.  K-step permutation: at MFMA
 // step j the lanes of half h (lane / 32) feed k = 8h + j, so a lane's k
@@ -204,7 +288,7 @@ __device__ __forceinline__ int xcd_tile(int bid, int n) {
   return (bid % kXcds) * (full / kXcds) + bid / kXcds;
 }
 
-template <int BM, int BN, bool TA, bool TB, bool EDGE>
+template <int BM, int BN, bool TA, bool TB, bool EDGE, bool XF = false>
 __global__ __launch_bounds__(gemm_threads(BM), 4) void k_gemm(GemmArgs g) {
   constexpr int LA = BM + 4, LB = BN + 4;       // LDS row lengths
   constexpr int WM = BM / (gemm_threads(BM) / 128), WN = BN / 2;  // wave tile: (T/128) x 2 waves
@@ -266,8 +350,15 @@ __global__ __launch_bounds__(gemm_threads(BM), 4) void k_gemm(GemmArgs g) {
   const bool row_sums = g.bias_mode >= 3 && tn == 0;
   Kahan rsum;
   floatx4 ra[VA], rb[VB];
+  // XF: lse, scale and target of the logits row of each A float4
+  float cl[XF ? VA : 1], cs[XF ? VA : 1];
+  int ct[XF ? VA : 1];
   load_tile<TA, BM, VA, EDGE, T>(A, g.lda, g.M, kend, m0, kbeg, g.vecA, ra);
   load_tile<!TB, BN, VB, EDGE, T>(B, g.ldb, g.N, kend, n0, kbeg, g.vecB, rb);
+  if constexpr (XF) {
+    ce_fetch<TA, BM, VA, EDGE, T>(g, g.M, kend, m0, kbeg, cl, cs, ct);
+    ce_apply<TA, BM, VA, EDGE, T>(g, g.M, kend, m0, kbeg, cl, cs, ct, ra);
+  }
   store_tile<TA, AKC, BM, VA, LA, T>(As[0], ra);
   store_tile<!TB, BKC, BN, VB, LB, T>(Bs[0], rb);
   __syncthreads();
@@ -279,6 +370,7 @@ __global__ __launch_bounds__(gemm_threads(BM), 4) void k_gemm(GemmArgs g) {
       const int64_t k0 = kbeg + (kt + 1) * BK;
       load_tile<TA, BM, VA, EDGE, T>(A, g.lda, g.M, kend, m0, k0, g.vecA, ra);
       load_tile<!TB, BN, VB, EDGE, T>(B, g.ldb, g.N, kend, n0, k0, g.vecB, rb);
+      if constexpr (XF && TA) ce_fetch<TA, BM, VA, EDGE, T>(g, g.M, kend, m0, k0, cl, cs, ct);
     }
     if (AKC || BKC) {
 #pragma unroll
@@ -327,6 +419,8 @@ __global__ __launch_bounds__(gemm_threads(BM), 4) void k_gemm(GemmArgs g) {
         rsum.add(AKC ? As[cur][rm * KS + rk + i] : As[cur][(rk + i) * LA + rm]);
     }
     if (more) {
+      if constexpr (XF)
+        ce_apply<TA, BM, VA, EDGE, T>(g, g.M, kend, m0, kbeg + (kt + 1) * BK, cl, cs, ct, ra);
       store_tile<TA, AKC, BM, VA, LA, T>(As[cur ^ 1], ra);
       store_tile<!TB, BKC, BN, VB, LB, T>(Bs[cur ^ 1], rb);
     }
@@ -537,6 +631,15 @@ Plan choose_plan(int64_t M, int64_t N, int64_t K, int64_t batch, int cus, int ta
 
 template <int BM, int BN, bool EDGE>
 void launch_e(const GemmArgs& g, dim3 grid, int ta, int tb) {
+  if (g.xrow) {  // A formed from logits: B is never transposed here
+    if (ta)
+      tjh_launch((k_gemm<BM, BN, true, false, EDGE, true>), grid, dim3(gemm_threads(BM)), 0,
+                 stream(), g);
+    else
+      tjh_launch((k_gemm<BM, BN, false, false, EDGE, true>), grid, dim3(gemm_threads(BM)), 0,
+                 stream(), g);
+    return;
+  }
   if (!ta && !tb)
     tjh_launch((k_gemm<BM, BN, false, false, EDGE>), grid, dim3(gemm_threads(BM)), 0, stream(), g);
   else if (!ta && tb)
@@ -614,6 +717,8 @@ GemmArgs sub(const GemmArgs& g, int ta, int tb, int64_t m0, int64_t M, int64_t n
   s.B = g.B + (tb ? n0 * g.ldb + k0 : k0 * g.ldb + n0);
   s.C = g.C + m0 * g.ldc + n0;
   if (g.aux) s.aux = g.aux + m0 * g.ldaux + n0;
+  s.xm0 = g.xm0 + m0;
+  s.xk0 = g.xk0 + k0;
   if (g.bias_mode == 1) s.bias = g.bias + n0;
   else if (g.bias_mode >= 2) s.bias = g.bias + m0;
   return s;
@@ -627,7 +732,8 @@ using namespace tjh;
 int tjh::gemm(const char* family, int transA, int transB, int64_t M, int64_t N, int64_t K,
               float alpha, const float* A, int64_t lda, int64_t strideA, const float* B,
               int64_t ldb, int64_t strideB, float beta, float* C, int64_t ldc, int64_t strideC,
-              int64_t batch, const float* bias, int bias_mode, float* aux, int64_t ldaux, int act) {
+              int64_t batch, const float* bias, int bias_mode, float* aux, int64_t ldaux, int act,
+              const float* ce_rows) {
   TJH_REQUIRE_INIT();
   TJH_ARG(M >= 0 && N >= 0 && K >= 0 && batch >= 0, "tjh_gemm: negative size");
   TJH_ARG(bias_mode >= 0 && bias_mode <= 3, "tjh_gemm: bad bias_mode %d", bias_mode);
@@ -636,6 +742,8 @@ int tjh::gemm(const char* family, int transA, int transB, int64_t M, int64_t N, 
   TJH_ARG(act >= 0 && act <= 3, "tjh_gemm_act: bad activation %d", act);
   TJH_ARG(act == 0 || (aux && ldaux >= N && batch <= 1),
           "tjh_gemm_act: activation %d needs aux (ld >= N) and batch 1", act);
+  TJH_ARG(!ce_rows || (!transB && batch <= 1 && bias_mode == 0 && act == 0),
+          "tjh_gemm_ce: B not transposed, no batch, bias or activation");
   if (M == 0 || N == 0 || batch == 0) return TJH_OK;
   TJH_ARG(batch <= 65535, "tjh_gemm: batch %lld exceeds 65535", (long long)batch);
   // row strides must cover the contiguous extent
@@ -658,6 +766,8 @@ int tjh::gemm(const char* family, int transA, int transB, int64_t M, int64_t N, 
   g.aux = act ? aux : nullptr;
   g.ldaux = ldaux;
   g.act = act;
+  g.xrow = reinterpret_cast<const floatx4*>(ce_rows);
+  g.xm0 = g.xk0 = 0;
   KernelScope ks(family);
   const Plan plan = choose_plan(M, N, K, batch, cus, transA, transB);
   const TileCfg& tc = kTiles[plan.tile];
@@ -723,4 +833,26 @@ extern "C" int tjh_gemm_act(int transA, int transB, int64_t M, int64_t N, int64_
                             int64_t ldaux, int act) {
   return tjh::gemm("gemm", transA, transB, M, N, K, alpha, A, lda, 0, B, ldb, 0, beta, C, ldc, 0,
                    1, bias, bias_mode, aux, ldaux, act);
+}
+
+extern "C" int tjh_gemm_ce(int transA, int64_t M, int64_t N, int64_t K, const float* logits,
+                           int64_t ld, const float* lse, const int32_t* targets,
+                           const float* row_scale, const float* B, int64_t ldb, float* C,
+                           int64_t ldc) {
+  TJH_REQUIRE_INIT();
+  TJH_ARG(lse && targets && row_scale && logits, "tjh_gemm_ce: NULL operand");
+  TJH_ARG(M >= 0 && N >= 0 && K >= 0, "tjh_gemm_ce: negative size");
+  const int64_t rows = transA ? K : M;  // logits rows
+  if (M == 0 || N == 0) return TJH_OK;
+  Scratch xrow((size_t)(rows > 0 ? rows : 1) * 4 * sizeof(float));
+  if (!xrow.ok()) return set_error(TJH_ERR_OOM, "tjh_gemm_ce: no scratch");
+  if (rows > 0) {
+    KernelScope ks("gemm");
+    tjh_launch(k_ce_rows, dim3((unsigned)cdiv(rows, 256)), dim3(256), 0, stream(), lse, targets,
+               row_scale, rows, xrow.as<floatx4>());
+    int rc = check_launch("gemm_ce_rows");
+    if (rc != TJH_OK) return rc;
+  }
+  return tjh::gemm("gemm", transA, 0, M, N, K, 1.0f, logits, ld, 0, B, ldb, 0, 0.0f, C, ldc, 0, 1,
+                   nullptr, 0, nullptr, 0, 0, xrow.as<float>());
 }

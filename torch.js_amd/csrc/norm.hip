@@ -219,6 +219,22 @@ __device__ __forceinline__ float ce_scale(const float* __restrict__ gout, int re
   return gout[0];
 }
 
+// Row r's factor of the cross-entropy gradient, (softmax - onehot) * sc[r]
+// (0 for a row whose target is ignored or out of range), as the backward
+// kernels form it: for GEMMs that build the gradient while loading it.
+__global__ __launch_bounds__(kBlock) void k_ce_row_scale(const int32_t* __restrict__ t,
+                                                         const float* __restrict__ gout,
+                                                         const float* __restrict__ count,
+                                                         int64_t rows, int64_t cols,
+                                                         int32_t ignore, int reduction,
+                                                         float* __restrict__ sc) {
+  const int64_t r = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (r >= rows) return;
+  const int32_t tr = t[r];
+  const bool valid = !(tr == ignore || tr < 0 || tr >= cols);
+  sc[r] = valid ? ce_scale(gout, reduction, r, count ? 1.0f / count[0] : 1.0f) : 0.f;
+}
+
 // dlogits = (softmax - onehot) * scale.  One row per block/wave.
 template <bool WAVE>
 __global__ __launch_bounds__(kBlock) void k_ce_bwd(const float* __restrict__ x, int64_t ld,
@@ -986,6 +1002,32 @@ int tjh_cross_entropy_backward(const float* logits, int64_t ld, const int32_t* t
                        ld, targets, lse, grad_out, count, rows, cols, ignore_index, reduction,
                        dlogits, ldd, accumulate);
   return check_launch("cross_entropy_backward");
+}
+
+int tjh_cross_entropy_row_scale(const int32_t* targets, const float* grad_out, int64_t rows,
+                                int64_t cols, int32_t ignore_index, int reduction,
+                                float* row_scale) {
+  TJH_REQUIRE_INIT();
+  TJH_ARG(rows >= 0 && cols > 0, "tjh_cross_entropy_row_scale: bad sizes");
+  TJH_ARG(reduction >= 0 && reduction <= 3, "tjh_cross_entropy_row_scale: bad reduction");
+  TJH_ARG(rows == 0 || (targets && grad_out && row_scale),
+          "tjh_cross_entropy_row_scale: NULL operand");
+  if (rows == 0) return TJH_OK;
+  const bool mean = reduction == 1 || reduction == 3;
+  Scratch cnt(mean ? 2 * sizeof(float) : 0);
+  if (mean) {
+    if (!cnt.ok()) return set_error(TJH_ERR_OOM, "cross_entropy_row_scale: no scratch");
+    KernelScope ks("loss_reduce");
+    tjh_launch(k_count_valid, dim3(1), dim3(kBlock), 0, stream(), targets, rows, cols,
+               ignore_index, nullptr, reduction, cnt.as<float>(), nullptr);
+    int rc = check_launch("count_valid");
+    if (rc != TJH_OK) return rc;
+  }
+  KernelScope ks("cross_entropy_bwd");
+  tjh_launch(k_ce_row_scale, dim3((unsigned)cdiv(rows, kBlock)), dim3(kBlock), 0, stream(),
+             targets, grad_out, mean ? cnt.as<float>() : nullptr, rows, cols, ignore_index,
+             reduction, row_scale);
+  return check_launch("cross_entropy_row_scale");
 }
 
 int tjh_nll_loss_forward(const float* logp, int64_t ld, const int32_t* targets, int64_t rows,

@@ -8,6 +8,7 @@ import math
 import numpy as np
 
 from . import _lib as L
+from . import tensor as _T
 from .tensor import (Tensor, _DT, _alias, _contig_strides, _empty_padded, _gemm, _k_binary,
                      _k_contiguous, _k_reduce, _k_scalar, _numel, _record, _view_raw, _wrap_dim,
                      contiguous, empty, full, mul, permute, reduce_mean, reshape, reshape_raw,
@@ -187,8 +188,11 @@ def cross_entropy(input, target, weight=None, reduction="mean", label_smoothing=
 
     def bwd(g):
         g = g.contiguous()
-        d = _empty_padded(rows, cols) if cols % 4 else empty((rows, cols))
         xp, ld = _rows_view(xd)
+        if w is None and eps == 0.0 and _T._FUSE_CE and ld % 4 == 0 and xp % 16 == 0:
+            # left unformed: a Linear that produced x forms it in its GEMMs
+            return [_T._CEGrad((rows, cols), xd, t, lse, g, int(ignore_index), red)]
+        d = _empty_padded(rows, cols) if cols % 4 else empty((rows, cols))
         wb = w.data_ptr() if w is not None else None  # keeps w alive with the graph
         L.check(L.lib().tjh_cross_entropy_backward(xp, ld, t.data_ptr(), wb, eps, lse.data_ptr(),
                                                    g.data_ptr(), rows, cols, int(ignore_index),
@@ -357,6 +361,14 @@ def linear(x, weight, bias=None):
     rb = bias is not None and bias.requires_grad
 
     def bwd(g):
+        if isinstance(g, _T._CEGrad):
+            if not rb and g.rows == M and g.cols == out_f:
+                # the cross-entropy gradient of the logits this layer made,
+                # formed inside both GEMMs instead of read from memory
+                dx = reshape_raw(_T._gemm_ce(g, wd, False), lead + (in_f,)) if rx else None
+                dw = _T._gemm_ce(g, x2, True) if rw else None
+                return [dx, dw, None]
+            g = g.materialize()
         g2 = reshape_raw(g, (M, out_f))
         dx = reshape_raw(_gemm(g2, wd), lead + (in_f,)) if rx else None
         dw = db = None

@@ -675,6 +675,28 @@ static napi_value js_gemm_act(napi_env env, napi_callback_info info) {
   return undef(env);
 }
 
+/* crossEntropyRowScale(targets, gradOut, rows, cols, ignoreIndex, reduction, rowScale) */
+static napi_value js_ce_row_scale(napi_env env, napi_callback_info info) {
+  napi_value a[7];
+  if (!get_args(env, info, 7, a)) return NULL;
+  CHECK_RC(tjh_cross_entropy_row_scale((const int32_t*)ptr(env, a[0]), (const float*)ptr(env, a[1]),
+                                       i64(env, a[2]), i64(env, a[3]), (int32_t)i64(env, a[4]),
+                                       (int)i64(env, a[5]), (float*)ptr(env, a[6])));
+  return undef(env);
+}
+
+/* gemmCe(transA, M, N, K, logits, ld, lse, targets, rowScale, B, ldb, C, ldc) */
+static napi_value js_gemm_ce(napi_env env, napi_callback_info info) {
+  napi_value a[13];
+  if (!get_args(env, info, 13, a)) return NULL;
+  CHECK_RC(tjh_gemm_ce((int)i64(env, a[0]), i64(env, a[1]), i64(env, a[2]), i64(env, a[3]),
+                       (const float*)ptr(env, a[4]), i64(env, a[5]), (const float*)ptr(env, a[6]),
+                       (const int32_t*)ptr(env, a[7]), (const float*)ptr(env, a[8]),
+                       (const float*)ptr(env, a[9]), i64(env, a[10]), (float*)ptr(env, a[11]),
+                       i64(env, a[12])));
+  return undef(env);
+}
+
 /* sdpaForward(q, k, v, o, lse, B, H, Tq, Tk, D, qs[3], ks[3], vs[3], os[3], scale, causal) */
 static napi_value js_sdpa_forward(napi_env env, napi_callback_info info) {
   napi_value a[16];
@@ -1181,6 +1203,7 @@ static napi_value init_module(napi_env env, napi_value exports) {
       FN("layerNormBackwardNoalloc", js_ln_backward_noalloc),
       FN("flushDeferred", js_flush_deferred), FN("embeddingForward", js_emb_forward),
       FN("embeddingBackward", js_emb_backward), FN("gemm", js_gemm), FN("gemmAct", js_gemm_act),
+      FN("gemmCe", js_gemm_ce), FN("crossEntropyRowScale", js_ce_row_scale),
       FN("sdpaForward", js_sdpa_forward), FN("sdpaBackward", js_sdpa_backward),
       FN("adamStep", js_adam_step), FN("adamStepDev", js_adam_step_dev), FN("isInitialized", js_is_initialized),
       FN("deviceCount", js_device_count), FN("free", js_free), FN("resetPeak", js_reset_peak),

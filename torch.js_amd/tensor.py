@@ -2015,6 +2015,8 @@ def view(x, shape):
 
 
 def reshape_raw(g, shape):
+    if isinstance(g, _CEGrad):
+        return g.reshaped(shape)
     st = _view_strides(g.shape, g._strides, tuple(shape))
     if st is None:
         g = g.contiguous()
@@ -2431,6 +2433,29 @@ def _gemm(a, b, out=None, alpha=1.0, beta=0.0, bias=None, bias_mode=0, rowsum_ou
     return out
 
 
+def _gemm_ce(ce, b, trans):
+    """op(D) @ b for the unformed cross-entropy gradient D = ce [rows, cols]:
+    trans False gives D [rows, cols] @ b [cols, N], trans True D^T @ b [rows,
+    N]; D is formed while the GEMM loads it (tjh_gemm_ce), bit for bit the
+    product over the stored gradient."""
+    M, K = (ce.cols, ce.rows) if trans else (ce.rows, ce.cols)
+    if b.shape[0] != K:
+        raise RuntimeError("gemm_ce: %d rows for a K of %d" % (b.shape[0], K))
+    N = b.shape[1]
+    ob = _mat_operand(b)
+    if ob is None or ob[2]:
+        b = _k_contiguous(b)
+        ob = _mat_operand(b)
+    out = _empty_padded(M, N) if N % 4 else empty((M, N))
+    ldc = out._strides[0] if out._strides[0] >= N else N
+    xp, ld = ce.rows_view()
+    rs = ce.row_scale()
+    L.check(L.lib().tjh_gemm_ce(1 if trans else 0, M, N, K, xp, ld, ce.lse.data_ptr(),
+                                ce.t.data_ptr(), rs.data_ptr(), ob[0], ob[1], out.data_ptr(), ldc),
+            "gemm_ce")
+    return out
+
+
 def _bgemm(a, b):
     """Batched a[B,M,K] @ b[B,N,K...] with uniform batch strides (3-D views)."""
     Bn, M, K = a.shape
@@ -2589,8 +2614,75 @@ class _SliceGrad:
         return out
 
 
+class _CEGrad:
+    """The cross-entropy gradient of logits x [rows, cols] (row stride ld)
+    without weights or smoothing, (softmax(x) - onehot(t)) * s_r, kept
+    unformed: the Linear layer that produced the logits forms it while its
+    backward GEMMs load their A tiles (tjh_gemm_ce), so the [rows, cols]
+    gradient is never written; any other consumer gets it materialized by
+    the cross-entropy backward kernel.  `shape` is the logical shape: [rows,
+    cols] or a reshape of it that keeps cols last."""
+
+    __slots__ = ("shape", "x", "t", "lse", "g", "rows", "cols", "ignore", "red", "_rs")
+
+    def __init__(self, shape, x, t, lse, g, ignore, red, rs=None):
+        self.shape = tuple(shape)
+        self.x, self.t, self.lse, self.g = x, t, lse, g
+        self.rows, self.cols = x.shape
+        self.ignore, self.red = ignore, red
+        self._rs = rs
+
+    @property
+    def ndim(self):
+        return len(self.shape)
+
+    def numel(self):
+        return self.rows * self.cols
+
+    def reshaped(self, shape):
+        shape = tuple(shape)
+        if shape and shape[-1] == self.cols and _numel(shape) == self.numel():
+            return _CEGrad(shape, self.x, self.t, self.lse, self.g, self.ignore, self.red,
+                           self._rs)
+        return reshape_raw(self.materialize(), shape)
+
+    def rows_view(self):
+        return self.x.data_ptr(), self.x._strides[0]
+
+    def row_scale(self):
+        if self._rs is None:
+            rs = empty((self.rows,))
+            L.check(L.lib().tjh_cross_entropy_row_scale(
+                self.t.data_ptr(), self.g.data_ptr(), self.rows, self.cols, self.ignore,
+                self.red, rs.data_ptr()), "cross_entropy_row_scale")
+            self._rs = rs
+        return self._rs
+
+    def materialize(self):
+        rows, cols = self.rows, self.cols
+        d = _empty_padded(rows, cols) if cols % 4 else empty((rows, cols))
+        xp, ld = self.rows_view()
+        L.check(L.lib().tjh_cross_entropy_backward(
+            xp, ld, self.t.data_ptr(), None, 0.0, self.lse.data_ptr(), self.g.data_ptr(), rows,
+            cols, self.ignore, self.red, d.data_ptr(), d._strides[0], 0), "cross_entropy_backward")
+        return d if self.shape == (rows, cols) else reshape_raw(d, self.shape)
+
+
+# nodes whose VJP takes a _CEGrad as it is (View reshapes it, Linear forms
+# it inside its GEMMs); every other node receives it materialized
+_CE_NODES = ("View", "Linear")
+# forming the cross-entropy gradient inside the LM head's GEMMs instead of
+# storing it (TJH_FUSE_CE=1).  Off by default: it saves the [rows, classes]
+# gradient's memory and its write and read (0.56 ms per GPT-2 step), but
+# the exp per element that every column tile of the two GEMMs repeats runs
+# between their MFMAs and their LDS stores and costs them 2.6 ms
+_FUSE_CE = os.environ.get("TJH_FUSE_CE", "0") == "1"
+
+
 def _dense(g):
-    return g.materialize() if isinstance(g, _SliceGrad) else g
+    if isinstance(g, (_SliceGrad, _CEGrad)):
+        return g.materialize()
+    return g
 
 
 def _accumulate(store, key, g):
@@ -2653,7 +2745,9 @@ def run_backward(pairs, retain_graph=False, inputs=None):
             roots.append(t.grad_fn)
         order = _toposort(roots)
         for node in reversed(order):
-            g = _dense(grads.pop(id(node), None))
+            g = grads.pop(id(node), None)
+            if not (isinstance(g, _CEGrad) and node.name in _CE_NODES):
+                g = _dense(g)
             if g is None:
                 continue
             if node.fn is None:
@@ -2686,8 +2780,11 @@ def run_backward(pairs, retain_graph=False, inputs=None):
                     else:
                         grads[id(t.grad_fn)] = gi
                     continue
-                if isinstance(gi, _SliceGrad) and (t.grad_fn is None or t._retains_grad or
-                                                   (wanted is not None and id(t) in wanted)):
+                if isinstance(gi, (_SliceGrad, _CEGrad)) and (
+                        t.grad_fn is None or t._retains_grad or
+                        (wanted is not None and id(t) in wanted)):
+                    gi = gi.materialize()
+                if isinstance(gi, _CEGrad) and tuple(gi.shape) != t.shape:
                     gi = gi.materialize()
                 if tuple(gi.shape) != t.shape:
                     gi = _sum_to(gi, t.shape) if gi.ndim >= t.ndim else reshape_raw(gi, t.shape)
@@ -2766,7 +2863,7 @@ def _pending_for(node, grads, wanted, owned):
         if t._retains_grad:
             return None
         prev = grads.get(id(t.grad_fn))
-        if prev is None or isinstance(prev, _SliceGrad):
+        if prev is None or isinstance(prev, (_SliceGrad, _CEGrad)):
             return None
         # a pending gradient may be the very tensor an add / sub / scalar-add
         # VJP also handed to another input, a leaf's .grad among them: the
@@ -2779,6 +2876,8 @@ def _pending_for(node, grads, wanted, owned):
         return None
     pk = _skey(prev)
     for p in others:
+        if isinstance(p, _CEGrad):
+            continue  # holds no gradient storage yet
         pieces = p.pieces if isinstance(p, _SliceGrad) else [(0, p)]
         if any(_skey(q) == pk for _, q in pieces):
             return None
