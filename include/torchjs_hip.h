@@ -364,9 +364,11 @@ typedef struct {
 /* A program: n_ins instructions in order over TJH_EXPR_MAX_REGS
  * registers (each source defined by an earlier instruction); the value of
  * output element e is r[result] after the last one.  Every instruction
- * computes exactly what the single-op entry points compute. */
+ * computes exactly what the single-op entry points compute.  result2, when
+ * not 0, names a second value r[result2 - 1] that tjh_expr_colsum2 also
+ * writes out (two values of one chain, computed from the same loads). */
 typedef struct {
-  int32_t n_ins, n_leaves, result, pad;
+  int32_t n_ins, n_leaves, result, result2;
   tjh_expr_ins ins[TJH_EXPR_MAX_INS];
   const float* leaf[TJH_EXPR_MAX_LEAVES];
   int64_t period[TJH_EXPR_MAX_LEAVES];
@@ -382,6 +384,13 @@ int tjh_expr_eval(const tjh_expr* prog, int64_t n, float* out);
  * r >= 64, inner >= 2 (else TJH_ERR_UNSUPPORTED). */
 int tjh_expr_colsum(const tjh_expr* prog, int64_t outer, int64_t r, int64_t inner,
                     float* out, float* values);
+/* tjh_expr_colsum that also writes the program's second value
+ * (prog->result2 != 0) to `values2` (may be NULL), in the same pass: the
+ * gradients of two inputs of one elementwise chain (y's and x's of
+ * GELU(x + b) * y, the latter with the bias gradient's column sum) from
+ * one read of the chain's inputs. */
+int tjh_expr_colsum2(const tjh_expr* prog, int64_t outer, int64_t r, int64_t inner,
+                     float* out, float* values, float* values2);
 /* Validates `prog` and compiles the kernel tjh_expr_eval (colsum == 0) or
  * tjh_expr_colsum (colsum != 0) would run for n elements, without a
  * device (kernels are compiled at run time, once per program shape). */

@@ -82,6 +82,51 @@ def test_chain_fwd_bwd_bitwise_and_fused(torch, T, both):
     assert fams.get("unary", 0) == 0 and fams.get("binary", 0) == 0, fams
 
 
+@pytest.mark.parametrize("extra", [False, True])
+def test_chain_sibling_gradients_in_one_pass(torch, T, extra):
+    """y's gradient of the C2 chain is written by the column-sum launch that
+    writes x's gradient and the bias gradient (one read of x and y for the
+    whole backward), bit for bit the separately evaluated gradients; with a
+    second contribution to y's gradient (`extra`) as well."""
+    R, C = 512, 2048
+    xs, bs, ys = _rand((R, C), 21), _rand((C,), 22), _rand((R, C), 23, -1, 1)
+
+    def step():
+        x = torch.tensor(xs, requires_grad=True)
+        b = torch.tensor(bs, requires_grad=True)
+        y = torch.tensor(ys, requires_grad=True)
+        loss = ((x + b).gelu() * y).sum(0).mean()
+        if extra:
+            loss = loss + (y * 3.0).sum()
+        loss.backward()
+        return [_np(loss), _np(x.grad), _np(b.grad), _np(y.grad)]
+
+    runs, launches = [], []
+    prev = T._FUSE_SIB
+    for sib in (True, False):
+        T._FUSE_SIB = sib
+        try:
+            runs.append(step())
+            torch.hip.kernel_timing(True)
+            torch.hip.kernel_timing_reset()
+            try:
+                step()
+                launches.append(dict((f, torch.hip.kernel_time(f)[0])
+                                     for f in torch.hip.kernel_families()))
+            finally:
+                torch.hip.kernel_timing(False)
+        finally:
+            T._FUSE_SIB = prev
+    _same(runs[0], runs[1])
+    assert not T._SIBLINGS
+    if not extra:
+        # forward sum(0) and the backward's one pass, and fewer launches in all:
+        # y's gradient is not evaluated on its own
+        assert launches[0].get("expr_colsum", 0) == 2, launches[0]
+        assert launches[0].get("expr", 0) < launches[1].get("expr", 0), launches
+        assert sum(launches[0].values()) < sum(launches[1].values()), launches
+
+
 @pytest.mark.parametrize("op", ["neg", "exp", "log", "sqrt", "rsqrt", "tanh", "sigmoid", "relu",
                                 "gelu", "square", "reciprocal", "erf", "abs", "sin", "cos",
                                 "silu", "leaky_relu", "elu", "softplus", "sign"])

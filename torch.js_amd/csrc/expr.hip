@@ -61,6 +61,8 @@ int check_prog(const tjh_expr* P, int64_t n, const float* const* extra, int next
     return set_error(TJH_ERR_INVALID, "tjh_expr: %d leaves", P->n_leaves), 0;
   if (P->result < 0 || P->result >= NR)
     return set_error(TJH_ERR_INVALID, "tjh_expr: result register %d", P->result), 0;
+  if (P->result2 < 0 || P->result2 > NR)
+    return set_error(TJH_ERR_INVALID, "tjh_expr: second result %d", P->result2), 0;
   bool vec = n % 4 == 0;
   for (int k = 0; k < P->n_leaves; ++k) {
     const int kind = P->kind[k];
@@ -97,6 +99,8 @@ int check_prog(const tjh_expr* P, int64_t n, const float* const* extra, int next
     defined |= 1u << in.dst;
   }
   if (!def(P->result)) return set_error(TJH_ERR_INVALID, "tjh_expr: result never written"), 0;
+  if (P->result2 && !def(P->result2 - 1))
+    return set_error(TJH_ERR_INVALID, "tjh_expr: second result never written"), 0;
   for (int i = 0; i < nextra; ++i) vec = vec && (!extra[i] || aligned16(extra[i]));
   return vec ? 4 : 1;
 }
@@ -159,6 +163,9 @@ std::string generate(const tjh_expr* P, int W, Mode mode) {
     s += "    const V<" + w + "> " + t + " = " + rhs + ";\n";
     reg[in.dst] = t;
   }
+  if (P->result2)
+    s += "    if (a.values2) store<" + std::to_string(W) + ">(a.values2 + e, " + reg[P->result2 - 1] +
+         ");\n";
   s += "    return " + reg[P->result] + ";\n  }\n};\n}  // namespace\n";
   snprintf(buf, sizeof buf,
            "extern \"C\" __global__ __launch_bounds__(%d) void tjh_expr_kernel(Args a) {\n"
@@ -227,6 +234,7 @@ std::string signature(const tjh_expr* P, int W, Mode mode) {
   k.push_back((char)P->n_ins);
   k.push_back((char)P->n_leaves);
   k.push_back((char)P->result);
+  k.push_back((char)P->result2);
   for (int i = 0; i < P->n_ins; ++i) {
     const tjh_expr_ins& in = P->ins[i];
     const char b[6] = {(char)in.op, (char)in.code, (char)in.dst, (char)in.a, (char)in.b, (char)in.c};
@@ -315,14 +323,19 @@ int tjh_expr_compile(const tjh_expr* prog, int64_t n, int colsum) {
 
 int tjh_expr_colsum(const tjh_expr* prog, int64_t outer, int64_t r, int64_t inner, float* out,
                     float* values) {
+  return tjh_expr_colsum2(prog, outer, r, inner, out, values, nullptr);
+}
+
+int tjh_expr_colsum2(const tjh_expr* prog, int64_t outer, int64_t r, int64_t inner, float* out,
+                     float* values, float* values2) {
   TJH_REQUIRE_INIT();
   TJH_ARG(outer >= 0 && r >= 0 && inner >= 0, "tjh_expr_colsum: negative size");
   if (outer > kFinalMax || r < 64 || inner < 2)
     return set_error(TJH_ERR_UNSUPPORTED,
                      "tjh_expr_colsum: outer %lld <= %d, r %lld >= 64 and inner %lld >= 2 needed",
                      (long long)outer, kFinalMax, (long long)r, (long long)inner);
-  const float* ex[1] = {values};
-  int W = check_prog(prog, outer * r * inner, ex, 1);
+  const float* ex[2] = {values, values2};
+  int W = check_prog(prog, outer * r * inner, ex, 2);
   if (W == 0) return TJH_ERR_INVALID;
   if (outer == 0) return TJH_OK;
   TJH_ARG(out != nullptr, "tjh_expr_colsum: NULL output");
@@ -339,6 +352,7 @@ int tjh_expr_colsum(const tjh_expr* prog, int64_t outer, int64_t r, int64_t inne
   jit::Args a = make_args(prog);
   a.out = part.as<float>();
   a.values = values;
+  a.values2 = prog->result2 ? values2 : nullptr;
   a.r = r;
   a.inner = inner;
   a.rchunk = rchunk;

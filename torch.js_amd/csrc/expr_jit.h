@@ -24,6 +24,7 @@ struct Args {
   float f[TJH_EXPR_MAX_INS];
   float* out;     // eval: the value; colsum: the partial rows
   float* values;  // colsum: the value too (may be null)
+  float* values2; // colsum: the program's second value (may be null)
   long long n;    // eval: elements
   long long r, inner, rchunk;
 };

@@ -534,6 +534,17 @@ static napi_value js_expr_colsum(napi_env env, napi_callback_info info) {
   return undef(env);
 }
 
+/* exprColsum2(program, outer, r, inner, out, values, values2) */
+static napi_value js_expr_colsum2(napi_env env, napi_callback_info info) {
+  napi_value a[7];
+  if (!get_args(env, info, 7, a)) return NULL;
+  tjh_expr P;
+  if (!get_expr(env, a[0], &P)) return NULL;
+  CHECK_RC(tjh_expr_colsum2(&P, i64(env, a[1]), i64(env, a[2]), i64(env, a[3]),
+                            (float*)ptr(env, a[4]), (float*)ptr(env, a[5]), (float*)ptr(env, a[6])));
+  return undef(env);
+}
+
 static napi_value js_softmax_forward(napi_env env, napi_callback_info info) {
   napi_value a[7];
   if (!get_args(env, info, 7, a)) return NULL;
@@ -1192,6 +1203,7 @@ static napi_value init_module(napi_env env, napi_value exports) {
       FN("copyStrided", js_copy_strided), FN("unary", js_unary),
       FN("unaryBackward", js_unary_backward), FN("binary", js_binary), FN("scalar", js_scalar),
       FN("reduce", js_reduce), FN("exprEval", js_expr_eval), FN("exprColsum", js_expr_colsum),
+      FN("exprColsum2", js_expr_colsum2),
       FN("exprCompile", js_expr_compile),
       FN("graphBegin", js_graph_begin), FN("graphEnd", js_graph_end),
       FN("graphReplay", js_graph_replay), FN("graphDestroy", js_graph_destroy),

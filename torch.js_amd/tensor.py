@@ -1055,10 +1055,12 @@ class _TooBig(Exception):
     pass
 
 
-def _program(root):
+def _program(root, root2=None):
     """The tjh_expr program of deferred tensor `root` and the tensors it
     keeps alive.  Inputs of another shape, evaluated inputs and views are
-    leaves; deferred inputs of the same shape are inlined."""
+    leaves; deferred inputs of the same shape are inlined.  `root2` (same
+    shape) becomes the program's second value, sharing loads and common
+    subexpressions with the first."""
     shape = root._shape
     leaves, leaf_ix, code, memo = [], {}, [], {}
     max_ins = L.EXPR_MAX_INS
@@ -1106,10 +1108,11 @@ def _program(root):
         return v
 
     result = emit(root, None)
-    sig = (tuple(code), result, tuple(k for _, k in leaves))
+    result2 = emit(root2, None) if root2 is not None else None
+    sig = (tuple(code), result, result2, tuple(k for _, k in leaves))
     hit = _PROGRAMS.get(sig)
     if hit is None:
-        hit = _PROGRAMS[sig] = _pack_code(code, result)
+        hit = _PROGRAMS[sig] = _pack_code(code, result, result2)
         if len(_PROGRAMS) > 512:
             _PROGRAMS.pop(next(iter(_PROGRAMS)))
     buf = bytearray(hit)
@@ -1122,12 +1125,13 @@ def _program(root):
     return L.Expr.from_buffer(buf), [a for a, _ in leaves]
 
 
-_PROGRAMS = {}  # (code, result, leaf kinds) -> packed program without its leaves
+_PROGRAMS = {}  # (code, results, leaf kinds) -> packed program without its leaves
 
 
-def _pack_code(code, result):
+def _pack_code(code, result, result2=None):
     """Packs instructions with registers allocated: a value's register is
-    freed after its last use."""
+    freed after its last use (the results' stay held)."""
+    keep = (result, result2)
     last = {}
     for i, ins in enumerate(code):
         for v in (ins[3:5] if ins[0] == "load" else ins[2:5]):  # a load's `a` is a leaf index
@@ -1140,7 +1144,7 @@ def _pack_code(code, result):
     op_ids = L.EXPR_OP
     for i, (op, c, a, b, cc, f) in enumerate(code):
         for v in set(x for x in ((a, b, cc) if op != "load" else (b, cc)) if x is not None):
-            if last.get(v) == i and v != result:
+            if last.get(v) == i and v not in keep:
                 free.append(reg[v])
         if not free:
             raise _TooBig()
@@ -1154,9 +1158,10 @@ def _pack_code(code, result):
             rb = reg[b] if b is not None else none
             rc = reg[cc] if cc is not None else none
         _EXPR_INS.pack_into(buf, _EXPR_INS_OFF + _EXPR_INS.size * i, op_ids[op], c, r, ra, rb, rc, f)
-        if last.get(i) is None and i != result:
+        if last.get(i) is None and i not in keep:
             free.append(r)  # never read
-    _EXPR_HDR.pack_into(buf, 0, len(code), 0, reg[result], 0)
+    _EXPR_HDR.pack_into(buf, 0, len(code), 0, reg[result],
+                        reg[result2] + 1 if result2 is not None else 0)
     return bytes(buf)
 
 
@@ -1279,21 +1284,62 @@ def _lazy_colsum(x, dims, keep=False):
     outer, r, inner = _numel(shape[:beg]), _numel(shape[beg:end]), _numel(shape[end:])
     if outer > 64 or r < 64 or inner < 2:
         return None
-    try:
-        prog, keep_alive = _program_fit(x)
-    except RuntimeError:
-        return None
+    sib = _sibling_for(x) if keep else None
+    prog = None
+    if sib is not None:
+        try:
+            prog, keep_alive = _program(x, sib)
+        except _TooBig:
+            sib = None
+    if prog is None:
+        try:
+            prog, keep_alive = _program_fit(x)
+        except RuntimeError:
+            return None
     out = empty(shape[:beg] + [1] * (end - beg) + shape[end:])
     vals = empty(x._shape) if keep else None
-    rc = L.lib().tjh_expr_colsum(ctypes.byref(prog), outer, r, inner, out.data_ptr(),
-                                 vals.data_ptr() if vals is not None else None)
+    vals2 = empty(sib._shape) if sib is not None else None
+    rc = L.lib().tjh_expr_colsum2(ctypes.byref(prog), outer, r, inner, out.data_ptr(),
+                                  vals.data_ptr() if vals is not None else None,
+                                  vals2.data_ptr() if vals2 is not None else None)
     if rc == L.ERR_UNSUPPORTED or (rc and _jit_failed(rc)):
         return None
     L.check(rc, "expr_colsum")
     del keep_alive
     if vals is not None:
         _settle(x, vals._st)
+    if sib is not None:
+        _settle(sib, vals2._st)
+        _SIBLINGS.remove(sib)
     return out
+
+
+# Deferred leaf gradients of the running backward pass not yet evaluated:
+# a column sum that writes another deferred value of the same shape (x's
+# gradient with the bias gradient) writes one of these in the same pass
+# when they read common inputs (y's gradient of GELU(x + b) * y).
+_SIBLINGS = []
+# evaluating sibling leaf gradients together; off only to compare in tests
+_FUSE_SIB = True
+
+
+def _sibling_for(x):
+    """A pending deferred leaf gradient of x's shape that reads one of x's
+    inputs, or None."""
+    for s in _SIBLINGS:
+        if (s._st is None and s._lz is not None and s._shape == x._shape and
+                not s._lz.deps.isdisjoint(x._lz.deps) and id(x) not in s._lz.deps and
+                id(s) not in x._lz.deps):
+            return s
+    return None
+
+
+def _finish_siblings():
+    """Evaluates the sibling gradients no column sum took along."""
+    while _SIBLINGS:
+        s = _SIBLINGS.pop()
+        if s._st is None:
+            s._storage
 
 
 # ----------------------------------------------------------------- HIP graphs
@@ -2803,12 +2849,14 @@ def run_backward(pairs, retain_graph=False, inputs=None):
                 node.inputs = [None] * len(node.inputs)
         if deferred:
             _flush_deferred(deferred)
+        _finish_siblings()
         if wanted is not None:
             return [_dense(results.get(id(t))) for t in inputs]
         return None
     finally:
         if deferred:
             _flush_deferred(deferred)
+        _SIBLINGS.clear()
         _grad["enabled"] = prev
 
 
@@ -2895,6 +2943,14 @@ def _leaf_accumulate(t, g, owned, force_copy=False):
     """Accumulates into t.grad.  A gradient tensor handed to a leaf is never
     shared with another leaf (the same incoming grad can flow to several
     inputs of an add), so later in-place edits of one .grad stay local."""
+    if (_is_lazy(g) and g._lz.kind != "alias" and not force_copy and t._grad is None and
+            _FUSE_SIB and _LAZY["jit"]):
+        # a deferred gradient stays deferred until a column sum over a
+        # sibling takes it along, or the pass ends; nothing else holds it
+        owned.add(_skey(g))
+        t._grad = g
+        _SIBLINGS.append(g)
+        return
     if _is_lazy(g) and g._lz.kind != "alias" and not force_copy:
         g._storage  # a deferred gradient evaluates into memory nothing else holds
     elif force_copy or not g.is_contiguous() or _skey(g) in owned:
