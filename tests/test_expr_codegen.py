@@ -98,6 +98,10 @@ def test_invalid_programs_are_rejected():
         assert lib.tjh_expr_compile(ctypes.byref(p), 16, 0) == 1, lib.tjh_last_error()
     p = _prog([], [], 0)
     assert lib.tjh_expr_compile(ctypes.byref(p), 16, 0) == 1
+    for r2 in (2, 17, -1):  # second result: unwritten register, out of range
+        p = _prog([("load", 0, 0, 0, N, N, 0.0)], [(ALIGNED, "contig", 0)], 0)
+        p.result2 = r2
+        assert lib.tjh_expr_compile(ctypes.byref(p), 16, 1) == 1, r2
 
 
 # ------------------------------------------------------------ the host builder
@@ -115,8 +119,9 @@ _NP_BINARY = {"add": np.add, "sub": np.subtract, "mul": np.multiply, "maximum": 
 _NP_SCALAR = {"add": np.add, "sub": np.subtract, "mul": np.multiply}
 
 
-def _interpret(prog, shape, data):
-    """Runs a tjh_expr program over numpy leaves (`data`: ptr -> array)."""
+def _interpret(prog, shape, data, second=False):
+    """Runs a tjh_expr program over numpy leaves (`data`: ptr -> array);
+    returns its value, or its second value (result2)."""
     n = int(np.prod(shape))
     e = np.arange(n)
     leaves = []
@@ -148,7 +153,7 @@ def _interpret(prog, shape, data):
         else:
             raise AssertionError(op)
         regs[q.dst] = v
-    return regs[prog.result].reshape(shape)
+    return regs[prog.result2 - 1 if second else prog.result].reshape(shape)
 
 
 def _leaf(shape, ptr, data, rng, strides=None, full=None):
@@ -199,6 +204,32 @@ def test_builder_matches_graph(lazy_on):
     kinds = sorted(prog.kind[k] for k in range(prog.n_leaves))
     assert kinds == sorted([0, 0, L.LEAF["row"], L.LEAF["col"], L.LEAF["scalar"]])
     _compile(prog, 48, 0)
+
+
+def test_builder_second_value(lazy_on):
+    """Two deferred values over common leaves as one program: each leaf
+    loaded once, shared subexpressions computed once, the second value's
+    register held to the end; both values as the graph computes them, and
+    the two-output column-sum kernel compiles."""
+    rng = np.random.default_rng(9)
+    data = {}
+    S = (8, 16)
+    x = _leaf(S, 0x1000, data, rng)
+    y = _leaf(S, 0x2000, data, rng)
+    b = _leaf((16,), 0x3000, data, rng)
+    e = T._k_unary("exp", T._k_binary("add", x, b))
+    gx = T._k_binary("mul", e, y)                      # x's gradient
+    gy = T._k_scalar("mul", e, 2.0)                    # y's gradient
+    prog, _ = T._program(gx, gy)
+    assert prog.result2 > 0
+    X, Y, B = (data[p].astype(np.float64) for p in (0x1000, 0x2000, 0x3000))
+    np.testing.assert_allclose(_interpret(prog, S, data), np.exp(X + B) * Y, rtol=1e-12)
+    np.testing.assert_allclose(_interpret(prog, S, data, second=True), 2.0 * np.exp(X + B),
+                               rtol=1e-12)
+    ops = [prog.ins[i].op for i in range(prog.n_ins)]
+    assert ops.count(L.EXPR_OP["load"]) == 3
+    assert ops.count(L.EXPR_OP["unary"]) == 1           # exp(x + b) once for both
+    _compile(prog, 128, 1)
 
 
 def test_builder_register_reuse_and_limits(lazy_on):
