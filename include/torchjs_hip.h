@@ -674,6 +674,14 @@ typedef struct {
 
 int tjh_conv2d_forward(const tjh_conv2d_desc* d, const float* x,
                        const float* w, const float* bias, float* y);
+/* tjh_conv2d_forward with the activation that follows the convolution in
+ * torch.js's CNNs (conv2d then relu, src/nn/conv.ts + F.relu's
+ * unary.wgsl) applied as the output is written: act 0 none, 1 ReLU (the
+ * library's own, so the result equals tjh_conv2d_forward then tjh_unary
+ * RELU bit for bit; ReLU's gradient can be taken from this output). */
+int tjh_conv2d_forward_act(const tjh_conv2d_desc* d, const float* x,
+                           const float* w, const float* bias, float* y,
+                           int act);
 /* dx = conv_transpose(dy, w) (written, not accumulated). */
 int tjh_conv2d_backward_input(const tjh_conv2d_desc* d, const float* dy,
                               const float* w, float* dx);

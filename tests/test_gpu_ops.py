@@ -855,6 +855,30 @@ def test_conv2d_weight_and_bias_grad_in_one_pass(torch, N, C, H, OC, s, grp, acc
     assert np.array_equal(dbt.numpy(), dbt2.numpy())
 
 
+@pytest.mark.parametrize("N,C,H,OC,s,p,grp", [(4, 3, 17, 8, 1, 1, 1), (3, 8, 16, 12, 2, 1, 2),
+                                               (2, 6, 9, 6, 1, 0, 3)])
+def test_conv2d_relu_equals_conv_then_relu(torch, N, C, H, OC, s, p, grp):
+    """F.conv2d_relu: the output, and the input, weight and bias gradients,
+    equal F.relu(F.conv2d(...)) bit for bit."""
+    r = np.random.default_rng(N * 100 + OC + s)
+    x0 = f32(r.standard_normal((N, C, H, H)))
+    w0 = f32(r.standard_normal((OC, C // grp, 3, 3)) * 0.3)
+    b0 = f32(r.standard_normal(OC) * 0.3)
+    outs = []
+    for fused in (True, False):
+        x, w, b = (torch.tensor(a, requires_grad=True) for a in (x0, w0, b0))
+        if fused:
+            y = torch.F.conv2d_relu(x, w, b, s, p, 1, grp)
+        else:
+            y = torch.F.relu(torch.F.conv2d(x, w, b, s, p, 1, grp))
+        g = f32(np.random.default_rng(5).standard_normal(y.shape))
+        y.backward(torch.tensor(g))
+        outs.append([y.numpy(), x.grad.numpy(), w.grad.numpy(), b.grad.numpy()])
+    for a_, b_ in zip(*outs):
+        assert np.array_equal(a_, b_)
+    assert (outs[0][0] == 0).any() and (outs[0][0] > 0).any()
+
+
 # ------------------------------------------------------------------ optimizers
 
 

@@ -88,7 +88,9 @@ def test_chain_full_config(torch, n):
 
 
 def test_cnn_full_batch(torch):
-    """The small CNN at its full config (batch 32, 3x64x64) against the oracle."""
+    """The small CNN at its full config (batch 32, 3x64x64) against the
+    oracle, with each conv and its ReLU as one op (the default) and as two:
+    the same loss and gradients bit for bit."""
     from torchjs_amd import workloads as W
     g = Generator(7)
     x = g.randn((32, 3, 64, 64))
@@ -96,14 +98,22 @@ def test_cnn_full_batch(torch):
     p = {"conv1.weight": g.uniform((32, 3, 3, 3), -0.19, 0.19), "conv1.bias": g.uniform((32,), -0.19, 0.19),
          "conv2.weight": g.uniform((64, 32, 3, 3), -0.059, 0.059), "conv2.bias": g.uniform((64,), -0.059, 0.059),
          "fc.weight": g.uniform((10, 64), -0.125, 0.125), "fc.bias": g.uniform((10,), -0.125, 0.125)}
-    model = W.CNN()
-    W.load_params(model, p)
-    loss = torch.F.cross_entropy(model(torch.tensor(x)), torch.tensor(t))
-    loss.backward()
     ref, rg = om.cnn_loss_and_grads(p, x, t)
-    check_red(loss.item(), ref, "loss")
-    for k, prm in model.named_parameters():
-        check_red(prm.grad.numpy(), rg[k], k)
+    runs = []
+    for fused in (True, False):
+        model = W.CNN(fused=fused)
+        W.load_params(model, p)
+        loss = torch.F.cross_entropy(model(torch.tensor(x)), torch.tensor(t))
+        loss.backward()
+        check_red(loss.item(), ref, "loss")
+        grads = {}
+        for k, prm in model.named_parameters():
+            grads[k] = prm.grad.numpy()
+            check_red(grads[k], rg[k], k)
+        runs.append((loss.item(), grads))
+    assert runs[0][0] == runs[1][0]
+    for k in runs[0][1]:
+        assert np.array_equal(runs[0][1][k], runs[1][1][k]), k
 
 
 @pytest.mark.parametrize("B,T", [(2, 128), (1, 1024)])

@@ -23,7 +23,7 @@ EXPORTS = ["init", "deviceInfo", "malloc", "h2d", "d2h", "d2hAsync", "synchroniz
            "kprofNames", "timerStart", "timerStop", "fillI32", "copyStridedI32", "castF32I32",
            "castI32F32", "ternary", "powScalarBackward", "axpy", "maskedFill", "compare",
            "argmax", "nllLossForward", "nllLossBackward", "indexSelect", "indexAdd", "gather",
-           "scatterAdd", "oneHot", "oneHotI32", "nonzero", "conv2dForward",
+           "scatterAdd", "oneHot", "oneHotI32", "nonzero", "conv2dForward", "conv2dForwardAct",
            "conv2dBackwardInput", "conv2dBackwardWeight", "conv2dBackwardWeightBias", "cast", "fillU8", "copyStridedU8",
            "triangle", "multinomial", "timerEnd", "timerRead", "rangePush", "rangePop",
            "mark", "exprEval", "exprColsum", "exprColsum2", "exprCompile", "graphBegin", "graphEnd", "graphReplay",

@@ -168,6 +168,7 @@ SIGNATURES = {
     "tjh_sdpa_backward": [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64,
                           c_i64, c_i64, c_i64, ctypes.POINTER(P_i64), c_f32, c_int],
     "tjh_conv2d_forward": [ctypes.POINTER(Conv2dDesc), c_vp, c_vp, c_vp, c_vp],
+    "tjh_conv2d_forward_act": [ctypes.POINTER(Conv2dDesc), c_vp, c_vp, c_vp, c_vp, c_int],
     "tjh_conv2d_backward_input": [ctypes.POINTER(Conv2dDesc), c_vp, c_vp, c_vp],
     "tjh_conv2d_backward_weight": [ctypes.POINTER(Conv2dDesc), c_vp, c_vp, c_vp, c_int],
     "tjh_conv2d_backward_weight_bias": [ctypes.POINTER(Conv2dDesc), c_vp, c_vp, c_vp, c_vp, c_int],

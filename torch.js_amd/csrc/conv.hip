@@ -87,6 +87,7 @@ struct ConvArgs {
   float* db;          // wgrad: the bias gradient (row sums of dy), or null
   float* rsw;         // wgrad split partials of db [groups][splits][M], or null
   int accumulate;     // wgrad without split: dW (and db) += instead of =
+  int relu;           // forward: the output is ReLU(conv + bias)
   uint32_t n, c, h, w, oc, kh, kw, sh, sw, ph, pw, dh, dw, oh, ow;
   uint32_t cg, ocg, kk;      // channels per group, KH*KW
   uint32_t M, N, K;          // GEMM sizes per group
@@ -539,7 +540,8 @@ __global__ __launch_bounds__(kThreads, 2) void k_conv_igemm(ConvArgs a0, ClassSe
     const float v = acc[r];
     if (MODE == kFwd) {
       const uint32_t oc = g * a.ocg + row;
-      a.out[(n_img * a.oc + oc) * P + pix] = a.bias ? v + a.bias[oc] : v;
+      const float o = a.bias ? v + a.bias[oc] : v;
+      a.out[(n_img * a.oc + oc) * P + pix] = a.relu ? fmaxf(o, 0.0f) : o;  // the library's ReLU
     } else if (MODE == kDgrad || MODE == kDgradClass) {
       a.out[(n_img * a.c + g * a.cg + row) * HW + pix] = v;
     } else if (a.ws) {
@@ -700,12 +702,19 @@ extern "C" {
 
 int tjh_conv2d_forward(const tjh_conv2d_desc* d, const float* x, const float* w,
                        const float* bias, float* y) {
+  return tjh_conv2d_forward_act(d, x, w, bias, y, 0);
+}
+
+int tjh_conv2d_forward_act(const tjh_conv2d_desc* d, const float* x, const float* w,
+                           const float* bias, float* y, int act) {
   TJH_REQUIRE_INIT();
+  TJH_ARG(act == 0 || act == 1, "tjh_conv2d_forward_act: bad activation %d", act);
   int rc = check_desc(d);
   if (rc != TJH_OK) return rc;
   if (d->n == 0) return TJH_OK;
   ConvArgs a = make_args(d);
   a.x = x; a.wt = w; a.bias = bias; a.out = y;
+  a.relu = act;
   a.M = a.ocg;
   a.N = (uint32_t)(d->n * d->oh * d->ow);
   a.K = a.cg * a.kk;

@@ -9,6 +9,7 @@ import numpy as np
 
 from . import _lib as L
 from . import tensor as _T
+from .tensor import _e_unary_bwd
 from .tensor import (Tensor, _DT, _alias, _contig_strides, _empty_padded, _gemm, _k_binary,
                      _k_contiguous, _k_reduce, _k_scalar, _numel, _record, _view_raw, _wrap_dim,
                      contiguous, empty, full, mul, permute, reduce_mean, reshape, reshape_raw,
@@ -502,6 +503,18 @@ def conv2d(input, weight, bias=None, stride=1, padding=0, dilation=1, groups=1):
     """F.conv2d (src/nn/functional.ts:438-660): NCHW cross-correlation with
     stride / padding / dilation / groups; dgrad, wgrad and bias grad
     (torch.js never runs its conv backward, D8)."""
+    return _conv2d(input, weight, bias, stride, padding, dilation, groups, False)
+
+
+def conv2d_relu(input, weight, bias=None, stride=1, padding=0, dilation=1, groups=1):
+    """F.relu(F.conv2d(...)) as one op: the convolution writes ReLU of its
+    output, and the backward takes ReLU's gradient mask from that output
+    (y > 0 exactly where the pre-activation is > 0); bit for bit the two
+    ops in sequence."""
+    return _conv2d(input, weight, bias, stride, padding, dilation, groups, True)
+
+
+def _conv2d(input, weight, bias, stride, padding, dilation, groups, relu):
     x = input
     if x.dtype != "float32":
         x = x.float()
@@ -521,13 +534,16 @@ def conv2d(input, weight, bias=None, stride=1, padding=0, dilation=1, groups=1):
     wc = weight.detach().contiguous()
     bc = bias.detach().contiguous() if bias is not None else None
     y = empty((n, oc, oh, ow))
-    L.check(L.lib().tjh_conv2d_forward(ctypes.byref(desc), xc.data_ptr(), wc.data_ptr(),
-                                       bc.data_ptr() if bc is not None else None, y.data_ptr()),
-            "conv2d")
+    L.check(L.lib().tjh_conv2d_forward_act(ctypes.byref(desc), xc.data_ptr(), wc.data_ptr(),
+                                           bc.data_ptr() if bc is not None else None,
+                                           y.data_ptr(), 1 if relu else 0), "conv2d")
     rx, rw = x.requires_grad, weight.requires_grad
     rb = bias is not None and bias.requires_grad
+    yd = y.detach() if relu else None
 
     def bwd(g):
+        if relu:
+            g = _e_unary_bwd("relu", g, yd, None)  # ReLU'(pre) = (y > 0)
         g = g.contiguous()
         dx = dwt = db = None
         if rx:
@@ -546,7 +562,7 @@ def conv2d(input, weight, bias=None, stride=1, padding=0, dilation=1, groups=1):
         elif rb:
             db = _view_raw(_k_reduce("sum", g, [0, 2, 3]), (oc,))
         return [dx, dwt, db]
-    return _record(y, "Conv2d", [x, weight, bias], bwd)
+    return _record(y, "Conv2dReLU" if relu else "Conv2d", [x, weight, bias], bwd)
 
 
 # ------------------------------------------------------------ attention

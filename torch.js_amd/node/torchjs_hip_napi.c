@@ -1163,6 +1163,15 @@ static napi_value js_conv_forward(napi_env env, napi_callback_info info) {
   CHECK_RC(tjh_conv2d_forward(&d, CF32(a[1]), CF32(a[2]), CF32(a[3]), F32(a[4])));
   return undef(env);
 }
+/* conv2dForwardAct(desc, x, w, bias, y, act) */
+static napi_value js_conv_forward_act(napi_env env, napi_callback_info info) {
+  napi_value a[6];
+  tjh_conv2d_desc d;
+  if (!get_args(env, info, 6, a) || !conv_desc(env, a[0], &d)) return NULL;
+  CHECK_RC(tjh_conv2d_forward_act(&d, CF32(a[1]), CF32(a[2]), CF32(a[3]), F32(a[4]),
+                                  (int)i64(env, a[5])));
+  return undef(env);
+}
 static napi_value js_conv_backward_input(napi_env env, napi_callback_info info) {
   napi_value a[4];
   tjh_conv2d_desc d;
@@ -1231,6 +1240,7 @@ static napi_value init_module(napi_env env, napi_value exports) {
       FN("indexSelect", js_index_select), FN("indexAdd", js_index_add), FN("gather", js_gather),
       FN("scatterAdd", js_scatter_add), FN("oneHot", js_one_hot), FN("oneHotI32", js_one_hot_i32),
       FN("nonzero", js_nonzero), FN("conv2dForward", js_conv_forward),
+      FN("conv2dForwardAct", js_conv_forward_act),
       FN("conv2dBackwardInput", js_conv_backward_input),
       FN("conv2dBackwardWeight", js_conv_backward_weight),
       FN("conv2dBackwardWeightBias", js_conv_backward_weight_bias),
