@@ -508,18 +508,24 @@ __global__ __launch_bounds__(kBlock) void k_ln_fwd_wave(const float* __restrict_
   if (r >= rows) return;
   const int c4 = (int)(cols >> 2);
   const float4* xr = reinterpret_cast<const float4*>(x + r * cols);
-  float4 v[V4];
-  float s = 0.f;
+  const float4* g4 = reinterpret_cast<const float4*>(gamma);
+  const float4* b4 = reinterpret_cast<const float4*>(beta);
+  float4 v[V4], gv[V4], bv[V4];
+  // gamma and beta go out with the row's loads, not after the reductions
 #pragma unroll
   for (int j = 0; j < V4; ++j) {
     int i = lane + 64 * j;
     if (EXACT || i < c4) {
       v[j] = xr[i];
-      s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
+      gv[j] = gamma ? g4[i] : make_float4(1.f, 1.f, 1.f, 1.f);
+      bv[j] = beta ? b4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
     } else {
       v[j] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
   }
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < V4; ++j) s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
   float mean = wave_sum(s) / (float)cols;
   float q = 0.f;
 #pragma unroll
@@ -533,8 +539,6 @@ __global__ __launch_bounds__(kBlock) void k_ln_fwd_wave(const float* __restrict_
   float var = wave_sum(q) / (float)cols;
   float rstd = 1.0f / sqrtf(var + eps);
   float4* yr = reinterpret_cast<float4*>(y + r * cols);
-  const float4* g4 = reinterpret_cast<const float4*>(gamma);
-  const float4* b4 = reinterpret_cast<const float4*>(beta);
 #pragma unroll
   for (int j = 0; j < V4; ++j) {
     int i = lane + 64 * j;
@@ -545,11 +549,11 @@ __global__ __launch_bounds__(kBlock) void k_ln_fwd_wave(const float* __restrict_
       o.z = (v[j].z - mean) * rstd;
       o.w = (v[j].w - mean) * rstd;
       if (gamma) {
-        float4 gg = g4[i];
+        const float4 gg = gv[j];
         o.x *= gg.x; o.y *= gg.y; o.z *= gg.z; o.w *= gg.w;
       }
       if (beta) {
-        float4 bb = b4[i];
+        const float4 bb = bv[j];
         o.x += bb.x; o.y += bb.y; o.z += bb.z; o.w += bb.w;
       }
       yr[i] = o;
