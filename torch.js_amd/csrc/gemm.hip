@@ -501,7 +501,20 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(GemmArgs g, int splits) {
     const uint32_t row = e / w, c0 = (e - row * w) * (VEC ? 4 : 1);
     const int64_t off = (int64_t)row * g.N + c0;
     float s[4] = {0.f, 0.f, 0.f, 0.f};
-    for (int q = 0; q < splits; ++q) {
+    // four splits' loads in flight before their adds (the same order of adds)
+    int q = 0;
+    if (VEC) {
+      for (; q + 4 <= splits; q += 4) {
+        float4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[u] = ld_nt(W + (q + u) * mn + off);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          s[0] += v[u].x; s[1] += v[u].y; s[2] += v[u].z; s[3] += v[u].w;
+        }
+      }
+    }
+    for (; q < splits; ++q) {
       if (VEC) {
         const float4 v = ld_nt(W + q * mn + off);
         s[0] += v.x; s[1] += v.y; s[2] += v.z; s[3] += v.w;
