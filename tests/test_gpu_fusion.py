@@ -127,6 +127,29 @@ def test_chain_sibling_gradients_in_one_pass(torch, T, extra):
         assert sum(launches[0].values()) < sum(launches[1].values()), launches
 
 
+def test_deferred_gradient_shared_by_two_leaves(torch, T):
+    """An add hands one deferred gradient to both of its leaf inputs: each
+    leaf's .grad gets memory of its own, so an in-place edit of one leaves
+    the other unchanged (with sibling evaluation on and off)."""
+    xs, ys = _rand((256, 512), 61), _rand((256, 512), 62)
+    prev = T._FUSE_SIB
+    try:
+        for sib in (True, False):
+            T._FUSE_SIB = sib
+            a = torch.tensor(xs, requires_grad=True)
+            b = torch.tensor(ys, requires_grad=True)
+            ((a + b).exp() * 0.5).sum().backward()
+            assert not T._SIBLINGS
+            want = 0.5 * np.exp(xs.astype(np.float64) + ys)
+            np.testing.assert_allclose(a.grad.numpy(), want, rtol=1e-5)
+            gb = b.grad.numpy().copy()
+            a.grad.zero_()
+            assert np.array_equal(b.grad.numpy(), gb), sib
+            assert not a.grad.numpy().any()
+    finally:
+        T._FUSE_SIB = prev
+
+
 @pytest.mark.parametrize("op", ["neg", "exp", "log", "sqrt", "rsqrt", "tanh", "sigmoid", "relu",
                                 "gelu", "square", "reciprocal", "erf", "abs", "sin", "cos",
                                 "silu", "leaky_relu", "elu", "softplus", "sign"])

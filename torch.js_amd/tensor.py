@@ -2943,15 +2943,16 @@ def _leaf_accumulate(t, g, owned, force_copy=False):
     """Accumulates into t.grad.  A gradient tensor handed to a leaf is never
     shared with another leaf (the same incoming grad can flow to several
     inputs of an add), so later in-place edits of one .grad stay local."""
-    if (_is_lazy(g) and g._lz.kind != "alias" and not force_copy and t._grad is None and
-            _FUSE_SIB and _LAZY["jit"]):
+    lazy = _is_lazy(g) and g._lz.kind != "alias"
+    if (lazy and not force_copy and t._grad is None and _FUSE_SIB and _LAZY["jit"] and
+            _skey(g) not in owned):
         # a deferred gradient stays deferred until a column sum over a
-        # sibling takes it along, or the pass ends; nothing else holds it
+        # sibling takes it along, or the pass ends; no other leaf holds it
         owned.add(_skey(g))
         t._grad = g
         _SIBLINGS.append(g)
         return
-    if _is_lazy(g) and g._lz.kind != "alias" and not force_copy:
+    if lazy and not force_copy and _skey(g) not in owned:
         g._storage  # a deferred gradient evaluates into memory nothing else holds
     elif force_copy or not g.is_contiguous() or _skey(g) in owned:
         g = _k_contiguous(g)
