@@ -101,7 +101,10 @@ typedef struct {
   uint64_t pooled_bytes;  /* bytes cached for reuse                       */
   uint64_t peak_bytes;    /* max active_bytes since the last reset        */
   uint64_t allocations;   /* tjh_malloc calls served                      */
-  uint64_t device_mallocs;/* hipMalloc calls made (cache misses)          */
+  uint64_t device_mallocs;/* hipMalloc calls made (cache misses): the
+                             reference's allocationCount /
+                             total_allocations, which count the buffers its
+                             pool creates (buffer.ts:50-57)               */
 } tjh_mem_stats;
 
 /* Stream-ordered caching allocator on HBM.  Blocks are 256-byte aligned.
@@ -572,13 +575,18 @@ int tjh_nonzero(const float* x, int ndim, const int64_t* shape,
 
 /* Tensor.multinomial (src/tensor/Tensor.ts:271-359) on the device: out
  * [rows, num_samples] int32 category indices drawn from each row of probs
- * [rows, cols] (contiguous).  Row weights are max(0, x) (NaN as 0),
- * normalised by their sum; a row summing to <= 0 samples uniformly.  With
- * replacement, a draw u picks the first index whose running sum of the
- * normalised weights exceeds u; without it, each draw renormalises over
- * the indices not yet taken (num_samples <= cols, cols <= 2^18).  Draw s
- * of row r uses the uniform of element r * num_samples + s of tjh_random
- * with the same seed, so callers can replay every draw. */
+ * [rows, cols] (contiguous).  Row weights are max(0, x) (negatives and
+ * -inf weigh 0), normalised by their sum; a row summing to <= 0 samples
+ * uniformly.  With replacement, a draw u picks the first index whose
+ * running sum of the normalised weights exceeds u; without it, each draw
+ * renormalises over the indices not yet taken (num_samples <= cols,
+ * cols <= 2^18), and once the positive-weight categories are used up each
+ * draw takes the last untaken index.  Draw s of row r uses the uniform of
+ * element r * num_samples + s of tjh_random with the same seed, so callers
+ * can replay every draw.  A row holding NaN or +inf is an error
+ * (TJH_ERR_INVALID, as PyTorch raises; the reference's result is undefined
+ * there): its draws are written as -1.  The call reads a status word per
+ * row back, so it synchronises the stream and is refused during capture. */
 int tjh_multinomial(const float* probs, int64_t rows, int64_t cols,
                     int64_t num_samples, int replacement, uint32_t seed,
                     int32_t* out);

@@ -156,6 +156,12 @@ def binary_backward(op, g, a, b):
         elif op == "mul": ga, gb = g * b, g * a
         elif op == "div": ga, gb = g / b, -g * a / (b * b)
         elif op == "pow": ga, gb = g * b * np.power(a, b - 1), g * np.power(a, b) * np.log(a)
+        elif op in ("maximum", "minimum"):
+            # the selected operand takes g; a tie gives each operand g / 2
+            # (PyTorch's rule for torch.maximum / torch.minimum)
+            wa = np.where(a == b, 0.5, np.where(a > b, 1.0, 0.0) if op == "maximum"
+                          else np.where(a < b, 1.0, 0.0))
+            ga, gb = g * wa, g * (1.0 - wa)
         else: raise ValueError(op)
     return sum_to(ga, a.shape), sum_to(gb, b.shape)
 
@@ -646,19 +652,34 @@ def adam_step(p, g, m, v, step, lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_de
 
 def multinomial(x, num_samples, replacement, u):
     """Tensor.multinomial (src/tensor/Tensor.ts:271-359) given the draws
-    u[row, s] in [0, 1): weights p = max(0, x) (NaN as 0), uniform when
-    their sum is not positive (Tensor.ts:331-339).  With replacement, the
-    first index whose running sum of p / sum exceeds u (the last index when
-    none does, Tensor.ts:344-356).  Without replacement, each draw picks
-    the first untaken index whose running sum of p exceeds u times the
-    untaken mass (the last untaken index when none does): the distribution
-    of the reference's redraw-until-new loop (Tensor.ts:331-343), one draw
-    per sample.  Float64 running sums, in index order."""
+    u[row, s] in [0, 1): weights p = max(0, x) (Tensor.ts:316; negative
+    weights and -inf weigh 0), uniform when their sum is not positive
+    (Tensor.ts:319-322).  With replacement, the first index whose running
+    sum of p / sum exceeds u (the last index when none does,
+    Tensor.ts:343-353).  Without replacement, each draw picks the first
+    untaken index whose running sum of p exceeds u times the untaken mass:
+    the distribution of the reference's redraw-until-new loop
+    (Tensor.ts:327-341), one draw per sample.  Float64 running sums, in
+    index order.
+
+    Two cases the reference leaves undefined get a stated contract:
+    - a row holding NaN or +inf raises ValueError (PyTorch raises; in the
+      reference Math.max(0, NaN) is NaN, every cumulative probability is
+      NaN, and the draws fall to the last index with replacement or loop
+      forever without it);
+    - without replacement, once every positive-weight category is taken,
+      each further draw takes the last untaken index (the reference falls
+      back to index 0 and redraws until it finds a new one, which never
+      ends when 0 is taken; PyTorch raises)."""
     x = np.asarray(x, dtype=F64)
     one = x.ndim == 1
     x = np.atleast_2d(x)
     u = np.asarray(u, dtype=F64).reshape(x.shape[0], num_samples)
     rows, C = x.shape
+    bad = np.isnan(x) | (x == np.inf)
+    if bad.any():
+        raise ValueError("multinomial: probability row %d contains NaN or inf"
+                         % int(np.flatnonzero(bad.any(axis=1))[0]))
     out = np.zeros((rows, num_samples), dtype=np.int32)
     for r in range(rows):
         p = np.where(x[r] > 0, x[r], 0.0)

@@ -42,12 +42,20 @@ def unary_ops(rng):
         "sin": (torch.sin, x), "cos": (torch.cos, x), "silu": (torch.nn.functional.silu, x),
         "softplus": (torch.nn.functional.softplus, x),
     }
+    F = torch.nn.functional
+    fns.update({
+        "leaky_relu_0.01": (lambda v: F.leaky_relu(v, 0.01), x),
+        "leaky_relu_0.2": (lambda v: F.leaky_relu(v, 0.2), x),
+        "elu_1.0": (lambda v: F.elu(v, 1.0), x), "elu_0.7": (lambda v: F.elu(v, 0.7), x),
+        "sign": (torch.sign, np.concatenate([x[:60], [0.0, -0.0, 1e-300, -1e-300]])),
+    })
     for name, (fn, inp) in fns.items():
         a = t(inp, True)
         y = fn(a)
         y.backward(t(g))
         d["fwd_" + name] = y
         d["bwd_" + name] = a.grad
+    d["x_sign"] = fns["sign"][1]
     save("unary", **d)
 
 
@@ -57,11 +65,23 @@ def binary_ops(rng):
     g = rng.standard_normal((3, 4, 5))
     d = {"a": a, "b": b, "g": g}
     for name, fn in {"add": torch.add, "sub": torch.sub, "mul": torch.mul, "div": torch.div,
-                     "pow": torch.pow}.items():
+                     "pow": torch.pow, "maximum": torch.maximum,
+                     "minimum": torch.minimum}.items():
         ta, tb = t(a, True), t(b, True)
         y = fn(ta, tb)
         y.backward(t(g))
         d["fwd_" + name], d["ga_" + name], d["gb_" + name] = y, ta.grad, tb.grad
+    # maximum / minimum with ties (PyTorch splits a tied gradient evenly)
+    rt = np.random.default_rng(20261203)  # own stream: the other files keep theirs
+    at = rt.integers(-2, 3, size=(6, 7)).astype(np.float64)
+    bt = rt.integers(-2, 3, size=(7,)).astype(np.float64)
+    gt = rt.standard_normal((6, 7))
+    d["a_tie"], d["b_tie"], d["g_tie"] = at, bt, gt
+    for name, fn in {"maximum": torch.maximum, "minimum": torch.minimum}.items():
+        ta, tb = t(at, True), t(bt, True)
+        y = fn(ta, tb)
+        y.backward(t(gt))
+        d["tie_fwd_" + name], d["tie_ga_" + name], d["tie_gb_" + name] = y, ta.grad, tb.grad
     save("binary", **d)
 
 
@@ -73,6 +93,18 @@ def reductions(rng):
     d["mean_02"] = t(x).mean((0, 2))
     d["max_2"] = t(x).amax(2)
     d["argmax_1"] = t(x).argmax(1).to(torch.int32)
+    d["min_2"] = t(x).amin(2)
+    d["min_0"] = t(x).amin(0)
+    d["prod_1"] = t(x).prod(1)
+    d["prod_all"] = t(x[:2, :3]).prod()
+    d["argmin_1"] = t(x).argmin(1).to(torch.int32)
+    d["argmin_all"] = t(x).argmin().to(torch.int32)
+    xt = np.random.default_rng(20261204).integers(-2, 3, size=(5, 9)).astype(np.float64)
+    # ties: the first index wins
+    d["x_tie"] = xt
+    d["tie_argmax_1"] = t(xt).argmax(1).to(torch.int32)
+    d["tie_argmin_1"] = t(xt).argmin(1).to(torch.int32)
+    d["tie_argmin_0"] = t(xt).argmin(0).to(torch.int32)
     ta = t(x, True)
     up = rng.standard_normal(5)
     ta.mean((0, 2)).backward(t(up))
@@ -335,9 +367,12 @@ def serialization_fixtures():
             np.array([[-128, 5], [0, 127]], "i1")]
     zb = io.BytesIO()
     with zipfile.ZipFile(zb, "w", zipfile.ZIP_DEFLATED) as z:
-        z.writestr("model.json", json.dumps(doc, indent=2))
+        # a fixed entry date, so that a rerun writes the same bytes
+        def entry(name):
+            return zipfile.ZipInfo(name, date_time=(2026, 12, 2, 3, 23, 0))
+        z.writestr(entry("model.json"), json.dumps(doc, indent=2), zipfile.ZIP_DEFLATED)
         for i, a in enumerate(bins):
-            z.writestr("tensors/%d.bin" % i, a.tobytes())
+            z.writestr(entry("tensors/%d.bin" % i), a.tobytes(), zipfile.ZIP_DEFLATED)
     with open(os.path.join(OUT, "torchjs_archive.zip"), "wb") as f:
         f.write(zb.getvalue())
 

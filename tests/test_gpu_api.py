@@ -387,12 +387,12 @@ def test_multinomial_replays_oracle(torch, rows, cols, ns, repl):
     x[0, ::4] = 0.0
     if rows > 2:
         x[1] = -1.0  # no positive weight: uniform
-        x[2, 5] = np.nan  # counts as 0
+        x[2, 5] = -np.inf  # weighs 0, like a negative weight
     torch.manual_seed(4321)
     got = torch.tensor(x).multinomial(ns, repl).numpy()
     seed = rng.lcg_next(4321)
     u = rng.rand(rows * ns, seed).reshape(rows, ns)
-    want = ops.multinomial(np.nan_to_num(x, nan=0.0), ns, repl, u)
+    want = ops.multinomial(x, ns, repl, u)
     assert got.shape == (rows, ns) and got.dtype == np.int32
     assert np.array_equal(got, want)
     if not repl:
@@ -407,6 +407,25 @@ def test_multinomial_literal_and_errors(torch):
     assert tok.shape == (1,) and 0 <= tok.item() < 100
     with pytest.raises(RuntimeError):
         torch.tensor([0.5, 0.5]).multinomial(3)
+
+
+@pytest.mark.parametrize("bad", [np.nan, np.inf])
+@pytest.mark.parametrize("repl", [True, False])
+def test_multinomial_rejects_nan_and_inf_rows(torch, bad, repl):
+    """A row holding NaN or +inf raises, as in the oracle (and PyTorch); the
+    call reads the per-row status back, so the error names the row.  The
+    library stays usable afterwards and a clean row still replays the
+    oracle."""
+    x = np.full((3, 40), 0.25, dtype=np.float32)
+    x[1, 17] = bad
+    with pytest.raises(ValueError):
+        ops.multinomial(x, 2, repl, np.zeros((3, 2)))
+    with pytest.raises(RuntimeError, match="row 1 contains NaN or inf"):
+        torch.tensor(x).multinomial(2, repl)
+    torch.manual_seed(77)
+    got = torch.tensor(x[:1]).multinomial(2, repl).numpy()
+    u = rng.rand(2, rng.lcg_next(77)).reshape(1, 2)
+    assert np.array_equal(got, ops.multinomial(x[:1], 2, repl, u))
 
 
 # ------------------------------------------------------------ attention masks, KV cache

@@ -146,8 +146,43 @@ def test_deferred_gradient_shared_by_two_leaves(torch, T):
             a.grad.zero_()
             assert np.array_equal(b.grad.numpy(), gb), sib
             assert not a.grad.numpy().any()
+            # three leaves along a chain of adds, ((q + r) + p): p takes the
+            # deferred gradient first, q's copy computes it, r must still get
+            # memory of its own (the deferred value's storage is owned by p)
+            zs = _rand((256, 512), 63)
+            q = torch.tensor(xs, requires_grad=True)
+            r = torch.tensor(ys, requires_grad=True)
+            p = torch.tensor(zs, requires_grad=True)
+            ((q + r) + p).exp().sum().backward()
+            assert not T._SIBLINGS
+            want = np.exp(xs.astype(np.float64) + ys + zs)
+            for leaf in (q, r, p):
+                np.testing.assert_allclose(leaf.grad.numpy(), want, rtol=1e-5)
+            keep = {id(leaf): leaf.grad.numpy().copy() for leaf in (q, r, p)}
+            for victim in (r, p, q):
+                victim.grad.zero_()
+                for leaf in (q, r, p):
+                    if leaf is victim:
+                        assert not leaf.grad.numpy().any()
+                    else:
+                        assert np.array_equal(leaf.grad.numpy(), keep[id(leaf)]), sib
+                keep[id(victim)] = victim.grad.numpy().copy()
     finally:
         T._FUSE_SIB = prev
+
+
+def test_write_through_detached_alias_of_deferred_value(torch, T):
+    """y = x.exp() stays deferred, p = y * 2 reads it; writing zeros through
+    y.detach() must first compute p from the old y (p = 2 exp(x)), and y
+    itself then reads as zeros."""
+    xs = _rand((256, 512), 64)  # above the size from which elementwise ops defer
+    x = torch.tensor(xs)
+    y = x.exp()
+    p = y * 2.0
+    assert T._is_lazy(y) and T._is_lazy(p)
+    y.detach().zero_()
+    np.testing.assert_allclose(p.numpy(), 2.0 * np.exp(xs.astype(np.float64)), rtol=1e-6)
+    assert not y.numpy().any()
 
 
 @pytest.mark.parametrize("op", ["neg", "exp", "log", "sqrt", "rsqrt", "tanh", "sigmoid", "relu",

@@ -3,6 +3,7 @@ inputs (MI355X).  Tolerances: integer / index work bit-exact; fp32
 elementwise rtol 1e-5; reductions, GEMM, attention, conv rtol 1e-4 /
 atol 1e-5 (reduction order differs from the float64 oracle)."""
 import ctypes
+import math
 
 import numpy as np
 import pytest
@@ -74,6 +75,17 @@ def test_roundtrip_and_allocator(torch):
     s1 = torch.hip.memory_stats()
     assert s1["device_mallocs"] - s0["device_mallocs"] <= 1  # cached blocks are reused
     assert s1["peak_bytes"] >= s1["active_bytes"]
+    # torch.webgpu.memory_stats()'s keys (src/webgpu.ts:11-19): total_allocations
+    # counts blocks created on a cache miss, like the reference's pool
+    assert set(s1) >= {"active_bytes", "pooled_bytes", "peak_bytes", "total_allocations"}
+    assert s1["total_allocations"] == s1["device_mallocs"]
+    assert s1["allocation_requests"] - s0["allocation_requests"] >= 5
+    assert torch.webgpu.memory_stats()["total_allocations"] == s1["total_allocations"]
+    summ = torch.webgpu.memory_summary()
+    lines = [l for l in summ.splitlines() if l]
+    assert lines[0] == "GPU Memory Summary" and lines[1] == "-" * 55
+    assert lines[2].startswith("Active Memory:   ") and lines[2].endswith(" MB")
+    assert lines[5] == "Total Allocs:    %d" % torch.hip.memory_stats()["total_allocations"]
     ints = torch.tensor(np.array([3, -7, 2 ** 30], dtype=np.int32))
     assert ints.dtype == "int32" and ints.numpy().tolist() == [3, -7, 2 ** 30]
     assert torch.tensor([-0.0, 1.5]).toArray() == [0.0, 1.5]
@@ -135,6 +147,31 @@ def test_rng_matches_oracle_stream(torch):
             assert np.array_equal(g, rng.rand(n, sd))
 
 
+def test_randn_box_muller_special_states(torch):
+    """tjh_random's normal stream at the seeds whose element 0 has the states
+    the oracle's closed-form checks use (u2 = 1/2, u2 = 1/4, u1 clamped at
+    1e-7, found by inverting xorshift32): the device gives -sqrt(-2 ln u1),
+    ~0 and +-5.677 as the mathematics fixes them."""
+    from test_oracle import _seed_for_states, _xs_inverse
+    from torchjs_amd import _lib as L
+    cases = []
+    for s2, cos_want in ((2 ** 31, -1.0), (2 ** 30, math.cos(float(np.float32(2 * math.pi)) / 4))):
+        seed, s1 = _seed_for_states(s2)
+        u1 = float(np.float32(s1 / 2 ** 32))
+        cases.append((seed, math.sqrt(-2.0 * math.log(u1)) * cos_want))
+    r_clamp = math.sqrt(-2.0 * math.log(float(np.float32(1e-7))))
+    for s1 in (1, 7, 429):
+        u2 = float(np.float32(int(rng.xorshift32(s1)) / 2 ** 32))
+        theta = float(np.float32(np.float32(2 * math.pi) * np.float32(u2)))
+        cases.append((_xs_inverse(s1) ^ 1013904223, r_clamp * math.cos(theta)))
+    out = torch.empty((1,))
+    for seed, want in cases:
+        L.check(L.lib().tjh_random(out.data_ptr(), 1, seed, 1), "random")
+        got = float(out.numpy()[0])
+        assert abs(got - want) <= 2e-6, (seed, got, want)
+        assert abs(got - float(rng.randn(1, seed)[0])) <= 2e-6
+
+
 # ------------------------------------------------------------------ elementwise
 
 
@@ -151,6 +188,48 @@ def test_unary_fwd_bwd(torch, op, n):
     out, g, (gx,) = grad_of(torch, lambda t: getattr(t, op)(), x)
     check(out, ops.unary(op, x), **EW)
     check(gx, ops.unary_backward(op, g, x), **EW)
+
+
+@pytest.mark.parametrize("n", [7, 4099, 1 << 20])
+@pytest.mark.parametrize("op,alpha", [("leaky_relu", 0.01), ("leaky_relu", 0.2), ("elu", 1.0),
+                                      ("elu", 0.7), ("sign", 0.0)])
+def test_parametric_unary_and_sign(torch, op, alpha, n):
+    """leaky_relu / elu at two slopes and sign against the oracle, with
+    zeros in the input (x > 0 selects the positive branch; sign(0) = 0 and
+    sign's gradient is 0)."""
+    r = np.random.default_rng(n + int(alpha * 100))
+    x = f32(r.uniform(-5, 5, n))
+    x[::5] = 0.0
+    if op == "sign":
+        fn = lambda t: t.sign()
+    else:
+        fn = lambda t: getattr(t, op)(alpha)
+    out, g, (gx,) = grad_of(torch, fn, x)
+    check(out, ops.unary(op, x, alpha), **EW)
+    check(gx, ops.unary_backward(op, g, x, alpha), **EW)
+
+
+@pytest.mark.parametrize("sa,sb", [((64, 33), (64, 33)), ((4096, 1024), (1024,)),
+                                   ((7, 5), (7, 1)), ((3, 4, 5), (4, 1))])
+@pytest.mark.parametrize("op", ["maximum", "minimum"])
+@pytest.mark.parametrize("ties", [False, True])
+def test_maximum_minimum_fwd_bwd(torch, op, sa, sb, ties):
+    """maximum / minimum forward and both gradients (summed over broadcast
+    dims) against the oracle; with integer operands many elements tie and
+    the oracle gives each side half of a tied gradient."""
+    r = np.random.default_rng(len(sa) * 11 + len(sb) + ties)
+    if ties:
+        a = f32(r.integers(-2, 3, sa))
+        b = f32(r.integers(-2, 3, sb))
+    else:
+        a = f32(r.uniform(-2.0, 2.0, sa))
+        b = f32(r.uniform(-2.0, 2.0, sb))
+    out, g, (ga, gb) = grad_of(torch, lambda x, y: getattr(x, op)(y), a, b)
+    assert np.array_equal(out, ops.binary(op, a, b).astype(np.float32))
+    ra, rb = ops.binary_backward(op, g, a, b)
+    tol = RED if (ra.size < g.size or rb.size < g.size) else EW
+    check(ga, ra, **tol)
+    check(gb, rb, **tol)
 
 
 def test_unary_on_unaligned_view(torch):

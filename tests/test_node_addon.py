@@ -80,3 +80,8 @@ def test_addon_end_to_end():
     # free() followed by GC never returns a block twice
     fg = out["free_then_gc"]
     assert fg["distinct"] and fg["doubleFreeThrows"] and fg["intact"], out
+    # bufferPool.getStats()'s names (src/backend/webgpu/buffer.ts:10-15)
+    mem = out["mem"]
+    for k in ("activeBytes", "pooledBytes", "peakBytes", "allocationCount"):
+        assert isinstance(mem[k], (int, float)) and mem[k] >= 0, mem
+    assert mem["allocationCount"] >= 1 and mem["allocationRequests"] >= mem["allocationCount"]

@@ -35,13 +35,40 @@ def test_unary_golden():
           atol=1e-6 * np.abs(z["g"]).max())
 
 
+@pytest.mark.parametrize("op,alpha", [("leaky_relu", 0.01), ("leaky_relu", 0.2), ("elu", 1.0),
+                                      ("elu", 0.7)])
+def test_unary_parametric_golden(op, alpha):
+    z = golden("unary")
+    key = "%s_%s" % (op, alpha)
+    close(ops.unary(op, z["x"], alpha), z["fwd_" + key])
+    close(ops.unary_backward(op, z["g"], z["x"], alpha), z["bwd_" + key])
+
+
+def test_sign_golden():
+    """sign, including 0, -0 and subnormal-sized inputs; its gradient is 0."""
+    z = golden("unary")
+    close(ops.unary("sign", z["x_sign"]), z["fwd_sign"], rtol=0, atol=0)
+    close(ops.unary_backward("sign", z["g"], z["x_sign"]), z["bwd_sign"], rtol=0, atol=0)
+
+
 def test_binary_golden():
     z = golden("binary")
-    for op in ["add", "sub", "mul", "div", "pow"]:
+    for op in ["add", "sub", "mul", "div", "pow", "maximum", "minimum"]:
         close(ops.binary(op, z["a"], z["b"]), z["fwd_" + op])
         ga, gb = ops.binary_backward(op, z["g"], z["a"], z["b"])
         close(ga, z["ga_" + op])
         close(gb, z["gb_" + op])
+
+
+@pytest.mark.parametrize("op", ["maximum", "minimum"])
+def test_maximum_minimum_ties_golden(op):
+    """Integer operands with many ties: a tied gradient is split evenly."""
+    z = golden("binary")
+    assert (z["a_tie"] == z["b_tie"]).any()
+    close(ops.binary(op, z["a_tie"], z["b_tie"]), z["tie_fwd_" + op], rtol=0, atol=0)
+    ga, gb = ops.binary_backward(op, z["g_tie"], z["a_tie"], z["b_tie"])
+    close(ga, z["tie_ga_" + op])
+    close(gb, z["tie_gb_" + op])
 
 
 def test_reduce_golden():
@@ -52,6 +79,17 @@ def test_reduce_golden():
     close(ops.reduce_backward("mean", z["up_mean_02"], z["x"].shape, [0, 2]), z["g_mean_02"])
     close(ops.reduce("max", z["x"], [2]), z["max_2"])
     assert np.array_equal(ops.argmax(z["x"], 1), z["argmax_1"])
+    close(ops.reduce("min", z["x"], [2]), z["min_2"], rtol=0, atol=0)
+    close(ops.reduce("min", z["x"], [0]), z["min_0"], rtol=0, atol=0)
+    close(ops.reduce("prod", z["x"], [1]), z["prod_1"])
+    close(ops.reduce("prod", z["x"][:2, :3]), z["prod_all"])
+    assert np.array_equal(ops.argmax(z["x"], 1, is_min=True), z["argmin_1"])
+    assert ops.argmax(z["x"], None, is_min=True) == z["argmin_all"]
+    # ties: the first extreme index (Tensor.ts:2568 keeps the first)
+    xt = z["x_tie"]
+    assert np.array_equal(ops.argmax(xt, 1), z["tie_argmax_1"])
+    assert np.array_equal(ops.argmax(xt, 1, is_min=True), z["tie_argmin_1"])
+    assert np.array_equal(ops.argmax(xt, 0, is_min=True), z["tie_argmin_0"])
 
 
 def test_softmax_losses_golden():
@@ -415,6 +453,64 @@ def test_rng_integer_streams():
     assert abs(n.mean()) < 0.05 and abs(n.std() - 1) < 0.05
 
 
+def _xs_inverse(y):
+    """Inverse of xorshift32 (13, 17, 5): each step x ^= x << k (or >> k)
+    is undone by repeating it until the shifted-in bits settle."""
+    def unshift(y, k, left):
+        x = y
+        for _ in range(32 // k + 1):
+            x = (y ^ ((x << k) & 0xFFFFFFFF)) if left else (y ^ (x >> k))
+        return x
+    return unshift(unshift(unshift(y, 5, True), 17, False), 13, True)
+
+
+def _seed_for_states(s2):
+    """The call seed whose element 0 has second state s2 (and first state
+    s1 = xorshift32^-1(s2)): element 0 starts from seed ^ 1013904223."""
+    s1 = _xs_inverse(s2)
+    return _xs_inverse(s1) ^ 1013904223, s1
+
+
+def test_xorshift_inverse():
+    for y in (1, 2 ** 30, 2 ** 31, 0xDEADBEEF, 723471715):
+        assert int(rng.xorshift32(_xs_inverse(y))) == y
+    assert _xs_inverse(723471715) == 2463534242  # Marsaglia's known pair
+
+
+def test_randn_box_muller_special_states():
+    """random.wgsl:31-46 at states whose result the mathematics fixes,
+    computed with math.log / math.cos on the float32 inputs:
+    - u2 = 1/2 (s2 = 2^31): the angle is float32(2 pi) / 2 = pi + 8.7e-8, cos
+      = -1 to double precision, so the output is -sqrt(-2 ln u1);
+    - u2 = 1/4 (s2 = 2^30): cos of float32(2 pi) / 4 is -4.37e-8, so the
+      output is ~0 (a sine in place of the cosine would give sqrt(-2 ln u1),
+      and u1, u2 swapped would give neither);
+    - u1 below 1e-7 (s1 < 430): u1 is clamped to float32(1e-7), so the
+      radius is sqrt(-2 ln float32(1e-7)) = 5.677, whatever u1 is."""
+    for s2, cos_want in ((2 ** 31, -1.0), (2 ** 30, math.cos(float(np.float32(2 * math.pi)) / 4))):
+        seed, s1 = _seed_for_states(s2)
+        u1 = float(np.float32(s1 / 2 ** 32))
+        r = math.sqrt(-2.0 * math.log(u1))
+        want = r * cos_want
+        assert abs(float(rng.randn(1, seed)[0]) - want) <= 1e-7 * r
+        if s2 == 2 ** 30:
+            assert abs(want) < 1e-7 and r > 1.0  # a sine would give r
+    r_clamp = math.sqrt(-2.0 * math.log(float(np.float32(1e-7))))
+    assert abs(r_clamp - 5.6777) < 1e-4
+    # among the states with u1 < 1e-7, the one whose u2 puts the angle
+    # nearest a multiple of pi: the output is then +-r_clamp
+    best = max(range(1, 430), key=lambda s1: abs(math.cos(
+        float(np.float32(np.float32(2 * math.pi) * np.float32(int(rng.xorshift32(s1)) / 2 ** 32))))))
+    seed = _xs_inverse(best) ^ 1013904223
+    u2 = float(np.float32(int(rng.xorshift32(best)) / 2 ** 32))
+    theta = float(np.float32(np.float32(2 * math.pi) * np.float32(u2)))
+    got = float(rng.randn(1, seed)[0])
+    assert abs(abs(math.cos(theta)) - 1.0) < 1e-3
+    assert abs(got - r_clamp * math.cos(theta)) <= 1e-6
+    # without the clamp the radius would be sqrt(-2 ln(best / 2^32)) > 6.3
+    assert math.sqrt(-2.0 * math.log(best / 2 ** 32)) > 6.3
+
+
 # ------------------------------------------------------------------ sampling
 
 
@@ -452,6 +548,23 @@ def test_multinomial_closed_forms():
     p = ops.softmax(np.random.default_rng(1).standard_normal(100))
     t = int(ops.multinomial(p, 1, False, np.array([0.42]))[0])
     assert 0 <= t < 100
+
+
+def test_multinomial_nan_and_inf_contract():
+    """NaN or +inf in a row raises (PyTorch's torch.multinomial raises on
+    both); -inf and negatives weigh 0 like Math.max(0, x) makes them."""
+    u = np.array([[0.5, 0.5]])
+    for bad in (np.nan, np.inf):
+        with pytest.raises(ValueError, match="row 0"):
+            ops.multinomial(np.array([1.0, bad, 1.0]), 2, True, u)
+        with pytest.raises(ValueError):
+            ops.multinomial(np.array([1.0, bad, 1.0]), 2, False, u)
+        import torch
+        with pytest.raises(RuntimeError):
+            torch.multinomial(torch.tensor([1.0, bad, 1.0]), 2, True)
+    # -inf weighs 0: only indices 0 and 2 can be drawn, 2 for u >= 0.5
+    got = ops.multinomial(np.array([1.0, -np.inf, 1.0]), 2, True, np.array([0.25, 0.75]))
+    assert got.tolist() == [0, 2]
 
 
 def test_multinomial_distribution():

@@ -92,3 +92,53 @@ def test_host_round_trip_keeps_bytes(S):
         assert back[k].array.tobytes() == obj[k].array.tobytes()
     assert back["w"].requires_grad and not back["i"].requires_grad
     assert back["meta"] == {"epoch": 3, "lr": 1e-3, "names": ["a", "b"]}
+
+
+def _crafted_pt(storage_floats, offset, size, stride):
+    """A .pt archive whose data.pkl rebuilds one float32 tensor from a
+    storage of `storage_floats` elements with the given offset, size and
+    stride (written with the real torch._utils._rebuild_tensor_v2 global, so
+    the file is what a tampered torch.save output would hold)."""
+    import torch
+
+    class _Stor:
+        pass
+    st = _Stor()
+
+    class _P(pickle.Pickler):
+        def persistent_id(self, obj):
+            if obj is st:
+                return ("storage", torch.FloatStorage, "0", "cpu", storage_floats)
+            return None
+
+    class _T:
+        def __reduce__(self):
+            return (torch._utils._rebuild_tensor_v2, (st, offset, size, stride, False, None))
+    buf = io.BytesIO()
+    _P(buf, protocol=2).dump({"t": _T()})
+    out = io.BytesIO()
+    with zipfile.ZipFile(out, "w") as z:
+        z.writestr("archive/data.pkl", buf.getvalue())
+        z.writestr("archive/data/0", np.arange(storage_floats, dtype="<f4").tobytes())
+    return out.getvalue()
+
+
+def test_pt_loader_bounds_checks_views(S):
+    """Views that reach outside their storage are refused: negative strides
+    (which would read before the storage's start), negative sizes, offsets
+    outside it and views past its end.  Well-formed views still load."""
+    ok = S.read_archive(_crafted_pt(12, 2, (2, 3), (4, 1)))["t"]
+    assert ok.array.tolist() == [[2, 3, 4], [6, 7, 8]]
+    ok = S.read_archive(_crafted_pt(4, 3, (1,), (1,)))["t"]
+    assert ok.array.tolist() == [3]
+    empty = S.read_archive(_crafted_pt(4, 4, (0,), (1,)))["t"]
+    assert empty.array.shape == (0,)
+    for off, size, stride in [(0, (3,), (-1,)), (3, (3,), (-1,)), (2, (2, 2), (1, -2)),
+                              (-1, (2,), (1,)), (0, (-2,), (1,)), (5, (1,), (1,)),
+                              (0, (5,), (1,)), (2, (2, 2), (2, 1)), (4, (1,), (1,))]:
+        with pytest.raises(ValueError):
+            S.read_archive(_crafted_pt(4, off, size, stride))
+    # the advisor's repro, called directly: storage of 4 floats, (3,), (-1,)
+    stor = S._Storage(np.arange(4, dtype="<f4").tobytes(), "float32", False)
+    with pytest.raises(ValueError):
+        S._rebuild_tensor_v2(stor, 0, (3,), (-1,))

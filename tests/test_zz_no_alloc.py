@@ -60,7 +60,7 @@ def test_noalloc_equals_allocating_entry(torch, with_res, acc):
         assert _call(L, "noalloc", ins, got, rows, cols, acc) == 0, L.lib().tjh_last_error()
         torch.synchronize()
         s1 = torch.hip.memory_stats()
-        assert s1["allocations"] == s0["allocations"]       # no tjh_malloc
+        assert s1["allocation_requests"] == s0["allocation_requests"]  # no tjh_malloc
         assert s1["device_mallocs"] == s0["device_mallocs"]  # no hipMalloc
         for a, b in zip(ref, got):
             assert np.array_equal(a.numpy(), b.numpy())

@@ -35,7 +35,7 @@ __all__ = [
     "manual_seed", "matmul", "multinomial", "nn", "no_grad", "ones", "ones_like", "optim",
     "profiler", "rand",
     "randn", "save", "set_grad_enabled", "split", "stack", "synchronize", "tensor", "tril",
-    "triu",
+    "triu", "webgpu",
     "zeros", "zeros_like",
 ]
 
@@ -53,11 +53,33 @@ class hip:
 
     @staticmethod
     def memory_stats():
+        """torch.webgpu.memory_stats() (src/webgpu.ts:11-19) with its keys:
+        active_bytes, pooled_bytes, peak_bytes and total_allocations, the
+        number of blocks the allocator created because its cache had none
+        to hand out (the reference's totalAllocations grows only when the
+        pool creates a buffer, src/backend/webgpu/buffer.ts:50-57).  Two
+        keys of this allocator's own: device_mallocs (the same count, under
+        the name the library uses) and allocation_requests (every request
+        served, cached or not)."""
         s = _lib.MemStats()
         _lib.check(_lib.lib().tjh_memory_stats(ctypes.byref(s)), "memory_stats")
         return {"active_bytes": s.active_bytes, "pooled_bytes": s.pooled_bytes,
-                "peak_bytes": s.peak_bytes, "allocations": s.allocations,
-                "device_mallocs": s.device_mallocs}
+                "peak_bytes": s.peak_bytes, "total_allocations": s.device_mallocs,
+                "device_mallocs": s.device_mallocs, "allocation_requests": s.allocations}
+
+    @staticmethod
+    def memory_summary():
+        """torch.webgpu.memory_summary() (src/webgpu.ts:24-37): the same four
+        lines, sizes in MB with two decimals."""
+        st = hip.memory_stats()
+
+        def mb(b):
+            return "%.2f" % (b / 1024 / 1024)
+        rule = "-" * 55
+        return ("\nGPU Memory Summary\n%s\nActive Memory:   %s MB\nPooled Memory:   %s MB\n"
+                "Peak Memory:     %s MB\nTotal Allocs:    %d\n%s\n"
+                % (rule, mb(st["active_bytes"]), mb(st["pooled_bytes"]), mb(st["peak_bytes"]),
+                   st["total_allocations"], rule))
 
     @staticmethod
     def empty_cache():
@@ -99,3 +121,8 @@ class hip:
         buf = ctypes.create_string_buffer(65536)
         _lib.check(_lib.lib().tjh_kprof_names(buf, len(buf)), "kprof_names")
         return [s for s in buf.value.decode().split("\n") if s]
+
+
+# torch.webgpu.* (src/core.ts:24): the memory functions under the name
+# torch.js exports them as
+webgpu = hip

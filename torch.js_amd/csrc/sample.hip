@@ -2,15 +2,27 @@
 // (src/tensor/Tensor.ts:271-359), which torch.js evaluates on the host
 // after a readback, with Math.random.
 //
-// Semantics kept from the reference (Tensor.ts:327-359): the weights of a
-// row are p_i = max(0, x_i) (NaN counts as 0), normalised by their sum; a
-// row whose sum is not positive samples uniformly.  With replacement, a
-// draw u in [0, 1) picks the first index whose running sum of p / sum
-// exceeds u (the last index when rounding leaves u above the total).
-// Without replacement each draw renormalises over the indices not taken
-// yet (the distribution of the reference's redraw-until-new loop): the
-// first untaken index whose running sum of p exceeds u times the untaken
-// mass.
+// Semantics kept from the reference (Tensor.ts:308-359): the weights of a
+// row are p_i = max(0, x_i) (negative weights and -inf weigh 0),
+// normalised by their sum; a row whose sum is not positive samples
+// uniformly.  With replacement, a draw u in [0, 1) picks the first index
+// whose running sum of p / sum exceeds u (the last index when rounding
+// leaves u above the total).  Without replacement each draw renormalises
+// over the indices not taken yet (the distribution of the reference's
+// redraw-until-new loop): the first untaken index whose running sum of p
+// exceeds u times the untaken mass.
+//
+// Where the reference is undefined this file states its own contract:
+// - a row holding NaN or +inf is an error (PyTorch raises; the reference's
+//   Math.max(0, NaN) is NaN, so its cumulative probabilities are NaN and it
+//   returns the last index with replacement or loops forever without).
+//   The kernel writes -1 for every draw of such a row and a status word
+//   per row, which tjh_multinomial reads back (the call synchronises) to
+//   return TJH_ERR_INVALID;
+// - without replacement, once every positive-weight category is taken,
+//   each further draw takes the last untaken index (the reference falls
+//   back to index 0 and redraws until it finds a new one, which never
+//   ends when 0 is taken; PyTorch raises).
 //
 // The uniforms are the library's seeded stream, not Math.random: draw s of
 // row r uses element e = r * num_samples + s of tjh_random's uniform
@@ -21,6 +33,8 @@
 // One workgroup per row; thread t owns a contiguous segment of the row, so
 // a running sum is a per-segment sequential sum plus the exclusive scan of
 // the segment totals (double precision throughout).
+
+#include <vector>
 
 #include "common.h"
 
@@ -77,7 +91,8 @@ template <bool REPL>
 __global__ __launch_bounds__(kThreads) void k_multinomial(const float* __restrict__ probs,
                                                           int64_t cols, int64_t ns,
                                                           uint32_t seed,
-                                                          int32_t* __restrict__ out) {
+                                                          int32_t* __restrict__ out,
+                                                          int32_t* __restrict__ status) {
   __shared__ double sm[kThreads / 64];
   __shared__ int32_t pick;
   __shared__ uint32_t taken[REPL ? 1 : kTakenBits / 32];
@@ -89,10 +104,21 @@ __global__ __launch_bounds__(kThreads) void k_multinomial(const float* __restric
   const int64_t hi = lo + seg < cols ? lo + seg : cols;
   auto weight = [&](int64_t i) -> double {
     const float v = x[i];
-    return v > 0.f ? (double)v : 0.0;  // NaN and negatives weigh 0
+    return v > 0.f ? (double)v : 0.0;  // negatives and -inf weigh 0
   };
   double local = 0.0;
-  for (int64_t i = lo; i < hi; ++i) local += weight(i);
+  int bad = 0;
+  for (int64_t i = lo; i < hi; ++i) {
+    const float v = x[i];
+    bad |= (v != v) | (v == __builtin_huge_valf());
+    local += v > 0.f ? (double)v : 0.0;
+  }
+  if (__syncthreads_or(bad)) {  // the same value in every thread of the row
+    for (int64_t s = t; s < ns; s += kThreads) out[r * ns + s] = -1;
+    if (t == 0) status[r] = 1;
+    return;
+  }
+  if (t == 0) status[r] = 0;
   const double total = block_sum_d(local, sm);
   const bool uniform = !(total > 0.0);
   auto w_of = [&](int64_t i) -> double { return uniform ? 1.0 : weight(i); };
@@ -180,14 +206,32 @@ int tjh_multinomial(const float* probs, int64_t rows, int64_t cols, int64_t num_
   TJH_ARG(rows < (int64_t(1) << 31), "tjh_multinomial: too many rows");
   if (rows == 0 || num_samples == 0) return TJH_OK;
   TJH_ARG(probs && out, "tjh_multinomial: NULL pointer");
-  KernelScope ks("multinomial");
-  if (replacement)
-    tjh_launch(k_multinomial<true>, dim3((unsigned)rows), dim3(kThreads), 0, stream(), probs,
-               cols, num_samples, seed, out);
-  else
-    tjh_launch(k_multinomial<false>, dim3((unsigned)rows), dim3(kThreads), 0, stream(), probs,
-               cols, num_samples, seed, out);
-  return check_launch("multinomial");
+  if (capturing())  // the per-row status is read back to the host
+    return set_error(TJH_ERR_UNSUPPORTED,
+                     "tjh_multinomial: not allowed while a graph is being captured");
+  Scratch st((size_t)rows * sizeof(int32_t));
+  if (!st.ok()) return set_error(TJH_ERR_OOM, "tjh_multinomial: no scratch");
+  {
+    KernelScope ks("multinomial");
+    if (replacement)
+      tjh_launch(k_multinomial<true>, dim3((unsigned)rows), dim3(kThreads), 0, stream(), probs,
+                 cols, num_samples, seed, out, st.as<int32_t>());
+    else
+      tjh_launch(k_multinomial<false>, dim3((unsigned)rows), dim3(kThreads), 0, stream(), probs,
+                 cols, num_samples, seed, out, st.as<int32_t>());
+    const int rc = check_launch("multinomial");
+    if (rc != TJH_OK) return rc;
+  }
+  std::vector<int32_t> hs((size_t)rows);
+  hipError_t e = hipMemcpyAsync(hs.data(), st.p, (size_t)rows * sizeof(int32_t),
+                                hipMemcpyDeviceToHost, stream());
+  if (e == hipSuccess) e = hipStreamSynchronize(stream());
+  if (e != hipSuccess) return hip_fail(e, "multinomial status readback");
+  for (int64_t r = 0; r < rows; ++r)
+    if (hs[(size_t)r])
+      return set_error(TJH_ERR_INVALID,
+                       "tjh_multinomial: probability row %lld contains NaN or inf", (long long)r);
+  return TJH_OK;
 }
 
 }  // extern "C"

@@ -345,7 +345,12 @@ static napi_value js_memory_stats(napi_env env, napi_callback_info info) {
   napi_set_named_property(env, o, "activeBytes", num(env, (double)s.active_bytes));
   napi_set_named_property(env, o, "pooledBytes", num(env, (double)s.pooled_bytes));
   napi_set_named_property(env, o, "peakBytes", num(env, (double)s.peak_bytes));
-  napi_set_named_property(env, o, "allocations", num(env, (double)s.allocations));
+  /* bufferPool.getStats() (src/backend/webgpu/buffer.ts:10-15, 98-105):
+   * allocationCount counts the blocks created on a cache miss, as the
+   * reference's totalAllocations does; allocationRequests (every request
+   * served) is this allocator's own */
+  napi_set_named_property(env, o, "allocationCount", num(env, (double)s.device_mallocs));
+  napi_set_named_property(env, o, "allocationRequests", num(env, (double)s.allocations));
   return o;
 }
 

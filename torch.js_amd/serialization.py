@@ -118,14 +118,32 @@ class _Storage:
 def _rebuild_tensor_v2(storage, storage_offset, size, stride, requires_grad=False,
                        backward_hooks=None, metadata=None):
     v = storage.values
-    size = tuple(int(s) for s in size)
-    stride = tuple(int(s) for s in stride)
+    if not isinstance(storage_offset, int) or isinstance(storage_offset, bool):
+        raise ValueError("tensor storage offset must be an int")
+    if not isinstance(size, (tuple, list)) or not isinstance(stride, (tuple, list)):
+        raise ValueError("tensor size and stride must be sequences")
+    if len(size) != len(stride):
+        raise ValueError("tensor size and stride differ in length")
+    for d in tuple(size) + tuple(stride):
+        if not isinstance(d, int) or isinstance(d, bool):
+            raise ValueError("tensor size and stride entries must be ints")
+    size = tuple(size)
+    stride = tuple(stride)
+    # PyTorch writes no negative sizes or strides; a file that has them is
+    # malformed (a negative stride would make the view reach before the
+    # start of its storage)
+    if any(s < 0 for s in size) or any(st < 0 for st in stride):
+        raise ValueError("tensor sizes and strides must be non-negative")
+    if storage_offset < 0 or storage_offset > v.size:
+        raise ValueError("tensor storage offset outside its storage")
     n = int(np.prod(size)) if size else 1
     if n:
-        last = int(storage_offset) + sum((s - 1) * st for s, st in zip(size, stride) if s > 0)
-        if storage_offset < 0 or last >= v.size:
+        # with every stride >= 0 the lowest element reached is the offset
+        # and the highest is offset + sum((size - 1) * stride)
+        last = storage_offset + sum((s - 1) * st for s, st in zip(size, stride))
+        if storage_offset >= v.size or last >= v.size:
             raise ValueError("tensor view past the end of its storage")
-        view = np.lib.stride_tricks.as_strided(v[int(storage_offset):], shape=size,
+        view = np.lib.stride_tricks.as_strided(v[storage_offset:], shape=size,
                                                strides=[st * v.itemsize for st in stride])
     else:
         view = np.zeros(size, dtype=v.dtype)

@@ -1259,11 +1259,15 @@ def _before_write(*ts):
         return
     keys = set()
     for t in ts:
-        if t is None:
-            continue
-        keys.add(id(t))
-        if t._st is not None:
-            keys.add(id(t._st))
+        # t, and the values it aliases (a detach() or view of a deferred
+        # value writes into that value's memory once it is computed)
+        while t is not None:
+            keys.add(id(t))
+            if t._st is not None:
+                keys.add(id(t._st))
+                break
+            lz = t._lz
+            t = lz.args[0] if lz is not None and lz.kind == "alias" else None
     for p in _pending_tensors():
         lz = p._lz
         if p._st is None and lz is not None and not keys.isdisjoint(lz.deps):
@@ -1859,7 +1863,9 @@ def multinomial(x, num_samples=1, replacement=False):
     [num_samples] for a 1-D input, [rows, num_samples] for a 2-D one.
     Weights are max(0, x) normalised by their sum (uniform when it is not
     positive); the draws come from the seeded stream (one LCG step of the
-    manual_seed state per call, like rand), not Math.random."""
+    manual_seed state per call, like rand), not Math.random.  A row holding
+    NaN or +inf raises RuntimeError (PyTorch's contract; the reference's
+    result is undefined there).  The call synchronises with the device."""
     if x.ndim not in (1, 2):
         raise RuntimeError("multinomial: expected a 1-D or 2-D tensor of probabilities")
     cols = x.shape[-1]
@@ -2773,7 +2779,7 @@ def run_backward(pairs, retain_graph=False, inputs=None):
         roots = []
         wanted = {id(t): t for t in inputs} if inputs is not None else None
         results = {}
-        owned = set()  # storages already handed to a leaf in this pass
+        owned = _Owned()  # gradient memory already handed to a leaf in this pass
         for t, g in pairs:
             if g.shape != t.shape:
                 if g.numel() == t.numel():
@@ -2816,7 +2822,7 @@ def run_backward(pairs, retain_graph=False, inputs=None):
                 if defer and slot in node.defer_slots:
                     # a leaf's first gradient, finished by the next flush
                     t._grad = gi
-                    owned.add(_skey(gi))
+                    owned.add(gi)
                     deferred.add(id(t))
                     continue
                 if acc is not None and slot == node.acc_slot:
@@ -2883,6 +2889,42 @@ def _can_defer(node, wanted):
     return bool(seen)
 
 
+class _Owned:
+    """Gradient memory a backward pass has handed to one holder (a leaf's
+    .grad, or a gradient folded into a VJP's output).  Memory is recorded
+    by storage identity.  A deferred gradient, which has no storage yet, is
+    recorded by its own identity and held for the pass (so that identity is
+    never reused by another object); once it is computed its storage counts
+    as recorded too, so a gradient handed to two leaves is seen as owned
+    under either key, before and after it is computed."""
+
+    __slots__ = ("keys", "held", "waiting")
+
+    def __init__(self):
+        self.keys = set()
+        self.held = []     # every tensor recorded while deferred
+        self.waiting = []  # those whose storage is not recorded yet
+
+    def add(self, t):
+        k = _skey(t)
+        self.keys.add(k)
+        if not isinstance(k, int):
+            self.held.append(t)
+            self.waiting.append(t)
+
+    def has(self, t):
+        if self.waiting:
+            still = []
+            for h in self.waiting:
+                k = _skey(h)
+                if isinstance(k, int):
+                    self.keys.add(k)
+                else:
+                    still.append(h)
+            self.waiting = still
+        return _skey(t) in self.keys
+
+
 def _flush_deferred(deferred):
     L.check(L.lib().tjh_flush_deferred(), "flush_deferred")
     deferred.clear()
@@ -2904,7 +2946,7 @@ def _pending_for(node, grads, wanted, owned):
         return None
     if t.grad_fn is None:
         prev = t._grad
-        if prev is None or _skey(prev) not in owned:
+        if prev is None or not owned.has(prev):
             return None
         others = [p for p in grads.values()]
     else:
@@ -2916,7 +2958,7 @@ def _pending_for(node, grads, wanted, owned):
         # a pending gradient may be the very tensor an add / sub / scalar-add
         # VJP also handed to another input, a leaf's .grad among them: the
         # VJP may add into it in place only if nothing else holds it
-        if _skey(prev) in owned:
+        if owned.has(prev):
             return None
         others = [p for key, p in grads.items() if key != id(t.grad_fn)]
     if (prev is None or isinstance(prev, _SliceGrad) or prev.shape != t.shape or
@@ -2945,19 +2987,19 @@ def _leaf_accumulate(t, g, owned, force_copy=False):
     inputs of an add), so later in-place edits of one .grad stay local."""
     lazy = _is_lazy(g) and g._lz.kind != "alias"
     if (lazy and not force_copy and t._grad is None and _FUSE_SIB and _LAZY["jit"] and
-            _skey(g) not in owned):
+            not owned.has(g)):
         # a deferred gradient stays deferred until a column sum over a
         # sibling takes it along, or the pass ends; no other leaf holds it
-        owned.add(_skey(g))
+        owned.add(g)
         t._grad = g
         _SIBLINGS.append(g)
         return
-    if lazy and not force_copy and _skey(g) not in owned:
+    if lazy and not force_copy and not owned.has(g):
         g._storage  # a deferred gradient evaluates into memory nothing else holds
-    elif force_copy or not g.is_contiguous() or _skey(g) in owned:
+    elif force_copy or not g.is_contiguous() or owned.has(g):
         g = _k_contiguous(g)
     if t._grad is None:
-        owned.add(_skey(g))
+        owned.add(g)
         t._grad = Tensor(g._storage, g._shape, g._strides, g._offset, g._dtype)
     else:
         t._grad = _k_binary("add", t._grad, g)
