@@ -206,3 +206,99 @@ def adamw_step(p, grads, lr, wd, step, betas=(0.9, 0.999), eps=1e-8, state=None)
         out[k], _, _ = ops.adam_step(v, np.asarray(grads[k], dtype=np.float32), m, s, step, lr,
                                      betas, eps, wd, decoupled=True)
     return out
+
+
+# ------------------------------------------------------------------ MultiheadAttention
+
+
+def mha_mask(N, H, L, S, attn_mask=None, key_padding_mask=None):
+    """The additive float mask [N, H, L, S] (or None) that nn.MultiheadAttention
+    applies, with PyTorch's meanings (the reference throws on both masks,
+    src/nn/attention.ts:121-126): a bool mask is True where attention is
+    NOT allowed (-inf), a float mask is added; attn_mask is [L, S] or
+    [N * H, L, S], key_padding_mask is [N, S]."""
+    m = np.zeros((N, H, L, S))
+    used = False
+    if attn_mask is not None:
+        a = np.asarray(attn_mask)
+        a = np.where(a, -np.inf, 0.0) if a.dtype == bool else a.astype(F64)
+        m = m + (a.reshape(1, 1, L, S) if a.ndim == 2 else a.reshape(N, H, L, S))
+        used = True
+    if key_padding_mask is not None:
+        k = np.asarray(key_padding_mask)
+        k = np.where(k, -np.inf, 0.0) if k.dtype == bool else k.astype(F64)
+        m = m + k.reshape(N, 1, 1, S)
+        used = True
+    return m if used else None
+
+
+def _mha_inputs(query, key, value, batch_first):
+    """(N, L, E) views of the three inputs."""
+    if batch_first:
+        return [np.asarray(t, dtype=F64) for t in (query, key, value)]
+    return [np.swapaxes(np.asarray(t, dtype=F64), 0, 1) for t in (query, key, value)]
+
+
+def mha_forward(p, query, key, value, heads, batch_first=False, mask=None, causal=False):
+    """nn.MultiheadAttention.forward (src/nn/attention.ts:112-271): q, k, v
+    projected by the three row blocks of in_proj_weight [3E, E] (+ the
+    blocks of in_proj_bias), split into heads, softmax(q k^T / sqrt(hd)
+    [+ mask]) v, heads merged, out_proj_weight / out_proj_bias; inputs and
+    output [L, N, E], or [N, L, E] with batch_first.  Returns (out,
+    weights [N, H, L, S], cache for mha_backward)."""
+    q_in, k_in, v_in = _mha_inputs(query, key, value, batch_first)
+    N, L, E = q_in.shape
+    S = k_in.shape[1]
+    hd = E // heads
+    W = np.asarray(p["in_proj_weight"], dtype=F64)
+    b = p.get("in_proj_bias")
+    b = np.zeros(3 * E) if b is None else np.asarray(b, dtype=F64)
+    proj = [x @ W[i * E:(i + 1) * E].T + b[i * E:(i + 1) * E] for i, x in
+            enumerate((q_in, k_in, v_in))]
+    qh, kh, vh = [t.reshape(t.shape[0], t.shape[1], heads, hd).transpose(0, 2, 1, 3)
+                  for t in proj]
+    o, _ = ops.sdpa(qh, kh, vh, causal=causal, mask=mask)
+    wts = ops.sdpa_weights(qh, kh, causal=causal, mask=mask)
+    y = o.transpose(0, 2, 1, 3).reshape(N, L, E)
+    Wo = np.asarray(p["out_proj_weight"], dtype=F64)
+    bo = p.get("out_proj_bias")
+    out = y @ Wo.T + (0.0 if bo is None else np.asarray(bo, dtype=F64))
+    if not batch_first:
+        out = np.swapaxes(out, 0, 1)
+    cache = dict(q_in=q_in, k_in=k_in, v_in=v_in, qh=qh, kh=kh, vh=vh, y=y, heads=heads,
+                 batch_first=batch_first, mask=mask, causal=causal)
+    return out, wts, cache
+
+
+def mha_backward(p, dout, cache):
+    """Gradients of mha_forward's output: a dict with in_proj_weight,
+    in_proj_bias, out_proj_weight, out_proj_bias and query, key, value (each
+    input's own gradient; a caller passing one tensor as several inputs
+    adds them)."""
+    dout = np.asarray(dout, dtype=F64)
+    if not cache["batch_first"]:
+        dout = np.swapaxes(dout, 0, 1)
+    N, L, E = dout.shape
+    heads = cache["heads"]
+    hd = E // heads
+    Wo = np.asarray(p["out_proj_weight"], dtype=F64)
+    W = np.asarray(p["in_proj_weight"], dtype=F64)
+    g = {}
+    d2 = dout.reshape(-1, E)
+    g["out_proj_weight"] = d2.T @ cache["y"].reshape(-1, E)
+    g["out_proj_bias"] = d2.sum(axis=0)
+    dy = (dout @ Wo).reshape(N, L, heads, hd).transpose(0, 2, 1, 3)
+    dqh, dkh, dvh = ops.sdpa_backward(dy, cache["qh"], cache["kh"], cache["vh"],
+                                      causal=cache["causal"], mask=cache["mask"])
+    dW = np.zeros_like(W)
+    db = np.zeros(3 * E)
+    for i, (dh, x, name) in enumerate(((dqh, cache["q_in"], "query"), (dkh, cache["k_in"], "key"),
+                                       (dvh, cache["v_in"], "value"))):
+        dp = dh.transpose(0, 2, 1, 3).reshape(x.shape[0], x.shape[1], E)
+        dW[i * E:(i + 1) * E] = dp.reshape(-1, E).T @ x.reshape(-1, E)
+        db[i * E:(i + 1) * E] = dp.reshape(-1, E).sum(axis=0)
+        dx = dp @ W[i * E:(i + 1) * E]
+        g[name] = dx if cache["batch_first"] else np.swapaxes(dx, 0, 1)
+    g["in_proj_weight"] = dW
+    g["in_proj_bias"] = db
+    return g

@@ -301,7 +301,9 @@ def cross_entropy(x, t, reduction="mean", ignore_index=-100, weight=None, label_
     wt = w[ts]
     lp = log_softmax(x)
     eps = float(label_smoothing)
-    rows = (1.0 - eps) * wt * -lp[np.arange(len(t)), ts] + (eps / C) * (-(lp * w)).sum(axis=1)
+    rows = (1.0 - eps) * wt * -lp[np.arange(len(t)), ts]
+    if eps != 0.0:  # (without smoothing a -inf logit's term is absent, not 0 * inf)
+        rows = rows + (eps / C) * (-(lp * w)).sum(axis=1)
     rows = np.where(ok, rows, 0.0)
     return _reduce_rows(rows, reduction, ok, wt)
 
@@ -503,19 +505,26 @@ def matmul_backward(g, a, b):
 # ------------------------------------------------------------------ attention
 
 
-def sdpa(q, k, v, causal=False, scale=None):
-    """softmax(Q K^T scale [+ causal mask]) V (src/nn/functional.ts:866-890
-    with torch's is_causal: key j > query i is masked).  Returns (o, lse)."""
-    q = np.asarray(q, dtype=F64)
-    k = np.asarray(k, dtype=F64)
-    v = np.asarray(v, dtype=F64)
+def _scores(q, k, causal, scale, mask):
     D = q.shape[-1]
     sc = 1.0 / math.sqrt(D) if scale is None else scale
     s = (q @ np.swapaxes(k, -1, -2)) * sc
     if causal:
         Tq, Tk = s.shape[-2], s.shape[-1]
-        mask = np.triu(np.ones((Tq, Tk), dtype=bool), 1)
-        s = np.where(mask, -np.inf, s)
+        s = np.where(np.triu(np.ones((Tq, Tk), dtype=bool), 1), -np.inf, s)
+    if mask is not None:
+        s = s + np.asarray(mask, dtype=F64)  # additive, broadcast; -inf masks out
+    return s, sc
+
+
+def sdpa(q, k, v, causal=False, scale=None, mask=None):
+    """softmax(Q K^T scale [+ causal mask] [+ mask]) V
+    (src/nn/functional.ts:866-890 with torch's is_causal: key j > query i
+    is masked; `mask` is an additive float mask).  Returns (o, lse)."""
+    q = np.asarray(q, dtype=F64)
+    k = np.asarray(k, dtype=F64)
+    v = np.asarray(v, dtype=F64)
+    s, _ = _scores(q, k, causal, scale, mask)
     m = s.max(axis=-1, keepdims=True)
     e = np.exp(s - m)
     ssum = e.sum(axis=-1, keepdims=True)
@@ -523,18 +532,20 @@ def sdpa(q, k, v, causal=False, scale=None):
     return p @ v, (m + np.log(ssum))[..., 0]
 
 
-def sdpa_backward(g, q, k, v, causal=False, scale=None):
+def sdpa_weights(q, k, causal=False, scale=None, mask=None):
+    """The attention weights softmax(Q K^T scale [+ masks]) of sdpa."""
+    s, _ = _scores(np.asarray(q, dtype=F64), np.asarray(k, dtype=F64), causal, scale, mask)
+    p = np.exp(s - s.max(axis=-1, keepdims=True))
+    return p / p.sum(axis=-1, keepdims=True)
+
+
+def sdpa_backward(g, q, k, v, causal=False, scale=None, mask=None):
     """(dq, dk, dv) of sdpa."""
     g = np.asarray(g, dtype=F64)
     q = np.asarray(q, dtype=F64)
     k = np.asarray(k, dtype=F64)
     v = np.asarray(v, dtype=F64)
-    D = q.shape[-1]
-    sc = 1.0 / math.sqrt(D) if scale is None else scale
-    s = (q @ np.swapaxes(k, -1, -2)) * sc
-    if causal:
-        Tq, Tk = s.shape[-2], s.shape[-1]
-        s = np.where(np.triu(np.ones((Tq, Tk), dtype=bool), 1), -np.inf, s)
+    s, sc = _scores(q, k, causal, scale, mask)
     p = np.exp(s - s.max(axis=-1, keepdims=True))
     p /= p.sum(axis=-1, keepdims=True)
     dv = np.swapaxes(p, -1, -2) @ g

@@ -377,6 +377,84 @@ def serialization_fixtures():
         f.write(zb.getvalue())
 
 
+def multihead_attention(rng):
+    """nn.MultiheadAttention in float64: self- and cross-attention, both
+    layouts, bool / float / key-padding masks, the causal hint, weights
+    averaged over heads and per head.  Parameters are stored under the
+    reference's names (in_proj_weight, in_proj_bias, out_proj_weight,
+    out_proj_bias; src/nn/attention.ts:38-95)."""
+    E, H, N, L, S = 16, 4, 2, 5, 7
+    d = {"E": E, "H": H}
+    cases = [
+        # name, batch_first, self, attn_mask kind, key_padding, causal, average
+        ("self_sf", False, True, None, False, False, True),
+        ("self_bf", True, True, None, False, False, False),
+        ("cross_sf", False, False, "bool", True, False, True),
+        ("cross_bf", True, False, "float3", True, False, False),
+        ("causal_bf", True, True, "causal", False, True, True),
+        ("kpm_sf", False, True, None, True, False, True),
+    ]
+    for name, bf, self_attn, mk, kpm, causal, avg in cases:
+        m = torch.nn.MultiheadAttention(E, H, bias=True, batch_first=bf, dtype=torch.float64)
+        Wi = rng.standard_normal((3 * E, E)) * 0.3
+        bi = rng.standard_normal(3 * E) * 0.1
+        Wo = rng.standard_normal((E, E)) * 0.3
+        bo = rng.standard_normal(E) * 0.1
+        with torch.no_grad():
+            m.in_proj_weight.copy_(t(Wi))
+            m.in_proj_bias.copy_(t(bi))
+            m.out_proj.weight.copy_(t(Wo))
+            m.out_proj.bias.copy_(t(bo))
+        Lk = L if self_attn else S
+        shp_q = (N, L, E) if bf else (L, N, E)
+        shp_k = (N, Lk, E) if bf else (Lk, N, E)
+        xq = rng.standard_normal(shp_q)
+        if self_attn:
+            q = t(xq, True)
+            k = v = q
+        else:
+            q = t(xq, True)
+            k = t(rng.standard_normal(shp_k), True)
+            v = t(rng.standard_normal(shp_k), True)
+        am = None
+        if mk == "bool":
+            am = rng.random((L, Lk)) < 0.3
+            am[:, 0] = False  # no query row fully masked
+        elif mk == "float3":
+            am = rng.standard_normal((N * H, L, Lk))
+        elif mk == "causal":
+            am = np.triu(np.ones((L, Lk), dtype=bool), 1)
+        kp = None
+        if kpm:
+            kp = np.zeros((N, Lk), dtype=bool)
+            kp[0, -2:] = True
+            kp[1, 1] = True
+        out, w = m(q, k, v, key_padding_mask=None if kp is None else torch.tensor(kp),
+                   need_weights=True,
+                   attn_mask=None if am is None else (torch.tensor(am) if am.dtype == bool
+                                                      else t(am)),
+                   average_attn_weights=avg, is_causal=causal)
+        g = rng.standard_normal(out.shape)
+        out.backward(t(g))
+        pre = name + ":"
+        d.update({pre + "bf": bf, pre + "self": self_attn, pre + "causal": causal,
+                  pre + "avg": avg, pre + "in_proj_weight": Wi, pre + "in_proj_bias": bi,
+                  pre + "out_proj_weight": Wo, pre + "out_proj_bias": bo, pre + "query": xq,
+                  pre + "g": g, pre + "out": out, pre + "weights": w,
+                  pre + "d_in_proj_weight": m.in_proj_weight.grad,
+                  pre + "d_in_proj_bias": m.in_proj_bias.grad,
+                  pre + "d_out_proj_weight": m.out_proj.weight.grad,
+                  pre + "d_out_proj_bias": m.out_proj.bias.grad, pre + "d_query": q.grad})
+        if not self_attn:
+            d.update({pre + "key": k, pre + "value": v, pre + "d_key": k.grad,
+                      pre + "d_value": v.grad})
+        if am is not None:
+            d[pre + "attn_mask"] = am
+        if kp is not None:
+            d[pre + "key_padding_mask"] = kp
+    save("mha", **d)
+
+
 def main():
     serialization_fixtures()
     losses_ext(np.random.default_rng(20261202))
@@ -392,6 +470,7 @@ def main():
     conv(rng)
     optim(rng)
     models(rng)
+    multihead_attention(np.random.default_rng(20261205))
     print("wrote", sorted(f for f in os.listdir(OUT) if f.endswith(".npz")))
 
 

@@ -336,6 +336,51 @@ def test_softmax(torch, shape, log):
     check(gx, want, **RED)
 
 
+@pytest.mark.parametrize("cols", [5, 37, 1000, 5000])
+@pytest.mark.parametrize("log", [False, True])
+def test_softmax_with_minus_inf_entries(torch, cols, log):
+    """Masked scores: -inf at the first, interior and last positions and in
+    every lane's first element of some rows (a lane whose running maximum
+    is still -inf must add exp(-inf) = 0, not exp(-inf - -inf) = NaN); rows
+    with one finite entry give 1 there.  Softmax and log-softmax, forward
+    and backward, on row offsets that are not 16-byte aligned."""
+    r = np.random.default_rng(cols + log)
+    x = f32(r.standard_normal((40, cols)) * 3)
+    x[0, 0] = x[1, 1] = x[2, -1] = -np.inf
+    x[3, ::2] = -np.inf
+    x[4, :-1] = -np.inf  # one finite entry
+    x[5, 1:] = -np.inf
+    x[6:, :] = np.where(r.random((34, cols)) < 0.4, -np.inf, x[6:])
+    x[6:, 0] = 1.0
+    fn = (lambda t: t.log_softmax(-1)) if log else (lambda t: t.softmax(-1))
+    out, g, (gx,) = grad_of(torch, fn, x)
+    y = ops.log_softmax(x) if log else ops.softmax(x)
+    assert np.isfinite(out).sum() == np.isfinite(y).sum()
+    assert np.array_equal(np.isneginf(out), np.isneginf(y))
+    fin = np.isfinite(y)
+    check(out[fin], y[fin], **RED)
+    if not log:
+        assert out[4, -1] == 1.0 and out[5, 0] == 1.0
+        want = ops.softmax_backward(g, y)
+        check(gx, want, **RED)
+    assert not np.isnan(out).any() and not np.isnan(gx).any()
+
+
+def test_cross_entropy_with_minus_inf_logits(torch):
+    """-inf logits of classes other than the target weigh nothing."""
+    r = np.random.default_rng(12)
+    x = f32(r.standard_normal((16, 37)))
+    x[:, 5:9] = -np.inf
+    t = r.integers(9, 37, 16).astype(np.int32)
+    xt = torch.tensor(x, requires_grad=True)
+    loss = torch.F.cross_entropy(xt, torch.tensor(t))
+    loss.backward()
+    check(loss.item(), ops.cross_entropy(x, t), **RED)
+    dx = xt.grad.numpy()
+    assert not np.isnan(dx).any() and (dx[:, 5:9] == 0).all()
+    check(dx, ops.cross_entropy_backward(x, t), **RED)
+
+
 def test_softmax_other_dim(torch):
     x = f32(np.random.default_rng(9).standard_normal((4, 6, 5)))
     out, g, (gx,) = grad_of(torch, lambda t: torch.F.softmax(t, 1), x)

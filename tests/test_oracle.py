@@ -345,6 +345,23 @@ def test_softmax_ce_closed_forms():
     assert np.allclose(ops.softmax(x).sum(axis=1), 1.0)
 
 
+def test_minus_inf_logits():
+    """A -inf logit is a class with probability 0 (PyTorch's softmax and
+    cross_entropy give exactly that, checked here): softmax 0, log-softmax
+    -inf, no NaN in the loss or its gradient."""
+    import torch as cpu
+    x = np.array([[1.0, -np.inf, 2.0, 0.5], [-np.inf, 3.0, -np.inf, -np.inf]])
+    t = np.array([2, 1])
+    xt = cpu.tensor(x, requires_grad=True)
+    lt = cpu.nn.functional.cross_entropy(xt, cpu.tensor(t))
+    lt.backward()
+    close(ops.softmax(x), cpu.softmax(cpu.tensor(x), -1).numpy())
+    assert np.array_equal(np.isneginf(ops.log_softmax(x)), np.isneginf(x))
+    close(ops.cross_entropy(x, t), lt.item())
+    close(ops.cross_entropy_backward(x, t), xt.grad.numpy())
+    assert ops.softmax(x)[1, 1] == 1.0
+
+
 def test_layer_norm_invariants():
     x = np.random.default_rng(2).standard_normal((4, 33)) * 5 + 3
     y, _, _ = ops.layer_norm(x)
@@ -576,3 +593,53 @@ def test_multinomial_distribution():
     exp = 20000 * w / w.sum()
     assert ((cnt - exp) ** 2 / exp).sum() < 35.0
 
+
+
+# ------------------------------------------------------------------ MultiheadAttention
+
+
+MHA_CASES = ["self_sf", "self_bf", "cross_sf", "cross_bf", "causal_bf", "kpm_sf"]
+
+
+@pytest.mark.parametrize("case", MHA_CASES)
+def test_mha_golden(case):
+    """oracle mha_forward / mha_backward against torch.nn.MultiheadAttention
+    in float64: output, weights (averaged over heads or per head), and the
+    gradient of every parameter and input."""
+    z = golden("mha")
+    pre = case + ":"
+    H = int(z["H"])
+    bf, self_attn = bool(z[pre + "bf"]), bool(z[pre + "self"])
+    p = {k: z[pre + k] for k in ("in_proj_weight", "in_proj_bias", "out_proj_weight",
+                                 "out_proj_bias")}
+    q = z[pre + "query"]
+    k = q if self_attn else z[pre + "key"]
+    v = q if self_attn else z[pre + "value"]
+    N = q.shape[0] if bf else q.shape[1]
+    L = q.shape[1] if bf else q.shape[0]
+    S = k.shape[1] if bf else k.shape[0]
+    mask = om.mha_mask(N, H, L, S, z.get(pre + "attn_mask"), z.get(pre + "key_padding_mask"))
+    out, w, cache = om.mha_forward(p, q, k, v, H, batch_first=bf, mask=mask)
+    close(out, z[pre + "out"])
+    close(w.mean(axis=1) if bool(z[pre + "avg"]) else w, z[pre + "weights"])
+    g = om.mha_backward(p, z[pre + "g"], cache)
+    for name in ("in_proj_weight", "in_proj_bias", "out_proj_weight", "out_proj_bias"):
+        close(g[name], z[pre + "d_" + name])
+    if self_attn:
+        close(g["query"] + g["key"] + g["value"], z[pre + "d_query"])
+    else:
+        for name in ("query", "key", "value"):
+            close(g[name], z[pre + "d_" + name])
+
+
+def test_mha_causal_flag_equals_causal_mask():
+    """The causal flag of the oracle's attention equals an explicit -inf
+    upper-triangle mask (the causal golden case uses the mask)."""
+    r = np.random.default_rng(3)
+    q, k, v = (r.standard_normal((2, 3, 6, 8)) for _ in range(3))
+    m = np.where(np.triu(np.ones((6, 6), dtype=bool), 1), -np.inf, 0.0)
+    close(ops.sdpa(q, k, v, causal=True)[0], ops.sdpa(q, k, v, mask=m)[0])
+    g = r.standard_normal((2, 3, 6, 8))
+    for a, b in zip(ops.sdpa_backward(g, q, k, v, causal=True),
+                    ops.sdpa_backward(g, q, k, v, mask=m)):
+        close(a, b)

@@ -48,6 +48,9 @@ __device__ __forceinline__ MS ms_comb(MS a, MS b) {
 }
 __device__ __forceinline__ MS ms_add(MS a, float x) {
   if (x > a.m) return MS{x, a.s * __expf(a.m - x) + 1.0f};
+  // a -inf element adds exp(-inf) = 0 (with a.m = -inf too, x - a.m would
+  // be NaN); NaN still propagates through the last line
+  if (x == -INFINITY) return a;
   return MS{a.m, a.s + __expf(x - a.m)};
 }
 __device__ __forceinline__ MS wave_ms(MS v) {

@@ -192,6 +192,145 @@ class Conv2d(Module):
                         self.groups)
 
 
+class MultiheadAttention(Module):
+    """nn.MultiheadAttention (src/nn/attention.ts:31-271) with the
+    reference's parameters: in_proj_weight [3E, E] (rows: the q, k and v
+    projections), in_proj_bias [3E], out_proj_weight [E, E] and
+    out_proj_bias [E], weights initialised randn * sqrt(1/E) and biases to
+    zero (attention.ts:72-95).  `dropout` is stored and not applied, as in
+    the reference (attention.ts:224-231).
+
+    On this device the projections are GEMMs with the bias in the epilogue:
+    one GEMM over in_proj_weight when query, key and value are one tensor
+    (self-attention; q, k and v are then strided views of its output, and
+    the backward assembles their gradients into that output's gradient
+    with no copy), two when key is value.  Attention runs on the flash
+    kernels (head dim 64; other head dims on the library's other attention
+    kernel) unless attention weights or masks are asked for, when the
+    scores are formed by batched GEMMs and softmaxed explicitly."""
+
+    def __init__(self, embed_dim, num_heads, dropout=0.0, bias=True, batch_first=False):
+        super().__init__()
+        if embed_dim <= 0 or num_heads <= 0:
+            raise ValueError("embed_dim and num_heads must be greater than 0, got embed_dim=%d "
+                             "and num_heads=%d" % (embed_dim, num_heads))
+        if embed_dim % num_heads:
+            raise ValueError("embed_dim must be divisible by num_heads")
+        self.embed_dim = embed_dim
+        self.num_heads = num_heads
+        self.dropout = dropout
+        self.batch_first = batch_first
+        self.head_dim = embed_dim // num_heads
+        k = math.sqrt(1.0 / embed_dim)
+        self.register_parameter("in_proj_weight",
+                                Parameter.create(randn(3 * embed_dim, embed_dim).mul(k)))
+        self.register_parameter("in_proj_bias",
+                                Parameter.create(zeros(3 * embed_dim)) if bias else None)
+        self.register_parameter("out_proj_weight",
+                                Parameter.create(randn(embed_dim, embed_dim).mul(k)))
+        self.register_parameter("out_proj_bias",
+                                Parameter.create(zeros(embed_dim)) if bias else None)
+
+    def _project(self, x, block, count):
+        """x [rows..., E] times `count` row blocks of in_proj_weight starting
+        at `block` (+ the same blocks of in_proj_bias), split per block."""
+        E = self.embed_dim
+        W = self.in_proj_weight
+        b = self.in_proj_bias
+        if block or count != 3:
+            W = W.narrow(0, block * E, count * E)
+            b = b.narrow(0, block * E, count * E) if b is not None else None
+        y = F.linear(x, W, b)
+        return list(y.split(E, dim=-1)) if count > 1 else [y]
+
+    def _mask(self, N, L, S, attn_mask, key_padding_mask):
+        """The additive float mask [N or 1, H or 1, L, S] of PyTorch's
+        nn.MultiheadAttention (the reference throws on both masks,
+        attention.ts:121-126): bool True = not allowed (-inf), float added;
+        attn_mask [L, S] or [N * H, L, S], key_padding_mask [N, S]."""
+        from .tensor import Tensor as _Tn, tensor as _tensor
+
+        def as_float(m, shape):
+            if not isinstance(m, _Tn):
+                m = _tensor(np.asarray(m))
+            if m.dtype in ("bool", "uint8"):
+                m = zeros(*m.shape).masked_fill(m, float("-inf"))
+            elif m.dtype != "float32":
+                m = m.float()
+            return m.reshape(*shape)
+        H = self.num_heads
+        out = None
+        if attn_mask is not None:
+            nd = attn_mask.ndim if isinstance(attn_mask, Tensor) else np.ndim(attn_mask)
+            if nd == 2:
+                out = as_float(attn_mask, (1, 1, L, S))
+            elif nd == 3:
+                out = as_float(attn_mask, (N, H, L, S))
+            else:
+                raise RuntimeError("attn_mask must be 2-D [L, S] or 3-D [N * num_heads, L, S]")
+        if key_padding_mask is not None:
+            kp = as_float(key_padding_mask, (N, 1, 1, S))
+            out = kp if out is None else out + kp
+        return out
+
+    def forward(self, query, key, value, key_padding_mask=None, need_weights=False,
+                attn_mask=None, average_attn_weights=True, is_causal=False):
+        """Returns (output, weights).  output is [L, N, E] ([N, L, E] with
+        batch_first); weights is None unless need_weights, then the softmax
+        weights averaged over heads [N, L, S] (PyTorch's default), or per head
+        [N, H, L, S] with average_attn_weights=False (what the reference
+        returns, attention.ts:260-266).  is_causal is PyTorch's hint that
+        attn_mask is the causal mask: it needs attn_mask, and without a
+        key-padding mask or weights the causal kernels run in its place."""
+        E, H, hd = self.embed_dim, self.num_heads, self.head_dim
+        if query.shape[-1] != E:
+            raise RuntimeError("MultiheadAttention: expected embed_dim %d, got %d"
+                               % (E, query.shape[-1]))
+        if is_causal and attn_mask is None:
+            raise RuntimeError("Need attn_mask if specifying the is_causal hint")
+        causal = bool(is_causal and key_padding_mask is None and not need_weights)
+        if causal:
+            attn_mask = None
+        if self.batch_first:
+            N, L = query.shape[0], query.shape[1]
+            S = key.shape[1]
+        else:
+            L, N = query.shape[0], query.shape[1]
+            S = key.shape[0]
+        if query is key and key is value:
+            q, k, v = self._project(query, 0, 3)
+        elif key is value:
+            q, = self._project(query, 0, 1)
+            k, v = self._project(key, 1, 2)
+        else:
+            q, = self._project(query, 0, 1)
+            k, = self._project(key, 1, 1)
+            v, = self._project(value, 2, 1)
+
+        def heads(t, T):  # [N, H, T, hd] view of a projection
+            if self.batch_first:
+                return t.view(N, T, H, hd).transpose(1, 2)
+            return t.view(T, N, H, hd).permute(1, 2, 0, 3)
+        q, k, v = heads(q, L), heads(k, S), heads(v, S)
+        mask = self._mask(N, L, S, attn_mask, key_padding_mask)
+        weights = None
+        if need_weights:
+            scores = (q @ k.transpose(-2, -1)) * (1.0 / math.sqrt(hd))
+            if mask is not None:
+                scores = scores + mask
+            p = F.softmax(scores, -1)
+            y = p @ v
+            weights = p.mean(1) if average_attn_weights else p
+        else:
+            y = F.scaled_dot_product_attention(q, k, v, attn_mask=mask, is_causal=causal)
+        # [N, H, L, hd] -> [N, L, E] rows, then the output projection
+        y = y.transpose(1, 2).contiguous().view(N, L, E)
+        out = F.linear(y, self.out_proj_weight, self.out_proj_bias)
+        if not self.batch_first:
+            out = out.transpose(0, 1)
+        return out, weights
+
+
 class ReLU(Module):
     def forward(self, x):
         return F.relu(x)
