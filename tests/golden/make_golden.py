@@ -455,6 +455,56 @@ def multihead_attention(rng):
     save("mha", **d)
 
 
+def second_order_functions(T, F):
+    """f(inputs) -> scalar, written with calls torch and the hip package
+    share; the second-derivative golden and its GPU test use the same
+    definitions."""
+    return {
+        "elementwise": lambda x: ((x.tanh() * x.sigmoid()).sum()
+                                  + (x.pow(3) / (x * x + 1.0)).mean()
+                                  + (x.exp() * x.sin()).sum() + (x * x + 2.0).log().sum()
+                                  + (x * x + 1.0).sqrt().sum() + x.cos().pow(2).sum()),
+        "linear_gelu": lambda x, w, b: F.gelu(F.linear(x, w, b)).pow(2).sum(),
+        "softmax": lambda x, w, t: (F.log_softmax(x @ w, -1) * t).sum()
+        + F.softmax(x @ w, -1).pow(2).sum(),
+        "broadcast": lambda x, y: ((x + y).exp().sin().sum() + (x * y).maximum(x - y).sum()
+                                   + (x / (y * y + 1.0)).sum()),
+        "views": lambda x: T.cat([x[0:2] * 2.0, x[2:5].relu() + x[2:5]], 0)
+        .transpose(0, 1).reshape(-1).pow(2).sum() + x.permute(1, 0).mean(1).pow(3).sum(),
+        "bmm": lambda x, w: (x @ w).tanh().pow(2).sum() + (x.sum(1, keepdim=True) * x).sum(),
+    }
+
+
+SECOND_ORDER_SHAPES = {
+    "elementwise": [(5, 7)], "linear_gelu": [(6, 5), (4, 5), (4,)],
+    "softmax": [(6, 5), (5, 7), (6, 7)], "broadcast": [(4, 6), (6,)], "views": [(5, 3)],
+    "bmm": [(2, 3, 4), (2, 4, 5)],
+}
+SECOND_ORDER_CONST = {"softmax": [2]}  # inputs that are constants (no gradient)
+
+
+def second_order(rng):
+    """First derivatives built with create_graph=True, then Hessian-vector
+    products: grad of sum_i <grad_i, v_i> w.r.t. the inputs."""
+    d = {}
+    for name, fn in second_order_functions(torch, torch.nn.functional).items():
+        const = SECOND_ORDER_CONST.get(name, [])
+        xs = [rng.standard_normal(shp) * 0.7 for shp in SECOND_ORDER_SHAPES[name]]
+        ts = [t(x, i not in const) for i, x in enumerate(xs)]
+        var = [tt for i, tt in enumerate(ts) if i not in const]
+        g1 = torch.autograd.grad(fn(*ts), var, create_graph=True)
+        vs = [rng.standard_normal(tuple(g.shape)) for g in g1]
+        dot = sum((g * t(v)).sum() for g, v in zip(g1, vs))
+        h = torch.autograd.grad(dot, var)
+        for i, x in enumerate(xs):
+            d["%s:x%d" % (name, i)] = x
+        for i, (g, v, hv) in enumerate(zip(g1, vs, h)):
+            d["%s:g%d" % (name, i)] = g
+            d["%s:v%d" % (name, i)] = v
+            d["%s:h%d" % (name, i)] = hv
+    save("second_order", **d)
+
+
 def main():
     serialization_fixtures()
     losses_ext(np.random.default_rng(20261202))
@@ -471,6 +521,7 @@ def main():
     optim(rng)
     models(rng)
     multihead_attention(np.random.default_rng(20261205))
+    second_order(np.random.default_rng(20261206))
     print("wrote", sorted(f for f in os.listdir(OUT) if f.endswith(".npz")))
 
 

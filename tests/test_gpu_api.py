@@ -48,11 +48,32 @@ def test_autograd_grad_literals(torch):
     close4(gw.toArray(), [1.0, 2.0])
     # grad leaves .grad untouched
     assert x.grad is None and w.grad is None
-    # second order needs create_graph, which the hip path does not build
-    # (autograd.test.ts:47-55): a clear error, not a wrong number
+    # second order with create_graph (autograd.test.ts:47-55): d2(x^3)/dx2 = 6x = 12
     x = torch.tensor([2.0], requires_grad=True)
-    with pytest.raises(NotImplementedError):
-        torch.autograd.grad(x.pow(3), x, torch.ones_like(x), True, True)
+    y = x.pow(3)
+    (g1,) = torch.autograd.grad(y, x, torch.ones_like(y), True, True)
+    close4(g1.toArray(), [12.0])
+    assert g1.requires_grad and g1.grad_fn is not None
+    (g2,) = torch.autograd.grad(g1, x, torch.ones_like(g1))
+    close4(g2.toArray(), [12.0])
+    # and a third: d3/dx3 = 6
+    x = torch.tensor([2.0], requires_grad=True)
+    (g1,) = torch.autograd.grad(x.pow(3), x, create_graph=True)
+    (g2,) = torch.autograd.grad(g1, x, create_graph=True)
+    (g3,) = torch.autograd.grad(g2, x)
+    close4(g3.toArray(), [6.0])
+    # backward(create_graph=True): the leaf's .grad carries a graph
+    x = torch.tensor([1.5, -0.5], requires_grad=True)
+    (x.exp() * x).sum().backward(create_graph=True)
+    gx = x.grad
+    assert gx.grad_fn is not None
+    (h,) = torch.autograd.grad(gx.sum(), x)
+    xv = np.array([1.5, -0.5])
+    close4(h.toArray(), list(np.exp(xv) * (xv + 2)))       # (x e^x)'' = e^x (x + 2)
+    # an op with no differentiable backward says so
+    x = torch.tensor(np.ones((4, 8), np.float32), requires_grad=True)
+    with pytest.raises(NotImplementedError, match="LayerNorm"):
+        torch.autograd.grad(torch.F.layer_norm(x, (8,)).pow(2).sum(), x, create_graph=True)
 
 
 def test_autograd_vjp_literals(torch):
@@ -66,9 +87,12 @@ def test_autograd_vjp_literals(torch):
     _, v = torch.autograd.vjp(f, torch.tensor([1.0, 2.0, 3.0], requires_grad=True),
                               torch.tensor([1.0, 1.0]))
     close4(v.toArray(), [1.0, 2.0, 1.0])                  # :77-91
-    _, v = torch.autograd.vjp(lambda t: t.pow(3), torch.tensor([2.0], requires_grad=True),
-                              torch.tensor([1.0]), True)
+    x = torch.tensor([2.0], requires_grad=True)
+    _, v = torch.autograd.vjp(lambda t: t.pow(3), x, torch.tensor([1.0]), True)
     close4(v.toArray(), [12.0])                           # :93-105
+    # with create_graph the product differentiates again: d(3x^2)/dx = 12
+    (h,) = torch.autograd.grad(v, x)
+    close4(h.toArray(), [12.0])
 
 
 def test_autograd_jvp_literals(torch):
@@ -82,6 +106,55 @@ def test_autograd_jvp_literals(torch):
     _, j = torch.autograd.jvp(lambda t: t.pow(2).sum(-1, True), torch.tensor([2.0, 3.0]),
                               torch.tensor([1.0, 0.0]))
     close4(j.toArray(), [4.0])                            # :137-149
+
+
+SECOND_ORDER = ["elementwise", "linear_gelu", "softmax", "broadcast", "views", "bmm"]
+
+
+@pytest.mark.parametrize("name", SECOND_ORDER)
+def test_second_order_golden(torch, name):
+    """First derivatives built with create_graph=True and Hessian-vector
+    products (the gradient of sum_i <grad_i, v_i>) against PyTorch in
+    float64 (tests/golden/second_order.npz), through the unary, binary
+    (broadcast), scalar, reduction, view, cat / narrow, matmul, Linear and
+    softmax ops.  The functions are the ones the golden was written from."""
+    from conftest import golden
+    z = golden("second_order")
+    fn = _second_order_functions(torch)[name]
+    xs = [z["%s:x%d" % (name, i)] for i in range(8) if "%s:x%d" % (name, i) in z]
+    const = {"softmax": [2]}.get(name, [])
+    ts = [torch.tensor(f32(x), requires_grad=i not in const) for i, x in enumerate(xs)]
+    var = [t for i, t in enumerate(ts) if i not in const]
+    g1 = torch.autograd.grad(fn(*ts), var, create_graph=True)
+    for i, g in enumerate(g1):
+        check(g.numpy(), z["%s:g%d" % (name, i)], **RED)
+    dot = None
+    for i, g in enumerate(g1):
+        term = (g * torch.tensor(f32(z["%s:v%d" % (name, i)]))).sum()
+        dot = term if dot is None else dot + term
+    h = torch.autograd.grad(dot, var)
+    for i, hv in enumerate(h):
+        check(hv.numpy(), z["%s:h%d" % (name, i)], **RED)
+
+
+def _second_order_functions(torch):
+    """The definitions of tests/golden/make_golden.py second_order_functions,
+    over the hip package."""
+    T, F = torch, torch.F
+    return {
+        "elementwise": lambda x: ((x.tanh() * x.sigmoid()).sum()
+                                  + (x.pow(3) / (x * x + 1.0)).mean()
+                                  + (x.exp() * x.sin()).sum() + (x * x + 2.0).log().sum()
+                                  + (x * x + 1.0).sqrt().sum() + x.cos().pow(2).sum()),
+        "linear_gelu": lambda x, w, b: F.gelu(F.linear(x, w, b)).pow(2).sum(),
+        "softmax": lambda x, w, t: (F.log_softmax(x @ w, -1) * t).sum()
+        + F.softmax(x @ w, -1).pow(2).sum(),
+        "broadcast": lambda x, y: ((x + y).exp().sin().sum() + (x * y).maximum(x - y).sum()
+                                   + (x / (y * y + 1.0)).sum()),
+        "views": lambda x: T.cat([x[0:2] * 2.0, x[2:5].relu() + x[2:5]], 0)
+        .transpose(0, 1).reshape(-1).pow(2).sum() + x.permute(1, 0).mean(1).pow(3).sum(),
+        "bmm": lambda x, w: (x @ w).tanh().pow(2).sum() + (x.sum(1, keepdim=True) * x).sum(),
+    }
 
 
 def test_autograd_function_literals(torch):

@@ -24,13 +24,15 @@ def _pairs(outputs, grad_outputs):
 def grad(outputs, inputs, grad_outputs=None, retain_graph=None, create_graph=False,
          allow_unused=False):
     """autograd.grad (src/autograd.ts:22-72): gradients of outputs w.r.t.
-    inputs, without touching .grad."""
-    if create_graph:
-        raise NotImplementedError("create_graph=True is not supported on the hip device")
+    inputs, without touching .grad.  With create_graph the gradients carry
+    graphs of their own, so grad() can be applied to them again (second
+    derivatives); retain_graph then defaults to True, as in PyTorch."""
     single = isinstance(inputs, Tensor)
     inputs = [inputs] if single else list(inputs)
+    if retain_graph is None:
+        retain_graph = create_graph
     res = run_backward(_pairs(outputs, grad_outputs), retain_graph=bool(retain_graph),
-                       inputs=inputs)
+                       inputs=inputs, create_graph=bool(create_graph))
     for t, r in zip(inputs, res):
         if r is None and not allow_unused:
             raise RuntimeError("One of the differentiated Tensors appears to not have been used "
@@ -38,20 +40,24 @@ def grad(outputs, inputs, grad_outputs=None, retain_graph=None, create_graph=Fal
     return tuple(res)
 
 
-def backward(tensors, grad_tensors=None, retain_graph=False):
-    run_backward(_pairs(tensors, grad_tensors), retain_graph=retain_graph)
+def backward(tensors, grad_tensors=None, retain_graph=None, create_graph=False):
+    if retain_graph is None:
+        retain_graph = create_graph
+    run_backward(_pairs(tensors, grad_tensors), retain_graph=retain_graph,
+                 create_graph=create_graph)
 
 
 def vjp(func, inputs, v=None, create_graph=False):
     """autograd.functional.vjp (src/autograd.ts:74-86): (func(inputs), v^T J).
-    The product is computed the same with create_graph; it is returned
-    without a graph of its own (double backward is not on the hip path)."""
+    With create_graph the product carries a graph back to `inputs` (which
+    keep requiring grad), so it can be differentiated again."""
     single = isinstance(inputs, Tensor)
     ins = [inputs] if single else list(inputs)
-    ins = [i.detach().requires_grad_(True) for i in ins]
+    if not create_graph:
+        ins = [i.detach().requires_grad_(True) for i in ins]
     out = func(*ins)
-    g = grad(out, ins, grad_outputs=v, allow_unused=True)
-    return out.detach(), (g[0] if single else g)
+    g = grad(out, ins, grad_outputs=v, allow_unused=True, create_graph=create_graph)
+    return (out if create_graph else out.detach()), (g[0] if single else g)
 
 
 def jvp(func, inputs, v, create_graph=False):
@@ -116,7 +122,10 @@ class Function:
                 return [gs[i] if i < len(gs) else None for i in positions]
             out = out.detach()
             out.requires_grad = True
-            out.grad_fn = Node(cls.__name__, [t if t.requires_grad else None for t in tens], fn)
+            # with create_graph the engine runs backward() in grad mode, so
+            # the user's ops record the gradient's own graph (gfn = fn)
+            out.grad_fn = Node(cls.__name__, [t if t.requires_grad else None for t in tens], fn,
+                               gfn=fn)
         return out
 
     @staticmethod

@@ -89,7 +89,13 @@ def _softmax_impl(x, dim, log):
         L.check(L.lib().tjh_softmax_backward(g.data_ptr(), y.data_ptr(), dx.data_ptr(), rows, cols,
                                              1 if log else 0), "softmax_backward")
         return [dx]
-    return _record(out, "LogSoftmax" if log else "Softmax", [x], bwd)
+
+    def gbwd(g):  # recording ops, softmax recomputed from x
+        p = _softmax_impl(x, -1, False)
+        if log:
+            return [_T.sub(g, _T.mul(p, _T.reduce_sum(g, -1, keepdim=True)))]
+        return [_T.mul(p, _T.sub(g, _T.reduce_sum(_T.mul(g, p), -1, keepdim=True)))]
+    return _record(out, "LogSoftmax" if log else "Softmax", [x], bwd, gfn=gbwd)
 
 
 def softmax(x, dim=-1):
@@ -383,7 +389,14 @@ def linear(x, weight, bias=None):
             gc = g2 if g2.is_contiguous() else _k_contiguous(g2)
             db = _view_raw(_k_reduce("sum", gc, [0]), (out_f,))
         return [dx, dw, db]
-    return _record(out, "Linear", [x, weight, bias], bwd)
+
+    def gbwd(g):  # recording ops: the gradients can be differentiated again
+        g2 = _T.reshape(g, (M, out_f))
+        dx = _T.reshape(_T.matmul(g2, weight), lead + (in_f,)) if rx else None
+        dw = _T.matmul(_T.transpose(g2, 0, 1), _T.reshape(x, (M, in_f))) if rw else None
+        db = _T.reduce_sum(g2, 0) if rb else None
+        return [dx, dw, db]
+    return _record(out, "Linear", [x, weight, bias], bwd, gfn=gbwd)
 
 
 def _linear_add(x, weight, bias, residual):

@@ -226,16 +226,21 @@ class Node:
     until the library's tjh_flush_deferred (`fn(grad, defer=True)`); the
     engine allows it when each of them is a leaf receiving its first
     gradient of the pass, and flushes before any of those gradients is
-    read (a second contribution, the end of the pass)."""
+    read (a second contribution, the end of the pass).
 
-    __slots__ = ("name", "inputs", "fn", "acc_slot", "defer_slots", "__weakref__")
+    `gfn(grad)`: the same vector-Jacobian product written with recording
+    ops, for backward passes that build a graph of their own
+    (create_graph=True, second derivatives); None where the op has none."""
 
-    def __init__(self, name, inputs, fn, acc_slot=None, defer_slots=()):
+    __slots__ = ("name", "inputs", "fn", "acc_slot", "defer_slots", "gfn", "__weakref__")
+
+    def __init__(self, name, inputs, fn, acc_slot=None, defer_slots=(), gfn=None):
         self.name = name
         self.inputs = inputs
         self.fn = fn
         self.acc_slot = acc_slot
         self.defer_slots = defer_slots
+        self.gfn = gfn
 
     def __repr__(self):
         return "<%sBackward>" % self.name
@@ -246,11 +251,11 @@ class Node:
         return [t for t in self.inputs if t is not None]
 
 
-def _record(out, name, inputs, fn, acc_slot=None, defer_slots=()):
+def _record(out, name, inputs, fn, acc_slot=None, defer_slots=(), gfn=None):
     if _grad["enabled"] and any(t is not None and t.requires_grad for t in inputs):
         out.requires_grad = True
         out.grad_fn = Node(name, [t if (t is not None and t.requires_grad) else None
-                                  for t in inputs], fn, acc_slot, defer_slots)
+                                  for t in inputs], fn, acc_slot, defer_slots, gfn)
     return out
 
 
@@ -398,16 +403,17 @@ class Tensor:
 
     # ------------------------------------------------------------ autograd
     def backward(self, gradient=None, retain_graph=False, create_graph=False):
-        """Tensor.backward (Tensor.ts:3686-3740)."""
-        if create_graph:
-            raise NotImplementedError("create_graph=True is not supported on the hip device")
+        """Tensor.backward (Tensor.ts:3686-3740).  With create_graph the
+        gradients carry graphs of their own (leaf .grad can be
+        differentiated again)."""
         if not self.requires_grad:
             raise RuntimeError("element 0 of tensors does not require grad and does not have a grad_fn")
         if gradient is None:
             if self.numel() != 1:
                 raise RuntimeError("grad can be implicitly created only for scalar outputs")
             gradient = full(self._shape, 1.0)
-        run_backward([(self, gradient)], retain_graph=retain_graph)
+        run_backward([(self, gradient)], retain_graph=retain_graph or create_graph,
+                     create_graph=create_graph)
 
     def detach(self):
         if self._st is None:  # stays deferred, sharing the value
@@ -1661,6 +1667,128 @@ def _view_raw(t, shape):
     return Tensor(t._storage, shape, None, t._offset, t._dtype)
 
 
+def _sum_to_g(g, shape):
+    """_sum_to with recording ops (a gradient that is itself differentiated)."""
+    shape = tuple(shape)
+    if g.shape == shape:
+        return g
+    off = g.ndim - len(shape)
+    dims = [d for d in range(g.ndim) if d < off or (shape[d - off] == 1 and g.shape[d] != 1)]
+    r = reduce_sum(g, dims, keepdim=True) if dims else g
+    return reshape(r, shape)
+
+
+def _const(t, v):
+    return full((), float(v))
+
+
+def _unary_gvjp(op, g, x, alpha):
+    """g * op'(x) with recording ops, so the result can be differentiated
+    again (second derivatives through the unary ops)."""
+    sc = lambda t, v: _scalar_op("mul", t, v)
+    if op == "neg":
+        return unary("neg", g)
+    if op == "exp":
+        return mul(g, unary("exp", x))
+    if op == "log":
+        return div(g, x)
+    if op == "sqrt":
+        return mul(g, sc(unary("rsqrt", x), 0.5))
+    if op == "rsqrt":
+        r = unary("rsqrt", x)
+        return mul(g, sc(mul(r, mul(r, r)), -0.5))
+    if op == "tanh":
+        t = unary("tanh", x)
+        return mul(g, _scalar_op("sub", mul(t, t), 1.0, reverse=True))
+    if op == "sigmoid":
+        sg = unary("sigmoid", x)
+        return mul(g, mul(sg, _scalar_op("sub", sg, 1.0, reverse=True)))
+    if op == "relu":
+        return mul(g, compare_raw(x, _const(x, 0.0), "gt"))
+    if op == "square":
+        return mul(g, sc(x, 2.0))
+    if op == "reciprocal":
+        return unary("neg", div(g, mul(x, x)))
+    if op == "sin":
+        return mul(g, unary("cos", x))
+    if op == "cos":
+        return unary("neg", mul(g, unary("sin", x)))
+    if op == "abs":
+        return mul(g, unary("sign", x))
+    if op == "sign":
+        return sc(g, 0.0)
+    if op == "erf":
+        return mul(g, sc(unary("exp", unary("neg", mul(x, x))), 2.0 / math.sqrt(math.pi)))
+    if op == "gelu":  # Phi(x) + x phi(x)
+        phi_cdf = sc(_scalar_op("add", unary("erf", sc(x, 1.0 / math.sqrt(2.0))), 1.0), 0.5)
+        pdf = sc(unary("exp", sc(mul(x, x), -0.5)), 1.0 / math.sqrt(2.0 * math.pi))
+        return mul(g, add(phi_cdf, mul(x, pdf)))
+    if op == "silu":
+        sg = unary("sigmoid", x)
+        return mul(g, mul(sg, _scalar_op("add", mul(x, _scalar_op("sub", sg, 1.0, reverse=True)),
+                                         1.0)))
+    if op == "softplus":  # sigmoid(x), and 1 above the threshold of 20
+        big = compare_raw(x, _const(x, 20.0), "gt")
+        return mul(g, add(mul(unary("sigmoid", x), _scalar_op("sub", big, 1.0, reverse=True)),
+                          big))
+    if op == "leaky_relu":
+        pos = compare_raw(x, _const(x, 0.0), "gt")
+        return mul(g, _scalar_op("add", sc(pos, 1.0 - alpha), alpha))
+    if op == "elu":
+        pos = compare_raw(x, _const(x, 0.0), "gt")
+        negw = mul(sc(unary("exp", x), alpha), _scalar_op("sub", pos, 1.0, reverse=True))
+        return mul(g, add(negw, pos))
+    raise NotImplementedError("create_graph: no differentiable backward for %s" % op)
+
+
+def _binary_gvjp(op, g, a, b):
+    """Both operands' gradients of a (broadcasting) binary op with
+    recording ops, summed back to each operand's shape."""
+    ra, rb = a.requires_grad, b.requires_grad
+    if op == "add":
+        ga, gb = g, g
+    elif op == "sub":
+        ga, gb = g, (unary("neg", g) if rb else None)
+    elif op == "mul":
+        ga = mul(g, b) if ra else None
+        gb = mul(g, a) if rb else None
+    elif op == "div":
+        ga = div(g, b) if ra else None
+        gb = unary("neg", div(mul(g, a), mul(b, b))) if rb else None
+    elif op == "pow":
+        ga = mul(g, mul(b, _binary_op("pow", a, _scalar_op("sub", b, 1.0)))) if ra else None
+        gb = mul(g, mul(_binary_op("pow", a, b), unary("log", a))) if rb else None
+    else:  # maximum / minimum: the selected operand, ties split evenly
+        sel = compare_raw(a, b, "gt" if op == "maximum" else "lt")
+        wa = _k_binary("add", sel, _k_scalar("mul", compare_raw(a, b, "eq"), 0.5))
+        ga = mul(g, wa) if ra else None
+        gb = mul(g, _scalar_op("sub", wa, 1.0, reverse=True)) if rb else None
+    return [_sum_to_g(ga, a.shape) if (ra and ga is not None) else None,
+            _sum_to_g(gb, b.shape) if (rb and gb is not None) else None]
+
+
+def _scalar_gvjp(op, g, x, s, reverse):
+    """The gradient of x (op) s, or s (op) x with `reverse`, with recording
+    ops."""
+    if op == "add":
+        return g
+    if op == "sub":
+        return unary("neg", g) if reverse else g
+    if op == "mul":
+        return _scalar_op("mul", g, s)
+    if op == "div":
+        if not reverse:
+            return _scalar_op("div", g, s)
+        return unary("neg", div(_scalar_op("mul", g, s), mul(x, x)))
+    if op == "pow":
+        if not reverse:
+            return mul(g, _scalar_op("mul", _scalar_op("pow", x, s - 1.0), s))
+        return mul(g, _scalar_op("mul", _scalar_op("pow", x, s, reverse=True), math.log(s)))
+    if op in ("maximum", "minimum"):
+        return mul(g, compare_raw(x, full((), s), "gt" if op == "maximum" else "lt"))
+    raise NotImplementedError("create_graph: no differentiable backward for %s_scalar" % op)
+
+
 # ----------------------------------------------------------------- differentiable ops
 
 
@@ -1678,7 +1806,7 @@ def unary(op, x, alpha=0.0):
 
     def bwd(g):
         return [_k_unary_bwd(op, g, saved_x, saved_y, alpha)]
-    return _record(out, op, [x], bwd)
+    return _record(out, op, [x], bwd, gfn=lambda g: [_unary_gvjp(op, g, x, alpha)])
 
 
 def neg(x):
@@ -1731,7 +1859,7 @@ def _binary_op(op, a, b):
                 wb = _k_scalar("add", _k_scalar("mul", wa, -1.0), 1.0)
                 return [_sum_to(_k_binary("mul", g, wa), ash) if ra else None,
                         _sum_to(_k_binary("mul", g, wb), bsh) if rb else None]
-    return _record(out, op, [a, b], bwd)
+    return _record(out, op, [a, b], bwd, gfn=lambda g: _binary_gvjp(op, g, a, b))
 
 
 def _scalar_op(op, x, s, reverse=False):
@@ -1767,7 +1895,8 @@ def _scalar_op(op, x, s, reverse=False):
             m = compare_raw(x, full((), s), "gt" if op == "maximum" else "lt")
             return [_k_binary("mul", g, m)]
         raise NotImplementedError(op)
-    return _record(out, op + "_scalar", [x], bwd)
+    return _record(out, op + "_scalar", [x], bwd,
+                   gfn=lambda g: [_scalar_gvjp(op, g, x, s, reverse)])
 
 
 def add(a, b):
@@ -1942,7 +2071,7 @@ def reduce_sum(x, dim=None, keepdim=False):
 
     def bwd(g):
         return [_view_raw(g.contiguous(), kshape).expand(xs)]
-    return _record(out, "Sum", [x], bwd)
+    return _record(out, "Sum", [x], bwd, gfn=lambda g: [expand(reshape(g, kshape), xs)])
 
 
 def reduce_mean(x, dim=None, keepdim=False):
@@ -1961,7 +2090,11 @@ def reduce_mean(x, dim=None, keepdim=False):
     def bwd(g):
         gs = _k_scalar("mul", g, 1.0 / cnt) if cnt else g
         return [_view_raw(gs.contiguous(), kshape).expand(xs)]
-    return _record(out, "Mean", [x], bwd)
+
+    def gbwd(g):
+        gs = _scalar_op("mul", g, 1.0 / cnt) if cnt else g
+        return [expand(reshape(gs, kshape), xs)]
+    return _record(out, "Mean", [x], bwd, gfn=gbwd)
 
 
 def reduce_minmax(x, dim, keepdim, which):
@@ -2063,7 +2196,8 @@ def view(x, shape):
         raise RuntimeError("view size is not compatible with input tensor's size and stride; use reshape")
     out = _alias(x, shape, st, x._offset)
     xs = x.shape
-    return _record(out, "View", [x], lambda g: [reshape_raw(g, xs)])
+    return _record(out, "View", [x], lambda g: [reshape_raw(g, xs)],
+                   gfn=lambda g: [reshape(g, xs)])
 
 
 def reshape_raw(g, shape):
@@ -2110,7 +2244,8 @@ def unsqueeze(x, dim):
     st.insert(d, (x._strides[d] * x.shape[d]) if d < x.ndim else 1)
     out = _alias(x, shape, tuple(st), x._offset)
     xs = x.shape
-    return _record(out, "Unsqueeze", [x], lambda g: [reshape_raw(g, xs)])
+    return _record(out, "Unsqueeze", [x], lambda g: [reshape_raw(g, xs)],
+                   gfn=lambda g: [reshape(g, xs)])
 
 
 def permute(x, dims):
@@ -2127,7 +2262,7 @@ def permute(x, dims):
     def bwd(g):
         return [_alias(g, tuple(g.shape[i] for i in inv), tuple(g._strides[i] for i in inv),
                        g._offset)]
-    return _record(out, "Permute", [x], bwd)
+    return _record(out, "Permute", [x], bwd, gfn=lambda g: [permute(g, inv)])
 
 
 def transpose(x, d0, d1):
@@ -2169,19 +2304,20 @@ def expand(x, shape):
                 raise RuntimeError("expand: size %d cannot expand to %d" % (have, want))
     out = _alias(x, tuple(new_shape), tuple(st), x._offset)
     xs = x.shape
-    return _record(out, "Expand", [x], lambda g: [_sum_to(g, xs)])
+    return _record(out, "Expand", [x], lambda g: [_sum_to(g, xs)],
+                   gfn=lambda g: [_sum_to_g(g, xs)])
 
 
 def contiguous(x):
     if x.is_contiguous():
         return x
     out = _k_contiguous(x)
-    return _record(out, "Contiguous", [x], lambda g: [g])
+    return _record(out, "Contiguous", [x], lambda g: [g], gfn=lambda g: [g])
 
 
 def clone(x):
     out = _k_contiguous(x)
-    return _record(out, "Clone", [x], lambda g: [g])
+    return _record(out, "Clone", [x], lambda g: [g], gfn=lambda g: [g])
 
 
 def narrow(x, dim, start, length):
@@ -2194,7 +2330,16 @@ def narrow(x, dim, start, length):
     shape = x.shape[:d] + (length,) + x.shape[d + 1:]
     out = _alias(x, shape, x._strides, x._offset + start * x._strides[d])
     xs = x.shape
-    return _record(out, "Narrow", [x], lambda g: [_SliceGrad(xs, d, [(start, g)])])
+
+    def gbwd(g):  # g placed at [start, start + length) of zeros along d
+        parts = []
+        if start:
+            parts.append(zeros(*(xs[:d] + (start,) + xs[d + 1:])))
+        parts.append(g)
+        if start + length < n:
+            parts.append(zeros(*(xs[:d] + (n - start - length,) + xs[d + 1:])))
+        return [cat(parts, d) if len(parts) > 1 else g]
+    return _record(out, "Narrow", [x], lambda g: [_SliceGrad(xs, d, [(start, g)])], gfn=gbwd)
 
 
 def select(x, dim, index):
@@ -2287,7 +2432,14 @@ def cat(tensors, dim=0):
                               g._offset + p * g._strides[d]))
             p += s
         return res
-    return _record(out, "Cat", tensors, bwd)
+
+    def gbwd(g):
+        res, p = [], 0
+        for s in sizes:
+            res.append(narrow(g, d, p, s))
+            p += s
+        return res
+    return _record(out, "Cat", tensors, bwd, gfn=gbwd)
 
 
 def stack(tensors, dim=0):
@@ -2319,7 +2471,7 @@ def masked_fill(x, mask, value):
                                         L.i64arr(g._strides), m.data_ptr(), L.i64arr(mst), 0.0,
                                         o.data_ptr()), "masked_fill_backward")
         return [o]
-    return _record(out, "MaskedFill", [x], bwd)
+    return _record(out, "MaskedFill", [x], bwd, gfn=lambda g: [masked_fill(g, m, 0.0)])
 
 
 def _to_mask(t):
@@ -2594,7 +2746,11 @@ def matmul(a, b):
                                                            a3._strides[1]), a3._offset)
             gb = _sum_to(_view_raw(_bgemm(at, g3), tuple(bshape) + (K, N)), bsh)
         return [ga, gb]
-    return _record(out, "BMM", [a, b], bwd)
+
+    def gbwd(g):
+        return [_sum_to_g(matmul(g, transpose(b, -2, -1)), ash) if a.requires_grad else None,
+                _sum_to_g(matmul(transpose(a, -2, -1), g), bsh) if b.requires_grad else None]
+    return _record(out, "BMM", [a, b], bwd, gfn=gbwd)
 
 
 def _mm(a, b):
@@ -2604,7 +2760,11 @@ def _mm(a, b):
         ga = _gemm(g, b.detach().T) if a.requires_grad else None
         gb = _gemm(a.detach().T, g) if b.requires_grad else None
         return [ga, gb]
-    return _record(out, "MM", [a, b], bwd)
+
+    def gbwd(g):
+        return [matmul(g, transpose(b, 0, 1)) if a.requires_grad else None,
+                matmul(transpose(a, 0, 1), g) if b.requires_grad else None]
+    return _record(out, "MM", [a, b], bwd, gfn=gbwd)
 
 
 _add_unary_methods()
@@ -2767,10 +2927,86 @@ def _toposort(roots):
     return order  # post-order: inputs before users
 
 
-def run_backward(pairs, retain_graph=False, inputs=None):
+def _run_backward_graph(pairs, retain_graph, inputs):
+    """The sweep of run_backward with create_graph: grad mode stays on and
+    every node runs its recording VJP (Node.gfn), so the gradients it
+    produces carry graphs back to the leaves and can be differentiated again
+    (torch.js runs its backward closures with grad mode on, Tensor.ts:3686,
+    so its gradients record the same way).  None of the engine's fusions
+    take part: gradients are summed with recording adds."""
+    prev = _grad["enabled"]
+    _grad["enabled"] = True
+    try:
+        grads = {}
+        roots = []
+        wanted = {id(t): t for t in inputs} if inputs is not None else None
+        results = {}
+
+        def acc(d, key, g):
+            d[key] = g if key not in d else add(d[key], g)
+
+        def to_leaf(t, g):
+            if t._grad is None:
+                t._grad = g
+            else:
+                t._grad = add(t._grad, g)
+
+        for t, g in pairs:
+            if g.shape != t.shape:
+                g = reshape(g, t.shape) if g.numel() == t.numel() else expand(g, t.shape)
+            if t.grad_fn is None:
+                if wanted is not None:
+                    if id(t) in wanted:
+                        acc(results, id(t), g)
+                elif t.requires_grad:
+                    to_leaf(t, g)
+                continue
+            acc(grads, id(t.grad_fn), g)
+            roots.append(t.grad_fn)
+        for node in reversed(_toposort(roots)):
+            g = grads.pop(id(node), None)
+            if g is None:
+                continue
+            if node.fn is None:
+                raise RuntimeError("Trying to backward through the graph a second time; "
+                                   "pass retain_graph=True the first time")
+            if node.gfn is None:
+                raise NotImplementedError(
+                    "create_graph: %s has no differentiable backward on the hip device"
+                    % node.name)
+            in_grads = node.gfn(g)
+            for t, gi in zip(node.inputs, in_grads):
+                if t is None or gi is None:
+                    continue
+                if tuple(gi.shape) != t.shape:
+                    gi = _sum_to_g(gi, t.shape) if gi.ndim >= t.ndim else reshape(gi, t.shape)
+                if wanted is not None and id(t) in wanted:
+                    acc(results, id(t), gi)
+                if t.grad_fn is not None:
+                    acc(grads, id(t.grad_fn), gi)
+                    if t._retains_grad and wanted is None:
+                        to_leaf(t, gi)
+                elif wanted is None and t.requires_grad:
+                    to_leaf(t, gi)
+            if not retain_graph:
+                node.fn = None
+                node.gfn = None
+                node.inputs = [None] * len(node.inputs)
+        if wanted is not None:
+            return [results.get(id(t)) for t in inputs]
+        return None
+    finally:
+        _grad["enabled"] = prev
+
+
+def run_backward(pairs, retain_graph=False, inputs=None, create_graph=False):
     """Reverse-topological VJP sweep (Tensor.backward, Tensor.ts:3686-3740;
     accumulateGrad, Tensor.ts:3670-3677).  With `inputs`, returns their
-    gradients instead of accumulating into leaves (autograd.grad)."""
+    gradients instead of accumulating into leaves (autograd.grad).  With
+    `create_graph`, the gradients are built from recording ops
+    (_run_backward_graph)."""
+    if create_graph:
+        return _run_backward_graph(pairs, retain_graph, inputs)
     prev = _grad["enabled"]
     _grad["enabled"] = False
     deferred = set()  # ids of leaves whose .grad awaits tjh_flush_deferred
