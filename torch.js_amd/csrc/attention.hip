@@ -16,6 +16,7 @@
 // Scratch holds [H, Tq, Tk] scores for ONE batch item at a time.
 
 #include "common.h"
+#include "wave.h"
 
 #include <float.h>
 
@@ -24,16 +25,6 @@ namespace {
 
 constexpr int kBlock = 256;
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
-}
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-  return v;
-}
 
 // In place: S (already scaled) -> P, lse[row] written.  Row r of [H*Tq]
 // has query index i = r % Tq; with causal only cols j <= i are valid.

@@ -39,6 +39,7 @@
 // causal blocks (balanced_rank).
 
 #include "common.h"
+#include "wave.h"
 
 #include <float.h>
 #include <stdlib.h>
@@ -348,8 +349,7 @@ __global__ __launch_bounds__(256) void k_flash_dsum(FlashArgs a, float* __restri
   const int64_t b = bh / a.H, hh = bh % a.H;
   float x = a.dout[b * a.gs.b + hh * a.gs.h + q * a.gs.t + lane] *
             a.o[b * a.os.b + hh * a.os.h + q * a.os.t + lane];
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off, 64);
+  x = wave_sum(x);
   if (lane == 0) dsum[r] = x;
 }
 
@@ -376,8 +376,7 @@ __global__ __launch_bounds__(256) void k_flash_dsum4(FlashArgs a, float* __restr
 #pragma unroll
   for (int i = 0; i < R; ++i) {
     float x = (g[i].x * o[i].x + g[i].y * o[i].y) + (g[i].z * o[i].z + g[i].w * o[i].w);
-#pragma unroll
-    for (int off = 8; off >= 1; off >>= 1) x += __shfl_xor(x, off, 16);
+    x = row16_sum(x);  // the 16-lane group is one DPP row
     if (sub == 0 && r0 + i < rows) dsum[r0 + i] = x;
   }
 }

@@ -15,6 +15,7 @@
 // 16-byte boundary, stream float4s, and finish with a scalar tail.
 
 #include "colsum.h"
+#include "wave.h"
 
 #include <vector>
 
@@ -25,17 +26,6 @@ namespace {
 
 constexpr int kBlock = 256;
 constexpr int kLnBwdWaves = 8;  // waves per k_ln_bwd_wave workgroup
-
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
-}
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-  return v;
-}
 
 // Online (max, sum-of-exp) pair.
 struct MS {
@@ -53,13 +43,19 @@ __device__ __forceinline__ MS ms_add(MS a, float x) {
   if (x == -INFINITY) return a;
   return MS{a.m, a.s + __expf(x - a.m)};
 }
+template <int CTRL>
+__device__ __forceinline__ MS ms_dpp(MS v) {
+  return ms_comb(v, MS{dpp_f<CTRL>(v.m), dpp_f<CTRL>(v.s)});
+}
+// The pair over the wave through the DPP network (wave.h), every lane.
 __device__ __forceinline__ MS wave_ms(MS v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-    MS o{__shfl_xor(v.m, off, 64), __shfl_xor(v.s, off, 64)};
-    v = ms_comb(v, o);
-  }
-  return v;
+  v = ms_dpp<kDppXor1>(v);
+  v = ms_dpp<kDppXor2>(v);
+  v = ms_dpp<kDppRor4>(v);
+  v = ms_dpp<kDppRor8>(v);
+  const MS a = ms_comb(MS{lane_f(v.m, 0), lane_f(v.s, 0)}, MS{lane_f(v.m, 16), lane_f(v.s, 16)});
+  const MS b = ms_comb(MS{lane_f(v.m, 32), lane_f(v.s, 32)}, MS{lane_f(v.m, 48), lane_f(v.s, 48)});
+  return ms_comb(a, b);
 }
 
 // Calls f(index, value) for every element of row[0..n) with 128-bit loads
@@ -637,9 +633,10 @@ __global__ __launch_bounds__(64 * kLnBwdWaves) void k_ln_bwd_wave(const float* _
   const float inv_n = 1.0f / (float)cols;
   int64_t r_beg = (int64_t)blockIdx.x * rpb;
   int64_t r_end = r_beg + rpb < rows ? r_beg + rpb : rows;
-  // four rows per wave per step: all four rows' loads are issued before any
-  // row's reductions
-  constexpr int kPair = 4;
+  // rows per wave per step (four at GPT-2's 768-wide rows, fewer for wider
+  // rows so the registers hold them): every row's loads are issued before
+  // any row's reductions
+  constexpr int kPair = V4 <= 3 ? 4 : (V4 <= 6 ? 2 : 1);
   constexpr int kStep = NW;
   for (int64_t r0 = r_beg + w; r0 < r_end; r0 += kStep * kPair) {
     float4 gv[kPair][V4], xh[kPair][V4];

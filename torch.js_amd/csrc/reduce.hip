@@ -17,6 +17,7 @@
 // split point and combine order is fixed, so results are deterministic.
 
 #include "colsum.h"
+#include "wave.h"
 
 #include <float.h>
 
@@ -42,10 +43,14 @@ __device__ __forceinline__ float rcomb(float a, float b) {
 }
 
 template <int OP>
+struct RComb {
+  __device__ __forceinline__ float operator()(float a, float b) const { return rcomb<OP>(a, b); }
+};
+
+// The combination over the wave through the DPP network (wave.h).
+template <int OP>
 __device__ __forceinline__ float wave_reduce(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v = rcomb<OP>(v, __shfl_xor(v, off, 64));
-  return v;
+  return wave_reduce_dpp(v, RComb<OP>{});
 }
 
 // Block-wide reduce of one value per lane; result valid in every lane.
