@@ -76,12 +76,10 @@ def hbm_bytes_per_step(b, t, nparams, distinct_ids):
                           2 * LAYERS * tok * D * f,
         # AdamW: read p, g, m, v; write p, m, v
         "adam": 7 * nparams * f,
-        # embedding backward, both tables: wte reads the token rows of dout
-        # and adds them into its distinct rows of the tied head gradient
-        # (read + write each); wpe reads the batch-summed [T, D] gradient
-        # and writes its T rows (read + write into the zeroed table); ids
-        "embedding_bwd": (tok * D * f + 2 * distinct_ids * D * f + tok * 4) +
-                         (t * D * f + 2 * t * D * f + t * 4),
+        # embedding backward, both tables in one launch: dout read once, the
+        # token table's distinct rows of the tied head gradient read and
+        # written, the ids read, the position table's T rows written
+        "embedding_bwd": tok * D * f + 2 * distinct_ids * D * f + tok * 4 + t * D * f,
     }
 
 

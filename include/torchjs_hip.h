@@ -538,6 +538,27 @@ int tjh_embedding_forward(const float* weight, int64_t num, int64_t dim,
 int tjh_embedding_backward(const float* dout, const int32_t* ids,
                            int64_t n, int64_t dim, float* dweight,
                            int64_t num, int accumulate);
+/* A token embedding plus a position embedding over [batch, T] ids, as a
+ * transformer's input is built from two Embedding lookups and an add
+ * (src/nn/embedding.ts:25-101 twice, then Tensor.add, Tensor.ts:3409-3466):
+ * out[b,t,:] = weight[clamp(ids[b,t])] + pos_weight[pos0 + t], with
+ * pos0 + T <= num_pos.  The sum is the same float add as the two lookups
+ * followed by the add. */
+int tjh_embedding_pos_forward(const float* weight, int64_t num, int64_t dim,
+                              const int32_t* ids, int64_t batch, int64_t T,
+                              const float* pos_weight, int64_t num_pos,
+                              int64_t pos0, float* out);
+/* Both tables' gradients of tjh_embedding_pos_forward in one launch: dweight
+ * as tjh_embedding_backward over the batch * T ids, and dpos[pos0 + t,:]
+ * (+)= dout[0,t,:] + dout[1,t,:] + ... in batch order (the embedding
+ * backward's rule for ids pos0 + t repeated per batch item; rows outside
+ * [pos0, pos0 + T) are zeroed unless acc_pos).  Either table may be NULL
+ * (no gradient wanted). */
+int tjh_embedding_pos_backward(const float* dout, const int32_t* ids,
+                               int64_t batch, int64_t T, int64_t dim,
+                               float* dweight, int64_t num, int accumulate,
+                               float* dpos, int64_t num_pos, int64_t pos0,
+                               int acc_pos);
 /* x viewed [outer, src_len, inner]; out [outer, n_idx, inner] =
  * x[:, idx[j], :] (index_select.wgsl:20-55).  Valid indices are
  * 0 <= idx[j] < src_len, PyTorch's contract for index_select: the host

@@ -498,6 +498,74 @@ def test_embedding(torch, V, D, n):
     assert np.array_equal(wt.grad.numpy(), got)
 
 
+@pytest.mark.parametrize("V,P,D,B,T,pos0", [(50257, 1024, 768, 8, 1024, 0), (97, 16, 64, 2, 16, 0),
+                                              (211, 64, 128, 3, 40, 7), (30, 9, 6, 4, 5, 2),
+                                              (1000, 1200, 768, 80, 1024, 100),
+                                              (13, 5, 4, 1, 1, 4)])
+def test_embedding_pos_against_oracle(torch, V, P, D, B, T, pos0):
+    """F._embedding_pos: wte[ids] + wpe[pos0 + t] and both gradients in one
+    launch.  The forward equals the two lookups and the add bit for bit; the
+    token table's gradient is np.add.at's (float32, position order) bit for
+    bit; each position row is its batch items' rows added in batch order
+    (float32, exactly), rows outside [pos0, pos0 + T) zero; both against the
+    oracle.  Widths not divisible by 4 take the scalar path, 80 x 1024 ids
+    the sorting path for the token table."""
+    r = np.random.default_rng(V + P + D + B)
+    w = f32(r.standard_normal((V, D)))
+    wp = f32(r.standard_normal((P, D)))
+    ids = r.integers(0, V, (B, T)).astype(np.int32)
+    ids[0, : T // 2] = ids[0, 0]
+    wt = torch.tensor(w, requires_grad=True)
+    wpt = torch.tensor(wp, requires_grad=True)
+    out = torch.F._embedding_pos(torch.tensor(ids), wt, wpt, pos0)
+    pos = pos0 + np.arange(T)
+    want = w[ids] + wp[pos][None]
+    assert np.array_equal(out.numpy(), want)  # the same float add
+    g = f32(r.standard_normal((B, T, D)))
+    out.backward(torch.tensor(g))
+    tok32 = np.zeros((V, D), np.float32)
+    np.add.at(tok32, ids.reshape(-1), g.reshape(-1, D))
+    assert np.array_equal(wt.grad.numpy(), tok32)
+    pos32 = np.zeros((P, D), np.float32)
+    for b in range(B):
+        pos32[pos] += g[b]
+    assert np.array_equal(wpt.grad.numpy(), pos32)
+    check_floor(wt.grad.numpy(), ops.embedding_backward(g.reshape(-1, D), ids.reshape(-1), V), tok32)
+    check_floor(wpt.grad.numpy(),
+                ops.embedding_backward(g.reshape(-1, D), np.tile(pos, B), P), pos32)
+
+
+def test_embedding_pos_one_table_and_tied(torch):
+    """Only the position table wanting a gradient (the token table frozen),
+    and a token table tied to a Linear that ran after it: its rows are added
+    into that layer's weight gradient in place, as embedding() does."""
+    r = np.random.default_rng(3)
+    V, P, D, B, T = 211, 64, 128, 3, 64
+    w = f32(r.standard_normal((V, D)) * 0.1)
+    wp = f32(r.standard_normal((P, D)))
+    ids = r.integers(0, V, (B, T)).astype(np.int32)
+    g = f32(r.standard_normal((B, T, D)))
+    wt = torch.tensor(w)
+    wpt = torch.tensor(wp, requires_grad=True)
+    torch.F._embedding_pos(torch.tensor(ids), wt, wpt).backward(torch.tensor(g))
+    assert wt.grad is None
+    assert np.array_equal(wpt.grad.numpy(), g.sum(0, dtype=np.float32) if B == 1 else
+                          (g[0] + g[1]) + g[2])
+    wt = torch.tensor(w, requires_grad=True)
+    x = torch.F._embedding_pos(torch.tensor(ids), wt, torch.tensor(wp))
+    logits = torch.F.linear(x, wt)
+    gl = f32(r.standard_normal((B, T, V)))
+    logits.backward(torch.tensor(gl))
+    x64 = w[ids].astype(np.float64) + wp[np.arange(T)][None]
+    head = gl.reshape(-1, V).T.astype(np.float64) @ x64.reshape(-1, D)
+    dx = gl.reshape(-1, V).astype(np.float64) @ w.astype(np.float64)
+    want = head + ops.embedding_backward(dx, ids.reshape(-1), V)
+    x32 = (w[ids] + wp[np.arange(T)][None]).reshape(-1, D)
+    ref32 = gl.reshape(-1, V).T @ x32
+    np.add.at(ref32, ids.reshape(-1), gl.reshape(-1, V) @ w)
+    check_floor(wt.grad.numpy(), want, ref32)
+
+
 @pytest.mark.parametrize("V,D,n", [(50257, 768, 8192), (1024, 768, 1024), (40, 5, 3000),
                                    (600, 8, 70000)])
 def test_embedding_backward_accumulates_in_position_order(torch, V, D, n):

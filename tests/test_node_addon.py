@@ -16,7 +16,8 @@ EXPORTS = ["init", "deviceInfo", "malloc", "h2d", "d2h", "d2hAsync", "synchroniz
            "memoryStats", "emptyCache", "fill", "random", "copyStrided", "unary",
            "unaryBackward", "binary", "scalar", "reduce", "softmaxForward", "softmaxBackward",
            "crossEntropyForward", "crossEntropyBackward", "layerNormForward",
-           "layerNormBackward", "layerNormBackwardRes", "layerNormBackwardNoalloc", "flushDeferred", "embeddingForward", "embeddingBackward", "gemm", "gemmAct", "gemmCe", "crossEntropyRowScale",
+           "layerNormBackward", "layerNormBackwardRes", "layerNormBackwardNoalloc", "flushDeferred", "embeddingForward", "embeddingBackward",
+           "embeddingPosForward", "embeddingPosBackward", "gemm", "gemmAct", "gemmCe", "crossEntropyRowScale",
            "sdpaForward",
            "sdpaBackward", "adamStep", "version", "isInitialized", "deviceCount", "free",
            "resetPeak", "d2d", "kprofEnable", "kprofFilter", "kprofReset", "kprofQuery",

@@ -150,6 +150,10 @@ SIGNATURES = {
                                         c_i64, c_i64, c_int],
     "tjh_embedding_forward": [c_vp, c_i64, c_i64, c_vp, c_i64, c_vp],
     "tjh_embedding_backward": [c_vp, c_vp, c_i64, c_i64, c_vp, c_i64, c_int],
+    "tjh_embedding_pos_forward": [c_vp, c_i64, c_i64, c_vp, c_i64, c_i64, c_vp, c_i64, c_i64,
+                                  c_vp],
+    "tjh_embedding_pos_backward": [c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_i64, c_int, c_vp,
+                                   c_i64, c_i64, c_int],
     "tjh_index_select": [c_vp, c_i64, c_i64, c_i64, c_vp, c_i64, c_vp],
     "tjh_index_add": [c_vp, c_i64, c_i64, c_i64, c_vp, c_i64, c_vp],
     "tjh_gather": [c_vp, c_i64, c_i64, c_i64, c_vp, c_i64, c_vp],

@@ -50,6 +50,34 @@ __global__ __launch_bounds__(kBlock) void k_emb_fwd(const float* __restrict__ w,
   }
 }
 
+// out[p] = w[ids[p]] + wp[pos0 + p mod T]: the sum of a token and a
+// position embedding, one wave per token row.
+template <bool VEC>
+__global__ __launch_bounds__(kBlock) void k_emb_pos_fwd(const float* __restrict__ w, int64_t num,
+                                                        int64_t dim,
+                                                        const int32_t* __restrict__ ids, int64_t n,
+                                                        const float* __restrict__ wp,
+                                                        int64_t num_pos, int64_t pos0, int64_t T,
+                                                        float* __restrict__ out) {
+  int64_t t = (int64_t)blockIdx.x * (kBlock / 64) + (threadIdx.x >> 6);
+  int lane = threadIdx.x & 63;
+  if (t >= n) return;
+  const float* src = w + clamp_id(ids[t], num) * dim;
+  const float* psrc = wp + clamp_id((int32_t)(pos0 + t % T), num_pos) * dim;
+  float* dst = out + t * dim;
+  if (VEC) {
+    const float4* s4 = reinterpret_cast<const float4*>(src);
+    const float4* p4 = reinterpret_cast<const float4*>(psrc);
+    float4* d4 = reinterpret_cast<float4*>(dst);
+    for (int64_t i = lane; i < dim / 4; i += 64) {
+      const float4 a = s4[i], b = p4[i];
+      d4[i] = make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+    }
+  } else {
+    for (int64_t i = lane; i < dim; i += 64) dst[i] = src[i] + psrc[i];
+  }
+}
+
 // ------------------------------------------------------------ bitonic sort
 
 __global__ __launch_bounds__(kBlock) void k_make_keys(const int32_t* __restrict__ ids, int64_t n,
@@ -127,10 +155,12 @@ struct EmbUnit<false> {
   static __device__ __forceinline__ void add(T& a, const T& b) { a += b; }
 };
 
+// The rows [blk * span, ...) of the table, owned by one workgroup.
 template <bool VEC>
-__global__ __launch_bounds__(kOwnThreads) void k_emb_bwd_owned(
-    const int32_t* __restrict__ ids, int n, int ids_vec, int num, int span, int span_bits,
-    const float* __restrict__ dout, int units, float* __restrict__ dw, int accumulate) {
+__device__ __forceinline__ void emb_owned_body(
+    int blk, const int32_t* __restrict__ ids, int n, int ids_vec, int num, int span,
+    int span_bits, const float* __restrict__ dout, int units, float* __restrict__ dw,
+    int accumulate) {
   typedef EmbUnit<VEC> U;
   typedef typename U::T T;
   __shared__ uint32_t lpos[kOwnCap];     // list: positions, in position order
@@ -140,7 +170,7 @@ __global__ __launch_bounds__(kOwnThreads) void k_emb_bwd_owned(
   __shared__ uint32_t rows[kOwnMaxSpan]; // the rows to write, in order
   __shared__ uint32_t wcnt[kOwnSub * kOwnWaves];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int lo = (int)blockIdx.x * span;
+  const int lo = blk * span;
   const int nrows = num - lo < span ? num - lo : span;  // >= 1 by the grid
   const T* __restrict__ src = reinterpret_cast<const T*>(dout);
   T* __restrict__ dst = reinterpret_cast<T*>(dw);
@@ -312,6 +342,79 @@ __global__ __launch_bounds__(kOwnThreads) void k_emb_bwd_owned(
     __syncthreads();  // the LDS lists are rebuilt by the next chunk
     if (scan >= n) break;
   }
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(kOwnThreads) void k_emb_bwd_owned(
+    const int32_t* __restrict__ ids, int n, int ids_vec, int num, int span, int span_bits,
+    const float* __restrict__ dout, int units, float* __restrict__ dw, int accumulate) {
+  emb_owned_body<VEC>((int)blockIdx.x, ids, n, ids_vec, num, span, span_bits, dout, units, dw,
+                      accumulate);
+}
+
+// Rows of a position table [num_pos, units] whose ids are pos0 + t for the
+// positions t of a [batch, T] gradient: row pos0 + t is its prior value (or
+// zero) plus dout[b][t] for b = 0, 1, ... in that order -- the embedding
+// backward's rule (rows summed in increasing position order) for the ids
+// pos0 + (p mod T).  Rows outside [pos0, pos0 + T) are zeroed when not
+// accumulating.  Work item i = (row, unit); four items per thread with the
+// loads of all four issued before their sums.
+template <bool VEC>
+__device__ __forceinline__ void emb_pos_body(int pg, int npg, const float* __restrict__ dout,
+                                             int batch, int T, int units,
+                                             float* __restrict__ dwp, int num_pos, int pos0,
+                                             int accumulate) {
+  typedef EmbUnit<VEC> U;
+  typedef typename U::T E;
+  const E* __restrict__ src = reinterpret_cast<const E*>(dout);
+  E* __restrict__ dst = reinterpret_cast<E*>(dwp);
+  const int64_t items = (int64_t)num_pos * units;
+  const int64_t stride = (int64_t)npg * kOwnThreads;
+  const int64_t bstride = (int64_t)T * units;
+  constexpr int kPer = 4;
+  for (int64_t i0 = (int64_t)pg * kOwnThreads + threadIdx.x; i0 < items; i0 += stride * kPer) {
+    E s[kPer];
+    int64_t base[kPer];
+    bool in[kPer], live[kPer];
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      const int64_t i = i0 + u * stride;
+      live[u] = i < items;
+      const int64_t r = live[u] ? i / units : 0;
+      const int64_t t = r - pos0;
+      in[u] = live[u] && t >= 0 && t < T;
+      base[u] = in[u] ? t * units + (i - r * units) : 0;
+      s[u] = (live[u] && accumulate) ? dst[i] : U::zero();
+    }
+    for (int b = 0; b < batch; ++b) {
+      E v[kPer];
+#pragma unroll
+      for (int u = 0; u < kPer; ++u) v[u] = in[u] ? src[b * bstride + base[u]] : U::zero();
+#pragma unroll
+      for (int u = 0; u < kPer; ++u)
+        if (in[u]) U::add(s[u], v[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < kPer; ++u)
+      if (live[u] && (in[u] || !accumulate)) dst[i0 + u * stride] = s[u];
+  }
+}
+
+// One launch for the gradients of x = wte[ids] + wpe[pos0 + t]: workgroups
+// [0, tok_groups) own row ranges of wte (emb_owned_body), the rest write
+// wpe (emb_pos_body).
+template <bool VEC>
+__global__ __launch_bounds__(kOwnThreads) void k_emb_bwd_tok_pos(
+    const int32_t* __restrict__ ids, int n, int ids_vec, int num, int span, int span_bits,
+    const float* __restrict__ dout, int units, float* __restrict__ dw, int accumulate,
+    int tok_groups, int batch, int T, float* __restrict__ dwp, int num_pos, int pos0,
+    int acc_pos) {
+  if ((int)blockIdx.x < tok_groups)
+    emb_owned_body<VEC>((int)blockIdx.x, ids, n, ids_vec, num, span, span_bits, dout, units, dw,
+                        accumulate);
+  else
+    emb_pos_body<VEC>((int)blockIdx.x - tok_groups, (int)gridDim.x - tok_groups, dout, batch, T,
+                      units, dwp, num_pos, pos0, acc_pos);
 }
 
 constexpr int kSortChunk = 2048;  // elements per LDS stage (1024 lanes x 2)
@@ -625,6 +728,76 @@ int tjh_embedding_backward(const float* dout, const int32_t* ids, int64_t n, int
     tjh_launch(k_emb_bwd_runs<false>, dim3(g), dim3(kBlock), 0, stream(), keys, n, dout, dim,
                dweight, 1);
   return check_launch("embedding_backward");
+}
+
+int tjh_embedding_pos_forward(const float* weight, int64_t num, int64_t dim, const int32_t* ids,
+                              int64_t batch, int64_t T, const float* pos_weight,
+                              int64_t num_pos, int64_t pos0, float* out) {
+  TJH_REQUIRE_INIT();
+  TJH_ARG(num > 0 && num_pos > 0 && dim >= 0 && batch >= 0 && T >= 0 && pos0 >= 0,
+          "tjh_embedding_pos_forward: bad sizes");
+  TJH_ARG(pos0 + T <= num_pos, "tjh_embedding_pos_forward: positions [%lld, %lld) past the "
+          "%lld-row position table", (long long)pos0, (long long)(pos0 + T), (long long)num_pos);
+  const int64_t n = batch * T;
+  if (n == 0 || dim == 0) return TJH_OK;
+  TJH_ARG(weight && pos_weight && ids && out, "tjh_embedding_pos_forward: NULL pointer");
+  KernelScope ks("embedding_fwd");
+  const unsigned g = (unsigned)cdiv(n, kBlock / 64);
+  const bool vec = dim % 4 == 0 && aligned16(weight) && aligned16(pos_weight) && aligned16(out);
+  if (vec)
+    tjh_launch(k_emb_pos_fwd<true>, dim3(g), dim3(kBlock), 0, stream(), weight, num, dim, ids, n,
+               pos_weight, num_pos, pos0, T, out);
+  else
+    tjh_launch(k_emb_pos_fwd<false>, dim3(g), dim3(kBlock), 0, stream(), weight, num, dim, ids,
+               n, pos_weight, num_pos, pos0, T, out);
+  return check_launch("embedding_pos_forward");
+}
+
+int tjh_embedding_pos_backward(const float* dout, const int32_t* ids, int64_t batch, int64_t T,
+                               int64_t dim, float* dweight, int64_t num, int accumulate,
+                               float* dpos, int64_t num_pos, int64_t pos0, int acc_pos) {
+  TJH_REQUIRE_INIT();
+  TJH_ARG(num > 0 && num_pos > 0 && dim >= 0 && batch >= 0 && T >= 0 && pos0 >= 0,
+          "tjh_embedding_pos_backward: bad sizes");
+  TJH_ARG(pos0 + T <= num_pos, "tjh_embedding_pos_backward: positions past the table");
+  const int64_t n = batch * T;
+  TJH_ARG(n < (int64_t(1) << 31) && num_pos * dim < (int64_t(1) << 31),
+          "tjh_embedding_pos_backward: too many elements");
+  if (dim == 0) return TJH_OK;
+  const bool vec = dim % 4 == 0 && aligned16(dout) && (!dweight || aligned16(dweight)) &&
+                   (!dpos || aligned16(dpos));
+  const int64_t units = vec ? dim / 4 : dim;
+  int64_t span = cdiv(num, (int64_t)kOwnGroups);
+  if (span > kOwnMaxSpan) span = kOwnMaxSpan;
+  int64_t tok_groups = cdiv(num, span);
+  const bool owned = n > 0 && n <= kOwnMaxN && tok_groups * n <= kOwnMaxScan &&
+                     num < (int64_t(1) << 31) && span * units < (int64_t(1) << 31);
+  if (dweight && !owned) {
+    // a long id list: the sorting path for the token table, then the
+    // position rows alone
+    const int rc = tjh_embedding_backward(dout, ids, n, dim, dweight, num, accumulate);
+    if (rc != TJH_OK) return rc;
+  }
+  if (!dweight || !owned) tok_groups = 0;
+  int64_t pos_groups = 0;
+  if (dpos) pos_groups = cdiv(num_pos * units, (int64_t)kOwnThreads * 4);
+  if (pos_groups > 1024) pos_groups = 1024;
+  if (tok_groups + pos_groups == 0) return TJH_OK;
+  TJH_ARG(!tok_groups || ids, "tjh_embedding_pos_backward: NULL ids");
+  int span_bits = 0;
+  while ((int64_t(1) << span_bits) < span) ++span_bits;
+  const int ids_vec = ((uintptr_t)ids & 15) == 0;
+  KernelScope ks("embedding_bwd");
+  const dim3 grid((unsigned)(tok_groups + pos_groups));
+  if (vec)
+    tjh_launch(k_emb_bwd_tok_pos<true>, grid, dim3(kOwnThreads), 0, stream(), ids, (int)n,
+               ids_vec, (int)num, (int)span, span_bits, dout, (int)units, dweight, accumulate,
+               (int)tok_groups, (int)batch, (int)T, dpos, (int)num_pos, (int)pos0, acc_pos);
+  else
+    tjh_launch(k_emb_bwd_tok_pos<false>, grid, dim3(kOwnThreads), 0, stream(), ids, (int)n,
+               ids_vec, (int)num, (int)span, span_bits, dout, (int)units, dweight, accumulate,
+               (int)tok_groups, (int)batch, (int)T, dpos, (int)num_pos, (int)pos0, acc_pos);
+  return check_launch("embedding_pos_backward");
 }
 
 int tjh_index_select(const float* x, int64_t outer, int64_t src_len, int64_t inner,

@@ -347,6 +347,51 @@ def embedding(input, weight):
     return _record(out, "Embedding", [weight], bwd, acc_slot=0)
 
 
+def _embedding_pos(input, weight, pos_weight, pos0=0):
+    """embedding(input, weight) + embedding(pos0 + arange(T), pos_weight)
+    for input [B, T] ids -- a transformer's token plus position embedding
+    (two nn.Embedding lookups and an add, src/nn/embedding.ts:25-101) in
+    one kernel, the same float add.  The backward gives both tables their
+    gradients in one launch: the token rows as embedding() does (added into
+    a pending gradient in place, as for a table tied to the LM head) and the
+    position rows as the sum over the batch in batch order."""
+    ids = input
+    if not isinstance(ids, Tensor):
+        from .tensor import tensor as _tensor
+        ids = _tensor(np.asarray(ids, dtype=np.int32), dtype="int32")
+    if ids.dtype != "int32":
+        ids = ids.to("int32")
+    if ids.ndim != 2:
+        raise RuntimeError("_embedding_pos: ids must be [batch, T]")
+    ids = ids.contiguous()
+    B, T = ids.shape
+    V, D = weight.shape
+    P, D2 = pos_weight.shape
+    if D2 != D:
+        raise RuntimeError("_embedding_pos: tables of widths %d and %d" % (D, D2))
+    if pos0 < 0 or pos0 + T > P:
+        raise RuntimeError("_embedding_pos: positions [%d, %d) past the %d-row table"
+                           % (pos0, pos0 + T, P))
+    w = weight.detach().contiguous()
+    wp = pos_weight.detach().contiguous()
+    out = empty((B, T, D))
+    L.check(L.lib().tjh_embedding_pos_forward(w.data_ptr(), V, D, ids.data_ptr(), B, T,
+                                              wp.data_ptr(), P, pos0, out.data_ptr()),
+            "embedding_pos")
+    rw, rp = weight.requires_grad, pos_weight.requires_grad
+
+    def bwd(g, pending=None):
+        g = g.contiguous()
+        dw = (pending if pending is not None else empty((V, D))) if rw else None
+        dp = empty((P, D)) if rp else None
+        L.check(L.lib().tjh_embedding_pos_backward(
+            g.data_ptr(), ids.data_ptr(), B, T, D, dw.data_ptr() if dw is not None else None, V,
+            1 if pending is not None else 0, dp.data_ptr() if dp is not None else None, P, pos0,
+            0), "embedding_pos_backward")
+        return [dw, dp]
+    return _record(out, "EmbeddingPos", [weight, pos_weight], bwd, acc_slot=0)
+
+
 def linear(x, weight, bias=None):
     """y = x W^T + b (src/nn/linear.ts:43-66) as ONE GEMM with the bias in
     the epilogue and W^T read in place; backward dx = g W, and dW = g^T x

@@ -665,6 +665,31 @@ static napi_value js_emb_backward(napi_env env, napi_callback_info info) {
   return undef(env);
 }
 
+/* embeddingPosForward(weight, num, dim, ids, batch, T, posWeight, numPos, pos0, out) */
+static napi_value js_emb_pos_forward(napi_env env, napi_callback_info info) {
+  napi_value a[10];
+  if (!get_args(env, info, 10, a)) return NULL;
+  CHECK_RC(tjh_embedding_pos_forward((const float*)ptr(env, a[0]), i64(env, a[1]),
+                                     i64(env, a[2]), (const int32_t*)ptr(env, a[3]),
+                                     i64(env, a[4]), i64(env, a[5]), (const float*)ptr(env, a[6]),
+                                     i64(env, a[7]), i64(env, a[8]), (float*)ptr(env, a[9])));
+  return undef(env);
+}
+
+/* embeddingPosBackward(dout, ids, batch, T, dim, dweight, num, accumulate, dpos, numPos, pos0,
+ * accPos); a table passed as null gets no gradient */
+static napi_value js_emb_pos_backward(napi_env env, napi_callback_info info) {
+  napi_value a[12];
+  if (!get_args(env, info, 12, a)) return NULL;
+  CHECK_RC(tjh_embedding_pos_backward((const float*)ptr(env, a[0]),
+                                      (const int32_t*)ptr(env, a[1]), i64(env, a[2]),
+                                      i64(env, a[3]), i64(env, a[4]), (float*)ptr(env, a[5]),
+                                      i64(env, a[6]), (int)i64(env, a[7]),
+                                      (float*)ptr(env, a[8]), i64(env, a[9]), i64(env, a[10]),
+                                      (int)i64(env, a[11])));
+  return undef(env);
+}
+
 /* gemm(transA, transB, M, N, K, alpha, A, lda, sA, B, ldb, sB, beta, C, ldc, sC, batch, bias, biasMode) */
 static napi_value js_gemm(napi_env env, napi_callback_info info) {
   napi_value a[19];
@@ -1228,7 +1253,8 @@ static napi_value init_module(napi_env env, napi_value exports) {
       FN("layerNormBackwardRes", js_ln_backward_res),
       FN("layerNormBackwardNoalloc", js_ln_backward_noalloc),
       FN("flushDeferred", js_flush_deferred), FN("embeddingForward", js_emb_forward),
-      FN("embeddingBackward", js_emb_backward), FN("gemm", js_gemm), FN("gemmAct", js_gemm_act),
+      FN("embeddingBackward", js_emb_backward), FN("embeddingPosForward", js_emb_pos_forward),
+      FN("embeddingPosBackward", js_emb_pos_backward), FN("gemm", js_gemm), FN("gemmAct", js_gemm_act),
       FN("gemmCe", js_gemm_ce), FN("crossEntropyRowScale", js_ce_row_scale),
       FN("sdpaForward", js_sdpa_forward), FN("sdpaBackward", js_sdpa_backward),
       FN("adamStep", js_adam_step), FN("adamStepDev", js_adam_step_dev), FN("isInitialized", js_is_initialized),

@@ -163,19 +163,26 @@ class GPT2(nn.Module):
     def __init__(self, vocab=50257, ctx=1024, d=768, heads=12, layers=12, fused=True):
         super().__init__()
         self.vocab, self.ctx = vocab, ctx
+        self.fused = fused
         self.wte = nn.Embedding(vocab, d)
         self.wpe = nn.Embedding(ctx, d)
         self.h = nn.ModuleList([Block(d, heads, fused) for _ in range(layers)])
         self.ln_f = nn.LayerNorm(d)
 
     def forward(self, ids):
-        B, T = ids.shape
-        pos = arange(T, dtype="int32")
-        x = self.wte(ids) + self.wpe(pos)
+        x = self._embed(ids, 0)
         for blk in self.h:
             x = blk(x)
         x = self.ln_f(x)
         return F.linear(x, self.wte.weight)
+
+    def _embed(self, ids, pos0):
+        """wte(ids) + wpe(positions pos0 .. pos0 + T - 1); with `fused` one
+        kernel each way (F._embedding_pos), else the public lookups and +."""
+        if self.fused:
+            return F._embedding_pos(ids, self.wte.weight, self.wpe.weight, pos0)
+        T = ids.shape[1]
+        return self.wte(ids) + self.wpe(arange(pos0, pos0 + T, dtype="int32"))
 
     def loss(self, ids, targets):
         logits = self(ids)
@@ -189,9 +196,7 @@ class GPT2(nn.Module):
         """Logits of positions [pos, pos + T) of ids [B, T], the keys and
         values of earlier positions read from (and these appended to) the
         cache."""
-        B, T = ids.shape
-        p = arange(pos, pos + T, dtype="int32")
-        x = self.wte(ids) + self.wpe(p)
+        x = self._embed(ids, pos)
         for i, blk in enumerate(self.h):
             x = blk.forward_cached(x, cache, i, pos)
         x = self.ln_f(x)
