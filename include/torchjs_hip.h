@@ -369,9 +369,11 @@ typedef struct {
  * output element e is r[result] after the last one.  Every instruction
  * computes exactly what the single-op entry points compute.  result2, when
  * not 0, names a second value r[result2 - 1] that tjh_expr_colsum2 also
- * writes out (two values of one chain, computed from the same loads). */
+ * writes out (two values of one chain, computed from the same loads);
+ * result3, when not 0, a third value r[result3 - 1] that tjh_expr_colsum3
+ * also sums over the same rows. */
 typedef struct {
-  int32_t n_ins, n_leaves, result, result2;
+  int32_t n_ins, n_leaves, result, result2, result3, pad;
   tjh_expr_ins ins[TJH_EXPR_MAX_INS];
   const float* leaf[TJH_EXPR_MAX_LEAVES];
   int64_t period[TJH_EXPR_MAX_LEAVES];
@@ -394,6 +396,14 @@ int tjh_expr_colsum(const tjh_expr* prog, int64_t outer, int64_t r, int64_t inne
  * one read of the chain's inputs. */
 int tjh_expr_colsum2(const tjh_expr* prog, int64_t outer, int64_t r, int64_t inner,
                      float* out, float* values, float* values2);
+/* tjh_expr_colsum2 that also sums the program's third value
+ * (prog->result3 != 0) over the same rows into out3 [outer, inner], with
+ * the same partition and order (bit-identical to summing that value
+ * alone): a forward column sum left pending until the backward pass reads
+ * the same inputs (the loss of GELU(x + b) * y summed over rows, from the
+ * pass that forms x's and y's gradients).  Needs 2 * outer <= 64. */
+int tjh_expr_colsum3(const tjh_expr* prog, int64_t outer, int64_t r, int64_t inner,
+                     float* out, float* values, float* values2, float* out3);
 /* Validates `prog` and compiles the kernel tjh_expr_eval (colsum == 0) or
  * tjh_expr_colsum (colsum != 0) would run for n elements, without a
  * device (kernels are compiled at run time, once per program shape). */

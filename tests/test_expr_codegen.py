@@ -232,6 +232,36 @@ def test_builder_second_value(lazy_on):
     _compile(prog, 128, 1)
 
 
+def test_builder_three_values(lazy_on):
+    """A backward column sum with its sibling gradient and a pending
+    forward column sum of the same inputs as one program: the chain's
+    loads and GELU-like subexpression shared by all three values, the
+    third value's register held, result3 set; the three-output
+    column-sum kernel compiles; a third result register never written is
+    rejected."""
+    rng = np.random.default_rng(10)
+    data = {}
+    S = (8, 16)
+    x = _leaf(S, 0x1000, data, rng)
+    y = _leaf(S, 0x2000, data, rng)
+    b = _leaf((16,), 0x3000, data, rng)
+    e = T._k_unary("exp", T._k_binary("add", x, b))
+    z = T._k_binary("mul", e, y)                       # the forward value
+    gx = T._k_binary("mul", T._k_scalar("mul", e, 0.5), y)
+    gy = T._k_scalar("mul", e, 0.5)
+    prog, _ = T._program(gx, gy, z)
+    assert prog.result2 > 0 and prog.result3 > 0
+    ops = [prog.ins[i].op for i in range(prog.n_ins)]
+    assert ops.count(L.EXPR_OP["load"]) == 3
+    assert ops.count(L.EXPR_OP["unary"]) == 1
+    X, Y, B = (data[p].astype(np.float64) for p in (0x1000, 0x2000, 0x3000))
+    np.testing.assert_allclose(_interpret(prog, S, data), 0.5 * np.exp(X + B) * Y, rtol=1e-12)
+    _compile(prog, 128, 1)
+    p = _prog([("load", 0, 0, 0, N, N, 0.0)], [(ALIGNED, "contig", 0)], 0)
+    p.result3 = 2
+    assert L.lib().tjh_expr_compile(ctypes.byref(p), 16, 1) == 1
+
+
 def test_builder_register_reuse_and_limits(lazy_on):
     rng = np.random.default_rng(6)
     data = {}

@@ -7,6 +7,8 @@ import sys
 import numpy as np
 import pytest
 
+from oracle import ops
+
 pytestmark = pytest.mark.gpu
 
 
@@ -55,8 +57,10 @@ def _rand(shape, seed, lo=-2.0, hi=2.0):
 
 def test_chain_fwd_bwd_bitwise_and_fused(torch, T, both):
     """The C2 chain: ((x + bias).gelu() * y).sum(0).mean(), forward and
-    backward, fused against op by op; with deferral the chain's forward is
-    one column-sum launch and no elementwise kernel writes an intermediate."""
+    backward, fused against op by op; with deferral the whole step is one
+    pass over x and y (the forward column sum rides along with x's and y's
+    gradients and the bias gradient) and no elementwise kernel writes an
+    intermediate."""
     R, C = 512, 2048
     xs, bs, ys = _rand((R, C), 1), _rand((C,), 2), _rand((R, C), 3, -1, 1)
 
@@ -78,7 +82,8 @@ def test_chain_fwd_bwd_bitwise_and_fused(torch, T, both):
         fams = dict((f, torch.hip.kernel_time(f)[0]) for f in torch.hip.kernel_families())
     finally:
         torch.hip.kernel_timing(False)
-    assert fams.get("expr_colsum", 0) >= 2, fams     # forward sum(0) and the bias gradient
+    assert fams.get("expr_colsum3", 0) == 1, fams    # sum(0) and the bias gradient, one pass
+    assert fams.get("expr_colsum", 0) == 0 and fams.get("expr", 0) == 0, fams
     assert fams.get("unary", 0) == 0 and fams.get("binary", 0) == 0, fams
 
 
@@ -120,11 +125,52 @@ def test_chain_sibling_gradients_in_one_pass(torch, T, extra):
     _same(runs[0], runs[1])
     assert not T._SIBLINGS
     if not extra:
-        # forward sum(0) and the backward's one pass, and fewer launches in all:
-        # y's gradient is not evaluated on its own
-        assert launches[0].get("expr_colsum", 0) == 2, launches[0]
+        # one pass for the forward sum(0) and the gradients, and fewer
+        # launches in all: y's gradient is not evaluated on its own
+        assert launches[0].get("expr_colsum3", 0) == 1, launches[0]
         assert launches[0].get("expr", 0) < launches[1].get("expr", 0), launches
         assert sum(launches[0].values()) < sum(launches[1].values()), launches
+
+
+@pytest.mark.parametrize("read", ["never", "before", "after", "write_first"])
+def test_deferred_forward_column_sum(torch, T, read):
+    """sum(0) of a deferred value stays deferred; the backward's column-sum
+    pass over the same inputs computes it (expr_colsum3), bit for bit what
+    the immediate sum gives, and a loss that is a deferred reduction is
+    evaluated by the end of backward().  Read before backward it is computed
+    on its own; an in-place write to an input first computes it from the
+    old values."""
+    R, C = 512, 2048
+    xs, bs, ys = _rand((R, C), 31), _rand((C,), 32), _rand((R, C), 33, -1, 1)
+
+    def run(defer):
+        T._DEFER_SUMS["on"] = defer
+        try:
+            x = torch.tensor(xs, requires_grad=True)
+            b = torch.tensor(bs, requires_grad=True)
+            y = torch.tensor(ys, requires_grad=True)
+            col = ((x + b).gelu() * y).sum(0)
+            loss = col.mean()
+            if defer:
+                assert T._is_lazy(col) and T._is_lazy(loss)
+            early = loss.numpy().copy() if read == "before" else None
+            if read == "write_first":
+                with torch.no_grad():
+                    y.fill_(0.5)  # the pending sum is computed from the old y first
+            else:
+                loss.backward()
+                assert not T._is_lazy(loss)  # evaluated by the end of the pass
+            out = [_np(loss), _np(col)]
+            if read != "write_first":
+                out += [_np(x.grad), _np(b.grad), _np(y.grad)]
+            if early is not None:
+                assert np.array_equal(early, out[0])
+            return out
+        finally:
+            T._DEFER_SUMS["on"] = True
+    _same(run(True), run(False))
+    want = (ops.gelu(xs.astype(np.float64) + bs) * ys).sum(0)
+    np.testing.assert_allclose(run(True)[1], want, rtol=1e-5, atol=1e-4)
 
 
 def test_deferred_gradient_shared_by_two_leaves(torch, T):

@@ -27,7 +27,7 @@ EXPORTS = ["init", "deviceInfo", "malloc", "h2d", "d2h", "d2hAsync", "synchroniz
            "scatterAdd", "oneHot", "oneHotI32", "nonzero", "conv2dForward", "conv2dForwardAct",
            "conv2dBackwardInput", "conv2dBackwardWeight", "conv2dBackwardWeightBias", "cast", "fillU8", "copyStridedU8",
            "triangle", "multinomial", "timerEnd", "timerRead", "rangePush", "rangePop",
-           "mark", "exprEval", "exprColsum", "exprColsum2", "exprCompile", "graphBegin", "graphEnd", "graphReplay",
+           "mark", "exprEval", "exprColsum", "exprColsum2", "exprColsum3", "exprCompile", "graphBegin", "graphEnd", "graphReplay",
            "graphDestroy", "adamStepDev"]
 HEADER = os.path.join(ROOT, "include", "torchjs_hip.h")
 SOURCE = os.path.join(ROOT, "torch.js_amd", "node", "torchjs_hip_napi.c")

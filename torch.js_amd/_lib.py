@@ -72,6 +72,7 @@ class ExprIns(ctypes.Structure):
 class Expr(ctypes.Structure):
     _fields_ = [("n_ins", ctypes.c_int32), ("n_leaves", ctypes.c_int32),
                 ("result", ctypes.c_int32), ("result2", ctypes.c_int32),
+                ("result3", ctypes.c_int32), ("pad", ctypes.c_int32),
                 ("ins", ExprIns * EXPR_MAX_INS),
                 ("leaf", ctypes.c_void_p * EXPR_MAX_LEAVES),
                 ("period", ctypes.c_int64 * EXPR_MAX_LEAVES),
@@ -128,6 +129,7 @@ SIGNATURES = {
     "tjh_graph_destroy": [c_int],
     "tjh_expr_colsum": [c_vp, c_i64, c_i64, c_i64, c_vp, c_vp],
     "tjh_expr_colsum2": [c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp],
+    "tjh_expr_colsum3": [c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp, c_vp],
     "tjh_expr_compile": [c_vp, c_i64, c_int],
     "tjh_argmax": [c_vp, c_i64, c_i64, c_i64, c_int, c_vp],
     "tjh_softmax_forward": [c_vp, c_i64, c_vp, c_i64, c_i64, c_i64, c_int],

@@ -63,6 +63,8 @@ int check_prog(const tjh_expr* P, int64_t n, const float* const* extra, int next
     return set_error(TJH_ERR_INVALID, "tjh_expr: result register %d", P->result), 0;
   if (P->result2 < 0 || P->result2 > NR)
     return set_error(TJH_ERR_INVALID, "tjh_expr: second result %d", P->result2), 0;
+  if (P->result3 < 0 || P->result3 > NR)
+    return set_error(TJH_ERR_INVALID, "tjh_expr: third result %d", P->result3), 0;
   bool vec = n % 4 == 0;
   for (int k = 0; k < P->n_leaves; ++k) {
     const int kind = P->kind[k];
@@ -101,6 +103,8 @@ int check_prog(const tjh_expr* P, int64_t n, const float* const* extra, int next
   if (!def(P->result)) return set_error(TJH_ERR_INVALID, "tjh_expr: result never written"), 0;
   if (P->result2 && !def(P->result2 - 1))
     return set_error(TJH_ERR_INVALID, "tjh_expr: second result never written"), 0;
+  if (P->result3 && !def(P->result3 - 1))
+    return set_error(TJH_ERR_INVALID, "tjh_expr: third result never written"), 0;
   for (int i = 0; i < nextra; ++i) vec = vec && (!extra[i] || aligned16(extra[i]));
   return vec ? 4 : 1;
 }
@@ -114,15 +118,21 @@ int grid_for(int64_t items) {
 
 // ------------------------------------------------------------ codegen
 
-enum Mode { kEval = 0, kColsum = 1 };
+enum Mode { kEval = 0, kColsum = 1, kColsum3 = 2 };
 
 // HIP source of the kernel for program P at width W.
 std::string generate(const tjh_expr* P, int W, Mode mode) {
   std::string s;
   char buf[256];
   s += "#include \"expr_jit.h\"\nusing namespace tjh::jit;\nnamespace {\nstruct F {\n";
-  snprintf(buf, sizeof buf,
-           "  __device__ __forceinline__ V<%d> operator()(const Args& a, long long e) const {\n", W);
+  if (mode == kColsum3)
+    snprintf(buf, sizeof buf,
+             "  __device__ __forceinline__ V<%d> operator()(const Args& a, long long e, V<%d>* c3) "
+             "const {\n", W, W);
+  else
+    snprintf(buf, sizeof buf,
+             "  __device__ __forceinline__ V<%d> operator()(const Args& a, long long e) const {\n",
+             W);
   s += buf;
   for (int k = 0; k < P->n_leaves; ++k) {
     snprintf(buf, sizeof buf, "    const V<%d> l%d = leaf<%d, %d>(a, %d, e);\n", W, k, W, P->kind[k], k);
@@ -166,11 +176,13 @@ std::string generate(const tjh_expr* P, int W, Mode mode) {
   if (P->result2)
     s += "    if (a.values2) store<" + std::to_string(W) + ">(a.values2 + e, " + reg[P->result2 - 1] +
          ");\n";
+  if (mode == kColsum3) s += "    *c3 = " + reg[P->result3 - 1] + ";\n";
   s += "    return " + reg[P->result] + ";\n  }\n};\n}  // namespace\n";
   snprintf(buf, sizeof buf,
            "extern \"C\" __global__ __launch_bounds__(%d) void tjh_expr_kernel(Args a) {\n"
            "  %s<%d>(F(), a);\n}\n",
-           kBlock, mode == kEval ? "eval_body" : "colsum_body", W);
+           kBlock, mode == kEval ? "eval_body" : (mode == kColsum ? "colsum_body" : "colsum3_body"),
+           W);
   s += buf;
   return s;
 }
@@ -235,6 +247,7 @@ std::string signature(const tjh_expr* P, int W, Mode mode) {
   k.push_back((char)P->n_leaves);
   k.push_back((char)P->result);
   k.push_back((char)P->result2);
+  k.push_back((char)P->result3);
   for (int i = 0; i < P->n_ins; ++i) {
     const tjh_expr_ins& in = P->ins[i];
     const char b[6] = {(char)in.op, (char)in.code, (char)in.dst, (char)in.a, (char)in.b, (char)in.c};
@@ -318,7 +331,8 @@ int tjh_expr_compile(const tjh_expr* prog, int64_t n, int colsum) {
   const int W = check_prog(prog, n, nullptr, 0);
   if (W == 0) return TJH_ERR_INVALID;
   std::string code;
-  return compile_code(generate(prog, W, colsum ? kColsum : kEval), &code);
+  const Mode m = !colsum ? kEval : (prog->result3 ? kColsum3 : kColsum);
+  return compile_code(generate(prog, W, m), &code);
 }
 
 int tjh_expr_colsum(const tjh_expr* prog, int64_t outer, int64_t r, int64_t inner, float* out,
@@ -328,12 +342,21 @@ int tjh_expr_colsum(const tjh_expr* prog, int64_t outer, int64_t r, int64_t inne
 
 int tjh_expr_colsum2(const tjh_expr* prog, int64_t outer, int64_t r, int64_t inner, float* out,
                      float* values, float* values2) {
+  return tjh_expr_colsum3(prog, outer, r, inner, out, values, values2, nullptr);
+}
+
+int tjh_expr_colsum3(const tjh_expr* prog, int64_t outer, int64_t r, int64_t inner, float* out,
+                     float* values, float* values2, float* out3) {
   TJH_REQUIRE_INIT();
   TJH_ARG(outer >= 0 && r >= 0 && inner >= 0, "tjh_expr_colsum: negative size");
   if (outer > kFinalMax || r < 64 || inner < 2)
     return set_error(TJH_ERR_UNSUPPORTED,
                      "tjh_expr_colsum: outer %lld <= %d, r %lld >= 64 and inner %lld >= 2 needed",
                      (long long)outer, kFinalMax, (long long)r, (long long)inner);
+  const bool third = prog && prog->result3 && out3;
+  if (third && 2 * outer > kFinalMax)
+    return set_error(TJH_ERR_UNSUPPORTED, "tjh_expr_colsum3: 2 * outer %lld > %d",
+                     (long long)(2 * outer), kFinalMax);
   const float* ex[2] = {values, values2};
   int W = check_prog(prog, outer * r * inner, ex, 2);
   if (W == 0) return TJH_ERR_INVALID;
@@ -341,16 +364,18 @@ int tjh_expr_colsum2(const tjh_expr* prog, int64_t outer, int64_t r, int64_t inn
   TJH_ARG(out != nullptr, "tjh_expr_colsum: NULL output");
   if (inner % 4) W = 1;
   hipFunction_t fn;
-  int rc = get_kernel(prog, W, kColsum, &fn);
+  int rc = get_kernel(prog, W, third ? kColsum3 : kColsum, &fn);
   if (rc != TJH_OK) return rc;
-  KernelScope ks("expr_colsum");
+  KernelScope ks(third ? "expr_colsum3" : "expr_colsum");
   // the partition of the unfused sum of the materialised (aligned) value
   int64_t nb = 0, rchunk = 0;
   colsum_plan(outer, r, inner, inner % 4 == 0, &nb, &rchunk);
-  Scratch part((size_t)(outer * nb * inner) * sizeof(float));
+  const int64_t per = outer * nb * inner;  // partial rows of one column sum
+  Scratch part((size_t)(third ? 2 * per : per) * sizeof(float));
   if (!part.ok()) return set_error(TJH_ERR_OOM, "tjh_expr_colsum: no scratch memory");
   jit::Args a = make_args(prog);
   a.out = part.as<float>();
+  a.out3 = third ? part.as<float>() + per : nullptr;
   a.values = values;
   a.values2 = prog->result2 ? values2 : nullptr;
   a.r = r;
@@ -364,8 +389,12 @@ int tjh_expr_colsum2(const tjh_expr* prog, int64_t outer, int64_t r, int64_t inn
   for (int64_t i = 0; i < outer; ++i) {
     parts[i] = part.as<float>() + i * nb * inner;
     outs[i] = out + i * inner;
+    if (third) {  // the third value's sums finish in the same launch
+      parts[outer + i] = a.out3 + i * nb * inner;
+      outs[outer + i] = out3 + i * inner;
+    }
   }
-  return colsum_final(parts, outs, (int)outer, nb, inner, 0, 1.0f);
+  return colsum_final(parts, outs, (int)(third ? 2 * outer : outer), nb, inner, 0, 1.0f);
 }
 
 }  // extern "C"

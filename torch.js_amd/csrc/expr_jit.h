@@ -25,6 +25,7 @@ struct Args {
   float* out;     // eval: the value; colsum: the partial rows
   float* values;  // colsum: the value too (may be null)
   float* values2; // colsum: the program's second value (may be null)
+  float* out3;    // colsum3: the partial rows of the third value's column sums
   long long n;    // eval: elements
   long long r, inner, rchunk;
 };
@@ -178,6 +179,46 @@ __device__ __forceinline__ void colsum_body(const F& f, const Args& a) {
 #pragma unroll
   for (int j = 0; j < W; ++j) s.x[j] = acc[j].s;
   store<W>(a.out + (o * nb + b) * a.inner + c, s);
+}
+
+// colsum_body for two column sums from one pass: f(a, e, &third) returns
+// the first value and sets the third; both are summed over the same rows
+// in the same order into out and out3 (the first value written to
+// `values` too when that is set).
+template <int W, class F>
+__device__ __forceinline__ void colsum3_body(const F& f, const Args& a) {
+  const long long o = blockIdx.z;
+  const long long nb = gridDim.x, b = blockIdx.x;
+  const long long r0 = b * a.rchunk, r1 = r0 + a.rchunk < a.r ? r0 + a.rchunk : a.r;
+  const long long c = ((long long)blockIdx.y * kBlock + threadIdx.x) * W;
+  if (c >= a.inner) return;
+  Kahan acc[W], acc3[W];
+  constexpr int U = 4;  // rows whose loads are in flight together (8 measured slower)
+  for (long long k = r0; k < r1; k += U) {
+    V<W> v[U], v3[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (k + u < r1) v[u] = f(a, ((o * a.r + k + u) * a.inner) + c, &v3[u]);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (k + u < r1) {
+        if (a.values) store<W>(a.values + (o * a.r + k + u) * a.inner + c, v[u]);
+#pragma unroll
+        for (int j = 0; j < W; ++j) {
+          acc[j].add(v[u].x[j]);
+          acc3[j].add(v3[u].x[j]);
+        }
+      }
+    }
+  }
+  V<W> s, s3;
+#pragma unroll
+  for (int j = 0; j < W; ++j) {
+    s.x[j] = acc[j].s;
+    s3.x[j] = acc3[j].s;
+  }
+  store<W>(a.out + (o * nb + b) * a.inner + c, s);
+  store<W>(a.out3 + (o * nb + b) * a.inner + c, s3);
 }
 
 }  // namespace jit

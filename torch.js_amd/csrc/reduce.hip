@@ -288,8 +288,8 @@ void colsum_plan(int64_t outer, int64_t r, int64_t inner, bool vec, int64_t* nb_
                  int64_t* rchunk_out) {
   const int cus = num_cus() > 0 ? num_cus() : 256;
   const int64_t col_waves = cdiv(vec ? inner / 4 : inner, kBlock);
-  // ~2 workgroups per CU in total, >= 16 rows each
-  int64_t nb = cdiv(2LL * cus, outer * col_waves);
+  // ~4 workgroups per CU in total, >= 16 rows each
+  int64_t nb = cdiv(4LL * cus, outer * col_waves);
   if (nb > cdiv(r, 16)) nb = cdiv(r, 16);
   if (nb < 1) nb = 1;
   const int64_t rchunk = cdiv(r, nb);

@@ -455,6 +455,17 @@ static int get_expr(napi_env env, napi_value obj, tjh_expr* P) {
   P->n_ins = (int32_t)n;
   P->n_leaves = (int32_t)nl;
   P->result = (int32_t)i64(env, res);
+  /* optional: the second (written) and third (column-summed) values,
+   * register + 1, 0 for none */
+  bool has = false;
+  napi_value v;
+  if (napi_has_named_property(env, obj, "result2", &has) == napi_ok && has &&
+      napi_get_named_property(env, obj, "result2", &v) == napi_ok)
+    P->result2 = (int32_t)i64(env, v);
+  has = false;
+  if (napi_has_named_property(env, obj, "result3", &has) == napi_ok && has &&
+      napi_get_named_property(env, obj, "result3", &v) == napi_ok)
+    P->result3 = (int32_t)i64(env, v);
   for (uint32_t i = 0; i < n; ++i) {
     napi_value row, e[7];
     napi_get_element(env, ins, i, &row);
@@ -547,6 +558,18 @@ static napi_value js_expr_colsum2(napi_env env, napi_callback_info info) {
   if (!get_expr(env, a[0], &P)) return NULL;
   CHECK_RC(tjh_expr_colsum2(&P, i64(env, a[1]), i64(env, a[2]), i64(env, a[3]),
                             (float*)ptr(env, a[4]), (float*)ptr(env, a[5]), (float*)ptr(env, a[6])));
+  return undef(env);
+}
+
+/* exprColsum3(program, outer, r, inner, out, values, values2, out3) */
+static napi_value js_expr_colsum3(napi_env env, napi_callback_info info) {
+  napi_value a[8];
+  if (!get_args(env, info, 8, a)) return NULL;
+  tjh_expr P;
+  if (!get_expr(env, a[0], &P)) return NULL;
+  CHECK_RC(tjh_expr_colsum3(&P, i64(env, a[1]), i64(env, a[2]), i64(env, a[3]),
+                            (float*)ptr(env, a[4]), (float*)ptr(env, a[5]), (float*)ptr(env, a[6]),
+                            (float*)ptr(env, a[7])));
   return undef(env);
 }
 
@@ -1242,7 +1265,7 @@ static napi_value init_module(napi_env env, napi_value exports) {
       FN("copyStrided", js_copy_strided), FN("unary", js_unary),
       FN("unaryBackward", js_unary_backward), FN("binary", js_binary), FN("scalar", js_scalar),
       FN("reduce", js_reduce), FN("exprEval", js_expr_eval), FN("exprColsum", js_expr_colsum),
-      FN("exprColsum2", js_expr_colsum2),
+      FN("exprColsum2", js_expr_colsum2), FN("exprColsum3", js_expr_colsum3),
       FN("exprCompile", js_expr_compile),
       FN("graphBegin", js_graph_begin), FN("graphEnd", js_graph_end),
       FN("graphReplay", js_graph_replay), FN("graphDestroy", js_graph_destroy),

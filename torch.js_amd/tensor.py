@@ -925,9 +925,10 @@ _EXPR_KIND = {"u": "unary", "ub": "unary_bwd", "b": "binary", "t": "ternary", "s
 
 class _Lz:
     """A deferred op: kind ('u' unary, 'ub' unary backward, 'b' binary,
-    't' ternary, 's' / 'sr' scalar, 'axpy', 'alias'), op code, scalar
-    operand, input tensors, and `deps`: ids of the storages and deferred
-    tensors its value reads (transitively)."""
+    't' ternary, 's' / 'sr' scalar, 'axpy', 'alias', or 'thunk': a
+    deferred reduction whose `name` is the function that computes it), op
+    code, scalar operand, input tensors, and `deps`: ids of the storages
+    and deferred tensors its value reads (transitively)."""
 
     __slots__ = ("kind", "code", "f", "args", "kinds", "deps", "name")
 
@@ -980,6 +981,19 @@ def _lazy(kind, code, f, args, shape, kinds=None, name=None):
     t._retains_grad = False
     _pend(t)
     return t
+
+
+def _thunk(fn, shape, inputs):
+    """A deferred value computed by fn() (an evaluated tensor of `shape`)
+    the first time its memory is needed: a reduction of deferred values.
+    It is never inlined into a fused program (it is a leaf there)."""
+    return _lazy("thunk", 0, 0.0, tuple(inputs), shape, name=fn)
+
+
+# Forward column sums left deferred (_colsum_deferred): weakrefs of
+# (thunk, source, dims, scale); a backward column sum over the same rows
+# of values that read the same inputs computes them in its own pass.
+_COLSUMS = []
 
 
 def _leaf_kind(shape, bst):
@@ -1061,12 +1075,12 @@ class _TooBig(Exception):
     pass
 
 
-def _program(root, root2=None):
+def _program(root, root2=None, root3=None):
     """The tjh_expr program of deferred tensor `root` and the tensors it
     keeps alive.  Inputs of another shape, evaluated inputs and views are
     leaves; deferred inputs of the same shape are inlined.  `root2` (same
-    shape) becomes the program's second value, sharing loads and common
-    subexpressions with the first."""
+    shape) becomes the program's second value and `root3` its third,
+    sharing loads and common subexpressions with the first."""
     shape = root._shape
     leaves, leaf_ix, code, memo = [], {}, [], {}
     max_ins = L.EXPR_MAX_INS
@@ -1079,7 +1093,7 @@ def _program(root, root2=None):
                 break
             t = lz.args[0]
             st = t._st
-        if st is None and t._shape == shape:
+        if st is None and t._shape == shape and t._lz.kind != "thunk":
             v = memo.get(id(t))
             if v is not None:
                 return v
@@ -1115,10 +1129,11 @@ def _program(root, root2=None):
 
     result = emit(root, None)
     result2 = emit(root2, None) if root2 is not None else None
-    sig = (tuple(code), result, result2, tuple(k for _, k in leaves))
+    result3 = emit(root3, None) if root3 is not None else None
+    sig = (tuple(code), result, result2, result3, tuple(k for _, k in leaves))
     hit = _PROGRAMS.get(sig)
     if hit is None:
-        hit = _PROGRAMS[sig] = _pack_code(code, result, result2)
+        hit = _PROGRAMS[sig] = _pack_code(code, result, result2, result3)
         if len(_PROGRAMS) > 512:
             _PROGRAMS.pop(next(iter(_PROGRAMS)))
     buf = bytearray(hit)
@@ -1134,10 +1149,10 @@ def _program(root, root2=None):
 _PROGRAMS = {}  # (code, results, leaf kinds) -> packed program without its leaves
 
 
-def _pack_code(code, result, result2=None):
+def _pack_code(code, result, result2=None, result3=None):
     """Packs instructions with registers allocated: a value's register is
     freed after its last use (the results' stay held)."""
-    keep = (result, result2)
+    keep = (result, result2, result3)
     last = {}
     for i, ins in enumerate(code):
         for v in (ins[3:5] if ins[0] == "load" else ins[2:5]):  # a load's `a` is a leaf index
@@ -1167,12 +1182,13 @@ def _pack_code(code, result, result2=None):
         if last.get(i) is None and i not in keep:
             free.append(r)  # never read
     _EXPR_HDR.pack_into(buf, 0, len(code), 0, reg[result],
-                        reg[result2] + 1 if result2 is not None else 0)
+                        reg[result2] + 1 if result2 is not None else 0,
+                        reg[result3] + 1 if result3 is not None else 0, 0)
     return bytes(buf)
 
 
 _EXPR_SIZE = ctypes.sizeof(L.Expr)
-_EXPR_HDR = struct.Struct("<4i")
+_EXPR_HDR = struct.Struct("<6i")
 _EXPR_NLEAF = struct.Struct("<i")
 _EXPR_INS = struct.Struct("<6B2xf")
 _EXPR_INS_OFF = L.Expr.ins.offset
@@ -1211,6 +1227,12 @@ def _settle(t, st):
 
 def _realize(t):
     lz = t._lz
+    if lz.kind == "thunk":
+        out = lz.name()
+        if out._offset or not out.is_contiguous() or out._st is None:
+            out = _k_contiguous(out)
+        _settle(t, out._st)
+        return out._st
     if lz.kind == "alias":
         st = lz.args[0]._storage
         _settle(t, st)
@@ -1295,23 +1317,27 @@ def _lazy_colsum(x, dims, keep=False):
     if outer > 64 or r < 64 or inner < 2:
         return None
     sib = _sibling_for(x) if keep else None
+    third = _pending_colsum_for(x, dims, sib) if 2 * outer <= 64 else None
     prog = None
-    if sib is not None:
+    if sib is not None or third is not None:
         try:
-            prog, keep_alive = _program(x, sib)
+            prog, keep_alive = _program(x, sib, third[1] if third is not None else None)
         except _TooBig:
-            sib = None
+            sib = third = None
     if prog is None:
         try:
             prog, keep_alive = _program_fit(x)
         except RuntimeError:
             return None
-    out = empty(shape[:beg] + [1] * (end - beg) + shape[end:])
+    kshape = shape[:beg] + [1] * (end - beg) + shape[end:]
+    out = empty(kshape)
     vals = empty(x._shape) if keep else None
     vals2 = empty(sib._shape) if sib is not None else None
-    rc = L.lib().tjh_expr_colsum2(ctypes.byref(prog), outer, r, inner, out.data_ptr(),
+    out3 = empty(kshape) if third is not None else None
+    rc = L.lib().tjh_expr_colsum3(ctypes.byref(prog), outer, r, inner, out.data_ptr(),
                                   vals.data_ptr() if vals is not None else None,
-                                  vals2.data_ptr() if vals2 is not None else None)
+                                  vals2.data_ptr() if vals2 is not None else None,
+                                  out3.data_ptr() if out3 is not None else None)
     if rc == L.ERR_UNSUPPORTED or (rc and _jit_failed(rc)):
         return None
     L.check(rc, "expr_colsum")
@@ -1321,7 +1347,39 @@ def _lazy_colsum(x, dims, keep=False):
     if sib is not None:
         _settle(sib, vals2._st)
         _SIBLINGS.remove(sib)
+    if third is not None:
+        # the pending forward column sum, from the same pass: settled as its
+        # own computation would have left it (then scaled for a mean)
+        c, _, scale = third
+        red = _k_scalar("mul", out3, scale) if scale != 1.0 else out3
+        _settle(c, red._st)
     return out
+
+
+def _pending_colsum_for(x, dims, sib):
+    """A deferred column sum (thunk, source value, scale) over the same dims
+    of a deferred value of x's shape that reads one of x's inputs and that
+    neither x nor sib reads, or None."""
+    found = None
+    keep = []
+    for entry in _COLSUMS:
+        c = entry[0]()
+        if c is None or c._st is not None:
+            continue  # evaluated or gone: dropped from the list
+        keep.append(entry)
+        if found is not None:
+            continue
+        z = c._lz.args[0]
+        if (z._st is not None or z is x or z._shape != x._shape or entry[1] != tuple(dims) or
+                z._lz.kind in ("alias", "thunk")):
+            continue
+        if z._lz.deps.isdisjoint(x._lz.deps) or id(c) in x._lz.deps or id(x) in z._lz.deps:
+            continue
+        if sib is not None and (id(c) in sib._lz.deps or sib is z):
+            continue
+        found = (c, z, entry[2])
+    _COLSUMS[:] = keep
+    return found
 
 
 # Deferred leaf gradients of the running backward pass not yet evaluated:
@@ -1613,7 +1671,7 @@ def _k_reduce(op, x, dims, keep=False):
     """Reduces the given dims of x (keepdim=True layout), fp32.  A sum /
     mean of a deferred x reads x's inputs directly (and, with `keep`,
     writes x's value in the same pass)."""
-    if op in ("sum", "mean") and _is_lazy(x) and x._lz.kind != "alias":
+    if op in ("sum", "mean") and _is_lazy(x) and x._lz.kind not in ("alias", "thunk"):
         r = _lazy_colsum(x, dims, keep)
         if r is not None:
             if op == "mean":
@@ -2056,17 +2114,69 @@ def _squeeze_shape(shape, dims):
     return tuple(s for i, s in enumerate(shape) if i not in dims)
 
 
+# column sums of deferred values left deferred until a backward pass can
+# compute them with the gradients it forms from the same inputs; off only
+# to compare with the immediate sums in tests
+_DEFER_SUMS = {"on": True}
+
+
+def _reduced_shape(x, dims, dim, keepdim):
+    if keepdim:
+        return tuple(1 if i in dims else s for i, s in enumerate(x.shape))
+    if dim is None:
+        return ()
+    return _squeeze_shape(x.shape, dims)
+
+
+def _deferred_reduce(op, x, dims, oshape):
+    """A deferred sum / mean of x over `dims` with output shape `oshape`,
+    or None.  A column sum of a deferred elementwise value (one run of
+    adjacent dims, the fused column-sum kernel's layout) is registered so
+    a backward column sum over the same rows of values reading the same
+    inputs computes it in its own pass (_lazy_colsum); a reduction of a
+    deferred reduction stays deferred after it."""
+    if not (_LAZY["on"] and _LAZY["jit"] and _DEFER_SUMS["on"] and x._st is None and dims):
+        return None
+    kind = x._lz.kind
+    cnt = _numel([x._shape[d] for d in dims])
+    scale = 1.0 / cnt if (op == "mean" and cnt) else (float("nan") if op == "mean" else 1.0)
+    if kind == "thunk":
+        def compute():
+            r = _k_reduce(op, x, dims)
+            return _view_raw(r.contiguous(), oshape)
+        return _thunk(compute, oshape, [x])
+    if kind == "alias" or dims != list(range(dims[0], dims[-1] + 1)):
+        return None
+    shape = x._shape
+    outer = _numel(shape[:dims[0]])
+    r = _numel(shape[dims[0]:dims[-1] + 1])
+    inner = _numel(shape[dims[-1] + 1:])
+    if 2 * outer > 64 or r < 64 or inner < 2:
+        return None
+
+    def compute():
+        red = _k_reduce("sum", x, dims)
+        if scale != 1.0:
+            red = _k_scalar("mul", red, scale)
+        return _view_raw(red.contiguous(), oshape)
+    t = _thunk(compute, oshape, [x])
+    _COLSUMS.append((weakref.ref(t), tuple(dims), scale))
+    return t
+
+
 def reduce_sum(x, dim=None, keepdim=False):
     """sum (Tensor.ts:2427-2431); backward broadcasts g over the reduced dims
     after restoring them (torch.js expands without unsqueezing, D13)."""
     if x.dtype != "float32":
         x = x.float()
     dims = _norm_dims(x, dim)
-    r = _k_reduce("sum", x, dims) if dims else x.contiguous()
     kshape = tuple(1 if i in dims else s for i, s in enumerate(x.shape))
-    out = r if keepdim else _view_raw(r, _squeeze_shape(x.shape, dims))
-    if not keepdim and dim is None:
-        out = _view_raw(r, ())
+    out = _deferred_reduce("sum", x, dims, _reduced_shape(x, dims, dim, keepdim))
+    if out is None:
+        r = _k_reduce("sum", x, dims) if dims else x.contiguous()
+        out = r if keepdim else _view_raw(r, _squeeze_shape(x.shape, dims))
+        if not keepdim and dim is None:
+            out = _view_raw(r, ())
     xs = x.shape
 
     def bwd(g):
@@ -2082,9 +2192,11 @@ def reduce_mean(x, dim=None, keepdim=False):
     cnt = 1
     for d in dims:
         cnt *= x.shape[d]
-    r = _k_reduce("mean", x, dims) if dims else x.contiguous()
     kshape = tuple(1 if i in dims else s for i, s in enumerate(x.shape))
-    out = r if keepdim else _view_raw(r, _squeeze_shape(x.shape, dims))
+    out = _deferred_reduce("mean", x, dims, _reduced_shape(x, dims, dim, keepdim))
+    if out is None:
+        r = _k_reduce("mean", x, dims) if dims else x.contiguous()
+        out = r if keepdim else _view_raw(r, _squeeze_shape(x.shape, dims))
     xs = x.shape
 
     def bwd(g):
@@ -3092,6 +3204,11 @@ def run_backward(pairs, retain_graph=False, inputs=None, create_graph=False):
         if deferred:
             _flush_deferred(deferred)
         _finish_siblings()
+        # a loss that is a deferred reduction is evaluated with the pass
+        # (its column sums usually came with the gradients' own kernel)
+        for t, _ in pairs:
+            if t._st is None and t._lz is not None and t._lz.kind == "thunk":
+                t._storage
         if wanted is not None:
             return [_dense(results.get(id(t))) for t in inputs]
         return None
