@@ -400,9 +400,13 @@ def run_config(name, steps, warmup, cpu):
                                  "peak": HBM_PEAK_GBS, "unit": "GB/s",
                                  "frac": round(CHAIN_FUSED_BYTES / sec / 1e9 / HBM_PEAK_GBS, 3),
                                  "note": "end to end over the fused minimum (read x, y; write "
-                                         "gx, gy); the fused chain moves 576 MB: forward column "
-                                         "sum, y's gradient, x's gradient with the bias "
-                                         "column sum"}})
+                                         "gx, gy): one pass (expr_colsum3) forms the loss's "
+                                         "column sum, x's and y's gradients and the bias "
+                                         "gradient; then the loss's mean and the small "
+                                         "launches of the step"},
+                    "kernels": {f: {"ms_per_step": ms, "GB/s": round(CHAIN_FUSED_BYTES / ms / 1e6, 1),
+                                    "frac": round(CHAIN_FUSED_BYTES / ms / 1e6 / HBM_PEAK_GBS, 3)}
+                                for f, ms in per.items() if f.startswith("expr")}})
         if cpu:
             dt = _cpu_time(lambda: om.chain_loss_and_grads(x, b, y))
             out["cpu_baseline"] = {"value": round(CHAIN_FUSED_BYTES / dt / 1e9, 2), "unit": "GB/s",
