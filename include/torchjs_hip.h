@@ -684,7 +684,10 @@ int tjh_gemm_ce(int transA, int64_t M, int64_t N, int64_t K,
 /* q [B,H,Tq,D], k/v [B,H,Tk,D] given by strides (elements) for the B, H
  * and T axes; D is contiguous.  o written with its own strides.  lse
  * [B,H,Tq] (contiguous) saved for the backward.  causal masks key j >
- * query i (top-left aligned, as torch's is_causal). */
+ * query i (top-left aligned, as torch's is_causal).  Head dims D <= 128
+ * with D % 4 == 0 and 16-byte aligned rows run the flash kernels (O(T)
+ * extra memory); any other D runs GEMM-composed attention over [H,Tq,Tk]
+ * scores of one batch item at a time. */
 int tjh_sdpa_forward(const float* q, const float* k, const float* v,
                      float* o, float* lse, int64_t B, int64_t H, int64_t Tq,
                      int64_t Tk, int64_t D, const int64_t* q_strides,

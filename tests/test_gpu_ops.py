@@ -900,6 +900,101 @@ def test_sdpa_flash_recompute_path(torch, monkeypatch, causal):
     assert not np.array_equal(stored[0], recomputed[0])  # two different paths ran
 
 
+def _sdpa_families(torch, fn):
+    """Runs fn with kernel timing on; returns {family: launches}."""
+    torch.hip.kernel_timing(True)
+    torch.hip.kernel_timing_reset()
+    try:
+        fn()
+        return dict((f, torch.hip.kernel_time(f)[0]) for f in torch.hip.kernel_families())
+    finally:
+        torch.hip.kernel_timing(False)
+
+
+@pytest.mark.parametrize("D", [4, 16, 32, 40, 60, 96, 100, 128])
+@pytest.mark.parametrize("causal", [True, False])
+def test_sdpa_flash_head_dims(torch, D, causal):
+    """Head dims other than 64 on the flash kernels (compiled for 32, 64,
+    96 and 128; a smaller D reads its padded columns as zero), ragged and
+    cross lengths, against the oracle; the composed path must not run."""
+    Tq, Tk = (77, 77) if causal else (45, 130)
+    r = np.random.default_rng(D * 10 + causal)
+    B, H = 2, 3
+    q = f32(r.standard_normal((B, H, Tq, D)))
+    k = f32(r.standard_normal((B, H, Tk, D)))
+    v = f32(r.standard_normal((B, H, Tk, D)))
+    fn = lambda a, b, c: torch.F.scaled_dot_product_attention(a, b, c, is_causal=causal)
+    res = {}
+    fams = _sdpa_families(torch, lambda: res.update(r=grad_of(torch, fn, q, k, v)))
+    out, g, (gq, gk, gv) = res["r"]
+    # family counts match by prefix: "sdpa_fwd" includes "sdpa_fwd_composite"
+    assert fams.get("sdpa_fwd", 0) == 1 and fams.get("sdpa_bwd", 0) >= 1, fams
+    assert fams.get("sdpa_fwd_composite", 0) == 0 and fams.get("sdpa_bwd_composite", 0) == 0, fams
+    f64 = lambda z: z.astype(np.float64)
+    o, _ = ops.sdpa(f64(q), f64(k), f64(v), causal)
+    check(out, o, rtol=1e-4, atol=1e-5)
+    wq, wk, wv = ops.sdpa_backward(f64(g), f64(q), f64(k), f64(v), causal)
+    check(gq, wq, **RED)
+    check(gk, wk, **RED)
+    check(gv, wv, **RED)
+
+
+@pytest.mark.parametrize("D", [20, 32, 96, 128])
+def test_sdpa_flash_head_dims_recompute_path(torch, monkeypatch, D):
+    """The four-product key kernel and the recomputing query kernel at each
+    compiled head dim agree with the stored-dS path."""
+    r = np.random.default_rng(300 + D)
+    q, k, v = (f32(r.standard_normal((1, 2, 97, D))) for _ in range(3))
+    fn = lambda a, b, c: torch.F.scaled_dot_product_attention(a, b, c, is_causal=True)
+    _, _, stored = grad_of(torch, fn, q, k, v)
+    monkeypatch.setenv("TJH_SDPA_RECOMPUTE", "1")
+    _, _, recomputed = grad_of(torch, fn, q, k, v)
+    for s_, r_ in zip(stored, recomputed):
+        check(r_, s_, rtol=1e-4, atol=1e-5)
+
+
+@pytest.mark.parametrize("D", [96, 128])
+def test_sdpa_flash_large_head_dim_full_length(torch, D):
+    """T = 1024 causal at head dims 96 and 128 (every query block length of
+    the cost-ranked placement), against the oracle."""
+    r = np.random.default_rng(400 + D)
+    B, H, T = 1, 2, 1024
+    q, k, v = (f32(r.standard_normal((B, H, T, D))) for _ in range(3))
+    out, g, (gq, gk, gv) = grad_of(
+        torch, lambda a, b, c: torch.F.scaled_dot_product_attention(a, b, c, is_causal=True),
+        q, k, v)
+    f64 = lambda z: z.astype(np.float64)
+    o, _ = ops.sdpa(f64(q), f64(k), f64(v), True)
+    check(out, o, rtol=1e-4, atol=1e-5)
+    wq, wk, wv = ops.sdpa_backward(f64(g), f64(q), f64(k), f64(v), True)
+    check(gq, wq, **RED)
+    check(gk, wk, **RED)
+    check(gv, wv, **RED)
+
+
+@pytest.mark.parametrize("D", [6, 160])
+def test_sdpa_composed_path_head_dims(torch, D):
+    """Head dims the flash kernels do not take (not a multiple of 4, or
+    above 128) run the GEMM-composed path, against the oracle."""
+    r = np.random.default_rng(500 + D)
+    q, k, v = (f32(r.standard_normal((2, 2, 40, D))) for _ in range(3))
+    fn = lambda a, b, c: torch.F.scaled_dot_product_attention(a, b, c, is_causal=True)
+    res = {}
+    fams = _sdpa_families(torch, lambda: res.update(r=grad_of(torch, fn, q, k, v)))
+    out, g, (gq, gk, gv) = res["r"]
+    # family counts match by prefix: "sdpa_fwd" includes "sdpa_fwd_composite"
+    assert fams.get("sdpa_fwd_composite", 0) >= 1, fams
+    assert fams.get("sdpa_fwd", 0) == fams["sdpa_fwd_composite"], fams
+    assert fams.get("sdpa_bwd", 0) == fams.get("sdpa_bwd_composite", 0) >= 1, fams
+    f64 = lambda z: z.astype(np.float64)
+    o, _ = ops.sdpa(f64(q), f64(k), f64(v), True)
+    check(out, o, rtol=1e-4, atol=1e-5)
+    wq, wk, wv = ops.sdpa_backward(f64(g), f64(q), f64(k), f64(v), True)
+    check(gq, wq, **RED)
+    check(gk, wk, **RED)
+    check(gv, wv, **RED)
+
+
 def test_split_and_narrow_gradients(torch):
     """Pieces of a split that are unused, overlapping narrows and a reused
     piece: the input gradient is the sum over every use (zero elsewhere)."""

@@ -6,9 +6,9 @@
 // implemented is torch's: optional causal mask (key j > query i masked,
 // top-left aligned), lse saved for the backward.
 //
-// Head dim 64 with D-contiguous, 16-byte aligned rows runs the flash
-// kernels of flash.hip.  Any other shape takes the GEMM-composed path
-// below, per batch item: S = scale * Q K^T on the
+// Head dims up to 128 that are multiples of 4, with D-contiguous, 16-byte
+// aligned rows, run the flash kernels of flash.hip.  Any other shape takes
+// the GEMM-composed path below, per batch item: S = scale * Q K^T on the
 // MFMA GEMM (all heads of one batch item in one batched launch), a fused
 // masked softmax that also writes lse, then O = P V.  The backward
 // recomputes P from lse and issues dV = P^T dO, dP = dO V^T,
@@ -115,7 +115,7 @@ int tjh_sdpa_forward(const float* q, const float* k, const float* v, float* o, f
     const void* ptrs[4] = {q, k, v, o};
     const int64_t* sts[4] = {qs, ks, vs, os};
     if (flash_supported(D, ptrs, sts, 4))
-      return flash_forward(q, k, v, o, lse, B, H, Tq, Tk, qs, ks, vs, os, scale, causal);
+      return flash_forward(q, k, v, o, lse, B, H, Tq, Tk, D, qs, ks, vs, os, scale, causal);
   }
   Scratch S((size_t)(H * Tq * Tk) * sizeof(float));
   if (!S.ok()) return set_error(TJH_ERR_OOM, "sdpa_forward: no scratch for scores");
@@ -151,7 +151,7 @@ int tjh_sdpa_backward(const float* q, const float* k, const float* v, const floa
   {
     const void* ptrs[8] = {q, k, v, o, do_, dq, dk, dv};
     if (flash_supported(D, ptrs, strides, 8))
-      return flash_backward(q, k, v, o, do_, lse, dq, dk, dv, B, H, Tq, Tk, strides, scale,
+      return flash_backward(q, k, v, o, do_, lse, dq, dk, dv, B, H, Tq, Tk, D, strides, scale,
                             causal);
   }
   Scratch Ps((size_t)(H * Tq * Tk) * sizeof(float));

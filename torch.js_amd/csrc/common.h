@@ -95,16 +95,18 @@ int gemm(const char* family, int transA, int transB, int64_t M, int64_t N, int64
          const float* bias, int bias_mode, float* aux = nullptr, int64_t ldaux = 0, int act = 0,
          const float* ce_rows = nullptr);
 
-// Flash attention for head dim 64 (flash.hip).  `flash_supported` checks
-// the head dim and that every tensor has 16-byte aligned, D-contiguous rows.
+// Flash attention for head dims D <= 128, D % 4 == 0 (flash.hip).
+// `flash_supported` checks the head dim and that every tensor has 16-byte
+// aligned, D-contiguous rows.
 bool flash_supported(int64_t D, const void* const* ptrs, const int64_t* const* strides, int n);
 int flash_forward(const float* q, const float* k, const float* v, float* o, float* lse, int64_t B,
-                  int64_t H, int64_t Tq, int64_t Tk, const int64_t* qs, const int64_t* ks,
-                  const int64_t* vs, const int64_t* os, float scale, int causal);
+                  int64_t H, int64_t Tq, int64_t Tk, int64_t D, const int64_t* qs,
+                  const int64_t* ks, const int64_t* vs, const int64_t* os, float scale,
+                  int causal);
 int flash_backward(const float* q, const float* k, const float* v, const float* o,
                    const float* dout, const float* lse, float* dq, float* dk, float* dv,
-                   int64_t B, int64_t H, int64_t Tq, int64_t Tk, const int64_t* const* strides,
-                   float scale, int causal);
+                   int64_t B, int64_t H, int64_t Tq, int64_t Tk, int64_t D,
+                   const int64_t* const* strides, float scale, int causal);
 
 // 16-byte alignment of a device pointer (128-bit access paths).
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }

@@ -205,9 +205,10 @@ class MultiheadAttention(Module):
     (self-attention; q, k and v are then strided views of its output, and
     the backward assembles their gradients into that output's gradient
     with no copy), two when key is value.  Attention runs on the flash
-    kernels (head dim 64; other head dims on the library's other attention
-    kernel) unless attention weights or masks are asked for, when the
-    scores are formed by batched GEMMs and softmaxed explicitly."""
+    kernels (head dims up to 128 that are multiples of 4; others on the
+    library's GEMM-composed attention) unless attention weights or masks
+    are asked for, when the scores are formed by batched GEMMs and
+    softmaxed explicitly."""
 
     def __init__(self, embed_dim, num_heads, dropout=0.0, bias=True, batch_first=False):
         super().__init__()
