@@ -681,7 +681,7 @@ def test_gemm_layouts(torch, M, N, K, ta, tb):
     check_floor(got, want, (A.T if ta else A) @ (B.T if tb else B))
 
 
-@pytest.mark.parametrize("tile", ["256x128", "128x128", "128x64", "64x64"])
+@pytest.mark.parametrize("tile", ["256x128", "128x128", "128x64", "64x64", "256x256"])
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
 @pytest.mark.parametrize("M,N,K", [(300, 260, 200), (256, 128, 4096)])
 def test_gemm_every_tile(torch, monkeypatch, tile, ta, tb, M, N, K):
@@ -698,6 +698,22 @@ def test_gemm_every_tile(torch, monkeypatch, tile, ta, tb, M, N, K):
     got = _raw_gemm(torch, ta, tb, A, B, M, N, K, alpha=0.5, beta=0.25, C0=C0, bias=bias, bmode=1)
     ref32 = np.float32(0.5) * ((A.T if ta else A) @ (B.T if tb else B)) + np.float32(0.25) * C0 + bias
     check_floor(got, want, ref32)
+
+
+@pytest.mark.parametrize("forced", [None, "256x256"])
+def test_gemm_long_k_input_gradient(torch, monkeypatch, forced):
+    """A . B with K = 50257 (the LM head's input gradient, dlogits . W), at
+    2048 rows the planner takes the 256 x 256 tile over split K slices;
+    forced, and by the planner, against float64 on the float32 floor."""
+    if forced:
+        monkeypatch.setenv("TJH_GEMM_TILE", forced)
+    M, N, K = 2048, 768, 50257
+    r = np.random.default_rng(50257)
+    A = f32(r.standard_normal((M, K)) * 0.02)
+    B = f32(r.standard_normal((K, N)) * 0.02)
+    want = A.astype(np.float64) @ B.astype(np.float64)
+    got = _raw_gemm(torch, 0, 0, A, B, M, N, K)
+    check_floor(got, want, A @ B)
 
 
 @pytest.mark.parametrize("tile", ["256x128", "128x128", "128x64", "64x64"])

@@ -9,10 +9,12 @@
 //
 // Tiling (one workgroup = 4 wave64 arranged 2 x 2, or 8 arranged 4 x 2 for
 // 256-row tiles):
-//   block tile BM x BN in {256x128, 128x128, 128x64, 64x64}, K step 16;
-//   each wave owns a (BM/2 or 64) x (BN/2) sub-tile of 32x32 MFMA blocks;
-//   the 8-wave 256x128 tile shares each B tile among four row waves (a
-//   quarter fewer global loads and LDS stores per FLOP than 128x128).  Tiles
+//   block tile BM x BN in {256x128, 128x128, 128x64, 64x64, 256x256}, K
+//   step 16; each wave owns a (BM/2 or 64) x (BN/2) sub-tile of 32x32 MFMA
+//   blocks; the 8-wave 256x128 tile shares each B tile among four row waves
+//   (a quarter fewer global loads and LDS stores per FLOP than 128x128);
+//   the 8-wave 256x256 tile (64x128 per wave, two waves per SIMD) serves
+//   only A . B with a very long K, where it halves the re-reads of A.  Tiles
 //   are double-buffered in LDS: the next K tile is fetched from HBM into
 //   registers while the MFMAs consume the current LDS tile.  A stored
 //   [M][K] (k contiguous) is staged As[m][k] and read as 128-bit fragments
@@ -289,7 +291,7 @@ __device__ __forceinline__ int xcd_tile(int bid, int n) {
 }
 
 template <int BM, int BN, bool TA, bool TB, bool EDGE, bool XF = false>
-__global__ __launch_bounds__(gemm_threads(BM), 4) void k_gemm(GemmArgs g) {
+__global__ __launch_bounds__(gemm_threads(BM), BN >= 256 ? 2 : 4) void k_gemm(GemmArgs g) {
   constexpr int LA = BM + 4, LB = BN + 4;       // LDS row lengths
   constexpr int WM = BM / (gemm_threads(BM) / 128), WN = BN / 2;  // wave tile: (T/128) x 2 waves
   constexpr int FM = WM / 32, FN = WN / 32;     // MFMA blocks per wave
@@ -550,7 +552,7 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(GemmArgs g, int splits) {
 struct TileCfg {
   int bm, bn;
 };
-constexpr TileCfg kTiles[] = {{256, 128}, {128, 128}, {128, 64}, {64, 64}};
+constexpr TileCfg kTiles[] = {{256, 128}, {128, 128}, {128, 64}, {64, 64}, {256, 256}};
 constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
 
 // Measured relative per-FLOP throughput of each tile with the CUs full, by
@@ -559,9 +561,9 @@ constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
 // CUs with it (the LM head's three, the 3072-wide ones); 128x64 is 3-5%
 // slower per FLOP and wins only where the larger tiles leave CUs idle.
 float tile_speed(int ti, int ta, int tb) {
-  static const float nt[kNumTiles] = {1.04f, 1.00f, 0.95f, 0.85f};
-  static const float nn[kNumTiles] = {1.03f, 1.00f, 0.97f, 0.85f};
-  static const float tn[kNumTiles] = {1.03f, 1.00f, 0.97f, 0.85f};
+  static const float nt[kNumTiles] = {1.04f, 1.00f, 0.95f, 0.85f, 0.0f};
+  static const float nn[kNumTiles] = {1.03f, 1.00f, 0.97f, 0.85f, 1.10f};
+  static const float tn[kNumTiles] = {1.03f, 1.00f, 0.97f, 0.85f, 0.0f};
   if (!ta && tb) return nt[ti];
   if (!ta && !tb) return nn[ti];
   if (ta && !tb) return tn[ti];
@@ -627,11 +629,17 @@ Plan choose_plan(int64_t M, int64_t N, int64_t K, int64_t batch, int cus, int ta
   for (int i = 0; i < kNumTiles; ++i) {
     if (forced >= 0 && i != forced) continue;
     const TileCfg& t = kTiles[i];
+    // 256 x 256 (two waves per SIMD, 64 x 128 per wave): only for A . B
+    // with a very long K (the LM head's input gradient, K = vocab), where
+    // halving the column tiles halves the re-reads of the [M, K] operand
+    // (5.69 against 6.27 ms); slower on every other GPT-2 product
+    const bool wide = t.bn >= 256;
+    if (wide && forced < 0 && (ta || tb || K < 32768)) continue;
     int64_t tm = cdiv(M, t.bm), tn = cdiv(N, t.bn);
     double useful = (double)(M * N) / (double)(tm * t.bm * tn * t.bn);
     int64_t tiles = tm * tn * batch;
     int64_t s = choose_splits(tiles, K, cus);
-    if (t.bm >= 256 && forced < 0 && s > 1) continue;
+    if (t.bm >= 256 && !wide && forced < 0 && s > 1) continue;
     double score = useful * fill_of(tiles * s, cus) * tile_speed(i, ta, tb);
     if (tiles * s < cus) score *= (double)(tiles * s) / cus;
     if (score > best_score + 1e-9) {
@@ -674,6 +682,7 @@ void launch_tile(int ti, const GemmArgs& g, dim3 grid, int ta, int tb, bool edge
     case 0: launch<256, 128>(g, grid, ta, tb, edge); break;
     case 1: launch<128, 128>(g, grid, ta, tb, edge); break;
     case 2: launch<128, 64>(g, grid, ta, tb, edge); break;
+    case 4: launch<256, 256>(g, grid, ta, tb, edge); break;
     default: launch<64, 64>(g, grid, ta, tb, edge); break;
   }
 }
