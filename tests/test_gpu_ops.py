@@ -716,6 +716,19 @@ def test_gemm_long_k_input_gradient(torch, monkeypatch, forced):
     check_floor(got, want, A @ B)
 
 
+def test_gemm_vocab_rows_weight_gradient(torch):
+    """A^T . B with vocabulary-sized M (the LM head's weight gradient,
+    dlogits^T . x): the planner takes the 256 x 256 tile over two K slices
+    here (M = 32768, K = 2048), against float64 on the float32 floor."""
+    M, N, K = 32768, 768, 2048
+    r = np.random.default_rng(32768)
+    A = f32(r.standard_normal((K, M)) * 0.05)
+    B = f32(r.standard_normal((K, N)))
+    want = A.T.astype(np.float64) @ B.astype(np.float64)
+    got = _raw_gemm(torch, 1, 0, A, B, M, N, K)
+    check_floor(got, want, A.T @ B)
+
+
 @pytest.mark.parametrize("tile", ["256x128", "128x128", "128x64", "64x64"])
 @pytest.mark.parametrize("ta", [0, 1])
 @pytest.mark.parametrize("M,N,K", [(300, 260, 200), (256, 128, 4096), (768, 192, 8192), (5, 3, 7)])

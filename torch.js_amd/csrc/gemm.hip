@@ -563,7 +563,7 @@ constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
 float tile_speed(int ti, int ta, int tb) {
   static const float nt[kNumTiles] = {1.04f, 1.00f, 0.95f, 0.85f, 0.0f};
   static const float nn[kNumTiles] = {1.03f, 1.00f, 0.97f, 0.85f, 1.10f};
-  static const float tn[kNumTiles] = {1.03f, 1.00f, 0.97f, 0.85f, 0.0f};
+  static const float tn[kNumTiles] = {1.03f, 1.00f, 0.97f, 0.85f, 1.10f};
   if (!ta && tb) return nt[ti];
   if (!ta && !tb) return nn[ti];
   if (ta && !tb) return tn[ti];
@@ -606,6 +606,22 @@ int64_t choose_splits(int64_t tiles, int64_t K, int cus) {
   return best;
 }
 
+// K slices for the 256 x 256 tile when its tiles alone leave the last
+// round of workgroups part-empty (one workgroup per CU): the best fill,
+// each slice charged 2% for its [M, N] partials (written, then summed).
+int64_t wide_splits(int64_t tiles, int64_t K, int cus) {
+  int64_t best = 1;
+  double best_f = -1.0;
+  for (int64_t s = 1; s <= 8 && K / s >= 1024; ++s) {
+    const double f = fill_of(tiles * s, cus) * (1.0 - 0.02 * (double)s);
+    if (f > best_f + 1e-9) {
+      best_f = f;
+      best = s;
+    }
+  }
+  return best;
+}
+
 // Picks tile and split maximising (useful fraction of padded work) x
 // (CU fill) x tile speed.  TJH_GEMM_TILE=BMxBN forces a tile (read on every
 // call, so a test can sweep the tiles in one process).  The 8-wave 256x128
@@ -630,15 +646,19 @@ Plan choose_plan(int64_t M, int64_t N, int64_t K, int64_t batch, int cus, int ta
     if (forced >= 0 && i != forced) continue;
     const TileCfg& t = kTiles[i];
     // 256 x 256 (two waves per SIMD, 64 x 128 per wave): only for A . B
-    // with a very long K (the LM head's input gradient, K = vocab), where
-    // halving the column tiles halves the re-reads of the [M, K] operand
-    // (5.69 against 6.27 ms); slower on every other GPT-2 product
+    // with a very long K (the LM head's input gradient, K = vocab: 5.68
+    // against 6.27 ms) and for A^T . B with vocabulary-sized M (its weight
+    // gradient, over three K slices: 5.31 against 5.86 ms), where halving
+    // the column tiles halves the re-reads of the [vocab, tokens] operand;
+    // slower on every other GPT-2 product
     const bool wide = t.bn >= 256;
-    if (wide && forced < 0 && (ta || tb || K < 32768)) continue;
+    const bool wide_ok = tb == 0 && ((!ta && K >= 32768) || (ta && M >= 32768));
+    if (wide && forced < 0 && !wide_ok) continue;
     int64_t tm = cdiv(M, t.bm), tn = cdiv(N, t.bn);
     double useful = (double)(M * N) / (double)(tm * t.bm * tn * t.bn);
     int64_t tiles = tm * tn * batch;
     int64_t s = choose_splits(tiles, K, cus);
+    if (wide && ta && s == 1) s = wide_splits(tiles, K, cus);
     if (t.bm >= 256 && !wide && forced < 0 && s > 1) continue;
     double score = useful * fill_of(tiles * s, cus) * tile_speed(i, ta, tb);
     if (tiles * s < cus) score *= (double)(tiles * s) / cus;
