@@ -472,6 +472,18 @@ def second_order_functions(T, F):
         "views": lambda x: T.cat([x[0:2] * 2.0, x[2:5].relu() + x[2:5]], 0)
         .transpose(0, 1).reshape(-1).pow(2).sum() + x.permute(1, 0).mean(1).pow(3).sum(),
         "bmm": lambda x, w: (x @ w).tanh().pow(2).sum() + (x.sum(1, keepdim=True) * x).sum(),
+        "layer_norm": lambda x, w, b: (F.layer_norm(x, (6,), w, b).pow(3).sum()
+                                       + F.layer_norm(x, (6,)).tanh().sum()),
+        "cross_entropy": lambda x: (F.cross_entropy(x, T.tensor([1, 0, 4, 2, 4]), label_smoothing=0.1)
+                                    + F.cross_entropy(x * 2.0, T.tensor([3, 3, 0, 1, 2]),
+                                                      reduction="sum")),
+        "nll": lambda x: F.nll_loss(F.log_softmax(x, 1), T.tensor([0, 2, -100, 2])),
+        "embedding": lambda w: F.embedding(T.tensor([3, 1, 3, 0]), w).pow(3).sum(),
+        "sdpa": lambda q, k, v: F.scaled_dot_product_attention(q, k, v, is_causal=True).pow(2).sum(),
+        "clamp_max": lambda x: ((x.clamp(-0.5, 0.8) * x).pow(2).sum() + x.amax(1).pow(2).sum()
+                                + (x.triu(1) * x).sum()),
+        "index": lambda x: (x.index_select(0, T.tensor([2, 0, 2])).pow(3).sum()
+                            + x.gather(1, T.tensor([[0, 1], [2, 2], [1, 0]])).pow(2).sum()),
     }
 
 
@@ -479,6 +491,8 @@ SECOND_ORDER_SHAPES = {
     "elementwise": [(5, 7)], "linear_gelu": [(6, 5), (4, 5), (4,)],
     "softmax": [(6, 5), (5, 7), (6, 7)], "broadcast": [(4, 6), (6,)], "views": [(5, 3)],
     "bmm": [(2, 3, 4), (2, 4, 5)],
+    "layer_norm": [(4, 6), (6,), (6,)], "cross_entropy": [(5, 5)], "nll": [(4, 3)],
+    "embedding": [(5, 4)], "sdpa": [(1, 2, 5, 8)] * 3, "clamp_max": [(4, 5)], "index": [(3, 4)],
 }
 SECOND_ORDER_CONST = {"softmax": [2]}  # inputs that are constants (no gradient)
 
@@ -487,6 +501,11 @@ def second_order(rng):
     """First derivatives built with create_graph=True, then Hessian-vector
     products: grad of sum_i <grad_i, v_i> w.r.t. the inputs."""
     d = {}
+    # the math attention backend: PyTorch's CPU flash kernel has no double
+    # backward
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    ctx = sdpa_kernel(SDPBackend.MATH)
+    ctx.__enter__()
     for name, fn in second_order_functions(torch, torch.nn.functional).items():
         const = SECOND_ORDER_CONST.get(name, [])
         xs = [rng.standard_normal(shp) * 0.7 for shp in SECOND_ORDER_SHAPES[name]]
@@ -502,6 +521,7 @@ def second_order(rng):
             d["%s:g%d" % (name, i)] = g
             d["%s:v%d" % (name, i)] = v
             d["%s:h%d" % (name, i)] = hv
+    ctx.__exit__(None, None, None)
     save("second_order", **d)
 
 

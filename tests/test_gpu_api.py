@@ -71,9 +71,10 @@ def test_autograd_grad_literals(torch):
     xv = np.array([1.5, -0.5])
     close4(h.toArray(), list(np.exp(xv) * (xv + 2)))       # (x e^x)'' = e^x (x + 2)
     # an op with no differentiable backward says so
-    x = torch.tensor(np.ones((4, 8), np.float32), requires_grad=True)
-    with pytest.raises(NotImplementedError, match="LayerNorm"):
-        torch.autograd.grad(torch.F.layer_norm(x, (8,)).pow(2).sum(), x, create_graph=True)
+    x = torch.tensor(np.ones((1, 1, 4, 4), np.float32), requires_grad=True)
+    w = torch.tensor(np.ones((1, 1, 3, 3), np.float32), requires_grad=True)
+    with pytest.raises(NotImplementedError, match="Conv2d"):
+        torch.autograd.grad(torch.F.conv2d(x, w).pow(2).sum(), x, create_graph=True)
 
 
 def test_autograd_vjp_literals(torch):
@@ -108,7 +109,8 @@ def test_autograd_jvp_literals(torch):
     close4(j.toArray(), [4.0])                            # :137-149
 
 
-SECOND_ORDER = ["elementwise", "linear_gelu", "softmax", "broadcast", "views", "bmm"]
+SECOND_ORDER = ["elementwise", "linear_gelu", "softmax", "broadcast", "views", "bmm",
+                "layer_norm", "cross_entropy", "nll", "embedding", "sdpa", "clamp_max", "index"]
 
 
 @pytest.mark.parametrize("name", SECOND_ORDER)
@@ -137,6 +139,54 @@ def test_second_order_golden(torch, name):
         check(hv.numpy(), z["%s:h%d" % (name, i)], **RED)
 
 
+@pytest.mark.parametrize("which", ["mlp", "linear_add", "embedding_pos"])
+def test_second_order_fused_ops_equal_composites(torch, which):
+    """create_graph through the fused ops the GPT-2 model runs (the GELU
+    MLP, the projection with its residual add, the token + position
+    embedding): gradients and Hessian-vector products equal those of the
+    same function written with the public ops."""
+    F = torch.F
+    r = np.random.default_rng(7)
+    if which == "mlp":
+        shapes = [(6, 8), (12, 8), (12,), (8, 12), (8,), (6, 8)]
+        fused = lambda x, w1, b1, w2, b2, res: F._mlp_gelu(x, w1, b1, w2, b2, res).pow(2).sum()
+        ref = lambda x, w1, b1, w2, b2, res: (
+            res + F.linear(F.gelu(F.linear(x, w1, b1)), w2, b2)).pow(2).sum()
+    elif which == "linear_add":
+        shapes = [(6, 8), (5, 8), (5,), (6, 5)]
+        fused = lambda x, w, b, res: F._linear_add(x, w, b, res).pow(3).sum()
+        ref = lambda x, w, b, res: (res + F.linear(x, w, b)).pow(3).sum()
+    else:
+        shapes = [(7, 4), (6, 4)]
+        ids = torch.tensor(np.array([[1, 6, 1], [0, 3, 5]], np.int32), dtype="int32")
+        fused = lambda w, p: F._embedding_pos(ids, w, p, 2).pow(3).sum()
+        ref = lambda w, p: (F.embedding(ids, w) + p[2:5]).pow(3).sum()
+    xs = [f32(r.standard_normal(s) * 0.5) for s in shapes]
+    vs = [f32(r.standard_normal(s)) for s in shapes]
+    res = []
+    for fn in (fused, ref):
+        ts = [torch.tensor(x, requires_grad=True) for x in xs]
+        g1 = torch.autograd.grad(fn(*ts), ts, create_graph=True)
+        dot = None
+        for g, v in zip(g1, vs):
+            term = (g * torch.tensor(v)).sum()
+            dot = term if dot is None else dot + term
+        h = torch.autograd.grad(dot, ts)
+        res.append(([g.numpy() for g in g1], [hh.numpy() for hh in h]))
+    for a, b in zip(res[0][0] + res[0][1], res[1][0] + res[1][1]):
+        check(a, b, **RED)
+
+
+def test_second_order_conv2d_refused(torch):
+    """The convolution has no differentiable backward: create_graph through
+    it raises, naming the op."""
+    x = torch.tensor(f32(np.ones((1, 2, 5, 5))), requires_grad=True)
+    w = torch.tensor(f32(np.ones((3, 2, 3, 3)) * 0.1), requires_grad=True)
+    y = torch.F.conv2d(x, w, None, 1, 1).pow(2).sum()
+    with pytest.raises(NotImplementedError, match="Conv2d"):
+        torch.autograd.grad(y, [x, w], create_graph=True)
+
+
 def _second_order_functions(torch):
     """The definitions of tests/golden/make_golden.py second_order_functions,
     over the hip package."""
@@ -154,6 +204,18 @@ def _second_order_functions(torch):
         "views": lambda x: T.cat([x[0:2] * 2.0, x[2:5].relu() + x[2:5]], 0)
         .transpose(0, 1).reshape(-1).pow(2).sum() + x.permute(1, 0).mean(1).pow(3).sum(),
         "bmm": lambda x, w: (x @ w).tanh().pow(2).sum() + (x.sum(1, keepdim=True) * x).sum(),
+        "layer_norm": lambda x, w, b: (F.layer_norm(x, (6,), w, b).pow(3).sum()
+                                       + F.layer_norm(x, (6,)).tanh().sum()),
+        "cross_entropy": lambda x: (F.cross_entropy(x, T.tensor([1, 0, 4, 2, 4]), label_smoothing=0.1)
+                                    + F.cross_entropy(x * 2.0, T.tensor([3, 3, 0, 1, 2]),
+                                                      reduction="sum")),
+        "nll": lambda x: F.nll_loss(F.log_softmax(x, 1), T.tensor([0, 2, -100, 2])),
+        "embedding": lambda w: F.embedding(T.tensor([3, 1, 3, 0]), w).pow(3).sum(),
+        "sdpa": lambda q, k, v: F.scaled_dot_product_attention(q, k, v, is_causal=True).pow(2).sum(),
+        "clamp_max": lambda x: ((x.clamp(-0.5, 0.8) * x).pow(2).sum() + x.amax(1).pow(2).sum()
+                                + (x.triu(1) * x).sum()),
+        "index": lambda x: (x.index_select(0, T.tensor([2, 0, 2])).pow(3).sum()
+                            + x.gather(1, T.tensor([[0, 1], [2, 2], [1, 0]])).pow(2).sum()),
     }
 
 

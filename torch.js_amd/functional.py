@@ -13,7 +13,7 @@ from .tensor import _e_unary_bwd
 from .tensor import (Tensor, _DT, _alias, _contig_strides, _empty_padded, _gemm, _k_binary,
                      _k_contiguous, _k_reduce, _k_scalar, _numel, _record, _view_raw, _wrap_dim,
                      contiguous, empty, full, mul, permute, reduce_mean, reshape, reshape_raw,
-                     sub, unary, zeros)
+                     neg, sub, unary, zeros)
 
 
 def relu(x, inplace=False):
@@ -156,6 +156,40 @@ def _class_weight(weight, cols):
     return w.contiguous()
 
 
+def _class_coef(t, w, rows, cols, eps, ignore_index, smooth):
+    """The constant [rows, cols] coefficients Q with loss_i = -sum_c Q[i, c]
+    * logp[i, c] for the losses below: (1 - eps) w_t at the target and
+    (eps / C) w_c everywhere when `smooth`, rows whose target is
+    ignore_index zero; and the 'mean' divisor, the valid rows' target
+    weights summed (computed without recording: no gradient flows to them,
+    as in PyTorch)."""
+    valid = _T.compare_raw(t.float(), float(ignore_index), "ne")       # [rows]
+    oh = one_hot(t, cols)               # a target outside [0, C) gives a zero row
+    wt = valid if w is None else _k_binary("mul", valid, _T.index_select(
+        w, 0, _k_binary("mul", t.float(), valid).to("int32")))
+    q = _k_binary("mul", oh, reshape_raw(_k_scalar("mul", wt, 1.0 - eps), (rows, 1)))
+    if smooth and eps:
+        wc = full((1, cols), eps / cols) if w is None else \
+            reshape_raw(_k_scalar("mul", w, eps / cols), (1, cols))
+        q = _k_binary("add", q, _k_binary("mul", wc, reshape_raw(valid, (rows, 1))))
+    den = float(_k_reduce("sum", wt, [0]).numpy().reshape(-1)[0])
+    return q, den
+
+
+def _class_loss(logp, q, den, red, rows):
+    """-sum_c q * logp per row, reduced as `red` (0 none, 1 mean over den,
+    2 sum, 3 sum / rows), with recording ops."""
+    per = neg(_T.reduce_sum(mul(logp, q), 1))
+    if red == 0:
+        return per
+    tot = _T.reduce_sum(per)
+    if red == 1:
+        return mul(tot, 1.0 / den)
+    if red == 3:
+        return mul(tot, 1.0 / rows)
+    return tot
+
+
 def cross_entropy(input, target, weight=None, reduction="mean", label_smoothing=0.0, *,
                   ignore_index=-100):
     """F.cross_entropy(input, target, weight, reduction, label_smoothing)
@@ -206,7 +240,10 @@ def cross_entropy(input, target, weight=None, reduction="mean", label_smoothing=
                                                    red, d.data_ptr(), d._strides[0], 0),
                 "cross_entropy_backward")
         return [d]
-    res = _record(out, "CrossEntropy", [x], bwd)
+    def gbwd(g):  # from log_softmax and the constant coefficients, recorded
+        q, den = _class_coef(t, w, rows, cols, eps, ignore_index, True)
+        return _T._regrad(lambda xx: _class_loss(log_softmax(xx, 1), q, den, red, rows), [x], g)
+    res = _record(out, "CrossEntropy", [x], bwd, gfn=gbwd)
     if x is not input and input.ndim == 1 and red == 0:
         res = reshape(res, ())
     return res
@@ -242,7 +279,10 @@ def nll_loss(input, target, weight=None, reduction="mean", *, ignore_index=-100)
                                               int(ignore_index), red, d.data_ptr()),
                 "nll_loss_backward")
         return [d]
-    return _record(out, "NLLLoss", [x], bwd)
+    def gbwd(g):
+        q, den = _class_coef(t, w, rows, cols, 0.0, ignore_index, False)
+        return _T._regrad(lambda xx: _class_loss(xx, q, den, red, rows), [x], g)
+    return _record(out, "NLLLoss", [x], bwd, gfn=gbwd)
 
 
 def mse_loss(input, target, reduction="mean"):
@@ -310,7 +350,18 @@ def layer_norm(x, normalized_shape, weight=None, bias=None, eps=1e-5):
         else:
             L.check(L.lib().tjh_layer_norm_backward(*args, *outs), "layer_norm_backward")
         return [dx, dw, db]
-    return _record(y, "LayerNorm", [x, weight, bias], bwd, acc_slot=0, defer_slots=(1, 2))
+    def gbwd(g):  # the forward from recording ops (layernorm.wgsl's arithmetic)
+        def ref(xx, ww, bb):
+            dims = tuple(range(xx.ndim - k, xx.ndim))
+            xm = sub(xx, reduce_mean(xx, dims, keepdim=True))
+            var = reduce_mean(mul(xm, xm), dims, keepdim=True)
+            yy = mul(xm, (var + float(eps)).pow(-0.5))
+            if ww is not None:
+                yy = mul(yy, ww)
+            return yy if bb is None else _T.add(yy, bb)
+        return _T._regrad(ref, [x, weight, bias], g)
+    return _record(y, "LayerNorm", [x, weight, bias], bwd, acc_slot=0, defer_slots=(1, 2),
+                   gfn=gbwd)
 
 
 # ------------------------------------------------------------ embedding / linear
@@ -344,7 +395,10 @@ def embedding(input, weight):
                                                V, 1 if pending is not None else 0),
                 "embedding_backward")
         return [dw]
-    return _record(out, "Embedding", [weight], bwd, acc_slot=0)
+    def gbwd(g):  # an index_add of the rows (ids clamped as the lookup clamps)
+        ic = _T.tensor(np.clip(ids.numpy().reshape(-1), 0, V - 1).astype(np.int32), dtype="int32")
+        return [_T._index_add_rec((V, D), 0, ic, reshape(g, (n, D)))]
+    return _record(out, "Embedding", [weight], bwd, acc_slot=0, gfn=gbwd)
 
 
 def _embedding_pos(input, weight, pos_weight, pos0=0):
@@ -389,7 +443,18 @@ def _embedding_pos(input, weight, pos_weight, pos0=0):
             1 if pending is not None else 0, dp.data_ptr() if dp is not None else None, P, pos0,
             0), "embedding_pos_backward")
         return [dw, dp]
-    return _record(out, "EmbeddingPos", [weight, pos_weight], bwd, acc_slot=0)
+    def gbwd(g):  # token rows: an index_add; position rows: the batch sum, placed
+        ic = _T.tensor(np.clip(ids.numpy().reshape(-1), 0, V - 1).astype(np.int32), dtype="int32")
+        dw = _T._index_add_rec((V, D), 0, ic, reshape(g, (B * T, D))) if rw else None
+        dp = None
+        if rp:
+            parts = [zeros((pos0, D))] if pos0 else []
+            parts.append(_T.reduce_sum(reshape(g, (B, T, D)), 0))
+            if P - pos0 - T:
+                parts.append(zeros((P - pos0 - T, D)))
+            dp = _T.cat(parts, 0) if len(parts) > 1 else parts[0]
+        return [dw, dp]
+    return _record(out, "EmbeddingPos", [weight, pos_weight], bwd, acc_slot=0, gfn=gbwd)
 
 
 def linear(x, weight, bias=None):
@@ -484,7 +549,9 @@ def _linear_add(x, weight, bias, residual):
             gc = g2 if g2.is_contiguous() else _k_contiguous(g2)
             db = _view_raw(_k_reduce("sum", gc, [0]), (out_f,))
         return [dx, dw, db, g]
-    return _record(out, "LinearAdd", [x, weight, bias, residual], bwd)
+    return _record(out, "LinearAdd", [x, weight, bias, residual], bwd,
+                   gfn=lambda g: _T._regrad(lambda xx, ww, bb, rr: _T.add(rr, linear(xx, ww, bb)),
+                                            [x, weight, bias, residual], g))
 
 
 def _mlp_gelu(x, w1, b1, w2, b2, residual=None):
@@ -547,7 +614,12 @@ def _mlp_gelu(x, w1, b1, w2, b2, residual=None):
             elif need[2]:
                 db1 = _view_raw(_k_reduce("sum", dh, [0]), (hid,))
         return [dx, dw1, db1, dw2, db2, g]
-    return _record(out, "MLP", [x, w1, b1, w2, b2, residual], bwd)
+    def gbwd(g):  # nn.Linear, GELU, nn.Linear (+ residual) from recording ops
+        def ref(xx, a1, c1, a2, c2, rr):
+            yy = linear(gelu(linear(xx, a1, c1)), a2, c2)
+            return yy if rr is None else _T.add(rr, yy)
+        return _T._regrad(ref, [x, w1, b1, w2, b2, residual], g)
+    return _record(out, "MLP", [x, w1, b1, w2, b2, residual], bwd, gfn=gbwd)
 
 
 # ------------------------------------------------------------ convolution
@@ -729,7 +801,15 @@ def scaled_dot_product_attention(query, key, value, attn_mask=None, dropout_p=0.
     out = o
     if three:
         out = _alias(ob, (B, Tq, D), (Tq * D, D, 1), 0)
-    return _record(out, "SDPA", [query, key, value], bwd)
+    def gbwd(g):  # softmax(Q K^T * scale [causal]) V with recording ops
+        def ref(qq, kk, vv):
+            scores = mul(_T.matmul(qq, kk.transpose(-2, -1)), sc)
+            if is_causal:
+                drop = _T.triu(_T.ones((Tq, Tk)), 1)  # key j > query i
+                scores = _T.masked_fill(scores, drop, float("-inf"))
+            return _T.matmul(softmax(scores, -1), vv)
+        return _T._regrad(ref, [query, key, value], g)
+    return _record(out, "SDPA", [query, key, value], bwd, gfn=gbwd)
 
 
 def _sdpa_masked(query, key, value, attn_mask, scale):

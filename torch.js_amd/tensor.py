@@ -2034,7 +2034,8 @@ def triangle(x, diagonal=0, upper=True):
         L.check(L.lib().tjh_triangle(gc.data_ptr(), o.data_ptr(), batch, rows, cols,
                                      int(diagonal), 1 if upper else 0), "triangle_backward")
         return [o]
-    return _record(out, "Triu" if upper else "Tril", [x], bwd)
+    return _record(out, "Triu" if upper else "Tril", [x], bwd,
+                   gfn=lambda g: [triangle(g, diagonal, upper)])
 
 
 def triu(x, diagonal=0):
@@ -2088,15 +2089,19 @@ def clamp(x, min=None, max=None):
         out = _k_contiguous(x)
     xd = x.detach()
 
-    def bwd(g):
+    def mask():
         m = None
         if min is not None:
             m = compare_raw(xd, float(min), "ge")
         if max is not None:
             mx = compare_raw(xd, float(max), "le")
             m = mx if m is None else _k_binary("mul", m, mx)
-        return [_k_binary("mul", g, m)]
-    return _record(out, "Clamp", [x], bwd)
+        return m
+
+    def bwd(g):
+        return [_k_binary("mul", g, mask())]
+    # the pass-through mask is piecewise constant in x: a constant factor
+    return _record(out, "Clamp", [x], bwd, gfn=lambda g: [mul(g, mask())])
 
 
 # ------------------------------------------------------------ reductions
@@ -2219,12 +2224,16 @@ def reduce_minmax(x, dim, keepdim, which):
     out = r if keepdim else _view_raw(r, _squeeze_shape(x.shape, dims))
     xs = x.shape
 
-    def bwd(g):
+    def share():
         mask = compare_raw(x, r, "eq")
         cnt = _k_reduce("sum", mask, dims)
-        w = _k_binary("div", mask, cnt)
-        return [_k_binary("mul", w, _view_raw(g.contiguous(), kshape))]
-    return _record(out, which.capitalize(), [x], bwd)
+        return _k_binary("div", mask, cnt)
+
+    def bwd(g):
+        return [_k_binary("mul", share(), _view_raw(g.contiguous(), kshape))]
+    # the tie shares are piecewise constant in x: a constant factor
+    return _record(out, which.capitalize(), [x], bwd,
+                   gfn=lambda g: [mul(share(), expand(reshape(g, kshape), xs))])
 
 
 def argmax(x, dim=None, keepdim=False, is_min=False):
@@ -2632,7 +2641,22 @@ def index_select(x, dim, index):
         L.check(L.lib().tjh_index_add(z.data_ptr(), outer, src, inner, index.data_ptr(), n,
                                       g.data_ptr()), "index_add")
         return [z]
-    return _record(out, "IndexSelect", [x], bwd)
+    return _record(out, "IndexSelect", [x], bwd,
+                   gfn=lambda g: [_index_add_rec(xs, d, index, g)])
+
+
+def _index_add_rec(xs, d, index, src):
+    """zeros(xs) with src's slices added at `index` along dim d (the ordered
+    index_add of index_select's backward) as a recorded op of src, whose
+    own gradient is index_select of the incoming one: index_select's
+    differentiable backward."""
+    src = src.contiguous()
+    outer, n_src, inner = _numel(xs[:d]), xs[d], _numel(xs[d + 1:])
+    z = zeros(xs)
+    L.check(L.lib().tjh_index_add(z.data_ptr(), outer, n_src, inner, index.data_ptr(),
+                                  index.numel(), src.data_ptr()), "index_add")
+    return _record(z, "IndexAdd", [src], lambda g: [index_select(g, d, index)],
+                   gfn=lambda g: [index_select(g, d, index)])
 
 
 def gather(x, dim, index):
@@ -2660,7 +2684,20 @@ def gather(x, dim, index):
         L.check(L.lib().tjh_scatter_add(z.data_ptr(), outer, src, inner, index.data_ptr(), ilen,
                                         g.data_ptr()), "scatter_add")
         return [z]
-    return _record(out, "Gather", [x], bwd)
+    return _record(out, "Gather", [x], bwd, gfn=lambda g: [_scatter_add_rec(xs, d, index, g)])
+
+
+def _scatter_add_rec(xs, d, index, src):
+    """zeros(xs) with src scattered-added at `index` along dim d (gather's
+    ordered backward) as a recorded op of src, whose own gradient is the
+    gather of the incoming one: gather's differentiable backward."""
+    src = src.contiguous()
+    outer, n_src, inner = _numel(xs[:d]), xs[d], _numel(xs[d + 1:])
+    z = zeros(xs)
+    L.check(L.lib().tjh_scatter_add(z.data_ptr(), outer, n_src, inner, index.data_ptr(),
+                                    index.shape[d], src.data_ptr()), "scatter_add")
+    return _record(z, "ScatterAdd", [src], lambda g: [gather(g, d, index)],
+                   gfn=lambda g: [gather(g, d, index)])
 
 
 def _take_along(x, d, index):
@@ -3037,6 +3074,65 @@ def _toposort(roots):
             if t is not None and t.grad_fn is not None and id(t.grad_fn) not in seen:
                 stack.append((t.grad_fn, False))
     return order  # post-order: inputs before users
+
+
+def _graph_vjp(out, g, inputs):
+    """Recording VJP of the subgraph between `inputs` and `out`: the
+    create_graph sweep run from `out` with gradient g, stopping at the
+    inputs (nothing past them is visited).  Returns their gradients (None
+    for an input the output does not depend on), which carry graphs back
+    to g and to the inputs."""
+    stop = {id(t) for t in inputs if t is not None}
+    res = [None] * len(inputs)
+    if out.grad_fn is None:
+        return res
+    order, seen = [], set()
+    stack = [(out.grad_fn, False)]
+    while stack:
+        node, done = stack.pop()
+        if done:
+            order.append(node)
+            continue
+        if id(node) in seen:
+            continue
+        seen.add(id(node))
+        stack.append((node, True))
+        for t in node.inputs:
+            if t is not None and id(t) not in stop and t.grad_fn is not None \
+                    and id(t.grad_fn) not in seen:
+                stack.append((t.grad_fn, False))
+    grads = {id(out.grad_fn): g}
+    found = {}
+    for node in reversed(order):
+        gn = grads.pop(id(node), None)
+        if gn is None:
+            continue
+        if node.gfn is None:
+            raise NotImplementedError(
+                "create_graph: %s has no differentiable backward on the hip device" % node.name)
+        for t, gi in zip(node.inputs, node.gfn(gn)):
+            if t is None or gi is None:
+                continue
+            if tuple(gi.shape) != t.shape:
+                gi = _sum_to_g(gi, t.shape) if gi.ndim >= t.ndim else reshape(gi, t.shape)
+            if id(t) in stop:
+                found[id(t)] = gi if id(t) not in found else add(found[id(t)], gi)
+            elif t.grad_fn is not None:
+                k = id(t.grad_fn)
+                grads[k] = gi if k not in grads else add(grads[k], gi)
+    return [found.get(id(t)) if t is not None else None for t in inputs]
+
+
+def _regrad(fn, inputs, g):
+    """Recording VJP of a fused op from its definition: fn(*inputs) written
+    with recording (differentiable) ops is recomputed in grad mode and its
+    subgraph differentiated down to the inputs (_graph_vjp)."""
+    prev = _grad["enabled"]
+    _grad["enabled"] = True
+    try:
+        return _graph_vjp(fn(*inputs), g, inputs)
+    finally:
+        _grad["enabled"] = prev
 
 
 def _run_backward_graph(pairs, retain_graph, inputs):
