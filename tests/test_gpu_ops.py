@@ -700,6 +700,32 @@ def test_gemm_every_tile(torch, monkeypatch, tile, ta, tb, M, N, K):
     check_floor(got, want, ref32)
 
 
+@pytest.mark.parametrize("tile", ["256x128", "128x128", "128x64", "64x64", "256x256"])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_gemm_odd_strides_every_tile(torch, monkeypatch, tile, ta, tb):
+    """Operands whose rows start at any 4-byte boundary (odd row strides,
+    base pointers one float past a 16-byte boundary) load 128 bits per
+    access in the unguarded interior kernel: every tile and layout, with an
+    interior block, edge strips and a K remainder."""
+    from torchjs_amd import _lib as L
+    monkeypatch.setenv("TJH_GEMM_TILE", tile)
+    M, N, K = 300, 260, 203
+    r = np.random.default_rng(M + N + K + 2 * ta + tb)
+    ar, ac = (K, M) if ta else (M, K)
+    br, bc = (N, K) if tb else (K, N)
+    lda, ldb = ac + 3, bc + 1  # odd row strides
+    Ab = f32(r.standard_normal(1 + ar * lda))
+    Bb = f32(r.standard_normal(1 + br * ldb))
+    A = Ab[1:].reshape(ar, lda)[:, :ac]
+    B = Bb[1:].reshape(br, ldb)[:, :bc]
+    a, b = torch.tensor(Ab), torch.tensor(Bb)
+    c = torch.tensor(np.zeros((M, N), np.float32))
+    L.check(L.lib().tjh_gemm(ta, tb, M, N, K, 1.0, a.data_ptr() + 4, lda, 0, b.data_ptr() + 4,
+                             ldb, 0, 0.0, c.data_ptr(), N, 0, 1, None, 0), "gemm")
+    opA, opB = (A.T if ta else A), (B.T if tb else B)
+    check_floor(c.numpy(), opA.astype(np.float64) @ opB.astype(np.float64), opA @ opB)
+
+
 @pytest.mark.parametrize("forced", [None, "256x256"])
 def test_gemm_long_k_input_gradient(torch, monkeypatch, forced):
     """A . B with K = 50257 (the LM head's input gradient, dlogits . W), at

@@ -28,8 +28,11 @@
 // MFMA operand layout (32x32x2 f32): lane l feeds A[m = l%32][k = l/32] and
 //   B[k = l/32][n = l%32]; accumulator register r of lane l holds
 //   C[8*(r/4) + 4*(l/32) + r%4][l%32].
-// Global loads are 128-bit when the operand's contiguous dimension and row
-// stride allow it; edge tiles fall back to guarded scalar loads.
+// Operand loads are 128-bit at any 4-byte alignment (HSA runs the GPU in
+// unaligned-access mode; the compiler itself emits such loads for packed
+// data), so an odd row stride — the 50257-wide logits — still loads a
+// float4 per access; only runs that cross the problem's edge go
+// element-wise.
 // Workgroup order: tiles are grouped 8 M-tiles at a time so neighbouring
 // tiles share B columns, and each XCD receives a contiguous run of that
 // order so the sharing happens inside one L2.
@@ -52,6 +55,9 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 // of a reinterpret_cast load is not always split into registers by the
 // compiler and then lives in scratch memory.
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+// The same vector at 4-byte alignment: operand rows start wherever the row
+// stride puts them.
+typedef float floatx4u __attribute__((ext_vector_type(4), aligned(4)));
 
 struct GemmArgs {
   const float* A;
@@ -97,11 +103,11 @@ __device__ __forceinline__ float epilogue_act(const GemmArgs& g, int64_t row, in
 // Loads a logical OUTER x BK tile (outer = m for A, n for B) for this lane:
 // V float4 per lane.  !TRANS: storage [outer][k] (k contiguous, 4 float4
 // per outer row); TRANS: storage [k][outer] (outer contiguous).
-// EDGE == false: the caller guarantees the tile is in bounds and 16-byte
-// aligned, so every load is an unconditional 128-bit load.  EDGE == true:
-// every 4-run is bounds-checked (tiles on the problem's edge); `vec` (the
-// operand is 16-byte aligned with a row stride divisible by 4) lets runs
-// that are wholly in bounds load as one 128-bit access.
+// EDGE == false: the caller guarantees the tile is in bounds, so every load
+// is an unconditional 128-bit load.  EDGE == true: every 4-run is
+// bounds-checked (tiles on the problem's edge); `vec` (the operand is
+// 4-byte aligned) lets runs that are wholly in bounds load as one 128-bit
+// access.
 template <bool TRANS, int OUTER, int V, bool EDGE, int T>
 __device__ __forceinline__ void load_tile(const float* __restrict__ P, int64_t ld, int64_t rows,
                                           int64_t cols, int64_t r0, int64_t c0, bool vec,
@@ -113,11 +119,11 @@ __device__ __forceinline__ void load_tile(const float* __restrict__ P, int64_t l
     if (!EDGE) {
       if (!TRANS) {
         int o = f >> 2, kq = f & 3;
-        reg[i] = *reinterpret_cast<const floatx4*>(P + (r0 + o) * ld + c0 + kq * 4);
+        reg[i] = *reinterpret_cast<const floatx4u*>(P + (r0 + o) * ld + c0 + kq * 4);
       } else {
         constexpr int Q = OUTER / 4;
         int k = f / Q, oq = f % Q;
-        reg[i] = *reinterpret_cast<const floatx4*>(P + (c0 + k) * ld + r0 + oq * 4);
+        reg[i] = *reinterpret_cast<const floatx4u*>(P + (c0 + k) * ld + r0 + oq * 4);
       }
     } else {
       // guarded: a 4-run wholly in bounds of an aligned operand is still
@@ -127,7 +133,7 @@ __device__ __forceinline__ void load_tile(const float* __restrict__ P, int64_t l
         int o = f >> 2, kq = f & 3;
         int64_t go = r0 + o, gk = c0 + kq * 4;
         if (vec && go < rows && gk + 3 < cols) {
-          reg[i] = *reinterpret_cast<const floatx4*>(P + go * ld + gk);
+          reg[i] = *reinterpret_cast<const floatx4u*>(P + go * ld + gk);
           continue;
         }
 #pragma unroll
@@ -138,7 +144,7 @@ __device__ __forceinline__ void load_tile(const float* __restrict__ P, int64_t l
         int k = f / Q, oq = f % Q;
         int64_t gk = c0 + k, go = r0 + oq * 4;
         if (vec && gk < cols && go + 3 < rows) {
-          reg[i] = *reinterpret_cast<const floatx4*>(P + gk * ld + go);
+          reg[i] = *reinterpret_cast<const floatx4u*>(P + gk * ld + go);
           continue;
         }
 #pragma unroll
@@ -799,8 +805,8 @@ int tjh::gemm(const char* family, int transA, int transB, int64_t M, int64_t N, 
   g.lda = lda; g.ldb = ldb; g.ldc = ldc;
   g.sA = strideA; g.sB = strideB; g.sC = strideC;
   g.alpha = alpha; g.beta = beta; g.bias_mode = bias_mode;
-  g.vecA = aligned16(A) && (lda % 4 == 0) && (strideA % 4 == 0);
-  g.vecB = aligned16(B) && (ldb % 4 == 0) && (strideB % 4 == 0);
+  g.vecA = ((uintptr_t)A & 3) == 0;
+  g.vecB = ((uintptr_t)B & 3) == 0;
   g.tiles_m = g.tiles_n = 0;
   g.kchunk = BK;
   g.ws = nullptr;
@@ -814,7 +820,7 @@ int tjh::gemm(const char* family, int transA, int transB, int64_t M, int64_t N, 
   const Plan plan = choose_plan(M, N, K, batch, cus, transA, transB);
   const TileCfg& tc = kTiles[plan.tile];
   if (!(g.vecA && g.vecB)) {
-    // unaligned operands: guarded loads everywhere
+    // operands not 4-byte aligned: guarded scalar loads everywhere
     return run_block(plan.tile, g, transA, transB, plan.splits, batch, true, cus);
   }
   // Interior block [0,Mm) x [0,Nm) x [0,Km) runs the unguarded kernel; the
