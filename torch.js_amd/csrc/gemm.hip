@@ -285,9 +285,15 @@ __device__ __forceinline__ void read_frags(const float* __restrict__ S, int oute
 // receives the contiguous run [x*n/8, (x+1)*n/8) of the grouped tile order
 // keeps the tiles that share A rows and B columns on one L2.  A bijection on
 // [0, n): ids past the last multiple of 8 keep their number.
-// Lanes per workgroup: 2 x 2 waves, or 4 x 2 waves for 256-row tiles
-// (each wave keeps a 64 x BN/2 sub-tile; B is shared by four waves).
-constexpr int gemm_threads(int bm) { return bm >= 256 ? 512 : 256; }
+// Waves per workgroup: WR rows x 2 columns, each wave keeping a
+// (BM / WR) x (BN / 2) sub-tile: 2 x 2 waves, or 4 x 2 for the 8-wave
+// 256-row tiles (B shared by four waves).
+constexpr int gemm_threads(int wr) { return wr * 128; }
+// Wave tiles of 64 x 128 or more run two waves per SIMD (their
+// accumulators alone take 128 registers), smaller ones four.
+constexpr int gemm_waves_per_simd(int bm, int bn, int wr) {
+  return (bm / wr) * (bn / 2) >= 64 * 128 ? 2 : 4;
+}
 
 constexpr int kXcds = 8;
 __device__ __forceinline__ int xcd_tile(int bid, int n) {
@@ -296,18 +302,20 @@ __device__ __forceinline__ int xcd_tile(int bid, int n) {
   return (bid % kXcds) * (full / kXcds) + bid / kXcds;
 }
 
-template <int BM, int BN, bool TA, bool TB, bool EDGE, bool XF = false>
-__global__ __launch_bounds__(gemm_threads(BM), BN >= 256 ? 2 : 4) void k_gemm(GemmArgs g) {
+template <int BM, int BN, int WR, bool TA, bool TB, bool EDGE, bool XF = false>
+__global__ __launch_bounds__(gemm_threads(WR), gemm_waves_per_simd(BM, BN, WR)) void k_gemm(
+    GemmArgs g) {
   constexpr int LA = BM + 4, LB = BN + 4;       // LDS row lengths
-  constexpr int WM = BM / (gemm_threads(BM) / 128), WN = BN / 2;  // wave tile: (T/128) x 2 waves
+  constexpr int WM = BM / WR, WN = BN / 2;      // wave tile: WR x 2 waves
   constexpr int FM = WM / 32, FN = WN / 32;     // MFMA blocks per wave
-  constexpr int T = gemm_threads(BM);
+  constexpr int T = gemm_threads(WR);
   constexpr int VA = BM * BK / (T * 4);  // float4 loads per lane
   constexpr int VB = BN * BK / (T * 4);
   static_assert(FM >= 1 && FN >= 1 && VA >= 1 && VB >= 1, "tile too small");
   // A with k contiguous is staged [m][k] (128-bit stores and reads).  B
   // stays k-major: staging a k-contiguous B as [n][k] measured slower on
-  // the forward products (A . B^T) of GPT-2's shapes.
+  // the forward products (A . B^T) of GPT-2's shapes (on the 4-wave
+  // 256 x 128 tile too: 470 against 378 us for 8192 x 3072 x 768).
   constexpr bool AKC = !TA, BKC = false;
   constexpr int SA = AKC ? BM * KS : BK * LA, SB = BKC ? BN * KS : BK * LB;
   __shared__ __attribute__((aligned(16))) float As[2][SA];
@@ -363,9 +371,9 @@ __global__ __launch_bounds__(gemm_threads(BM), BN >= 256 ? 2 : 4) void k_gemm(Ge
   int ct[XF ? VA : 1];
   // PF2: two register sets in flight (tile t + 2 is fetched while tile t's
   // MFMAs run, and tile t + 1, fetched one K step earlier, is stored after
-  // them), for the 256 x 256 tile, whose one workgroup per CU has no other
-  // workgroup to cover the fetch of the next tile
-  constexpr bool PF2 = BN >= 256 && !XF;
+  // them), for the tiles at two waves per SIMD, where few other waves cover
+  // the fetch of the next tile
+  constexpr bool PF2 = gemm_waves_per_simd(BM, BN, WR) == 2 && !XF && (WR == 4 || TA);
   floatx4 ra2[VA], rb2[VB];
   auto fetch = [&](int64_t k0, floatx4 (&xa)[VA], floatx4 (&xb)[VB]) {
     load_tile<TA, BM, VA, EDGE, T>(A, g.lda, g.M, kend, m0, k0, g.vecA, xa);
@@ -619,9 +627,10 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(GemmArgs g, int splits) {
 // ------------------------------------------------------------ tile choice
 
 struct TileCfg {
-  int bm, bn;
+  int bm, bn, wr;  // block tile, wave rows (2 wave columns)
 };
-constexpr TileCfg kTiles[] = {{256, 128}, {128, 128}, {128, 64}, {64, 64}, {256, 256}};
+constexpr TileCfg kTiles[] = {{256, 128, 4}, {128, 128, 2}, {128, 64, 2},
+                              {64, 64, 2},   {256, 256, 4}, {256, 128, 2}};
 constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
 
 // Measured relative per-FLOP throughput of each tile with the CUs full, by
@@ -630,9 +639,9 @@ constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
 // CUs with it (the LM head's three, the 3072-wide ones); 128x64 is 3-5%
 // slower per FLOP and wins only where the larger tiles leave CUs idle.
 float tile_speed(int ti, int ta, int tb) {
-  static const float nt[kNumTiles] = {1.04f, 1.00f, 0.95f, 0.85f, 0.0f};
-  static const float nn[kNumTiles] = {1.03f, 1.00f, 0.97f, 0.85f, 1.10f};
-  static const float tn[kNumTiles] = {1.03f, 1.00f, 0.97f, 0.85f, 1.10f};
+  static const float nt[kNumTiles] = {1.04f, 1.00f, 0.95f, 0.85f, 0.0f, 0.0f};
+  static const float nn[kNumTiles] = {1.03f, 1.00f, 0.97f, 0.85f, 1.10f, 0.0f};
+  static const float tn[kNumTiles] = {1.03f, 1.00f, 0.97f, 0.85f, 1.10f, 1.04f};
   if (!ta && tb) return nt[ti];
   if (!ta && !tb) return nn[ti];
   if (ta && !tb) return tn[ti];
@@ -693,7 +702,8 @@ int64_t wide_splits(int64_t tiles, int64_t K, int cus) {
 
 // Picks tile and split maximising (useful fraction of padded work) x
 // (CU fill) x tile speed.  TJH_GEMM_TILE=BMxBN forces a tile (read on every
-// call, so a test can sweep the tiles in one process).  The 8-wave 256x128
+// call, so a test can sweep the tiles in one process; the 4-wave 256 x 128
+// tile is 256x128w4).  The 8-wave 256x128
 // tile needs more K splits than 128x128 for the same fill, which doubles
 // the split-sum traffic: it is taken only with no K split (measured on the
 // GPT-2 products, the best of three interleaved runs each: the split
@@ -705,7 +715,9 @@ Plan choose_plan(int64_t M, int64_t N, int64_t K, int64_t batch, int cus, int ta
   if (const char* e = getenv("TJH_GEMM_TILE")) {
     for (int i = 0; i < kNumTiles; ++i) {
       char buf[32];
-      snprintf(buf, sizeof(buf), "%dx%d", kTiles[i].bm, kTiles[i].bn);
+      // the 4-wave 256 x 128 tile is named 256x128w4
+      snprintf(buf, sizeof(buf), "%dx%d%s", kTiles[i].bm, kTiles[i].bn,
+               kTiles[i].bm / kTiles[i].wr > 64 ? "w4" : "");
       if (strcmp(buf, e) == 0) forced = i;
     }
   }
@@ -728,7 +740,12 @@ Plan choose_plan(int64_t M, int64_t N, int64_t K, int64_t batch, int cus, int ta
     int64_t tiles = tm * tn * batch;
     int64_t s = choose_splits(tiles, K, cus);
     if (wide && ta && s == 1) s = wide_splits(tiles, K, cus);
-    if (t.bm >= 256 && !wide && forced < 0 && s > 1) continue;
+    // 4-wave 256 x 128 (128 x 64 per wave, two workgroups per CU): only for
+    // A^T . B over K slices of >= 1024 (GPT-2's 3072 x 768 weight
+    // gradients over 7 slices: 351 against 363 us; 3-4% slower over the 14
+    // and 28 slices of the smaller ones, and on every A . B and A . B^T)
+    if (i == 5 && forced < 0 && (!ta || tb || K / s < 1024)) continue;
+    if (t.bm >= 256 && t.wr == 4 && !wide && forced < 0 && s > 1) continue;
     double score = useful * fill_of(tiles * s, cus) * tile_speed(i, ta, tb);
     if (tiles * s < cus) score *= (double)(tiles * s) / cus;
     if (score > best_score + 1e-9) {
@@ -739,40 +756,40 @@ Plan choose_plan(int64_t M, int64_t N, int64_t K, int64_t batch, int cus, int ta
   return best;
 }
 
-template <int BM, int BN, bool EDGE>
+template <int BM, int BN, int WR, bool EDGE>
 void launch_e(const GemmArgs& g, dim3 grid, int ta, int tb) {
+  const dim3 block(gemm_threads(WR));
   if (g.xrow) {  // A formed from logits: B is never transposed here
     if (ta)
-      tjh_launch((k_gemm<BM, BN, true, false, EDGE, true>), grid, dim3(gemm_threads(BM)), 0,
-                 stream(), g);
+      tjh_launch((k_gemm<BM, BN, WR, true, false, EDGE, true>), grid, block, 0, stream(), g);
     else
-      tjh_launch((k_gemm<BM, BN, false, false, EDGE, true>), grid, dim3(gemm_threads(BM)), 0,
-                 stream(), g);
+      tjh_launch((k_gemm<BM, BN, WR, false, false, EDGE, true>), grid, block, 0, stream(), g);
     return;
   }
   if (!ta && !tb)
-    tjh_launch((k_gemm<BM, BN, false, false, EDGE>), grid, dim3(gemm_threads(BM)), 0, stream(), g);
+    tjh_launch((k_gemm<BM, BN, WR, false, false, EDGE>), grid, block, 0, stream(), g);
   else if (!ta && tb)
-    tjh_launch((k_gemm<BM, BN, false, true, EDGE>), grid, dim3(gemm_threads(BM)), 0, stream(), g);
+    tjh_launch((k_gemm<BM, BN, WR, false, true, EDGE>), grid, block, 0, stream(), g);
   else if (ta && !tb)
-    tjh_launch((k_gemm<BM, BN, true, false, EDGE>), grid, dim3(gemm_threads(BM)), 0, stream(), g);
+    tjh_launch((k_gemm<BM, BN, WR, true, false, EDGE>), grid, block, 0, stream(), g);
   else
-    tjh_launch((k_gemm<BM, BN, true, true, EDGE>), grid, dim3(gemm_threads(BM)), 0, stream(), g);
+    tjh_launch((k_gemm<BM, BN, WR, true, true, EDGE>), grid, block, 0, stream(), g);
 }
 
-template <int BM, int BN>
+template <int BM, int BN, int WR>
 void launch(const GemmArgs& g, dim3 grid, int ta, int tb, bool edge) {
-  if (edge) launch_e<BM, BN, true>(g, grid, ta, tb);
-  else launch_e<BM, BN, false>(g, grid, ta, tb);
+  if (edge) launch_e<BM, BN, WR, true>(g, grid, ta, tb);
+  else launch_e<BM, BN, WR, false>(g, grid, ta, tb);
 }
 
 void launch_tile(int ti, const GemmArgs& g, dim3 grid, int ta, int tb, bool edge) {
   switch (ti) {
-    case 0: launch<256, 128>(g, grid, ta, tb, edge); break;
-    case 1: launch<128, 128>(g, grid, ta, tb, edge); break;
-    case 2: launch<128, 64>(g, grid, ta, tb, edge); break;
-    case 4: launch<256, 256>(g, grid, ta, tb, edge); break;
-    default: launch<64, 64>(g, grid, ta, tb, edge); break;
+    case 0: launch<256, 128, 4>(g, grid, ta, tb, edge); break;
+    case 1: launch<128, 128, 2>(g, grid, ta, tb, edge); break;
+    case 2: launch<128, 64, 2>(g, grid, ta, tb, edge); break;
+    case 4: launch<256, 256, 4>(g, grid, ta, tb, edge); break;
+    case 5: launch<256, 128, 2>(g, grid, ta, tb, edge); break;
+    default: launch<64, 64, 2>(g, grid, ta, tb, edge); break;
   }
 }
 
