@@ -88,6 +88,12 @@ struct GemmArgs {
   int64_t xm0, xk0;
 };
 
+// A compile-time int carried by a value (dispatch into generic lambdas).
+template <int V>
+struct IConst {
+  static constexpr int value = V;
+};
+
 // The activation epilogue, shared by the GEMM and the split-K sum.
 __device__ __forceinline__ float epilogue_act(const GemmArgs& g, int64_t row, int64_t col,
                                               float v) {
@@ -321,6 +327,13 @@ __global__ __launch_bounds__(gemm_threads(WR), gemm_waves_per_simd(BM, BN, WR)) 
   __shared__ __attribute__((aligned(16))) float As[2][SA];
   __shared__ __attribute__((aligned(16))) float Bs[2][SB];
 
+  // Wave priority: the prologue and the epilogue run at raised priority.
+  // Two workgroups share a CU, and at equal priority the one in its
+  // epilogue (address arithmetic and stores) barely advances while the
+  // other issues MFMAs: its stores drained only when the other's main loop
+  // ended, ~40 us per launch for GPT-2's 8192 x 3072 products, and its
+  // successor could not start.
+  __builtin_amdgcn_s_setprio(3);
   // ---- tile coordinates (grouped ordering for L2 reuse)
   const int tiles_m = g.tiles_m, tiles_n = g.tiles_n;
   int bid = xcd_tile(blockIdx.x, gridDim.x);
@@ -462,6 +475,7 @@ __global__ __launch_bounds__(gemm_threads(WR), gemm_waves_per_simd(BM, BN, WR)) 
   }
   stage(0, ra, rb);
   __syncthreads();
+  __builtin_amdgcn_s_setprio(0);
 
   if constexpr (PF2) {
     // tile t sits in LDS buffer t % 2 and, until staged, in register set
@@ -506,6 +520,7 @@ __global__ __launch_bounds__(gemm_threads(WR), gemm_waves_per_simd(BM, BN, WR)) 
     }
   }
 
+  __builtin_amdgcn_s_setprio(3);
   if (row_sums) {
     // lanes t, t + BM, ... hold slices of row t: combined in that order.
     // The staging tiles are free here (the K loop ended on a barrier).
@@ -525,43 +540,76 @@ __global__ __launch_bounds__(gemm_threads(WR), gemm_waves_per_simd(BM, BN, WR)) 
   }
 
   // ---- epilogue
-  if (g.ws) {
-    // raw partial sums; the reduce kernel applies alpha / beta / bias
-    float* __restrict__ W = g.ws + ((int64_t)b * gridDim.y + blockIdx.y) * g.M * g.N;
+  // Element (i, j, r) of this wave sits at row r0 + ro(i, r), column
+  // c0 + 32 j, with ro = 32 i + 8 (r / 4) + r % 4.  Addresses are one base
+  // per lane plus a uniform row offset (ro x ld, scalar arithmetic), and
+  // the beta / bias / activation choice is made once, not per element:
+  // the epilogue runs beside the other workgroup's MFMAs, where every
+  // vector instruction it issues is slow.
+  const int64_t r0 = m0 + wm * WM + 4 * h, c0 = n0 + wn * WN + l32;
+  auto each = [&](auto&& put) {
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
-        const int64_t col = n0 + wn * WN + j * 32 + l32;
-        if (col >= g.N) continue;
+        if (EDGE && c0 + j * 32 >= g.N) continue;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const int64_t row = m0 + wm * WM + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-          if (row < g.M) W[row * g.N + col] = acc[i][j][r];
+          const int ro = i * 32 + 8 * (r >> 2) + (r & 3);
+          if (!EDGE || r0 + ro < g.M) put(acc[i][j][r], ro, j * 32);
         }
       }
+  };
+  if (g.ws) {
+    // raw partial sums; the reduce kernel applies alpha / beta / bias
+    float* __restrict__ W =
+        g.ws + ((int64_t)b * gridDim.y + blockIdx.y) * g.M * g.N + r0 * g.N + c0;
+    const int64_t ld = g.N;
+    each([&](float a, int ro, int co) { W[ro * ld + co] = a; });
     return;
   }
-#pragma unroll
-  for (int i = 0; i < FM; ++i) {
-#pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      const int64_t col = n0 + wn * WN + j * 32 + l32;
-      if (col >= g.N) continue;
-      float bn = (g.bias_mode == 1) ? g.bias[col] : 0.f;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t row = m0 + wm * WM + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-        if (row < g.M) {
-          float v = g.alpha * acc[i][j][r];
-          float* cp = C + row * g.ldc + col;
-          if (g.beta != 0.f) v += g.beta * *cp;
-          if (g.bias_mode == 1) v += bn;
-          else if (g.bias_mode == 2) v += g.bias[row];
-          *cp = epilogue_act(g, row, col, v);
+  float* __restrict__ Cb = C + r0 * g.ldc + c0;
+  const int64_t ldc = g.ldc, ldx = g.ldaux;
+  float* __restrict__ Xb = g.aux ? g.aux + r0 * ldx + c0 : nullptr;
+  const float alpha = g.alpha;
+  const bool nobias = g.bias_mode == 0 || g.bias_mode >= 3;  // 3, 4: row sums, no add
+  if (g.beta == 0.f && nobias && g.act == 0) {
+    each([&](float a, int ro, int co) { Cb[ro * ldc + co] = alpha * a; });
+  } else if (g.beta == 0.f && g.bias_mode == 1 && (g.act == 0 || g.act == 1 || g.act == 3)) {
+    // bias per column (+ GELU with its input kept, or + residual)
+    const float* __restrict__ bb = g.bias + c0;
+    const int act = g.act;
+    auto run = [&](auto ACT) {
+      constexpr int A = decltype(ACT)::value;
+      each([&](float a, int ro, int co) {
+        float v = alpha * a + bb[co];
+        if (A == 1) {
+          Xb[ro * ldx + co] = v;
+          v = gelu_f(v);
+        } else if (A == 3) {
+          v += Xb[ro * ldx + co];
         }
-      }
-    }
+        Cb[ro * ldc + co] = v;
+      });
+    };
+    if (act == 0) run(IConst<0>());
+    else if (act == 1) run(IConst<1>());
+    else run(IConst<3>());
+  } else if (g.beta == 0.f && nobias && g.act == 2) {
+    // the GELU gradient of the kept input
+    each([&](float a, int ro, int co) {
+      Cb[ro * ldc + co] = alpha * a * gelu_grad(Xb[ro * ldx + co]);
+    });
+  } else {
+    each([&](float a, int ro, int co) {
+      const int64_t row = r0 + ro, col = c0 + co;
+      float v = alpha * a;
+      float* cp = Cb + ro * ldc + co;
+      if (g.beta != 0.f) v += g.beta * *cp;
+      if (g.bias_mode == 1) v += g.bias[col];
+      else if (g.bias_mode == 2) v += g.bias[row];
+      *cp = epilogue_act(g, row, col, v);
+    });
   }
 }
 
