@@ -682,7 +682,7 @@ def test_gemm_layouts(torch, M, N, K, ta, tb):
 
 
 @pytest.mark.parametrize("tile", ["256x128", "128x128", "128x64", "64x64", "256x256",
-                                  "256x128w4"])
+                                  "256x128w4", "256x192"])
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
 @pytest.mark.parametrize("M,N,K", [(300, 260, 200), (256, 128, 4096)])
 def test_gemm_every_tile(torch, monkeypatch, tile, ta, tb, M, N, K):
@@ -702,7 +702,7 @@ def test_gemm_every_tile(torch, monkeypatch, tile, ta, tb, M, N, K):
 
 
 @pytest.mark.parametrize("tile", ["256x128", "128x128", "128x64", "64x64", "256x256",
-                                  "256x128w4"])
+                                  "256x128w4", "256x192"])
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
 def test_gemm_odd_strides_every_tile(torch, monkeypatch, tile, ta, tb):
     """Operands whose rows start at any 4-byte boundary (odd row strides,
@@ -757,7 +757,8 @@ def test_gemm_vocab_rows_weight_gradient(torch):
     check_floor(got, want, A.T @ B)
 
 
-@pytest.mark.parametrize("tile", ["256x128", "128x128", "128x64", "64x64", "256x128w4"])
+@pytest.mark.parametrize("tile", ["256x128", "128x128", "128x64", "64x64", "256x128w4",
+                                  "256x192"])
 @pytest.mark.parametrize("ta", [0, 1])
 @pytest.mark.parametrize("M,N,K", [(300, 260, 200), (256, 128, 4096), (768, 192, 8192), (5, 3, 7)])
 def test_gemm_row_sums(torch, monkeypatch, tile, ta, M, N, K):
@@ -1564,7 +1565,8 @@ def _ln_chain_input(x0, gms, bts):
     return ops.layer_norm(h + x, gms[0], bts[0])[0]
 
 
-@pytest.mark.parametrize("tile", ["256x128", "128x128", "128x64", "64x64", "256x128w4"])
+@pytest.mark.parametrize("tile", ["256x128", "128x128", "128x64", "64x64", "256x128w4",
+                                  "256x192"])
 @pytest.mark.parametrize("red", ["mean", "sum", "none"])
 def test_gemm_ce_equals_stored_gradient(torch, monkeypatch, tile, red):
     """tjh_gemm_ce in both orientations (dx = dlogits W, dW = dlogits^T x)
@@ -1670,7 +1672,8 @@ def test_lm_head_cross_entropy_formed_in_gemms(torch, monkeypatch, red):
         assert np.array_equal(a, b)
 
 
-@pytest.mark.parametrize("tile", ["256x128", "128x128", "128x64", "64x64", "256x128w4"])
+@pytest.mark.parametrize("tile", ["256x128", "128x128", "128x64", "64x64", "256x128w4",
+                                  "256x192"])
 def test_gemm_epilogue_activations_every_tile(torch, monkeypatch, tile):
     """The fused epilogues on every tile (interior, edge strips, K
     remainder): act 1 writes the pre-activation and GELU of it, act 2

@@ -119,9 +119,14 @@ __device__ __forceinline__ void load_tile(const float* __restrict__ P, int64_t l
                                           int64_t cols, int64_t r0, int64_t c0, bool vec,
                                           floatx4 (&reg)[V]) {
   const int t = threadIdx.x;
+  constexpr int NF = OUTER * BK / 4;  // float4s in the tile (the last pass may be partial)
 #pragma unroll
   for (int i = 0; i < V; ++i) {
     int f = t + T * i;
+    if (NF % T != 0 && f >= NF) {
+      reg[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+      continue;
+    }
     if (!EDGE) {
       if (!TRANS) {
         int o = f >> 2, kq = f & 3;
@@ -170,9 +175,11 @@ constexpr int KS = BK + 4;  // [outer][k] row length: 16-lane groups of 128-bit 
 template <bool TRANS, bool KC, int OUTER, int V, int W, int T>
 __device__ __forceinline__ void store_tile(float* __restrict__ S, const floatx4 (&reg)[V]) {
   const int t = threadIdx.x;
+  constexpr int NF = OUTER * BK / 4;
 #pragma unroll
   for (int i = 0; i < V; ++i) {
     int f = t + T * i;
+    if (NF % T != 0 && f >= NF) continue;
     if (!TRANS && KC) {
       int o = f >> 2, kq = f & 3;
       *reinterpret_cast<floatx4*>(S + o * KS + kq * 4) = reg[i];
@@ -295,10 +302,10 @@ __device__ __forceinline__ void read_frags(const float* __restrict__ S, int oute
 // (BM / WR) x (BN / 2) sub-tile: 2 x 2 waves, or 4 x 2 for the 8-wave
 // 256-row tiles (B shared by four waves).
 constexpr int gemm_threads(int wr) { return wr * 128; }
-// Wave tiles of 64 x 128 or more run two waves per SIMD (their
-// accumulators alone take 128 registers), smaller ones four.
+// Wave tiles of 64 x 96 or more run two waves per SIMD (their
+// accumulators alone take 96 registers or more), smaller ones four.
 constexpr int gemm_waves_per_simd(int bm, int bn, int wr) {
-  return (bm / wr) * (bn / 2) >= 64 * 128 ? 2 : 4;
+  return (bm / wr) * (bn / 2) >= 64 * 96 ? 2 : 4;
 }
 
 constexpr int kXcds = 8;
@@ -315,8 +322,8 @@ __global__ __launch_bounds__(gemm_threads(WR), gemm_waves_per_simd(BM, BN, WR)) 
   constexpr int WM = BM / WR, WN = BN / 2;      // wave tile: WR x 2 waves
   constexpr int FM = WM / 32, FN = WN / 32;     // MFMA blocks per wave
   constexpr int T = gemm_threads(WR);
-  constexpr int VA = BM * BK / (T * 4);  // float4 loads per lane
-  constexpr int VB = BN * BK / (T * 4);
+  constexpr int VA = (BM * BK / 4 + T - 1) / T;  // float4 loads per lane (last pass may be partial)
+  constexpr int VB = (BN * BK / 4 + T - 1) / T;
   static_assert(FM >= 1 && FN >= 1 && VA >= 1 && VB >= 1, "tile too small");
   // A with k contiguous is staged [m][k] (128-bit stores and reads).  B
   // stays k-major: staging a k-contiguous B as [n][k] measured slower on
@@ -677,8 +684,8 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(GemmArgs g, int splits) {
 struct TileCfg {
   int bm, bn, wr;  // block tile, wave rows (2 wave columns)
 };
-constexpr TileCfg kTiles[] = {{256, 128, 4}, {128, 128, 2}, {128, 64, 2},
-                              {64, 64, 2},   {256, 256, 4}, {256, 128, 2}};
+constexpr TileCfg kTiles[] = {{256, 128, 4}, {128, 128, 2}, {128, 64, 2}, {64, 64, 2},
+                              {256, 256, 4}, {256, 128, 2}, {256, 192, 4}};
 constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
 
 // Measured relative per-FLOP throughput of each tile with the CUs full, by
@@ -687,9 +694,9 @@ constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
 // CUs with it (the LM head's three, the 3072-wide ones); 128x64 is 3-5%
 // slower per FLOP and wins only where the larger tiles leave CUs idle.
 float tile_speed(int ti, int ta, int tb) {
-  static const float nt[kNumTiles] = {1.04f, 1.00f, 0.95f, 0.85f, 0.0f, 0.0f};
-  static const float nn[kNumTiles] = {1.03f, 1.00f, 0.97f, 0.85f, 1.10f, 0.0f};
-  static const float tn[kNumTiles] = {1.03f, 1.00f, 0.97f, 0.85f, 1.10f, 1.04f};
+  static const float nt[kNumTiles] = {1.04f, 1.00f, 0.95f, 0.85f, 0.0f, 0.0f, 1.08f};
+  static const float nn[kNumTiles] = {1.03f, 1.00f, 0.97f, 0.85f, 1.10f, 0.0f, 1.08f};
+  static const float tn[kNumTiles] = {1.03f, 1.00f, 0.97f, 0.85f, 1.10f, 1.04f, 0.0f};
   if (!ta && tb) return nt[ti];
   if (!ta && !tb) return nn[ti];
   if (ta && !tb) return tn[ti];
@@ -758,7 +765,8 @@ int64_t wide_splits(int64_t tiles, int64_t K, int cus) {
 // weight gradients and 768-wide input gradients run 3-8% slower with it,
 // the LM head's K-split input gradient (K = 50257) 3.4% slower, 6.45
 // against 6.23 ms; the MLP's 3072-wide GEMMs 2-5% faster).
-Plan choose_plan(int64_t M, int64_t N, int64_t K, int64_t batch, int cus, int ta, int tb) {
+Plan choose_plan(int64_t M, int64_t N, int64_t K, int64_t batch, int cus, int ta, int tb,
+                 int act) {
   int forced = -1;
   if (const char* e = getenv("TJH_GEMM_TILE")) {
     for (int i = 0; i < kNumTiles; ++i) {
@@ -793,6 +801,16 @@ Plan choose_plan(int64_t M, int64_t N, int64_t K, int64_t batch, int cus, int ta
     // gradients over 7 slices: 351 against 363 us; 3-4% slower over the 14
     // and 28 slices of the smaller ones, and on every A . B and A . B^T)
     if (i == 5 && forced < 0 && (!ta || tb || K / s < 1024)) continue;
+    // 256 x 192 (8 waves of 64 x 96, one workgroup per CU): for A . B and
+    // A . B^T split over K into at most two rounds of the CUs (GPT-2's
+    // 8192 x 768 products over K = 2304 or 3072 in two slices: 3-5% faster
+    // than 128 x 128).  Unsplit, or with the GELU-gradient epilogue (which
+    // reads the kept input; nothing else on the CU hides it), the tiles that
+    // share a CU at four waves per SIMD are as fast or faster (8192 x 3072 x
+    // 768 with GELU': 350 against 323 us on 256 x 128), and with more rounds
+    // they hide each other's fetch and epilogue better (LM head: 4.81
+    // against 5.00 ms).
+    if (i == 6 && forced < 0 && (ta || act == 2 || s < 2 || tiles * s > 2LL * cus)) continue;
     if (t.bm >= 256 && t.wr == 4 && !wide && forced < 0 && s > 1) continue;
     double score = useful * fill_of(tiles * s, cus) * tile_speed(i, ta, tb);
     if (tiles * s < cus) score *= (double)(tiles * s) / cus;
@@ -837,6 +855,7 @@ void launch_tile(int ti, const GemmArgs& g, dim3 grid, int ta, int tb, bool edge
     case 2: launch<128, 64, 2>(g, grid, ta, tb, edge); break;
     case 4: launch<256, 256, 4>(g, grid, ta, tb, edge); break;
     case 5: launch<256, 128, 2>(g, grid, ta, tb, edge); break;
+    case 6: launch<256, 192, 4>(g, grid, ta, tb, edge); break;
     default: launch<64, 64, 2>(g, grid, ta, tb, edge); break;
   }
 }
@@ -945,7 +964,7 @@ int tjh::gemm(const char* family, int transA, int transB, int64_t M, int64_t N, 
   g.xrow = reinterpret_cast<const floatx4*>(ce_rows);
   g.xm0 = g.xk0 = 0;
   KernelScope ks(family);
-  const Plan plan = choose_plan(M, N, K, batch, cus, transA, transB);
+  const Plan plan = choose_plan(M, N, K, batch, cus, transA, transB, act);
   const TileCfg& tc = kTiles[plan.tile];
   if (!(g.vecA && g.vecB)) {
     // operands not 4-byte aligned: guarded scalar loads everywhere
@@ -971,13 +990,13 @@ int tjh::gemm(const char* family, int transA, int transB, int64_t M, int64_t N, 
   // product (the 81 leftover rows of a 50257-row weight gradient) would
   // otherwise run on a dozen workgroups for the whole K range.
   if (rc == TJH_OK && Nm < N) {  // right strip (all rows)
-    const Plan ps = choose_plan(M, N - Nm, Km, batch, cus, transA, transB);
+    const Plan ps = choose_plan(M, N - Nm, Km, batch, cus, transA, transB, act);
     GemmArgs gs = sub(gk, transA, transB, 0, M, Nm, N - Nm, 0, Km);
     if (gs.bias_mode == 3 && Nm > 0) gs.bias_mode = 0;  // row sums come from column 0's tiles
     rc = run_block(ps.tile, gs, transA, transB, ps.splits, batch, true, cus);
   }
   if (rc == TJH_OK && Mm < M && Nm > 0) {  // bottom strip (interior columns)
-    const Plan ps = choose_plan(M - Mm, Nm, Km, batch, cus, transA, transB);
+    const Plan ps = choose_plan(M - Mm, Nm, Km, batch, cus, transA, transB, act);
     rc = run_block(ps.tile, sub(gk, transA, transB, Mm, M - Mm, 0, Nm, 0, Km), transA, transB,
                    ps.splits, batch, true, cus);
   }
