@@ -811,7 +811,7 @@ Plan choose_plan(int64_t M, int64_t N, int64_t K, int64_t batch, int cus, int ta
     // they hide each other's fetch and epilogue better (LM head: 4.81
     // against 5.00 ms).
     if (i == 6 && forced < 0 && (ta || act == 2 || s < 2 || tiles * s > 2LL * cus)) continue;
-    if (t.bm >= 256 && t.wr == 4 && !wide && forced < 0 && s > 1) continue;
+    if (t.bm >= 256 && t.wr == 4 && t.bn == 128 && forced < 0 && s > 1) continue;
     double score = useful * fill_of(tiles * s, cus) * tile_speed(i, ta, tb);
     if (tiles * s < cus) score *= (double)(tiles * s) / cus;
     if (score > best_score + 1e-9) {
