@@ -616,6 +616,10 @@ __global__ __launch_bounds__(64 * kLnBwdWaves) void k_ln_bwd_wave(const float* _
                                                         float* __restrict__ pg,
                                                         float* __restrict__ pb, int64_t rows,
                                                         int64_t cols, int64_t rpb) {
+  // no implicit contraction: the compiler versions the row loop on res,
+  // and the folded and unfolded residual paths must round alike (the only
+  // fused multiply-adds are the explicit ones below)
+#pragma clang fp contract(off)
   constexpr int NW = kLnBwdWaves;
   __shared__ float4 red[2][NW][64 * 3];  // partial combine across waves
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -699,10 +703,10 @@ __global__ __launch_bounds__(64 * kLnBwdWaves) void k_ln_bwd_wave(const float* _
           const int i = lane + 64 * j;
           if (EXACT || i < c4) {
             float4 o;
-            o.x = rs[q] * (gv[q][j].x * gm[j].x - s1 - xh[q][j].x * s2);
-            o.y = rs[q] * (gv[q][j].y * gm[j].y - s1 - xh[q][j].y * s2);
-            o.z = rs[q] * (gv[q][j].z * gm[j].z - s1 - xh[q][j].z * s2);
-            o.w = rs[q] * (gv[q][j].w * gm[j].w - s1 - xh[q][j].w * s2);
+            o.x = rs[q] * fmaf(-xh[q][j].x, s2, fmaf(gv[q][j].x, gm[j].x, -s1));
+            o.y = rs[q] * fmaf(-xh[q][j].y, s2, fmaf(gv[q][j].y, gm[j].y, -s1));
+            o.z = rs[q] * fmaf(-xh[q][j].z, s2, fmaf(gv[q][j].z, gm[j].z, -s1));
+            o.w = rs[q] * fmaf(-xh[q][j].w, s2, fmaf(gv[q][j].w, gm[j].w, -s1));
             if (res) {
               o.x = rv[j].x + o.x; o.y = rv[j].y + o.y;
               o.z = rv[j].z + o.z; o.w = rv[j].w + o.w;
