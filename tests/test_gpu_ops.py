@@ -26,7 +26,7 @@ def check(got, want, **tol):
 
 
 def check_floor(got, want, ref32, k=3.0):
-    """north_star's rtol 1e-4 / atol 1e-5, with atol raised to k times the
+    """The required rtol 1e-4 / atol 1e-5, with atol raised to k times the
     float32 floor of the same computation when that floor exceeds 1e-5: the
     floor is max |ref32 - want|, ref32 the same product evaluated in
     float32 on the CPU.  Unit-variance operands summed over thousands of

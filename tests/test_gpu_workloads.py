@@ -17,7 +17,7 @@ def check(got, want, rtol=1e-4, atol=1e-5):
                                rtol=rtol, atol=atol)
 
 
-# Reductions, GEMM, attention, conv: north_star's rtol 1e-4 / atol 1e-5 per
+# Reductions, GEMM, attention, conv: the required rtol 1e-4 / atol 1e-5 per
 # element, and a scale-free bound on the whole tensor, since atol 1e-5 is
 # loose for gradients of 1e-3: ||got - want|| / ||want|| <= 1e-5.  Measured
 # at GPT-2 124M (B=1, T=1024): <= 1.8e-6 on the GPU, <= 1.05e-6 for
@@ -164,8 +164,8 @@ def test_gpt2_124m_full_shape_against_oracle(torch):
     """GPT-2 small itself (12 layers, 12 heads, d 768, vocab 50257, tied
     embeddings) on a full 1024-token sequence: the loss, the logits'
     gradient, every parameter's gradient (wte / wpe, every layer, ln_f) and
-    the AdamW(lr 6e-4, wd 0.1) step, against the float64 oracle at
-    north_star's tolerances."""
+    the AdamW(lr 6e-4, wd 0.1) step, against the float64 oracle at the
+    required tolerances."""
     from torchjs_amd import workloads as W
     cfg = om.Config()
     r = np.random.default_rng(11)
