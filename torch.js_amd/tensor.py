@@ -2185,6 +2185,10 @@ def reduce_sum(x, dim=None, keepdim=False):
     xs = x.shape
 
     def bwd(g):
+        if g._lz is None and g._st is not None and all(st == 0 for st in g._strides):
+            # one element broadcast (a mean's gradient): broadcast it on as a
+            # view, not materialised (the fused kernels read it as a scalar)
+            return [Tensor(g._st, xs, (0,) * len(xs), g._offset, g._dtype)]
         return [_view_raw(g.contiguous(), kshape).expand(xs)]
     return _record(out, "Sum", [x], bwd, gfn=lambda g: [expand(reshape(g, kshape), xs)])
 
