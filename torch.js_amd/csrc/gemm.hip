@@ -392,7 +392,9 @@ __global__ __launch_bounds__(gemm_threads(WR), gemm_waves_per_simd(BM, BN, WR)) 
   // PF2: two register sets in flight (tile t + 2 is fetched while tile t's
   // MFMAs run, and tile t + 1, fetched one K step earlier, is stored after
   // them), for the tiles at two waves per SIMD, where few other waves cover
-  // the fetch of the next tile
+  // the fetch of the next tile; not for the A . B and A . B^T forms of the
+  // 4-wave 256 x 128 tile, whose second set leaves its 128 x 64 wave tiles
+  // too few registers to read fragments ahead (measured slower)
   constexpr bool PF2 = gemm_waves_per_simd(BM, BN, WR) == 2 && !XF && (WR == 4 || TA);
   floatx4 ra2[VA], rb2[VB];
   auto fetch = [&](int64_t k0, floatx4 (&xa)[VA], floatx4 (&xb)[VB]) {
