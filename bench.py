@@ -67,7 +67,10 @@ def hbm_bytes_per_step(b, t, nparams, distinct_ids):
     tok = b * t
     f = 4
     return {
-        # dlogits = softmax - onehot: read logits, write dlogits
+        # the loss and dlogits = (softmax - onehot) / rows in one pass
+        # (loss.backward()'s unit seed): read logits, write dlogits
+        "cross_entropy_fwd_grad": 2 * tok * V * f,
+        # the same gradient for another upstream gradient, after the forward
         "cross_entropy_bwd": 2 * tok * V * f,
         # 25 LayerNorms: read dy, x; write dx (+ mean/rstd, gamma); the 24
         # in the blocks also read the residual stream's gradient, which they

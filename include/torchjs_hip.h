@@ -463,6 +463,19 @@ int tjh_cross_entropy_row_scale(const int32_t* targets,
                                 const float* grad_out, int64_t rows,
                                 int64_t cols, int32_t ignore_index,
                                 int reduction, float* row_scale);
+/* The forward of F.cross_entropy without class weights or smoothing
+ * (losses.ts:129-168: lse, loss_rows, the scalar loss in `out` for
+ * reduction 1 mean, 2 sum, 3 batchmean) together with the logits' gradient
+ * of that loss for a unit upstream gradient — what loss.backward() seeds
+ * (Tensor.ts:3686-3740) — written to dlogits [rows, ldd].  Equal bit for bit
+ * to tjh_cross_entropy_forward followed by tjh_cross_entropy_backward with
+ * grad_out = 1; rows of up to 51200 classes are read once (the row kept in
+ * registers between the two), others take those two calls. */
+int tjh_cross_entropy_forward_grad(const float* logits, int64_t ld,
+                                   const int32_t* targets, int64_t rows,
+                                   int64_t cols, int32_t ignore_index,
+                                   float* lse, float* loss_rows, int reduction,
+                                   float* out, float* dlogits, int64_t ldd);
 /* nll over log-probs [rows, cols] (F.nll_loss, losses.ts:63-94):
  * loss_rows[r] = -w_t logp[r, t] for valid rows, else 0. */
 int tjh_nll_loss_forward(const float* logp, int64_t ld,

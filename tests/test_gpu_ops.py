@@ -431,6 +431,63 @@ def test_cross_entropy_aligned_rows(torch, rows, cols, ld, red):
     assert not g[:, cols:].any()
 
 
+@pytest.mark.parametrize("rows,cols,lead", [(37, 50257, 0), (64, 4100, 0), (9, 2049, 0),
+                                            (37, 50257, 3), (5, 51201, 0)])
+@pytest.mark.parametrize("red", ["mean", "sum", "batchmean"])
+def test_cross_entropy_seeded_gradient_in_forward(torch, rows, cols, lead, red):
+    """loss.backward() with its implicit unit seed on a cross-entropy of
+    more than 2048 classes takes the logits' gradient that the forward
+    formed in its pass over the logits: the loss and the gradient equal,
+    bit for bit, those of the separate forward and backward passes (an
+    explicit seed of 1 and a root that is not the loss take those), and the
+    oracle's within 1e-5 relative (RED).  `lead` shifts the rows off 16-byte
+    alignment (the library then runs the two passes itself); 51201 classes
+    exceed what one block keeps in registers, the same."""
+    r = np.random.default_rng(rows * 7 + cols + lead)
+    full = f32(r.standard_normal((rows, cols + lead)) * 2)
+    t = r.integers(0, cols, rows).astype(np.int32)
+    t[::4] = -100
+    t[1] = cols - 1
+    t[2] = 0
+    runs = []
+    for how in ("implicit", "explicit", "not-root"):
+        ft = torch.tensor(full, requires_grad=True)
+        loss = torch.F.cross_entropy(ft[:, lead:], torch.tensor(t), reduction=red)
+        if how == "implicit":
+            loss.backward()
+        elif how == "explicit":
+            loss.backward(torch.tensor(np.float32(1.0)))
+        else:
+            (loss * 1.0).backward()
+        g = ft.grad.numpy()
+        assert not g[:, :lead].any()
+        runs.append((loss.numpy(), g[:, lead:]))
+    for lo, g in runs[1:]:
+        assert np.array_equal(lo, runs[0][0]) and np.array_equal(g, runs[0][1])
+    xs = full[:, lead:]
+    check(runs[0][0], ops.cross_entropy(xs, t, red), **RED)
+    check(runs[0][1], ops.cross_entropy_backward(xs, t, np.float32(1.0), red), **RED)
+
+
+def test_cross_entropy_seeded_gradient_used_once(torch):
+    """A second backward through a retained graph gets the gradient from
+    the backward kernel (the forward's is handed out once), and an
+    unreduced or no-grad loss forms none."""
+    r = np.random.default_rng(5)
+    x = f32(r.standard_normal((8, 4099)))
+    t = r.integers(0, 4099, 8).astype(np.int32)
+    xt = torch.tensor(x, requires_grad=True)
+    loss = torch.F.cross_entropy(xt, torch.tensor(t))
+    loss.backward(retain_graph=True)
+    g1 = xt.grad.numpy().copy()
+    loss.backward()
+    assert np.array_equal(xt.grad.numpy(), 2 * g1)
+    with torch.no_grad():
+        lo = torch.F.cross_entropy(xt, torch.tensor(t))
+    assert lo.grad_fn is None
+    check(lo.item(), ops.cross_entropy(x, t), **RED)
+
+
 def test_nll_loss(torch):
     r = np.random.default_rng(11)
     lp = ops.log_softmax(r.standard_normal((9, 6))).astype(np.float32)

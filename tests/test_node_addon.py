@@ -15,7 +15,8 @@ NODE = shutil.which("node")
 EXPORTS = ["init", "deviceInfo", "malloc", "h2d", "d2h", "d2hAsync", "synchronize",
            "memoryStats", "emptyCache", "fill", "random", "copyStrided", "unary",
            "unaryBackward", "binary", "scalar", "reduce", "softmaxForward", "softmaxBackward",
-           "crossEntropyForward", "crossEntropyBackward", "layerNormForward",
+           "crossEntropyForward", "crossEntropyBackward", "crossEntropyForwardGrad",
+           "layerNormForward",
            "layerNormBackward", "layerNormBackwardRes", "layerNormBackwardNoalloc", "flushDeferred", "embeddingForward", "embeddingBackward",
            "embeddingPosForward", "embeddingPosBackward", "gemm", "gemmAct", "gemmCe", "crossEntropyRowScale",
            "sdpaForward",

@@ -139,6 +139,8 @@ SIGNATURES = {
     "tjh_cross_entropy_backward": [c_vp, c_i64, c_vp, c_vp, c_f32, c_vp, c_vp, c_i64, c_i64,
                                    ctypes.c_int32, c_int, c_vp, c_i64, c_int],
     "tjh_cross_entropy_row_scale": [c_vp, c_vp, c_i64, c_i64, ctypes.c_int32, c_int, c_vp],
+    "tjh_cross_entropy_forward_grad": [c_vp, c_i64, c_vp, c_i64, c_i64, ctypes.c_int32, c_vp, c_vp,
+                                       c_int, c_vp, c_vp, c_i64],
     "tjh_nll_loss_forward": [c_vp, c_i64, c_vp, c_i64, c_i64, ctypes.c_int32, c_vp, c_vp, c_int,
                              c_vp],
     "tjh_nll_loss_backward": [c_vp, c_vp, c_vp, c_i64, c_i64, ctypes.c_int32, c_int, c_vp],

@@ -188,6 +188,74 @@ __global__ __launch_bounds__(kBlock) void k_ce_fwd(const float* __restrict__ x, 
   }
 }
 
+// Cross-entropy forward and the logits' gradient of the reduced loss for
+// a unit upstream gradient (what loss.backward() seeds), in one pass over
+// wide rows: a block of kBlock lanes keeps its row in registers between the
+// two, so the logits are read once instead of once per pass.  lse and the
+// per-row loss come out bit for bit as k_ce_fwd<false> computes them (the
+// same per-lane element order and reductions: lane l takes float4 l,
+// l + kBlock, ..., then the tail element l), the gradient as k_ce_bwd_flat
+// writes it with grad_out = 1.  Rows 16-byte aligned, cols <= kBlock*4*NV.
+template <int NV>
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2))) void k_ce_fwd_grad(
+    const float* __restrict__ x, int64_t ld, const int32_t* __restrict__ t, int64_t cols,
+    int32_t ignore, const float* __restrict__ count, int reduction,
+    float* __restrict__ lse_out, float* __restrict__ loss_rows, float* __restrict__ d,
+    int64_t ldd) {
+  __shared__ float sm[2 * kBlock / 64];
+  const int64_t r = blockIdx.x;
+  const int lane = threadIdx.x;
+  const float* xr = x + r * ld;
+  const int nc = (int)cols;
+  const int n4 = nc >> 2;  // >= 1: rows are wider than 2048
+  // every load in bounds and unconditional (a lane past the row re-reads
+  // the last chunk), so all NV are in flight together; what lies past the
+  // row enters the reduction as -inf, which ms_add leaves out exactly
+  float4 v[NV];
+#pragma unroll
+  for (int k = 0; k < NV; ++k) v[k] = ld_nt(xr + 4 * min(lane + kBlock * k, n4 - 1));
+  const int ti = 4 * n4 + lane;  // the tail (cols % 4 < kBlock elements)
+  const float tv = xr[min(ti, nc - 1)];
+  MS ms{-INFINITY, 0.f};
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    const bool in = lane + kBlock * k < n4;
+    ms = ms_add(ms, in ? v[k].x : -INFINITY);
+    ms = ms_add(ms, in ? v[k].y : -INFINITY);
+    ms = ms_add(ms, in ? v[k].z : -INFINITY);
+    ms = ms_add(ms, in ? v[k].w : -INFINITY);
+  }
+  ms = ms_add(ms, ti < nc ? tv : -INFINITY);
+  ms = block_ms(ms, sm);
+  const float l = ms.m + logf(ms.s);
+  const int32_t tr = t[r];
+  const bool valid = !(tr == ignore || tr < 0 || tr >= cols);
+  if (lane == 0) {
+    lse_out[r] = l;
+    loss_rows[r] = valid ? l - xr[tr] : 0.f;
+  }
+  // ce_scale with grad_out[0] = 1
+  const float inv = count ? 1.0f / count[0] : 1.0f;
+  const float sc = valid ? ((reduction == 1 || reduction == 3) ? 1.0f * inv : 1.0f) : 0.f;
+  float* dr = d + r * ldd;
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    const int i = lane + kBlock * k;
+    if (i < n4) {
+      const int c = 4 * i;
+      float4 o;
+      o.x = (__expf(v[k].x - l) - (c == tr ? 1.f : 0.f)) * sc;
+      o.y = (__expf(v[k].y - l) - (c + 1 == tr ? 1.f : 0.f)) * sc;
+      o.z = (__expf(v[k].z - l) - (c + 2 == tr ? 1.f : 0.f)) * sc;
+      o.w = (__expf(v[k].w - l) - (c + 3 == tr ? 1.f : 0.f)) * sc;
+      st_nt(dr + c, o);
+    }
+  }
+  if (ti < nc) dr[ti] = (__expf(tv - l) - (ti == tr ? 1.f : 0.f)) * sc;
+  else if ((nc & 3) && ti < 4 * n4 + 4) dr[ti] = 0.f;  // the last chunk's padding, as there
+}
+constexpr int kCeFusedNV = 50;  // rows up to 51200 classes (GPT-2's 50257)
+
 // Final reduction of per-row losses.  reduction 1: sum / (sum over valid
 // rows of the target's class weight, 1 without weights), 2: sum,
 // 3 ('batchmean', losses.ts:27-28): sum / rows.  One block.
@@ -1036,6 +1104,56 @@ int tjh_cross_entropy_row_scale(const int32_t* targets, const float* grad_out, i
              targets, grad_out, mean ? cnt.as<float>() : nullptr, rows, cols, ignore_index,
              reduction, row_scale);
   return check_launch("cross_entropy_row_scale");
+}
+
+int tjh_cross_entropy_forward_grad(const float* logits, int64_t ld, const int32_t* targets,
+                                   int64_t rows, int64_t cols, int32_t ignore_index, float* lse,
+                                   float* loss_rows, int reduction, float* out, float* dlogits,
+                                   int64_t ldd) {
+  TJH_REQUIRE_INIT();
+  TJH_ARG(rows >= 0 && cols > 0 && ld >= cols && ldd >= cols,
+          "tjh_cross_entropy_forward_grad: bad sizes");
+  TJH_ARG(reduction >= 1 && reduction <= 3,
+          "tjh_cross_entropy_forward_grad: the reduction must give a scalar loss (1, 2 or 3)");
+  TJH_ARG(out && lse && loss_rows && dlogits && targets && logits,
+          "tjh_cross_entropy_forward_grad: NULL operand");
+  if (rows == 0) return tjh_fill_f32(out, 1, reduction == 2 ? 0.f : __builtin_nanf(""));
+  const bool fused = cols > 2048 && cols <= (int64_t)kBlock * 4 * kCeFusedNV && ld % 4 == 0 &&
+                     ldd % 4 == 0 && aligned16(logits) && aligned16(dlogits);
+  if (!fused) {
+    // the two passes, with a unit upstream gradient
+    int rc = tjh_cross_entropy_forward(logits, ld, targets, rows, cols, ignore_index, nullptr,
+                                       0.f, lse, loss_rows, reduction, out);
+    if (rc != TJH_OK) return rc;
+    Scratch one(sizeof(float));
+    if (!one.ok()) return set_error(TJH_ERR_OOM, "cross_entropy_forward_grad: no scratch");
+    rc = tjh_fill_f32(one.as<float>(), 1, 1.0f);
+    if (rc != TJH_OK) return rc;
+    return tjh_cross_entropy_backward(logits, ld, targets, nullptr, 0.f, lse, one.as<float>(),
+                                      rows, cols, ignore_index, reduction, dlogits, ldd, 0);
+  }
+  const bool mean = reduction == 1 || reduction == 3;
+  Scratch cnt(mean ? 2 * sizeof(float) : 0);
+  if (mean) {
+    if (!cnt.ok()) return set_error(TJH_ERR_OOM, "cross_entropy_forward_grad: no scratch");
+    KernelScope ks("loss_reduce");
+    tjh_launch(k_count_valid, dim3(1), dim3(kBlock), 0, stream(), targets, rows, cols,
+               ignore_index, nullptr, reduction, cnt.as<float>(), nullptr);
+    int rc = check_launch("count_valid");
+    if (rc != TJH_OK) return rc;
+  }
+  {
+    KernelScope ks("cross_entropy_fwd_grad");
+    tjh_launch(k_ce_fwd_grad<kCeFusedNV>, dim3((unsigned)rows), dim3(kBlock), 0, stream(),
+               logits, ld, targets, cols, ignore_index, mean ? cnt.as<float>() : nullptr,
+               reduction, lse, loss_rows, dlogits, ldd);
+    int rc = check_launch("cross_entropy_forward_grad");
+    if (rc != TJH_OK) return rc;
+  }
+  KernelScope ks("loss_reduce");
+  tjh_launch(k_loss_reduce, dim3(1), dim3(kBlock), 0, stream(), loss_rows, targets, nullptr,
+             rows, cols, ignore_index, reduction, out);
+  return check_launch("loss_reduce");
 }
 
 int tjh_nll_loss_forward(const float* logp, int64_t ld, const int32_t* targets, int64_t rows,

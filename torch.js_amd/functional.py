@@ -221,13 +221,32 @@ def cross_entropy(input, target, weight=None, reduction="mean", label_smoothing=
     lse = empty((rows,))
     loss_rows = empty((rows,))
     out = empty(()) if red else loss_rows
-    L.check(L.lib().tjh_cross_entropy_forward(rv[0], rv[1], t.data_ptr(), rows, cols,
-                                              int(ignore_index), wp, eps, lse.data_ptr(),
-                                              loss_rows.data_ptr(), red,
-                                              out.data_ptr() if red else None),
-            "cross_entropy")
+    # The logits' gradient for the unit seed of loss.backward(), formed in
+    # the forward's pass over the logits (read once instead of twice) when
+    # the loss is a scalar that will be differentiated; another upstream
+    # gradient takes the backward kernel below.
+    pre, me = [None], [None]
+    if (red and w is None and eps == 0.0 and not _T._FUSE_CE and cols > 2048
+            and _T._grad["enabled"] and x.requires_grad):
+        d = _empty_padded(rows, cols) if cols % 4 else empty((rows, cols))
+        L.check(L.lib().tjh_cross_entropy_forward_grad(rv[0], rv[1], t.data_ptr(), rows, cols,
+                                                       int(ignore_index), lse.data_ptr(),
+                                                       loss_rows.data_ptr(), red,
+                                                       out.data_ptr(), d.data_ptr(),
+                                                       d._strides[0]),
+                "cross_entropy")
+        pre[0] = d
+    else:
+        L.check(L.lib().tjh_cross_entropy_forward(rv[0], rv[1], t.data_ptr(), rows, cols,
+                                                  int(ignore_index), wp, eps, lse.data_ptr(),
+                                                  loss_rows.data_ptr(), red,
+                                                  out.data_ptr() if red else None),
+                "cross_entropy")
 
     def bwd(g):
+        d0, pre[0] = pre[0], None  # handed out once (the engine may own it)
+        if d0 is not None and g is _T._unit_seed["g"] and me[0] == _T._unit_seed["node"]:
+            return [d0]
         g = g.contiguous()
         xp, ld = _rows_view(xd)
         if w is None and eps == 0.0 and _T._FUSE_CE and ld % 4 == 0 and xp % 16 == 0:
@@ -244,6 +263,9 @@ def cross_entropy(input, target, weight=None, reduction="mean", label_smoothing=
         q, den = _class_coef(t, w, rows, cols, eps, ignore_index, True)
         return _T._regrad(lambda xx: _class_loss(log_softmax(xx, 1), q, den, red, rows), [x], g)
     res = _record(out, "CrossEntropy", [x], bwd, gfn=gbwd)
+    me[0] = id(res.grad_fn) if res.grad_fn is not None else None
+    if pre[0] is not None and res.grad_fn is None:
+        pre[0] = None
     if x is not input and input.ndim == 1 and red == 0:
         res = reshape(res, ())
     return res

@@ -617,6 +617,20 @@ static napi_value js_ce_backward(napi_env env, napi_callback_info info) {
   return undef(env);
 }
 
+/* crossEntropyForwardGrad(logits, ld, targets, rows, cols, ignore, lse, lossRows, reduction,
+ *                         out, d, ldd): the scalar loss and its logits' gradient for a unit
+ * seed, one pass over the logits */
+static napi_value js_ce_forward_grad(napi_env env, napi_callback_info info) {
+  napi_value a[12];
+  if (!get_args(env, info, 12, a)) return NULL;
+  CHECK_RC(tjh_cross_entropy_forward_grad(
+      (const float*)ptr(env, a[0]), i64(env, a[1]), (const int32_t*)ptr(env, a[2]),
+      i64(env, a[3]), i64(env, a[4]), (int32_t)i64(env, a[5]), (float*)ptr(env, a[6]),
+      (float*)ptr(env, a[7]), (int)i64(env, a[8]), (float*)ptr(env, a[9]),
+      (float*)ptr(env, a[10]), i64(env, a[11])));
+  return undef(env);
+}
+
 static napi_value js_ln_forward(napi_env env, napi_callback_info info) {
   napi_value a[9];
   if (!get_args(env, info, 9, a)) return NULL;
@@ -1271,7 +1285,8 @@ static napi_value init_module(napi_env env, napi_value exports) {
       FN("graphReplay", js_graph_replay), FN("graphDestroy", js_graph_destroy),
       FN("softmaxForward", js_softmax_forward),
       FN("softmaxBackward", js_softmax_backward), FN("crossEntropyForward", js_ce_forward),
-      FN("crossEntropyBackward", js_ce_backward), FN("layerNormForward", js_ln_forward),
+      FN("crossEntropyBackward", js_ce_backward),
+      FN("crossEntropyForwardGrad", js_ce_forward_grad), FN("layerNormForward", js_ln_forward),
       FN("layerNormBackward", js_ln_backward),
       FN("layerNormBackwardRes", js_ln_backward_res),
       FN("layerNormBackwardNoalloc", js_ln_backward_noalloc),

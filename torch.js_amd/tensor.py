@@ -89,6 +89,9 @@ def synchronize():
 # ----------------------------------------------------------------- grad mode
 
 _grad = {"enabled": True}
+# the implicit seed of the running Tensor.backward() and the id of the root's
+# node: the seed is the root VJP's upstream gradient, equal to 1
+_unit_seed = {"node": None, "g": None}
 
 
 def is_grad_enabled():
@@ -412,8 +415,16 @@ class Tensor:
             if self.numel() != 1:
                 raise RuntimeError("grad can be implicitly created only for scalar outputs")
             gradient = full(self._shape, 1.0)
-        run_backward([(self, gradient)], retain_graph=retain_graph or create_graph,
-                     create_graph=create_graph)
+            if not create_graph:
+                # known on the host to be 1 where it reaches the root's own
+                # VJP: a loss may have formed its input's gradient for that
+                # seed already (cross_entropy)
+                _unit_seed["node"], _unit_seed["g"] = id(self.grad_fn), gradient
+        try:
+            run_backward([(self, gradient)], retain_graph=retain_graph or create_graph,
+                         create_graph=create_graph)
+        finally:
+            _unit_seed["node"] = _unit_seed["g"] = None
 
     def detach(self):
         if self._st is None:  # stays deferred, sharing the value
