@@ -1011,7 +1011,11 @@ int tjh::gemm(const char* family, int transA, int transB, int64_t M, int64_t N, 
       gr.bias_mode = 0;
       gr.bias = nullptr;
     }
-    rc = run_block(plan.tile, gr, transA, transB, 1, batch, true, cus);
+    // its own tile: a few K steps over the whole of C is a pass over C,
+    // which wants every CU (the LM head's 17-deep remainder on the 256 x 256
+    // tile ran on 96 workgroups)
+    const Plan pr = choose_plan(M, N, Kr, batch, cus, transA, transB, act);
+    rc = run_block(pr.tile, gr, transA, transB, 1, batch, true, cus);
   }
   return rc;
 }
