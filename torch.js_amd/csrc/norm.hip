@@ -256,6 +256,8 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2))) voi
 }
 constexpr int kCeFusedNV = 50;  // rows up to 51200 classes (GPT-2's 50257)
 
+constexpr int kRowBatch = 16;  // rows per lane whose loads are in flight together
+
 // Final reduction of per-row losses.  reduction 1: sum / (sum over valid
 // rows of the target's class weight, 1 without weights), 2: sum,
 // 3 ('batchmean', losses.ts:27-28): sum / rows.  One block.
@@ -267,10 +269,26 @@ __global__ __launch_bounds__(kBlock) void k_loss_reduce(const float* __restrict_
                                                         float* __restrict__ out) {
   __shared__ float sm[kBlock / 64];
   float s = 0.f, c = 0.f;
-  for (int64_t i = threadIdx.x; i < rows; i += kBlock) {
-    s += loss_rows[i];
-    int32_t tr = t[i];
-    c += (tr == ignore || tr < 0 || tr >= cols) ? 0.f : (w ? w[tr] : 1.f);
+  // each lane adds rows lane, lane + kBlock, ... in that order, with
+  // kRowBatch rows' loads issued before their adds (one round trip per
+  // batch instead of per row)
+  for (int64_t i0 = threadIdx.x; i0 < rows; i0 += (int64_t)kBlock * kRowBatch) {
+    float lv[kRowBatch];
+    int32_t tv[kRowBatch];
+#pragma unroll
+    for (int u = 0; u < kRowBatch; ++u) {
+      const int64_t i = i0 + (int64_t)u * kBlock;
+      lv[u] = i < rows ? loss_rows[i] : 0.f;
+      tv[u] = i < rows ? t[i] : 0;
+    }
+#pragma unroll
+    for (int u = 0; u < kRowBatch; ++u) {
+      if (i0 + (int64_t)u * kBlock < rows) {
+        s += lv[u];
+        const int32_t tr = tv[u];
+        c += (tr == ignore || tr < 0 || tr >= cols) ? 0.f : (w ? w[tr] : 1.f);
+      }
+    }
   }
   s = block_sum(s, sm);
   c = block_sum(c, sm);
@@ -438,9 +456,21 @@ __global__ __launch_bounds__(kBlock) void k_count_valid(const int32_t* __restric
                                                         float* __restrict__ wsum) {
   __shared__ float sm[kBlock / 64];
   float c = 0.f;
-  for (int64_t i = threadIdx.x; i < rows; i += kBlock) {
-    int32_t tr = t[i];
-    c += (tr == ignore || tr < 0 || tr >= cols) ? 0.f : (w ? w[tr] : 1.f);
+  // per lane in row order, kRowBatch targets loaded before their adds
+  for (int64_t i0 = threadIdx.x; i0 < rows; i0 += (int64_t)kBlock * kRowBatch) {
+    int32_t tv[kRowBatch];
+#pragma unroll
+    for (int u = 0; u < kRowBatch; ++u) {
+      const int64_t i = i0 + (int64_t)u * kBlock;
+      tv[u] = i < rows ? t[i] : 0;
+    }
+#pragma unroll
+    for (int u = 0; u < kRowBatch; ++u) {
+      if (i0 + (int64_t)u * kBlock < rows) {
+        const int32_t tr = tv[u];
+        c += (tr == ignore || tr < 0 || tr >= cols) ? 0.f : (w ? w[tr] : 1.f);
+      }
+    }
   }
   c = block_sum(c, sm);
   if (wsum) {

@@ -200,9 +200,12 @@ __global__ __launch_bounds__(kBlock) void k_colsum(const float* __restrict__ x, 
 }
 
 // Final pass: workgroup (x, i) owns 64 columns of output i; wave w of 16
-// sums partial rows w, w+16, ... (compensated, fetched kBatch at a time)
+// sums partial rows w, w+16, ... (compensated, fetched kFinalBatch at a time)
 // and the 16 wave sums are added in wave order.
 constexpr int kFinalWaves = 16;
+// partial rows per wave fetched together: 256 partial rows (one per CU) in
+// one round trip per wave
+constexpr int kFinalBatch = 16;
 
 struct FinalArgs {
   const float* part[kFinalMax];
@@ -221,15 +224,16 @@ __global__ __launch_bounds__(64 * kFinalWaves) void k_colsum_final(FinalArgs fa,
   const float* __restrict__ p = fa.part[i];
   Kahan k;
   if (c < cols) {
-    for (int64_t b = w; b < nb; b += kFinalWaves * kBatch) {
-      float v[kBatch];
+    for (int64_t b = w; b < nb; b += kFinalWaves * kFinalBatch) {
+      float v[kFinalBatch];
 #pragma unroll
-      for (int u = 0; u < kBatch; ++u) {
+      for (int u = 0; u < kFinalBatch; ++u) {
         const int64_t bb = b + (int64_t)u * kFinalWaves;
         v[u] = bb < nb ? p[bb * cols + c] : 0.f;
       }
 #pragma unroll
-      for (int u = 0; u < kBatch; ++u) k.add(v[u]);
+      for (int u = 0; u < kFinalBatch; ++u)
+        if (b + (int64_t)u * kFinalWaves < nb) k.add(v[u]);  // rows past nb add nothing
     }
   }
   red[w][lane] = k.s;
