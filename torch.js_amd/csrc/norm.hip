@@ -722,15 +722,23 @@ __global__ __launch_bounds__(64 * kLnBwdWaves) void k_ln_bwd_wave(const float* _
   __shared__ float4 red[2][NW][64 * 3];  // partial combine across waves
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int c4 = (int)(cols >> 2);
+  // Rows of up to 1536 keep gamma in registers and load a residual row
+  // before its reductions; wider rows (up to 3072: the dgamma / dbeta
+  // partials alone take 96 registers) read gamma at each use (an L1-resident
+  // row) and the residual as they write, so nothing spills.
+  constexpr bool kWide = V4 > 6;
   float4 ag[V4], ab[V4];
-  float4 gm[V4];
+  float4 gm[kWide ? 1 : V4];
+  auto gam = [&](int j) {
+    const int i = lane + 64 * j;
+    return (gamma && (EXACT || i < c4)) ? reinterpret_cast<const float4*>(gamma)[i]
+                                        : make_float4(1.f, 1.f, 1.f, 1.f);
+  };
 #pragma unroll
   for (int j = 0; j < V4; ++j) {
     ag[j] = make_float4(0.f, 0.f, 0.f, 0.f);
     ab[j] = make_float4(0.f, 0.f, 0.f, 0.f);
-    int i = lane + 64 * j;
-    gm[j] = (gamma && (EXACT || i < c4)) ? reinterpret_cast<const float4*>(gamma)[i]
-                              : make_float4(1.f, 1.f, 1.f, 1.f);
+    if (!kWide) gm[kWide ? 0 : j] = gam(j);
   }
   const float inv_n = 1.0f / (float)cols;
   int64_t r_beg = (int64_t)blockIdx.x * rpb;
@@ -773,8 +781,8 @@ __global__ __launch_bounds__(64 * kLnBwdWaves) void k_ln_bwd_wave(const float* _
           const float4 g = gv[q][j], xv = xh[q][j];
           xh[q][j] = make_float4((xv.x - mu[q]) * rs[q], (xv.y - mu[q]) * rs[q],
                                  (xv.z - mu[q]) * rs[q], (xv.w - mu[q]) * rs[q]);
-          const float4 gg = make_float4(g.x * gm[j].x, g.y * gm[j].y, g.z * gm[j].z,
-                                        g.w * gm[j].w);
+          const float4 gmj = kWide ? gam(j) : gm[kWide ? 0 : j];
+          const float4 gg = make_float4(g.x * gmj.x, g.y * gmj.y, g.z * gmj.z, g.w * gmj.w);
           s1 += (gg.x + gg.y) + (gg.z + gg.w);
           s2 += (gg.x * xh[q][j].x + gg.y * xh[q][j].y) + (gg.z * xh[q][j].z + gg.w * xh[q][j].w);
           ag[j].x += g.x * xh[q][j].x; ag[j].y += g.y * xh[q][j].y;
@@ -783,13 +791,13 @@ __global__ __launch_bounds__(64 * kLnBwdWaves) void k_ln_bwd_wave(const float* _
         }
       }
       // the residual row's loads go out before the row reductions
-      float4 rv[V4];
-      if (dx && res) {
+      float4 rv[kWide ? 1 : V4];
+      if (!kWide && dx && res) {
         const float4* r4 = reinterpret_cast<const float4*>(res + r * cols);
 #pragma unroll
         for (int j = 0; j < V4; ++j) {
           const int i = lane + 64 * j;
-          if (EXACT || i < c4) rv[j] = ld_nt(reinterpret_cast<const float*>(r4 + i));
+          if (EXACT || i < c4) rv[kWide ? 0 : j] = ld_nt(reinterpret_cast<const float*>(r4 + i));
         }
       }
       s1 = wave_sum(s1) * inv_n;
@@ -801,13 +809,16 @@ __global__ __launch_bounds__(64 * kLnBwdWaves) void k_ln_bwd_wave(const float* _
           const int i = lane + 64 * j;
           if (EXACT || i < c4) {
             float4 o;
-            o.x = rs[q] * fmaf(-xh[q][j].x, s2, fmaf(gv[q][j].x, gm[j].x, -s1));
-            o.y = rs[q] * fmaf(-xh[q][j].y, s2, fmaf(gv[q][j].y, gm[j].y, -s1));
-            o.z = rs[q] * fmaf(-xh[q][j].z, s2, fmaf(gv[q][j].z, gm[j].z, -s1));
-            o.w = rs[q] * fmaf(-xh[q][j].w, s2, fmaf(gv[q][j].w, gm[j].w, -s1));
+            const float4 gmj = kWide ? gam(j) : gm[kWide ? 0 : j];
+            o.x = rs[q] * fmaf(-xh[q][j].x, s2, fmaf(gv[q][j].x, gmj.x, -s1));
+            o.y = rs[q] * fmaf(-xh[q][j].y, s2, fmaf(gv[q][j].y, gmj.y, -s1));
+            o.z = rs[q] * fmaf(-xh[q][j].z, s2, fmaf(gv[q][j].z, gmj.z, -s1));
+            o.w = rs[q] * fmaf(-xh[q][j].w, s2, fmaf(gv[q][j].w, gmj.w, -s1));
             if (res) {
-              o.x = rv[j].x + o.x; o.y = rv[j].y + o.y;
-              o.z = rv[j].z + o.z; o.w = rv[j].w + o.w;
+              const float4 rr =
+                  kWide ? ld_nt(res + r * cols + 4 * (int64_t)i) : rv[kWide ? 0 : j];
+              o.x = rr.x + o.x; o.y = rr.y + o.y;
+              o.z = rr.z + o.z; o.w = rr.w + o.w;
             }
             d4[i] = o;
           }
