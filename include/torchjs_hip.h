@@ -469,8 +469,9 @@ int tjh_cross_entropy_row_scale(const int32_t* targets,
  * of that loss for a unit upstream gradient — what loss.backward() seeds
  * (Tensor.ts:3686-3740) — written to dlogits [rows, ldd].  Equal bit for bit
  * to tjh_cross_entropy_forward followed by tjh_cross_entropy_backward with
- * grad_out = 1; rows of up to 51200 classes are read once (the row kept in
- * registers between the two), others take those two calls. */
+ * grad_out = 1; rows of 2049 to 51200 classes, 16-byte aligned with ld and
+ * ldd multiples of 4, are read once (the row kept in registers between the
+ * two), others take those two calls. */
 int tjh_cross_entropy_forward_grad(const float* logits, int64_t ld,
                                    const int32_t* targets, int64_t rows,
                                    int64_t cols, int32_t ignore_index,
